@@ -1,0 +1,285 @@
+"""ctypes bindings for the CPU checker (test infrastructure only).
+
+`Oracle` wraps oracle/liboracle.so (the C restatement, sw_oracle.c);
+`Ref` wraps oracle/_ref/libref_*.so (the reference's own kernels and its
+laguna.c MoE entry point, compiled from the reference sources).  Only tests/,
+__graft_entry__.smoke() and bench.py's cpu_baseline leg use this module.
+"""
+import ctypes as C
+import os
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+F32P = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
+U8P = np.ctypeslib.ndpointer(np.uint8, flags="C_CONTIGUOUS")
+U16P = np.ctypeslib.ndpointer(np.uint16, flags="C_CONTIGUOUS")
+I32P = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
+
+ROUTE_SIGMOID, ROUTE_SOFTMAX, ROUTE_SOFTPLUS = 0, 1, 2
+SHARED_NONE, SHARED_UNSCALED = 0, 1
+MODE_F32, MODE_IDOT, MODE_EXACT = 0, 1, 2
+T_ROUTER, T_GATE_UP, T_DOWN, T_SH_GATE, T_SH_UP, T_SH_DOWN, T_X, T_CORR_BIAS, T_NORM, T_HEAD = range(1, 11)
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+class SwMoeDesc(C.Structure):
+    _fields_ = [("n_experts", C.c_int), ("topk", C.c_int), ("route_act", C.c_int),
+                ("use_corr_bias", C.c_int), ("norm_topk", C.c_int), ("route_scale", C.c_float),
+                ("shared_mode", C.c_int)]
+
+
+class SwMoeLayer(C.Structure):
+    _fields_ = [("D", C.c_int), ("I", C.c_int), ("Is", C.c_int), ("E", C.c_int), ("gs", C.c_int),
+                ("router_bf16", C.c_int), ("shared_f32", C.c_int),
+                ("router", C.c_void_p), ("corr_bias", C.c_void_p), ("logit_bias", C.c_void_p),
+                ("gu_q", C.c_void_p), ("dn_q", C.c_void_p), ("gu_s", C.c_void_p), ("dn_s", C.c_void_p),
+                ("sg", C.c_void_p), ("su", C.c_void_p), ("sd", C.c_void_p)]
+
+
+class Oracle:
+    def __init__(self, path=None):
+        self.lib = C.CDLL(path or os.path.join(HERE, "liboracle.so"))
+        L = self.lib
+        L.sw_mix64.restype = C.c_uint64; L.sw_mix64.argtypes = [C.c_uint64]
+        L.sw_u64.restype = C.c_uint64; L.sw_u64.argtypes = [C.c_uint64, C.c_uint64]
+        L.sw_normal.restype = C.c_double; L.sw_normal.argtypes = [C.c_uint64, C.c_uint64]
+        L.sw_tensor_seed.restype = C.c_uint64; L.sw_tensor_seed.argtypes = [C.c_uint64, C.c_int, C.c_int]
+        L.sw_fill_normal_f32.argtypes = [F32P, C.c_int64, C.c_uint64, C.c_uint64, C.c_double]
+        L.sw_round_bf16.restype = C.c_float; L.sw_round_bf16.argtypes = [C.c_float]
+        L.sw_f32_to_bf16_array.argtypes = [U16P, F32P, C.c_int64]
+        L.sw_round_bf16_inplace.argtypes = [F32P, C.c_int64]
+        L.sw_quant_i4.argtypes = [U8P, F32P, F32P, C.c_int, C.c_int, C.c_int]
+        L.sw_gen_q4.argtypes = [U8P, F32P, C.c_uint64, C.c_double, C.c_int64, C.c_int64, C.c_int, C.c_int]
+        L.sw_matmul_f32.argtypes = [F32P, F32P, F32P] + [C.c_int] * 4
+        L.sw_matmul_bf16.argtypes = [F32P, F32P, U16P] + [C.c_int] * 4
+        L.sw_matmul_q4.argtypes = [F32P, F32P, U8P, F32P] + [C.c_int] * 5
+        L.sw_matmul_i4_grouped.argtypes = [F32P, F32P, U8P, F32P] + [C.c_int] * 4
+        for f in ("sw_siluf", "sw_softplusf", "sw_sigmoidf"):
+            getattr(L, f).restype = C.c_float; getattr(L, f).argtypes = [C.c_float]
+        L.sw_softmax_row.argtypes = [F32P, C.c_int]
+        L.sw_moe_topk.argtypes = [F32P, C.c_void_p, C.c_int, C.c_int, C.c_int, I32P]
+        L.sw_rmsnorm_row.argtypes = [F32P, F32P, F32P, C.c_int, C.c_float]
+        L.sw_argmax.restype = C.c_int; L.sw_argmax.argtypes = [F32P, C.c_int]
+        L.sw_moe_route.argtypes = [C.POINTER(SwMoeDesc), C.POINTER(SwMoeLayer), F32P, C.c_int, C.c_int,
+                                   C.c_void_p, I32P, F32P]
+        L.sw_moe_block_rows.argtypes = [C.POINTER(SwMoeDesc), C.POINTER(SwMoeLayer), F32P, F32P, C.c_int, C.c_int]
+        L.sw_moe_group_rows.argtypes = [C.POINTER(SwMoeDesc), C.POINTER(SwMoeLayer), F32P, F32P, C.c_int, C.c_int]
+        L.sw_bucket.restype = C.c_int
+        L.sw_bucket.argtypes = [I32P, C.c_int, C.c_int, C.c_int, I32P, I32P, I32P, I32P, I32P]
+
+    # ---- data ----
+    def tensor_seed(self, base, layer, tid):
+        return self.lib.sw_tensor_seed(base, layer, tid)
+
+    def normal(self, n, seed, sigma=1.0, offset=0):
+        out = np.empty(n, np.float32)
+        self.lib.sw_fill_normal_f32(out, n, seed, offset, sigma)
+        return out
+
+    def bf16_round(self, x):
+        x = np.ascontiguousarray(x, np.float32).copy()
+        self.lib.sw_round_bf16_inplace(x, x.size)
+        return x
+
+    def to_bf16(self, x):
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.empty(x.shape, np.uint16)
+        self.lib.sw_f32_to_bf16_array(out, x, x.size)
+        return out
+
+    def quant_i4(self, w, gs):
+        w = np.ascontiguousarray(w, np.float32)
+        O, I = w.shape
+        ng = (I + gs - 1) // gs if gs > 0 else 1
+        p = np.empty((O, (I + 1) // 2), np.uint8)
+        s = np.empty((O, ng), np.float32)
+        self.lib.sw_quant_i4(p, s, w, O, I, gs)
+        return p, s
+
+    def gen_q4(self, seed, sigma, rows, I, gs, row0=0):
+        ng = (I + gs - 1) // gs if gs > 0 else 1
+        p = np.empty((rows, (I + 1) // 2), np.uint8)
+        s = np.empty((rows, ng), np.float32)
+        self.lib.sw_gen_q4(p, s, seed, sigma, row0, rows, I, gs)
+        return p, s
+
+    # ---- kernels ----
+    def matmul_f32(self, x, W, exact=0):
+        S, I = x.shape; O = W.shape[0]
+        y = np.empty((S, O), np.float32)
+        self.lib.sw_matmul_f32(y, np.ascontiguousarray(x), np.ascontiguousarray(W), S, I, O, exact)
+        return y
+
+    def matmul_bf16(self, x, Wb, exact=0):
+        S, I = x.shape; O = Wb.shape[0]
+        y = np.empty((S, O), np.float32)
+        self.lib.sw_matmul_bf16(y, np.ascontiguousarray(x), np.ascontiguousarray(Wb), S, I, O, exact)
+        return y
+
+    def matmul_q4(self, x, p, s, mode=0, exact=0):
+        S, I = x.shape; O = p.shape[0]
+        y = np.empty((S, O), np.float32)
+        self.lib.sw_matmul_q4(y, np.ascontiguousarray(x), p, np.ascontiguousarray(s, np.float32).reshape(-1), S, I, O, mode, exact)
+        return y
+
+    def matmul_i4_grouped(self, x, p, s, gs):
+        S, I = x.shape; O = p.shape[0]
+        y = np.empty((S, O), np.float32)
+        self.lib.sw_matmul_i4_grouped(y, np.ascontiguousarray(x), p, np.ascontiguousarray(s, np.float32).reshape(-1), S, I, O, gs)
+        return y
+
+    def softmax_row(self, x):
+        x = np.ascontiguousarray(x, np.float32).copy()
+        self.lib.sw_softmax_row(x, x.size)
+        return x
+
+    def topk(self, score, K, bias=None):
+        sel = np.empty(K, np.int32)
+        b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+        self.lib.sw_moe_topk(np.ascontiguousarray(score, np.float32), _ptr(b), 1 if b is not None else 0,
+                             score.size, K, sel)
+        return sel
+
+    def bucket(self, sel, S, K, E):
+        T = S * K
+        gexp = np.zeros(E, np.int32); gbeg = np.zeros(E, np.int32); gcnt = np.zeros(E, np.int32)
+        grow = np.zeros(T, np.int32); rowof = np.zeros(T, np.int32)
+        G = self.lib.sw_bucket(np.ascontiguousarray(sel, np.int32).reshape(-1), S, K, E, gexp, gbeg, gcnt, grow, rowof)
+        return G, gexp[:G], gbeg[:G], gcnt[:G], grow, rowof
+
+    # ---- MoE block ----
+    @staticmethod
+    def make(desc, layer):
+        d = SwMoeDesc(desc.E, desc.K, desc.route_act, desc.use_corr_bias, desc.norm_topk,
+                      desc.route_scale, desc.shared_mode)
+        L = SwMoeLayer(layer.D, layer.I, layer.Is, layer.E, layer.gs, int(layer.router_bf16), 0,
+                       _ptr(layer.router), _ptr(layer.corr_bias), _ptr(layer.logit_bias),
+                       _ptr(layer.gu_q), _ptr(layer.dn_q), _ptr(layer.gu_s), _ptr(layer.dn_s),
+                       _ptr(layer.sg), _ptr(layer.su), _ptr(layer.sd))
+        return d, L
+
+    def route(self, desc, layer, x, mode=MODE_F32):
+        d, L = self.make(desc, layer)
+        S = x.shape[0]
+        sel = np.empty((S, desc.K), np.int32); w = np.empty((S, desc.K), np.float32)
+        lg = np.empty((S, desc.E), np.float32)
+        self.lib.sw_moe_route(C.byref(d), C.byref(L), np.ascontiguousarray(x, np.float32), S, mode,
+                              lg.ctypes.data_as(C.c_void_p), sel, w)
+        return lg, sel, w
+
+    def moe_block_rows(self, desc, layer, x, out, mode=MODE_F32):
+        d, L = self.make(desc, layer)
+        out = np.ascontiguousarray(out, np.float32).copy()
+        self.lib.sw_moe_block_rows(C.byref(d), C.byref(L), np.ascontiguousarray(x, np.float32), out, x.shape[0], mode)
+        return out
+
+    def moe_group_rows(self, desc, layer, x, out, mode=MODE_F32):
+        d, L = self.make(desc, layer)
+        out = np.ascontiguousarray(out, np.float32).copy()
+        self.lib.sw_moe_group_rows(C.byref(d), C.byref(L), np.ascontiguousarray(x, np.float32), out, x.shape[0], mode)
+        return out
+
+
+class Ref:
+    """The reference's own kernels (oracle/_ref), when built."""
+
+    def __init__(self, isa=None):
+        isa = isa or "avx512"
+        self.lib = C.CDLL(os.path.join(HERE, "_ref", f"libref_kernels_{isa}.so"))
+        L = self.lib
+        L.ref_matmul_f32.argtypes = [F32P, F32P, F32P] + [C.c_int] * 4
+        L.ref_matmul_bf16.argtypes = [F32P, F32P, U16P] + [C.c_int] * 5
+        L.ref_matmul_q4_kb.argtypes = [F32P, F32P, U8P, F32P] + [C.c_int] * 5
+        L.ref_matmul_i4_grouped.argtypes = [F32P, F32P, U8P, F32P] + [C.c_int] * 4
+        L.ref_softmax_row.argtypes = [F32P, C.c_int]
+        L.ref_moe_topk.argtypes = [F32P, C.c_void_p, C.c_int, C.c_int, C.c_int, I32P]
+        for f in ("ref_siluf", "ref_softplusf", "ref_expf", "ref_log1pf"):
+            getattr(L, f).restype = C.c_float; getattr(L, f).argtypes = [C.c_float]
+        L.ref_rmsnorm_row.argtypes = [F32P, F32P, F32P, C.c_int, C.c_float]
+        L.ref_physical_cores.restype = C.c_int
+        L.ref_moe_block_rows.restype = C.c_int
+        L.ref_moe_block_rows.argtypes = ([C.c_int] * 5 + [C.c_float] + [C.c_int] * 6
+                                         + [C.c_void_p] * 3 + [C.c_void_p] * 4 + [C.c_void_p] * 3
+                                         + [F32P, F32P, C.c_int, C.c_int, C.c_int])
+
+    @staticmethod
+    def available(isa="avx512"):
+        return os.path.exists(os.path.join(HERE, "_ref", f"libref_kernels_{isa}.so"))
+
+    def matmul_f32(self, x, W, exact=0):
+        S, I = x.shape; O = W.shape[0]
+        y = np.empty((S, O), np.float32)
+        self.lib.ref_matmul_f32(y, np.ascontiguousarray(x), np.ascontiguousarray(W), S, I, O, exact)
+        return y
+
+    def matmul_bf16(self, x, Wb, exact=0, round_x=0):
+        S, I = x.shape; O = Wb.shape[0]
+        y = np.empty((S, O), np.float32)
+        self.lib.ref_matmul_bf16(y, np.ascontiguousarray(x), np.ascontiguousarray(Wb), S, I, O, round_x, exact)
+        return y
+
+    def matmul_q4(self, x, p, s, mode=0, exact=0):
+        S, I = x.shape; O = p.shape[0]
+        y = np.empty((S, O), np.float32)
+        self.lib.ref_matmul_q4_kb(y, np.ascontiguousarray(x), p, np.ascontiguousarray(s, np.float32).reshape(-1), S, I, O, mode, exact)
+        return y
+
+    def matmul_i4_grouped(self, x, p, s, gs):
+        S, I = x.shape; O = p.shape[0]
+        y = np.empty((S, O), np.float32)
+        self.lib.ref_matmul_i4_grouped(y, np.ascontiguousarray(x), p, np.ascontiguousarray(s, np.float32).reshape(-1), S, I, O, gs)
+        return y
+
+    def softmax_row(self, x):
+        x = np.ascontiguousarray(x, np.float32).copy()
+        self.lib.ref_softmax_row(x, x.size)
+        return x
+
+    def topk(self, score, K, bias=None):
+        sel = np.empty(K, np.int32)
+        b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+        self.lib.ref_moe_topk(np.ascontiguousarray(score, np.float32), _ptr(b), 1 if b is not None else 0,
+                              score.size, K, sel)
+        return sel
+
+    def moe_block_rows(self, desc, layer, x, out, mode=0, exact=0):
+        out = np.ascontiguousarray(out, np.float32).copy()
+        rc = self.lib.ref_moe_block_rows(
+            desc.E, desc.K, desc.route_act, desc.use_corr_bias, desc.norm_topk, desc.route_scale,
+            desc.shared_mode, layer.D, layer.I, layer.Is, layer.gs, int(layer.router_bf16),
+            _ptr(layer.router), _ptr(layer.corr_bias), _ptr(layer.logit_bias),
+            _ptr(layer.gu_q), _ptr(layer.gu_s), _ptr(layer.dn_q), _ptr(layer.dn_s),
+            _ptr(layer.sg), _ptr(layer.su), _ptr(layer.sd),
+            np.ascontiguousarray(x, np.float32), out, x.shape[0], mode, exact)
+        assert rc == 0
+        return out
+
+
+class RefLaguna:
+    """The reference Laguna engine's lag_moe_rows (gs = 0 container)."""
+
+    def __init__(self):
+        self.lib = C.CDLL(os.path.join(HERE, "_ref", "libref_laguna_avx512.so"))
+        f = self.lib.ref_laguna_moe_rows
+        f.restype = C.c_int
+        f.argtypes = ([C.c_int] * 3 + [C.c_float] + [C.c_int] * 3 + [C.c_void_p] * 2 + [C.c_void_p] * 4
+                      + [C.c_void_p] * 3 + [F32P, F32P, C.c_int, C.c_int, C.c_int])
+
+    @staticmethod
+    def available():
+        return os.path.exists(os.path.join(HERE, "_ref", "libref_laguna_avx512.so"))
+
+    def moe_rows(self, desc, layer, x, h, exact=0, group=1):
+        assert layer.gs == 0 and not layer.router_bf16
+        h = np.ascontiguousarray(h, np.float32).copy()
+        rc = self.lib.ref_laguna_moe_rows(
+            desc.E, desc.K, desc.norm_topk, desc.route_scale, layer.D, layer.I, layer.Is,
+            _ptr(layer.router), _ptr(layer.corr_bias),
+            _ptr(layer.gu_q), _ptr(layer.gu_s), _ptr(layer.dn_q), _ptr(layer.dn_s),
+            _ptr(layer.sg), _ptr(layer.su), _ptr(layer.sd),
+            np.ascontiguousarray(x, np.float32), h, x.shape[0], exact, group)
+        assert rc == 0
+        return h

@@ -1,0 +1,548 @@
+/* sw_oracle.c -- CPU restatement of the sabrewing MoE-block hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY (see sw_oracle.h).  Built with -ffp-contract=off:
+ * every fused multiply-add the reference gets from GCC's default contraction
+ * (-O3 -march=native, GNU C => -ffp-contract=fast) is written here as an
+ * explicit fmaf(), and nothing else is fused.  The SIMD reductions are
+ * restated lane by lane:
+ *   _mm512_reduce_add_ps (GCC avx512fintrin.h __MM512_REDUCE_OP):
+ *       t8[j]=a[j]+a[j+8]; t4[j]=t8[j]+t8[j+4]; (t4[0]+t4[2]) + (t4[1]+t4[3])
+ *   hsum256 (c/quant.h:20-24):
+ *       ((v0+v4)+(v2+v6)) + ((v1+v5)+(v3+v7))
+ *
+ * Pinning: tests/test_oracle_ref.py checks every kernel here bit-for-bit
+ * against oracle/_ref (the reference headers compiled from /root/reference),
+ * tests/test_oracle_golden.py against the committed golden vectors, and
+ * tests/test_oracle_math.py against closed forms and brute force. */
+#include "sw_oracle.h"
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ======================= seeded synthetic data ======================= */
+
+uint64_t sw_mix64(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+/* i-th draw of the SplitMix64 stream seeded with `seed` */
+uint64_t sw_u64(uint64_t seed, uint64_t i) { return sw_mix64(seed + (i + 1) * 0x9E3779B97F4A7C15ull); }
+
+uint64_t sw_tensor_seed(uint64_t base, int layer, int tensor_id) {
+    uint64_t k = ((uint64_t)(uint32_t)layer << 8) | (uint64_t)(uint32_t)tensor_id;
+    return sw_mix64(base ^ sw_mix64(k + 0x632BE59BD9B4E019ull));
+}
+
+/* Fixed-sequence double ln / sincos: only IEEE +,-,*,/ and explicit fma, so
+ * any IEEE-754 machine (the HIP generator included) evaluates the same bits. */
+static const double SW_LN_C[13] = {
+    0x1.0000000000000p+0, 0x1.5555555555555p-2, 0x1.999999999999ap-3, 0x1.2492492492492p-3,
+    0x1.c71c71c71c71cp-4, 0x1.745d1745d1746p-4, 0x1.3b13b13b13b14p-4, 0x1.1111111111111p-4,
+    0x1.e1e1e1e1e1e1ep-5, 0x1.af286bca1af28p-5, 0x1.8618618618618p-5, 0x1.642c8590b2164p-5,
+    0x1.47ae147ae147bp-5 };
+static const double SW_SIN_C[10] = {
+    0x1.0000000000000p+0, -0x1.5555555555555p-3, 0x1.1111111111111p-7, -0x1.a01a01a01a01ap-13,
+    0x1.71de3a556c734p-19, -0x1.ae64567f544e4p-26, 0x1.6124613a86d09p-33, -0x1.ae7f3e733b81fp-41,
+    0x1.952c77030ad4ap-49, -0x1.2f49b46814157p-57 };
+static const double SW_COS_C[10] = {
+    0x1.0000000000000p+0, -0x1.0000000000000p-1, 0x1.5555555555555p-5, -0x1.6c16c16c16c17p-10,
+    0x1.a01a01a01a01ap-16, -0x1.27e4fb7789f5cp-22, 0x1.1eed8eff8d898p-29, -0x1.93974a8c07c9dp-37,
+    0x1.ae7f3e733b81fp-45, -0x1.6827863b97d97p-53 };
+#define SW_PIO2   0x1.921fb54442d18p+0
+#define SW_LN2    0x1.62e42fefa39efp-1
+#define SW_SQRT2  0x1.6a09e667f3bcdp+0
+#define SW_SQRTH  0x1.6a09e667f3bcdp-1
+
+static double sw_ln(double x) {                 /* x in [2^-53, 1] */
+    uint64_t b; memcpy(&b, &x, 8);
+    int e = (int)((b >> 52) & 0x7ff) - 1023;
+    b = (b & 0x000fffffffffffffull) | 0x3ff0000000000000ull;
+    double m; memcpy(&m, &b, 8);
+    if (m > SW_SQRT2) { m = m * 0.5; e += 1; }
+    double f = m - 1.0;
+    double s = f / (2.0 + f);
+    double z = s * s;
+    double p = SW_LN_C[12];
+    for (int k = 11; k >= 0; k--) p = fma(p, z, SW_LN_C[k]);
+    return fma((double)e, SW_LN2, (2.0 * s) * p);
+}
+
+static void sw_sincos2pi(double u, double *sn, double *cs) {   /* u in [0,1) */
+    double u4 = u * 4.0;
+    int q = (int)u4;
+    double r = u4 - (double)q;
+    double t = (r - 0.5) * SW_PIO2;
+    double t2 = t * t;
+    double ps = SW_SIN_C[9], pc = SW_COS_C[9];
+    for (int k = 8; k >= 0; k--) { ps = fma(ps, t2, SW_SIN_C[k]); pc = fma(pc, t2, SW_COS_C[k]); }
+    double st = t * ps, ct = pc;
+    double cphi = (ct - st) * SW_SQRTH, sphi = (ct + st) * SW_SQRTH;
+    switch (q & 3) {
+    case 0: *cs = cphi;  *sn = sphi;  break;
+    case 1: *cs = -sphi; *sn = cphi;  break;
+    case 2: *cs = -cphi; *sn = -sphi; break;
+    default: *cs = sphi; *sn = -cphi; break;
+    }
+}
+
+double sw_normal(uint64_t seed, uint64_t i) {
+    uint64_t p = i >> 1;
+    uint64_t a = sw_u64(seed, 2 * p), b = sw_u64(seed, 2 * p + 1);
+    double u1 = (double)((a >> 11) + 1) * 0x1.0p-53;
+    double u2 = (double)(b >> 11) * 0x1.0p-53;
+    double r = sqrt(-2.0 * sw_ln(u1));
+    double sn, cs; sw_sincos2pi(u2, &sn, &cs);
+    return (i & 1) ? r * sn : r * cs;
+}
+
+void sw_fill_normal_f32(float *out, int64_t n, uint64_t seed, uint64_t offset, double sigma) {
+    #pragma omp parallel for schedule(static) if(n >= 65536)
+    for (int64_t i = 0; i < n; i++) out[i] = (float)(sigma * sw_normal(seed, offset + (uint64_t)i));
+}
+
+/* f32 -> bf16 round-to-nearest-even (c/tools/kernel_check.c:23 f2bf16) */
+uint16_t sw_f32_to_bf16(float f) { uint32_t u; memcpy(&u, &f, 4); u += 0x7FFF + ((u >> 16) & 1); return (uint16_t)(u >> 16); }
+/* exact widening (c/moe_math.h:51 bf16_f32) */
+float sw_bf16_to_f32(uint16_t b) { uint32_t u = (uint32_t)b << 16; float f; memcpy(&f, &u, 4); return f; }
+float sw_round_bf16(float x) { return sw_bf16_to_f32(sw_f32_to_bf16(x)); }
+void sw_round_bf16_inplace(float *x, int64_t n) { for (int64_t i = 0; i < n; i++) x[i] = sw_round_bf16(x[i]); }
+void sw_f32_to_bf16_array(uint16_t *out, const float *x, int64_t n) { for (int64_t i = 0; i < n; i++) out[i] = sw_f32_to_bf16(x[i]); }
+
+uint64_t sw_fnv1a64(const void *p, size_t n, uint64_t h) {
+    const uint8_t *b = (const uint8_t *)p;
+    if (!h) h = 0xcbf29ce484222325ull;
+    for (size_t i = 0; i < n; i++) { h ^= b[i]; h *= 0x100000001b3ull; }
+    return h;
+}
+
+/* ======================= int4 container quantisers ======================= */
+
+/* per-row: c/tools/convert_laguna_int4.py:49-60 (s = amax/7, floor 1e-8);
+ * per-group: c/tools/convert_fp8_to_int4.py:54-85 (s = max(amax/7, 1e-8),
+ * scale layout s[o*ng + g]).  Both: q = clip(rint(w/s), -8, 7) in f32,
+ * byte = (q_even + 8) | (q_odd + 8) << 4; an odd I leaves the last high nibble 0. */
+static void quant_row(uint8_t *p, float *scale, const float *w, int I, int gs) {
+    int egs = gs > 0 ? gs : I, ng = gs > 0 ? (I + gs - 1) / gs : 1;
+    int rb = (I + 1) / 2;
+    memset(p, 0, (size_t)rb);
+    for (int g = 0; g < ng; g++) {
+        int base = g * egs, end = base + egs < I ? base + egs : I;
+        float am = 0.f;
+        for (int i = base; i < end; i++) { float a = fabsf(w[i]); if (a > am) am = a; }
+        float s = am / 7.f;
+        if (s < 1e-8f) s = 1e-8f;
+        scale[g] = s;
+        for (int i = base; i < end; i++) {
+            int q = (int)rintf(w[i] / s);
+            if (q < -8) q = -8;
+            if (q > 7) q = 7;
+            uint8_t nib = (uint8_t)(q + 8);
+            if (i & 1) p[i >> 1] |= (uint8_t)(nib << 4); else p[i >> 1] |= nib;
+        }
+    }
+}
+
+void sw_quant_i4(uint8_t *packed, float *scale, const float *w, int O, int I, int gs) {
+    int rb = (I + 1) / 2, ng = gs > 0 ? (I + gs - 1) / gs : 1;
+    #pragma omp parallel for schedule(static) if(O >= 64)
+    for (int o = 0; o < O; o++)
+        quant_row(packed + (int64_t)o * rb, scale + (int64_t)o * ng, w + (int64_t)o * I, I, gs);
+}
+
+void sw_gen_q4(uint8_t *packed, float *scale, uint64_t seed, double sigma,
+               int64_t row0, int64_t nrows, int I, int gs) {
+    int rb = (I + 1) / 2, ng = gs > 0 ? (I + gs - 1) / gs : 1;
+    #pragma omp parallel
+    {
+        float *w = (float *)malloc((size_t)I * sizeof(float));
+        #pragma omp for schedule(static)
+        for (int64_t r = 0; r < nrows; r++) {
+            uint64_t off = (uint64_t)(row0 + r) * (uint64_t)I;
+            for (int i = 0; i < I; i++) w[i] = (float)(sigma * sw_normal(seed, off + (uint64_t)i));
+            quant_row(packed + r * rb, scale + r * ng, w, I, gs);
+        }
+        free(w);
+    }
+}
+
+/* ======================= reductions ======================= */
+
+static float reduce16(const float *a) {         /* GCC _mm512_reduce_add_ps */
+    float t8[8], t4[4];
+    for (int j = 0; j < 8; j++) t8[j] = a[j + 8] + a[j];
+    for (int j = 0; j < 4; j++) t4[j] = t8[j + 4] + t8[j];
+    return (t4[0] + t4[2]) + (t4[1] + t4[3]);
+}
+static float hsum8(const float *v) {            /* hsum256, c/quant.h:20-24 */
+    return ((v[0] + v[4]) + (v[2] + v[6])) + ((v[1] + v[5]) + (v[3] + v[7]));
+}
+
+/* ======================= GEMV / GEMM contracts ======================= */
+
+/* c/moe_matmul.h:25-55.  SIMD: lane j sums i = j mod 16 ascending with FMA,
+ * reduce16, then the scalar tail fused into the sum.  exact: double sum. */
+void sw_matmul_f32(float *y, const float *x, const float *W, int S, int I, int O, int exact) {
+    #pragma omp parallel for schedule(static) if((int64_t)S * O >= 512)
+    for (int o = 0; o < O; o++) {
+        const float *w = W + (int64_t)o * I;
+        for (int s = 0; s < S; s++) {
+            const float *xs = x + (int64_t)s * I;
+            if (exact) {
+                double sm = 0; for (int i = 0; i < I; i++) sm += (double)xs[i] * w[i];
+                y[(int64_t)s * O + o] = (float)sm;
+                continue;
+            }
+            float ln[16] = {0};
+            int i = 0;
+            for (; i + 16 <= I; i += 16)
+                for (int j = 0; j < 16; j++) ln[j] = fmaf(xs[i + j], w[i + j], ln[j]);
+            float sm = reduce16(ln);
+            for (; i < I; i++) sm = fmaf(xs[i], w[i], sm);
+            y[(int64_t)s * O + o] = sm;
+        }
+    }
+}
+
+/* c/moe_matmul.h:65-122 at round_x=0: weight widened bf16->f32 exactly, same
+ * lane contract as matmul_f32 (so a bf16 router equals an f32 router holding
+ * the widened values, c/laguna.c:126-128). */
+void sw_matmul_bf16(float *y, const float *x, const uint16_t *W, int S, int I, int O, int exact) {
+    #pragma omp parallel for schedule(static) if((int64_t)S * O >= 512)
+    for (int o = 0; o < O; o++) {
+        const uint16_t *w = W + (int64_t)o * I;
+        for (int s = 0; s < S; s++) {
+            const float *xs = x + (int64_t)s * I;
+            if (exact) {
+                double sm = 0; for (int i = 0; i < I; i++) sm += (double)xs[i] * sw_bf16_to_f32(w[i]);
+                y[(int64_t)s * O + o] = (float)sm;
+                continue;
+            }
+            float ln[16] = {0};
+            int i = 0;
+            for (; i + 16 <= I; i += 16)
+                for (int j = 0; j < 16; j++) ln[j] = fmaf(xs[i + j], sw_bf16_to_f32(w[i + j]), ln[j]);
+            float sm = reduce16(ln);
+            for (; i < I; i++) sm = fmaf(xs[i], sw_bf16_to_f32(w[i]), sm);
+            y[(int64_t)s * O + o] = sm;
+        }
+    }
+}
+
+static inline int nib_at(const uint8_t *p, int col) {
+    uint8_t b = p[col >> 1];
+    return (col & 1) ? (b >> 4) : (b & 0xF);
+}
+
+/* per-row int4, c/moe_quant.h:45-217 (matmul_q4_k / matmul_q4_kb; every row
+ * reduces in the S=1 order).
+ *   F32 SIMD: 16 lanes, per 16 packed bytes two FMAs per lane -- columns
+ *             2c+j then 2c+16+j -- reduce16, byte tail, * scale.
+ *   IDOT:     x per 32-block to int8 (amax/127, floor 1e-12, lrintf), exact
+ *             integer dot per block, acc = fma(xs_b, dot, acc), * scale.
+ *   exact:    double sum, (float)(s * scale); also what IDOT degrades to when
+ *             I % 32 != 0 or I > 8192 (c/moe_quant.h:48,85,115). */
+void sw_matmul_q4(float *y, const float *x, const uint8_t *packed, const float *scale,
+                  int S, int I, int O, int mode, int exact) {
+    int rb = I / 2;
+    if (mode != SW_Q4_F32 && !(mode == SW_Q4_IDOT && I % 32 == 0 && I <= 8192)) exact = 1;
+    if (mode == SW_Q4_IDOT && I % 32 == 0 && I <= 8192) {
+        int nb = I / 32;
+        int8_t *xi = (int8_t *)malloc((size_t)S * I);
+        float *xs = (float *)malloc((size_t)S * nb * sizeof(float));
+        for (int s = 0; s < S; s++) {
+            const float *xr = x + (int64_t)s * I;
+            for (int b = 0; b < nb; b++) {
+                const float *xb = xr + b * 32;
+                float am = 0.f; for (int i = 0; i < 32; i++) { float a = fabsf(xb[i]); if (a > am) am = a; }
+                float sc = am / 127.f; if (sc < 1e-12f) sc = 1e-12f;
+                xs[(int64_t)s * nb + b] = sc; float inv = 1.f / sc;
+                for (int i = 0; i < 32; i++) xi[(int64_t)s * I + b * 32 + i] = (int8_t)lrintf(xb[i] * inv);
+            }
+        }
+        #pragma omp parallel for schedule(static)
+        for (int o = 0; o < O; o++) {
+            const uint8_t *p = packed + (int64_t)o * rb;
+            for (int s = 0; s < S; s++) {
+                float acc = 0.f;
+                for (int b = 0; b < nb; b++) {
+                    int dot = 0;
+                    for (int i = 0; i < 32; i++) dot += (int)xi[(int64_t)s * I + b * 32 + i] * (nib_at(p, b * 32 + i) - 8);
+                    acc = fmaf(xs[(int64_t)s * nb + b], (float)dot, acc);
+                }
+                y[(int64_t)s * O + o] = acc * scale[o];
+            }
+        }
+        free(xi); free(xs);
+        return;
+    }
+    #pragma omp parallel for schedule(static) if((int64_t)S * O >= 512)
+    for (int o = 0; o < O; o++) {
+        const uint8_t *p = packed + (int64_t)o * rb;
+        for (int s = 0; s < S; s++) {
+            const float *xs = x + (int64_t)s * I;
+            if (exact) {
+                double sm = 0;
+                for (int c = 0; c < rb; c++) {
+                    uint8_t b = p[c];
+                    sm += (double)xs[2 * c] * ((int)(b & 0xF) - 8) + (double)xs[2 * c + 1] * ((int)(b >> 4) - 8);
+                }
+                y[(int64_t)s * O + o] = (float)(sm * scale[o]);
+                continue;
+            }
+            float ln[16] = {0};
+            int c = 0;
+            for (; c + 16 <= rb; c += 16) {
+                for (int j = 0; j < 16; j++) ln[j] = fmaf(xs[2 * c + j], (float)(nib_at(p, 2 * c + j) - 8), ln[j]);
+                for (int j = 0; j < 16; j++) ln[j] = fmaf(xs[2 * c + 16 + j], (float)(nib_at(p, 2 * c + 16 + j) - 8), ln[j]);
+            }
+            float sm = reduce16(ln);
+            for (; c < rb; c++) {
+                uint8_t b = p[c];
+                sm = sm + fmaf(xs[2 * c], (float)((int)(b & 0xF) - 8), xs[2 * c + 1] * (float)((int)(b >> 4) - 8));
+            }
+            y[(int64_t)s * O + o] = sm * scale[o];
+        }
+    }
+}
+
+/* group-scale int4, c/quant.h:168-203 (AVX2 body): per group an 8-lane FMA
+ * chain, two FMAs per 16 columns (cols i..i+7 then i+8..i+15), hsum256, then
+ * a = fma(h, scale, a); scalar tail for a group length not divisible by 16. */
+void sw_matmul_i4_grouped(float *y, const float *x, const uint8_t *q4, const float *scale,
+                          int S, int I, int O, int gs) {
+    int rb = (I + 1) / 2, ng = (I + gs - 1) / gs;
+    #pragma omp parallel for schedule(static)
+    for (int o = 0; o < O; o++) {
+        const uint8_t *w = q4 + (int64_t)o * rb;
+        const float *scl = scale + (int64_t)o * ng;
+        for (int s = 0; s < S; s++) {
+            const float *xs = x + (int64_t)s * I;
+            float a = 0;
+            for (int g = 0; g * gs < I; g++) {
+                int base = g * gs, glen = gs;
+                if (base + glen > I) glen = I - base;
+                float sc = scl[g];
+                int i = base;
+                float ln[8] = {0};
+                for (; i + 16 <= base + glen; i += 16) {
+                    for (int j = 0; j < 8; j++) ln[j] = fmaf(xs[i + j], (float)(nib_at(w, i + j) - 8), ln[j]);
+                    for (int j = 0; j < 8; j++) ln[j] = fmaf(xs[i + 8 + j], (float)(nib_at(w, i + 8 + j) - 8), ln[j]);
+                }
+                a = fmaf(hsum8(ln), sc, a);
+                for (; i < base + glen; i += 2) {
+                    uint8_t byte = w[i >> 1];
+                    float lo = (float)((int)(byte & 0xF) - 8), hi = (float)((int)(byte >> 4) - 8);
+                    if (i + 1 < base + glen) a = fmaf(fmaf(xs[i + 1], hi, xs[i] * lo), sc, a);
+                    else a = fmaf(xs[i] * lo, sc, a);
+                }
+            }
+            y[(int64_t)s * O + o] = a;
+        }
+    }
+}
+
+/* ======================= scalar math ======================= */
+
+float sw_siluf(float x) { return x / (1.f + expf(-x)); }                         /* c/moe_math.h:53 */
+float sw_softplusf(float x) { return x > 20.f ? x : log1pf(expf(x)); }           /* c/moe_math.h:54 */
+float sw_sigmoidf(float x) { return 1.f / (1.f + expf(-x)); }                    /* c/moe_block.h:26 */
+
+/* c/moe_math.h:68-72: max, expf(x-mx) summed in double, (float)(1/s) multiply */
+void sw_softmax_row(float *x, int n) {
+    float mx = x[0]; for (int i = 1; i < n; i++) if (x[i] > mx) mx = x[i];
+    double s = 0; for (int i = 0; i < n; i++) { x[i] = expf(x[i] - mx); s += x[i]; }
+    float inv = (float)(1.0 / s); for (int i = 0; i < n; i++) x[i] *= inv;
+}
+
+/* c/moe_arch.h:64-89: K passes, strict > from -1e30 (ties -> lowest id), bias
+ * for selection only, all-non-finite -> lowest unselected expert */
+void sw_moe_topk(const float *score, const float *corr_bias, int use_bias, int E, int K, int *sel) {
+    for (int a = 0; a < K; a++) {
+        int best = -1; float bv = -1e30f;
+        for (int e = 0; e < E; e++) {
+            int used = 0; for (int b = 0; b < a; b++) if (sel[b] == e) { used = 1; break; }
+            if (used) continue;
+            float s = score[e] + (use_bias && corr_bias ? corr_bias[e] : 0.f);
+            if (s > bv) { bv = s; best = e; }
+        }
+        if (best < 0) {
+            for (int e = 0; e < E && best < 0; e++) {
+                int used = 0; for (int b = 0; b < a; b++) if (sel[b] == e) { used = 1; break; }
+                if (!used) best = e;
+            }
+            if (best < 0) best = 0;
+        }
+        sel[a] = best;
+    }
+}
+
+/* c/moe_math.h:58-62 */
+void sw_rmsnorm_row(float *out, const float *x, const float *w, int D, float eps) {
+    double ss = 0; for (int i = 0; i < D; i++) ss += (double)x[i] * x[i];
+    float inv = 1.f / sqrtf((float)(ss / D) + eps);
+    for (int i = 0; i < D; i++) out[i] = x[i] * inv * w[i];
+}
+
+/* greedy argmax, lowest index wins ties */
+int sw_argmax(const float *v, int n) {
+    int b = 0; for (int i = 1; i < n; i++) if (v[i] > v[b]) b = i;
+    return b;
+}
+
+/* ======================= MoE block ======================= */
+
+static void router_logits(const SwMoeLayer *L, const float *x, int S, int mode, float *rl) {
+    int exact = mode == SW_MODE_EXACT;
+    if (L->router_bf16) sw_matmul_bf16(rl, x, (const uint16_t *)L->router, S, L->D, L->E, exact);
+    else sw_matmul_f32(rl, x, (const float *)L->router, S, L->D, L->E, exact);
+    if (L->logit_bias)
+        for (int s = 0; s < S; s++) for (int e = 0; e < L->E; e++) rl[(int64_t)s * L->E + e] += L->logit_bias[e];
+}
+
+/* moe_block.h:115-122 (and c/laguna.c:697-706 per row) */
+static void route_row(const SwMoeDesc *d, const SwMoeLayer *L, float *rl, float *sc, int *sel, float *w) {
+    int E = d->n_experts, K = d->topk;
+    if (d->route_act == SW_ROUTE_SOFTMAX) { sw_softmax_row(rl, E); for (int e = 0; e < E; e++) sc[e] = rl[e]; }
+    else if (d->route_act == SW_ROUTE_SOFTPLUS) { for (int e = 0; e < E; e++) sc[e] = sw_softplusf(rl[e]); }
+    else for (int e = 0; e < E; e++) sc[e] = 1.f / (1.f + expf(-rl[e]));
+    sw_moe_topk(sc, L->corr_bias, d->use_corr_bias, E, K, sel);
+    for (int a = 0; a < K; a++) w[a] = sc[sel[a]];
+    if (d->norm_topk) { float sm = 0; for (int a = 0; a < K; a++) sm += w[a]; for (int a = 0; a < K; a++) w[a] /= sm; }
+}
+
+void sw_moe_route(const SwMoeDesc *d, const SwMoeLayer *L, const float *x, int S,
+                  int mode, float *logits, int *sel, float *w) {
+    int E = d->n_experts, K = d->topk;
+    float *rl = (float *)malloc((size_t)S * E * sizeof(float)), *sc = (float *)malloc((size_t)E * sizeof(float));
+    router_logits(L, x, S, mode, rl);
+    if (logits) memcpy(logits, rl, (size_t)S * E * sizeof(float));
+    for (int s = 0; s < S; s++) route_row(d, L, rl + (int64_t)s * E, sc, sel + s * K, w + s * K);
+    free(rl); free(sc);
+}
+
+/* int4 expert matmul dispatch: gs>0 -> matmul_i4_grouped (the only group-scale
+ * CPU kernel), gs==0 -> matmul_q4_kb at the caller's mode (c/laguna.c:248-252) */
+static void q4mm(float *y, const float *x, const uint8_t *p, const float *s, int S, int I, int O, int gs, int mode) {
+    if (gs > 0) sw_matmul_i4_grouped(y, x, p, s, S, I, O, gs);
+    else sw_matmul_q4(y, x, p, s, S, I, O, mode == SW_MODE_IDOT ? SW_Q4_IDOT : SW_Q4_F32, mode == SW_MODE_EXACT);
+}
+
+/* routed expert over n rows (c/laguna.c:577-595, batched form :744-752) */
+static void expert_rows(const SwMoeLayer *L, int e, const float *x, int n, float *out, int mode, float *gu, float *glu) {
+    int D = L->D, I = L->I, gs = L->gs;
+    int ngD = gs > 0 ? (D + gs - 1) / gs : 1, ngI = gs > 0 ? (I + gs - 1) / gs : 1;
+    const uint8_t *p13 = L->gu_q + (int64_t)e * 2 * I * ((D + 1) / 2);
+    const float *s13 = L->gu_s + (int64_t)e * 2 * I * ngD;
+    const uint8_t *p2 = L->dn_q + (int64_t)e * D * ((I + 1) / 2);
+    const float *s2 = L->dn_s + (int64_t)e * D * ngI;
+    q4mm(gu, x, p13, s13, n, D, 2 * I, gs, mode);
+    for (int j = 0; j < n; j++) {
+        const float *g = gu + (int64_t)j * 2 * I; float *o = glu + (int64_t)j * I;
+        for (int i = 0; i < I; i++) o[i] = sw_siluf(g[i]) * g[I + i];
+    }
+    q4mm(out, glu, p2, s2, n, I, D, gs, mode);
+}
+
+static void resmm(float *y, const float *x, const void *W, int S, int I, int O, int f32w, int mode) {
+    int exact = mode == SW_MODE_EXACT;
+    if (f32w) sw_matmul_f32(y, x, (const float *)W, S, I, O, exact);
+    else sw_matmul_bf16(y, x, (const uint16_t *)W, S, I, O, exact);
+}
+
+/* shared expert over S rows (c/laguna.c:596-604, batched :776-781) */
+static void shared_rows(const SwMoeLayer *L, const float *x, int S, float *out, int mode) {
+    int D = L->D, SI = L->Is;
+    float *sg = (float *)malloc((size_t)S * SI * 4), *su = (float *)malloc((size_t)S * SI * 4);
+    resmm(sg, x, L->sg, S, D, SI, L->shared_f32, mode);
+    resmm(su, x, L->su, S, D, SI, L->shared_f32, mode);
+    for (int64_t i = 0; i < (int64_t)S * SI; i++) sg[i] = sw_siluf(sg[i]) * su[i];
+    resmm(out, sg, L->sd, S, SI, D, L->shared_f32, mode);
+    free(sg); free(su);
+}
+
+/* moe_block.h:109-145 with laguna's hooks (c/laguna.c:574-617) */
+void sw_moe_block_rows(const SwMoeDesc *d, const SwMoeLayer *L, const float *x, float *out, int S, int mode) {
+    int E = d->n_experts, K = d->topk, D = L->D, I = L->I;
+    float *rl = (float *)malloc((size_t)E * 4), *sc = (float *)malloc((size_t)E * 4), *w = (float *)malloc((size_t)K * 4);
+    int *sel = (int *)malloc((size_t)K * sizeof(int));
+    float *scr = (float *)malloc((size_t)D * 4), *acc = (float *)malloc((size_t)D * 4);
+    float *gu = (float *)malloc((size_t)2 * I * 4), *glu = (float *)malloc((size_t)I * 4);
+    for (int s = 0; s < S; s++) {
+        const float *xs = x + (int64_t)s * D; float *os = out + (int64_t)s * D;
+        router_logits(L, xs, 1, mode, rl);
+        route_row(d, L, rl, sc, sel, w);
+        for (int i = 0; i < D; i++) acc[i] = 0;
+        for (int a = 0; a < K; a++) {
+            expert_rows(L, sel[a], xs, 1, scr, mode, gu, glu);
+            for (int i = 0; i < D; i++) acc[i] = fmaf(w[a], scr[i], acc[i]);
+        }
+        for (int i = 0; i < D; i++) acc[i] *= d->route_scale;
+        if (d->shared_mode != SW_SHARED_NONE) {
+            shared_rows(L, xs, 1, scr, mode);
+            for (int i = 0; i < D; i++) acc[i] += scr[i];
+        }
+        for (int i = 0; i < D; i++) os[i] += acc[i];
+    }
+    free(rl); free(sc); free(w); free(sel); free(scr); free(acc); free(gu); free(glu);
+}
+
+/* counting sort of c/laguna.c:708-727: groups in ascending expert id, packed
+ * rows stable in (s, a) order */
+int sw_bucket(const int *sel, int S, int K, int E, int *gexp, int *gbeg, int *gcnt, int *grow, int *rowof) {
+    int T = S * K;
+    int *cnt = (int *)calloc((size_t)E, sizeof(int)), *pos = (int *)malloc((size_t)E * sizeof(int));
+    for (int i = 0; i < T; i++) cnt[sel[i]]++;
+    int G = 0, off = 0;
+    for (int e = 0; e < E; e++) {
+        if (!cnt[e]) continue;
+        gexp[G] = e; gbeg[G] = off; gcnt[G] = cnt[e]; pos[e] = off; off += cnt[e]; G++;
+    }
+    for (int s = 0; s < S; s++) for (int a = 0; a < K; a++) {
+        int slot = pos[sel[s * K + a]]++;
+        grow[slot] = s; rowof[s * K + a] = slot;
+    }
+    free(cnt); free(pos);
+    return G;
+}
+
+/* lag_moe_group, c/laguna.c:689-786 (CPU tier) */
+void sw_moe_group_rows(const SwMoeDesc *d, const SwMoeLayer *L, const float *x, float *out, int S, int mode) {
+    int E = d->n_experts, K = d->topk, D = L->D, I = L->I, T = S * K;
+    float *w = (float *)malloc((size_t)T * 4);
+    int *sel = (int *)malloc((size_t)T * sizeof(int));
+    sw_moe_route(d, L, x, S, mode, NULL, sel, w);
+    int *gexp = (int *)malloc((size_t)E * sizeof(int)), *gbeg = (int *)malloc((size_t)E * sizeof(int));
+    int *gcnt = (int *)malloc((size_t)E * sizeof(int));
+    int *grow = (int *)malloc((size_t)T * sizeof(int)), *rowof = (int *)malloc((size_t)T * sizeof(int));
+    int G = sw_bucket(sel, S, K, E, gexp, gbeg, gcnt, grow, rowof);
+    float *slots = (float *)malloc((size_t)T * D * 4), *xg = (float *)malloc((size_t)S * D * 4);
+    float *gu = (float *)malloc((size_t)S * 2 * I * 4), *glu = (float *)malloc((size_t)S * I * 4);
+    for (int g = 0; g < G; g++) {
+        int e = gexp[g], n = gcnt[g], beg = gbeg[g];
+        for (int j = 0; j < n; j++) memcpy(xg + (int64_t)j * D, x + (int64_t)grow[beg + j] * D, (size_t)D * 4);
+        expert_rows(L, e, xg, n, slots + (int64_t)beg * D, mode, gu, glu);
+    }
+    float *acc = (float *)malloc((size_t)S * D * 4);
+    for (int s = 0; s < S; s++) {
+        float *o = acc + (int64_t)s * D;
+        for (int i = 0; i < D; i++) o[i] = 0;
+        for (int a = 0; a < K; a++) {
+            const float *v = slots + (int64_t)rowof[s * K + a] * D; float wa = w[s * K + a];
+            for (int i = 0; i < D; i++) o[i] = fmaf(wa, v[i], o[i]);
+        }
+    }
+    for (int64_t i = 0; i < (int64_t)S * D; i++) acc[i] *= d->route_scale;
+    if (d->shared_mode != SW_SHARED_NONE) {
+        float *so = (float *)malloc((size_t)S * D * 4);
+        shared_rows(L, x, S, so, mode);
+        for (int64_t i = 0; i < (int64_t)S * D; i++) out[i] += acc[i] + so[i];
+        free(so);
+    } else {
+        for (int64_t i = 0; i < (int64_t)S * D; i++) out[i] += acc[i];
+    }
+    free(w); free(sel); free(gexp); free(gbeg); free(gcnt); free(grow); free(rowof);
+    free(slots); free(xg); free(gu); free(glu); free(acc);
+}

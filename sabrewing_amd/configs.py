@@ -1,0 +1,95 @@
+"""Workload configurations of the MoE-block benchmark.
+
+C1  OLMoE-1B-7B-shaped layer: D=2048, E=64, top-8 softmax, I=1024, no shared
+    expert, f32 router, f32 activations.
+C2  Laguna-style layer: D=4096, E=256, top-10 + 1 always-on shared expert,
+    I=1024, Is=1024 (shared width not stated by the benchmark; Laguna's own
+    shared expert is as wide as a routed one), bf16 router and shared expert,
+    bf16-valued activations.  Gate "softplus" with renormalised top-k weights
+    (the benchmark's wording), plus the Laguna-faithful "sigmoid" variant
+    (e_score_correction_bias for selection, norm_topk, route_scale 2.5;
+    c/laguna.c:819) used for engine-level parity.
+C3  C2 at batch 1/8/32/64 (batched decode through the grouped path).
+C4  C2 prefill, 2048 tokens, plus a Zipf(1.1)-skewed router variant.
+C5  48 resident layers of D=4096, E=256, top-8 softmax, I=1536, batch 8,
+    RMSNorm + residual between layers, bf16 4096x32000 head + greedy argmax.
+All int4 experts use group-32 f32 scales (moe_quant.h nibbles, quant.h fmt=4
+scale layout).  Weights N(0, 0.02), activations N(0, 1).
+"""
+from dataclasses import dataclass, replace
+
+ROUTE_SIGMOID, ROUTE_SOFTMAX, ROUTE_SOFTPLUS = 0, 1, 2
+SHARED_NONE, SHARED_UNSCALED = 0, 1
+WEIGHT_SIGMA = 0.02
+
+
+@dataclass(frozen=True)
+class MoeConfig:
+    name: str
+    D: int
+    E: int
+    K: int
+    I: int
+    Is: int
+    route_act: int
+    use_corr_bias: int
+    norm_topk: int
+    route_scale: float
+    shared_mode: int
+    gs: int = 32
+    router_bf16: bool = True
+    x_bf16: bool = True
+    zipf: float = 0.0          # >0: per-expert logit bias -zipf*ln(rank) (skew variant)
+
+    @property
+    def ngD(self):
+        return (self.D + self.gs - 1) // self.gs if self.gs > 0 else 1
+
+    @property
+    def ngI(self):
+        return (self.I + self.gs - 1) // self.gs if self.gs > 0 else 1
+
+    def expert_bytes(self):
+        """int4 nibbles + f32 scales of one routed expert (gate_up + down)."""
+        nib = 2 * self.I * ((self.D + 1) // 2) + self.D * ((self.I + 1) // 2)
+        sc = 4 * (2 * self.I * self.ngD + self.D * self.ngI)
+        return nib + sc
+
+    def router_bytes(self):
+        return self.E * self.D * (2 if self.router_bf16 else 4)
+
+    def shared_bytes(self):
+        return 3 * self.D * self.Is * 2 if self.shared_mode else 0
+
+    def step_bytes(self, S, G):
+        """Algorithmic HBM bytes of one layer pass over S tokens touching G
+        distinct experts: each expert, the router and the shared expert read
+        once, activations in (f32) and out (f32 read-modify-write)."""
+        return G * self.expert_bytes() + self.router_bytes() + self.shared_bytes() + 3 * S * self.D * 4
+
+    def flops(self, S):
+        return 2 * S * (self.K * 3 * self.D * self.I + (3 * self.D * self.Is if self.shared_mode else 0) + self.D * self.E)
+
+
+C1 = MoeConfig("C1-olmoe", D=2048, E=64, K=8, I=1024, Is=0, route_act=ROUTE_SOFTMAX, use_corr_bias=0,
+               norm_topk=0, route_scale=1.0, shared_mode=SHARED_NONE, router_bf16=False, x_bf16=False)
+C2 = MoeConfig("C2-laguna-softplus", D=4096, E=256, K=10, I=1024, Is=1024, route_act=ROUTE_SOFTPLUS,
+               use_corr_bias=1, norm_topk=1, route_scale=2.5, shared_mode=SHARED_UNSCALED)
+C2_SIGMOID = replace(C2, name="C2-laguna-sigmoid", route_act=ROUTE_SIGMOID)
+C4_ZIPF = replace(C2, name="C4-laguna-zipf", zipf=1.1)
+C5_LAYER = MoeConfig("C5-inkling-small", D=4096, E=256, K=8, I=1536, Is=0, route_act=ROUTE_SOFTMAX,
+                     use_corr_bias=0, norm_topk=0, route_scale=1.0, shared_mode=SHARED_NONE)
+C5_LAYERS, C5_BATCH, C5_VOCAB = 48, 8, 32000
+
+CONFIGS = {c.name: c for c in (C1, C2, C2_SIGMOID, C4_ZIPF, C5_LAYER)}
+
+
+def scaled(cfg, D=None, E=None, K=None, I=None, Is=None, name=None):
+    """A reduced-size copy of a config (same contracts) for quick parity runs."""
+    kw = {}
+    for k, v in dict(D=D, E=E, K=K, I=I, Is=Is).items():
+        if v is not None:
+            kw[k] = v
+    if cfg.shared_mode == SHARED_NONE:
+        kw["Is"] = 0
+    return replace(cfg, name=name or (cfg.name + "-small"), **kw)
