@@ -1,0 +1,224 @@
+"""MoE-layer benchmark on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--batch B] [--config NAME]
+
+A step is one pass of the MoE block (router -> gate -> top-k -> group-by-expert
+-> int4 SwiGLU experts -> combine -> shared expert -> residual) over one batch
+of synthetic tokens already resident in HBM, through lag_hip_moe_forward.
+Weights are seeded N(0, 0.02) int4 group-32 (generated on the device); every
+step takes fresh N(0,1) tokens and steps rotate over `--layers` distinct layers
+so that the 256 MB Infinity Cache cannot hold what a step reads.
+
+Prints one JSON line: tokens/s of the whole job, the roofline of the dominant
+kernel (algorithmic bytes / average launch time, from HIP events on the
+backend stream), the layer's HBM fraction, and the reference CPU path timed
+on this host's cores on a bounded sample.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def kernel_bytes(cfg, S, G):
+    """algorithmic HBM bytes per launch of each kernel of the forward pass"""
+    D, I, Is, E, K = cfg.D, cfg.I, cfg.Is, cfg.E, cfg.K
+    ngD, ngI = (D // cfg.gs, I // cfg.gs) if cfg.gs else (1, 1)
+    T = S * K
+    b = {
+        "router": cfg.router_bytes() + S * D * 4 + S * E * 4,
+        "gate_topk": S * E * 4 + T * 8,
+        "prep_f16": S * D * 4 + 2 * S * D * 2,
+        "q4_gateup_glu": G * (2 * I * D // 2 + 2 * I * ngD * 4) + 2 * S * D * 2 + 2 * T * I * 2,
+        "q4_down": G * (D * I // 2 + D * ngI * 4) + 2 * T * I * 2 + T * D * 4,
+        "combine": T * D * 4 + 2 * S * D * 4 + (S * D * 4 if cfg.shared_mode else 0) + T * 8,
+    }
+    if cfg.shared_mode:
+        b["prep_bf16"] = S * D * 4 + 2 * S * D * 2
+        b["shared_gateup_glu"] = 2 * Is * D * 2 + 2 * S * D * 2 + 2 * S * Is * 2
+        b["shared_down"] = D * Is * 2 + 2 * S * Is * 2 + S * D * 4
+    if S > 1:
+        b["bucket"] = T * 4 * 3 + E * 12
+    return b
+
+
+def cpu_baseline(be, cfg, dl, xs, seconds):
+    """The reference CPU moe_block (oracle/_ref, compiled from the reference
+    sources: moe_block.h + matmul_i4_grouped + matmul_bf16_k) over the same
+    layer, one token at a time, for about `seconds` of host time."""
+    from oracle.oracle import Ref
+    from oracle import synth as osyn
+    isa = "avx512" if "avx512f" in open("/proc/cpuinfo").read() else "avx2"
+    if not Ref.available(isa):
+        return None
+    ref = Ref(isa)
+    ref.lib.ref_omp_autotune()                       # one OpenMP thread per physical core (c/moe_util.h:78-86)
+    cores = ref.lib.ref_physical_cores()
+    D, I, E, gs = cfg.D, cfg.I, cfg.E, cfg.gs
+    ngD, ngI = D // gs, I // gs
+    get = lambda b, shape, dt: be.d2h(b, shape, dt)
+    # host copy of the layer (router back in natural order from its seed)
+    from sabrewing_amd import synth as S
+    from oracle.oracle import Oracle
+    orc = Oracle()
+    r = orc.normal(E * D, S.tensor_seed(dl.seed, dl.layer, S.T_ROUTER), 0.02).reshape(E, D)
+    router = orc.to_bf16(r) if cfg.router_bf16 else r
+    L = osyn.Layer(D, I, cfg.Is, E, gs, cfg.router_bf16, router,
+                   np.zeros(E, np.float32) if cfg.use_corr_bias else None, None,
+                   get(dl.gu_q, E * 2 * I * D // 2, np.uint8), get(dl.gu_s, E * 2 * I * ngD, np.float32),
+                   get(dl.dn_q, E * D * I // 2, np.uint8), get(dl.dn_s, E * D * ngI, np.float32),
+                   get(dl.sg, (cfg.Is, D), np.uint16) if cfg.shared_mode else None,
+                   get(dl.su, (cfg.Is, D), np.uint16) if cfg.shared_mode else None,
+                   get(dl.sd, (D, cfg.Is), np.uint16) if cfg.shared_mode else None)
+    d = osyn.desc_of(cfg)
+    if cfg.route_act == 2:                         # softplus is the descriptor extension: time the
+        from dataclasses import replace            # reference block with its sigmoid gate (same work)
+        d = osyn.desc_of(replace(cfg, route_act=0))
+    out = np.zeros((1, D), np.float32)
+    ref.moe_block_rows(d, L, xs[0:1], out)           # warm
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds and n < 4096:
+        ref.moe_block_rows(d, L, xs[n % len(xs):n % len(xs) + 1], out)
+        n += 1
+    dt = time.perf_counter() - t0
+    return {"value": n / dt, "unit": "tokens/s", "cores": int(cores), "kind": "reference",
+            "sample": f"{n} single-token moe_block calls ({cfg.name}, B=1, gs={gs}) on one layer, "
+                      f"{isa} build, {dt:.1f} s"}
+
+
+def run(args):
+    from sabrewing_amd import configs as cf
+    from sabrewing_amd.backend import Backend, DeviceLayer, desc_of, gen_x
+
+    cfg = cf.CONFIGS[args.config]
+    B = args.batch
+    be = Backend(0)
+    t0 = time.time()
+    layers = []
+    for l in range(args.layers):
+        dl = DeviceLayer.generate(be, cfg, args.seed, layer=l)
+        dl.seed, dl.layer = args.seed, l
+        layers.append(dl)
+    log(f"generated {args.layers} x {cfg.name} layers in {time.time() - t0:.1f}s")
+    nx = args.warmup + args.steps
+    xbuf = gen_x(be, cfg, args.seed, B * nx)
+    outs = [be.alloc(B * cfg.D * 4) for _ in layers]
+    for o in outs:
+        be.lib.lag_hip_memset(int(o), 0, B * cfg.D * 4)
+    desc = desc_of(cfg)
+    wts = [dl.weights() for dl in layers]
+    xptr = lambda i: int(xbuf) + i * B * cfg.D * 4
+
+    def step(i):
+        l = i % len(layers)
+        be.moe_forward(desc, wts[l], xptr(i), outs[l], B)
+
+    for i in range(args.warmup):
+        step(i)
+    be.sync()
+    ev0, ev1 = be.event(), be.event()
+    be.record(ev0)
+    for i in range(args.steps):
+        step(args.warmup + i)
+    be.record(ev1)
+    be.sync()
+    ms = be.elapsed_ms(ev0, ev1) / args.steps
+    tok_s = B / (ms * 1e-3)
+    log(f"{cfg.name} B={B}: {ms * 1e3:.1f} us/step, {tok_s:.0f} tokens/s")
+
+    # per-kernel times: the same steps again with every launch bracketed by events
+    be.profile_reset()
+    be.profile(True)
+    G_sum = 0
+    for i in range(args.steps):
+        step(args.warmup + i)
+        if B > 1:
+            G_sum += be.last_groups()[0]
+    be.sync()
+    prof = be.profile_read()
+    be.profile(False)
+    G = G_sum / args.steps if B > 1 else cfg.K
+    if B > 1 and G_sum == 0:
+        G = cfg.K
+    kb = kernel_bytes(cfg, B, G)
+    kern = {k: {"avg_us": 1e3 * v[0] / max(v[1], 1), "launches": v[1]} for k, v in prof.items()}
+    for k, v in kern.items():
+        if k in kb:
+            v["bytes"] = kb[k]
+            v["GBs"] = kb[k] / (v["avg_us"] * 1e-6) / 1e9
+    dom = max(kern, key=lambda k: kern[k]["avg_us"] * kern[k]["launches"])
+    dk = kern[dom]
+    layer_bytes = cfg.step_bytes(B, G)
+    roof = {"bound": "hbm", "kernel": dom, "achieved": round(dk.get("GBs", 0.0), 1), "peak": HBM_PEAK_GBS,
+            "unit": "GB/s", "frac": round(dk.get("GBs", 0.0) / HBM_PEAK_GBS, 4), "traffic": None,
+            "bytes_per_launch": dk.get("bytes"), "avg_launch_us": round(dk["avg_us"], 2)}
+    layer_gbs = layer_bytes / (ms * 1e-3) / 1e9
+    log("kernels:", json.dumps({k: {kk: (round(vv, 2) if isinstance(vv, float) else vv) for kk, vv in v.items()}
+                                for k, v in kern.items()}))
+
+    cpu = None
+    if not args.no_cpu:
+        rng_x = gen_x(be, cfg, args.seed + 1, 64)
+        xs = be.d2h(rng_x, (64, cfg.D), np.float32)
+        rng_x.free()
+        try:
+            cpu = cpu_baseline(be, cfg, layers[0], xs, args.cpu_seconds)
+        except Exception as e:                      # the baseline is reported, never required
+            log("cpu baseline failed:", repr(e))
+
+    res = {
+        "metric": "MoE-layer tokens/s + % peak HBM GB/s, int4 experts, batch 1 and batch 32",
+        "value": round(tok_s, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int4 weights (group-32 f32 scales) x f32 activations, f32 accumulate",
+        "data": "synthetic: seeded N(0,0.02) int4 weights generated on device, N(0,1) bf16-valued tokens",
+        "config": {"workload": cfg.name, "batch": B, "hidden": cfg.D, "experts": cfg.E, "topk": cfg.K,
+                   "moe_inter": cfg.I, "shared_inter": cfg.Is, "gs": cfg.gs, "gate": ["sigmoid", "softmax", "softplus"][cfg.route_act],
+                   "layers_rotated": args.layers, "distinct_experts_per_step": round(G, 2),
+                   "layer_bytes_per_step": int(layer_bytes), "layer_hbm_GBs": round(layer_gbs, 1),
+                   "layer_hbm_frac": round(layer_gbs / HBM_PEAK_GBS, 4)},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "kernels": {k: {kk: (round(vv, 2) if isinstance(vv, float) else vv) for kk, vv in v.items()} for k, v in kern.items()},
+    }
+    print(json.dumps(res), flush=True)
+    for o in outs:
+        o.free()
+    xbuf.free()
+    for dl in layers:
+        dl.free()
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--batch", type=int, default=1)
+    ap.add_argument("--config", default="C2-laguna-softplus")
+    ap.add_argument("--layers", type=int, default=12)
+    ap.add_argument("--seed", type=int, default=20261201)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build measures one GPU only (the MoE block on one MI355X); "
+              "--gpus N > 1 is not supported", file=sys.stderr)
+        sys.exit(2)
+    run(args)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,151 @@
+/* sabrewing_hip.h -- C ABI of the MI355X (gfx950) MoE-block backend,
+ * libsabrewing_hip.so.  Plain pointers and sizes only.
+ *
+ * Three layers of entry points:
+ *   1. lag_hip_*            the Laguna backend ABI, entry for entry: same
+ *                           arguments, same 0 = ok / -1 = failure convention,
+ *                           host activations, device weights from
+ *                           lag_hip_upload (c/backend_cuda_laguna.h:25-75).
+ *                           The Linux loader (libsabrewing_loader.so,
+ *                           include/sabrewing_loader.h) exports them under the
+ *                           reference's lag_cuda_* names for unmodified engines.
+ *   2. lag_hip_*_g          the same entries for group-scaled int4 (one f32
+ *                           scale per gs inputs, the fmt=4 layout of
+ *                           c/quant.h:168-203); the reference's lag family is
+ *                           per-row only.
+ *   3. lag_hip_moe_forward  the whole MoE block with routing on the device
+ *                           (router GEMV -> gate -> top-k -> group-by-expert
+ *                           -> SwiGLU experts -> combine -> shared expert ->
+ *                           residual), device activations, the descriptor of
+ *                           c/moe_arch.h:33-41.
+ *
+ * Like the reference backend: one device and one stream per process, results
+ * valid on return for the host-pointer entries, not thread-safe.
+ * COLI_GPU_FAIL_AFTER=N makes every compute entry fail after N successful
+ * calls (the reference's fault-injection hook, c/backend_cuda.cu:684-693). */
+#ifndef SABREWING_HIP_H
+#define SABREWING_HIP_H
+#include <stddef.h>
+#include <stdint.h>
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------- 1. Laguna backend ABI (replaces c/backend_cuda_laguna.h) ---------------- */
+/* lag_cuda_init (c/backend_cuda_laguna.h:25): select device, create the stream. 0 = ok */
+int    lag_hip_init(int dev);
+/* lag_cuda_free_bytes / lag_cuda_total_bytes (:26-27) */
+size_t lag_hip_free_bytes(void);
+size_t lag_hip_total_bytes(void);
+/* lag_cuda_upload / lag_cuda_free (:28-29): plain byte copy, NULL = error */
+void  *lag_hip_upload(const void *h, size_t n);
+void   lag_hip_free(void *d);
+/* lag_cuda_matmul_bf16 (:32): y[S,O] = x[S,I] @ W^T, W device bf16 [O,I], x/y host f32 */
+int    lag_hip_matmul_bf16(float *y, const float *x, const void *W, int S, int I, int O);
+/* lag_cuda_matmul_q4 (:39): per-row int4 [O,I/2] + f32 scale [O], nibble-8 */
+int    lag_hip_matmul_q4(float *y, const float *x, const void *packed, const void *scale, int S, int I, int O);
+/* lag_cuda_expert_q4 (:44): out[D] = W2 @ silu_glu(W13 @ x), gate_up block-concatenated */
+int    lag_hip_expert_q4(float *out, const float *x, const void *p13, const void *s13,
+                         const void *p2, const void *s2, int I, int D);
+/* lag_cuda_moe_experts (:51): out[D] = sum_k w[k] * expert(sel[k], x), layer blobs */
+int    lag_hip_moe_experts(float *out, const float *x, const void *gu_q, const float *gu_s,
+                           const void *dn_q, const float *dn_s, const int *sel, const float *w,
+                           int K, int I, int D);
+/* lag_cuda_moe_group (:70): acc[S,D] = rank-order sum over the packed groups */
+int    lag_hip_moe_group(float *acc, const float *x, const void *gu_q, const float *gu_s,
+                         const void *dn_q, const float *dn_s, const int *gexp, const int *gbeg,
+                         const int *gcnt, int G, const int *grow, const int *rowof, const float *w,
+                         int S, int K, int I, int D);
+
+/* ---------------- 2. group-scaled int4 forms (scale[o*ng + g], ng = I/gs) ---------------- */
+int    lag_hip_matmul_q4_g(float *y, const float *x, const void *packed, const void *scale,
+                           int S, int I, int O, int gs);
+int    lag_hip_expert_q4_g(float *out, const float *x, const void *p13, const void *s13,
+                           const void *p2, const void *s2, int I, int D, int gs);
+int    lag_hip_moe_experts_g(float *out, const float *x, const void *gu_q, const float *gu_s,
+                             const void *dn_q, const float *dn_s, const int *sel, const float *w,
+                             int K, int I, int D, int gs);
+int    lag_hip_moe_group_g(float *acc, const float *x, const void *gu_q, const float *gu_s,
+                           const void *dn_q, const float *dn_s, const int *gexp, const int *gbeg,
+                           const int *gcnt, int G, const int *grow, const int *rowof, const float *w,
+                           int S, int K, int I, int D, int gs);
+
+/* ---------------- 3. device-resident MoE block ---------------- */
+enum { LAG_HIP_ROUTE_SIGMOID = 0, LAG_HIP_ROUTE_SOFTMAX = 1, LAG_HIP_ROUTE_SOFTPLUS = 2 };
+enum { LAG_HIP_SHARED_NONE = 0, LAG_HIP_SHARED_UNSCALED = 1 };
+
+/* MoeDesc (c/moe_arch.h:33-41) plus the layer shape.  route_act SOFTPLUS
+ * (x > 20 ? x : log1pf(expf(x)), c/moe_math.h:54) is an extension; the
+ * reference wires SIGMOID and SOFTMAX, shared NONE and UNSCALED. */
+typedef struct {
+    int   n_experts, topk, route_act, use_corr_bias, norm_topk;
+    float route_scale;
+    int   shared_mode;
+    int   hidden, moe_inter, shared_inter, gs;   /* D, I, Is; gs = 0: per-row int4 scale */
+    int   router_bf16;                           /* router element type: 1 bf16, 0 f32 */
+} LagHipMoeDesc;
+
+/* Device pointers of one layer.  Experts in the reference container layout
+ * (c/laguna.c:586-588; docs/laguna.md:34-44); router from lag_hip_router_upload. */
+typedef struct {
+    const void  *router;
+    const float *corr_bias;     /* [E] e_score_correction_bias (selection only) or NULL */
+    const float *logit_bias;    /* [E] added to the router logits (a router-hook wrapper) or NULL */
+    const void  *gu_q;
+    const float *gu_s;
+    const void  *dn_q;
+    const float *dn_s;
+    const void  *sg, *su, *sd;  /* bf16 shared expert [Is,D],[Is,D],[D,Is] or NULL */
+} LagHipMoeWeights;
+
+/* Upload a router [E,D] (bf16 or f32, host) into the chain-major device order
+ * the routing kernel reads.  NULL = error.  Free with lag_hip_free. */
+void  *lag_hip_router_upload(const void *W, int E, int D, int w_bf16);
+/* the same transform from a device router W [E,D] into device Wc (0 = ok) */
+int    lag_hip_router_chain(const void *W, void *Wc, int E, int D, int w_bf16);
+/* out[S,D] += MoE(x[S,D]) for S tokens (device pointers), queued on the
+ * backend stream; S == 1 runs the per-token path, S > 1 the grouped path
+ * (bit-identical per token).  0 = ok. */
+int    lag_hip_moe_forward(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const float *x, float *out, int S);
+/* the same with host x/out; synchronous */
+int    lag_hip_moe_block(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const float *x, float *out, int S);
+/* routing only (device pointers): logits [S,E] (may be NULL), sel [S,K], w [S,K] */
+int    lag_hip_route(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const float *x, int S,
+                     float *logits, int *sel, float *wts);
+/* last routing's expert groups (device pointers of the backend's scratch;
+ * valid until the next forward): G (host out), gexp/gbeg/gcnt [G] host copies */
+int    lag_hip_last_groups(int *G, int *gexp, int *gbeg, int *gcnt, int cap);
+
+/* ---------------- memory, stream, timing ---------------- */
+void  *lag_hip_alloc(size_t n);
+int    lag_hip_h2d(void *dst, const void *src, size_t n);
+int    lag_hip_d2h(void *dst, const void *src, size_t n);
+int    lag_hip_memset(void *dst, int v, size_t n);
+int    lag_hip_sync(void);
+void  *lag_hip_event_create(void);
+int    lag_hip_event_record(void *ev);
+float  lag_hip_event_elapsed_ms(void *start, void *end);
+void   lag_hip_event_destroy(void *ev);
+
+/* per-kernel timing with events on the backend stream (the analogue of the
+ * reference's COLI_CUDA_PROFILE=1, c/backend_cuda.cu:822-940) */
+int    lag_hip_profile(int enable);
+int    lag_hip_profile_count(void);
+int    lag_hip_profile_read(int idx, char *name, int cap, double *total_ms, long long *launches);
+void   lag_hip_profile_reset(void);
+
+/* ---------------- synthetic data (bit-identical to the host generator) ---------------- */
+int    lag_hip_gen_normal(float *out, int64_t n, uint64_t seed, uint64_t offset, double sigma, int to_bf16);
+int    lag_hip_gen_bf16(uint16_t *out, int64_t n, uint64_t seed, uint64_t offset, double sigma);
+int    lag_hip_gen_q4(uint8_t *q, float *s, uint64_t seed, double sigma, int64_t row0, int64_t nrows, int K, int gs);
+
+/* ---------------- diagnostics ---------------- */
+/* MFMA lane-layout probe + libm evaluation on n host inputs; out_host gets
+ * 512 + 2n floats (see k_route.hip).  0 = ran */
+int    lag_hip_selftest(float *out_host, const float *xin_host, int n);
+const char *lag_hip_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

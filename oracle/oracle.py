@@ -60,6 +60,8 @@ class Oracle:
         for f in ("sw_siluf", "sw_softplusf", "sw_sigmoidf"):
             getattr(L, f).restype = C.c_float; getattr(L, f).argtypes = [C.c_float]
         L.sw_softmax_row.argtypes = [F32P, C.c_int]
+        L.sw_expf_array.argtypes = [F32P, F32P, C.c_int64]
+        L.sw_log1pf_array.argtypes = [F32P, F32P, C.c_int64]
         L.sw_moe_topk.argtypes = [F32P, C.c_void_p, C.c_int, C.c_int, C.c_int, I32P]
         L.sw_rmsnorm_row.argtypes = [F32P, F32P, F32P, C.c_int, C.c_float]
         L.sw_argmax.restype = C.c_int; L.sw_argmax.argtypes = [F32P, C.c_int]
@@ -135,6 +137,16 @@ class Oracle:
         x = np.ascontiguousarray(x, np.float32).copy()
         self.lib.sw_softmax_row(x, x.size)
         return x
+
+    def expf(self, x):
+        x = np.ascontiguousarray(x, np.float32); y = np.empty_like(x)
+        self.lib.sw_expf_array(y, x, x.size)
+        return y
+
+    def log1pf(self, x):
+        x = np.ascontiguousarray(x, np.float32); y = np.empty_like(x)
+        self.lib.sw_log1pf_array(y, x, x.size)
+        return y
 
     def topk(self, score, K, bias=None):
         sel = np.empty(K, np.int32)

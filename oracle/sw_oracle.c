@@ -350,6 +350,10 @@ float sw_siluf(float x) { return x / (1.f + expf(-x)); }                        
 float sw_softplusf(float x) { return x > 20.f ? x : log1pf(expf(x)); }           /* c/moe_math.h:54 */
 float sw_sigmoidf(float x) { return 1.f / (1.f + expf(-x)); }                    /* c/moe_block.h:26 */
 
+/* host libm over arrays (the values the device restatements must reproduce) */
+void sw_expf_array(float *y, const float *x, int64_t n) { for (int64_t i = 0; i < n; i++) y[i] = expf(x[i]); }
+void sw_log1pf_array(float *y, const float *x, int64_t n) { for (int64_t i = 0; i < n; i++) y[i] = log1pf(x[i]); }
+
 /* c/moe_math.h:68-72: max, expf(x-mx) summed in double, (float)(1/s) multiply */
 void sw_softmax_row(float *x, int n) {
     float mx = x[0]; for (int i = 1; i < n; i++) if (x[i] > mx) mx = x[i];

@@ -58,6 +58,8 @@ void sw_matmul_q4(float *y, const float *x, const uint8_t *packed, const float *
                   int S, int I, int O, int mode, int exact);
 void sw_matmul_i4_grouped(float *y, const float *x, const uint8_t *q4, const float *scale,
                           int S, int I, int O, int gs);
+void  sw_expf_array(float *y, const float *x, int64_t n);
+void  sw_log1pf_array(float *y, const float *x, int64_t n);
 float sw_siluf(float x);
 float sw_softplusf(float x);
 float sw_sigmoidf(float x);

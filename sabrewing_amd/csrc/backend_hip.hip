@@ -1,0 +1,569 @@
+// backend_hip.hip -- host side of the gfx950 MoE backend (include/sabrewing_hip.h).
+//
+// Replaces c/backend_cuda_laguna.cu's host code.  Same process model: one
+// device, one stream, pinned staging grown on demand, results of the
+// host-pointer entries valid on return.  Different inside: every MoE entry is
+// a fixed short sequence of launches over device-side groups (no per-expert
+// launch loop, no host bounce of intermediate results), and the device-side
+// forward keeps routing, bucketing and the combine on the GPU.
+#include "sw_hip.h"
+#include "../../include/sabrewing_hip.h"
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#include <vector>
+#include <string>
+
+static int g_ok = 0;
+static int g_dev = 0;
+static hipStream_t g_st = nullptr;
+static char g_err[256] = "";
+
+static int fail(const char *what, hipError_t e) {
+    snprintf(g_err, sizeof g_err, "%s: %s", what, hipGetErrorString(e));
+    fprintf(stderr, "[sabrewing-hip] %s\n", g_err);
+    (void)hipGetLastError();                     // consume the sticky error
+    return -1;
+}
+#define CK(call, what)                        \
+    do {                                      \
+        hipError_t e_ = (call);               \
+        if (e_ != hipSuccess) return fail(what, e_); \
+    } while (0)
+static int fail_msg(const char *what) {
+    snprintf(g_err, sizeof g_err, "%s", what);
+    return -1;
+}
+
+// COLI_GPU_FAIL_AFTER=N: compute entries report failure after N successful calls
+static long g_calls = 0;
+static int fault_injected(void) {
+    const char *fa = getenv("COLI_GPU_FAIL_AFTER");
+    return fa && g_calls++ >= atol(fa);
+}
+
+// ------------------------------------------------------------ profiling ----
+struct ProfRec { std::string name; double ms; long long n; };
+struct Pending { int rec; hipEvent_t a, b; };
+static int g_prof = 0;
+static std::vector<ProfRec> g_prof_recs;
+static std::vector<Pending> g_pending;
+static std::vector<hipEvent_t> g_evpool;
+
+static hipEvent_t ev_get(void) {
+    if (!g_evpool.empty()) { hipEvent_t e = g_evpool.back(); g_evpool.pop_back(); return e; }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+}
+static int prof_rec(const char *name) {
+    for (size_t i = 0; i < g_prof_recs.size(); i++) if (g_prof_recs[i].name == name) return (int)i;
+    g_prof_recs.push_back({name, 0.0, 0});
+    return (int)g_prof_recs.size() - 1;
+}
+static void prof_flush(void) {
+    if (g_pending.empty()) return;
+    (void)hipStreamSynchronize(g_st);
+    for (auto &p : g_pending) {
+        float ms = 0.f;
+        if (hipEventElapsedTime(&ms, p.a, p.b) == hipSuccess) { g_prof_recs[p.rec].ms += ms; g_prof_recs[p.rec].n++; }
+        g_evpool.push_back(p.a); g_evpool.push_back(p.b);
+    }
+    g_pending.clear();
+}
+// bracket one launch with events when profiling
+struct ProfScope {
+    Pending p; bool on;
+    ProfScope(const char *name) : on(g_prof != 0) {
+        if (!on) return;
+        p.rec = prof_rec(name); p.a = ev_get(); p.b = ev_get();
+        if (!p.a || !p.b) { on = false; return; }
+        (void)hipEventRecord(p.a, g_st);
+    }
+    ~ProfScope() {
+        if (!on) return;
+        (void)hipEventRecord(p.b, g_st);
+        g_pending.push_back(p);
+        if (g_pending.size() > 4096) prof_flush();
+    }
+};
+#define PROF(name) ProfScope prof_scope_(name)
+
+// ------------------------------------------------------------ buffers ----
+// grow-only device arena and pinned staging (2x slack, as the reference)
+struct Buf { void *p = nullptr; size_t cap = 0; };
+static int grow_dev(Buf &b, size_t need) {
+    if (need <= b.cap) return 0;
+    if (b.p) (void)hipFree(b.p);
+    b.p = nullptr; b.cap = 0;
+    CK(hipMalloc(&b.p, need * 2), "device scratch allocation");
+    b.cap = need * 2;
+    return 0;
+}
+static int grow_pinned(Buf &b, size_t need) {
+    if (need <= b.cap) return 0;
+    if (b.p) (void)hipHostFree(b.p);
+    b.p = nullptr; b.cap = 0;
+    CK(hipHostMalloc(&b.p, need * 2, hipHostMallocDefault), "pinned staging allocation");
+    b.cap = need * 2;
+    return 0;
+}
+static Buf g_arena, g_hin, g_hout, g_consts;
+static int g_consts_k = 0;
+
+// carve aligned sub-buffers out of the arena
+struct Carve {
+    size_t off = 0;
+    size_t take(size_t n) { size_t o = (off + 255) & ~(size_t)255; off = o + n; return o; }
+};
+
+static int ensure_consts(int K) {   // iota[K], ones[K], zeros[K]
+    if (K <= g_consts_k) return 0;
+    int k = K < 64 ? 64 : K;
+    if (grow_dev(g_consts, (size_t)3 * k * sizeof(int))) return -1;
+    std::vector<int> h((size_t)3 * k);
+    for (int i = 0; i < k; i++) { h[i] = i; h[k + i] = 1; h[2 * k + i] = 0; }
+    CK(hipMemcpy(g_consts.p, h.data(), h.size() * sizeof(int), hipMemcpyHostToDevice), "constant upload");
+    g_consts_k = k;
+    return 0;
+}
+static const int *c_iota(void) { return (const int *)g_consts.p; }
+static const int *c_ones(void) { return (const int *)g_consts.p + g_consts_k; }
+static const int *c_zeros(void) { return (const int *)g_consts.p + 2 * g_consts_k; }
+
+// ------------------------------------------------------------ lag family ----
+extern "C" int lag_hip_init(int dev) {
+    if (g_ok && dev == g_dev) return 0;
+    CK(hipSetDevice(dev), "hipSetDevice");
+    if (!g_st) CK(hipStreamCreateWithFlags(&g_st, hipStreamNonBlocking), "stream creation");
+    void *probe = nullptr;
+    CK(hipMalloc(&probe, 1 << 20), "probe allocation");
+    (void)hipFree(probe);
+    g_dev = dev;
+    g_ok = 1;
+    return 0;
+}
+
+extern "C" size_t lag_hip_free_bytes(void) {
+    size_t fr = 0, to = 0;
+    if (hipMemGetInfo(&fr, &to) != hipSuccess) { (void)hipGetLastError(); return 0; }
+    return fr;
+}
+extern "C" size_t lag_hip_total_bytes(void) {
+    size_t fr = 0, to = 0;
+    if (hipMemGetInfo(&fr, &to) != hipSuccess) { (void)hipGetLastError(); return 0; }
+    return to;
+}
+
+extern "C" void *lag_hip_upload(const void *h, size_t n) {
+    if (!g_ok || !h || !n) return nullptr;
+    void *d = nullptr;
+    if (hipMalloc(&d, n) != hipSuccess) { fail("upload allocation", hipErrorOutOfMemory); return nullptr; }
+    if (hipMemcpy(d, h, n, hipMemcpyHostToDevice) != hipSuccess) { (void)hipFree(d); fail("upload copy", hipErrorUnknown); return nullptr; }
+    return d;
+}
+extern "C" void lag_hip_free(void *d) { if (d) (void)hipFree(d); }
+
+extern "C" void *lag_hip_alloc(size_t n) {
+    if (!g_ok || !n) return nullptr;
+    void *d = nullptr;
+    if (hipMalloc(&d, n) != hipSuccess) { fail("alloc", hipErrorOutOfMemory); return nullptr; }
+    return d;
+}
+extern "C" int lag_hip_h2d(void *dst, const void *src, size_t n) {
+    if (!g_ok) return -1;
+    CK(hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, g_st), "h2d");
+    CK(hipStreamSynchronize(g_st), "h2d sync");
+    return 0;
+}
+extern "C" int lag_hip_d2h(void *dst, const void *src, size_t n) {
+    if (!g_ok) return -1;
+    CK(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, g_st), "d2h");
+    CK(hipStreamSynchronize(g_st), "d2h sync");
+    return 0;
+}
+extern "C" int lag_hip_memset(void *dst, int v, size_t n) {
+    if (!g_ok) return -1;
+    CK(hipMemsetAsync(dst, v, n, g_st), "memset");
+    return 0;
+}
+extern "C" int lag_hip_sync(void) {
+    if (!g_ok) return -1;
+    CK(hipStreamSynchronize(g_st), "stream sync");
+    if (g_prof) prof_flush();
+    return 0;
+}
+
+// the int4 expert pipeline over device groups:
+//   xplanes <- x;  h <- silu_glu(gate_up . x);  slots <- down . h
+static int run_experts(SwQ4 gu, SwQ4 dn, const float *dx, int S, SwGroups g, int T, int I, int D,
+                       _Float16 *xpl, _Float16 *hpl, float *slots, int cb) {
+    { PROF("prep_f16"); if (sw_launch_prep_f16(g_st, dx, S, D, xpl)) return fail_msg("prep launch"); }
+    { PROF("q4_gateup_glu"); if (sw_launch_q4_gateup(g_st, gu, xpl, g, I, hpl, cb)) return fail_msg("gate_up launch (shape unsupported?)"); }
+    SwGroups gd = g;
+    gd.grow = nullptr;                     // down reads the packed rows directly
+    (void)T;
+    { PROF("q4_down"); if (sw_launch_q4_rows(g_st, dn, hpl, gd, slots, cb)) return fail_msg("down launch (shape unsupported?)"); }
+    return 0;
+}
+
+// host-index grouped entry shared by moe_experts / moe_group / expert_q4
+static int grouped_host(float *outh, const float *x, int S, const void *gu_q, const float *gu_s,
+                        const void *dn_q, const float *dn_s, const int *gexp, const int *gbeg, const int *gcnt, int G,
+                        const int *grow, const int *rowof, const float *w, int K, int I, int D, int gs, int combine) {
+    if (!g_ok || fault_injected()) return -1;
+    if (D <= 0 || I <= 0 || G <= 0 || S <= 0) return -1;
+    const int T = S * K;
+    const int ngD = gs > 0 ? D / gs : 1, ngI = gs > 0 ? I / gs : 1;
+    (void)ngD; (void)ngI;
+    Carve cv;
+    const size_t o_x = cv.take((size_t)S * D * 4), o_idx = cv.take((size_t)(3 * G + 2 * T) * 4 + (size_t)T * 4);
+    const size_t o_xpl = cv.take((size_t)2 * S * D * 2), o_hpl = cv.take((size_t)2 * T * I * 2);
+    const size_t o_slot = cv.take((size_t)T * D * 4), o_out = cv.take((size_t)S * D * 4);
+    if (grow_dev(g_arena, cv.off)) return -1;
+    char *A = (char *)g_arena.p;
+    // one pinned blob: x | gexp gbeg gcnt grow rowof w
+    const size_t xn = (size_t)S * D * 4, idxn = (size_t)(3 * G + 2 * T) * 4 + (size_t)T * 4;
+    if (grow_pinned(g_hin, xn + idxn) || grow_pinned(g_hout, (size_t)S * D * 4)) return -1;
+    char *H = (char *)g_hin.p;
+    memcpy(H, x, xn);
+    int *hi = (int *)(H + xn);
+    memcpy(hi, gexp, (size_t)G * 4);
+    memcpy(hi + G, gbeg, (size_t)G * 4);
+    memcpy(hi + 2 * G, gcnt, (size_t)G * 4);
+    memcpy(hi + 3 * G, grow, (size_t)T * 4);
+    memcpy(hi + 3 * G + T, rowof, (size_t)T * 4);
+    memcpy(hi + 3 * G + 2 * T, w, (size_t)T * 4);
+    CK(hipMemcpyAsync(A + o_x, H, xn, hipMemcpyHostToDevice, g_st), "x upload");
+    CK(hipMemcpyAsync(A + o_idx, H + xn, idxn, hipMemcpyHostToDevice, g_st), "index upload");
+    const int *d_gexp = (const int *)(A + o_idx), *d_gbeg = d_gexp + G, *d_gcnt = d_gexp + 2 * G;
+    const int *d_grow = d_gexp + 3 * G, *d_rowof = d_grow + T;
+    const float *d_w = (const float *)(d_rowof + T);
+    SwQ4 gu = {(const uint8_t *)gu_q, gu_s, 2 * I, D, gs};
+    SwQ4 dn = {(const uint8_t *)dn_q, dn_s, D, I, gs};
+    SwGroups g = {d_gexp, d_gbeg, d_gcnt, d_grow, nullptr, G};
+    int maxcnt = 0;
+    for (int i = 0; i < G; i++) maxcnt = gcnt[i] > maxcnt ? gcnt[i] : maxcnt;
+    if (run_experts(gu, dn, (const float *)(A + o_x), S, g, T, I, D, (_Float16 *)(A + o_xpl), (_Float16 *)(A + o_hpl),
+                    (float *)(A + o_slot), maxcnt > 1 ? 4 : 1)) return -1;
+    const float *res = (const float *)(A + o_slot);
+    if (combine) {
+        PROF("combine");
+        if (sw_launch_combine(g_st, (const float *)(A + o_slot), d_rowof, d_w, S, K, D, 1.0f, nullptr,
+                              (float *)(A + o_out), 0)) return fail_msg("combine launch");
+        res = (const float *)(A + o_out);
+    }
+    CK(hipMemcpyAsync(g_hout.p, res, (size_t)S * D * 4, hipMemcpyDeviceToHost, g_st), "result download");
+    CK(hipStreamSynchronize(g_st), "stream sync");
+    memcpy(outh, g_hout.p, (size_t)S * D * 4);
+    if (g_prof) prof_flush();
+    return 0;
+}
+
+extern "C" int lag_hip_moe_group_g(float *acc, const float *x, const void *gu_q, const float *gu_s,
+                                   const void *dn_q, const float *dn_s, const int *gexp, const int *gbeg,
+                                   const int *gcnt, int G, const int *grow, const int *rowof, const float *w,
+                                   int S, int K, int I, int D, int gs) {
+    if ((D & 1) || (I & 1)) return -1;
+    return grouped_host(acc, x, S, gu_q, gu_s, dn_q, dn_s, gexp, gbeg, gcnt, G, grow, rowof, w, K, I, D, gs, 1);
+}
+extern "C" int lag_hip_moe_group(float *acc, const float *x, const void *gu_q, const float *gu_s,
+                                 const void *dn_q, const float *dn_s, const int *gexp, const int *gbeg,
+                                 const int *gcnt, int G, const int *grow, const int *rowof, const float *w,
+                                 int S, int K, int I, int D) {
+    return lag_hip_moe_group_g(acc, x, gu_q, gu_s, dn_q, dn_s, gexp, gbeg, gcnt, G, grow, rowof, w, S, K, I, D, 0);
+}
+
+extern "C" int lag_hip_moe_experts_g(float *out, const float *x, const void *gu_q, const float *gu_s,
+                                     const void *dn_q, const float *dn_s, const int *sel, const float *w,
+                                     int K, int I, int D, int gs) {
+    if (K <= 0 || K > 1024 || (D & 1) || (I & 1)) return -1;
+    std::vector<int> gbeg(K), gcnt(K, 1), grow(K, 0), rowof(K);
+    for (int a = 0; a < K; a++) { gbeg[a] = a; rowof[a] = a; }
+    return grouped_host(out, x, 1, gu_q, gu_s, dn_q, dn_s, sel, gbeg.data(), gcnt.data(), K, grow.data(), rowof.data(),
+                        w, K, I, D, gs, 1);
+}
+extern "C" int lag_hip_moe_experts(float *out, const float *x, const void *gu_q, const float *gu_s,
+                                   const void *dn_q, const float *dn_s, const int *sel, const float *w,
+                                   int K, int I, int D) {
+    return lag_hip_moe_experts_g(out, x, gu_q, gu_s, dn_q, dn_s, sel, w, K, I, D, 0);
+}
+
+extern "C" int lag_hip_expert_q4_g(float *out, const float *x, const void *p13, const void *s13,
+                                   const void *p2, const void *s2, int I, int D, int gs) {
+    const int zero = 0, one = 1;
+    const float wone = 1.0f;
+    return grouped_host(out, x, 1, p13, (const float *)s13, p2, (const float *)s2, &zero, &zero, &one, 1, &zero, &zero,
+                        &wone, 1, I, D, gs, 0);
+}
+extern "C" int lag_hip_expert_q4(float *out, const float *x, const void *p13, const void *s13,
+                                 const void *p2, const void *s2, int I, int D) {
+    return lag_hip_expert_q4_g(out, x, p13, s13, p2, s2, I, D, 0);
+}
+
+extern "C" int lag_hip_matmul_q4_g(float *y, const float *x, const void *packed, const void *scale,
+                                   int S, int I, int O, int gs) {
+    if (!g_ok || fault_injected()) return -1;
+    if (S <= 0 || I <= 0 || O <= 0) return -1;
+    Carve cv;
+    const size_t o_x = cv.take((size_t)S * I * 4), o_idx = cv.take(16), o_xpl = cv.take((size_t)2 * S * I * 2);
+    const size_t o_y = cv.take((size_t)S * O * 4);
+    if (grow_dev(g_arena, cv.off) || grow_pinned(g_hin, (size_t)S * I * 4 + 16) || grow_pinned(g_hout, (size_t)S * O * 4)) return -1;
+    char *A = (char *)g_arena.p, *H = (char *)g_hin.p;
+    memcpy(H, x, (size_t)S * I * 4);
+    int *hi = (int *)(H + (size_t)S * I * 4);
+    hi[0] = 0; hi[1] = 0; hi[2] = S;
+    CK(hipMemcpyAsync(A + o_x, H, (size_t)S * I * 4, hipMemcpyHostToDevice, g_st), "x upload");
+    CK(hipMemcpyAsync(A + o_idx, hi, 12, hipMemcpyHostToDevice, g_st), "index upload");
+    const int *d = (const int *)(A + o_idx);
+    SwGroups g = {d, d + 1, d + 2, nullptr, nullptr, 1};
+    SwQ4 W = {(const uint8_t *)packed, (const float *)scale, O, I, gs};
+    { PROF("prep_f16"); if (sw_launch_prep_f16(g_st, (const float *)(A + o_x), S, I, (_Float16 *)(A + o_xpl))) return fail_msg("prep launch"); }
+    { PROF("q4_rows"); if (sw_launch_q4_rows(g_st, W, (const _Float16 *)(A + o_xpl), g, (float *)(A + o_y), S > 1 ? 4 : 1)) return fail_msg("q4 launch (shape unsupported?)"); }
+    CK(hipMemcpyAsync(g_hout.p, A + o_y, (size_t)S * O * 4, hipMemcpyDeviceToHost, g_st), "result download");
+    CK(hipStreamSynchronize(g_st), "stream sync");
+    memcpy(y, g_hout.p, (size_t)S * O * 4);
+    if (g_prof) prof_flush();
+    return 0;
+}
+extern "C" int lag_hip_matmul_q4(float *y, const float *x, const void *packed, const void *scale, int S, int I, int O) {
+    if (I & 1) return -1;
+    return lag_hip_matmul_q4_g(y, x, packed, scale, S, I, O, 0);
+}
+
+extern "C" int lag_hip_matmul_bf16(float *y, const float *x, const void *W, int S, int I, int O) {
+    if (!g_ok || fault_injected() || (I & 1)) return -1;
+    if (S <= 0 || I <= 0 || O <= 0) return -1;
+    Carve cv;
+    const size_t o_x = cv.take((size_t)S * I * 4), o_xpl = cv.take((size_t)2 * S * I * 2), o_y = cv.take((size_t)S * O * 4);
+    if (grow_dev(g_arena, cv.off) || grow_pinned(g_hin, (size_t)S * I * 4) || grow_pinned(g_hout, (size_t)S * O * 4)) return -1;
+    char *A = (char *)g_arena.p;
+    memcpy(g_hin.p, x, (size_t)S * I * 4);
+    CK(hipMemcpyAsync(A + o_x, g_hin.p, (size_t)S * I * 4, hipMemcpyHostToDevice, g_st), "x upload");
+    SwBf16 Wt = {(const uint16_t *)W, O, I};
+    { PROF("prep_bf16"); if (sw_launch_prep_bf16(g_st, (const float *)(A + o_x), S, I, (uint16_t *)(A + o_xpl))) return fail_msg("prep launch"); }
+    { PROF("bf16_rows"); if (sw_launch_bf16_rows(g_st, Wt, (const uint16_t *)(A + o_xpl), S, (float *)(A + o_y))) return fail_msg("bf16 launch (shape unsupported?)"); }
+    CK(hipMemcpyAsync(g_hout.p, A + o_y, (size_t)S * O * 4, hipMemcpyDeviceToHost, g_st), "result download");
+    CK(hipStreamSynchronize(g_st), "stream sync");
+    memcpy(y, g_hout.p, (size_t)S * O * 4);
+    if (g_prof) prof_flush();
+    return 0;
+}
+
+// ------------------------------------------------------------ device MoE block ----
+extern "C" void *lag_hip_router_upload(const void *W, int E, int D, int w_bf16) {
+    if (!g_ok || !W || E <= 0 || D % 128) return nullptr;
+    const size_t n = (size_t)E * D * (w_bf16 ? 2 : 4);
+    void *tmp = lag_hip_upload(W, n);
+    if (!tmp) return nullptr;
+    void *out = nullptr;
+    if (hipMalloc(&out, n) != hipSuccess) { (void)hipFree(tmp); fail("router allocation", hipErrorOutOfMemory); return nullptr; }
+    if (sw_launch_chain_major(g_st, tmp, w_bf16, E, D, out) || hipStreamSynchronize(g_st) != hipSuccess) {
+        (void)hipFree(tmp); (void)hipFree(out); fail("router transform", hipErrorUnknown); return nullptr;
+    }
+    (void)hipFree(tmp);
+    return out;
+}
+
+extern "C" int lag_hip_router_chain(const void *W, void *Wc, int E, int D, int w_bf16) {
+    if (!g_ok || !W || !Wc) return -1;
+    if (sw_launch_chain_major(g_st, W, w_bf16, E, D, Wc)) return fail_msg("router transform launch");
+    return 0;
+}
+
+struct FwdScratch {
+    float *logits, *w, *slots, *sout;
+    int *sel, *gexp, *gbeg, *gcnt, *G, *grow, *rowof;
+    _Float16 *xpl, *hpl;
+    uint16_t *xbpl, *shpl;
+};
+static int g_last_G_dev = 0;            // 1: last forward's groups live in the arena
+static FwdScratch g_last;
+static int g_last_ng = 0;
+
+static int desc_ok(const LagHipMoeDesc *d, const LagHipMoeWeights *w) {
+    if (!d || !w) return 0;
+    if (d->n_experts <= 0 || d->topk <= 0 || d->topk > d->n_experts || d->topk > 64) return 0;
+    if (d->hidden % 128 || d->moe_inter % 128) return 0;
+    if (d->gs > 0 && (d->gs % 32 || d->hidden % d->gs || d->moe_inter % d->gs)) return 0;
+    if (d->shared_mode && (!w->sg || !w->su || !w->sd || d->shared_inter % 128)) return 0;
+    if (!w->router || !w->gu_q || !w->gu_s || !w->dn_q || !w->dn_s) return 0;
+    return 1;
+}
+
+static int carve_fwd(const LagHipMoeDesc *d, int S, FwdScratch &f) {
+    const int E = d->n_experts, K = d->topk, D = d->hidden, I = d->moe_inter, Is = d->shared_inter;
+    const int T = S * K;
+    Carve cv;
+    const size_t o_lg = cv.take((size_t)S * E * 4), o_sel = cv.take((size_t)T * 4), o_w = cv.take((size_t)T * 4);
+    const size_t o_gexp = cv.take((size_t)E * 4), o_gbeg = cv.take((size_t)E * 4), o_gcnt = cv.take((size_t)E * 4);
+    const size_t o_G = cv.take(4), o_grow = cv.take((size_t)T * 4), o_rowof = cv.take((size_t)T * 4);
+    const size_t o_xpl = cv.take((size_t)2 * S * D * 2), o_hpl = cv.take((size_t)2 * T * I * 2);
+    const size_t o_slot = cv.take((size_t)T * D * 4);
+    size_t o_xb = 0, o_sh = 0, o_so = 0;
+    if (d->shared_mode) {
+        o_xb = cv.take((size_t)2 * S * D * 2); o_sh = cv.take((size_t)2 * S * Is * 2); o_so = cv.take((size_t)S * D * 4);
+    }
+    if (grow_dev(g_arena, cv.off)) return -1;
+    char *A = (char *)g_arena.p;
+    f.logits = (float *)(A + o_lg); f.sel = (int *)(A + o_sel); f.w = (float *)(A + o_w);
+    f.gexp = (int *)(A + o_gexp); f.gbeg = (int *)(A + o_gbeg); f.gcnt = (int *)(A + o_gcnt); f.G = (int *)(A + o_G);
+    f.grow = (int *)(A + o_grow); f.rowof = (int *)(A + o_rowof);
+    f.xpl = (_Float16 *)(A + o_xpl); f.hpl = (_Float16 *)(A + o_hpl); f.slots = (float *)(A + o_slot);
+    f.xbpl = d->shared_mode ? (uint16_t *)(A + o_xb) : nullptr;
+    f.shpl = d->shared_mode ? (uint16_t *)(A + o_sh) : nullptr;
+    f.sout = d->shared_mode ? (float *)(A + o_so) : nullptr;
+    return 0;
+}
+
+static int route_dev(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const float *x, int S, float *logits, int *sel, float *wts) {
+    { PROF("router");
+      if (sw_launch_router(g_st, w->router, d->router_bf16, x, S, d->hidden, d->n_experts, w->logit_bias, logits))
+          return fail_msg("router launch"); }
+    { PROF("gate_topk");
+      if (sw_launch_gate_topk(g_st, logits, S, d->n_experts, d->topk, d->route_act, w->corr_bias, d->use_corr_bias,
+                              d->norm_topk, sel, wts)) return fail_msg("gate/top-k launch"); }
+    return 0;
+}
+
+extern "C" int lag_hip_route(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const float *x, int S,
+                             float *logits, int *sel, float *wts) {
+    if (!g_ok || fault_injected() || !desc_ok(d, w) || S <= 0) return -1;
+    FwdScratch f;
+    if (carve_fwd(d, S, f)) return -1;
+    return route_dev(d, w, x, S, logits ? logits : f.logits, sel, wts);
+}
+
+extern "C" int lag_hip_moe_forward(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const float *x, float *out, int S) {
+    if (!g_ok || fault_injected()) return -1;
+    if (!desc_ok(d, w) || S <= 0) return fail_msg("moe_forward: unsupported descriptor/shape");
+    const int E = d->n_experts, K = d->topk, D = d->hidden, I = d->moe_inter, Is = d->shared_inter;
+    const int T = S * K;
+    FwdScratch f;
+    if (carve_fwd(d, S, f) || ensure_consts(K)) return -1;
+    if (route_dev(d, w, x, S, f.logits, f.sel, f.w)) return -1;
+    SwGroups g;
+    if (S == 1) {                        // per-token: groups are the K picks in rank order
+        g = {f.sel, c_iota(), c_ones(), c_zeros(), nullptr, K};
+    } else {
+        PROF("bucket");
+        if (sw_launch_bucket(g_st, f.sel, S, K, E, f.gexp, f.gbeg, f.gcnt, f.G, f.grow, f.rowof)) return fail_msg("bucket launch");
+        g = {f.gexp, f.gbeg, f.gcnt, f.grow, f.G, T < E ? T : E};
+    }
+    SwQ4 gu = {(const uint8_t *)w->gu_q, w->gu_s, 2 * I, D, d->gs};
+    SwQ4 dn = {(const uint8_t *)w->dn_q, w->dn_s, D, I, d->gs};
+    if (run_experts(gu, dn, x, S, g, T, I, D, f.xpl, f.hpl, f.slots, S > 1 ? 4 : 1)) return -1;
+    const float *shared = nullptr;
+    if (d->shared_mode) {
+        SwBf16 sg = {(const uint16_t *)w->sg, Is, D}, su = {(const uint16_t *)w->su, Is, D}, sd = {(const uint16_t *)w->sd, D, Is};
+        { PROF("prep_bf16"); if (sw_launch_prep_bf16(g_st, x, S, D, f.xbpl)) return fail_msg("prep launch"); }
+        { PROF("shared_gateup_glu"); if (sw_launch_bf16_gateup(g_st, sg, su, f.xbpl, S, f.shpl)) return fail_msg("shared gate_up launch"); }
+        { PROF("shared_down"); if (sw_launch_bf16_rows(g_st, sd, f.shpl, S, f.sout)) return fail_msg("shared down launch"); }
+        shared = f.sout;
+    }
+    { PROF("combine");
+      if (sw_launch_combine(g_st, f.slots, S == 1 ? c_iota() : f.rowof, f.w, S, K, D, d->route_scale, shared, out, 1))
+          return fail_msg("combine launch"); }
+    g_last = f; g_last_G_dev = S > 1; g_last_ng = S == 1 ? K : 0;
+    return 0;
+}
+
+extern "C" int lag_hip_last_groups(int *G, int *gexp, int *gbeg, int *gcnt, int cap) {
+    if (!g_ok) return -1;
+    CK(hipStreamSynchronize(g_st), "stream sync");
+    if (!g_last_G_dev) { *G = g_last_ng; return 0; }
+    CK(hipMemcpy(G, g_last.G, 4, hipMemcpyDeviceToHost), "G download");
+    const int n = *G < cap ? *G : cap;
+    if (n > 0) {
+        CK(hipMemcpy(gexp, g_last.gexp, (size_t)n * 4, hipMemcpyDeviceToHost), "gexp download");
+        CK(hipMemcpy(gbeg, g_last.gbeg, (size_t)n * 4, hipMemcpyDeviceToHost), "gbeg download");
+        CK(hipMemcpy(gcnt, g_last.gcnt, (size_t)n * 4, hipMemcpyDeviceToHost), "gcnt download");
+    }
+    return 0;
+}
+
+extern "C" int lag_hip_moe_block(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const float *x, float *out, int S) {
+    if (!g_ok || !d || S <= 0) return -1;
+    static Buf dx, dout;
+    const size_t n = (size_t)S * d->hidden * 4;
+    if (grow_dev(dx, n) || grow_dev(dout, n) || grow_pinned(g_hin, n) || grow_pinned(g_hout, n)) return -1;
+    memcpy(g_hin.p, x, n);
+    memcpy(g_hout.p, out, n);
+    CK(hipMemcpyAsync(dx.p, g_hin.p, n, hipMemcpyHostToDevice, g_st), "x upload");
+    CK(hipMemcpyAsync(dout.p, g_hout.p, n, hipMemcpyHostToDevice, g_st), "out upload");
+    if (lag_hip_moe_forward(d, w, (const float *)dx.p, (float *)dout.p, S)) return -1;
+    CK(hipMemcpyAsync(g_hout.p, dout.p, n, hipMemcpyDeviceToHost, g_st), "out download");
+    CK(hipStreamSynchronize(g_st), "stream sync");
+    memcpy(out, g_hout.p, n);
+    if (g_prof) prof_flush();
+    return 0;
+}
+
+// ------------------------------------------------------------ events / profile ----
+extern "C" void *lag_hip_event_create(void) {
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return (void *)e;
+}
+extern "C" int lag_hip_event_record(void *ev) {
+    if (!g_ok || !ev) return -1;
+    CK(hipEventRecord((hipEvent_t)ev, g_st), "event record");
+    return 0;
+}
+extern "C" float lag_hip_event_elapsed_ms(void *a, void *b) {
+    float ms = -1.f;
+    if (hipEventSynchronize((hipEvent_t)b) != hipSuccess) return -1.f;
+    if (hipEventElapsedTime(&ms, (hipEvent_t)a, (hipEvent_t)b) != hipSuccess) return -1.f;
+    return ms;
+}
+extern "C" void lag_hip_event_destroy(void *ev) { if (ev) (void)hipEventDestroy((hipEvent_t)ev); }
+
+extern "C" int lag_hip_profile(int enable) {
+    if (!enable) prof_flush();
+    g_prof = enable ? 1 : 0;
+    return 0;
+}
+extern "C" int lag_hip_profile_count(void) { prof_flush(); return (int)g_prof_recs.size(); }
+extern "C" int lag_hip_profile_read(int idx, char *name, int cap, double *total_ms, long long *launches) {
+    prof_flush();
+    if (idx < 0 || idx >= (int)g_prof_recs.size()) return -1;
+    if (name && cap > 0) { strncpy(name, g_prof_recs[idx].name.c_str(), (size_t)cap - 1); name[cap - 1] = 0; }
+    if (total_ms) *total_ms = g_prof_recs[idx].ms;
+    if (launches) *launches = g_prof_recs[idx].n;
+    return 0;
+}
+extern "C" void lag_hip_profile_reset(void) { prof_flush(); g_prof_recs.clear(); }
+
+// ------------------------------------------------------------ generators ----
+extern "C" int lag_hip_gen_normal(float *out, int64_t n, uint64_t seed, uint64_t offset, double sigma, int to_bf16) {
+    if (!g_ok) return -1;
+    if (sw_launch_gen_normal(g_st, out, n, seed, offset, sigma, to_bf16)) return fail_msg("gen launch");
+    return 0;
+}
+extern "C" int lag_hip_gen_bf16(uint16_t *out, int64_t n, uint64_t seed, uint64_t offset, double sigma) {
+    if (!g_ok) return -1;
+    if (sw_launch_gen_bf16(g_st, out, n, seed, offset, sigma)) return fail_msg("gen launch");
+    return 0;
+}
+extern "C" int lag_hip_gen_q4(uint8_t *q, float *s, uint64_t seed, double sigma, int64_t row0, int64_t nrows, int K, int gs) {
+    if (!g_ok) return -1;
+    if (sw_launch_gen_q4(g_st, q, s, seed, sigma, row0, nrows, K, gs)) return fail_msg("gen launch");
+    return 0;
+}
+
+// ------------------------------------------------------------ diagnostics ----
+extern "C" int lag_hip_selftest(float *out_host, const float *xin_host, int n) {
+    if (!g_ok || n < 0) return -1;
+    float *dout = nullptr, *din = nullptr;
+    CK(hipMalloc(&dout, (size_t)(512 + 2 * n) * 4), "selftest alloc");
+    if (n > 0 && hipMalloc(&din, (size_t)n * 4) != hipSuccess) { (void)hipFree(dout); return fail_msg("selftest alloc"); }
+    if (n > 0) CK(hipMemcpy(din, xin_host, (size_t)n * 4, hipMemcpyHostToDevice), "selftest upload");
+    int rc = sw_launch_selftest(g_st, dout, din, n);
+    if (rc == 0 && hipStreamSynchronize(g_st) != hipSuccess) rc = -1;
+    if (rc == 0 && hipMemcpy(out_host, dout, (size_t)(512 + 2 * n) * 4, hipMemcpyDeviceToHost) != hipSuccess) rc = -1;
+    (void)hipFree(dout);
+    if (din) (void)hipFree(din);
+    return rc ? fail_msg("selftest") : 0;
+}
+
+extern "C" const char *lag_hip_last_error(void) { return g_err; }

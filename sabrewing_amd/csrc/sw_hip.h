@@ -1,0 +1,100 @@
+// sw_hip.h -- internal declarations of the gfx950 MoE backend.
+//
+// Device data layout (HBM):
+//   weights    the reference container, unchanged (lag_hip_upload is a plain
+//              byte copy, like lag_cuda_upload): int4 gate_up [E*2I, D/2]
+//              (gate rows then up rows per expert), scales [E*2I, D/gs] f32,
+//              down [E*D, I/2], scales [E*D, I/gs]; bf16 shared expert
+//              [Is,D],[Is,D],[D,Is]; router in "chain-major" order (see below).
+//   x, out     f32 [S, D] (out is accumulated into: out += MoE(x)).
+//   f16 planes activations feeding the int4 MFMA GEMMs as two f16 rows per
+//              token, hi = RN(v) and lo = RN(v - hi) ([2S, K] f16, row 2t hi,
+//              row 2t+1 lo), each 8-element block stored in the order
+//              0,4,1,5,2,6,3,7 so one 16-byte load is one MFMA B fragment.
+//   bf16 planes the same split for the bf16 (shared-expert) GEMMs, natural order.
+//
+// MFMA operand convention for v_mfma_f32_16x16x32_{f16,bf16} (lane l):
+//   A: row l%16, hardware k 8*(l/16)+h for element h of the 8-vector
+//   B: col l%16, same k;   C: col l%16, rows 4*(l/16)+j, j = 0..3
+// (checked on the device by lag_hip_selftest).
+//
+// Per-output reduction contract of every int4 / bf16 GEMM here (B = 1
+// per-token, grouped decode and prefill kernels alike): K is walked in
+// 128-wide super-steps ss, each split into four 32-k MFMAs q = 0..3 (k =
+// 128 ss + 32 kb + 8 q + {0,4,1,5,2,6,3,7} for lane group kb), accumulated
+// in order into one f32 chain per column; the hi and lo columns of a token
+// are added at the end (hi + lo), then scaled (2^-8 weight prescale for group
+// scales, the f32 row scale for per-row scales).  Because no kernel splits K,
+// a token's output does not depend on which other tokens share its launch:
+// the grouped path is bit-identical to the per-token path.
+#ifndef SW_HIP_H
+#define SW_HIP_H
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+typedef _Float16 sw_half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 sw_half2 __attribute__((ext_vector_type(2)));
+typedef __bf16 sw_bf16x8 __attribute__((ext_vector_type(8)));
+typedef float sw_f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t sw_u32x4 __attribute__((ext_vector_type(4)));
+
+#define SW_WAVE 64
+
+static inline int64_t sw_imin64(int64_t a, int64_t b) { return a < b ? a : b; }
+#define SW_WPRESCALE 256.0f          // group-scale weights are stored as f16(s * 2^8 * (n-8))
+#define SW_WPRESCALE_INV 0.00390625f
+
+// ---- work description for the grouped GEMMs ----
+// A "group" is one expert applied to gcnt consecutive packed rows starting at
+// gbeg; packed row j takes its activation from row grow[j] of the input planes
+// (or row j itself when grow is null).
+struct SwGroups {
+    const int *gexp, *gbeg, *gcnt;   // [ngroups]
+    const int *grow;                 // [T] or null
+    const int *G;                    // device count (null: use ngroups_max)
+    int ngroups_max;
+};
+
+// int4 weight tensor of E experts, O rows each, K inputs
+struct SwQ4 {
+    const uint8_t *q;     // [E*O, K/2]
+    const float *s;       // [E*O, ng]
+    int O, K, gs;         // gs = 0: per-row scale
+};
+
+// bf16 weight tensor [O, K]
+struct SwBf16 {
+    const uint16_t *w;
+    int O, K;
+};
+
+// ---- kernels (launch wrappers, all async on `st`) ----
+int sw_launch_prep_f16(hipStream_t st, const float *x, int S, int D, _Float16 *planes);
+int sw_launch_prep_bf16(hipStream_t st, const float *x, int S, int D, uint16_t *planes);
+// logits[S,E] = x @ W^T under the 16-lane FMA-chain contract; Wc chain-major
+int sw_launch_router(hipStream_t st, const void *Wc, int w_bf16, const float *x, int S, int D, int E,
+                     const float *logit_bias, float *logits);
+int sw_launch_gate_topk(hipStream_t st, const float *logits, int S, int E, int K, int route_act,
+                        const float *corr_bias, int use_corr_bias, int norm_topk, int *sel, float *w);
+int sw_launch_bucket(hipStream_t st, const int *sel, int S, int K, int E, int *gexp, int *gbeg,
+                     int *gcnt, int *G, int *grow, int *rowof);
+// out planes of SiLU-GLU(gate, up) for every packed row of every group
+// cb: MFMA column blocks (8 tokens each) kept per pass: 1 for single-token groups, 4 otherwise
+int sw_launch_q4_gateup(hipStream_t st, SwQ4 W, const _Float16 *xplanes, SwGroups g, int I, _Float16 *hplanes, int cb);
+// Y[packed row, O] (f32) for every group
+int sw_launch_q4_rows(hipStream_t st, SwQ4 W, const _Float16 *xplanes, SwGroups g, float *Y, int cb);
+int sw_launch_bf16_gateup(hipStream_t st, SwBf16 Wg, SwBf16 Wu, const uint16_t *xplanes, int S, uint16_t *hplanes);
+int sw_launch_bf16_rows(hipStream_t st, SwBf16 W, const uint16_t *xplanes, int S, float *Y);
+// out[s] (+)= route_scale * sum_a w[s,a] * slots[rowof[s,a]] (+ shared[s])
+int sw_launch_combine(hipStream_t st, const float *slots, const int *rowof, const float *w, int S, int K, int D,
+                      float route_scale, const float *shared, float *out, int accumulate);
+// synthetic data
+int sw_launch_gen_normal(hipStream_t st, float *out, int64_t n, uint64_t seed, uint64_t offset, double sigma, int to_bf16);
+int sw_launch_gen_bf16(hipStream_t st, uint16_t *out, int64_t n, uint64_t seed, uint64_t offset, double sigma);
+int sw_launch_gen_q4(hipStream_t st, uint8_t *q, float *s, uint64_t seed, double sigma, int64_t row0, int64_t nrows, int K, int gs);
+int sw_launch_chain_major(hipStream_t st, const void *W, int w_bf16, int E, int D, void *Wc);
+// self test kernels
+int sw_launch_selftest(hipStream_t st, float *out, const float *xin, int n);
+
+#endif

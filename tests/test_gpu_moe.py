@@ -1,0 +1,123 @@
+"""The whole MoE block on the device (lag_hip_moe_block / moe_forward) against
+the CPU reference contract: routing identical, layer output within the
+benchmark tolerance (normwise max|a-b|/max|b| <= 2e-3), grouped batches
+bit-identical per token to single-token calls."""
+from dataclasses import replace
+
+import numpy as np
+import pytest
+
+from oracle import synth
+from sabrewing_amd import configs as cf
+from sabrewing_amd import synth as S
+from sabrewing_amd.backend import DeviceLayer, desc_of, gen_x
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-3
+
+
+def errs(got, want, base):
+    """normwise and floored-elementwise relative errors of the MoE update"""
+    dg, dw = got - base, want - base
+    m = float(np.max(np.abs(dw)))
+    nw = float(np.max(np.abs(dg - dw))) / m
+    el = float(np.max(np.abs(dg - dw) / np.maximum(np.abs(dw), 0.05 * m)))
+    return nw, el
+
+
+SMALL = [cf.scaled(cf.C1, D=512, E=16, K=4, I=256),
+         cf.scaled(cf.C2_SIGMOID, D=512, E=32, K=6, I=256, Is=256),
+         cf.scaled(cf.C2, D=512, E=32, K=6, I=256, Is=256),
+         cf.scaled(cf.C4_ZIPF, D=512, E=32, K=6, I=256, Is=256),
+         cf.scaled(cf.C5_LAYER, D=512, E=32, K=8, I=384),
+         replace(cf.scaled(cf.C2_SIGMOID, D=512, E=32, K=6, I=256, Is=256), name="C2-small-gs0", gs=0)]
+
+
+@pytest.mark.parametrize("cfg", SMALL, ids=lambda c: c.name)
+@pytest.mark.parametrize("S_", [1, 3, 33])
+def test_layer_small(be, orc, cfg, S_):
+    L = synth.make_layer(orc, cfg, 31, corr_bias_sigma=0.01)
+    x = synth.make_x(orc, cfg, 32, S_)
+    base = synth.make_x(orc, cfg, 33, S_)               # residual stream
+    want = orc.moe_block_rows(synth.desc_of(cfg), L, x, base)
+    dl = DeviceLayer.from_host(be, cfg, L)
+    got = be.moe_block(desc_of(cfg), dl.weights(), x, base)
+    _, sel_w, _ = orc.route(synth.desc_of(cfg), L, x)
+    xd = be.upload(x)
+    _, sel, _ = be.route(desc_of(cfg), dl.weights(), xd, S_)
+    xd.free(); dl.free()
+    assert np.array_equal(sel, sel_w)
+    nw, el = errs(got, want, base)
+    assert nw <= TOL, (nw, el)
+
+
+@pytest.mark.parametrize("cfg", [SMALL[1], SMALL[4]], ids=lambda c: c.name)
+def test_grouped_equals_per_token(be, orc, cfg):
+    """every stream of a batch gets the same bits as its own single-token call"""
+    L = synth.make_layer(orc, cfg, 41)
+    dl = DeviceLayer.from_host(be, cfg, L)
+    x = synth.make_x(orc, cfg, 42, 32)
+    base = np.zeros_like(x)
+    batched = be.moe_block(desc_of(cfg), dl.weights(), x, base)
+    single = np.stack([be.moe_block(desc_of(cfg), dl.weights(), x[s:s + 1], base[s:s + 1])[0] for s in range(32)])
+    dl.free()
+    assert np.array_equal(batched.view(np.uint32), single.view(np.uint32))
+
+
+def host_layer_for(orc, cfg, seed, x):
+    """the full-size host layer with only the experts x routes to generated
+    (the rest stay zero: moe_block never reads them)"""
+    D, I, E, gs = cfg.D, cfg.I, cfg.E, cfg.gs
+    ts = lambda tid: S.tensor_seed(seed, 0, tid)
+    r = orc.normal(E * D, ts(S.T_ROUTER), 0.02).reshape(E, D)
+    router = orc.to_bf16(r) if cfg.router_bf16 else r
+    corr = np.zeros(E, np.float32) if cfg.use_corr_bias else None
+    lb = S.zipf_bias(E, cfg.zipf, ts(S.T_ROUTER) ^ 0x5A5A) if cfg.zipf > 0 else None
+    ngD, ngI = D // gs, I // gs
+    gu_q = np.zeros((E * 2 * I, D // 2), np.uint8); gu_s = np.zeros((E * 2 * I, ngD), np.float32)
+    dn_q = np.zeros((E * D, I // 2), np.uint8); dn_s = np.zeros((E * D, ngI), np.float32)
+    sg = su = sd = None
+    if cfg.shared_mode:
+        sg = orc.to_bf16(orc.normal(cfg.Is * D, ts(S.T_SH_GATE), 0.02)).reshape(cfg.Is, D)
+        su = orc.to_bf16(orc.normal(cfg.Is * D, ts(S.T_SH_UP), 0.02)).reshape(cfg.Is, D)
+        sd = orc.to_bf16(orc.normal(D * cfg.Is, ts(S.T_SH_DOWN), 0.02)).reshape(D, cfg.Is)
+    L = synth.Layer(D, I, cfg.Is, E, gs, cfg.router_bf16, router, corr, lb, gu_q.reshape(-1), gu_s.reshape(-1),
+                    dn_q.reshape(-1), dn_s.reshape(-1), sg, su, sd)
+    _, sel, _ = orc.route(synth.desc_of(cfg), L, x)
+    for e in np.unique(sel):
+        e = int(e)
+        q, s = orc.gen_q4(ts(S.T_GATE_UP), 0.02, 2 * I, D, gs, row0=e * 2 * I)
+        gu_q[e * 2 * I:(e + 1) * 2 * I] = q; gu_s[e * 2 * I:(e + 1) * 2 * I] = s
+        q, s = orc.gen_q4(ts(S.T_DOWN), 0.02, D, I, gs, row0=e * D)
+        dn_q[e * D:(e + 1) * D] = q; dn_s[e * D:(e + 1) * D] = s
+    return L, sel
+
+
+@pytest.mark.parametrize("cfg", [cf.C1, cf.C2, cf.C2_SIGMOID], ids=lambda c: c.name)
+@pytest.mark.parametrize("S_", [1, 4])
+def test_layer_full_size(be, orc, cfg, S_):
+    """benchmark shapes: device-generated layer vs the oracle on the same bits"""
+    seed = 555
+    x = synth.make_x(orc, cfg, seed, S_)
+    L, sel_w = host_layer_for(orc, cfg, seed, x)
+    base = np.zeros_like(x)
+    want = orc.moe_block_rows(synth.desc_of(cfg), L, x, base)
+    dl = DeviceLayer.generate(be, cfg, seed)
+    xd = be.upload(x)
+    _, sel, _ = be.route(desc_of(cfg), dl.weights(), xd, S_)
+    od = be.upload(base)
+    be.moe_forward(desc_of(cfg), dl.weights(), xd, od, S_)
+    got = be.d2h(od, x.shape, np.float32)
+    xd.free(); od.free(); dl.free()
+    assert np.array_equal(sel, sel_w)
+    nw, el = errs(got, want, base)
+    assert nw <= TOL, (nw, el)
+
+
+def test_device_x_generator(be, orc):
+    cfg = cf.C2
+    xd = gen_x(be, cfg, 9, 3, stream=2)
+    got = be.d2h(xd, (3, cfg.D), np.float32)
+    xd.free()
+    want = orc.bf16_round(orc.normal(3 * cfg.D, S.tensor_seed(9, 1002, S.T_X), 1.0)).reshape(3, cfg.D)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))

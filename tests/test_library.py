@@ -1,0 +1,87 @@
+"""The C-ABI libraries load and export exactly what include/*.h declares, and
+the loader keeps the reference loader's fallback rules (no GPU needed: no
+compute entry is called here)."""
+import ctypes as C
+import os
+import re
+import subprocess
+import sys
+import textwrap
+
+import pytest
+
+from sabrewing_amd import backend as B
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_functions(path):
+    src = open(path).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return set(re.findall(r"\b(lag_(?:hip|cuda)_\w+|sabrewing_loader_\w+)\s*\(", src))
+
+
+def exported(path):
+    out = subprocess.run(["nm", "-D", "--defined-only", path], stdout=subprocess.PIPE, text=True, check=True).stdout
+    return {l.split()[-1] for l in out.splitlines() if " T " in l}
+
+
+def test_hip_library_exports_header():
+    assert os.path.exists(B.LIB_PATH), "libsabrewing_hip.so not built"
+    decl = header_functions(os.path.join(ROOT, "include", "sabrewing_hip.h"))
+    assert decl == set(B.EXPORTS)
+    missing = decl - exported(B.LIB_PATH)
+    assert not missing, missing
+    lib = C.CDLL(B.LIB_PATH)                   # loads without a GPU
+    for name in decl:
+        assert hasattr(lib, name)
+
+
+def test_loader_exports_header():
+    decl = header_functions(os.path.join(ROOT, "include", "sabrewing_loader.h"))
+    assert decl == set(B.LOADER_EXPORTS)
+    assert not decl - exported(B.LOADER_PATH)
+
+
+LOADER_PROBE = textwrap.dedent("""
+    import ctypes as C, sys
+    L = C.CDLL(sys.argv[1])
+    L.lag_cuda_upload.restype = C.c_void_p
+    L.sabrewing_loader_path.restype = C.c_char_p
+    L.lag_cuda_free_bytes.restype = C.c_size_t
+    print(L.sabrewing_loader_available(), L.lag_cuda_init(0), L.lag_cuda_upload(None, 16),
+          L.lag_cuda_free_bytes(), L.lag_cuda_matmul_q8(None, None, None, 1, 1, 1),
+          L.sabrewing_loader_path().decode())
+""")
+
+
+def run_probe(env_lib):
+    env = dict(os.environ)
+    env["SABREWING_HIP_LIB"] = env_lib
+    r = subprocess.run([sys.executable, "-c", LOADER_PROBE, B.LOADER_PATH], env=env,
+                       stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True, check=True)
+    return r.stdout.split(), r.stderr
+
+
+def test_loader_unavailable_sentinels(tmp_path):
+    # no backend library at the configured path: every wrapper answers "not initialised"
+    out, _ = run_probe(str(tmp_path / "absent.so"))
+    assert out[:5] == ["0", "-1", "None", "0", "-1"]
+    assert out[5] == str(tmp_path / "absent.so")
+
+
+def test_loader_all_or_nothing(tmp_path):
+    # a library that resolves only some slots is unloaded again (c/backend_loader.c:190-250)
+    src = tmp_path / "partial.c"
+    src.write_text("int lag_hip_init(int d){return 0;}\n")
+    so = tmp_path / "libpartial.so"
+    subprocess.run(["gcc", "-shared", "-fPIC", str(src), "-o", str(so)], check=True)
+    out, err = run_probe(str(so))
+    assert out[:2] == ["0", "-1"] and "missing symbol" in err
+
+
+def test_loader_relative_path_refused(tmp_path):
+    # a relative SABREWING_HIP_LIB is ignored (no search of the current directory);
+    # the loader falls back to the library next to itself
+    out, _ = run_probe("libsabrewing_hip.so")
+    assert out[5] == os.path.join(os.path.dirname(B.LOADER_PATH), "libsabrewing_hip.so")

@@ -1,0 +1,108 @@
+"""The oracle restatement against the compiled reference (oracle/_ref), bit for bit.
+
+Every kernel of the path on seeded inputs, including the shapes that take the
+scalar tails, plus moe_block over laguna-shaped hooks and the reference
+engine's own lag_moe_rows (per-token and grouped) at gs = 0.
+"""
+from dataclasses import replace
+
+import numpy as np
+import pytest
+
+from oracle import synth
+from oracle.oracle import RefLaguna
+from sabrewing_amd import configs as cf
+
+
+def bits_equal(a, b):
+    a = np.ascontiguousarray(a, np.float32); b = np.ascontiguousarray(b, np.float32)
+    return a.shape == b.shape and np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+@pytest.fixture(scope="module")
+def rng():
+    return np.random.default_rng(20261201)
+
+
+@pytest.mark.parametrize("S,I,O", [(1, 2048, 64), (3, 4096, 256), (2, 100, 7), (1, 33, 5), (4, 16, 3)])
+def test_router_contracts(orc, ref, rng, S, I, O):
+    x = rng.standard_normal((S, I)).astype(np.float32)
+    W = (rng.standard_normal((O, I)) * 0.02).astype(np.float32)
+    for exact in (0, 1):
+        assert bits_equal(orc.matmul_f32(x, W, exact), ref.matmul_f32(x, W, exact))
+        Wb = orc.to_bf16(W)
+        assert bits_equal(orc.matmul_bf16(x, Wb, exact), ref.matmul_bf16(x, Wb, exact))
+
+
+@pytest.mark.parametrize("S,I,O,gs", [(1, 2048, 64, 32), (3, 1024, 96, 32), (2, 512, 8, 64), (2, 200, 4, 64),
+                                      (1, 65, 3, 64), (2, 201, 4, 64), (1, 33, 2, 16), (8, 320, 6, 64),
+                                      (1, 64, 4, 128)])
+def test_i4_grouped(orc, ref, rng, S, I, O, gs):
+    x = rng.standard_normal((S, I)).astype(np.float32)
+    W = (rng.standard_normal((O, I)) * 0.02).astype(np.float32)
+    p, s = orc.quant_i4(W, gs)
+    assert bits_equal(orc.matmul_i4_grouped(x, p, s, gs), ref.matmul_i4_grouped(x, p, s, gs))
+
+
+@pytest.mark.parametrize("S,I,O", [(1, 2048, 64), (4, 1024, 96), (1, 100, 8), (3, 96, 8), (2, 8192, 4), (1, 8256, 3)])
+def test_q4_rows(orc, ref, rng, S, I, O):
+    x = rng.standard_normal((S, I)).astype(np.float32)
+    W = (rng.standard_normal((O, I)) * 0.02).astype(np.float32)
+    p, s = orc.quant_i4(W, 0)
+    for mode, exact in ((0, 0), (1, 0), (0, 1)):
+        assert bits_equal(orc.matmul_q4(x, p, s, mode, exact), ref.matmul_q4(x, p, s, mode, exact)), (mode, exact)
+
+
+def test_softmax_topk(orc, ref, rng):
+    for n in (8, 64, 256):
+        v = (rng.standard_normal(n) * 3).astype(np.float32)
+        assert bits_equal(orc.softmax_row(v), ref.softmax_row(v))
+        for K in (1, 4, min(10, n)):
+            assert np.array_equal(orc.topk(v, K), ref.topk(v, K))
+            b = (rng.standard_normal(n) * 0.1).astype(np.float32)
+            assert np.array_equal(orc.topk(v, K, b), ref.topk(v, K, b))
+    # ties, signed zeros, NaN and values at the -1e30 threshold
+    v = np.array([0.5, 0.5, -0.0, 0.0, np.nan, -1e30, 0.5, -np.inf], np.float32)
+    for K in range(1, 9):
+        assert np.array_equal(orc.topk(v, K), ref.topk(v, K))
+    v = np.full(6, np.nan, np.float32)
+    assert np.array_equal(orc.topk(v, 4), ref.topk(v, 4))
+
+
+def test_scalar_math(orc, ref):
+    xs = np.concatenate([np.linspace(-30, 30, 20001), [-104.0, -88.0, 0.0, -0.0, 20.0, 20.000002, 88.7]]).astype(np.float32)
+    f = lambda lib, name: np.array([getattr(lib, name)(float(v)) for v in xs], np.float32)
+    assert bits_equal(f(orc.lib, "sw_siluf"), f(ref.lib, "ref_siluf"))
+    assert bits_equal(f(orc.lib, "sw_softplusf"), f(ref.lib, "ref_softplusf"))
+
+
+SMALL = [cf.scaled(cf.C1, D=256, E=16, K=4, I=128),
+         cf.scaled(cf.C2_SIGMOID, D=256, E=32, K=6, I=128, Is=128),
+         cf.scaled(cf.C5_LAYER, D=256, E=32, K=8, I=384)]
+
+
+@pytest.mark.parametrize("cfg", SMALL, ids=lambda c: c.name)
+def test_moe_block_vs_ref(orc, ref, cfg):
+    L = synth.make_layer(orc, cfg, 42, corr_bias_sigma=0.01)
+    d = synth.desc_of(cfg)
+    x = synth.make_x(orc, cfg, 42, 5)
+    out0 = synth.make_x(orc, cfg, 43, 5)         # a non-zero residual
+    a = orc.moe_block_rows(d, L, x, out0)
+    assert bits_equal(a, ref.moe_block_rows(d, L, x, out0))
+    assert bits_equal(a, orc.moe_group_rows(d, L, x, out0))          # grouped == per-token
+
+
+def test_laguna_engine_path(orc):
+    if not RefLaguna.available():
+        pytest.skip("compiled reference engine not built")
+    lag = RefLaguna()
+    cfg = replace(cf.scaled(cf.C2_SIGMOID, D=256, E=32, K=6, I=128, Is=128), gs=0, router_bf16=False)
+    L = synth.make_layer(orc, cfg, 7, corr_bias_sigma=0.01)
+    d = synth.desc_of(cfg)
+    x = synth.make_x(orc, cfg, 7, 6)
+    h0 = synth.make_x(orc, cfg, 8, 6)
+    assert bits_equal(orc.moe_block_rows(d, L, x, h0), lag.moe_rows(d, L, x, h0, group=0))
+    assert bits_equal(orc.moe_group_rows(d, L, x, h0), lag.moe_rows(d, L, x, h0, group=1))
+    assert bits_equal(orc.moe_block_rows(d, L, x[:1], h0[:1]), lag.moe_rows(d, L, x[:1], h0[:1]))
+    for mode in (2,):                                # g_exact: the double-accumulate kernels
+        assert bits_equal(orc.moe_block_rows(d, L, x, h0, mode), lag.moe_rows(d, L, x, h0, exact=1, group=0))
