@@ -33,24 +33,26 @@ def log(*a):
 
 
 def kernel_bytes(cfg, S, G):
-    """algorithmic HBM bytes per launch of each kernel of the forward pass"""
+    """algorithmic HBM bytes per launch of each kernel of the forward pass:
+    every weight byte the launch needs once, activations in and out once"""
     D, I, Is, E, K = cfg.D, cfg.I, cfg.Is, cfg.E, cfg.K
     ngD, ngI = (D // cfg.gs, I // cfg.gs) if cfg.gs else (1, 1)
     T = S * K
+    gu_w = G * (2 * I * D // 2 + 2 * I * ngD * 4)
+    dn_w = G * (D * I // 2 + D * ngI * 4)
     b = {
-        "router": cfg.router_bytes() + S * D * 4 + S * E * 4,
-        "gate_topk": S * E * 4 + T * 8,
-        "prep_f16": S * D * 4 + 2 * S * D * 2,
-        "q4_gateup_glu": G * (2 * I * D // 2 + 2 * I * ngD * 4) + 2 * S * D * 2 + 2 * T * I * 2,
-        "q4_down": G * (D * I // 2 + D * ngI * 4) + 2 * T * I * 2 + T * D * 4,
-        "combine": T * D * 4 + 2 * S * D * 4 + (S * D * 4 if cfg.shared_mode else 0) + T * 8,
+        "router_topk": cfg.router_bytes() + S * D * 4 + S * E * 4 + T * 8,
+        "q4_gateup_glu": gu_w + S * D * 4 + 2 * T * I * 2,
     }
-    if cfg.shared_mode:
-        b["prep_bf16"] = S * D * 4 + 2 * S * D * 2
-        b["shared_gateup_glu"] = 2 * Is * D * 2 + 2 * S * D * 2 + 2 * S * Is * 2
-        b["shared_down"] = D * Is * 2 + 2 * S * Is * 2 + S * D * 4
-    if S > 1:
+    if S == 1:
+        b["q4_down_combine"] = dn_w + 2 * T * I * 2 + T * 8 + 2 * D * 4 + (D * 4 if cfg.shared_mode else 0)
+    else:
         b["bucket"] = T * 4 * 3 + E * 12
+        b["q4_down"] = dn_w + 2 * T * I * 2 + T * D * 4
+        b["combine"] = T * D * 4 + 2 * S * D * 4 + (S * D * 4 if cfg.shared_mode else 0) + T * 8
+    if cfg.shared_mode:
+        b["shared_gateup_glu"] = 2 * Is * D * 2 + S * D * 4 + 2 * S * Is * 2
+        b["shared_down"] = D * Is * 2 + 2 * S * Is * 2 + S * D * 4
     return b
 
 
@@ -89,7 +91,7 @@ def cpu_baseline(be, cfg, dl, xs, seconds):
     out = np.zeros((1, D), np.float32)
     ref.moe_block_rows(d, L, xs[0:1], out)           # warm
     n, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < seconds and n < 4096:
+    while time.perf_counter() - t0 < seconds and n < 1000000:
         ref.moe_block_rows(d, L, xs[n % len(xs):n % len(xs) + 1], out)
         n += 1
     dt = time.perf_counter() - t0

@@ -16,7 +16,9 @@
 
 static int g_ok = 0;
 static int g_dev = 0;
-static hipStream_t g_st = nullptr;
+static hipStream_t g_st = nullptr;      // the backend stream (all entry points are ordered on it)
+static hipStream_t g_side = nullptr;    // shared expert, overlapped with routing and the routed experts
+static hipEvent_t g_ev_fork = nullptr, g_ev_join = nullptr;
 static char g_err[256] = "";
 
 static int fail(const char *what, hipError_t e) {
@@ -64,6 +66,7 @@ static int prof_rec(const char *name) {
 static void prof_flush(void) {
     if (g_pending.empty()) return;
     (void)hipStreamSynchronize(g_st);
+    if (g_side) (void)hipStreamSynchronize(g_side);
     for (auto &p : g_pending) {
         float ms = 0.f;
         if (hipEventElapsedTime(&ms, p.a, p.b) == hipSuccess) { g_prof_recs[p.rec].ms += ms; g_prof_recs[p.rec].n++; }
@@ -73,21 +76,22 @@ static void prof_flush(void) {
 }
 // bracket one launch with events when profiling
 struct ProfScope {
-    Pending p; bool on;
-    ProfScope(const char *name) : on(g_prof != 0) {
+    Pending p; bool on; hipStream_t st;
+    ProfScope(const char *name, hipStream_t s) : on(g_prof != 0), st(s) {
         if (!on) return;
         p.rec = prof_rec(name); p.a = ev_get(); p.b = ev_get();
         if (!p.a || !p.b) { on = false; return; }
-        (void)hipEventRecord(p.a, g_st);
+        (void)hipEventRecord(p.a, st);
     }
     ~ProfScope() {
         if (!on) return;
-        (void)hipEventRecord(p.b, g_st);
+        (void)hipEventRecord(p.b, st);
         g_pending.push_back(p);
         if (g_pending.size() > 4096) prof_flush();
     }
 };
-#define PROF(name) ProfScope prof_scope_(name)
+#define PROF(name) ProfScope prof_scope_(name, g_st)
+#define PROF_SIDE(name) ProfScope prof_scope_(name, g_side)
 
 // ------------------------------------------------------------ buffers ----
 // grow-only device arena and pinned staging (2x slack, as the reference)
@@ -108,7 +112,7 @@ static int grow_pinned(Buf &b, size_t need) {
     b.cap = need * 2;
     return 0;
 }
-static Buf g_arena, g_hin, g_hout, g_consts;
+static Buf g_arena, g_hin, g_hout, g_consts, g_counters;
 static int g_consts_k = 0;
 
 // carve aligned sub-buffers out of the arena
@@ -127,6 +131,16 @@ static int ensure_consts(int K) {   // iota[K], ones[K], zeros[K]
     g_consts_k = k;
     return 0;
 }
+// per-token arrival counters of the fused router: zero on allocation, and
+// every use leaves them zero again
+static int g_counters_n = 0;
+static int ensure_counters(int S) {
+    if (S <= g_counters_n) return 0;
+    if (grow_dev(g_counters, (size_t)S * sizeof(int))) return -1;
+    CK(hipMemsetAsync(g_counters.p, 0, g_counters.cap, g_st), "counter clear");
+    g_counters_n = (int)(g_counters.cap / sizeof(int));
+    return 0;
+}
 static const int *c_iota(void) { return (const int *)g_consts.p; }
 static const int *c_ones(void) { return (const int *)g_consts.p + g_consts_k; }
 static const int *c_zeros(void) { return (const int *)g_consts.p + 2 * g_consts_k; }
@@ -136,6 +150,9 @@ extern "C" int lag_hip_init(int dev) {
     if (g_ok && dev == g_dev) return 0;
     CK(hipSetDevice(dev), "hipSetDevice");
     if (!g_st) CK(hipStreamCreateWithFlags(&g_st, hipStreamNonBlocking), "stream creation");
+    if (!g_side) CK(hipStreamCreateWithFlags(&g_side, hipStreamNonBlocking), "stream creation");
+    if (!g_ev_fork) CK(hipEventCreateWithFlags(&g_ev_fork, hipEventDisableTiming), "event creation");
+    if (!g_ev_join) CK(hipEventCreateWithFlags(&g_ev_join, hipEventDisableTiming), "event creation");
     void *probe = nullptr;
     CK(hipMalloc(&probe, 1 << 20), "probe allocation");
     (void)hipFree(probe);
@@ -189,21 +206,19 @@ extern "C" int lag_hip_memset(void *dst, int v, size_t n) {
 }
 extern "C" int lag_hip_sync(void) {
     if (!g_ok) return -1;
+    CK(hipStreamSynchronize(g_side), "stream sync");
     CK(hipStreamSynchronize(g_st), "stream sync");
     if (g_prof) prof_flush();
     return 0;
 }
 
 // the int4 expert pipeline over device groups:
-//   xplanes <- x;  h <- silu_glu(gate_up . x);  slots <- down . h
-static int run_experts(SwQ4 gu, SwQ4 dn, const float *dx, int S, SwGroups g, int T, int I, int D,
-                       _Float16 *xpl, _Float16 *hpl, float *slots, int cb) {
-    { PROF("prep_f16"); if (sw_launch_prep_f16(g_st, dx, S, D, xpl)) return fail_msg("prep launch"); }
-    { PROF("q4_gateup_glu"); if (sw_launch_q4_gateup(g_st, gu, xpl, g, I, hpl, cb)) return fail_msg("gate_up launch (shape unsupported?)"); }
+//   h <- silu_glu(gate_up . x);  slots <- down . h
+static int run_experts(SwQ4 gu, SwQ4 dn, const float *dx, SwGroups g, int I, _Float16 *hpl, float *slots, int maxtok) {
+    { PROF("q4_gateup_glu"); if (sw_launch_q4_gateup(g_st, gu, dx, g, I, hpl, maxtok)) return fail_msg("gate_up launch (shape unsupported?)"); }
     SwGroups gd = g;
     gd.grow = nullptr;                     // down reads the packed rows directly
-    (void)T;
-    { PROF("q4_down"); if (sw_launch_q4_rows(g_st, dn, hpl, gd, slots, cb)) return fail_msg("down launch (shape unsupported?)"); }
+    { PROF("q4_down"); if (sw_launch_q4_rows(g_st, dn, hpl, gd, slots, maxtok)) return fail_msg("down launch (shape unsupported?)"); }
     return 0;
 }
 
@@ -218,7 +233,7 @@ static int grouped_host(float *outh, const float *x, int S, const void *gu_q, co
     (void)ngD; (void)ngI;
     Carve cv;
     const size_t o_x = cv.take((size_t)S * D * 4), o_idx = cv.take((size_t)(3 * G + 2 * T) * 4 + (size_t)T * 4);
-    const size_t o_xpl = cv.take((size_t)2 * S * D * 2), o_hpl = cv.take((size_t)2 * T * I * 2);
+    const size_t o_hpl = cv.take((size_t)2 * T * I * 2);
     const size_t o_slot = cv.take((size_t)T * D * 4), o_out = cv.take((size_t)S * D * 4);
     if (grow_dev(g_arena, cv.off)) return -1;
     char *A = (char *)g_arena.p;
@@ -241,11 +256,10 @@ static int grouped_host(float *outh, const float *x, int S, const void *gu_q, co
     const float *d_w = (const float *)(d_rowof + T);
     SwQ4 gu = {(const uint8_t *)gu_q, gu_s, 2 * I, D, gs};
     SwQ4 dn = {(const uint8_t *)dn_q, dn_s, D, I, gs};
-    SwGroups g = {d_gexp, d_gbeg, d_gcnt, d_grow, nullptr, G};
+    SwGroups g = {d_gexp, d_gbeg, d_gcnt, d_grow, nullptr, G, 0};
     int maxcnt = 0;
     for (int i = 0; i < G; i++) maxcnt = gcnt[i] > maxcnt ? gcnt[i] : maxcnt;
-    if (run_experts(gu, dn, (const float *)(A + o_x), S, g, T, I, D, (_Float16 *)(A + o_xpl), (_Float16 *)(A + o_hpl),
-                    (float *)(A + o_slot), maxcnt > 1 ? 4 : 1)) return -1;
+    if (run_experts(gu, dn, (const float *)(A + o_x), g, I, (_Float16 *)(A + o_hpl), (float *)(A + o_slot), maxcnt)) return -1;
     const float *res = (const float *)(A + o_slot);
     if (combine) {
         PROF("combine");
@@ -306,7 +320,7 @@ extern "C" int lag_hip_matmul_q4_g(float *y, const float *x, const void *packed,
     if (!g_ok || fault_injected()) return -1;
     if (S <= 0 || I <= 0 || O <= 0) return -1;
     Carve cv;
-    const size_t o_x = cv.take((size_t)S * I * 4), o_idx = cv.take(16), o_xpl = cv.take((size_t)2 * S * I * 2);
+    const size_t o_x = cv.take((size_t)S * I * 4), o_idx = cv.take(16);
     const size_t o_y = cv.take((size_t)S * O * 4);
     if (grow_dev(g_arena, cv.off) || grow_pinned(g_hin, (size_t)S * I * 4 + 16) || grow_pinned(g_hout, (size_t)S * O * 4)) return -1;
     char *A = (char *)g_arena.p, *H = (char *)g_hin.p;
@@ -316,10 +330,9 @@ extern "C" int lag_hip_matmul_q4_g(float *y, const float *x, const void *packed,
     CK(hipMemcpyAsync(A + o_x, H, (size_t)S * I * 4, hipMemcpyHostToDevice, g_st), "x upload");
     CK(hipMemcpyAsync(A + o_idx, hi, 12, hipMemcpyHostToDevice, g_st), "index upload");
     const int *d = (const int *)(A + o_idx);
-    SwGroups g = {d, d + 1, d + 2, nullptr, nullptr, 1};
+    SwGroups g = {d, d + 1, d + 2, nullptr, nullptr, 1, 0};
     SwQ4 W = {(const uint8_t *)packed, (const float *)scale, O, I, gs};
-    { PROF("prep_f16"); if (sw_launch_prep_f16(g_st, (const float *)(A + o_x), S, I, (_Float16 *)(A + o_xpl))) return fail_msg("prep launch"); }
-    { PROF("q4_rows"); if (sw_launch_q4_rows(g_st, W, (const _Float16 *)(A + o_xpl), g, (float *)(A + o_y), S > 1 ? 4 : 1)) return fail_msg("q4 launch (shape unsupported?)"); }
+    { PROF("q4_rows"); if (sw_launch_q4_rows_x(g_st, W, (const float *)(A + o_x), g, (float *)(A + o_y), S)) return fail_msg("q4 launch (shape unsupported?)"); }
     CK(hipMemcpyAsync(g_hout.p, A + o_y, (size_t)S * O * 4, hipMemcpyDeviceToHost, g_st), "result download");
     CK(hipStreamSynchronize(g_st), "stream sync");
     memcpy(y, g_hout.p, (size_t)S * O * 4);
@@ -335,14 +348,13 @@ extern "C" int lag_hip_matmul_bf16(float *y, const float *x, const void *W, int 
     if (!g_ok || fault_injected() || (I & 1)) return -1;
     if (S <= 0 || I <= 0 || O <= 0) return -1;
     Carve cv;
-    const size_t o_x = cv.take((size_t)S * I * 4), o_xpl = cv.take((size_t)2 * S * I * 2), o_y = cv.take((size_t)S * O * 4);
+    const size_t o_x = cv.take((size_t)S * I * 4), o_y = cv.take((size_t)S * O * 4);
     if (grow_dev(g_arena, cv.off) || grow_pinned(g_hin, (size_t)S * I * 4) || grow_pinned(g_hout, (size_t)S * O * 4)) return -1;
     char *A = (char *)g_arena.p;
     memcpy(g_hin.p, x, (size_t)S * I * 4);
     CK(hipMemcpyAsync(A + o_x, g_hin.p, (size_t)S * I * 4, hipMemcpyHostToDevice, g_st), "x upload");
     SwBf16 Wt = {(const uint16_t *)W, O, I};
-    { PROF("prep_bf16"); if (sw_launch_prep_bf16(g_st, (const float *)(A + o_x), S, I, (uint16_t *)(A + o_xpl))) return fail_msg("prep launch"); }
-    { PROF("bf16_rows"); if (sw_launch_bf16_rows(g_st, Wt, (const uint16_t *)(A + o_xpl), S, (float *)(A + o_y))) return fail_msg("bf16 launch (shape unsupported?)"); }
+    { PROF("bf16_rows"); if (sw_launch_bf16_rows_x(g_st, Wt, (const float *)(A + o_x), S, (float *)(A + o_y))) return fail_msg("bf16 launch (shape unsupported?)"); }
     CK(hipMemcpyAsync(g_hout.p, A + o_y, (size_t)S * O * 4, hipMemcpyDeviceToHost, g_st), "result download");
     CK(hipStreamSynchronize(g_st), "stream sync");
     memcpy(y, g_hout.p, (size_t)S * O * 4);
@@ -374,8 +386,8 @@ extern "C" int lag_hip_router_chain(const void *W, void *Wc, int E, int D, int w
 struct FwdScratch {
     float *logits, *w, *slots, *sout;
     int *sel, *gexp, *gbeg, *gcnt, *G, *grow, *rowof;
-    _Float16 *xpl, *hpl;
-    uint16_t *xbpl, *shpl;
+    _Float16 *hpl;
+    uint16_t *shpl;
 };
 static int g_last_G_dev = 0;            // 1: last forward's groups live in the arena
 static FwdScratch g_last;
@@ -398,31 +410,27 @@ static int carve_fwd(const LagHipMoeDesc *d, int S, FwdScratch &f) {
     const size_t o_lg = cv.take((size_t)S * E * 4), o_sel = cv.take((size_t)T * 4), o_w = cv.take((size_t)T * 4);
     const size_t o_gexp = cv.take((size_t)E * 4), o_gbeg = cv.take((size_t)E * 4), o_gcnt = cv.take((size_t)E * 4);
     const size_t o_G = cv.take(4), o_grow = cv.take((size_t)T * 4), o_rowof = cv.take((size_t)T * 4);
-    const size_t o_xpl = cv.take((size_t)2 * S * D * 2), o_hpl = cv.take((size_t)2 * T * I * 2);
-    const size_t o_slot = cv.take((size_t)T * D * 4);
-    size_t o_xb = 0, o_sh = 0, o_so = 0;
-    if (d->shared_mode) {
-        o_xb = cv.take((size_t)2 * S * D * 2); o_sh = cv.take((size_t)2 * S * Is * 2); o_so = cv.take((size_t)S * D * 4);
-    }
+    const size_t o_hpl = cv.take((size_t)2 * T * I * 2);
+    const size_t o_slot = cv.take(S > 1 ? (size_t)T * D * 4 : 4);
+    size_t o_sh = 0, o_so = 0;
+    if (d->shared_mode) { o_sh = cv.take((size_t)2 * S * Is * 2); o_so = cv.take((size_t)S * D * 4); }
     if (grow_dev(g_arena, cv.off)) return -1;
     char *A = (char *)g_arena.p;
     f.logits = (float *)(A + o_lg); f.sel = (int *)(A + o_sel); f.w = (float *)(A + o_w);
     f.gexp = (int *)(A + o_gexp); f.gbeg = (int *)(A + o_gbeg); f.gcnt = (int *)(A + o_gcnt); f.G = (int *)(A + o_G);
     f.grow = (int *)(A + o_grow); f.rowof = (int *)(A + o_rowof);
-    f.xpl = (_Float16 *)(A + o_xpl); f.hpl = (_Float16 *)(A + o_hpl); f.slots = (float *)(A + o_slot);
-    f.xbpl = d->shared_mode ? (uint16_t *)(A + o_xb) : nullptr;
+    f.hpl = (_Float16 *)(A + o_hpl); f.slots = (float *)(A + o_slot);
     f.shpl = d->shared_mode ? (uint16_t *)(A + o_sh) : nullptr;
     f.sout = d->shared_mode ? (float *)(A + o_so) : nullptr;
     return 0;
 }
 
 static int route_dev(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const float *x, int S, float *logits, int *sel, float *wts) {
-    { PROF("router");
-      if (sw_launch_router(g_st, w->router, d->router_bf16, x, S, d->hidden, d->n_experts, w->logit_bias, logits))
-          return fail_msg("router launch"); }
-    { PROF("gate_topk");
-      if (sw_launch_gate_topk(g_st, logits, S, d->n_experts, d->topk, d->route_act, w->corr_bias, d->use_corr_bias,
-                              d->norm_topk, sel, wts)) return fail_msg("gate/top-k launch"); }
+    if (ensure_counters(S)) return -1;
+    PROF("router_topk");
+    if (sw_launch_router_topk(g_st, w->router, d->router_bf16, x, S, d->hidden, d->n_experts, w->logit_bias, logits,
+                              (int *)g_counters.p, d->topk, d->route_act, w->corr_bias, d->use_corr_bias, d->norm_topk,
+                              sel, wts)) return fail_msg("router launch");
     return 0;
 }
 
@@ -434,37 +442,50 @@ extern "C" int lag_hip_route(const LagHipMoeDesc *d, const LagHipMoeWeights *w, 
     return route_dev(d, w, x, S, logits ? logits : f.logits, sel, wts);
 }
 
+// The shared expert runs on the side stream, forked after everything queued
+// on the backend stream so far (x included) and joined before the combine.
+static int shared_fork(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const float *x, int S, FwdScratch &f) {
+    const int D = d->hidden, Is = d->shared_inter;
+    SwBf16 sg = {(const uint16_t *)w->sg, Is, D}, su = {(const uint16_t *)w->su, Is, D}, sd = {(const uint16_t *)w->sd, D, Is};
+    CK(hipEventRecord(g_ev_fork, g_st), "fork event");
+    CK(hipStreamWaitEvent(g_side, g_ev_fork, 0), "fork wait");
+    { PROF_SIDE("shared_gateup_glu"); if (sw_launch_bf16_gateup(g_side, sg, su, x, S, f.shpl)) return fail_msg("shared gate_up launch"); }
+    { PROF_SIDE("shared_down"); if (sw_launch_bf16_rows(g_side, sd, f.shpl, S, f.sout)) return fail_msg("shared down launch"); }
+    CK(hipEventRecord(g_ev_join, g_side), "join event");
+    return 0;
+}
+
 extern "C" int lag_hip_moe_forward(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const float *x, float *out, int S) {
     if (!g_ok || fault_injected()) return -1;
     if (!desc_ok(d, w) || S <= 0) return fail_msg("moe_forward: unsupported descriptor/shape");
-    const int E = d->n_experts, K = d->topk, D = d->hidden, I = d->moe_inter, Is = d->shared_inter;
+    const int E = d->n_experts, K = d->topk, D = d->hidden, I = d->moe_inter;
     const int T = S * K;
     FwdScratch f;
-    if (carve_fwd(d, S, f) || ensure_consts(K)) return -1;
+    if (carve_fwd(d, S, f) || ensure_consts(K) || ensure_counters(S)) return -1;
+    if (d->shared_mode && shared_fork(d, w, x, S, f)) return -1;
     if (route_dev(d, w, x, S, f.logits, f.sel, f.w)) return -1;
-    SwGroups g;
-    if (S == 1) {                        // per-token: groups are the K picks in rank order
-        g = {f.sel, c_iota(), c_ones(), c_zeros(), nullptr, K};
-    } else {
-        PROF("bucket");
-        if (sw_launch_bucket(g_st, f.sel, S, K, E, f.gexp, f.gbeg, f.gcnt, f.G, f.grow, f.rowof)) return fail_msg("bucket launch");
-        g = {f.gexp, f.gbeg, f.gcnt, f.grow, f.G, T < E ? T : E};
-    }
     SwQ4 gu = {(const uint8_t *)w->gu_q, w->gu_s, 2 * I, D, d->gs};
     SwQ4 dn = {(const uint8_t *)w->dn_q, w->dn_s, D, I, d->gs};
-    if (run_experts(gu, dn, x, S, g, T, I, D, f.xpl, f.hpl, f.slots, S > 1 ? 4 : 1)) return -1;
-    const float *shared = nullptr;
-    if (d->shared_mode) {
-        SwBf16 sg = {(const uint16_t *)w->sg, Is, D}, su = {(const uint16_t *)w->su, Is, D}, sd = {(const uint16_t *)w->sd, D, Is};
-        { PROF("prep_bf16"); if (sw_launch_prep_bf16(g_st, x, S, D, f.xbpl)) return fail_msg("prep launch"); }
-        { PROF("shared_gateup_glu"); if (sw_launch_bf16_gateup(g_st, sg, su, f.xbpl, S, f.shpl)) return fail_msg("shared gate_up launch"); }
-        { PROF("shared_down"); if (sw_launch_bf16_rows(g_st, sd, f.shpl, S, f.sout)) return fail_msg("shared down launch"); }
-        shared = f.sout;
+    if (S == 1) {                        // per-token: the K picks in rank order, fused down + combine
+        SwGroups g = {f.sel, c_iota(), c_ones(), c_zeros(), nullptr, K, 0};
+        { PROF("q4_gateup_glu"); if (sw_launch_q4_gateup(g_st, gu, x, g, I, f.hpl, 1)) return fail_msg("gate_up launch"); }
+        if (d->shared_mode) CK(hipStreamWaitEvent(g_st, g_ev_join, 0), "join wait");
+        { PROF("q4_down_combine");
+          if (sw_launch_q4_down_combine(g_st, dn, f.hpl, f.sel, f.w, K, d->route_scale, f.sout, out))
+              return fail_msg("down/combine launch"); }
+        g_last_G_dev = 0; g_last_ng = K;
+    } else {
+        { PROF("bucket");
+          if (sw_launch_bucket(g_st, f.sel, S, K, E, f.gexp, f.gbeg, f.gcnt, f.G, f.grow, f.rowof)) return fail_msg("bucket launch"); }
+        SwGroups g = {f.gexp, f.gbeg, f.gcnt, f.grow, f.G, T < E ? T : E, 0};
+        if (run_experts(gu, dn, x, g, I, f.hpl, f.slots, S)) return -1;
+        if (d->shared_mode) CK(hipStreamWaitEvent(g_st, g_ev_join, 0), "join wait");
+        { PROF("combine");
+          if (sw_launch_combine(g_st, f.slots, f.rowof, f.w, S, K, D, d->route_scale, f.sout, out, 1))
+              return fail_msg("combine launch"); }
+        g_last_G_dev = 1; g_last_ng = 0;
     }
-    { PROF("combine");
-      if (sw_launch_combine(g_st, f.slots, S == 1 ? c_iota() : f.rowof, f.w, S, K, D, d->route_scale, shared, out, 1))
-          return fail_msg("combine launch"); }
-    g_last = f; g_last_G_dev = S > 1; g_last_ng = S == 1 ? K : 0;
+    g_last = f;
     return 0;
 }
 

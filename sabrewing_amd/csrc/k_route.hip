@@ -6,63 +6,6 @@
 
 static int launch_err(void) { return hipGetLastError() == hipSuccess ? 0 : -1; }
 
-// ------------------------------------------------------------ activations ----
-// x f32 [S,D] -> f16 planes [2S,D]: row 2s = RN(x), row 2s+1 = RN(x - RN(x)),
-// 8-blocks permuted 0,4,1,5,2,6,3,7 (the int4 MFMA B-fragment order).
-__global__ void k_prep_f16(const float *__restrict__ x, int S, int D, _Float16 *__restrict__ p) {
-    const int64_t nb = (int64_t)S * (D / 8);
-    for (int64_t b = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; b < nb; b += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t s = b / (D / 8), k0 = (b % (D / 8)) * 8;
-        const sw_f32x4 v0 = *(const sw_f32x4 *)(x + s * D + k0);
-        const sw_f32x4 v1 = *(const sw_f32x4 *)(x + s * D + k0 + 4);
-        const float v[8] = {v0.x, v1.x, v0.y, v1.y, v0.z, v1.z, v0.w, v1.w};   // 0,4,1,5,2,6,3,7
-        sw_half8 hi, lo;
-#pragma unroll
-        for (int h = 0; h < 8; h++) {
-            const _Float16 a = (_Float16)v[h];
-            hi[h] = a;
-            lo[h] = (_Float16)(v[h] - (float)a);
-        }
-        *(sw_half8 *)(p + (2 * s) * D + k0) = hi;
-        *(sw_half8 *)(p + (2 * s + 1) * D + k0) = lo;
-    }
-}
-
-__device__ __forceinline__ uint16_t bf16_rne(float f) {
-    uint32_t u = __builtin_bit_cast(uint32_t, f);
-    u += 0x7FFFu + ((u >> 16) & 1u);
-    return (uint16_t)(u >> 16);
-}
-
-// x f32 [S,D] -> bf16 planes [2S,D] (natural order)
-__global__ void k_prep_bf16(const float *__restrict__ x, int S, int D, uint16_t *__restrict__ p) {
-    const int64_t n = (int64_t)S * D;
-    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t s = i / D, k = i % D;
-        const float v = x[i];
-        const uint16_t hi = bf16_rne(v);
-        const uint16_t lo = bf16_rne(v - __builtin_bit_cast(float, (uint32_t)hi << 16));
-        p[(2 * s) * D + k] = hi;
-        p[(2 * s + 1) * D + k] = lo;
-    }
-}
-
-int sw_launch_prep_f16(hipStream_t st, const float *x, int S, int D, _Float16 *planes) {
-    if (D % 8 || S <= 0) return -1;
-    const int64_t nb = (int64_t)S * (D / 8);
-    const unsigned grid = (unsigned)sw_imin64((nb + 255) / 256, 4096);
-    hipLaunchKernelGGL(k_prep_f16, dim3(grid), dim3(256), 0, st, x, S, D, planes);
-    return launch_err();
-}
-
-int sw_launch_prep_bf16(hipStream_t st, const float *x, int S, int D, uint16_t *planes) {
-    if (S <= 0) return -1;
-    const int64_t n = (int64_t)S * D;
-    const unsigned grid = (unsigned)sw_imin64((n + 255) / 256, 4096);
-    hipLaunchKernelGGL(k_prep_bf16, dim3(grid), dim3(256), 0, st, x, S, D, planes);
-    return launch_err();
-}
-
 // ------------------------------------------------------------ router ----
 // Chain-major router copy: Wc[(e*16 + j)*M + m] = W[e*D + 16m + j], M = D/16,
 // so lane j of expert e reads its FMA chain contiguously.
@@ -84,42 +27,195 @@ int sw_launch_chain_major(hipStream_t st, const void *W, int w_bf16, int E, int 
     return launch_err();
 }
 
+// ------------------------------------------------------------ gate + top-k ----
+// One wave finishes the routing of one token.  Activation with the reference's
+// host expressions and glibc-exact expf/log1pf (c/moe_block.h:26;
+// c/moe_math.h:54,68-72), then moe_topk (c/moe_arch.h:64-89): K passes of
+// "largest score+bias among the unselected, valid only if > -1e30, ties to
+// the lowest id", the all-invalid fallback to the lowest unselected id,
+// weight = unbiased score, optional renormalisation summed in rank order
+// (c/moe_block.h:121-122).  All four waves of the block call this (barriers);
+// only wave 0 works.
+#define TK_MAXE 1024
+#define TK_NPER (TK_MAXE / 64)
+struct TopkShared {
+    float sc[TK_MAXE];
+    float wk[64];
+    int sk[64];
+    float inv;
+};
+
+__device__ __forceinline__ float load_agent(const float *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ void gate_topk_token(const float *rl, int E, int K, int act, const float *__restrict__ bias, int use_bias,
+                                int norm, int *sel, float *wout, TopkShared &sh) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int nper = (E + 63) / 64;
+    float v[TK_NPER], key[TK_NPER];
+    if (wave == 0) {
+#pragma unroll
+        for (int i = 0; i < TK_NPER; i++) {
+            const int e = lane + 64 * i;
+            v[i] = (i < nper && e < E) ? load_agent(rl + e) : 0.f;
+        }
+    }
+    if (act == 1) {                                   // softmax (the laguna contract)
+        if (wave == 0) {
+            float mx = -__builtin_inff();
+            bool any = false;
+#pragma unroll
+            for (int i = 0; i < TK_NPER; i++) {
+                const int e = lane + 64 * i;
+                if (i < nper && e < E && v[i] == v[i]) { mx = any ? fmaxf(mx, v[i]) : v[i]; any = true; }
+            }
+            for (int o = 32; o; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+            const float r0 = __shfl(v[0], 0);
+            if (r0 != r0) mx = r0;                    // a NaN in slot 0 propagates, as in the scan
+#pragma unroll
+            for (int i = 0; i < TK_NPER; i++) {
+                const int e = lane + 64 * i;
+                if (i < nper && e < E) sh.sc[e] = sw_expf(v[i] - mx);
+            }
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            double sum = 0.0;
+            for (int e = 0; e < E; e++) sum += (double)sh.sc[e];
+            sh.inv = (float)(1.0 / sum);
+        }
+        __syncthreads();
+        if (wave == 0) {
+            const float inv = sh.inv;
+#pragma unroll
+            for (int i = 0; i < TK_NPER; i++) {
+                const int e = lane + 64 * i;
+                if (i < nper && e < E) { v[i] = sh.sc[e] * inv; sh.sc[e] = v[i]; }
+            }
+        }
+    } else if (wave == 0) {
+#pragma unroll
+        for (int i = 0; i < TK_NPER; i++) {
+            const int e = lane + 64 * i;
+            if (i < nper && e < E) {
+                v[i] = (act == 2) ? sw_softplus_ref(v[i]) : sw_sigmoid_ref(v[i]);
+                sh.sc[e] = v[i];
+            }
+        }
+    }
+    __syncthreads();
+    if (wave == 0) {
+#pragma unroll
+        for (int i = 0; i < TK_NPER; i++) {
+            const int e = lane + 64 * i;
+            key[i] = (i < nper && e < E) ? v[i] + ((use_bias && bias) ? bias[e] : 0.f) : 0.f;
+        }
+        uint32_t taken = 0;
+        for (int a = 0; a < K; a++) {
+            float bv = 0.f;
+            int bi = -1, lowfree = 0x7fffffff;
+#pragma unroll
+            for (int i = 0; i < TK_NPER; i++) {
+                const int e = lane + 64 * i;
+                if (i < nper && e < E && !((taken >> i) & 1u)) {
+                    if (e < lowfree) lowfree = e;
+                    if (key[i] > -1e30f && (bi < 0 || key[i] > bv)) { bv = key[i]; bi = e; }
+                }
+            }
+            for (int o = 32; o; o >>= 1) {
+                const float ov = __shfl_xor(bv, o);
+                const int oi = __shfl_xor(bi, o);
+                const int ol = __shfl_xor(lowfree, o);
+                bool take;
+                if (oi < 0) take = false;
+                else if (bi < 0) take = true;
+                else if (ov > bv) take = true;
+                else if (bv > ov) take = false;
+                else take = oi < bi;
+                if (take) { bv = ov; bi = oi; }
+                lowfree = min(lowfree, ol);
+            }
+            if (bi < 0) bi = (lowfree < E) ? lowfree : 0;
+            if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
+            if (lane == 0) { sh.sk[a] = bi; sh.wk[a] = sh.sc[bi]; }
+        }
+        if (lane == 0) {
+            if (norm) {
+                float sm = 0.f;
+                for (int a = 0; a < K; a++) sm += sh.wk[a];
+                for (int a = 0; a < K; a++) sh.wk[a] = sh.wk[a] / sm;
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+        if (lane < K) { sel[lane] = sh.sk[lane]; wout[lane] = sh.wk[lane]; }
+    }
+}
+
 // logits[s,e] = sum_i x[s,i] W[e,i] under the contract of the reference's
 // AVX-512 router (c/moe_matmul.h:25-43; bf16 weights c/moe_matmul.h:92-110):
 // 16 FMA chains, chain j over i = j mod 16 ascending, then GCC's
 // _mm512_reduce_add_ps tree (j,j+8) -> (j,j+4) -> (0+2, 1+3) -> final.
-// Lane j of a 16-lane group runs chain j; the tree is three shuffles.
-// One wave = 4 experts; one block per (4 experts, token).
+// Lane j of a 16-lane group runs chain j (weights chain-major, all loads in
+// flight before the chain starts; x transposed in LDS so a lane reads its
+// chain's inputs contiguously); the tree is four shuffles.  Block = 16
+// experts of one token; the block that finishes a token's last logits (a
+// per-token arrival counter, reset by that block) runs gate + top-k.
+#define RT_MAXLD 32
 template <int BF16>
-__global__ __launch_bounds__(64) void k_router(const void *__restrict__ Wc, const float *__restrict__ x, int D, int E,
-                                               const float *__restrict__ lbias, float *__restrict__ logits) {
-    extern __shared__ float xs[];
-    const int s = blockIdx.y;
-    const int tid = threadIdx.x;
-    const float *xr = x + (int64_t)s * D;
-    for (int i = tid * 4; i < D; i += 256) *(sw_f32x4 *)(xs + i) = *(const sw_f32x4 *)(xr + i);
-    __syncthreads();
-    const int e = blockIdx.x * 4 + (tid >> 4), j = tid & 15;
-    const int M = D / 16;
+__global__ __launch_bounds__(256) void k_router_topk(const void *__restrict__ Wc, const float *__restrict__ x, int D, int E,
+                                                     const float *__restrict__ lbias, float *__restrict__ logits,
+                                                     int *__restrict__ counters, int K, int act,
+                                                     const float *__restrict__ cbias, int use_bias, int norm,
+                                                     int *__restrict__ sel, float *__restrict__ wout) {
+    extern __shared__ __align__(16) float xt[];      // [16][M + 4]
+    __shared__ TopkShared sh;
+    __shared__ int last;
+    const int s = blockIdx.y, tid = threadIdx.x;
+    const int M = D / 16, ML = M + 4;
+    const int e = blockIdx.x * 16 + (tid >> 4), j = tid & 15;
+    const bool valid = e < E;
+    const int per = BF16 ? 8 : 4;                     // chain elements per 16-byte load
     float acc = 0.f;
-    if (e < E) {
-        if (BF16) {
-            const uint16_t *ch = (const uint16_t *)Wc + (int64_t)(e * 16 + j) * M;
-            for (int m0 = 0; m0 < M; m0 += 8) {
-                const sw_u32x4 wv = *(const sw_u32x4 *)(ch + m0);
-                const uint32_t wd[4] = {wv.x, wv.y, wv.z, wv.w};
+    for (int m0 = 0; m0 < M; m0 += RT_MAXLD * per) {
+        const int nld = min(RT_MAXLD, (M - m0) / per);
+        sw_u32x4 wr[RT_MAXLD];
+        const char *ch = (const char *)Wc + ((int64_t)(valid ? e : 0) * 16 + j) * M * (BF16 ? 2 : 4) + (int64_t)m0 * (BF16 ? 2 : 4);
 #pragma unroll
-                for (int u = 0; u < 8; u++) {
-                    const uint32_t bits = (u & 1) ? (wd[u >> 1] & 0xFFFF0000u) : (wd[u >> 1] << 16);
-                    acc = __builtin_fmaf(xs[16 * (m0 + u) + j], __builtin_bit_cast(float, bits), acc);
+        for (int l = 0; l < RT_MAXLD; l++)
+            if (l < nld && valid) wr[l] = *(const sw_u32x4 *)(ch + 16 * l);
+        if (m0 == 0) {
+            const float *xr = x + (int64_t)s * D;
+            for (int i = tid * 4; i < D; i += 1024) {
+                const sw_f32x4 v = *(const sw_f32x4 *)(xr + i);
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    const int k = i + c;
+                    xt[(k & 15) * ML + (k >> 4)] = v[c];
                 }
             }
-        } else {
-            const float *ch = (const float *)Wc + (int64_t)(e * 16 + j) * M;
-            for (int m0 = 0; m0 < M; m0 += 4) {
-                const sw_f32x4 wv = *(const sw_f32x4 *)(ch + m0);
+            __syncthreads();
+        }
+        if (valid) {
+            const float *xj = xt + j * ML + m0;
 #pragma unroll
-                for (int u = 0; u < 4; u++) acc = __builtin_fmaf(xs[16 * (m0 + u) + j], wv[u], acc);
+            for (int l = 0; l < RT_MAXLD; l++) {
+                if (l < nld) {
+                    const uint32_t wd[4] = {wr[l].x, wr[l].y, wr[l].z, wr[l].w};
+                    if (BF16) {
+                        const sw_f32x4 xa = *(const sw_f32x4 *)(xj + 8 * l), xb = *(const sw_f32x4 *)(xj + 8 * l + 4);
+                        const float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+#pragma unroll
+                        for (int u = 0; u < 8; u++) {
+                            const uint32_t bits = (u & 1) ? (wd[u >> 1] & 0xFFFF0000u) : (wd[u >> 1] << 16);
+                            acc = __builtin_fmaf(xv[u], __builtin_bit_cast(float, bits), acc);
+                        }
+                    } else {
+                        const sw_f32x4 xa = *(const sw_f32x4 *)(xj + 4 * l);
+#pragma unroll
+                        for (int u = 0; u < 4; u++) acc = __builtin_fmaf(xa[u], __builtin_bit_cast(float, wd[u]), acc);
+                    }
+                }
             }
         }
     }
@@ -128,116 +224,34 @@ __global__ __launch_bounds__(64) void k_router(const void *__restrict__ Wc, cons
     v = v + __shfl_down(v, 4, 16);
     v = v + __shfl_down(v, 2, 16);
     v = v + __shfl_down(v, 1, 16);
-    if (j == 0 && e < E) {
+    if (j == 0 && valid) {
         if (lbias) v = v + lbias[e];
         logits[(int64_t)s * E + e] = v;
     }
-}
-
-int sw_launch_router(hipStream_t st, const void *Wc, int w_bf16, const float *x, int S, int D, int E,
-                     const float *logit_bias, float *logits) {
-    if (D % 128 || D > 16384 || E <= 0 || S <= 0) return -1;
-    dim3 grid((unsigned)((E + 3) / 4), (unsigned)S);
-    const size_t lds = (size_t)D * sizeof(float);
-    if (w_bf16) hipLaunchKernelGGL(k_router<1>, grid, dim3(64), lds, st, Wc, x, D, E, logit_bias, logits);
-    else hipLaunchKernelGGL(k_router<0>, grid, dim3(64), lds, st, Wc, x, D, E, logit_bias, logits);
-    return launch_err();
-}
-
-// ------------------------------------------------------------ gate + top-k ----
-// One wave per token.  Activation with the reference's host expressions and
-// glibc-exact expf/log1pf (c/moe_block.h:26; c/moe_math.h:54,68-72), then
-// moe_topk (c/moe_arch.h:64-89): K passes of "largest score+bias among the
-// unselected, valid only if > -1e30, ties to the lowest id", the all-invalid
-// fallback to the lowest unselected id, weight = unbiased score, optional
-// renormalisation summed in rank order (c/moe_block.h:121-122).
-#define TK_MAXE 1024
-__global__ __launch_bounds__(64) void k_gate_topk(const float *__restrict__ logits, int E, int K, int act,
-                                                  const float *__restrict__ bias, int use_bias, int norm,
-                                                  int *__restrict__ sel, float *__restrict__ wout) {
-    __shared__ float sc[TK_MAXE];
-    __shared__ float wk[64];
-    __shared__ int sk[64];
-    __shared__ float bc;
-    const int s = blockIdx.x, lane = threadIdx.x;
-    const float *rl = logits + (int64_t)s * E;
-    if (act == 1) {                                   // softmax (laguna contract)
-        float mx = -__builtin_inff();
-        bool any = false;
-        for (int e = lane; e < E; e += 64) {
-            const float v = rl[e];
-            if (v == v) { mx = any ? fmaxf(mx, v) : v; any = true; }
-        }
-        for (int o = 32; o; o >>= 1) {
-            const float t = __shfl_xor(mx, o);
-            mx = fmaxf(mx, t);
-        }
-        if (rl[0] != rl[0]) mx = rl[0];               // a NaN in slot 0 propagates, as in the scan
-        for (int e = lane; e < E; e += 64) sc[e] = sw_expf(rl[e] - mx);
-        __syncthreads();
-        if (lane == 0) {
-            double sum = 0.0;
-            for (int e = 0; e < E; e++) sum += (double)sc[e];
-            bc = (float)(1.0 / sum);
-        }
-        __syncthreads();
-        const float inv = bc;
-        for (int e = lane; e < E; e += 64) sc[e] = sc[e] * inv;
-    } else {
-        for (int e = lane; e < E; e += 64) {
-            const float v = rl[e];
-            sc[e] = (act == 2) ? sw_softplus_ref(v) : sw_sigmoid_ref(v);
-        }
-    }
+    if (!counters) return;                            // logits only
+    __threadfence();
     __syncthreads();
-    uint32_t taken = 0;                               // bit i: expert lane + 64 i selected
-    const int nper = (E + 63) / 64;
-    for (int a = 0; a < K; a++) {
-        float bv = 0.f;
-        int bi = -1, lowfree = 0x7fffffff;
-        for (int i = 0; i < nper; i++) {
-            const int e = lane + 64 * i;
-            if (e >= E || ((taken >> i) & 1u)) continue;
-            if (e < lowfree) lowfree = e;
-            const float v = sc[e] + ((use_bias && bias) ? bias[e] : 0.f);
-            if (v > -1e30f && (bi < 0 || v > bv)) { bv = v; bi = e; }
-        }
-        for (int o = 32; o; o >>= 1) {
-            const float ov = __shfl_xor(bv, o);
-            const int oi = __shfl_xor(bi, o);
-            const int ol = __shfl_xor(lowfree, o);
-            bool take;
-            if (oi < 0) take = false;
-            else if (bi < 0) take = true;
-            else if (ov > bv) take = true;
-            else if (bv > ov) take = false;
-            else take = oi < bi;
-            if (take) { bv = ov; bi = oi; }
-            lowfree = min(lowfree, ol);
-        }
-        if (bi < 0) bi = (lowfree < E) ? lowfree : 0;
-        if ((bi & 63) == lane && bi < E) taken |= 1u << (bi >> 6);
-        if (lane == 0) { sk[a] = bi; wk[a] = sc[bi]; }
-    }
+    if (tid == 0) last = atomicAdd(&counters[s], 1) == (int)gridDim.x - 1;
     __syncthreads();
-    if (lane == 0) {
-        if (norm) {
-            float sm = 0.f;
-            for (int a = 0; a < K; a++) sm += wk[a];
-            for (int a = 0; a < K; a++) wk[a] = wk[a] / sm;
-        }
-        for (int a = 0; a < K; a++) {
-            sel[(int64_t)s * K + a] = sk[a];
-            wout[(int64_t)s * K + a] = wk[a];
-        }
-    }
+    if (!last) return;
+    __threadfence();
+    gate_topk_token(logits + (int64_t)s * E, E, K, act, cbias, use_bias, norm, sel + (int64_t)s * K, wout + (int64_t)s * K, sh);
+    if (tid == 0) counters[s] = 0;
 }
 
-int sw_launch_gate_topk(hipStream_t st, const float *logits, int S, int E, int K, int route_act,
-                        const float *corr_bias, int use_corr_bias, int norm_topk, int *sel, float *w) {
-    if (E <= 0 || E > TK_MAXE || K <= 0 || K > 64 || K > E || S <= 0 || route_act < 0 || route_act > 2) return -1;
-    hipLaunchKernelGGL(k_gate_topk, dim3((unsigned)S), dim3(64), 0, st, logits, E, K, route_act, corr_bias,
-                       use_corr_bias, norm_topk, sel, w);
+int sw_launch_router_topk(hipStream_t st, const void *Wc, int w_bf16, const float *x, int S, int D, int E,
+                          const float *logit_bias, float *logits, int *counters, int K, int route_act,
+                          const float *corr_bias, int use_corr_bias, int norm_topk, int *sel, float *w) {
+    if (D % 128 || D > 8192 || E <= 0 || E > TK_MAXE || S <= 0 || K <= 0 || K > 64 || K > E) return -1;
+    if (route_act < 0 || route_act > 2) return -1;
+    dim3 grid((unsigned)((E + 15) / 16), (unsigned)S);
+    const size_t lds = (size_t)16 * (D / 16 + 4) * sizeof(float);
+    if (w_bf16)
+        hipLaunchKernelGGL(k_router_topk<1>, grid, dim3(256), lds, st, Wc, x, D, E, logit_bias, logits, counters, K,
+                           route_act, corr_bias, use_corr_bias, norm_topk, sel, w);
+    else
+        hipLaunchKernelGGL(k_router_topk<0>, grid, dim3(256), lds, st, Wc, x, D, E, logit_bias, logits, counters, K,
+                           route_act, corr_bias, use_corr_bias, norm_topk, sel, w);
     return launch_err();
 }
 
@@ -332,11 +346,21 @@ __global__ void k_combine(const float *__restrict__ slots, const int *__restrict
     for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n4; i += (int64_t)gridDim.x * blockDim.x) {
         const int64_t s = i / (D / 4), d = (i % (D / 4)) * 4;
         sw_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        for (int a = 0; a < K; a++) {
-            const float wa = w[s * K + a];
-            const sw_f32x4 v = *(const sw_f32x4 *)(slots + (int64_t)rowof[s * K + a] * D + d);
+        for (int a0 = 0; a0 < K; a0 += 8) {
+            sw_f32x4 v[8];
+            float wa[8];
 #pragma unroll
-            for (int c = 0; c < 4; c++) acc[c] = __builtin_fmaf(wa, v[c], acc[c]);
+            for (int u = 0; u < 8; u++) {
+                if (a0 + u < K) {
+                    wa[u] = w[s * K + a0 + u];
+                    v[u] = *(const sw_f32x4 *)(slots + (int64_t)rowof[s * K + a0 + u] * D + d);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+                if (a0 + u < K)
+#pragma unroll
+                    for (int c = 0; c < 4; c++) acc[c] = __builtin_fmaf(wa[u], v[u][c], acc[c]);
         }
 #pragma unroll
         for (int c = 0; c < 4; c++) acc[c] = acc[c] * route_scale;

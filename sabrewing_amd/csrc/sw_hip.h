@@ -50,10 +50,11 @@ static inline int64_t sw_imin64(int64_t a, int64_t b) { return a < b ? a : b; }
 // gbeg; packed row j takes its activation from row grow[j] of the input planes
 // (or row j itself when grow is null).
 struct SwGroups {
-    const int *gexp, *gbeg, *gcnt;   // [ngroups]
+    const int *gexp, *gbeg, *gcnt;   // [ngroups]; null gexp/gbeg mean 0, null gcnt means cnt_const
     const int *grow;                 // [T] or null
     const int *G;                    // device count (null: use ngroups_max)
     int ngroups_max;
+    int cnt_const;
 };
 
 // int4 weight tensor of E experts, O rows each, K inputs
@@ -70,22 +71,28 @@ struct SwBf16 {
 };
 
 // ---- kernels (launch wrappers, all async on `st`) ----
-int sw_launch_prep_f16(hipStream_t st, const float *x, int S, int D, _Float16 *planes);
-int sw_launch_prep_bf16(hipStream_t st, const float *x, int S, int D, uint16_t *planes);
-// logits[S,E] = x @ W^T under the 16-lane FMA-chain contract; Wc chain-major
-int sw_launch_router(hipStream_t st, const void *Wc, int w_bf16, const float *x, int S, int D, int E,
-                     const float *logit_bias, float *logits);
-int sw_launch_gate_topk(hipStream_t st, const float *logits, int S, int E, int K, int route_act,
-                        const float *corr_bias, int use_corr_bias, int norm_topk, int *sel, float *w);
+// router logits [S,E] (exact 16-lane FMA-chain contract; Wc chain-major) and,
+// with counters (zeroed [S] ints, left zeroed), gate + top-k per token
+int sw_launch_router_topk(hipStream_t st, const void *Wc, int w_bf16, const float *x, int S, int D, int E,
+                          const float *logit_bias, float *logits, int *counters, int K, int route_act,
+                          const float *corr_bias, int use_corr_bias, int norm_topk, int *sel, float *w);
 int sw_launch_bucket(hipStream_t st, const int *sel, int S, int K, int E, int *gexp, int *gbeg,
                      int *gcnt, int *G, int *grow, int *rowof);
 // out planes of SiLU-GLU(gate, up) for every packed row of every group
-// cb: MFMA column blocks (8 tokens each) kept per pass: 1 for single-token groups, 4 otherwise
-int sw_launch_q4_gateup(hipStream_t st, SwQ4 W, const _Float16 *xplanes, SwGroups g, int I, _Float16 *hplanes, int cb);
-// Y[packed row, O] (f32) for every group
-int sw_launch_q4_rows(hipStream_t st, SwQ4 W, const _Float16 *xplanes, SwGroups g, float *Y, int cb);
-int sw_launch_bf16_gateup(hipStream_t st, SwBf16 Wg, SwBf16 Wu, const uint16_t *xplanes, int S, uint16_t *hplanes);
-int sw_launch_bf16_rows(hipStream_t st, SwBf16 W, const uint16_t *xplanes, int S, float *Y);
+// maxtok: an upper bound of any group's token count (1 for the per-token path)
+// (x: f32 activations [tokens, K], split into hi/lo planes while staged)
+int sw_launch_q4_gateup(hipStream_t st, SwQ4 W, const float *x, SwGroups g, int I, _Float16 *hplanes, int maxtok);
+// Y[packed row, O] (f32) for every group, from f16 planes or from f32 rows
+int sw_launch_q4_rows(hipStream_t st, SwQ4 W, const _Float16 *planes, SwGroups g, float *Y, int maxtok);
+int sw_launch_q4_rows_x(hipStream_t st, SwQ4 W, const float *x, SwGroups g, float *Y, int maxtok);
+// bf16 weights, one implicit group of S tokens, K split in four quarters
+int sw_launch_bf16_gateup(hipStream_t st, SwBf16 Wg, SwBf16 Wu, const float *x, int S, uint16_t *hplanes);
+int sw_launch_bf16_rows(hipStream_t st, SwBf16 W, const uint16_t *planes, int S, float *Y);
+int sw_launch_bf16_rows_x(hipStream_t st, SwBf16 W, const float *x, int S, float *Y);
+// the int4 down projection fused with the rank-order combine for one token:
+// out[d] += (sum_a w[a] * down_{sel[a]}(h_a)[d]) * route_scale (+ shared[d])
+int sw_launch_q4_down_combine(hipStream_t st, SwQ4 W, const _Float16 *hplanes, const int *sel, const float *w, int K,
+                              float route_scale, const float *shared, float *out);
 // out[s] (+)= route_scale * sum_a w[s,a] * slots[rowof[s,a]] (+ shared[s])
 int sw_launch_combine(hipStream_t st, const float *slots, const int *rowof, const float *w, int S, int K, int D,
                       float route_scale, const float *shared, float *out, int accumulate);
