@@ -127,18 +127,32 @@ def run(args):
         l = i % len(layers)
         be.moe_forward(desc, wts[l], xptr(i), outs[l], B)
 
+    if args.calib_copy_mb:
+        # a plain device copy of known size, for scaling the FETCH_SIZE / WRITE_SIZE counters
+        n = args.calib_copy_mb << 20
+        a_, b_ = be.alloc(n), be.alloc(n)
+        be.lib.lag_hip_memset(int(a_), 1, n)
+        be.lib.lag_hip_d2d(int(b_), int(a_), n)
+        be.sync()
+        a_.free(); b_.free()
+        log(f"calibration copy: {args.calib_copy_mb} MiB device-to-device")
+
     for i in range(args.warmup):
         step(i)
     be.sync()
     ev0, ev1 = be.event(), be.event()
     be.record(ev0)
+    h0 = time.perf_counter()
     for i in range(args.steps):
         step(args.warmup + i)
+    host_us = (time.perf_counter() - h0) * 1e6 / args.steps
     be.record(ev1)
     be.sync()
     ms = be.elapsed_ms(ev0, ev1) / args.steps
     tok_s = B / (ms * 1e-3)
-    log(f"{cfg.name} B={B}: {ms * 1e3:.1f} us/step, {tok_s:.0f} tokens/s")
+    log(f"{cfg.name} B={B}: {ms * 1e3:.1f} us/step, {tok_s:.0f} tokens/s (host enqueue {host_us:.1f} us/step)")
+    if args.timed_only:
+        return
 
     # per-kernel times: the same steps again with every launch bracketed by events
     be.profile_reset()
@@ -214,6 +228,10 @@ def main():
     ap.add_argument("--seed", type=int, default=20261201)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--calib-copy-mb", type=int, default=0,
+                    help="one device-to-device copy of this many MiB before the timed steps (counter calibration)")
+    ap.add_argument("--timed-only", action="store_true",
+                    help="stop after the timed steps (no per-kernel pass, no CPU baseline, no JSON line)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the MoE block on one MI355X); "

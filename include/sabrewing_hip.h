@@ -120,6 +120,7 @@ int    lag_hip_last_groups(int *G, int *gexp, int *gbeg, int *gcnt, int cap);
 void  *lag_hip_alloc(size_t n);
 int    lag_hip_h2d(void *dst, const void *src, size_t n);
 int    lag_hip_d2h(void *dst, const void *src, size_t n);
+int    lag_hip_d2d(void *dst, const void *src, size_t n);   /* async on the backend stream */
 int    lag_hip_memset(void *dst, int v, size_t n);
 int    lag_hip_sync(void);
 void  *lag_hip_event_create(void);

@@ -112,7 +112,7 @@ static int grow_pinned(Buf &b, size_t need) {
     b.cap = need * 2;
     return 0;
 }
-static Buf g_arena, g_hin, g_hout, g_consts, g_counters;
+static Buf g_arena, g_hin, g_hout, g_consts;
 static int g_consts_k = 0;
 
 // carve aligned sub-buffers out of the arena
@@ -129,16 +129,6 @@ static int ensure_consts(int K) {   // iota[K], ones[K], zeros[K]
     for (int i = 0; i < k; i++) { h[i] = i; h[k + i] = 1; h[2 * k + i] = 0; }
     CK(hipMemcpy(g_consts.p, h.data(), h.size() * sizeof(int), hipMemcpyHostToDevice), "constant upload");
     g_consts_k = k;
-    return 0;
-}
-// per-token arrival counters of the fused router: zero on allocation, and
-// every use leaves them zero again
-static int g_counters_n = 0;
-static int ensure_counters(int S) {
-    if (S <= g_counters_n) return 0;
-    if (grow_dev(g_counters, (size_t)S * sizeof(int))) return -1;
-    CK(hipMemsetAsync(g_counters.p, 0, g_counters.cap, g_st), "counter clear");
-    g_counters_n = (int)(g_counters.cap / sizeof(int));
     return 0;
 }
 static const int *c_iota(void) { return (const int *)g_consts.p; }
@@ -197,6 +187,11 @@ extern "C" int lag_hip_d2h(void *dst, const void *src, size_t n) {
     if (!g_ok) return -1;
     CK(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, g_st), "d2h");
     CK(hipStreamSynchronize(g_st), "d2h sync");
+    return 0;
+}
+extern "C" int lag_hip_d2d(void *dst, const void *src, size_t n) {
+    if (!g_ok) return -1;
+    CK(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToDevice, g_st), "d2d");
     return 0;
 }
 extern "C" int lag_hip_memset(void *dst, int v, size_t n) {
@@ -384,7 +379,7 @@ extern "C" int lag_hip_router_chain(const void *W, void *Wc, int E, int D, int w
 }
 
 struct FwdScratch {
-    float *logits, *w, *slots, *sout;
+    float *logits, *scores, *w, *slots, *sout;
     int *sel, *gexp, *gbeg, *gcnt, *G, *grow, *rowof;
     _Float16 *hpl;
     uint16_t *shpl;
@@ -407,7 +402,8 @@ static int carve_fwd(const LagHipMoeDesc *d, int S, FwdScratch &f) {
     const int E = d->n_experts, K = d->topk, D = d->hidden, I = d->moe_inter, Is = d->shared_inter;
     const int T = S * K;
     Carve cv;
-    const size_t o_lg = cv.take((size_t)S * E * 4), o_sel = cv.take((size_t)T * 4), o_w = cv.take((size_t)T * 4);
+    const size_t o_lg = cv.take((size_t)S * E * 4), o_sc = cv.take((size_t)S * E * 4);
+    const size_t o_sel = cv.take((size_t)T * 4), o_w = cv.take((size_t)T * 4);
     const size_t o_gexp = cv.take((size_t)E * 4), o_gbeg = cv.take((size_t)E * 4), o_gcnt = cv.take((size_t)E * 4);
     const size_t o_G = cv.take(4), o_grow = cv.take((size_t)T * 4), o_rowof = cv.take((size_t)T * 4);
     const size_t o_hpl = cv.take((size_t)2 * T * I * 2);
@@ -416,7 +412,7 @@ static int carve_fwd(const LagHipMoeDesc *d, int S, FwdScratch &f) {
     if (d->shared_mode) { o_sh = cv.take((size_t)2 * S * Is * 2); o_so = cv.take((size_t)S * D * 4); }
     if (grow_dev(g_arena, cv.off)) return -1;
     char *A = (char *)g_arena.p;
-    f.logits = (float *)(A + o_lg); f.sel = (int *)(A + o_sel); f.w = (float *)(A + o_w);
+    f.logits = (float *)(A + o_lg); f.scores = (float *)(A + o_sc); f.sel = (int *)(A + o_sel); f.w = (float *)(A + o_w);
     f.gexp = (int *)(A + o_gexp); f.gbeg = (int *)(A + o_gbeg); f.gcnt = (int *)(A + o_gcnt); f.G = (int *)(A + o_G);
     f.grow = (int *)(A + o_grow); f.rowof = (int *)(A + o_rowof);
     f.hpl = (_Float16 *)(A + o_hpl); f.slots = (float *)(A + o_slot);
@@ -425,11 +421,11 @@ static int carve_fwd(const LagHipMoeDesc *d, int S, FwdScratch &f) {
     return 0;
 }
 
-static int route_dev(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const float *x, int S, float *logits, int *sel, float *wts) {
-    if (ensure_counters(S)) return -1;
+static int route_dev(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const float *x, int S, float *logits,
+                     float *scores, int *sel, float *wts) {
     PROF("router_topk");
     if (sw_launch_router_topk(g_st, w->router, d->router_bf16, x, S, d->hidden, d->n_experts, w->logit_bias, logits,
-                              (int *)g_counters.p, d->topk, d->route_act, w->corr_bias, d->use_corr_bias, d->norm_topk,
+                              scores, d->topk, d->route_act, w->corr_bias, d->use_corr_bias, d->norm_topk,
                               sel, wts)) return fail_msg("router launch");
     return 0;
 }
@@ -439,7 +435,7 @@ extern "C" int lag_hip_route(const LagHipMoeDesc *d, const LagHipMoeWeights *w, 
     if (!g_ok || fault_injected() || !desc_ok(d, w) || S <= 0) return -1;
     FwdScratch f;
     if (carve_fwd(d, S, f)) return -1;
-    return route_dev(d, w, x, S, logits ? logits : f.logits, sel, wts);
+    return route_dev(d, w, x, S, logits ? logits : f.logits, f.scores, sel, wts);
 }
 
 // The shared expert runs on the side stream, forked after everything queued
@@ -461,9 +457,9 @@ extern "C" int lag_hip_moe_forward(const LagHipMoeDesc *d, const LagHipMoeWeight
     const int E = d->n_experts, K = d->topk, D = d->hidden, I = d->moe_inter;
     const int T = S * K;
     FwdScratch f;
-    if (carve_fwd(d, S, f) || ensure_consts(K) || ensure_counters(S)) return -1;
+    if (carve_fwd(d, S, f) || ensure_consts(K)) return -1;
     if (d->shared_mode && shared_fork(d, w, x, S, f)) return -1;
-    if (route_dev(d, w, x, S, f.logits, f.sel, f.w)) return -1;
+    if (route_dev(d, w, x, S, f.logits, f.scores, f.sel, f.w)) return -1;
     SwQ4 gu = {(const uint8_t *)w->gu_q, w->gu_s, 2 * I, D, d->gs};
     SwQ4 dn = {(const uint8_t *)w->dn_q, w->dn_s, D, I, d->gs};
     if (S == 1) {                        // per-token: the K picks in rank order, fused down + combine

@@ -71,10 +71,11 @@ struct SwBf16 {
 };
 
 // ---- kernels (launch wrappers, all async on `st`) ----
-// router logits [S,E] (exact 16-lane FMA-chain contract; Wc chain-major) and,
-// with counters (zeroed [S] ints, left zeroed), gate + top-k per token
+// router logits [S,E] (exact 16-lane FMA-chain contract; Wc chain-major), the
+// sigmoid / softplus scores [S,E] next to them, and, with sel non-null, gate +
+// top-k per token (a second kernel; softmax is computed there)
 int sw_launch_router_topk(hipStream_t st, const void *Wc, int w_bf16, const float *x, int S, int D, int E,
-                          const float *logit_bias, float *logits, int *counters, int K, int route_act,
+                          const float *logit_bias, float *logits, float *scores, int K, int route_act,
                           const float *corr_bias, int use_corr_bias, int norm_topk, int *sel, float *w);
 int sw_launch_bucket(hipStream_t st, const int *sel, int S, int K, int E, int *gexp, int *gbeg,
                      int *gcnt, int *G, int *grow, int *rowof);

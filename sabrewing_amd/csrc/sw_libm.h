@@ -40,8 +40,16 @@ __host__ __device__ static inline double sw_asf64(uint64_t u) { return __builtin
       0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull, \
       0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull }
 
-__host__ __device__ static inline float sw_expf(float x) {
-    const uint64_t tab[32] = SW_EXP2F_TAB;
+// the table lives in memory on both sides (a per-lane index into a local
+// array would otherwise be lowered to register moves or private memory)
+#if defined(__HIP_DEVICE_COMPILE__)
+__device__ static const uint64_t sw_exp2f_tab[32] = SW_EXP2F_TAB;
+#else
+static const uint64_t sw_exp2f_tab[32] = SW_EXP2F_TAB;
+#endif
+
+// tab: the 32 entries above (sw_exp2f_tab, or a copy of it in LDS)
+__host__ __device__ static inline float sw_expf_t(float x, const uint64_t *tab) {
     const double inv_ln2_n = 0x1.71547652b82fep+5;       // 32 / ln 2
     const double shift = 0x1.8p+52;
     const double c0 = 0x1.c6af84b912394p-20, c1 = 0x1.ebfce50fac4f3p-13, c2 = 0x1.62e42ff0c52d6p-6;
@@ -66,6 +74,7 @@ __host__ __device__ static inline float sw_expf(float x) {
     y = y * s;
     return (float)y;
 }
+__host__ __device__ static inline float sw_expf(float x) { return sw_expf_t(x, sw_exp2f_tab); }
 
 __host__ __device__ static inline float sw_log1pf(float x) {
     const float ln2_hi = 6.9313812256e-01f, ln2_lo = 9.0580006145e-06f;
@@ -132,7 +141,11 @@ __host__ __device__ static inline float sw_log1pf(float x) {
 }
 
 // gate activations with the reference's expressions
-__host__ __device__ static inline float sw_sigmoid_ref(float x) { return 1.0f / (1.0f + sw_expf(-x)); }
-__host__ __device__ static inline float sw_softplus_ref(float x) { return x > 20.0f ? x : sw_log1pf(sw_expf(x)); }
+__host__ __device__ static inline float sw_sigmoid_ref_t(float x, const uint64_t *tab) { return 1.0f / (1.0f + sw_expf_t(-x, tab)); }
+__host__ __device__ static inline float sw_softplus_ref_t(float x, const uint64_t *tab) {
+    return x > 20.0f ? x : sw_log1pf(sw_expf_t(x, tab));
+}
+__host__ __device__ static inline float sw_sigmoid_ref(float x) { return sw_sigmoid_ref_t(x, sw_exp2f_tab); }
+__host__ __device__ static inline float sw_softplus_ref(float x) { return sw_softplus_ref_t(x, sw_exp2f_tab); }
 
 #endif

@@ -148,3 +148,29 @@ def test_fault_injection(be, orc):
     y = be.matmul_q4(x, dp, ds, 16, 0)
     assert np.allclose(y, orc.matmul_q4(x, p, s), rtol=1e-5, atol=1e-6)
     dp.free(); ds.free()
+
+
+@pytest.mark.parametrize("D,I", [(4096, 256), (1024, 1536)])
+def test_group_large_groups_chunked(be, orc, D, I):
+    """groups of 8 tokens: the activation staging no longer fits LDS whole and
+    runs in chunks (D=4096: K-split 2 with two chunks per slice; I=1536 down:
+    a last chunk shorter than the others), still bit-identical per token"""
+    from dataclasses import replace
+    cfg = replace(cf.scaled(cf.C2_SIGMOID, D=D, E=4, K=2, I=I, Is=128), gs=32)
+    L = synth.make_layer(orc, cfg, 77)
+    dev = DevExperts(be, L)
+    S_, K, E = 8, 2, 4
+    sel = np.tile(np.array([[1, 3]], np.int32), (S_, 1))
+    w = np.full((S_, K), 0.5, np.float32)
+    x = synth.make_x(orc, cfg, 78, S_)
+    ref = np.stack([be.moe_experts(x[s], dev, sel[s], w[s], 32) for s in range(S_)])
+    G, gexp, gbeg, gcnt, grow, rowof = orc.bucket(sel, S_, K, E)
+    assert list(gcnt[:G]) == [8, 8]
+    grp = be.moe_group(x, dev, gexp, gbeg, gcnt, grow, rowof, w, K, 32)
+    assert np.array_equal(grp.view(np.uint32), ref.view(np.uint32))
+    want = np.zeros((S_, D), np.float32)
+    for s in range(S_):
+        for a in range(K):
+            want[s] = np.float32(w[s, a]) * cpu_expert(orc, L, int(sel[s, a]), x[s], 32) + want[s]
+    assert normwise(grp, want) < 2e-3
+    dev.free()
