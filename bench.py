@@ -34,25 +34,27 @@ def log(*a):
 
 def kernel_bytes(cfg, S, G):
     """algorithmic HBM bytes per launch of each kernel of the forward pass:
-    every weight byte the launch needs once, activations in and out once"""
+    every weight byte the launch needs once, activations in and out once
+    (dot8 limbs: 80 bytes + one f32 factor per 32 inputs)"""
     D, I, Is, E, K = cfg.D, cfg.I, cfg.Is, cfg.E, cfg.K
     ngD, ngI = (D // cfg.gs, I // cfg.gs) if cfg.gs else (1, 1)
     T = S * K
+    limb = lambda n: n // 32 * (80 + 4)
     gu_w = G * (2 * I * D // 2 + 2 * I * ngD * 4)
     dn_w = G * (D * I // 2 + D * ngI * 4)
+    sh_gu = 2 * Is * D * 2 if cfg.shared_mode else 0
+    sh_dn = D * Is * 2 if cfg.shared_mode else 0
     b = {
-        "router_topk": cfg.router_bytes() + S * D * 4 + S * E * 4 + T * 8,
-        "q4_gateup_glu": gu_w + S * D * 4 + 2 * T * I * 2,
+        "stage_route": cfg.router_bytes() + S * D * 4 + 2 * S * E * 4 + S * limb(D) + sh_gu + S * Is * 4,
+        "stage_experts": gu_w + S * limb(D) + T * limb(I) + sh_dn + S * Is * 4 + S * D * 4,
     }
     if S == 1:
-        b["q4_down_combine"] = dn_w + 2 * T * I * 2 + T * 8 + 2 * D * 4 + (D * 4 if cfg.shared_mode else 0)
+        b["q4_down_combine"] = dn_w + T * limb(I) + T * 8 + 2 * D * 4 + (D * 4 if cfg.shared_mode else 0)
     else:
+        b["gate_topk"] = 2 * S * E * 4 + T * 8
         b["bucket"] = T * 4 * 3 + E * 12
-        b["q4_down"] = dn_w + 2 * T * I * 2 + T * D * 4
+        b["q4_down"] = dn_w + T * limb(I) + T * D * 4
         b["combine"] = T * D * 4 + 2 * S * D * 4 + (S * D * 4 if cfg.shared_mode else 0) + T * 8
-    if cfg.shared_mode:
-        b["shared_gateup_glu"] = 2 * Is * D * 2 + S * D * 4 + 2 * S * Is * 2
-        b["shared_down"] = D * Is * 2 + 2 * S * Is * 2 + S * D * 4
     return b
 
 
@@ -148,9 +150,27 @@ def run(args):
     host_us = (time.perf_counter() - h0) * 1e6 / args.steps
     be.record(ev1)
     be.sync()
-    ms = be.elapsed_ms(ev0, ev1) / args.steps
+    ms_eager = be.elapsed_ms(ev0, ev1) / args.steps
+    log(f"{cfg.name} B={B} eager: {ms_eager * 1e3:.1f} us/step, {B / (ms_eager * 1e-3):.0f} tokens/s "
+        f"(host enqueue {host_us:.1f} us/step)")
+    ms = ms_eager
+    if not args.eager:
+        # the same K steps recorded once and replayed with one submission: the
+        # device time of the steps without the host's per-launch cost
+        be.graph_begin()
+        for i in range(args.steps):
+            step(args.warmup + i)
+        g = be.graph_end()
+        be.graph_launch(g)
+        be.sync()
+        be.record(ev0)
+        be.graph_launch(g)
+        be.record(ev1)
+        be.sync()
+        be.graph_destroy(g)
+        ms = be.elapsed_ms(ev0, ev1) / args.steps
     tok_s = B / (ms * 1e-3)
-    log(f"{cfg.name} B={B}: {ms * 1e3:.1f} us/step, {tok_s:.0f} tokens/s (host enqueue {host_us:.1f} us/step)")
+    log(f"{cfg.name} B={B}: {ms * 1e3:.1f} us/step, {tok_s:.0f} tokens/s ({'eager' if args.eager else 'graph replay'})")
     if args.timed_only:
         return
 
@@ -198,6 +218,8 @@ def run(args):
         "metric": "MoE-layer tokens/s + % peak HBM GB/s, int4 experts, batch 1 and batch 32",
         "value": round(tok_s, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "submission": "eager" if args.eager else "graph replay of the timed steps",
+        "eager_value": round(B / (ms_eager * 1e-3), 1), "eager_host_enqueue_us": round(host_us, 1),
         "dtype": "int4 weights (group-32 f32 scales) x f32 activations, f32 accumulate",
         "data": "synthetic: seeded N(0,0.02) int4 weights generated on device, N(0,1) bf16-valued tokens",
         "config": {"workload": cfg.name, "batch": B, "hidden": cfg.D, "experts": cfg.E, "topk": cfg.K,
@@ -230,6 +252,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--calib-copy-mb", type=int, default=0,
                     help="one device-to-device copy of this many MiB before the timed steps (counter calibration)")
+    ap.add_argument("--eager", action="store_true",
+                    help="time the per-call submission only (default: also record the steps as one graph and time its replay)")
     ap.add_argument("--timed-only", action="store_true",
                     help="stop after the timed steps (no per-kernel pass, no CPU baseline, no JSON line)")
     args = ap.parse_args()

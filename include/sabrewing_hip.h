@@ -128,6 +128,19 @@ int    lag_hip_event_record(void *ev);
 float  lag_hip_event_elapsed_ms(void *start, void *end);
 void   lag_hip_event_destroy(void *ev);
 
+/* ---------------- graphs ----------------
+ * Record the device-pointer entries (lag_hip_moe_forward, lag_hip_route,
+ * lag_hip_d2d) issued between begin and end into one graph, replayed with a
+ * single submission by lag_hip_graph_launch (async on the backend stream).
+ * Pointers and shapes are fixed at recording; scratch must already be large
+ * enough (issue the same shapes once first), else the entry fails.  No
+ * counterpart in the reference (its decode loop launches per layer): this
+ * is the launch-overhead-free way to drive a decode step. */
+int    lag_hip_graph_begin(void);
+void  *lag_hip_graph_end(void);          /* NULL on failure */
+int    lag_hip_graph_launch(void *g);
+void   lag_hip_graph_destroy(void *g);
+
 /* per-kernel timing with events on the backend stream (the analogue of the
  * reference's COLI_CUDA_PROFILE=1, c/backend_cuda.cu:822-940) */
 int    lag_hip_profile(int enable);

@@ -26,7 +26,8 @@ EXPORTS = [
     "lag_hip_matmul_bf16", "lag_hip_matmul_q4", "lag_hip_expert_q4", "lag_hip_moe_experts", "lag_hip_moe_group",
     "lag_hip_matmul_q4_g", "lag_hip_expert_q4_g", "lag_hip_moe_experts_g", "lag_hip_moe_group_g",
     "lag_hip_router_upload", "lag_hip_router_chain", "lag_hip_moe_forward", "lag_hip_moe_block", "lag_hip_route",
-    "lag_hip_last_groups", "lag_hip_alloc", "lag_hip_h2d", "lag_hip_d2h", "lag_hip_d2d", "lag_hip_memset", "lag_hip_sync",
+    "lag_hip_last_groups", "lag_hip_alloc", "lag_hip_h2d", "lag_hip_d2h", "lag_hip_d2d", "lag_hip_memset",
+    "lag_hip_graph_begin", "lag_hip_graph_end", "lag_hip_graph_launch", "lag_hip_graph_destroy", "lag_hip_sync",
     "lag_hip_event_create", "lag_hip_event_record", "lag_hip_event_elapsed_ms", "lag_hip_event_destroy",
     "lag_hip_profile", "lag_hip_profile_count", "lag_hip_profile_read", "lag_hip_profile_reset",
     "lag_hip_gen_normal", "lag_hip_gen_bf16", "lag_hip_gen_q4", "lag_hip_selftest", "lag_hip_last_error",
@@ -76,6 +77,9 @@ def load_library(path=None):
     L.lag_hip_d2h.argtypes = [VP, VP, C.c_size_t]
     L.lag_hip_memset.argtypes = [VP, C.c_int, C.c_size_t]
     L.lag_hip_d2d.argtypes = [VP, VP, C.c_size_t]
+    L.lag_hip_graph_end.restype = VP
+    L.lag_hip_graph_launch.argtypes = [VP]
+    L.lag_hip_graph_destroy.argtypes = [VP]
     L.lag_hip_matmul_bf16.argtypes = [F32P, F32P, VP, C.c_int, C.c_int, C.c_int]
     L.lag_hip_matmul_q4.argtypes = [F32P, F32P, VP, VP, C.c_int, C.c_int, C.c_int]
     L.lag_hip_matmul_q4_g.argtypes = [F32P, F32P, VP, VP, C.c_int, C.c_int, C.c_int, C.c_int]
@@ -246,6 +250,22 @@ class Backend:
 
     def gen_q4(self, qbuf, sbuf, seed, sigma, rows, K, gs, row0=0):
         self.check(self.lib.lag_hip_gen_q4(VP(int(qbuf)), VP(int(sbuf)), seed, sigma, row0, rows, K, gs), "gen_q4")
+
+    # ---- graphs ----
+    def graph_begin(self):
+        self.check(self.lib.lag_hip_graph_begin(), "graph begin")
+
+    def graph_end(self):
+        g = self.lib.lag_hip_graph_end()
+        if not g:
+            raise BackendError(f"graph end failed: {self.last_error()}")
+        return g
+
+    def graph_launch(self, g):
+        self.check(self.lib.lag_hip_graph_launch(g), "graph launch")
+
+    def graph_destroy(self, g):
+        self.lib.lag_hip_graph_destroy(g)
 
     # ---- timing / profile ----
     def event(self):

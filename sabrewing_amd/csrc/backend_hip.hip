@@ -16,9 +16,8 @@
 
 static int g_ok = 0;
 static int g_dev = 0;
+static int g_capturing = 0;             // between lag_hip_graph_begin and _end: nothing may allocate or sync
 static hipStream_t g_st = nullptr;      // the backend stream (all entry points are ordered on it)
-static hipStream_t g_side = nullptr;    // shared expert, overlapped with routing and the routed experts
-static hipEvent_t g_ev_fork = nullptr, g_ev_join = nullptr;
 static char g_err[256] = "";
 
 static int fail(const char *what, hipError_t e) {
@@ -66,7 +65,6 @@ static int prof_rec(const char *name) {
 static void prof_flush(void) {
     if (g_pending.empty()) return;
     (void)hipStreamSynchronize(g_st);
-    if (g_side) (void)hipStreamSynchronize(g_side);
     for (auto &p : g_pending) {
         float ms = 0.f;
         if (hipEventElapsedTime(&ms, p.a, p.b) == hipSuccess) { g_prof_recs[p.rec].ms += ms; g_prof_recs[p.rec].n++; }
@@ -77,7 +75,7 @@ static void prof_flush(void) {
 // bracket one launch with events when profiling
 struct ProfScope {
     Pending p; bool on; hipStream_t st;
-    ProfScope(const char *name, hipStream_t s) : on(g_prof != 0), st(s) {
+    ProfScope(const char *name, hipStream_t s) : on(g_prof != 0 && !g_capturing), st(s) {
         if (!on) return;
         p.rec = prof_rec(name); p.a = ev_get(); p.b = ev_get();
         if (!p.a || !p.b) { on = false; return; }
@@ -91,13 +89,13 @@ struct ProfScope {
     }
 };
 #define PROF(name) ProfScope prof_scope_(name, g_st)
-#define PROF_SIDE(name) ProfScope prof_scope_(name, g_side)
 
 // ------------------------------------------------------------ buffers ----
 // grow-only device arena and pinned staging (2x slack, as the reference)
 struct Buf { void *p = nullptr; size_t cap = 0; };
 static int grow_dev(Buf &b, size_t need) {
     if (need <= b.cap) return 0;
+    if (g_capturing) return fail_msg("device scratch too small while recording a graph (run the same shapes once first)");
     if (b.p) (void)hipFree(b.p);
     b.p = nullptr; b.cap = 0;
     CK(hipMalloc(&b.p, need * 2), "device scratch allocation");
@@ -123,6 +121,7 @@ struct Carve {
 
 static int ensure_consts(int K) {   // iota[K], ones[K], zeros[K]
     if (K <= g_consts_k) return 0;
+    if (g_capturing) return fail_msg("constants not set up while recording a graph (run the same shapes once first)");
     int k = K < 64 ? 64 : K;
     if (grow_dev(g_consts, (size_t)3 * k * sizeof(int))) return -1;
     std::vector<int> h((size_t)3 * k);
@@ -140,9 +139,6 @@ extern "C" int lag_hip_init(int dev) {
     if (g_ok && dev == g_dev) return 0;
     CK(hipSetDevice(dev), "hipSetDevice");
     if (!g_st) CK(hipStreamCreateWithFlags(&g_st, hipStreamNonBlocking), "stream creation");
-    if (!g_side) CK(hipStreamCreateWithFlags(&g_side, hipStreamNonBlocking), "stream creation");
-    if (!g_ev_fork) CK(hipEventCreateWithFlags(&g_ev_fork, hipEventDisableTiming), "event creation");
-    if (!g_ev_join) CK(hipEventCreateWithFlags(&g_ev_join, hipEventDisableTiming), "event creation");
     void *probe = nullptr;
     CK(hipMalloc(&probe, 1 << 20), "probe allocation");
     (void)hipFree(probe);
@@ -201,7 +197,6 @@ extern "C" int lag_hip_memset(void *dst, int v, size_t n) {
 }
 extern "C" int lag_hip_sync(void) {
     if (!g_ok) return -1;
-    CK(hipStreamSynchronize(g_side), "stream sync");
     CK(hipStreamSynchronize(g_st), "stream sync");
     if (g_prof) prof_flush();
     return 0;
@@ -209,11 +204,18 @@ extern "C" int lag_hip_sync(void) {
 
 // the int4 expert pipeline over device groups:
 //   h <- silu_glu(gate_up . x);  slots <- down . h
-static int run_experts(SwQ4 gu, SwQ4 dn, const float *dx, SwGroups g, int I, _Float16 *hpl, float *slots, int maxtok) {
-    { PROF("q4_gateup_glu"); if (sw_launch_q4_gateup(g_st, gu, dx, g, I, hpl, maxtok)) return fail_msg("gate_up launch (shape unsupported?)"); }
+// (limbs_ready: xl/xs already hold the limbs of dx)
+static int run_experts(SwQ4 gu, SwQ4 dn, const float *dx, int S, sw_u32x4 *xl, float *xs, int limbs_ready, SwGroups g,
+                       int I, sw_u32x4 *hl, float *hs, float *slots, int maxtok) {
+    if (!limbs_ready) {
+        PROF("x_limbs");
+        if (sw_launch_limbs(g_st, dx, S, gu.K, xl, xs)) return fail_msg("limbs launch (shape unsupported?)");
+    }
+    { PROF("q4_gateup_glu"); if (sw_launch_q4_dot8_glu(g_st, gu, xl, xs, g, I, hl, hs)) return fail_msg("gate_up launch (shape unsupported?)"); }
     SwGroups gd = g;
     gd.grow = nullptr;                     // down reads the packed rows directly
-    { PROF("q4_down"); if (sw_launch_q4_rows(g_st, dn, hpl, gd, slots, maxtok)) return fail_msg("down launch (shape unsupported?)"); }
+    { PROF("q4_down"); if (sw_launch_q4_dot8_rows(g_st, dn, hl, hs, gd, slots)) return fail_msg("down launch (shape unsupported?)"); }
+    (void)maxtok;
     return 0;
 }
 
@@ -228,8 +230,9 @@ static int grouped_host(float *outh, const float *x, int S, const void *gu_q, co
     (void)ngD; (void)ngI;
     Carve cv;
     const size_t o_x = cv.take((size_t)S * D * 4), o_idx = cv.take((size_t)(3 * G + 2 * T) * 4 + (size_t)T * 4);
-    const size_t o_hpl = cv.take((size_t)2 * T * I * 2);
+    const size_t o_hl = cv.take((size_t)T * (I / 32) * SW_NL * 16), o_hs = cv.take((size_t)T * (I / 32) * 4);
     const size_t o_slot = cv.take((size_t)T * D * 4), o_out = cv.take((size_t)S * D * 4);
+    const size_t o_xl = cv.take((size_t)S * (D / 32) * SW_NL * 16), o_xs = cv.take((size_t)S * (D / 32) * 4);
     if (grow_dev(g_arena, cv.off)) return -1;
     char *A = (char *)g_arena.p;
     // one pinned blob: x | gexp gbeg gcnt grow rowof w
@@ -254,7 +257,8 @@ static int grouped_host(float *outh, const float *x, int S, const void *gu_q, co
     SwGroups g = {d_gexp, d_gbeg, d_gcnt, d_grow, nullptr, G, 0};
     int maxcnt = 0;
     for (int i = 0; i < G; i++) maxcnt = gcnt[i] > maxcnt ? gcnt[i] : maxcnt;
-    if (run_experts(gu, dn, (const float *)(A + o_x), g, I, (_Float16 *)(A + o_hpl), (float *)(A + o_slot), maxcnt)) return -1;
+    if (run_experts(gu, dn, (const float *)(A + o_x), S, (sw_u32x4 *)(A + o_xl), (float *)(A + o_xs), 0, g, I,
+                    (sw_u32x4 *)(A + o_hl), (float *)(A + o_hs), (float *)(A + o_slot), maxcnt)) return -1;
     const float *res = (const float *)(A + o_slot);
     if (combine) {
         PROF("combine");
@@ -381,8 +385,11 @@ extern "C" int lag_hip_router_chain(const void *W, void *Wc, int E, int D, int w
 struct FwdScratch {
     float *logits, *scores, *w, *slots, *sout;
     int *sel, *gexp, *gbeg, *gcnt, *G, *grow, *rowof;
-    _Float16 *hpl;
-    uint16_t *shpl;
+    sw_u32x4 *hl;           // h of every packed row as dot8 limbs
+    float *hs;
+    float *shh;             // shared expert h [S, Is]
+    sw_u32x4 *xl;
+    float *xs;
 };
 static int g_last_G_dev = 0;            // 1: last forward's groups live in the arena
 static FwdScratch g_last;
@@ -406,27 +413,30 @@ static int carve_fwd(const LagHipMoeDesc *d, int S, FwdScratch &f) {
     const size_t o_sel = cv.take((size_t)T * 4), o_w = cv.take((size_t)T * 4);
     const size_t o_gexp = cv.take((size_t)E * 4), o_gbeg = cv.take((size_t)E * 4), o_gcnt = cv.take((size_t)E * 4);
     const size_t o_G = cv.take(4), o_grow = cv.take((size_t)T * 4), o_rowof = cv.take((size_t)T * 4);
-    const size_t o_hpl = cv.take((size_t)2 * T * I * 2);
+    const size_t o_hl = cv.take((size_t)T * (I / 32) * SW_NL * 16), o_hs = cv.take((size_t)T * (I / 32) * 4);
     const size_t o_slot = cv.take(S > 1 ? (size_t)T * D * 4 : 4);
     size_t o_sh = 0, o_so = 0;
-    if (d->shared_mode) { o_sh = cv.take((size_t)2 * S * Is * 2); o_so = cv.take((size_t)S * D * 4); }
+    if (d->shared_mode) { o_sh = cv.take((size_t)S * Is * 4); o_so = cv.take((size_t)S * D * 4); }
+    const size_t o_xl = cv.take((size_t)S * (D / 32) * SW_NL * 16), o_xs = cv.take((size_t)S * (D / 32) * 4);
     if (grow_dev(g_arena, cv.off)) return -1;
     char *A = (char *)g_arena.p;
     f.logits = (float *)(A + o_lg); f.scores = (float *)(A + o_sc); f.sel = (int *)(A + o_sel); f.w = (float *)(A + o_w);
     f.gexp = (int *)(A + o_gexp); f.gbeg = (int *)(A + o_gbeg); f.gcnt = (int *)(A + o_gcnt); f.G = (int *)(A + o_G);
     f.grow = (int *)(A + o_grow); f.rowof = (int *)(A + o_rowof);
-    f.hpl = (_Float16 *)(A + o_hpl); f.slots = (float *)(A + o_slot);
-    f.shpl = d->shared_mode ? (uint16_t *)(A + o_sh) : nullptr;
+    f.hl = (sw_u32x4 *)(A + o_hl); f.hs = (float *)(A + o_hs); f.slots = (float *)(A + o_slot);
+    f.shh = d->shared_mode ? (float *)(A + o_sh) : nullptr;
     f.sout = d->shared_mode ? (float *)(A + o_so) : nullptr;
+    f.xl = (sw_u32x4 *)(A + o_xl); f.xs = (float *)(A + o_xs);
     return 0;
 }
 
+// router logits (+ scores); with sel, gate + top-k; with xl, the dot8 limbs of x
 static int route_dev(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const float *x, int S, float *logits,
-                     float *scores, int *sel, float *wts) {
+                     float *scores, int *sel, float *wts, sw_u32x4 *xl = nullptr, float *xs = nullptr) {
     PROF("router_topk");
     if (sw_launch_router_topk(g_st, w->router, d->router_bf16, x, S, d->hidden, d->n_experts, w->logit_bias, logits,
                               scores, d->topk, d->route_act, w->corr_bias, d->use_corr_bias, d->norm_topk,
-                              sel, wts)) return fail_msg("router launch");
+                              sel, wts, xl, xs)) return fail_msg("router launch");
     return 0;
 }
 
@@ -438,44 +448,55 @@ extern "C" int lag_hip_route(const LagHipMoeDesc *d, const LagHipMoeWeights *w, 
     return route_dev(d, w, x, S, logits ? logits : f.logits, f.scores, sel, wts);
 }
 
-// The shared expert runs on the side stream, forked after everything queued
-// on the backend stream so far (x included) and joined before the combine.
-static int shared_fork(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const float *x, int S, FwdScratch &f) {
-    const int D = d->hidden, Is = d->shared_inter;
-    SwBf16 sg = {(const uint16_t *)w->sg, Is, D}, su = {(const uint16_t *)w->su, Is, D}, sd = {(const uint16_t *)w->sd, D, Is};
-    CK(hipEventRecord(g_ev_fork, g_st), "fork event");
-    CK(hipStreamWaitEvent(g_side, g_ev_fork, 0), "fork wait");
-    { PROF_SIDE("shared_gateup_glu"); if (sw_launch_bf16_gateup(g_side, sg, su, x, S, f.shpl)) return fail_msg("shared gate_up launch"); }
-    { PROF_SIDE("shared_down"); if (sw_launch_bf16_rows(g_side, sd, f.shpl, S, f.sout)) return fail_msg("shared down launch"); }
-    CK(hipEventRecord(g_ev_join, g_side), "join event");
-    return 0;
-}
-
+// One decode step (sabrewing's moe_block over S tokens, device pointers):
+//   stage 1  router logits / scores / limbs + the shared expert's gate_up
+//   (S > 1 or E > 256: gate + top-k, and for S > 1 the counting sort)
+//   stage 2  routed gate_up (S == 1: routing fused) + the shared expert's down
+//   stage 3  S == 1: routed down fused with the rank-order combine;
+//            S > 1: grouped routed down into slots, then the combine
 extern "C" int lag_hip_moe_forward(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const float *x, float *out, int S) {
     if (!g_ok || fault_injected()) return -1;
     if (!desc_ok(d, w) || S <= 0) return fail_msg("moe_forward: unsupported descriptor/shape");
-    const int E = d->n_experts, K = d->topk, D = d->hidden, I = d->moe_inter;
+    const int E = d->n_experts, K = d->topk, D = d->hidden, I = d->moe_inter, Is = d->shared_inter;
     const int T = S * K;
     FwdScratch f;
     if (carve_fwd(d, S, f) || ensure_consts(K)) return -1;
-    if (d->shared_mode && shared_fork(d, w, x, S, f)) return -1;
-    if (route_dev(d, w, x, S, f.logits, f.scores, f.sel, f.w)) return -1;
     SwQ4 gu = {(const uint8_t *)w->gu_q, w->gu_s, 2 * I, D, d->gs};
     SwQ4 dn = {(const uint8_t *)w->dn_q, w->dn_s, D, I, d->gs};
-    if (S == 1) {                        // per-token: the K picks in rank order, fused down + combine
+    const bool sh = d->shared_mode != 0;
+    const uint16_t *sg = sh ? (const uint16_t *)w->sg : nullptr, *su = sh ? (const uint16_t *)w->su : nullptr;
+    const uint16_t *sd = sh ? (const uint16_t *)w->sd : nullptr;
+    { PROF("stage_route");
+      if (sw_launch_stage_route(g_st, w->router, d->router_bf16, x, S, D, E, w->logit_bias, f.logits, f.scores, d->route_act,
+                                f.xl, f.xs, sg, su, Is, f.shh)) return fail_msg("routing stage launch"); }
+    const bool fused = S == 1 && E <= 256;
+    if (!fused) {
+        PROF("gate_topk");
+        if (sw_launch_gate_topk(g_st, f.logits, f.scores, S, E, K, d->route_act, w->corr_bias, d->use_corr_bias,
+                                d->norm_topk, f.sel, f.w)) return fail_msg("gate/top-k launch");
+    }
+    if (S == 1) {                        // one token: its K picks in rank order, fused down + combine
         SwGroups g = {f.sel, c_iota(), c_ones(), c_zeros(), nullptr, K, 0};
-        { PROF("q4_gateup_glu"); if (sw_launch_q4_gateup(g_st, gu, x, g, I, f.hpl, 1)) return fail_msg("gate_up launch"); }
-        if (d->shared_mode) CK(hipStreamWaitEvent(g_st, g_ev_join, 0), "join wait");
+        { PROF("stage_experts");
+          if (sw_launch_stage_experts(g_st, gu, f.xl, f.xs, g, I, f.hl, f.hs,
+                                      fused ? (d->route_act == 1 ? f.logits : f.scores) : nullptr, E, K, d->route_act,
+                                      w->corr_bias, d->use_corr_bias, d->norm_topk, f.sel, f.w, sd, f.shh, S, Is, D, f.sout))
+              return fail_msg("expert stage launch"); }
         { PROF("q4_down_combine");
-          if (sw_launch_q4_down_combine(g_st, dn, f.hpl, f.sel, f.w, K, d->route_scale, f.sout, out))
+          if (sw_launch_q4_dot8_down_combine(g_st, dn, f.hl, f.hs, f.sel, f.w, K, d->route_scale, f.sout, out))
               return fail_msg("down/combine launch"); }
         g_last_G_dev = 0; g_last_ng = K;
     } else {
         { PROF("bucket");
           if (sw_launch_bucket(g_st, f.sel, S, K, E, f.gexp, f.gbeg, f.gcnt, f.G, f.grow, f.rowof)) return fail_msg("bucket launch"); }
         SwGroups g = {f.gexp, f.gbeg, f.gcnt, f.grow, f.G, T < E ? T : E, 0};
-        if (run_experts(gu, dn, x, g, I, f.hpl, f.slots, S)) return -1;
-        if (d->shared_mode) CK(hipStreamWaitEvent(g_st, g_ev_join, 0), "join wait");
+        { PROF("stage_experts");
+          if (sw_launch_stage_experts(g_st, gu, f.xl, f.xs, g, I, f.hl, f.hs, nullptr, E, K, d->route_act, w->corr_bias,
+                                      d->use_corr_bias, d->norm_topk, f.sel, f.w, sd, f.shh, S, Is, D, f.sout))
+              return fail_msg("expert stage launch"); }
+        SwGroups gd = g;
+        gd.grow = nullptr;                 // the down reads the packed rows directly
+        { PROF("q4_down"); if (sw_launch_q4_dot8_rows(g_st, dn, f.hl, f.hs, gd, f.slots)) return fail_msg("down launch"); }
         { PROF("combine");
           if (sw_launch_combine(g_st, f.slots, f.rowof, f.w, S, K, D, d->route_scale, f.sout, out, 1))
               return fail_msg("combine launch"); }
@@ -584,3 +605,35 @@ extern "C" int lag_hip_selftest(float *out_host, const float *xin_host, int n) {
 }
 
 extern "C" const char *lag_hip_last_error(void) { return g_err; }
+
+// ------------------------------------------------------------ graphs ----
+// Every device-pointer entry issued between begin and end (moe_forward,
+// route, d2d) is recorded, fork/join of the shared-expert stream included,
+// into one graph replayed by lag_hip_graph_launch with one submission.
+extern "C" int lag_hip_graph_begin(void) {
+    if (!g_ok || g_capturing) return -1;
+    prof_flush();
+    CK(hipStreamBeginCapture(g_st, hipStreamCaptureModeRelaxed), "begin capture");
+    g_capturing = 1;
+    return 0;
+}
+extern "C" void *lag_hip_graph_end(void) {
+    if (!g_ok || !g_capturing) return nullptr;
+    g_capturing = 0;
+    hipGraph_t graph = nullptr;
+    hipError_t e = hipStreamEndCapture(g_st, &graph);
+    if (e != hipSuccess || !graph) { fail("end capture", e); return nullptr; }
+    hipGraphExec_t exec = nullptr;
+    e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    if (e != hipSuccess) { fail("graph instantiate", e); return nullptr; }
+    return (void *)exec;
+}
+extern "C" int lag_hip_graph_launch(void *g) {
+    if (!g_ok || !g || g_capturing) return -1;
+    CK(hipGraphLaunch((hipGraphExec_t)g, g_st), "graph launch");
+    return 0;
+}
+extern "C" void lag_hip_graph_destroy(void *g) {
+    if (g) (void)hipGraphExecDestroy((hipGraphExec_t)g);
+}

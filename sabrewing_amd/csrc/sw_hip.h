@@ -72,11 +72,16 @@ struct SwBf16 {
 
 // ---- kernels (launch wrappers, all async on `st`) ----
 // router logits [S,E] (exact 16-lane FMA-chain contract; Wc chain-major), the
-// sigmoid / softplus scores [S,E] next to them, and, with sel non-null, gate +
+// sigmoid / softplus scores [S,E] next to them, with xl non-null the dot8
+// limbs of x (xl, xs as sw_launch_limbs), and, with sel non-null, gate +
 // top-k per token (a second kernel; softmax is computed there)
 int sw_launch_router_topk(hipStream_t st, const void *Wc, int w_bf16, const float *x, int S, int D, int E,
                           const float *logit_bias, float *logits, float *scores, int K, int route_act,
-                          const float *corr_bias, int use_corr_bias, int norm_topk, int *sel, float *w);
+                          const float *corr_bias, int use_corr_bias, int norm_topk, int *sel, float *w,
+                          sw_u32x4 *xl, float *xs);
+// gate + top-k of S tokens from their logits (act 1) or scores (one wave each)
+int sw_launch_gate_topk(hipStream_t st, const float *logits, const float *scores, int S, int E, int K, int route_act,
+                        const float *corr_bias, int use_corr_bias, int norm_topk, int *sel, float *w);
 int sw_launch_bucket(hipStream_t st, const int *sel, int S, int K, int E, int *gexp, int *gbeg,
                      int *gcnt, int *G, int *grow, int *rowof);
 // out planes of SiLU-GLU(gate, up) for every packed row of every group
@@ -90,6 +95,26 @@ int sw_launch_q4_rows_x(hipStream_t st, SwQ4 W, const float *x, SwGroups g, floa
 int sw_launch_bf16_gateup(hipStream_t st, SwBf16 Wg, SwBf16 Wu, const float *x, int S, uint16_t *hplanes);
 int sw_launch_bf16_rows(hipStream_t st, SwBf16 W, const uint16_t *planes, int S, float *Y);
 int sw_launch_bf16_rows_x(hipStream_t st, SwBf16 W, const float *x, int S, float *Y);
+// activation limbs for the dot8 GEMV (k_dot8.hip): rows x[rows, K] f32 ->
+// xl[rows][K/32][SW_NL] (32 signed nibbles each), xs[rows][K/32] f32
+#define SW_NL 5
+int sw_launch_limbs(hipStream_t st, const float *x, int rows, int K, sw_u32x4 *xl, float *xs);
+// SiLU-GLU(gate, up) for every packed row of every group, on the dot8 unit;
+// output h as limbs hl[packed row][I/32][SW_NL], hs[packed row][I/32]
+int sw_launch_q4_dot8_glu(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, const float *xs, SwGroups g, int I,
+                          sw_u32x4 *hl, float *hs);
+// the same for one token with its routing fused in (every block runs the
+// gate + top-k of route_src, the token's logits (act 1) or scores); the picks
+// and weights are written to sel[K], w[K]
+int sw_launch_q4_dot8_glu_routed(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, const float *xs, int I, sw_u32x4 *hl, float *hs,
+                                 const float *route_src, int E, int K, int act, const float *bias, int use_bias, int norm,
+                                 int *sel, float *w);
+// Y[packed row, O] f32 for every group, input as limbs (the grouped down projection)
+int sw_launch_q4_dot8_rows(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, const float *xs, SwGroups g, float *Y);
+// the dot8 down projection fused with the rank-order combine for one token
+// (h as limbs of the K packed rows in rank order)
+int sw_launch_q4_dot8_down_combine(hipStream_t st, SwQ4 W, const sw_u32x4 *hl, const float *hs, const int *sel, const float *w,
+                                   int K, float route_scale, const float *shared, float *out);
 // the int4 down projection fused with the rank-order combine for one token:
 // out[d] += (sum_a w[a] * down_{sel[a]}(h_a)[d]) * route_scale (+ shared[d])
 int sw_launch_q4_down_combine(hipStream_t st, SwQ4 W, const _Float16 *hplanes, const int *sel, const float *w, int K,
@@ -97,6 +122,21 @@ int sw_launch_q4_down_combine(hipStream_t st, SwQ4 W, const _Float16 *hplanes, c
 // out[s] (+)= route_scale * sum_a w[s,a] * slots[rowof[s,a]] (+ shared[s])
 int sw_launch_combine(hipStream_t st, const float *slots, const int *rowof, const float *w, int S, int K, int D,
                       float route_scale, const float *shared, float *out, int accumulate);
+// fused decode stages (k_dot8.hip): stage 1 = router logits/scores/limbs +
+// the shared expert's gate_up (sg null: none); stage 2 = routed gate_up
+// (route_src non-null: one token, routing fused, picks to sel/w) + the
+// shared expert's down (sd null: none)
+int sw_launch_stage_route(hipStream_t st, const void *Wc, int w_bf16, const float *x, int S, int D, int E,
+                          const float *logit_bias, float *logits, float *scores, int route_act, sw_u32x4 *xl, float *xs,
+                          const uint16_t *sg, const uint16_t *su, int Is, float *sh_h);
+int sw_launch_stage_experts(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, const float *xs, SwGroups g, int I, sw_u32x4 *hl,
+                            float *hs, const float *route_src, int E, int K, int act, const float *bias, int use_bias,
+                            int norm, int *sel, float *w, const uint16_t *sd, const float *sh_h, int S, int Is, int D,
+                            float *sh_out);
+// the shared expert on the VALU (sw_shared.h): h[S, Is] = silu(Wg x) * (Wu x)
+// and out[S, D] = Wd h, bf16 weights, f32 activations
+int sw_launch_sh_glu(hipStream_t st, const uint16_t *Wg, const uint16_t *Wu, const float *x, int S, int D, int Is, float *h);
+int sw_launch_sh_down(hipStream_t st, const uint16_t *Wd, const float *h, int S, int Is, int D, float *out);
 // synthetic data
 int sw_launch_gen_normal(hipStream_t st, float *out, int64_t n, uint64_t seed, uint64_t offset, double sigma, int to_bf16);
 int sw_launch_gen_bf16(hipStream_t st, uint16_t *out, int64_t n, uint64_t seed, uint64_t offset, double sigma);

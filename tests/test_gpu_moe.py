@@ -121,3 +121,37 @@ def test_device_x_generator(be, orc):
     xd.free()
     want = orc.bf16_round(orc.normal(3 * cfg.D, S.tensor_seed(9, 1002, S.T_X), 1.0)).reshape(3, cfg.D)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("S_", [1, 5])
+def test_graph_replay_matches_eager(be, orc, S_):
+    """a recorded forward (shared-expert fork/join included) replays bit-identical
+    to the eager call, every time, with eager work and syncs between replays"""
+    cfg = SMALL[2]
+    L = synth.make_layer(orc, cfg, 51)
+    dl = DeviceLayer.from_host(be, cfg, L)
+    x = synth.make_x(orc, cfg, 52, S_)
+    zero = np.zeros_like(x)
+    xd, oe, og = be.upload(x), be.upload(zero), be.upload(zero)
+    be.moe_forward(desc_of(cfg), dl.weights(), xd, oe, S_)       # eager; also sizes the scratch
+    be.sync()
+    want = be.d2h(oe, x.shape, np.float32)
+    be.graph_begin()
+    be.moe_forward(desc_of(cfg), dl.weights(), xd, og, S_)
+    g = be.graph_end()
+    try:
+        for rep in range(3):
+            be.h2d(og, zero)
+            be.graph_launch(g)
+            be.sync()
+            got = be.d2h(og, x.shape, np.float32)
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), rep
+            be.h2d(oe, zero)                                        # eager work between replays
+            be.moe_forward(desc_of(cfg), dl.weights(), xd, oe, S_)
+            be.sync()
+            assert np.array_equal(be.d2h(oe, x.shape, np.float32).view(np.uint32), want.view(np.uint32))
+    finally:
+        be.graph_destroy(g)
+        for b in (xd, oe, og):
+            b.free()
+        dl.free()
