@@ -98,10 +98,16 @@ typedef struct {
     const void  *sg, *su, *sd;  /* bf16 shared expert [Is,D],[Is,D],[D,Is] or NULL */
 } LagHipMoeWeights;
 
-/* Upload a router [E,D] (bf16 or f32, host) into the chain-major device order
- * the routing kernel reads.  NULL = error.  Free with lag_hip_free. */
+/* Upload a router [E,D] (bf16 or f32, host) into the order the routing
+ * kernel streams, in its own element type: experts in groups of 4
+ * (E4 = 4*ceil(E/4), the padding experts zero), each group a run of 1 KB
+ * slices, slice q holding the next P elements (P = 8 bf16 or 4 f32) of each
+ * of its 64 chains c = 16*(e%4) + i%16 (chain element m = i/16):
+ * element (e, i) at ((e/4 * D/(16P) + m/P) * 64 + c) * P + m%P.
+ * NULL = error.  Free with lag_hip_free. */
 void  *lag_hip_router_upload(const void *W, int E, int D, int w_bf16);
-/* the same transform from a device router W [E,D] into device Wc (0 = ok) */
+/* the same transform from a device router W [E,D] into device Wc
+ * (E4*D elements) (0 = ok) */
 int    lag_hip_router_chain(const void *W, void *Wc, int E, int D, int w_bf16);
 /* out[S,D] += MoE(x[S,D]) for S tokens (device pointers), queued on the
  * backend stream; S == 1 runs the per-token path, S > 1 the grouped path

@@ -343,7 +343,7 @@ class DeviceLayer:
             be.gen_bf16(tmp, E * D, ts(synth.T_ROUTER), WEIGHT_SIGMA)
         else:
             be.gen_normal(tmp, E * D, ts(synth.T_ROUTER), WEIGHT_SIGMA)
-        self.router = self._keep(be.alloc(E * D * rb))
+        self.router = self._keep(be.alloc((E + 3) // 4 * 4 * D * rb))    # streaming order
         be.check(be.lib.lag_hip_router_chain(VP(int(tmp)), VP(int(self.router)), E, D, int(cfg.router_bf16)), "router chain")
         be.sync()
         tmp.free()

@@ -252,8 +252,13 @@ static int grouped_host(float *outh, const float *x, int S, const void *gu_q, co
     const int *d_gexp = (const int *)(A + o_idx), *d_gbeg = d_gexp + G, *d_gcnt = d_gexp + 2 * G;
     const int *d_grow = d_gexp + 3 * G, *d_rowof = d_grow + T;
     const float *d_w = (const float *)(d_rowof + T);
-    SwQ4 gu = {(const uint8_t *)gu_q, gu_s, 2 * I, D, gs};
-    SwQ4 dn = {(const uint8_t *)dn_q, dn_s, D, I, gs};
+    int nexp = 0;                                     // the tensors hold experts 0..max(gexp)
+    for (int i = 0; i < G; i++) {
+        if (gexp[i] < 0) return fail_msg("negative expert id");
+        nexp = gexp[i] + 1 > nexp ? gexp[i] + 1 : nexp;
+    }
+    SwQ4 gu = {(const uint8_t *)gu_q, gu_s, 2 * I, D, gs, nexp};
+    SwQ4 dn = {(const uint8_t *)dn_q, dn_s, D, I, gs, nexp};
     SwGroups g = {d_gexp, d_gbeg, d_gcnt, d_grow, nullptr, G, 0};
     int maxcnt = 0;
     for (int i = 0; i < G; i++) maxcnt = gcnt[i] > maxcnt ? gcnt[i] : maxcnt;
@@ -330,7 +335,7 @@ extern "C" int lag_hip_matmul_q4_g(float *y, const float *x, const void *packed,
     CK(hipMemcpyAsync(A + o_idx, hi, 12, hipMemcpyHostToDevice, g_st), "index upload");
     const int *d = (const int *)(A + o_idx);
     SwGroups g = {d, d + 1, d + 2, nullptr, nullptr, 1, 0};
-    SwQ4 W = {(const uint8_t *)packed, (const float *)scale, O, I, gs};
+    SwQ4 W = {(const uint8_t *)packed, (const float *)scale, O, I, gs, 1};
     { PROF("q4_rows"); if (sw_launch_q4_rows_x(g_st, W, (const float *)(A + o_x), g, (float *)(A + o_y), S)) return fail_msg("q4 launch (shape unsupported?)"); }
     CK(hipMemcpyAsync(g_hout.p, A + o_y, (size_t)S * O * 4, hipMemcpyDeviceToHost, g_st), "result download");
     CK(hipStreamSynchronize(g_st), "stream sync");
@@ -368,7 +373,7 @@ extern "C" void *lag_hip_router_upload(const void *W, int E, int D, int w_bf16) 
     void *tmp = lag_hip_upload(W, n);
     if (!tmp) return nullptr;
     void *out = nullptr;
-    if (hipMalloc(&out, n) != hipSuccess) { (void)hipFree(tmp); fail("router allocation", hipErrorOutOfMemory); return nullptr; }
+    if (hipMalloc(&out, (size_t)((E + 3) / 4) * 4 * D * (w_bf16 ? 2 : 4)) != hipSuccess) { (void)hipFree(tmp); fail("router allocation", hipErrorOutOfMemory); return nullptr; }
     if (sw_launch_chain_major(g_st, tmp, w_bf16, E, D, out) || hipStreamSynchronize(g_st) != hipSuccess) {
         (void)hipFree(tmp); (void)hipFree(out); fail("router transform", hipErrorUnknown); return nullptr;
     }
@@ -461,8 +466,8 @@ extern "C" int lag_hip_moe_forward(const LagHipMoeDesc *d, const LagHipMoeWeight
     const int T = S * K;
     FwdScratch f;
     if (carve_fwd(d, S, f) || ensure_consts(K)) return -1;
-    SwQ4 gu = {(const uint8_t *)w->gu_q, w->gu_s, 2 * I, D, d->gs};
-    SwQ4 dn = {(const uint8_t *)w->dn_q, w->dn_s, D, I, d->gs};
+    SwQ4 gu = {(const uint8_t *)w->gu_q, w->gu_s, 2 * I, D, d->gs, E};
+    SwQ4 dn = {(const uint8_t *)w->dn_q, w->dn_s, D, I, d->gs, E};
     const bool sh = d->shared_mode != 0;
     const uint16_t *sg = sh ? (const uint16_t *)w->sg : nullptr, *su = sh ? (const uint16_t *)w->su : nullptr;
     const uint16_t *sd = sh ? (const uint16_t *)w->sd : nullptr;

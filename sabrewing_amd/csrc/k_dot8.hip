@@ -14,10 +14,10 @@
 // (Horner over the limbs: acc = (acc << 3) + four dot8), turned into f32 once
 // (|acc| < 2^24, exact) and multiplied by s_row,group * 2^(e - 3 NL) (exact
 // power-of-two scaling of the weight scale).  A row's output is then the sum
-// of its group terms in a fixed order: runs of CH consecutive groups summed
-// left to right, the run sums summed left to right.  Nothing of it depends on
-// which tokens share a launch, so grouped and per-token results are
-// bit-identical.
+// of its group terms in the fixed order of run_sum (sw_gate.h): runs of up to
+// 16 groups, each summed by a butterfly across the lanes holding them, the
+// run sums left to right.  Nothing of it depends on which tokens share a
+// launch, so grouped and per-token results are bit-identical.
 //
 // Per weight byte this is ~2 VALU ops (XOR, dot8, shift over NL = 5 limbs,
 // one fma per 32 weights) against ~3.3 for nibble-to-f16 dequant plus MFMA,
@@ -30,6 +30,40 @@
 
 #define RG SW_RG              // inputs per limb group
 #define CHG 16                // groups per run of the fixed row-sum order
+
+// Per-block timeline of the decode kernels, for a build with -DSW_TRACE only:
+// block b of kernel slot k writes its start and end (s_memrealtime, 100 MHz)
+// and hardware id to sw_trace[3 * (k * SW_TRACE_SLOT + b)].
+#ifdef SW_TRACE
+#define SW_TRACE_SLOT 16384
+static __device__ unsigned long long sw_trace[5 * SW_TRACE_SLOT * 3];
+#define TR_BEGIN() const unsigned long long tr_t0 = wall_clock64()
+#define TR_END(k)                                                                                  \
+    do {                                                                                           \
+        __syncthreads();                                                                           \
+        if (threadIdx.x == 0 && blockIdx.x + gridDim.x * blockIdx.y < SW_TRACE_SLOT) {             \
+            unsigned long long *tp = sw_trace + 3 * ((k) * SW_TRACE_SLOT + blockIdx.x + gridDim.x * blockIdx.y); \
+            tp[0] = tr_t0; tp[1] = wall_clock64();                                                 \
+            tp[2] = (unsigned long long)__smid() | ((unsigned long long)__builtin_amdgcn_s_getreg((20 << 0) | (0 << 6) | (3 << 11)) << 32); \
+        }                                                                                          \
+    } while (0)
+static __device__ unsigned long long sw_trace_mid[SW_TRACE_SLOT * 4];
+#define TR_MARK(i) do { if (threadIdx.x == 0 && blockIdx.x < SW_TRACE_SLOT) sw_trace_mid[blockIdx.x * 4 + (i)] = wall_clock64(); } while (0)
+extern "C" int sw_trace_read(void *dst, size_t n) {
+    return hipMemcpyFromSymbol(dst, HIP_SYMBOL(sw_trace), n) == hipSuccess ? 0 : -1;
+}
+extern "C" int sw_trace_read_mid(void *dst, size_t n) {
+    return hipMemcpyFromSymbol(dst, HIP_SYMBOL(sw_trace_mid), n) == hipSuccess ? 0 : -1;
+}
+extern "C" int sw_trace_clear() {
+    static unsigned long long z[5 * SW_TRACE_SLOT * 3];
+    return hipMemcpyToSymbol(HIP_SYMBOL(sw_trace), z, sizeof(z)) == hipSuccess ? 0 : -1;
+}
+#else
+#define TR_BEGIN()
+#define TR_END(k)
+#define TR_MARK(i)
+#endif
 
 // ------------------------------------------------------------ limbs ----
 // rows x[r, K] f32 -> limbs (limbs_group in sw_gate.h), half a wave per group
@@ -48,31 +82,67 @@ int sw_launch_limbs(hipStream_t st, const float *x, int rows, int K, sw_u32x4 *x
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
-// exact int32 sum_k (n_k - 8) D_k over one group (16 bytes of nibbles)
-__device__ __forceinline__ int dot8_group(sw_u32x4 w, const sw_u32x4 *X) {
-    const sw_u32x4 a = w ^ 0x88888888u;
-    int acc = 0;
+// exact int32 sum_k (n_k - 8) D_k over one group: a = the group's 16 weight
+// bytes with every nibble XOR 8 (signed nibbles n - 8); the NL limb dots are
+// independent chains, joined by Horner (every partial sum is exact)
+__device__ __forceinline__ int dot8_group(sw_u32x4 a, const sw_u32x4 *X) {
+    int p[SW_NL];
 #pragma unroll
     for (int l = 0; l < SW_NL; l++) {
-        acc <<= 3;
-        acc = __builtin_amdgcn_sdot8((int)a.x, (int)X[l].x, acc, false);
-        acc = __builtin_amdgcn_sdot8((int)a.y, (int)X[l].y, acc, false);
-        acc = __builtin_amdgcn_sdot8((int)a.z, (int)X[l].z, acc, false);
-        acc = __builtin_amdgcn_sdot8((int)a.w, (int)X[l].w, acc, false);
+        int t = __builtin_amdgcn_sdot8((int)a.x, (int)X[l].x, 0, false);
+        t = __builtin_amdgcn_sdot8((int)a.y, (int)X[l].y, t, false);
+        t = __builtin_amdgcn_sdot8((int)a.z, (int)X[l].z, t, false);
+        p[l] = __builtin_amdgcn_sdot8((int)a.w, (int)X[l].w, t, false);
     }
+    int acc = p[0];
+#pragma unroll
+    for (int l = 1; l < SW_NL; l++) acc = (acc << 3) + p[l];
     return acc;
+}
+
+// A row's terms: one per group of 32 inputs, the lanes of a row padded to
+// Gq = run_lanes(G).  C16 = 1 when G is a multiple of 16 (runs of 16 lanes,
+// no padding), else runs of Gq lanes and padding lanes adding zero terms.
+template <int C16>
+__device__ __forceinline__ float row_term(float p, bool gv, int CH) {
+    if constexpr (C16) return run_sum16(p);
+    return run_sum(gv ? p : 0.f, CH);
+}
+
+// The weight tensors are read through buffer descriptors over all E experts
+// (extent E * O * K/2 bytes, and E * O * ng * 4 for the scales).
+static bool q4_extent_ok(const SwQ4 &W) {
+    const int ng = W.gs > 0 ? W.K / W.gs : 1;
+    return W.E > 0 && (uint64_t)W.E * W.O * (W.K / 2) < (1ull << 32) && (uint64_t)W.E * W.O * ng * 4 < (1ull << 32);
+}
+__device__ __forceinline__ sw_rsrc q4_rq(const SwQ4 &W) { return sw_make_rsrc(W.q, (uint32_t)W.E * W.O * (W.K / 2)); }
+__device__ __forceinline__ sw_rsrc q4_rs(const SwQ4 &W) {
+    const int ng = W.gs > 0 ? W.K / W.gs : 1;
+    return sw_make_rsrc(W.s, (uint32_t)W.E * W.O * ng * 4);
+}
+
+// row slots of a block of nt threads: the largest power of two with rps * Gq <= nt, at most cap
+__host__ __device__ inline int dg_rps(int Gq, int cap, int nt) {
+    int r = 1;
+    while (r * 2 * Gq <= nt && r < cap) r *= 2;
+    return r;
 }
 
 // ------------------------------------------------------------ gate_up ----
 // One block = 32 consecutive intermediate outputs i of one group: gate rows
-// i0..i0+31 and up rows i0..i0+31 (64 weight rows), every input group, for
-// each token of the group in turn (later tokens re-read the block's 160 KB
-// from L2).  Thread (row offset ro, input group g) with TPR = G threads per
-// row and RPS = 256 / G rows per step keeps its group's limbs in registers
-// and streams one 16-byte weight load per step (PF steps in flight); the
-// group terms go to LDS and the fixed-order row sums, the SiLU-GLU and the
-// f16 hi/lo plane output (the down projection's input) follow.
+// i0..i0+31 and up rows i0..i0+31 (64 weight rows), every input group, for a
+// tile of up to TT tokens of the group per pass over the block's weights (a
+// group with more tokens takes further passes, which re-read the block's
+// weights from L2).  Thread (row slot ro, input group g): Gq threads per row,
+// RPS row slots; slot ro takes NSH = 32/RPS consecutive gate rows and the
+// same up rows, one row per step (steps 0..NSH-1 gate, NSH..2NSH-1 up), so
+// its addresses are a fixed lane offset plus a per-step scalar one.  The
+// tile's limbs of its group stay in registers; PF steps of weight loads are
+// in flight; a row's run sums go to LDS and the row sums, the SiLU-GLU and
+// the limbs of h (the down projection's input) follow.
 #define DG_ROWS 64
+#define DG_TT 2               // tokens per weight pass in the grouped kernels
+#define DG_NT 512             // threads per gate_up block
 // Fused routing for one token (NP > 0): every block runs the token's gate +
 // top-k on its first wave (gate_topk_wave, deterministic, so every block gets
 // the same picks) while the others fetch the limbs; block (0, 0) also writes
@@ -96,86 +166,109 @@ struct Dot8GluArgs {
     float *hs;
     DotRoute rt;
 };
-// block (bx = group or rank, by = set of 32 outputs); red: the dynamic LDS
-// ([DG_ROWS][G + 1], then [DG_ROWS][G / CH] floats)
-template <int PF, int NP>
-__device__ __forceinline__ void dot8_glu_block(const Dot8GluArgs &A, int bx, int by, float *red) {
+
+// K inputs as G = K/32 groups, G <= 256
+static bool dot8_shape_ok(int K) { return K > 0 && K % RG == 0 && K / RG <= 256; }
+static int dot8_gsh(const SwQ4 &W, int &gsh) {
+    gsh = 0;
+    if (W.gs > 0) {
+        if (W.gs % RG || W.K % W.gs || (W.gs & (W.gs - 1))) return -1;
+        while ((1 << gsh) < W.gs) gsh++;
+    }
+    return 0;
+}
+static int dot8_nc(int K) { const int G = K / RG; return G < CHG ? 1 : run_lanes(G) / CHG; }
+static int dot8_c16(int K) { return (K / RG) % CHG == 0; }
+// steps of weight loads in flight: min(8, steps per half) (a power of two dividing it)
+static int dg_pf_glu(int K) { const int n = 32 / dg_rps(run_lanes(K / RG), 32, DG_NT); return n < 8 ? n : 8; }
+static int dg_pf_rows(int K) { const int n = 64 / dg_rps(run_lanes(K / RG), 64, 256); return n < 8 ? n : 8; }
+
+// block (bx = group or rank, by = set of 32 outputs); runs: the dynamic LDS,
+// [TT][DG_ROWS][NC] floats
+template <int PF, int NP, int TT, int C16>
+__device__ __forceinline__ void dot8_glu_block(const Dot8GluArgs &A, int bx, int by, float *runs) {
+    static_assert(NP == 0 || TT == 1, "fused routing is one token");
     const SwQ4 W = A.W;
-    const int gsh = A.gsh, I = A.I;
+    const int I = A.I;
     const sw_u32x4 *__restrict__ xl = A.xl;
     const float *__restrict__ xs = A.xs;
     const SwGroups grp = A.grp;
-    sw_u32x4 *__restrict__ hl = A.hl;
-    float *__restrict__ hs = A.hs;
     const DotRoute rt = A.rt;
-    const int K = W.K, G = K / RG, Gp = G + 1;
-    const int tid = threadIdx.x;
-    const int RPS = 256 / G, NS = (DG_ROWS + RPS - 1) / RPS;
-    const int ro = tid / G, g = tid - ro * G;
-    const bool worker = ro < RPS;
-    const int gi = bx;
+    const int K = W.K, G = K / RG, Gq = C16 ? G : run_lanes(G);
+    const int CH = C16 ? CHG : (Gq < CHG ? Gq : CHG), NC = Gq / CH;
+    const int RPS = dg_rps(Gq, 32, DG_NT), NSH = 32 / RPS;    // a row slot: NSH gate rows and NSH up rows
+    const int tid = threadIdx.x, ro = tid / Gq, gq = tid - ro * Gq, c = gq / CH;
+    const bool worker = ro < RPS, lead = worker && (gq & (CH - 1)) == 0, gv = C16 || gq < G;
+    const int g = gv ? gq : G - 1;                   // padding lanes load group G-1 and add 0
+    const int roc = worker ? ro : 0;
     const int i0 = by * (DG_ROWS / 2);
     const int ng = W.gs > 0 ? K / W.gs : 1;
-    const int gshift = W.gs > 0 ? gsh : 31;
-    const int sg = (g * RG) >> gshift;               // this thread's weight-scale column
+    const int sg = W.gs > 0 ? (g * RG) >> A.gsh : 0;
+    const uint32_t rb = (uint32_t)K / 2, sb = (uint32_t)ng * 4;
     int e, beg, cnt;
-    int64_t tok0;
-    sw_u32x4 X[SW_NL];
+    sw_u32x4 X[TT][SW_NL];
+    float xf[TT];
     if constexpr (NP > 0) {                           // one token: rank gi of its picks
         __shared__ TopkLDS tk;
-        beg = gi; cnt = 1; tok0 = 0;
+        beg = bx; cnt = 1;
 #pragma unroll
-        for (int l = 0; l < SW_NL; l++) X[l] = xl[(int64_t)g * SW_NL + l];
+        for (int l = 0; l < SW_NL; l++) X[0][l] = xl[(int64_t)g * SW_NL + l];
+        xf[0] = xs[g];
         if (tid < 64) gate_topk_wave<NP>(rt.src, rt.E, rt.K, rt.act, rt.bias, rt.use_bias, rt.norm, tk);
         __syncthreads();
-        e = tk.sk[gi];
+        e = __builtin_amdgcn_readfirstlane(tk.sk[bx]);
+        TR_MARK(0);
         if (bx == 0 && by == 0 && tid < rt.K) { rt.sel_out[tid] = tk.sk[tid]; rt.w_out[tid] = tk.wk[tid]; }
     } else {
         const int gvalid = grp.G ? *grp.G : grp.ngroups_max;
-        if (gi >= gvalid) return;
-        e = grp.gexp ? grp.gexp[gi] : 0;
-        beg = grp.gbeg ? grp.gbeg[gi] : 0;
-        cnt = grp.gcnt ? grp.gcnt[gi] : grp.cnt_const;
-        tok0 = grp.grow ? grp.grow[beg] : beg;
-        if (cnt > 0) {
-#pragma unroll
-            for (int l = 0; l < SW_NL; l++) X[l] = xl[(tok0 * G + g) * SW_NL + l];
-        }
+        if (bx >= gvalid) return;
+        e = grp.gexp ? grp.gexp[bx] : 0;
+        beg = grp.gbeg ? grp.gbeg[bx] : 0;
+        cnt = grp.gcnt ? grp.gcnt[bx] : grp.cnt_const;
     }
-    // weight row of step s: local row lr = s*RPS + ro (clamped); gate rows first, then up rows
-    auto wrow = [&](int s) -> int64_t {
-        int lr = s * RPS + (worker ? ro : 0);
-        lr = lr < DG_ROWS ? lr : DG_ROWS - 1;
-        const int i = i0 + (lr & 31);
-        return (int64_t)e * (2 * I) + (lr < 32 ? i : I + i);
-    };
-    const float *sbase = W.s + (W.gs > 0 ? sg : 0);   // per-row scales: read (and ignored) in the loop
-    for (int t = 0; t < cnt; t++) {
-        const int64_t tok = t == 0 ? tok0 : (grp.grow ? grp.grow[beg + t] : beg + t);
-        if (t > 0) {
+    const sw_rsrc rq = q4_rq(W), rs = q4_rs(W);
+    // lane offsets (this thread's first row of a half) and the scalar offset of step s
+    const uint32_t voq = (uint32_t)(roc * NSH) * rb + (uint32_t)g * 16;
+    const uint32_t vos = (uint32_t)(roc * NSH) * sb + (uint32_t)sg * 4;
+    const uint32_t erow = (uint32_t)e * (uint32_t)(2 * I) + (uint32_t)i0;
+    auto srow = [&](int s) -> uint32_t { return s < NSH ? erow + s : erow + I + (s - NSH); };
+    const int NS = 2 * NSH;
+    float *myruns = runs + (roc * NSH) * NC + c;      // this lane's run sum of step s: myruns[(t*64 + h*32 + j) * NC]
+    for (int t0 = 0; t0 < cnt; t0 += TT) {
+        const int nt = min(TT, cnt - t0);
+        if constexpr (NP == 0) {
 #pragma unroll
-            for (int l = 0; l < SW_NL; l++) X[l] = xl[(tok * G + g) * SW_NL + l];
+            for (int t = 0; t < TT; t++) {
+                const int pr = beg + t0 + (t < nt ? t : 0);
+                const int64_t tok = grp.grow ? grp.grow[pr] : pr;
+#pragma unroll
+                for (int l = 0; l < SW_NL; l++) X[t][l] = xl[(tok * G + g) * SW_NL + l];
+                xf[t] = xs[tok * G + g];
+            }
         }
-        const float xf = xs[tok * G + g];
         sw_u32x4 ra[PF];
         float sa[PF];
 #pragma unroll
         for (int u = 0; u < PF; u++) {
-            const int64_t wr = wrow(u);
-            ra[u] = *(const sw_u32x4 *)(W.q + wr * (K / 2) + g * 16);
-            sa[u] = sbase[wr * ng];
+            ra[u] = sw_ld16(rq, voq, srow(u) * rb);
+            sa[u] = sw_ld4f(rs, vos, srow(u) * sb);
         }
         auto step = [&](int s, int u, bool refill) {
-            const int acc = dot8_group(ra[u], X);
-            const float sx = (W.gs > 0 ? sa[u] : 1.0f) * xf;
+            const sw_u32x4 w = ra[u] ^ 0x88888888u;
+            const float sc = W.gs > 0 ? sa[u] : 1.0f;
             if (refill) {
-                const int64_t wr = wrow(s + PF);
-                ra[u] = *(const sw_u32x4 *)(W.q + wr * (K / 2) + g * 16);
-                sa[u] = sbase[wr * ng];
+                ra[u] = sw_ld16(rq, voq, srow(s + PF) * rb);
+                sa[u] = sw_ld4f(rs, vos, srow(s + PF) * sb);
                 __builtin_amdgcn_sched_barrier(0);
             }
-            const int lr = s * RPS + ro;
-            if (worker && lr < DG_ROWS) red[lr * Gp + g] = (float)acc * sx;
+            const int urow = s < NSH ? s : 32 + s - NSH;                 // local row minus roc * NSH
+#pragma unroll
+            for (int t = 0; t < TT; t++) {
+                if (t < nt) {                          // uniform over the block
+                    const float p = row_term<C16>((float)dot8_group(w, X[t]) * (sc * xf[t]), gv, CH);
+                    if (lead) myruns[(t * DG_ROWS + urow) * NC] = p;
+                }
+            }
         };
         int s0 = 0;
         for (; s0 + PF < NS; s0 += PF) {
@@ -183,77 +276,74 @@ __device__ __forceinline__ void dot8_glu_block(const Dot8GluArgs &A, int bx, int
             for (int u = 0; u < PF; u++) step(s0 + u, u, true);
         }
 #pragma unroll
-        for (int u = 0; u < PF; u++)
-            if (s0 + u < NS) step(s0 + u, u, false);
+        for (int u = 0; u < PF; u++) step(s0 + u, u, false);
+        TR_MARK(1);
         __syncthreads();
-        // fixed-order row sums: runs of CH groups left to right, runs left to right
-        const int CH = G < CHG ? G : CHG, NC = G / CH;
-        float *runs = red + DG_ROWS * Gp;
-        for (int it = tid; it < DG_ROWS * NC; it += 256) {
-            const int r = it / NC, c = it - r * NC;
-            const float *p = red + r * Gp + c * CH;
-            float sum = p[0];
-            for (int j = 1; j < CH; j++) sum = sum + p[j];
-            runs[r * NC + c] = sum;
-        }
-        __syncthreads();
-        if (tid < 32) {
-            float yg = runs[tid * NC], yu = runs[(32 + tid) * NC];
-            for (int c = 1; c < NC; c++) { yg = yg + runs[tid * NC + c]; yu = yu + runs[(32 + tid) * NC + c]; }
+        TR_MARK(2);
+        // token t of the tile by the half-wave of threads 32t..32t+31
+        const int t = tid >> 5, i = tid & 31;
+        if (t < nt) {
+            const float *rg = runs + (t * DG_ROWS + i) * NC, *ru = runs + (t * DG_ROWS + 32 + i) * NC;
+            float yg = rg[0], yu = ru[0];
+            for (int cc = 1; cc < NC; cc++) { yg = yg + rg[cc]; yu = yu + ru[cc]; }
             if (W.gs <= 0) {                            // per-row scales after the sum
-                yg = yg * W.s[(int64_t)e * (2 * I) + i0 + tid];
-                yu = yu * W.s[(int64_t)e * (2 * I) + I + i0 + tid];
+                yg = yg * W.s[(int64_t)e * (2 * I) + i0 + i];
+                yu = yu * W.s[(int64_t)e * (2 * I) + I + i0 + i];
             }
             const float h = (yg / (1.0f + expf(-yg))) * yu;
             // the block's 32 outputs are one limb group of the down projection's input
             const int GI = I / RG, gi_out = i0 / RG;
-            const int64_t prow = beg + t;
-            limbs_group(h, tid, hl + (prow * GI + gi_out) * SW_NL, hs + prow * GI + gi_out);
+            const int64_t prow = beg + t0 + t;
+            limbs_group(h, i, A.hl + (prow * GI + gi_out) * SW_NL, A.hs + prow * GI + gi_out);
         }
         __syncthreads();
     }
 }
 
-template <int PF, int NP>
-__global__ __launch_bounds__(256) void k_dot8_glu(Dot8GluArgs A) {
+template <int PF, int NP, int TT, int C16>
+__global__ __launch_bounds__(DG_NT) void k_dot8_glu(Dot8GluArgs A) {
     extern __shared__ __align__(16) float red[];
-    dot8_glu_block<PF, NP>(A, blockIdx.x, blockIdx.y, red);
+    dot8_glu_block<PF, NP, TT, C16>(A, blockIdx.x, blockIdx.y, red);
 }
 
-template <int NP>
-static void launch_dot8_glu(int ns, dim3 grid, size_t lds, hipStream_t st, SwQ4 W, int gsh, const sw_u32x4 *xl, const float *xs,
-                            SwGroups g, int I, sw_u32x4 *hl, float *hs, DotRoute rt) {
-    const Dot8GluArgs A = {W, gsh, xl, xs, g, I, hl, hs, rt};
-    if (ns >= 8) hipLaunchKernelGGL((k_dot8_glu<8, NP>), grid, dim3(256), lds, st, A);
-    else if (ns >= 4) hipLaunchKernelGGL((k_dot8_glu<4, NP>), grid, dim3(256), lds, st, A);
-    else hipLaunchKernelGGL((k_dot8_glu<2, NP>), grid, dim3(256), lds, st, A);
+// dispatch on the prefetch depth pf (1, 2, 4 or 8) and C16
+template <template <int, int> class L, class... Args>
+static void dispatch_pf_c16(int pf, int c16, Args &&...args) {
+    if (c16) {
+        if (pf >= 8) L<8, 1>::go(args...);
+        else if (pf >= 4) L<4, 1>::go(args...);
+        else if (pf >= 2) L<2, 1>::go(args...);
+        else L<1, 1>::go(args...);
+    } else {
+        if (pf >= 8) L<8, 0>::go(args...);
+        else if (pf >= 4) L<4, 0>::go(args...);
+        else if (pf >= 2) L<2, 0>::go(args...);
+        else L<1, 0>::go(args...);
+    }
 }
+template <int NP, int TT>
+struct GluL {
+    template <int PF, int C16>
+    struct L {
+        static void go(dim3 grid, size_t lds, hipStream_t st, const Dot8GluArgs &A) {
+            hipLaunchKernelGGL((k_dot8_glu<PF, NP, TT, C16>), grid, dim3(DG_NT), lds, st, A);
+        }
+    };
+};
 
 static int dot8_glu_check(SwQ4 W, int I, int &gsh) {
-    const int K = W.K, G = K / RG;
-    if (K % RG || I % 32 || W.O != 2 * I || G > 192) return -1;   // LDS: 64 rows x G terms
-    const int CH = G < CHG ? G : CHG;
-    if (G % CH) return -1;
-    gsh = 0;
-    if (W.gs > 0) {
-        if (W.gs % RG || K % W.gs || (W.gs & (W.gs - 1))) return -1;
-        while ((1 << gsh) < W.gs) gsh++;
-    }
-    return 0;
+    if (!dot8_shape_ok(W.K) || I % 32 || W.O != 2 * I || !q4_extent_ok(W)) return -1;
+    return dot8_gsh(W, gsh);
 }
-static size_t dot8_glu_lds(int K) {
-    const int G = K / RG, CH = G < CHG ? G : CHG;
-    return ((size_t)DG_ROWS * (G + 1) + (size_t)DG_ROWS * (G / CH)) * 4;
-}
+static size_t dot8_glu_lds(int K, int TT) { return (size_t)TT * DG_ROWS * dot8_nc(K) * 4; }
 
 int sw_launch_q4_dot8_glu(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, const float *xs, SwGroups g, int I,
                           sw_u32x4 *hl, float *hs) {
     int gsh;
     if (dot8_glu_check(W, I, gsh) || g.ngroups_max <= 0) return -1;
-    const int G = W.K / RG, RPS = 256 / G, NS = (DG_ROWS + RPS - 1) / RPS;
-    const DotRoute rt = {};
-    launch_dot8_glu<0>(NS, dim3((unsigned)g.ngroups_max, (unsigned)(I / 32)), dot8_glu_lds(W.K), st, W, gsh, xl, xs, g, I,
-                       hl, hs, rt);
+    const Dot8GluArgs A = {W, gsh, xl, xs, g, I, hl, hs, DotRoute{}};
+    dispatch_pf_c16<GluL<0, DG_TT>::L>(dg_pf_glu(W.K), dot8_c16(W.K), dim3((unsigned)g.ngroups_max, (unsigned)(I / 32)),
+                                       dot8_glu_lds(W.K, DG_TT), st, A);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
@@ -262,22 +352,22 @@ int sw_launch_q4_dot8_glu_routed(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, con
                                  int *sel, float *w) {
     int gsh;
     if (dot8_glu_check(W, I, gsh) || E <= 0 || E > 256 || K <= 0 || K > 64 || K > E) return -1;
-    const int G = W.K / RG, RPS = 256 / G, NS = (DG_ROWS + RPS - 1) / RPS;
-    const SwGroups g = {};
-    const DotRoute rt = {route_src, bias, E, K, act, use_bias, norm, sel, w};
+    const Dot8GluArgs A = {W, gsh, xl, xs, SwGroups{}, I, hl, hs, DotRoute{route_src, bias, E, K, act, use_bias, norm, sel, w}};
     const dim3 grid((unsigned)K, (unsigned)(I / 32));
-    const size_t lds = dot8_glu_lds(W.K);
-    if (E <= 64) launch_dot8_glu<1>(NS, grid, lds, st, W, gsh, xl, xs, g, I, hl, hs, rt);
-    else if (E <= 128) launch_dot8_glu<2>(NS, grid, lds, st, W, gsh, xl, xs, g, I, hl, hs, rt);
-    else launch_dot8_glu<4>(NS, grid, lds, st, W, gsh, xl, xs, g, I, hl, hs, rt);
+    const size_t lds = dot8_glu_lds(W.K, 1);
+    const int pf = dg_pf_glu(W.K), c16 = dot8_c16(W.K);
+    if (E <= 64) dispatch_pf_c16<GluL<1, 1>::L>(pf, c16, grid, lds, st, A);
+    else if (E <= 128) dispatch_pf_c16<GluL<2, 1>::L>(pf, c16, grid, lds, st, A);
+    else dispatch_pf_c16<GluL<4, 1>::L>(pf, c16, grid, lds, st, A);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
 // ------------------------------------------------------------ rows ----
 // Y[packed row, O] = W_e . x for every packed row of every group (the down
 // projection of the grouped path): block = 64 consecutive output rows of one
-// group, thread (row offset, input group) as in the gate_up, same fixed-order
-// row sums, f32 rows out.
+// group, a tile of up to DG_TT tokens per weight pass; thread (row slot ro,
+// input group g) takes NS = 64/RPS consecutive rows, one per step; same
+// fixed-order row sums, f32 rows out.
 struct Dot8RowsArgs {
     SwQ4 W;
     int gsh;
@@ -286,59 +376,69 @@ struct Dot8RowsArgs {
     SwGroups grp;
     float *Y;
 };
-template <int PF>
-__device__ __forceinline__ void dot8_rows_block(const Dot8RowsArgs &A, int bx, int by, float *red) {
+template <int PF, int TT, int C16>
+__device__ __forceinline__ void dot8_rows_block(const Dot8RowsArgs &A, int bx, int by, float *runs) {
     const SwQ4 W = A.W;
-    const int gsh = A.gsh;
     const sw_u32x4 *__restrict__ xl = A.xl;
     const float *__restrict__ xs = A.xs;
     const SwGroups grp = A.grp;
     float *__restrict__ Y = A.Y;
-    const int K = W.K, G = K / RG, Gp = G + 1, O = W.O;
-    const int tid = threadIdx.x;
-    const int RPS = 256 / G, NS = (DG_ROWS + RPS - 1) / RPS;
-    const int ro = tid / G, g = tid - ro * G;
-    const bool worker = ro < RPS;
-    const int gi = bx;
+    const int K = W.K, G = K / RG, O = W.O, Gq = C16 ? G : run_lanes(G);
+    const int CH = C16 ? CHG : (Gq < CHG ? Gq : CHG), NC = Gq / CH;
+    const int RPS = dg_rps(Gq, 64, 256), NS = DG_ROWS / RPS;
+    const int tid = threadIdx.x, ro = tid / Gq, gq = tid - ro * Gq, c = gq / CH;
+    const bool worker = ro < RPS, lead = worker && (gq & (CH - 1)) == 0, gv = C16 || gq < G;
+    const int g = gv ? gq : G - 1;
+    const int roc = worker ? ro : 0;
     const int gvalid = grp.G ? *grp.G : grp.ngroups_max;
-    if (gi >= gvalid) return;
-    const int e = grp.gexp ? grp.gexp[gi] : 0, beg = grp.gbeg ? grp.gbeg[gi] : 0;
-    const int cnt = grp.gcnt ? grp.gcnt[gi] : grp.cnt_const;
+    if (bx >= gvalid) return;
+    const int e = grp.gexp ? grp.gexp[bx] : 0, beg = grp.gbeg ? grp.gbeg[bx] : 0;
+    const int cnt = grp.gcnt ? grp.gcnt[bx] : grp.cnt_const;
     const int r0 = by * DG_ROWS;
     const int nrows = min(DG_ROWS, O - r0);
     const int ng = W.gs > 0 ? K / W.gs : 1;
-    const int sg = W.gs > 0 ? (g * RG) >> gsh : 0;
-    auto wrow = [&](int s) -> int64_t {
-        int lr = s * RPS + (worker ? ro : 0);
-        lr = lr < nrows ? lr : nrows - 1;
-        return (int64_t)e * O + r0 + lr;
-    };
-    const float *sbase = W.s + sg;
-    for (int t = 0; t < cnt; t++) {
-        const int64_t tok = grp.grow ? grp.grow[beg + t] : beg + t;
-        sw_u32x4 X[SW_NL];
+    const int sg = W.gs > 0 ? (g * RG) >> A.gsh : 0;
+    const uint32_t rb = (uint32_t)K / 2, sb = (uint32_t)ng * 4;
+    const sw_rsrc rq = q4_rq(W), rs = q4_rs(W);
+    // rows past O read the next expert's rows (or zeros past the tensor) and are not stored
+    const uint32_t voq = (uint32_t)(roc * NS) * rb + (uint32_t)g * 16;
+    const uint32_t vos = (uint32_t)(roc * NS) * sb + (uint32_t)sg * 4;
+    const uint32_t erow = (uint32_t)e * (uint32_t)O + (uint32_t)r0;
+    float *myruns = runs + (roc * NS) * NC + c;
+    for (int t0 = 0; t0 < cnt; t0 += TT) {
+        const int nt = min(TT, cnt - t0);
+        sw_u32x4 X[TT][SW_NL];
+        float xf[TT];
 #pragma unroll
-        for (int l = 0; l < SW_NL; l++) X[l] = xl[(tok * G + g) * SW_NL + l];
-        const float xf = xs[tok * G + g];
+        for (int t = 0; t < TT; t++) {
+            const int pr = beg + t0 + (t < nt ? t : 0);
+            const int64_t tok = grp.grow ? grp.grow[pr] : pr;
+#pragma unroll
+            for (int l = 0; l < SW_NL; l++) X[t][l] = xl[(tok * G + g) * SW_NL + l];
+            xf[t] = xs[tok * G + g];
+        }
         sw_u32x4 ra[PF];
         float sa[PF];
 #pragma unroll
         for (int u = 0; u < PF; u++) {
-            const int64_t wr = wrow(u);
-            ra[u] = *(const sw_u32x4 *)(W.q + wr * (K / 2) + g * 16);
-            sa[u] = sbase[wr * ng];
+            ra[u] = sw_ld16(rq, voq, (erow + u) * rb);
+            sa[u] = sw_ld4f(rs, vos, (erow + u) * sb);
         }
         auto step = [&](int s, int u, bool refill) {
-            const int acc = dot8_group(ra[u], X);
-            const float sx = (W.gs > 0 ? sa[u] : 1.0f) * xf;
+            const sw_u32x4 w = ra[u] ^ 0x88888888u;
+            const float sc = W.gs > 0 ? sa[u] : 1.0f;
             if (refill) {
-                const int64_t wr = wrow(s + PF);
-                ra[u] = *(const sw_u32x4 *)(W.q + wr * (K / 2) + g * 16);
-                sa[u] = sbase[wr * ng];
+                ra[u] = sw_ld16(rq, voq, (erow + s + PF) * rb);
+                sa[u] = sw_ld4f(rs, vos, (erow + s + PF) * sb);
                 __builtin_amdgcn_sched_barrier(0);
             }
-            const int lr = s * RPS + ro;
-            if (worker && lr < DG_ROWS) red[lr * Gp + g] = (float)acc * sx;
+#pragma unroll
+            for (int t = 0; t < TT; t++) {
+                if (t < nt) {                          // uniform over the block
+                    const float p = row_term<C16>((float)dot8_group(w, X[t]) * (sc * xf[t]), gv, CH);
+                    if (lead) myruns[(t * DG_ROWS + s) * NC] = p;
+                }
+            }
         };
         int s0 = 0;
         for (; s0 + PF < NS; s0 += PF) {
@@ -346,52 +446,42 @@ __device__ __forceinline__ void dot8_rows_block(const Dot8RowsArgs &A, int bx, i
             for (int u = 0; u < PF; u++) step(s0 + u, u, true);
         }
 #pragma unroll
-        for (int u = 0; u < PF; u++)
-            if (s0 + u < NS) step(s0 + u, u, false);
+        for (int u = 0; u < PF; u++) step(s0 + u, u, false);
         __syncthreads();
-        const int CH = G < CHG ? G : CHG, NC = G / CH;
-        float *runs = red + DG_ROWS * Gp;
-        for (int it = tid; it < DG_ROWS * NC; it += 256) {
-            const int r = it / NC, c = it - r * NC;
-            const float *p = red + r * Gp + c * CH;
-            float sum = p[0];
-            for (int j = 1; j < CH; j++) sum = sum + p[j];
-            runs[r * NC + c] = sum;
-        }
-        __syncthreads();
-        if (tid < nrows) {
-            float y = runs[tid * NC];
-            for (int c = 1; c < NC; c++) y = y + runs[tid * NC + c];
-            if (W.gs <= 0) y = y * W.s[(int64_t)e * O + r0 + tid];
-            Y[(int64_t)(beg + t) * O + r0 + tid] = y;
+        for (int it = tid; it < TT * DG_ROWS; it += 256) {
+            const int t = it / DG_ROWS, r = it - t * DG_ROWS;
+            if (t < nt && r < nrows) {
+                const float *rr = runs + it * NC;
+                float y = rr[0];
+                for (int cc = 1; cc < NC; cc++) y = y + rr[cc];
+                if (W.gs <= 0) y = y * W.s[(int64_t)e * O + r0 + r];
+                Y[(int64_t)(beg + t0 + t) * O + r0 + r] = y;
+            }
         }
         __syncthreads();
     }
 }
 
-template <int PF>
+template <int PF, int TT, int C16>
 __global__ __launch_bounds__(256) void k_dot8_rows(Dot8RowsArgs A) {
     extern __shared__ __align__(16) float red[];
-    dot8_rows_block<PF>(A, blockIdx.x, blockIdx.y, red);
+    TR_BEGIN();
+    dot8_rows_block<PF, TT, C16>(A, blockIdx.x, blockIdx.y, red);
+    TR_END(3);
 }
+template <int PF, int C16>
+struct RowsL {
+    static void go(dim3 grid, size_t lds, hipStream_t st, const Dot8RowsArgs &A) {
+        hipLaunchKernelGGL((k_dot8_rows<PF, DG_TT, C16>), grid, dim3(256), lds, st, A);
+    }
+};
 
 int sw_launch_q4_dot8_rows(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, const float *xs, SwGroups g, float *Y) {
-    const int K = W.K, G = K / RG;
-    if (K % RG || G > 192 || g.ngroups_max <= 0 || W.O <= 0) return -1;
-    const int CH = G < CHG ? G : CHG;
-    if (G % CH) return -1;
-    int gsh = 0;
-    if (W.gs > 0) {
-        if (W.gs % RG || K % W.gs || (W.gs & (W.gs - 1))) return -1;
-        while ((1 << gsh) < W.gs) gsh++;
-    }
-    const int RPS = 256 / G, NS = (DG_ROWS + RPS - 1) / RPS;
+    int gsh;
+    if (!dot8_shape_ok(W.K) || g.ngroups_max <= 0 || W.O <= 0 || !q4_extent_ok(W) || dot8_gsh(W, gsh)) return -1;
     const dim3 grid((unsigned)g.ngroups_max, (unsigned)((W.O + DG_ROWS - 1) / DG_ROWS));
-    const size_t lds = dot8_glu_lds(K);
     const Dot8RowsArgs A = {W, gsh, xl, xs, g, Y};
-    if (NS >= 8) hipLaunchKernelGGL(k_dot8_rows<8>, grid, dim3(256), lds, st, A);
-    else if (NS >= 4) hipLaunchKernelGGL(k_dot8_rows<4>, grid, dim3(256), lds, st, A);
-    else hipLaunchKernelGGL(k_dot8_rows<2>, grid, dim3(256), lds, st, A);
+    dispatch_pf_c16<RowsL>(dg_pf_rows(W.K), dot8_c16(W.K), grid, dot8_glu_lds(W.K, DG_TT), st, A);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
@@ -403,7 +493,7 @@ int sw_launch_q4_dot8_rows(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, const flo
 // fixed-order row sum of the grouped rows kernel (so it is bit-identical to
 // that kernel's slot value) and the ranks are summed in order with one fma
 // each, the operation sequence of k_combine.
-#define DC_RB 16
+#define DC_RB 8
 struct Dot8DownArgs {
     SwQ4 W;
     int gsh;
@@ -416,11 +506,11 @@ struct Dot8DownArgs {
     const float *shared;
     float *out;
 };
-// block bx of DC_RB output rows; red: [K][DC_RB][G + 1], then [K][DC_RB][G / CH] floats
-template <int PF>
-__device__ __forceinline__ void dot8_down_combine_block(const Dot8DownArgs &A, int bx, float *red) {
+// block bx of DC_RB output rows; runs: [K][DC_RB][NC] floats
+template <int C16>
+__device__ __forceinline__ void dot8_down_combine_block(const Dot8DownArgs &A, int bx, float *runs) {
     const SwQ4 W = A.W;
-    const int gsh = A.gsh, K = A.K;
+    const int K = A.K;
     const sw_u32x4 *__restrict__ hl = A.hl;
     const float *__restrict__ hs = A.hs;
     const int *__restrict__ sel = A.sel;
@@ -429,13 +519,16 @@ __device__ __forceinline__ void dot8_down_combine_block(const Dot8DownArgs &A, i
     const float *__restrict__ shared = A.shared;
     float *__restrict__ out = A.out;
     __shared__ float wk[64];
-    const int I = W.K, G = I / RG, Gp = G + 1, D = W.O;
-    const int tid = threadIdx.x, a = tid / G, g = tid - a * G;
-    const bool worker = a < K;
+    const int I = W.K, G = I / RG, D = W.O, Gq = C16 ? G : run_lanes(G);
+    const int CH = C16 ? CHG : (Gq < CHG ? Gq : CHG), NC = Gq / CH;
+    const int tid = threadIdx.x, a = tid / Gq, gq = tid - a * Gq, c = gq / CH;
+    const bool worker = a < K, lead = worker && (gq & (CH - 1)) == 0, gv = C16 || gq < G;
+    const int g = gv ? gq : G - 1;
     const int ac = worker ? a : 0;
     const int d0 = bx * DC_RB;
     const int ng = W.gs > 0 ? I / W.gs : 1;
-    const int sg = W.gs > 0 ? (g * RG) >> gsh : 0;
+    const int sg = W.gs > 0 ? (g * RG) >> A.gsh : 0;
+    const uint32_t rb = (uint32_t)I / 2, sb = (uint32_t)ng * 4;
     if (tid < K) wk[tid] = wts[tid];
     float sh_d = 0.f, out_d = 0.f;
     if (tid < DC_RB) {
@@ -446,43 +539,23 @@ __device__ __forceinline__ void dot8_down_combine_block(const Dot8DownArgs &A, i
 #pragma unroll
     for (int l = 0; l < SW_NL; l++) X[l] = hl[((int64_t)ac * G + g) * SW_NL + l];
     const float xf = hs[(int64_t)ac * G + g];
-    const int e = sel[ac];
-    const uint8_t *wp = W.q + ((int64_t)e * D + d0) * (I / 2) + g * 16;
-    const float *sp = W.s + ((int64_t)e * D + d0) * ng + sg;
-    sw_u32x4 ra[PF];
-    float sa[PF];
+    const uint32_t e = (uint32_t)sel[ac];
+    const sw_rsrc rq = q4_rq(W), rs = q4_rs(W);
+    const uint32_t voq = (e * (uint32_t)D + (uint32_t)d0) * rb + (uint32_t)g * 16;
+    const uint32_t vos = (e * (uint32_t)D + (uint32_t)d0) * sb + (uint32_t)sg * 4;
+    sw_u32x4 ra[DC_RB];
+    float sa[DC_RB];
 #pragma unroll
-    for (int u = 0; u < PF; u++) {
-        ra[u] = *(const sw_u32x4 *)(wp + (int64_t)u * (I / 2));
-        sa[u] = sp[(int64_t)u * ng];
+    for (int r = 0; r < DC_RB; r++) {                // every row of the block in flight
+        ra[r] = sw_ld16(rq, voq, (uint32_t)r * rb);
+        sa[r] = sw_ld4f(rs, vos, (uint32_t)r * sb);
     }
-    float *myred = red + (ac * DC_RB) * Gp + g;
-    auto step = [&](int r, int u, bool refill) {
-        const int acc = dot8_group(ra[u], X);
-        const float sx = (W.gs > 0 ? sa[u] : 1.0f) * xf;
-        if (refill) {
-            ra[u] = *(const sw_u32x4 *)(wp + (int64_t)(r + PF) * (I / 2));
-            sa[u] = sp[(int64_t)(r + PF) * ng];
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        if (worker) myred[r * Gp] = (float)acc * sx;
-    };
-    int r0 = 0;
-    for (; r0 + PF < DC_RB; r0 += PF) {
+    float *myruns = runs + (ac * DC_RB) * NC + c;
 #pragma unroll
-        for (int u = 0; u < PF; u++) step(r0 + u, u, true);
-    }
-#pragma unroll
-    for (int u = 0; u < PF; u++) step(r0 + u, u, false);
-    __syncthreads();
-    const int CH = G < CHG ? G : CHG, NC = G / CH;
-    float *runs = red + K * DC_RB * Gp;
-    for (int it = tid; it < K * DC_RB * NC; it += blockDim.x) {
-        const int ar = it / NC, c = it - ar * NC;
-        const float *p = red + ar * Gp + c * CH;
-        float sum = p[0];
-        for (int j = 1; j < CH; j++) sum = sum + p[j];
-        runs[ar * NC + c] = sum;
+    for (int r = 0; r < DC_RB; r++) {
+        const float sc = W.gs > 0 ? sa[r] : 1.0f;
+        const float p = row_term<C16>((float)dot8_group(ra[r] ^ 0x88888888u, X) * (sc * xf), gv, CH);
+        if (lead) myruns[r * NC] = p;
     }
     __syncthreads();
     if (tid < DC_RB) {
@@ -490,7 +563,7 @@ __device__ __forceinline__ void dot8_down_combine_block(const Dot8DownArgs &A, i
         for (int aa = 0; aa < K; aa++) {
             const float *rr = runs + (aa * DC_RB + tid) * NC;
             float y = rr[0];
-            for (int c = 1; c < NC; c++) y = y + rr[c];
+            for (int cc = 1; cc < NC; cc++) y = y + rr[cc];
             if (W.gs <= 0) y = y * W.s[(int64_t)sel[aa] * D + d0 + tid];
             acc = __builtin_fmaf(wk[aa], y, acc);
         }
@@ -500,28 +573,25 @@ __device__ __forceinline__ void dot8_down_combine_block(const Dot8DownArgs &A, i
     }
 }
 
-template <int PF>
+template <int C16>
 __global__ __launch_bounds__(1024) void k_dot8_down_combine(Dot8DownArgs A) {
     extern __shared__ __align__(16) float red[];
-    dot8_down_combine_block<PF>(A, blockIdx.x, red);
+    TR_BEGIN();
+    dot8_down_combine_block<C16>(A, blockIdx.x, red);
+    TR_END(2);
 }
 
 int sw_launch_q4_dot8_down_combine(hipStream_t st, SwQ4 W, const sw_u32x4 *hl, const float *hs, const int *sel, const float *w,
                                    int K, float route_scale, const float *shared, float *out) {
     const int I = W.K, G = I / RG;
-    if (I % RG || W.O % DC_RB || K <= 0 || K > 64 || K * G > 1024) return -1;
-    const int CH = G < CHG ? G : CHG;
-    if (G % CH) return -1;
-    int gsh = 0;
-    if (W.gs > 0) {
-        if (W.gs % RG || I % W.gs || (W.gs & (W.gs - 1))) return -1;
-        while ((1 << gsh) < W.gs) gsh++;
-    }
-    const size_t lds = ((size_t)K * DC_RB * (G + 1) + (size_t)K * DC_RB * (G / CH)) * 4;
-    if (lds > 65536) return -1;
-    const int threads = (K * G + 63) / 64 * 64;
+    int gsh;
+    if (!dot8_shape_ok(I) || W.O % DC_RB || K <= 0 || K > 64 || K * run_lanes(G) > 1024 || !q4_extent_ok(W) ||
+        dot8_gsh(W, gsh)) return -1;
+    const size_t lds = (size_t)K * DC_RB * dot8_nc(I) * 4;
+    const int threads = (K * run_lanes(G) + 63) / 64 * 64;
     const Dot8DownArgs A = {W, gsh, hl, hs, sel, w, K, route_scale, shared, out};
-    hipLaunchKernelGGL(k_dot8_down_combine<8>, dim3((unsigned)(W.O / DC_RB)), dim3(threads), lds, st, A);
+    if (dot8_c16(I)) hipLaunchKernelGGL(k_dot8_down_combine<1>, dim3((unsigned)(W.O / DC_RB)), dim3(threads), lds, st, A);
+    else hipLaunchKernelGGL(k_dot8_down_combine<0>, dim3((unsigned)(W.O / DC_RB)), dim3(threads), lds, st, A);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
@@ -533,60 +603,64 @@ int sw_launch_q4_dot8_down_combine(hipStream_t st, SwQ4 W, const sw_u32x4 *hl, c
 // The blocks of the two jobs of a stage share one grid (the critical-path job
 // first), so the shared expert fills what the routed work leaves of the chip
 // instead of running as its own launches.
+static size_t lds_max(size_t a, size_t b) { return a > b ? a : b; }
+
 struct ShGluArgs { const uint16_t *Wg, *Wu; const float *x; int S, D, Is; float *h; };
 struct ShDownArgs { const uint16_t *Wd; const float *h; int S, Is, D; float *out; };
 
 template <int BF16, int TT>
-__global__ __launch_bounds__(256) void k_stage_route(RouterArgs R, int nbr, int S, ShGluArgs G) {
+__global__ __launch_bounds__(SH_NT) void k_stage_route(RouterArgs R, int nbr, int S, ShGluArgs G) {
     extern __shared__ __align__(16) float smem[];
+    TR_BEGIN();
     const int b = blockIdx.x;
     if (b < nbr * S) router_block<BF16>(R, b % nbr, b / nbr, nbr, smem);
     else sh_glu_block<TT>(G.Wg, G.Wu, G.x, G.S, G.D, G.Is, G.h, b - nbr * S, smem);
+    TR_END(0);
 }
 
-template <int PF, int NP, int TT>
-__global__ __launch_bounds__(256) void k_stage_experts(Dot8GluArgs A, int nbx, int nglu, ShDownArgs Sd) {
+// TTG: tokens per pass of the routed gate_up; TTS: of the shared down
+template <int PF, int NP, int TTG, int TTS, int C16>
+__global__ __launch_bounds__(DG_NT) void k_stage_experts(Dot8GluArgs A, int nbx, int nglu, ShDownArgs Sd) {
     extern __shared__ __align__(16) float smem[];
+    TR_BEGIN();
     const int b = blockIdx.x;
-    if (b < nglu) dot8_glu_block<PF, NP>(A, b % nbx, b / nbx, smem);
-    else sh_down_block<TT>(Sd.Wd, Sd.h, Sd.S, Sd.Is, Sd.D, Sd.out, b - nglu, smem);
+    if (b < nglu) dot8_glu_block<PF, NP, TTG, C16>(A, b % nbx, b / nbx, smem);
+    else sh_down_block<TTS>(Sd.Wd, Sd.h, Sd.S, Sd.Is, Sd.D, Sd.out, b - nglu, smem);
+    TR_END(1);
 }
+template <int NP, int TTG, int TTS>
+struct StageL {
+    template <int PF, int C16>
+    struct L {
+        static void go(dim3 grid, size_t lds, hipStream_t st, const Dot8GluArgs &A, int nbx, int nglu, const ShDownArgs &Sd) {
+            hipLaunchKernelGGL((k_stage_experts<PF, NP, TTG, TTS, C16>), grid, dim3(DG_NT), lds, st, A, nbx, nglu, Sd);
+        }
+    };
+};
 
-static size_t lds_max(size_t a, size_t b) { return a > b ? a : b; }
-
-// stage 1: sh_glu may be null (no shared expert)
+// stage 1: sg may be null (no shared expert)
 int sw_launch_stage_route(hipStream_t st, const void *Wc, int w_bf16, const float *x, int S, int D, int E,
                           const float *logit_bias, float *logits, float *scores, int route_act, sw_u32x4 *xl, float *xs,
                           const uint16_t *sg, const uint16_t *su, int Is, float *sh_h) {
     if (D % 128 || E <= 0 || S <= 0 || route_act < 0 || route_act > 2 || (route_act != 1 && !scores)) return -1;
-    const int nw = 4;
-    const size_t rl = router_lds(D, w_bf16, nw);
+    const size_t rl = router_lds(D);
     if (rl > 65536) return -1;
-    const int nbr = (E + nw - 1) / nw;
+    const int nbr = (E + router_epb(SH_NT) - 1) / router_epb(SH_NT);
     const RouterArgs R = {Wc, x, D, E, logit_bias, logits, route_act, scores, xl, xs};
     const ShGluArgs G = {sg, su, x, S, D, Is, sh_h};
-    const int TT = S >= 2 ? 2 : 1;
+    const int TT = S >= 2 ? SH_TT : 1;
     const int nsh = sg ? sh_glu_blocks(S, Is, TT) : 0;
-    if (sg && (Is % SH_GLU_O || (D / SH_RG) > 256)) return -1;
+    if (sg && (Is % SH_GLU_O || !sh_shape_ok(D))) return -1;
     const dim3 grid((unsigned)(nbr * S + nsh));
-    if (TT == 2) {
-        const size_t lds = lds_max(rl, sg ? sh_glu_lds<2>(D) : 0);
-        if (w_bf16) hipLaunchKernelGGL((k_stage_route<1, 2>), grid, dim3(256), lds, st, R, nbr, S, G);
-        else hipLaunchKernelGGL((k_stage_route<0, 2>), grid, dim3(256), lds, st, R, nbr, S, G);
+    const size_t lds = lds_max(rl, sg ? (TT == SH_TT ? sh_glu_lds<SH_TT>(D) : sh_glu_lds<1>(D)) : 0);
+    if (TT == SH_TT) {
+        if (w_bf16) hipLaunchKernelGGL((k_stage_route<1, SH_TT>), grid, dim3(SH_NT), lds, st, R, nbr, S, G);
+        else hipLaunchKernelGGL((k_stage_route<0, SH_TT>), grid, dim3(SH_NT), lds, st, R, nbr, S, G);
     } else {
-        const size_t lds = lds_max(rl, sg ? sh_glu_lds<1>(D) : 0);
-        if (w_bf16) hipLaunchKernelGGL((k_stage_route<1, 1>), grid, dim3(256), lds, st, R, nbr, S, G);
-        else hipLaunchKernelGGL((k_stage_route<0, 1>), grid, dim3(256), lds, st, R, nbr, S, G);
+        if (w_bf16) hipLaunchKernelGGL((k_stage_route<1, 1>), grid, dim3(SH_NT), lds, st, R, nbr, S, G);
+        else hipLaunchKernelGGL((k_stage_route<0, 1>), grid, dim3(SH_NT), lds, st, R, nbr, S, G);
     }
     return hipGetLastError() == hipSuccess ? 0 : -1;
-}
-
-template <int NP, int TT>
-static void launch_stage_experts(int ns, dim3 grid, size_t lds, hipStream_t st, const Dot8GluArgs &A, int nbx, int nglu,
-                                 const ShDownArgs &Sd) {
-    if (ns >= 8) hipLaunchKernelGGL((k_stage_experts<8, NP, TT>), grid, dim3(256), lds, st, A, nbx, nglu, Sd);
-    else if (ns >= 4) hipLaunchKernelGGL((k_stage_experts<4, NP, TT>), grid, dim3(256), lds, st, A, nbx, nglu, Sd);
-    else hipLaunchKernelGGL((k_stage_experts<2, NP, TT>), grid, dim3(256), lds, st, A, nbx, nglu, Sd);
 }
 
 // stage 2.  Routed gate_up for the groups g (route_src null), or for one token
@@ -598,29 +672,29 @@ int sw_launch_stage_experts(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, const fl
                             float *sh_out) {
     int gsh;
     if (dot8_glu_check(W, I, gsh)) return -1;
-    const int G = W.K / RG, RPS = 256 / G, NS = (DG_ROWS + RPS - 1) / RPS;
     const bool fused = route_src != nullptr;
     if (fused && (S != 1 || E <= 0 || E > 256 || K <= 0 || K > 64 || K > E)) return -1;
     if (!fused && g.ngroups_max <= 0) return -1;
-    if (sd && (D % SH_DN_O || (Is / SH_RG) > 256)) return -1;
+    if (sd && (D % SH_DN_O || !sh_shape_ok(Is))) return -1;
     const int nbx = fused ? K : g.ngroups_max;
     const int nglu = nbx * (I / 32);
-    const int TT = S >= 2 ? 2 : 1;
-    const int nsh = sd ? sh_down_blocks(S, D, TT) : 0;
+    const int TTS = S >= 2 ? SH_TT : 1;
+    const int nsh = sd ? sh_down_blocks(S, D, TTS) : 0;
     const DotRoute rt = fused ? DotRoute{route_src, bias, E, K, act, use_bias, norm, sel, w} : DotRoute{};
     const Dot8GluArgs A = {W, gsh, xl, xs, g, I, hl, hs, rt};
     const ShDownArgs Sd = {sd, sh_h, S, Is, D, sh_out};
     const dim3 grid((unsigned)(nglu + nsh));
-    const size_t lds = lds_max(dot8_glu_lds(W.K), sd ? (TT == 2 ? sh_down_lds<2>(Is) : sh_down_lds<1>(Is)) : 0);
+    const size_t shl = sd ? (TTS == SH_TT ? sh_down_lds<SH_TT>(Is) : sh_down_lds<1>(Is)) : 0;
+    const int pf = dg_pf_glu(W.K), c16 = dot8_c16(W.K);
     if (!fused) {
-        if (TT == 2) launch_stage_experts<0, 2>(NS, grid, lds, st, A, nbx, nglu, Sd);
-        else launch_stage_experts<0, 1>(NS, grid, lds, st, A, nbx, nglu, Sd);
-    } else if (E <= 64) {
-        launch_stage_experts<1, 1>(NS, grid, lds, st, A, nbx, nglu, Sd);
-    } else if (E <= 128) {
-        launch_stage_experts<2, 1>(NS, grid, lds, st, A, nbx, nglu, Sd);
+        const size_t lds = lds_max(dot8_glu_lds(W.K, DG_TT), shl);
+        if (TTS == SH_TT) dispatch_pf_c16<StageL<0, DG_TT, SH_TT>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd);
+        else dispatch_pf_c16<StageL<0, DG_TT, 1>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd);
     } else {
-        launch_stage_experts<4, 1>(NS, grid, lds, st, A, nbx, nglu, Sd);
+        const size_t lds = lds_max(dot8_glu_lds(W.K, 1), shl);
+        if (E <= 64) dispatch_pf_c16<StageL<1, 1, 1>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd);
+        else if (E <= 128) dispatch_pf_c16<StageL<2, 1, 1>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd);
+        else dispatch_pf_c16<StageL<4, 1, 1>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd);
     }
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }

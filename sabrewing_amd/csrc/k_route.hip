@@ -10,20 +10,25 @@ static int launch_err(void) { return hipGetLastError() == hipSuccess ? 0 : -1; }
 // ------------------------------------------------------------ router ----
 // Chain-major router copy: Wc[(e*16 + j)*M + m] = W[e*D + 16m + j], M = D/16,
 // so lane j of expert e reads its FMA chain contiguously.
+// The router in the order the routing kernel streams it (sw_router.h), in
+// its own element type: experts in groups of 4, group g a run of 1 KB
+// slices, slice q holding for each of the group's 64 chains c = 16*(e%4) + j
+// (j = i%16) the next P elements m = Pq..Pq+P-1 (m = i/16) of that chain,
+// P = 8 for bf16 and 4 for f32; experts past E in the last group are zero.
 __global__ void k_chain_major(const void *__restrict__ W, int w_bf16, int E, int D, void *__restrict__ Wc) {
-    const int M = D / 16;
-    const int64_t n = (int64_t)E * D;
-    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t e = i / D, k = i % D, m = k / 16, j = k % 16;
-        const int64_t o = (e * 16 + j) * M + m;
-        if (w_bf16) ((uint16_t *)Wc)[o] = ((const uint16_t *)W)[i];
-        else ((float *)Wc)[o] = ((const float *)W)[i];
+    const int P = w_bf16 ? 8 : 4, NQ = D / 16 / P;
+    const int64_t n = (int64_t)((E + 3) / 4) * 4 * D;
+    for (int64_t o = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; o < n; o += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t u = o % P, c = (o / P) & 63, q = (o / P / 64) % NQ, g = (o / P / 64) / NQ;
+        const int64_t e = 4 * g + (c >> 4), j = c & 15, m = (int64_t)P * q + u, i = 16 * m + j;
+        if (w_bf16) ((uint16_t *)Wc)[o] = e < E ? ((const uint16_t *)W)[e * D + i] : (uint16_t)0;
+        else ((float *)Wc)[o] = e < E ? ((const float *)W)[e * D + i] : 0.f;
     }
 }
 
 int sw_launch_chain_major(hipStream_t st, const void *W, int w_bf16, int E, int D, void *Wc) {
     if (D % 128 || E <= 0) return -1;
-    const int64_t n = (int64_t)E * D;
+    const int64_t n = (int64_t)((E + 3) / 4) * 4 * D;
     hipLaunchKernelGGL(k_chain_major, dim3((unsigned)sw_imin64((n + 255) / 256, 8192)), dim3(256), 0, st, W, w_bf16, E, D, Wc);
     return launch_err();
 }
@@ -54,14 +59,13 @@ int sw_launch_router_topk(hipStream_t st, const void *Wc, int w_bf16, const floa
                           sw_u32x4 *xl, float *xs) {
     if (D % 128 || D > 16384 || E <= 0 || E > TK_MAXE || S <= 0 || K <= 0 || K > 64 || K > E) return -1;
     if (route_act < 0 || route_act > 2 || (sel && route_act != 1 && !scores)) return -1;
-    // one expert per wave; several per block once there are enough tokens to fill the chip
-    int nw = S >= 4 ? 4 : 1;
-    while (nw > 1 && router_lds(D, w_bf16, nw) > 65536) nw >>= 1;
-    if (router_lds(D, w_bf16, nw) > 65536) return -1;
-    dim3 grid((unsigned)((E + nw - 1) / nw), (unsigned)S);
+    // four experts per wave, four waves per block
+    const int nt = 256, epb = router_epb(nt);
+    if (router_lds(D) > 65536) return -1;
+    dim3 grid((unsigned)((E + epb - 1) / epb), (unsigned)S);
     const RouterArgs R = {Wc, x, D, E, logit_bias, logits, route_act, scores, xl, xs};
-    if (w_bf16) hipLaunchKernelGGL(k_router_logits<1>, grid, dim3(64 * nw), router_lds(D, w_bf16, nw), st, R);
-    else hipLaunchKernelGGL(k_router_logits<0>, grid, dim3(64 * nw), router_lds(D, w_bf16, nw), st, R);
+    if (w_bf16) hipLaunchKernelGGL(k_router_logits<1>, grid, dim3(nt), router_lds(D), st, R);
+    else hipLaunchKernelGGL(k_router_logits<0>, grid, dim3(nt), router_lds(D), st, R);
     if (launch_err()) return -1;
     if (!sel) return 0;                              // logits only
     return sw_launch_gate_topk(st, logits, scores, S, E, K, route_act, corr_bias, use_corr_bias, norm_topk, sel, w);

@@ -15,9 +15,10 @@
 // the lowest unselected id, weight = unbiased score, optional renormalisation
 // summed in rank order (c/moe_block.h:121-122).
 //
-// A pass is one wave-wide max over 64-bit keys (order-preserving bits of
-// key + 0.0 above ~id, so a larger key wins and equal keys go to the lower
-// id; invalid or taken experts are key 0), reduced with DPP row operations.
+// A pass is one wave-wide max of the order-preserving bits of key + 0.0
+// (invalid or taken experts are 0), then the lowest id holding that maximum
+// found with one ballot per slot: a larger key wins, equal keys go to the
+// lower id.
 #define TK_MAXE 1024
 
 struct TopkLDS {
@@ -35,26 +36,61 @@ __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-template <int CTRL, int ROWMASK>
-__device__ __forceinline__ uint64_t dpp64(uint64_t v) {
-    const int lo = (int)(uint32_t)v, hi = (int)(uint32_t)(v >> 32);
-    const uint32_t lo2 = (uint32_t)__builtin_amdgcn_update_dpp(lo, lo, CTRL, ROWMASK, 0xF, false);
-    const uint32_t hi2 = (uint32_t)__builtin_amdgcn_update_dpp(hi, hi, CTRL, ROWMASK, 0xF, false);
-    return ((uint64_t)hi2 << 32) | lo2;
+// max over the 64 lanes, returned uniform: the max within each 16-lane row by
+// DPP (0 fills nothing: the operations stay inside the row), then the rows'
+// maxima by readlane
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_umax(uint32_t v) {
+    const uint32_t o = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, true);
+    return v > o ? v : o;
 }
-__device__ __forceinline__ uint64_t max64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+__device__ __forceinline__ uint32_t wave_umax(uint32_t v) {
+    v = dpp_umax<0xB1>(v);                  // quad_perm [1,0,3,2]
+    v = dpp_umax<0x4E>(v);                  // quad_perm [2,3,0,1]
+    v = dpp_umax<0x141>(v);                 // row_half_mirror
+    v = dpp_umax<0x140>(v);                 // row_mirror
+    const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)v, 0), r1 = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
+    const uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane((int)v, 32), r3 = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+    const uint32_t m01 = r0 > r1 ? r0 : r1, m23 = r2 > r3 ? r2 : r3;
+    return m01 > m23 ? m01 : m23;
+}
 
-// max over the 64 lanes, returned uniform
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-    v = max64(v, dpp64<0xB1, 0xF>(v));    // quad_perm [1,0,3,2]
-    v = max64(v, dpp64<0x4E, 0xF>(v));    // quad_perm [2,3,0,1]
-    v = max64(v, dpp64<0x141, 0xF>(v));   // row_half_mirror
-    v = max64(v, dpp64<0x140, 0xF>(v));   // row_mirror
-    v = max64(v, dpp64<0x142, 0xA>(v));   // row_bcast:15 into rows 1, 3
-    v = max64(v, dpp64<0x143, 0xC>(v));   // row_bcast:31 into rows 2, 3
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, 63);
-    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), 63);
-    return ((uint64_t)hi << 32) | lo;
+// The fixed summation order of every GEMV row here: a row's G terms (one per
+// group of 32 inputs) are padded with zero terms to Gq = run_lanes(G) (the
+// next power of two below 16, the next multiple of 16 above) and summed in
+// runs of n = min(Gq, 16) consecutive groups held by n consecutive lanes
+// (aligned to n), each run as the butterfly of pairs, quads, eights and
+// sixteens -- every lane of the run ends with the same sum, since
+// a + b == b + a -- then the run sums left to right.  It depends on nothing
+// but the row's terms.
+__host__ __device__ inline int run_lanes(int G) {
+    if (G >= 16) return (G + 15) & ~15;
+    int q = 1;
+    while (q < G) q <<= 1;
+    return q;
+}
+template <int CTRL>
+__device__ __forceinline__ float dppf(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, v), __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+// lane i of a 16-lane row gets v(i) + v(partner(i)), one v_add_f32_dpp
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float v) {
+    return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+__device__ __forceinline__ float run_sum16(float v) {
+    v = dpp_add<0xB1>(v);                   // quad_perm [1,0,3,2]
+    v = dpp_add<0x4E>(v);                   // quad_perm [2,3,0,1]
+    v = dpp_add<0x141>(v);                  // row_half_mirror
+    return dpp_add<0x140>(v);               // row_mirror
+}
+// the same butterfly over runs of n (a power of two <= 16) lanes
+__device__ __forceinline__ float run_sum(float v, int n) {
+    if (n >= 2) v = v + dppf<0xB1>(v);      // quad_perm [1,0,3,2]
+    if (n >= 4) v = v + dppf<0x4E>(v);      // quad_perm [2,3,0,1]
+    if (n >= 8) v = v + dppf<0x141>(v);     // row_half_mirror
+    if (n >= 16) v = v + dppf<0x140>(v);    // row_mirror
+    return v;
 }
 
 __device__ __forceinline__ uint32_t ord_f32(float f) {
@@ -116,25 +152,28 @@ __device__ void gate_topk_wave(const float *__restrict__ src, int E, int K, int 
         if (e < E) sh.sc[e] = v[i];
     }
     wave_sync();
-    uint64_t kk[NPER];
+    uint32_t ko[NPER];                                // order key, 0 = invalid or taken (valid keys order above 0)
     bool fr[NPER];
 #pragma unroll
     for (int i = 0; i < NPER; i++) {
         const int e = lane + 64 * i;
         const float key = v[i] + b[i];
         fr[i] = e < E;
-        kk[i] = (e < E && key > -1e30f) ? (((uint64_t)ord_f32(key) << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)e)) : 0ull;
+        ko[i] = (e < E && key > -1e30f) ? ord_f32(key) : 0u;
     }
     for (int a = 0; a < K; a++) {
-        uint64_t m = kk[0];
+        uint32_t lm = ko[0];
 #pragma unroll
-        for (int i = 1; i < NPER; i++) m = max64(m, kk[i]);
-        m = wave_max_u64(m);
-        int bi;
-        if (m != 0ull) {
-            bi = (int)(0xFFFFFFFFu - (uint32_t)m);
+        for (int i = 1; i < NPER; i++) lm = lm > ko[i] ? lm : ko[i];
+        const uint32_t m = wave_umax(lm);
+        int bi = 0x7fffffff;
+        if (m != 0u) {                                // the lowest id holding the maximum
+#pragma unroll
+            for (int i = NPER - 1; i >= 0; i--) {
+                const unsigned long long bal = __ballot(ko[i] == m);
+                if (bal) bi = 64 * i + __builtin_ctzll(bal);
+            }
         } else {                                      // nothing valid left: the lowest unselected id
-            bi = 0x7fffffff;
 #pragma unroll
             for (int i = NPER - 1; i >= 0; i--) {
                 const unsigned long long bal = __ballot(fr[i]);
@@ -145,7 +184,7 @@ __device__ void gate_topk_wave(const float *__restrict__ src, int E, int K, int 
         if ((bi & 63) == lane) {
 #pragma unroll
             for (int i = 0; i < NPER; i++)
-                if (i == (bi >> 6)) { kk[i] = 0ull; fr[i] = false; }
+                if (i == (bi >> 6)) { ko[i] = 0u; fr[i] = false; }
         }
         if (lane == 0) { sh.sk[a] = bi; sh.wk[a] = sh.sc[bi]; }
     }

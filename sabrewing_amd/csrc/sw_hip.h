@@ -39,6 +39,22 @@ typedef __bf16 sw_bf16x8 __attribute__((ext_vector_type(8)));
 typedef float sw_f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t sw_u32x4 __attribute__((ext_vector_type(4)));
 
+#ifdef __HIPCC__
+// Raw buffer access: a tensor is one descriptor (base and byte extent in
+// scalar registers); each lane adds a 32-bit offset and each step a scalar
+// one; a load past the extent returns 0 and touches no memory.
+typedef __amdgpu_buffer_rsrc_t sw_rsrc;
+__device__ __forceinline__ sw_rsrc sw_make_rsrc(const void *p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, bytes, 0x00020000);
+}
+__device__ __forceinline__ sw_u32x4 sw_ld16(sw_rsrc r, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+}
+__device__ __forceinline__ float sw_ld4f(sw_rsrc r, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+}
+#endif
+
 #define SW_WAVE 64
 
 static inline int64_t sw_imin64(int64_t a, int64_t b) { return a < b ? a : b; }
@@ -62,6 +78,7 @@ struct SwQ4 {
     const uint8_t *q;     // [E*O, K/2]
     const float *s;       // [E*O, ng]
     int O, K, gs;         // gs = 0: per-row scale
+    int E;                // experts in the tensor (the extent of its buffer descriptors)
 };
 
 // bf16 weight tensor [O, K]

@@ -4,14 +4,16 @@
 // Per output row and token, every group of 32 consecutive inputs gives one
 // term: a chain of 32 f32 fmas in input order from 0 (the bf16 weight is
 // exact in f32); the row is the sum of its group terms in the fixed order of
-// the int4 kernels (runs of 16 groups left to right, the runs left to right).
-// Tokens are independent, so a token's result does not depend on the batch.
+// the int4 kernels (run_sum in sw_gate.h).  Tokens are independent, so a
+// token's result does not depend on the batch.
 #ifndef SW_SHARED_H
 #define SW_SHARED_H
 #include "sw_hip.h"
+#include "sw_gate.h"
 
 #define SH_RG 32               // inputs per group
 #define SH_CHG 16              // groups per run of the row sum
+#define SH_TT 2                // tokens per weight pass of a batch
 
 __device__ __forceinline__ float bf16lo(uint32_t u) { return __builtin_bit_cast(float, u << 16); }
 __device__ __forceinline__ float bf16hi(uint32_t u) { return __builtin_bit_cast(float, u & 0xFFFF0000u); }
@@ -32,42 +34,42 @@ __device__ __forceinline__ float bf16_group_chain(const sw_u32x4 *w, const float
     return t;
 }
 
-// fixed-order sum of the G group terms p[0..G)
-__device__ __forceinline__ float sh_row_sum(const float *p, int G) {
-    const int CH = G < SH_CHG ? G : SH_CHG, NC = G / CH;
-    float y = 0.f;
-    for (int c = 0; c < NC; c++) {
-        float run = p[c * CH];
-        for (int j = 1; j < CH; j++) run = run + p[c * CH + j];
-        y = c == 0 ? run : y + run;
-    }
-    return y;
-}
+// K inputs in G = K/32 groups, G <= 256
+__host__ __device__ inline bool sh_shape_ok(int K) { return K > 0 && K % SH_RG == 0 && K / SH_RG <= 256; }
 
 // Rows job: NR rows (the K bf16 inputs of local row lr at rowp(lr)) against
 // the tokens tok0..tok0+nt-1 (nt <= TT) of x [*, K] f32; the row results go
-// out through emit(lr, t, y).  Block of 256 threads: thread (ro, g) with
-// G = K/32 groups and RPS = 256/G rows per step, SH_PF steps of loads in
-// flight.  LDS: red[NR * TT * (G + 1)] floats.
-#define SH_PF 4
-template <int NR, int TT, class RowPtr, class Emit>
+// out through emit(lr, t, y).  Block of NT threads: thread (row slot ro,
+// group g) with G = K/32 groups, Gq = run_lanes(G) lanes per row (lanes
+// g >= G add zero terms) and RPS row slots (a power of two); slot ro takes
+// NS = NR/RPS consecutive rows, one per step, SH_PF steps of loads in flight,
+// the group's inputs of every token of the tile in registers.  LDS:
+// runs[NR * TT * NC] floats, NC = Gq / min(Gq, 16).
+#define SH_PF 2
+__host__ __device__ inline int sh_rps(int Gq, int NR, int NT) {
+    int r = 1;
+    while (r * 2 * Gq <= NT && r < NR) r *= 2;
+    return r;
+}
+template <int NR, int TT, int NT, class RowPtr, class Emit>
 __device__ __forceinline__ void sh_rows_job(RowPtr rowp, int K, const float *__restrict__ x, int tok0, int nt, Emit emit,
-                                            float *red) {
-    const int G = K / SH_RG, Gp = G + 1;
+                                            float *runs) {
+    const int G = K / SH_RG, Gq = run_lanes(G);
+    const int CH = Gq < SH_CHG ? Gq : SH_CHG, NC = Gq / CH;
     const int tid = threadIdx.x;
-    const int RPS = 256 / G, NS = (NR + RPS - 1) / RPS;
-    const int ro = tid / G, g = tid - ro * G;
-    const bool worker = ro < RPS;
+    const int RPS = sh_rps(Gq, NR, NT), NS = NR / RPS;
+    const int ro = tid / Gq, gq = tid - ro * Gq, c = gq / CH;
+    const bool worker = ro < RPS, lead = worker && (gq & (CH - 1)) == 0, gv = gq < G;
+    const int g = gv ? gq : G - 1;                   // padding lanes load group G-1 and add 0
+    const int roc = worker ? ro : 0;
     auto wld = [&](int s, sw_u32x4 *w) {
-        int lr = s * RPS + (worker ? ro : 0);
-        lr = lr < NR ? lr : NR - 1;
-        const sw_u32x4 *wp = (const sw_u32x4 *)(rowp(lr) + g * SH_RG);
+        const sw_u32x4 *wp = (const sw_u32x4 *)(rowp(roc * NS + s) + g * SH_RG);
 #pragma unroll
         for (int q = 0; q < 4; q++) w[q] = wp[q];
     };
     sw_u32x4 ring[SH_PF][4];
 #pragma unroll
-    for (int u = 0; u < SH_PF; u++) wld(u, ring[u]);
+    for (int u = 0; u < SH_PF; u++) wld(u < NS ? u : NS - 1, ring[u]);
     float xv[TT][SH_RG];
 #pragma unroll
     for (int t = 0; t < TT; t++) {
@@ -84,12 +86,14 @@ __device__ __forceinline__ void sh_rows_job(RowPtr rowp, int K, const float *__r
 #pragma unroll
         for (int q = 0; q < 4; q++) w[q] = ring[u][q];
         if (refill) { wld(s + SH_PF, ring[u]); __builtin_amdgcn_sched_barrier(0); }
-        const int lr = s * RPS + ro;
-        const bool live = worker && lr < NR && s < NS;
+        const int lr = roc * NS + s;
 #pragma unroll
         for (int t = 0; t < TT; t++) {
-            const float p = bf16_group_chain(w, xv[t]);
-            if (live) red[(lr * TT + t) * Gp + g] = p;
+            if (t < nt) {                              // uniform over the block
+                const float q = bf16_group_chain(w, xv[t]);
+                const float p = CH == SH_CHG ? run_sum16(q) : run_sum(gv ? q : 0.f, CH);
+                if (lead && s < NS) runs[(lr * TT + t) * NC + c] = p;
+            }
         }
     };
     int s0 = 0;
@@ -100,16 +104,24 @@ __device__ __forceinline__ void sh_rows_job(RowPtr rowp, int K, const float *__r
 #pragma unroll
     for (int u = 0; u < SH_PF; u++) step(s0 + u, u, false);
     __syncthreads();
-    for (int it = tid; it < NR * TT; it += 256) {
+    for (int it = tid; it < NR * TT; it += NT) {
         const int lr = it / TT, t = it - lr * TT;
-        if (t < nt) emit(lr, t, sh_row_sum(red + it * Gp, G));
+        if (t < nt) {
+            const float *rr = runs + it * NC;
+            float y = rr[0];
+            for (int cc = 1; cc < NC; cc++) y = y + rr[cc];
+            emit(lr, t, y);
+        }
     }
     __syncthreads();
 }
 
+__host__ __device__ inline int sh_nc(int K) { return K / SH_RG < SH_CHG ? 1 : run_lanes(K / SH_RG) / SH_CHG; }
+
 // shared expert gate_up: SH_GLU_O outputs i per block; local rows 0..O-1 are
 // gate rows i0.., rows O..2O-1 the up rows; h[tok][i] = silu(gate) * up (f32)
-#define SH_GLU_O 8
+#define SH_NT 512              // threads per block of the shared-expert jobs
+#define SH_GLU_O 4
 template <int TT>
 __device__ __forceinline__ void sh_glu_block(const uint16_t *__restrict__ Wg, const uint16_t *__restrict__ Wu,
                                              const float *__restrict__ x, int S, int D, int Is, float *__restrict__ h,
@@ -118,8 +130,8 @@ __device__ __forceinline__ void sh_glu_block(const uint16_t *__restrict__ Wg, co
     const int rs = bid % nrs, tt = bid / nrs;
     const int i0 = rs * SH_GLU_O, tok0 = tt * TT;
     const int nt = min(TT, S - tok0);
-    float *ys = red + 2 * SH_GLU_O * TT * (D / SH_RG + 1);   // [2*SH_GLU_O][TT] row results
-    sh_rows_job<2 * SH_GLU_O, TT>(
+    float *ys = red + 2 * SH_GLU_O * TT * sh_nc(D);   // [2*SH_GLU_O][TT] row results
+    sh_rows_job<2 * SH_GLU_O, TT, SH_NT>(
         [&](int lr) { return (lr < SH_GLU_O ? Wg : Wu) + (int64_t)(i0 + (lr & (SH_GLU_O - 1))) * D; }, D, x, tok0, nt,
         [&](int lr, int t, float y) { ys[lr * TT + t] = y; }, red);
     const int tid = threadIdx.x;
@@ -133,8 +145,8 @@ __device__ __forceinline__ void sh_glu_block(const uint16_t *__restrict__ Wg, co
     __syncthreads();
 }
 template <int TT>
-__host__ __device__ constexpr size_t sh_glu_lds(int D) {
-    return ((size_t)2 * SH_GLU_O * TT * (D / SH_RG + 1) + (size_t)2 * SH_GLU_O * TT) * 4;
+__host__ __device__ inline size_t sh_glu_lds(int D) {
+    return ((size_t)2 * SH_GLU_O * TT * sh_nc(D) + (size_t)2 * SH_GLU_O * TT) * 4;
 }
 __host__ __device__ inline int sh_glu_blocks(int S, int Is, int TT) { return (Is / SH_GLU_O) * ((S + TT - 1) / TT); }
 
@@ -147,11 +159,11 @@ __device__ __forceinline__ void sh_down_block(const uint16_t *__restrict__ Wd, c
     const int rs = bid % nrs, tt = bid / nrs;
     const int d0 = rs * SH_DN_O, tok0 = tt * TT;
     const int nt = min(TT, S - tok0);
-    sh_rows_job<SH_DN_O, TT>([&](int lr) { return Wd + (int64_t)(d0 + lr) * Is; }, Is, h, tok0, nt,
+    sh_rows_job<SH_DN_O, TT, SH_NT>([&](int lr) { return Wd + (int64_t)(d0 + lr) * Is; }, Is, h, tok0, nt,
                              [&](int lr, int t, float y) { out[(int64_t)(tok0 + t) * D + d0 + lr] = y; }, red);
 }
 template <int TT>
-__host__ __device__ constexpr size_t sh_down_lds(int Is) { return (size_t)SH_DN_O * TT * (Is / SH_RG + 1) * 4; }
+__host__ __device__ inline size_t sh_down_lds(int Is) { return (size_t)SH_DN_O * TT * sh_nc(Is) * 4; }
 __host__ __device__ inline int sh_down_blocks(int S, int D, int TT) { return (D / SH_DN_O) * ((S + TT - 1) / TT); }
 
 #endif
