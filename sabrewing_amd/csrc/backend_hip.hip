@@ -102,6 +102,16 @@ static int grow_dev(Buf &b, size_t need) {
     b.cap = need * 2;
     return 0;
 }
+// per-token arrival counters of the routing stage: their own allocation (no
+// other scratch ever overlaps them), zero between launches (the last block of
+// each token resets its counter)
+static Buf g_cnt;
+static int ensure_cnt(int S) {
+    if ((size_t)S * 4 <= g_cnt.cap) return 0;
+    if (grow_dev(g_cnt, (size_t)S * 4)) return -1;
+    CK(hipMemsetAsync(g_cnt.p, 0, g_cnt.cap, g_st), "counter clear");
+    return 0;
+}
 static int grow_pinned(Buf &b, size_t need) {
     if (need <= b.cap) return 0;
     if (b.p) (void)hipHostFree(b.p);
@@ -454,9 +464,10 @@ extern "C" int lag_hip_route(const LagHipMoeDesc *d, const LagHipMoeWeights *w, 
 }
 
 // One decode step (sabrewing's moe_block over S tokens, device pointers):
-//   stage 1  router logits / scores / limbs + the shared expert's gate_up
-//   (S > 1 or E > 256: gate + top-k, and for S > 1 the counting sort)
-//   stage 2  routed gate_up (S == 1: routing fused) + the shared expert's down
+//   stage 1  router logits / scores / limbs, each token's gate + top-k by its
+//            last router block (E > 256: a gate + top-k launch after), and the
+//            shared expert's gate_up; for S > 1 then the counting sort
+//   stage 2  routed gate_up + the shared expert's down
 //   stage 3  S == 1: routed down fused with the rank-order combine;
 //            S > 1: grouped routed down into slots, then the combine
 extern "C" int lag_hip_moe_forward(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const float *x, float *out, int S) {
@@ -471,21 +482,26 @@ extern "C" int lag_hip_moe_forward(const LagHipMoeDesc *d, const LagHipMoeWeight
     const bool sh = d->shared_mode != 0;
     const uint16_t *sg = sh ? (const uint16_t *)w->sg : nullptr, *su = sh ? (const uint16_t *)w->su : nullptr;
     const uint16_t *sd = sh ? (const uint16_t *)w->sd : nullptr;
+    // E <= 256: one token's gate + top-k runs in every block of the expert stage
+    // (no device-scope handoff); several tokens' in the routing stage, each by
+    // its last router block; E > 256: a gate + top-k launch
+    const bool fused = E <= 256;
+    const bool in_route = fused && S > 1, in_experts = fused && S == 1;
+    if (in_route && ensure_cnt(S)) return -1;
     { PROF("stage_route");
       if (sw_launch_stage_route(g_st, w->router, d->router_bf16, x, S, D, E, w->logit_bias, f.logits, f.scores, d->route_act,
-                                f.xl, f.xs, sg, su, Is, f.shh)) return fail_msg("routing stage launch"); }
-    const bool fused = S == 1 && E <= 256;
+                                f.xl, f.xs, in_route ? (int *)g_cnt.p : nullptr, K, w->corr_bias, d->use_corr_bias,
+                                d->norm_topk, f.sel, f.w, sg, su, Is, f.shh)) return fail_msg("routing stage launch"); }
     if (!fused) {
         PROF("gate_topk");
         if (sw_launch_gate_topk(g_st, f.logits, f.scores, S, E, K, d->route_act, w->corr_bias, d->use_corr_bias,
                                 d->norm_topk, f.sel, f.w)) return fail_msg("gate/top-k launch");
     }
     if (S == 1) {                        // one token: its K picks in rank order, fused down + combine
-        SwGroups g = {f.sel, c_iota(), c_ones(), c_zeros(), nullptr, K, 0};
         { PROF("stage_experts");
-          if (sw_launch_stage_experts(g_st, gu, f.xl, f.xs, g, I, f.hl, f.hs,
-                                      fused ? (d->route_act == 1 ? f.logits : f.scores) : nullptr, E, K, d->route_act,
-                                      w->corr_bias, d->use_corr_bias, d->norm_topk, f.sel, f.w, sd, f.shh, S, Is, D, f.sout))
+          if (sw_launch_stage_experts(g_st, gu, f.xl, f.xs, SwGroups{}, I, f.hl, f.hs, f.sel, K,
+                                      in_experts ? (d->route_act == 1 ? f.logits : f.scores) : nullptr, E, d->route_act,
+                                      w->corr_bias, d->use_corr_bias, d->norm_topk, f.w, sd, f.shh, S, Is, D, f.sout))
               return fail_msg("expert stage launch"); }
         { PROF("q4_down_combine");
           if (sw_launch_q4_dot8_down_combine(g_st, dn, f.hl, f.hs, f.sel, f.w, K, d->route_scale, f.sout, out))
@@ -496,8 +512,8 @@ extern "C" int lag_hip_moe_forward(const LagHipMoeDesc *d, const LagHipMoeWeight
           if (sw_launch_bucket(g_st, f.sel, S, K, E, f.gexp, f.gbeg, f.gcnt, f.G, f.grow, f.rowof)) return fail_msg("bucket launch"); }
         SwGroups g = {f.gexp, f.gbeg, f.gcnt, f.grow, f.G, T < E ? T : E, 0};
         { PROF("stage_experts");
-          if (sw_launch_stage_experts(g_st, gu, f.xl, f.xs, g, I, f.hl, f.hs, nullptr, E, K, d->route_act, w->corr_bias,
-                                      d->use_corr_bias, d->norm_topk, f.sel, f.w, sd, f.shh, S, Is, D, f.sout))
+          if (sw_launch_stage_experts(g_st, gu, f.xl, f.xs, g, I, f.hl, f.hs, nullptr, K, nullptr, E, d->route_act,
+                                      w->corr_bias, d->use_corr_bias, d->norm_topk, f.w, sd, f.shh, S, Is, D, f.sout))
               return fail_msg("expert stage launch"); }
         SwGroups gd = g;
         gd.grow = nullptr;                 // the down reads the packed rows directly

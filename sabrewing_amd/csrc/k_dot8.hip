@@ -35,7 +35,6 @@
 // block b of kernel slot k writes its start and end (s_memrealtime, 100 MHz)
 // and hardware id to sw_trace[3 * (k * SW_TRACE_SLOT + b)].
 #ifdef SW_TRACE
-#define SW_TRACE_SLOT 16384
 static __device__ unsigned long long sw_trace[5 * SW_TRACE_SLOT * 3];
 #define TR_BEGIN() const unsigned long long tr_t0 = wall_clock64()
 #define TR_END(k)                                                                                  \
@@ -47,8 +46,7 @@ static __device__ unsigned long long sw_trace[5 * SW_TRACE_SLOT * 3];
             tp[2] = (unsigned long long)__smid() | ((unsigned long long)__builtin_amdgcn_s_getreg((20 << 0) | (0 << 6) | (3 << 11)) << 32); \
         }                                                                                          \
     } while (0)
-static __device__ unsigned long long sw_trace_mid[SW_TRACE_SLOT * 4];
-#define TR_MARK(i) do { if (threadIdx.x == 0 && blockIdx.x < SW_TRACE_SLOT) sw_trace_mid[blockIdx.x * 4 + (i)] = wall_clock64(); } while (0)
+#define TR_MARK(i) TR_MARKK(1, i)
 extern "C" int sw_trace_read(void *dst, size_t n) {
     return hipMemcpyFromSymbol(dst, HIP_SYMBOL(sw_trace), n) == hipSuccess ? 0 : -1;
 }
@@ -143,18 +141,18 @@ __host__ __device__ inline int dg_rps(int Gq, int cap, int nt) {
 #define DG_ROWS 64
 #define DG_TT 2               // tokens per weight pass in the grouped kernels
 #define DG_NT 512             // threads per gate_up block
-// Fused routing for one token (NP > 0): every block runs the token's gate +
-// top-k on its first wave (gate_topk_wave, deterministic, so every block gets
-// the same picks) while the others fetch the limbs; block (0, 0) also writes
-// the picks and weights out for the down projection.
+// One token (PICK = 1): block (rank a, set of outputs) takes pick a and
+// writes h of packed row a.  With NP = 0 the picks come in sel (from the
+// routing stage); with NP > 0 every block runs the token's gate + top-k on
+// its first wave (gate_topk_wave: deterministic, so every block gets the
+// same picks) while the others fetch the limbs, and block (0, 0) writes the
+// picks and weights to sel / w for the down projection.
 struct DotRoute {
     const float *src;          // the token's logits (act 1) or sigmoid/softplus scores
     const float *bias;         // selection bias (e_score_correction_bias) or null
     int E, K, act, use_bias, norm;
-    int *sel_out;
-    float *w_out;
+    float *w;
 };
-
 struct Dot8GluArgs {
     SwQ4 W;
     int gsh;
@@ -164,6 +162,7 @@ struct Dot8GluArgs {
     int I;
     sw_u32x4 *hl;
     float *hs;
+    int *sel;
     DotRoute rt;
 };
 
@@ -185,15 +184,14 @@ static int dg_pf_rows(int K) { const int n = 64 / dg_rps(run_lanes(K / RG), 64, 
 
 // block (bx = group or rank, by = set of 32 outputs); runs: the dynamic LDS,
 // [TT][DG_ROWS][NC] floats
-template <int PF, int NP, int TT, int C16>
+template <int PF, int PICK, int NP, int TT, int C16>
 __device__ __forceinline__ void dot8_glu_block(const Dot8GluArgs &A, int bx, int by, float *runs) {
-    static_assert(NP == 0 || TT == 1, "fused routing is one token");
+    static_assert(PICK == 0 || TT == 1, "picks are of one token");
     const SwQ4 W = A.W;
     const int I = A.I;
     const sw_u32x4 *__restrict__ xl = A.xl;
     const float *__restrict__ xs = A.xs;
     const SwGroups grp = A.grp;
-    const DotRoute rt = A.rt;
     const int K = W.K, G = K / RG, Gq = C16 ? G : run_lanes(G);
     const int CH = C16 ? CHG : (Gq < CHG ? Gq : CHG), NC = Gq / CH;
     const int RPS = dg_rps(Gq, 32, DG_NT), NSH = 32 / RPS;    // a row slot: NSH gate rows and NSH up rows
@@ -208,17 +206,21 @@ __device__ __forceinline__ void dot8_glu_block(const Dot8GluArgs &A, int bx, int
     int e, beg, cnt;
     sw_u32x4 X[TT][SW_NL];
     float xf[TT];
-    if constexpr (NP > 0) {                           // one token: rank gi of its picks
-        __shared__ TopkLDS tk;
+    if constexpr (PICK) {                             // one token: rank bx of its picks
         beg = bx; cnt = 1;
 #pragma unroll
         for (int l = 0; l < SW_NL; l++) X[0][l] = xl[(int64_t)g * SW_NL + l];
         xf[0] = xs[g];
-        if (tid < 64) gate_topk_wave<NP>(rt.src, rt.E, rt.K, rt.act, rt.bias, rt.use_bias, rt.norm, tk);
-        __syncthreads();
-        e = __builtin_amdgcn_readfirstlane(tk.sk[bx]);
+        if constexpr (NP > 0) {                       // the token's routing by the whole block
+            __shared__ TopkBlockLDS tk;
+            const DotRoute rt = A.rt;
+            gate_topk_block<DG_NT, NP>(rt.src, rt.E, rt.K, rt.act, rt.bias, rt.use_bias, rt.norm, tk);
+            e = __builtin_amdgcn_readfirstlane(tk.sk[bx]);
+            if (bx == 0 && by == 0 && tid < rt.K) { A.sel[tid] = tk.sk[tid]; rt.w[tid] = tk.wk[tid]; }
+        } else {
+            e = A.sel[bx];
+        }
         TR_MARK(0);
-        if (bx == 0 && by == 0 && tid < rt.K) { rt.sel_out[tid] = tk.sk[tid]; rt.w_out[tid] = tk.wk[tid]; }
     } else {
         const int gvalid = grp.G ? *grp.G : grp.ngroups_max;
         if (bx >= gvalid) return;
@@ -236,7 +238,7 @@ __device__ __forceinline__ void dot8_glu_block(const Dot8GluArgs &A, int bx, int
     float *myruns = runs + (roc * NSH) * NC + c;      // this lane's run sum of step s: myruns[(t*64 + h*32 + j) * NC]
     for (int t0 = 0; t0 < cnt; t0 += TT) {
         const int nt = min(TT, cnt - t0);
-        if constexpr (NP == 0) {
+        if constexpr (PICK == 0) {
 #pragma unroll
             for (int t = 0; t < TT; t++) {
                 const int pr = beg + t0 + (t < nt ? t : 0);
@@ -300,10 +302,10 @@ __device__ __forceinline__ void dot8_glu_block(const Dot8GluArgs &A, int bx, int
     }
 }
 
-template <int PF, int NP, int TT, int C16>
+template <int PF, int PICK, int TT, int C16>
 __global__ __launch_bounds__(DG_NT) void k_dot8_glu(Dot8GluArgs A) {
     extern __shared__ __align__(16) float red[];
-    dot8_glu_block<PF, NP, TT, C16>(A, blockIdx.x, blockIdx.y, red);
+    dot8_glu_block<PF, PICK, 0, TT, C16>(A, blockIdx.x, blockIdx.y, red);
 }
 
 // dispatch on the prefetch depth pf (1, 2, 4 or 8) and C16
@@ -321,12 +323,12 @@ static void dispatch_pf_c16(int pf, int c16, Args &&...args) {
         else L<1, 0>::go(args...);
     }
 }
-template <int NP, int TT>
+template <int PICK, int TT>
 struct GluL {
     template <int PF, int C16>
     struct L {
         static void go(dim3 grid, size_t lds, hipStream_t st, const Dot8GluArgs &A) {
-            hipLaunchKernelGGL((k_dot8_glu<PF, NP, TT, C16>), grid, dim3(DG_NT), lds, st, A);
+            hipLaunchKernelGGL((k_dot8_glu<PF, PICK, TT, C16>), grid, dim3(DG_NT), lds, st, A);
         }
     };
 };
@@ -341,24 +343,18 @@ int sw_launch_q4_dot8_glu(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, const floa
                           sw_u32x4 *hl, float *hs) {
     int gsh;
     if (dot8_glu_check(W, I, gsh) || g.ngroups_max <= 0) return -1;
-    const Dot8GluArgs A = {W, gsh, xl, xs, g, I, hl, hs, DotRoute{}};
+    const Dot8GluArgs A = {W, gsh, xl, xs, g, I, hl, hs, nullptr, DotRoute{}};
     dispatch_pf_c16<GluL<0, DG_TT>::L>(dg_pf_glu(W.K), dot8_c16(W.K), dim3((unsigned)g.ngroups_max, (unsigned)(I / 32)),
                                        dot8_glu_lds(W.K, DG_TT), st, A);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
-int sw_launch_q4_dot8_glu_routed(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, const float *xs, int I, sw_u32x4 *hl, float *hs,
-                                 const float *route_src, int E, int K, int act, const float *bias, int use_bias, int norm,
-                                 int *sel, float *w) {
+int sw_launch_q4_dot8_glu_picks(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, const float *xs, int I, sw_u32x4 *hl, float *hs,
+                                const int *sel, int K) {
     int gsh;
-    if (dot8_glu_check(W, I, gsh) || E <= 0 || E > 256 || K <= 0 || K > 64 || K > E) return -1;
-    const Dot8GluArgs A = {W, gsh, xl, xs, SwGroups{}, I, hl, hs, DotRoute{route_src, bias, E, K, act, use_bias, norm, sel, w}};
-    const dim3 grid((unsigned)K, (unsigned)(I / 32));
-    const size_t lds = dot8_glu_lds(W.K, 1);
-    const int pf = dg_pf_glu(W.K), c16 = dot8_c16(W.K);
-    if (E <= 64) dispatch_pf_c16<GluL<1, 1>::L>(pf, c16, grid, lds, st, A);
-    else if (E <= 128) dispatch_pf_c16<GluL<2, 1>::L>(pf, c16, grid, lds, st, A);
-    else dispatch_pf_c16<GluL<4, 1>::L>(pf, c16, grid, lds, st, A);
+    if (dot8_glu_check(W, I, gsh) || K <= 0 || K > 64 || !sel) return -1;
+    const Dot8GluArgs A = {W, gsh, xl, xs, SwGroups{}, I, hl, hs, const_cast<int *>(sel), DotRoute{}};
+    dispatch_pf_c16<GluL<1, 1>::L>(dg_pf_glu(W.K), dot8_c16(W.K), dim3((unsigned)K, (unsigned)(I / 32)), dot8_glu_lds(W.K, 1), st, A);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
@@ -608,93 +604,117 @@ static size_t lds_max(size_t a, size_t b) { return a > b ? a : b; }
 struct ShGluArgs { const uint16_t *Wg, *Wu; const float *x; int S, D, Is; float *h; };
 struct ShDownArgs { const uint16_t *Wd; const float *h; int S, Is, D; float *out; };
 
-template <int BF16, int TT>
+template <int BF16, int TT, int NP, int ONE>
 __global__ __launch_bounds__(SH_NT) void k_stage_route(RouterArgs R, int nbr, int S, ShGluArgs G) {
     extern __shared__ __align__(16) float smem[];
     TR_BEGIN();
     const int b = blockIdx.x;
-    if (b < nbr * S) router_block<BF16>(R, b % nbr, b / nbr, nbr, smem);
+    if (b < nbr * S) router_block<BF16, NP, ONE>(R, b % nbr, b / nbr, nbr, smem);
     else sh_glu_block<TT>(G.Wg, G.Wu, G.x, G.S, G.D, G.Is, G.h, b - nbr * S, smem);
     TR_END(0);
 }
 
 // TTG: tokens per pass of the routed gate_up; TTS: of the shared down
-template <int PF, int NP, int TTG, int TTS, int C16>
+template <int PF, int PICK, int NP, int TTG, int TTS, int C16>
 __global__ __launch_bounds__(DG_NT) void k_stage_experts(Dot8GluArgs A, int nbx, int nglu, ShDownArgs Sd) {
     extern __shared__ __align__(16) float smem[];
     TR_BEGIN();
     const int b = blockIdx.x;
-    if (b < nglu) dot8_glu_block<PF, NP, TTG, C16>(A, b % nbx, b / nbx, smem);
+    if (b < nglu) dot8_glu_block<PF, PICK, NP, TTG, C16>(A, b % nbx, b / nbx, smem);
     else sh_down_block<TTS>(Sd.Wd, Sd.h, Sd.S, Sd.Is, Sd.D, Sd.out, b - nglu, smem);
     TR_END(1);
 }
-template <int NP, int TTG, int TTS>
+template <int PICK, int NP, int TTG, int TTS>
 struct StageL {
     template <int PF, int C16>
     struct L {
         static void go(dim3 grid, size_t lds, hipStream_t st, const Dot8GluArgs &A, int nbx, int nglu, const ShDownArgs &Sd) {
-            hipLaunchKernelGGL((k_stage_experts<PF, NP, TTG, TTS, C16>), grid, dim3(DG_NT), lds, st, A, nbx, nglu, Sd);
+            hipLaunchKernelGGL((k_stage_experts<PF, PICK, NP, TTG, TTS, C16>), grid, dim3(DG_NT), lds, st, A, nbx, nglu, Sd);
         }
     };
 };
 
-// stage 1: sg may be null (no shared expert)
+template <int BF16, int TT, int ONE>
+static void launch_stage_route(int np, dim3 grid, size_t lds, hipStream_t st, const RouterArgs &R, int nbr, int S,
+                               const ShGluArgs &G) {
+    if (np == 0) hipLaunchKernelGGL((k_stage_route<BF16, TT, 0, ONE>), grid, dim3(SH_NT), lds, st, R, nbr, S, G);
+    else if (np == 1) hipLaunchKernelGGL((k_stage_route<BF16, TT, 1, ONE>), grid, dim3(SH_NT), lds, st, R, nbr, S, G);
+    else if (np == 2) hipLaunchKernelGGL((k_stage_route<BF16, TT, 2, ONE>), grid, dim3(SH_NT), lds, st, R, nbr, S, G);
+    else hipLaunchKernelGGL((k_stage_route<BF16, TT, 4, ONE>), grid, dim3(SH_NT), lds, st, R, nbr, S, G);
+}
+template <int TT, int ONE>
+static void launch_stage_route2(int bf16, int np, dim3 grid, size_t lds, hipStream_t st, const RouterArgs &R, int nbr,
+                                int S, const ShGluArgs &G) {
+    if (bf16) launch_stage_route<1, TT, ONE>(np, grid, lds, st, R, nbr, S, G);
+    else launch_stage_route<0, TT, ONE>(np, grid, lds, st, R, nbr, S, G);
+}
+
+// stage 1: router logits / scores and the limbs of x, the gate + top-k of
+// each token when cnt is non-null (E <= 256; picks to sel/w), and the shared
+// expert's gate_up when sg is non-null
 int sw_launch_stage_route(hipStream_t st, const void *Wc, int w_bf16, const float *x, int S, int D, int E,
                           const float *logit_bias, float *logits, float *scores, int route_act, sw_u32x4 *xl, float *xs,
+                          int *cnt, int K, const float *bias, int use_bias, int norm, int *sel, float *w,
                           const uint16_t *sg, const uint16_t *su, int Is, float *sh_h) {
     if (D % 128 || E <= 0 || S <= 0 || route_act < 0 || route_act > 2 || (route_act != 1 && !scores)) return -1;
+    if (cnt && (E > 256 || K <= 0 || K > 64 || K > E || !sel || !w)) return -1;
+    const int one = router_one(S, E);
     const size_t rl = router_lds(D);
-    if (rl > 65536) return -1;
-    const int nbr = (E + router_epb(SH_NT) - 1) / router_epb(SH_NT);
-    const RouterArgs R = {Wc, x, D, E, logit_bias, logits, route_act, scores, xl, xs};
+    if (rl > 65536 || D > 4 * RT_XB * (one ? SH_NT - 64 : SH_NT)) return -1;
+    const int nbr = (E + router_epb(one, SH_NT) - 1) / router_epb(one, SH_NT);
+    const RouterArgs R = {Wc, x, D, E, logit_bias, logits, route_act, scores, xl, xs, cnt, K, use_bias, norm, bias, sel, w};
     const ShGluArgs G = {sg, su, x, S, D, Is, sh_h};
     const int TT = S >= 2 ? SH_TT : 1;
     const int nsh = sg ? sh_glu_blocks(S, Is, TT) : 0;
     if (sg && (Is % SH_GLU_O || !sh_shape_ok(D))) return -1;
     const dim3 grid((unsigned)(nbr * S + nsh));
     const size_t lds = lds_max(rl, sg ? (TT == SH_TT ? sh_glu_lds<SH_TT>(D) : sh_glu_lds<1>(D)) : 0);
+    const int np = !cnt ? 0 : E <= 64 ? 1 : E <= 128 ? 2 : 4;
     if (TT == SH_TT) {
-        if (w_bf16) hipLaunchKernelGGL((k_stage_route<1, SH_TT>), grid, dim3(SH_NT), lds, st, R, nbr, S, G);
-        else hipLaunchKernelGGL((k_stage_route<0, SH_TT>), grid, dim3(SH_NT), lds, st, R, nbr, S, G);
+        if (one) launch_stage_route2<SH_TT, 1>(w_bf16, np, grid, lds, st, R, nbr, S, G);
+        else launch_stage_route2<SH_TT, 0>(w_bf16, np, grid, lds, st, R, nbr, S, G);
     } else {
-        if (w_bf16) hipLaunchKernelGGL((k_stage_route<1, 1>), grid, dim3(SH_NT), lds, st, R, nbr, S, G);
-        else hipLaunchKernelGGL((k_stage_route<0, 1>), grid, dim3(SH_NT), lds, st, R, nbr, S, G);
+        if (one) launch_stage_route2<1, 1>(w_bf16, np, grid, lds, st, R, nbr, S, G);
+        else launch_stage_route2<1, 0>(w_bf16, np, grid, lds, st, R, nbr, S, G);
     }
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
-// stage 2.  Routed gate_up for the groups g (route_src null), or for one token
-// with its routing fused (route_src = its logits or scores; g ignored; picks
-// to sel/w); plus the shared expert's down when sd is non-null.
+// stage 2.  Routed gate_up for the groups g (sel null), or for one token's K
+// picks: from sel (route_src null) or, with route_src (the token's logits or
+// scores), by a gate + top-k in every block, the picks and weights written to
+// sel / w; plus the shared expert's down when sd is non-null.
 int sw_launch_stage_experts(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, const float *xs, SwGroups g, int I, sw_u32x4 *hl,
-                            float *hs, const float *route_src, int E, int K, int act, const float *bias, int use_bias,
-                            int norm, int *sel, float *w, const uint16_t *sd, const float *sh_h, int S, int Is, int D,
+                            float *hs, int *sel, int K, const float *route_src, int E, int act, const float *bias,
+                            int use_bias, int norm, float *w, const uint16_t *sd, const float *sh_h, int S, int Is, int D,
                             float *sh_out) {
     int gsh;
     if (dot8_glu_check(W, I, gsh)) return -1;
-    const bool fused = route_src != nullptr;
-    if (fused && (S != 1 || E <= 0 || E > 256 || K <= 0 || K > 64 || K > E)) return -1;
-    if (!fused && g.ngroups_max <= 0) return -1;
+    const bool picks = sel != nullptr;
+    if (picks && (S != 1 || K <= 0 || K > 64)) return -1;
+    if (picks && route_src && (E <= 0 || E > 256 || K > E || !w)) return -1;
+    if (!picks && g.ngroups_max <= 0) return -1;
     if (sd && (D % SH_DN_O || !sh_shape_ok(Is))) return -1;
-    const int nbx = fused ? K : g.ngroups_max;
+    const int nbx = picks ? K : g.ngroups_max;
     const int nglu = nbx * (I / 32);
     const int TTS = S >= 2 ? SH_TT : 1;
     const int nsh = sd ? sh_down_blocks(S, D, TTS) : 0;
-    const DotRoute rt = fused ? DotRoute{route_src, bias, E, K, act, use_bias, norm, sel, w} : DotRoute{};
-    const Dot8GluArgs A = {W, gsh, xl, xs, g, I, hl, hs, rt};
+    const DotRoute rt = route_src ? DotRoute{route_src, bias, E, K, act, use_bias, norm, w} : DotRoute{};
+    const Dot8GluArgs A = {W, gsh, xl, xs, g, I, hl, hs, sel, rt};
     const ShDownArgs Sd = {sd, sh_h, S, Is, D, sh_out};
     const dim3 grid((unsigned)(nglu + nsh));
     const size_t shl = sd ? (TTS == SH_TT ? sh_down_lds<SH_TT>(Is) : sh_down_lds<1>(Is)) : 0;
     const int pf = dg_pf_glu(W.K), c16 = dot8_c16(W.K);
-    if (!fused) {
+    if (!picks) {
         const size_t lds = lds_max(dot8_glu_lds(W.K, DG_TT), shl);
-        if (TTS == SH_TT) dispatch_pf_c16<StageL<0, DG_TT, SH_TT>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd);
-        else dispatch_pf_c16<StageL<0, DG_TT, 1>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd);
+        if (TTS == SH_TT) dispatch_pf_c16<StageL<0, 0, DG_TT, SH_TT>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd);
+        else dispatch_pf_c16<StageL<0, 0, DG_TT, 1>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd);
     } else {
         const size_t lds = lds_max(dot8_glu_lds(W.K, 1), shl);
-        if (E <= 64) dispatch_pf_c16<StageL<1, 1, 1>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd);
-        else if (E <= 128) dispatch_pf_c16<StageL<2, 1, 1>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd);
-        else dispatch_pf_c16<StageL<4, 1, 1>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd);
+        if (!route_src) dispatch_pf_c16<StageL<1, 0, 1, 1>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd);
+        else if (E <= 64) dispatch_pf_c16<StageL<1, 1, 1, 1>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd);
+        else if (E <= 128) dispatch_pf_c16<StageL<1, 2, 1, 1>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd);
+        else dispatch_pf_c16<StageL<1, 4, 1, 1>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd);
     }
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }

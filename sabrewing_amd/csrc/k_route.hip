@@ -39,18 +39,20 @@ template <int NPER>   // expert slots per lane: E <= 64 * NPER
 __global__ __launch_bounds__(64) void k_gate_topk(const float *__restrict__ logits, const float *__restrict__ scores,
                                                   int E, int K, int act, const float *__restrict__ bias, int use_bias,
                                                   int norm, int *__restrict__ sel_all, float *__restrict__ w_all) {
-    __shared__ TopkLDS sh;
+    __shared__ uint64_t tab[32];
     const int lane = threadIdx.x, s = blockIdx.x;
-    gate_topk_wave<NPER>((act == 1 ? logits : scores) + (int64_t)s * E, E, K, act, bias, use_bias, norm, sh);
-    if (lane < K) { sel_all[(int64_t)s * K + lane] = sh.sk[lane]; w_all[(int64_t)s * K + lane] = sh.wk[lane]; }
+    int sk;
+    float wk;
+    gate_topk_wave<NPER>((act == 1 ? logits : scores) + (int64_t)s * E, E, K, act, bias, use_bias, norm, tab, sk, wk);
+    if (lane < K) { sel_all[(int64_t)s * K + lane] = sk; w_all[(int64_t)s * K + lane] = wk; }
 }
 
 #include "sw_router.h"
 
-template <int BF16>
-__global__ __launch_bounds__(256) void k_router_logits(RouterArgs R) {
+template <int BF16, int ONE>
+__global__ __launch_bounds__(512) void k_router_logits(RouterArgs R) {
     extern __shared__ __align__(16) float smem[];
-    router_block<BF16>(R, blockIdx.x, blockIdx.y, gridDim.x, smem);
+    router_block<BF16, 0, ONE>(R, blockIdx.x, blockIdx.y, gridDim.x, smem);
 }
 
 int sw_launch_router_topk(hipStream_t st, const void *Wc, int w_bf16, const float *x, int S, int D, int E,
@@ -59,13 +61,19 @@ int sw_launch_router_topk(hipStream_t st, const void *Wc, int w_bf16, const floa
                           sw_u32x4 *xl, float *xs) {
     if (D % 128 || D > 16384 || E <= 0 || E > TK_MAXE || S <= 0 || K <= 0 || K > 64 || K > E) return -1;
     if (route_act < 0 || route_act > 2 || (sel && route_act != 1 && !scores)) return -1;
-    // four experts per wave, four waves per block
-    const int nt = 256, epb = router_epb(nt);
-    if (router_lds(D) > 65536) return -1;
+    // four experts per block (wave 0; the others stage x) while that stays within 256 blocks,
+    // else four per wave of eight
+    const int nt = 512, one = router_one(S, E), epb = router_epb(one, nt);
+    if (router_lds(D) > 65536 || D > 4 * RT_XB * (one ? nt - 64 : nt)) return -1;
     dim3 grid((unsigned)((E + epb - 1) / epb), (unsigned)S);
-    const RouterArgs R = {Wc, x, D, E, logit_bias, logits, route_act, scores, xl, xs};
-    if (w_bf16) hipLaunchKernelGGL(k_router_logits<1>, grid, dim3(nt), router_lds(D), st, R);
-    else hipLaunchKernelGGL(k_router_logits<0>, grid, dim3(nt), router_lds(D), st, R);
+    const RouterArgs R = {Wc, x, D, E, logit_bias, logits, route_act, scores, xl, xs, nullptr, 0, 0, 0, nullptr, nullptr, nullptr};
+    if (one) {
+        if (w_bf16) hipLaunchKernelGGL((k_router_logits<1, 1>), grid, dim3(nt), router_lds(D), st, R);
+        else hipLaunchKernelGGL((k_router_logits<0, 1>), grid, dim3(nt), router_lds(D), st, R);
+    } else {
+        if (w_bf16) hipLaunchKernelGGL((k_router_logits<1, 0>), grid, dim3(nt), router_lds(D), st, R);
+        else hipLaunchKernelGGL((k_router_logits<0, 0>), grid, dim3(nt), router_lds(D), st, R);
+    }
     if (launch_err()) return -1;
     if (!sel) return 0;                              // logits only
     return sw_launch_gate_topk(st, logits, scores, S, E, K, route_act, corr_bias, use_corr_bias, norm_topk, sel, w);

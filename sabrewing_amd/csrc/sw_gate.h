@@ -21,14 +21,6 @@
 // lower id.
 #define TK_MAXE 1024
 
-struct TopkLDS {
-    float sc[TK_MAXE];
-    float wk[64];
-    int sk[64];
-    uint64_t tab[32];
-    float inv;
-};
-
 // LDS ordering between the lanes of one wave (its LDS operations run in order)
 __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -98,16 +90,21 @@ __device__ __forceinline__ uint32_t ord_f32(float f) {
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
+__device__ __forceinline__ float lanef(float v, int l) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+
 // The routing of one token, by the 64 lanes of one wave (no block barrier):
-// src is the token's logits (act == 1) or its sigmoid/softplus scores.
-// Leaves the picks in sh.sk[0..K) and their weights in sh.wk[0..K).
+// src is the token's logits (act == 1) or its sigmoid/softplus scores; tab is
+// 32 words of LDS for the expf table (softmax).  On return lane a < K holds
+// pick a (rank order) in sk and its weight in wk.
 template <int NPER>   // expert slots per lane: E <= 64 * NPER
 __device__ void gate_topk_wave(const float *__restrict__ src, int E, int K, int act, const float *__restrict__ bias,
-                               int use_bias, int norm, TopkLDS &sh) {
+                               int use_bias, int norm, uint64_t *tab, int &sk, float &wk) {
     const int lane = threadIdx.x & 63;
     float v[NPER], b[NPER];
     // every load of the token issued before any is used (clamped indices)
-    if (act == 1 && lane < 32) sh.tab[lane] = sw_exp2f_tab[lane];
+    if (act == 1 && lane < 32) tab[lane] = sw_exp2f_tab[lane];
     const bool hasb = use_bias && bias;
 #pragma unroll
     for (int i = 0; i < NPER; i++) {
@@ -115,6 +112,7 @@ __device__ void gate_topk_wave(const float *__restrict__ src, int E, int K, int 
         v[i] = src[e];
         b[i] = hasb ? bias[e] : 0.f;
     }
+    TR_MARKK(0, 4);
     if (act == 1) {                                   // softmax
         wave_sync();
         float mx = -__builtin_inff();
@@ -128,30 +126,15 @@ __device__ void gate_topk_wave(const float *__restrict__ src, int E, int K, int 
         const float r0 = __shfl(v[0], 0);
         if (r0 != r0) mx = r0;                        // a NaN in slot 0 propagates, as in the scan
 #pragma unroll
-        for (int i = 0; i < NPER; i++) {
-            const int e = lane + 64 * i;
-            if (e < E) sh.sc[e] = sw_expf_t(v[i] - mx, sh.tab);
-        }
-        wave_sync();
-        if (lane == 0) {
-            double sum = 0.0;
-            for (int e = 0; e < E; e++) sum += (double)sh.sc[e];
-            sh.inv = (float)(1.0 / sum);
-        }
-        wave_sync();
-        const float inv = sh.inv;
+        for (int i = 0; i < NPER; i++) v[i] = sw_expf_t(v[i] - mx, tab);
+        double sum = 0.0;                             // in expert order, in double (every lane the same)
 #pragma unroll
-        for (int i = 0; i < NPER; i++) {
-            const int e = lane + 64 * i;
-            if (e < E) v[i] = sh.sc[e] * inv;
-        }
-    }
+        for (int i = 0; i < NPER; i++)
+            for (int l = 0; l < 64 && l + 64 * i < E; l++) sum += (double)lanef(v[i], l);
+        const float inv = (float)(1.0 / sum);
 #pragma unroll
-    for (int i = 0; i < NPER; i++) {
-        const int e = lane + 64 * i;
-        if (e < E) sh.sc[e] = v[i];
+        for (int i = 0; i < NPER; i++) v[i] = v[i] * inv;
     }
-    wave_sync();
     uint32_t ko[NPER];                                // order key, 0 = invalid or taken (valid keys order above 0)
     bool fr[NPER];
 #pragma unroll
@@ -161,6 +144,8 @@ __device__ void gate_topk_wave(const float *__restrict__ src, int E, int K, int 
         fr[i] = e < E;
         ko[i] = (e < E && key > -1e30f) ? ord_f32(key) : 0u;
     }
+    TR_MARKK(0, 5);
+    sk = 0; wk = 0.f;
     for (int a = 0; a < K; a++) {
         uint32_t lm = ko[0];
 #pragma unroll
@@ -181,20 +166,131 @@ __device__ void gate_topk_wave(const float *__restrict__ src, int E, int K, int 
             }
             if (bi >= E) bi = 0;
         }
-        if ((bi & 63) == lane) {
+        const int slot = bi >> 6, bl = bi & 63;       // uniform
+        float vs = v[0];
+#pragma unroll
+        for (int i = 1; i < NPER; i++)
+            if (i == slot) vs = v[i];
+        const float wb = lanef(vs, bl);               // the pick's weight: its unbiased score
+        if (lane == bl) {
 #pragma unroll
             for (int i = 0; i < NPER; i++)
-                if (i == (bi >> 6)) { ko[i] = 0u; fr[i] = false; }
+                if (i == slot) { ko[i] = 0u; fr[i] = false; }
         }
-        if (lane == 0) { sh.sk[a] = bi; sh.wk[a] = sh.sc[bi]; }
+        if (lane == a) { sk = bi; wk = wb; }
     }
-    wave_sync();
-    if (lane == 0 && norm) {
+    TR_MARKK(0, 6);
+    if (norm) {                                       // renormalised: summed in rank order
         float sm = 0.f;
-        for (int a = 0; a < K; a++) sm += sh.wk[a];
-        for (int a = 0; a < K; a++) sh.wk[a] = sh.wk[a] / sm;
+        for (int a = 0; a < K; a++) sm += lanef(wk, a);
+        wk = wk / sm;
     }
-    wave_sync();
+}
+
+// The same routing by a whole block of NT threads (E <= NT), by counting
+// instead of K dependent passes.  Expert e gets the 64-bit word (order bits of
+// key + 0.0, ~e) when its key is valid (> -1e30; a NaN is not) and (0, ~e)
+// when not, so a larger word means a larger key, equal keys go to the lower
+// id and the invalid experts come last in id order -- the order in which the
+// K passes of moe_topk, with their all-invalid fallback to the lowest
+// unselected id, pick -- and pick a is the expert with exactly a larger
+// words.  On return the picks and weights (renormalised if norm) are in
+// sh.sk[0..K), sh.wk[0..K).
+struct TopkBlockLDS {
+    uint64_t key[256];
+    float val[256];
+    int part[512];
+    int sk[64];
+    float wk[64];
+    uint64_t tab[32];
+};
+template <int NT, int NPER>   // NPER: E <= 64 NPER (the softmax by one wave)
+__device__ void gate_topk_block(const float *__restrict__ src, int E, int K, int act, const float *__restrict__ bias,
+                                int use_bias, int norm, TopkBlockLDS &sh) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    float v = 0.f, b = 0.f;
+    if (tid < E) {
+        v = src[tid];
+        b = (use_bias && bias) ? bias[tid] : 0.f;
+    }
+    TR_MARKK(1, 3);
+    if (act == 1) {                                   // softmax on wave 0, the scan's expressions
+        if (tid < 32) sh.tab[tid] = sw_exp2f_tab[tid];
+        if (tid < E) sh.val[tid] = v;
+        __syncthreads();
+        if (tid < 64) {
+            float p[NPER];
+#pragma unroll
+            for (int i = 0; i < NPER; i++) p[i] = sh.val[min(lane + 64 * i, E - 1)];
+            float mx = -__builtin_inff();
+            bool any = false;
+#pragma unroll
+            for (int i = 0; i < NPER; i++) {
+                const int e = lane + 64 * i;
+                if (e < E && p[i] == p[i]) { mx = any ? fmaxf(mx, p[i]) : p[i]; any = true; }
+            }
+            for (int o = 32; o; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+            const float r0 = __shfl(p[0], 0);
+            if (r0 != r0) mx = r0;                    // a NaN in slot 0 propagates, as in the scan
+#pragma unroll
+            for (int i = 0; i < NPER; i++) p[i] = sw_expf_t(p[i] - mx, sh.tab);
+            double sum = 0.0;                         // in expert order, in double
+#pragma unroll
+            for (int i = 0; i < NPER; i++)
+                for (int l = 0; l < 64 && l + 64 * i < E; l++) sum += (double)lanef(p[i], l);
+            const float inv = (float)(1.0 / sum);
+#pragma unroll
+            for (int i = 0; i < NPER; i++) {
+                const int e = lane + 64 * i;
+                if (e < E) sh.val[e] = p[i] * inv;
+            }
+        }
+        __syncthreads();
+        if (tid < E) v = sh.val[tid];
+    }
+    uint64_t mykey = 0ull;
+    if (tid < E) {
+        const float key = v + b;
+        const uint32_t lo = 0xFFFFFFFFu - (uint32_t)tid;
+        mykey = key > -1e30f ? (((uint64_t)ord_f32(key) << 32) | lo) : (uint64_t)lo;
+        sh.key[tid] = mykey;
+        sh.val[tid] = v;
+    }
+    __syncthreads();
+    TR_MARKK(1, 4);
+    // H threads per expert, each counting the larger words in its E/H of them
+    const int H = NT / E, per = (E + H - 1) / H;
+    const int e = tid % E, h = tid / E;
+    if (h < H) {
+        const uint64_t kk = sh.key[e];
+        const int j0 = h * per, j1 = min(E, j0 + per);
+        int c = 0, jj = j0;
+        for (; jj + 8 <= j1; jj += 8) {               // eight words read together
+            uint64_t w8[8];
+#pragma unroll
+            for (int q = 0; q < 8; q++) w8[q] = sh.key[jj + q];
+#pragma unroll
+            for (int q = 0; q < 8; q++) c += w8[q] > kk ? 1 : 0;
+        }
+        for (; jj < j1; jj++) c += sh.key[jj] > kk ? 1 : 0;
+        sh.part[h * E + e] = c;
+    }
+    __syncthreads();
+    TR_MARKK(1, 5);
+    if (tid < E) {
+        int rank = 0;
+        for (int hh = 0; hh < H; hh++) rank += sh.part[hh * E + tid];
+        if (rank < K) { sh.sk[rank] = tid; sh.wk[rank] = v; }
+    }
+    __syncthreads();
+    TR_MARKK(1, 6);
+    if (tid < 64 && norm) {                           // renormalised: summed in rank order
+        float wk = tid < K ? sh.wk[tid] : 0.f;
+        float sm = 0.f;
+        for (int a = 0; a < K; a++) sm += lanef(wk, a);
+        if (tid < K) sh.wk[tid] = wk / sm;
+    }
+    __syncthreads();
 }
 
 // ------------------------------------------------------------ limbs ----

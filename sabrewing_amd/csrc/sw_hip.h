@@ -40,6 +40,16 @@ typedef float sw_f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t sw_u32x4 __attribute__((ext_vector_type(4)));
 
 #ifdef __HIPCC__
+// Mid-block timestamps of the decode kernels, for a build with -DSW_TRACE only:
+// TR_MARKK(k, i) stores s_memrealtime of thread 0 of block b into slot
+// (k, b, i) of sw_trace_mid (one definition per translation unit).
+#ifdef SW_TRACE
+#define SW_TRACE_SLOT 16384
+static __device__ unsigned long long sw_trace_mid[2 * SW_TRACE_SLOT * 8];
+#define TR_MARKK(k, i) do { if (threadIdx.x == 0 && blockIdx.x < SW_TRACE_SLOT) sw_trace_mid[((k) * SW_TRACE_SLOT + blockIdx.x) * 8 + (i)] = wall_clock64(); } while (0)
+#else
+#define TR_MARKK(k, i)
+#endif
 // Raw buffer access: a tensor is one descriptor (base and byte extent in
 // scalar registers); each lane adds a 32-bit offset and each step a scalar
 // one; a load past the extent returns 0 and touches no memory.
@@ -120,12 +130,9 @@ int sw_launch_limbs(hipStream_t st, const float *x, int rows, int K, sw_u32x4 *x
 // output h as limbs hl[packed row][I/32][SW_NL], hs[packed row][I/32]
 int sw_launch_q4_dot8_glu(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, const float *xs, SwGroups g, int I,
                           sw_u32x4 *hl, float *hs);
-// the same for one token with its routing fused in (every block runs the
-// gate + top-k of route_src, the token's logits (act 1) or scores); the picks
-// and weights are written to sel[K], w[K]
-int sw_launch_q4_dot8_glu_routed(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, const float *xs, int I, sw_u32x4 *hl, float *hs,
-                                 const float *route_src, int E, int K, int act, const float *bias, int use_bias, int norm,
-                                 int *sel, float *w);
+// the same for one token's K picks sel (block row a: expert sel[a], packed row a)
+int sw_launch_q4_dot8_glu_picks(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, const float *xs, int I, sw_u32x4 *hl, float *hs,
+                                const int *sel, int K);
 // Y[packed row, O] f32 for every group, input as limbs (the grouped down projection)
 int sw_launch_q4_dot8_rows(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, const float *xs, SwGroups g, float *Y);
 // the dot8 down projection fused with the rank-order combine for one token
@@ -139,16 +146,19 @@ int sw_launch_q4_down_combine(hipStream_t st, SwQ4 W, const _Float16 *hplanes, c
 // out[s] (+)= route_scale * sum_a w[s,a] * slots[rowof[s,a]] (+ shared[s])
 int sw_launch_combine(hipStream_t st, const float *slots, const int *rowof, const float *w, int S, int K, int D,
                       float route_scale, const float *shared, float *out, int accumulate);
-// fused decode stages (k_dot8.hip): stage 1 = router logits/scores/limbs +
-// the shared expert's gate_up (sg null: none); stage 2 = routed gate_up
-// (route_src non-null: one token, routing fused, picks to sel/w) + the
-// shared expert's down (sd null: none)
+// fused decode stages (k_dot8.hip): stage 1 = router logits/scores/limbs,
+// each token's gate + top-k by its last router block (cnt non-null: S zeroed
+// arrival counters, E <= 256; picks to sel/w) and the shared expert's gate_up
+// (sg null: none); stage 2 = routed gate_up (sel non-null: one token's K
+// picks, from sel or, with route_src, by a gate + top-k in every block; else
+// the groups g) + the shared expert's down (sd null: none)
 int sw_launch_stage_route(hipStream_t st, const void *Wc, int w_bf16, const float *x, int S, int D, int E,
                           const float *logit_bias, float *logits, float *scores, int route_act, sw_u32x4 *xl, float *xs,
+                          int *cnt, int K, const float *bias, int use_bias, int norm, int *sel, float *w,
                           const uint16_t *sg, const uint16_t *su, int Is, float *sh_h);
 int sw_launch_stage_experts(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, const float *xs, SwGroups g, int I, sw_u32x4 *hl,
-                            float *hs, const float *route_src, int E, int K, int act, const float *bias, int use_bias,
-                            int norm, int *sel, float *w, const uint16_t *sd, const float *sh_h, int S, int Is, int D,
+                            float *hs, int *sel, int K, const float *route_src, int E, int act, const float *bias,
+                            int use_bias, int norm, float *w, const uint16_t *sd, const float *sh_h, int S, int Is, int D,
                             float *sh_out);
 // the shared expert on the VALU (sw_shared.h): h[S, Is] = silu(Wg x) * (Wu x)
 // and out[S, D] = Wd h, bf16 weights, f32 activations

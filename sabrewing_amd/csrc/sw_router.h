@@ -16,13 +16,13 @@
 // slices, slice q holding the next P elements (8 bf16 or 4 f32) of each of
 // its 64 chains, so one 16-byte load per lane reads one slice, contiguous,
 // and gives each lane the next P elements of its own chain; RT_PF slices are
-// in flight (half of a D = 4096 bf16 chain, issued before the block's other
+// in flight (all of a D = 4096 bf16 chain, issued before the block's other
 // traffic); a bf16 weight widens exactly to f32; x is
 // staged transposed in LDS once per block, so chain j reads x[16m + j] as
 // xt[j][m]; the tree is four shuffles within each 16-lane row.  The chain is
 // M = D/16 dependent fmas per lane, the critical path of the routing.
-#define RT_PF 16
-#define RT_XB 8           // x float4 loads in flight per thread
+#define RT_PF 32
+#define RT_XB 8           // x float4 loads per thread: D <= 4 * RT_XB * threads
 struct RouterArgs {
     const void *Wc;            // router in the streaming order (k_chain_major)
     const float *x;            // [S, D]
@@ -33,11 +33,25 @@ struct RouterArgs {
     float *scores;             // [S, E] sigmoid / softplus scores (act != 1) or null
     sw_u32x4 *xl;              // dot8 limbs of x, or null
     float *xs;
+    // gate + top-k by the last router block of each token (cnt non-null):
+    // cnt[s] counts the token's finished blocks (0 between launches; the last
+    // block resets it), picks and weights to sel/w [S, K]
+    int *cnt;
+    int K, use_bias, norm;
+    const float *bias;         // selection bias (e_score_correction_bias) or null
+    int *sel;
+    float *w;
 };
-// experts per block of nt threads
-__host__ __device__ inline int router_epb(int nt) { return 4 * (nt / 64); }
-// block bx (of nbx per token) of token s; smem: the dynamic LDS (router_lds bytes)
-template <int BF16>
+// experts per router block of nt threads: 4 (ONE: wave 0 runs the chains,
+// the other waves stage x -- the router spread over as many CUs as there are
+// groups of 4 experts) or 4 per wave
+__host__ __device__ inline int router_epb(int one, int nt) { return one ? 4 : 4 * (nt / 64); }
+// ONE while the blocks of S tokens stay within 256
+__host__ inline int router_one(int S, int E) { return (int64_t)S * ((E + 3) / 4) <= 256; }
+
+// block bx (of nbx per token) of token s; smem: the dynamic LDS (router_lds
+// bytes); NP > 0: E <= 64 NP and the token's gate + top-k by its last block
+template <int BF16, int NP, int ONE>
 __device__ __forceinline__ void router_block(const RouterArgs &R, int bx, int s, int nbx, float *smem) {
     constexpr int P = BF16 ? 8 : 4;
     __shared__ uint64_t tab[32];                     // expf table for the sigmoid / softplus scores
@@ -47,8 +61,9 @@ __device__ __forceinline__ void router_block(const RouterArgs &R, int bx, int s,
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = nt >> 6;
     const int M = D / 16, ML = M + 4, NQ = M / P;
     const int j = lane & 15;
-    const int eg = bx * nw + wave, e = eg * 4 + (lane >> 4);
-    const bool valid = e < E;
+    const bool chain = ONE ? wave == 0 : true;        // uniform per wave
+    const int eg = ONE ? bx : bx * nw + wave, e = eg * 4 + (lane >> 4);
+    const bool valid = chain && e < E;
     // slice q of this lane: byte voff + 1024 q of the router (groups past the last: clamp)
     const int ng4 = (E + 3) / 4;
     const int egc = eg < ng4 ? eg : ng4 - 1;
@@ -56,37 +71,50 @@ __device__ __forceinline__ void router_block(const RouterArgs &R, int bx, int s,
     const uint32_t voff = ((uint32_t)egc * NQ * 64 + lane) * 16;
     auto slice = [&](int q) { return sw_ld16(rw, voff, (uint32_t)min(q, NQ - 1) * 1024u); };
     float *xt = smem;                                 // [16][ML]
-    sw_u32x4 ring[RT_PF];
+    const float *xr = x + (int64_t)s * D;
+    const int nx4 = D / 4;
+    // x staged transposed into LDS, xt[k % 16][k / 16], by xs threads from thread x0: one pass
+    // of unconditional loads (clamped; D <= 4 * RT_XB * xs), so no loop or branch join at
+    // which the wait counts would drain slices in flight
+    const int xs = ONE ? nt - 64 : nt, x0 = ONE ? 64 : 0, xt_id = tid - x0;
+    auto stage_x_load = [&](sw_f32x4 *xv) {
 #pragma unroll
-    for (int u = 0; u < RT_PF; u++) ring[u] = slice(u);
-    if (tid < 32) tab[tid] = sw_exp2f_tab[tid];
-    if (R.xl) {                                       // the token's dot8 limbs, half a wave per group
-        const int G = D / SW_RG;
-        for (int g = bx * 2 * nw + (tid >> 5); g < G; g += nbx * 2 * nw)
-            limbs_group(x[(int64_t)s * D + g * SW_RG + (tid & 31)], tid & 31, R.xl + ((int64_t)s * G + g) * SW_NL,
-                        R.xs + (int64_t)s * G + g);
-    }
-    {
-        const float *xr = x + (int64_t)s * D;
-        const int nx4 = D / 4;
-        for (int i0 = 0; i0 < nx4; i0 += RT_XB * nt) {
-            sw_f32x4 xv[RT_XB];
+        for (int u = 0; u < RT_XB; u++) xv[u] = *(const sw_f32x4 *)(xr + 4 * min(u * xs + xt_id, nx4 - 1));
+    };
+    auto stage_x_store = [&](const sw_f32x4 *xv) {
 #pragma unroll
-            for (int u = 0; u < RT_XB; u++) xv[u] = *(const sw_f32x4 *)(xr + 4 * min(i0 + u * nt + tid, nx4 - 1));
+        for (int u = 0; u < RT_XB; u++) {
+            const int i4 = u * xs + xt_id;
+            if (i4 < nx4) {
 #pragma unroll
-            for (int u = 0; u < RT_XB; u++) {
-                const int i4 = i0 + u * nt + tid;
-                if (i4 < nx4) {
-#pragma unroll
-                    for (int c = 0; c < 4; c++) {
-                        const int k = 4 * i4 + c;
-                        xt[(k & 15) * ML + (k >> 4)] = xv[u][c];
-                    }
+                for (int c = 0; c < 4; c++) {
+                    const int k = 4 * i4 + c;
+                    xt[(k & 15) * ML + (k >> 4)] = xv[u][c];
                 }
             }
         }
+    };
+    const uint64_t tabv = sw_exp2f_tab[lane & 31];  // stored after the chain, where the scores need it
+    sw_u32x4 ring[RT_PF];
+    if constexpr (ONE) {
+        if (wave == 0) {
+#pragma unroll
+            for (int u = 0; u < RT_PF; u++) ring[u] = slice(u);
+        } else {
+            sw_f32x4 xv[RT_XB];
+            stage_x_load(xv);
+            stage_x_store(xv);
+        }
+    } else {
+        sw_f32x4 xv[RT_XB];
+        stage_x_load(xv);                             // x first, then every slice of the ring
+#pragma unroll
+        for (int u = 0; u < RT_PF; u++) ring[u] = slice(u);
+        stage_x_store(xv);
     }
+    TR_MARKK(0, 7);
     __syncthreads();
+    TR_MARKK(0, 0);
     const float *xj = xt + j * ML;
     float acc = 0.f;
     auto chain4 = [&](int q, const sw_u32x4 &w) {
@@ -110,20 +138,32 @@ __device__ __forceinline__ void router_block(const RouterArgs &R, int bx, int s,
             acc = __builtin_fmaf(xa.w, wf.w, acc);
         }
     };
-    // full rounds with unconditional refills (a refill past the end re-reads the last slice),
-    // then the last round without: no ring rotation, loads stay in flight across rounds
-    int q0 = 0;
-    for (; q0 + RT_PF < NQ; q0 += RT_PF) {
-#pragma unroll
-        for (int u = 0; u < RT_PF; u++) {          // the slot is consumed before its refill
-            chain4(q0 + u, ring[u]);
-            ring[u] = slice(q0 + u + RT_PF);
-            __builtin_amdgcn_sched_barrier(0);        // keep the refill here, not sunk to the round's end
+    if (ONE && !chain && R.xl) {                      // the limbs by the staging waves while wave 0 chains
+        const int G = D / SW_RG, hw = (tid - 64) >> 5, nhw = 2 * (nw - 1);
+        for (int g = bx * nhw + hw; g < G; g += nbx * nhw) {
+            const int k = g * SW_RG + (tid & 31);
+            limbs_group(xt[(k & 15) * ML + (k >> 4)], tid & 31, R.xl + ((int64_t)s * G + g) * SW_NL, R.xs + (int64_t)s * G + g);
         }
     }
+    if (chain) {
+        // full rounds with unconditional refills (a refill past the end re-reads the last
+        // slice), then the last round without: no ring rotation, loads stay in flight
+        int q0 = 0;
+        for (; q0 + RT_PF < NQ; q0 += RT_PF) {
 #pragma unroll
-    for (int u = 0; u < RT_PF; u++)
-        if (q0 + u < NQ) chain4(q0 + u, ring[u]);
+            for (int u = 0; u < RT_PF; u++) {         // the slot is consumed before its refill
+                chain4(q0 + u, ring[u]);
+                ring[u] = slice(q0 + u + RT_PF);
+                __builtin_amdgcn_sched_barrier(0);    // keep the refill here, not sunk to the round's end
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < RT_PF; u++)
+            if (q0 + u < NQ) chain4(q0 + u, ring[u]);
+    }
+    TR_MARKK(0, 1);
+    tab[lane & 31] = tabv;                            // every wave writes the whole table (equal values)
+    wave_sync();
     float v = acc;
     v = v + __shfl_down(v, 8, 16);
     v = v + __shfl_down(v, 4, 16);
@@ -134,6 +174,40 @@ __device__ __forceinline__ void router_block(const RouterArgs &R, int bx, int s,
         R.logits[(int64_t)s * E + e] = v;
         if (act != 1 && R.scores)
             R.scores[(int64_t)s * E + e] = (act == 2) ? sw_softplus_ref_t(v, tab) : sw_sigmoid_ref_t(v, tab);
+    }
+    if (!ONE && R.xl) {                               // the token's dot8 limbs, half a wave per group, from xt
+        const int G = D / SW_RG;
+        for (int g = bx * 2 * nw + (tid >> 5); g < G; g += nbx * 2 * nw) {
+            const int k = g * SW_RG + (tid & 31);
+            limbs_group(xt[(k & 15) * ML + (k >> 4)], tid & 31, R.xl + ((int64_t)s * G + g) * SW_NL, R.xs + (int64_t)s * G + g);
+        }
+    }
+    if constexpr (NP > 0) {
+        // the last of the token's nbx blocks routes it: every block publishes its
+        // logits (device-scope release, then one arrival count); the block that
+        // counts last acquires them all and runs the gate + top-k on one wave
+        __shared__ int last;
+        __threadfence();
+        __syncthreads();
+        if (tid == 0) last = atomicAdd(R.cnt + s, 1) == nbx - 1;
+        __syncthreads();
+        TR_MARKK(0, 2);
+        if (last) {
+            __threadfence();
+            TR_MARKK(0, 3);
+            if (tid < 64) {
+                int sk;
+                float wk;
+                gate_topk_wave<NP>((act == 1 ? R.logits : R.scores) + (int64_t)s * E, E, R.K, act, R.bias, R.use_bias,
+                                   R.norm, tab, sk, wk);
+                if (tid < R.K) {
+                    R.sel[(int64_t)s * R.K + tid] = sk;
+                    R.w[(int64_t)s * R.K + tid] = wk;
+                }
+                if (tid == 0) R.cnt[s] = 0;
+            }
+            TR_MARKK(0, 7);
+        }
     }
 }
 __host__ inline size_t router_lds(int D) { return (size_t)16 * (D / 16 + 4) * 4; }

@@ -121,7 +121,7 @@ __host__ __device__ inline int sh_nc(int K) { return K / SH_RG < SH_CHG ? 1 : ru
 // shared expert gate_up: SH_GLU_O outputs i per block; local rows 0..O-1 are
 // gate rows i0.., rows O..2O-1 the up rows; h[tok][i] = silu(gate) * up (f32)
 #define SH_NT 512              // threads per block of the shared-expert jobs
-#define SH_GLU_O 4
+#define SH_GLU_O 8
 template <int TT>
 __device__ __forceinline__ void sh_glu_block(const uint16_t *__restrict__ Wg, const uint16_t *__restrict__ Wu,
                                              const float *__restrict__ x, int S, int D, int Is, float *__restrict__ h,
