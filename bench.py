@@ -196,9 +196,17 @@ def run(args):
             v["GBs"] = kb[k] / (v["avg_us"] * 1e-6) / 1e9
     dom = max(kern, key=lambda k: kern[k]["avg_us"] * kern[k]["launches"])
     dk = kern[dom]
+    # HBM bytes per launch of that kernel as rocprofv3 counted them (FETCH_SIZE x2 + WRITE_SIZE,
+    # calibrated on a device copy; profiles/decode_kernels_*.md), when a profile covers this workload
+    traffic = None
+    try:
+        with open(os.path.join(ROOT, "profiles", "traffic.json")) as f:
+            traffic = json.load(f).get(cfg.name, {}).get(str(B), {}).get(dom, {}).get("traffic_bytes")
+    except (OSError, ValueError):
+        pass
     layer_bytes = cfg.step_bytes(B, G)
     roof = {"bound": "hbm", "kernel": dom, "achieved": round(dk.get("GBs", 0.0), 1), "peak": HBM_PEAK_GBS,
-            "unit": "GB/s", "frac": round(dk.get("GBs", 0.0) / HBM_PEAK_GBS, 4), "traffic": None,
+            "unit": "GB/s", "frac": round(dk.get("GBs", 0.0) / HBM_PEAK_GBS, 4), "traffic": traffic,
             "bytes_per_launch": dk.get("bytes"), "avg_launch_us": round(dk["avg_us"], 2)}
     layer_gbs = layer_bytes / (ms * 1e-3) / 1e9
     log("kernels:", json.dumps({k: {kk: (round(vv, 2) if isinstance(vv, float) else vv) for kk, vv in v.items()}

@@ -72,18 +72,26 @@ static void prof_flush(void) {
     }
     g_pending.clear();
 }
-// bracket one launch with events when profiling
+thread_local SwLaunchEvents *sw_launch_events = nullptr;
+// Time one launch when profiling: kernels launched through SW_LAUNCH carry the
+// scope's events themselves (dispatch to end); otherwise the events are
+// recorded on the stream around the scope.
 struct ProfScope {
-    Pending p; bool on; hipStream_t st;
+    Pending p; bool on; hipStream_t st; SwLaunchEvents le;
     ProfScope(const char *name, hipStream_t s) : on(g_prof != 0 && !g_capturing), st(s) {
         if (!on) return;
         p.rec = prof_rec(name); p.a = ev_get(); p.b = ev_get();
         if (!p.a || !p.b) { on = false; return; }
-        (void)hipEventRecord(p.a, st);
+        le = {p.a, p.b, 0};
+        sw_launch_events = &le;
     }
     ~ProfScope() {
         if (!on) return;
-        (void)hipEventRecord(p.b, st);
+        sw_launch_events = nullptr;
+        if (!le.started) {                              // no kernel took the events: time the scope on the stream
+            (void)hipEventRecord(p.a, st);
+            (void)hipEventRecord(p.b, st);
+        }
         g_pending.push_back(p);
         if (g_pending.size() > 4096) prof_flush();
     }

@@ -76,7 +76,7 @@ __global__ __launch_bounds__(256) void k_limbs(const float *__restrict__ x, int 
 int sw_launch_limbs(hipStream_t st, const float *x, int rows, int K, sw_u32x4 *xl, float *xs) {
     if (K % RG || rows <= 0) return -1;
     const int G = K / RG;
-    hipLaunchKernelGGL(k_limbs, dim3((unsigned)((G + 7) / 8), (unsigned)rows), dim3(256), 0, st, x, K, rows, xl, xs);
+    SW_LAUNCH(k_limbs, dim3((unsigned)((G + 7) / 8), (unsigned)rows), dim3(256), 0, st, x, K, rows, xl, xs);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
@@ -328,7 +328,7 @@ struct GluL {
     template <int PF, int C16>
     struct L {
         static void go(dim3 grid, size_t lds, hipStream_t st, const Dot8GluArgs &A) {
-            hipLaunchKernelGGL((k_dot8_glu<PF, PICK, TT, C16>), grid, dim3(DG_NT), lds, st, A);
+            SW_LAUNCH((k_dot8_glu<PF, PICK, TT, C16>), grid, dim3(DG_NT), lds, st, A);
         }
     };
 };
@@ -468,7 +468,7 @@ __global__ __launch_bounds__(256) void k_dot8_rows(Dot8RowsArgs A) {
 template <int PF, int C16>
 struct RowsL {
     static void go(dim3 grid, size_t lds, hipStream_t st, const Dot8RowsArgs &A) {
-        hipLaunchKernelGGL((k_dot8_rows<PF, DG_TT, C16>), grid, dim3(256), lds, st, A);
+        SW_LAUNCH((k_dot8_rows<PF, DG_TT, C16>), grid, dim3(256), lds, st, A);
     }
 };
 
@@ -586,8 +586,8 @@ int sw_launch_q4_dot8_down_combine(hipStream_t st, SwQ4 W, const sw_u32x4 *hl, c
     const size_t lds = (size_t)K * DC_RB * dot8_nc(I) * 4;
     const int threads = (K * run_lanes(G) + 63) / 64 * 64;
     const Dot8DownArgs A = {W, gsh, hl, hs, sel, w, K, route_scale, shared, out};
-    if (dot8_c16(I)) hipLaunchKernelGGL(k_dot8_down_combine<1>, dim3((unsigned)(W.O / DC_RB)), dim3(threads), lds, st, A);
-    else hipLaunchKernelGGL(k_dot8_down_combine<0>, dim3((unsigned)(W.O / DC_RB)), dim3(threads), lds, st, A);
+    if (dot8_c16(I)) SW_LAUNCH(k_dot8_down_combine<1>, dim3((unsigned)(W.O / DC_RB)), dim3(threads), lds, st, A);
+    else SW_LAUNCH(k_dot8_down_combine<0>, dim3((unsigned)(W.O / DC_RB)), dim3(threads), lds, st, A);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
@@ -629,7 +629,7 @@ struct StageL {
     template <int PF, int C16>
     struct L {
         static void go(dim3 grid, size_t lds, hipStream_t st, const Dot8GluArgs &A, int nbx, int nglu, const ShDownArgs &Sd) {
-            hipLaunchKernelGGL((k_stage_experts<PF, PICK, NP, TTG, TTS, C16>), grid, dim3(DG_NT), lds, st, A, nbx, nglu, Sd);
+            SW_LAUNCH((k_stage_experts<PF, PICK, NP, TTG, TTS, C16>), grid, dim3(DG_NT), lds, st, A, nbx, nglu, Sd);
         }
     };
 };
@@ -637,10 +637,10 @@ struct StageL {
 template <int BF16, int TT, int ONE>
 static void launch_stage_route(int np, dim3 grid, size_t lds, hipStream_t st, const RouterArgs &R, int nbr, int S,
                                const ShGluArgs &G) {
-    if (np == 0) hipLaunchKernelGGL((k_stage_route<BF16, TT, 0, ONE>), grid, dim3(SH_NT), lds, st, R, nbr, S, G);
-    else if (np == 1) hipLaunchKernelGGL((k_stage_route<BF16, TT, 1, ONE>), grid, dim3(SH_NT), lds, st, R, nbr, S, G);
-    else if (np == 2) hipLaunchKernelGGL((k_stage_route<BF16, TT, 2, ONE>), grid, dim3(SH_NT), lds, st, R, nbr, S, G);
-    else hipLaunchKernelGGL((k_stage_route<BF16, TT, 4, ONE>), grid, dim3(SH_NT), lds, st, R, nbr, S, G);
+    if (np == 0) SW_LAUNCH((k_stage_route<BF16, TT, 0, ONE>), grid, dim3(SH_NT), lds, st, R, nbr, S, G);
+    else if (np == 1) SW_LAUNCH((k_stage_route<BF16, TT, 1, ONE>), grid, dim3(SH_NT), lds, st, R, nbr, S, G);
+    else if (np == 2) SW_LAUNCH((k_stage_route<BF16, TT, 2, ONE>), grid, dim3(SH_NT), lds, st, R, nbr, S, G);
+    else SW_LAUNCH((k_stage_route<BF16, TT, 4, ONE>), grid, dim3(SH_NT), lds, st, R, nbr, S, G);
 }
 template <int TT, int ONE>
 static void launch_stage_route2(int bf16, int np, dim3 grid, size_t lds, hipStream_t st, const RouterArgs &R, int nbr,

@@ -571,10 +571,10 @@ static int pick_pf(int nssq, int pfmax = PF_MAX) {
 template <int FMT, int EPI, int KSPLIT, int XSRC, int CH>
 static void launch_pf(int pf, dim3 grid, size_t shm, hipStream_t st, const GemmArgs &a) {
     switch (pf) {
-    case 8: hipLaunchKernelGGL((k_gemm<FMT, EPI, KSPLIT, XSRC, FMT == FMT_BF16 ? 4 : 8, CH>), grid, dim3(256), shm, st, a); break;
-    case 4: hipLaunchKernelGGL((k_gemm<FMT, EPI, KSPLIT, XSRC, 4, CH>), grid, dim3(256), shm, st, a); break;
-    case 2: hipLaunchKernelGGL((k_gemm<FMT, EPI, KSPLIT, XSRC, 2, CH>), grid, dim3(256), shm, st, a); break;
-    default: hipLaunchKernelGGL((k_gemm<FMT, EPI, KSPLIT, XSRC, 1, CH>), grid, dim3(256), shm, st, a); break;
+    case 8: SW_LAUNCH((k_gemm<FMT, EPI, KSPLIT, XSRC, FMT == FMT_BF16 ? 4 : 8, CH>), grid, dim3(256), shm, st, a); break;
+    case 4: SW_LAUNCH((k_gemm<FMT, EPI, KSPLIT, XSRC, 4, CH>), grid, dim3(256), shm, st, a); break;
+    case 2: SW_LAUNCH((k_gemm<FMT, EPI, KSPLIT, XSRC, 2, CH>), grid, dim3(256), shm, st, a); break;
+    default: SW_LAUNCH((k_gemm<FMT, EPI, KSPLIT, XSRC, 1, CH>), grid, dim3(256), shm, st, a); break;
     }
 }
 
@@ -652,10 +652,10 @@ int sw_launch_q4_down_combine(hipStream_t st, SwQ4 W, const _Float16 *hplanes, c
     if (lds > 65536) return -1;
     const dim3 grid((unsigned)(W.O / 16)), block(nw * 64);
     switch (pick_pf(W.K / 128)) {
-    case 8: hipLaunchKernelGGL(k_q4_down_combine<8>, grid, block, lds, st, W, gsh, hplanes, sel, w, K, route_scale, shared, out); break;
-    case 4: hipLaunchKernelGGL(k_q4_down_combine<4>, grid, block, lds, st, W, gsh, hplanes, sel, w, K, route_scale, shared, out); break;
-    case 2: hipLaunchKernelGGL(k_q4_down_combine<2>, grid, block, lds, st, W, gsh, hplanes, sel, w, K, route_scale, shared, out); break;
-    default: hipLaunchKernelGGL(k_q4_down_combine<1>, grid, block, lds, st, W, gsh, hplanes, sel, w, K, route_scale, shared, out); break;
+    case 8: SW_LAUNCH(k_q4_down_combine<8>, grid, block, lds, st, W, gsh, hplanes, sel, w, K, route_scale, shared, out); break;
+    case 4: SW_LAUNCH(k_q4_down_combine<4>, grid, block, lds, st, W, gsh, hplanes, sel, w, K, route_scale, shared, out); break;
+    case 2: SW_LAUNCH(k_q4_down_combine<2>, grid, block, lds, st, W, gsh, hplanes, sel, w, K, route_scale, shared, out); break;
+    default: SW_LAUNCH(k_q4_down_combine<1>, grid, block, lds, st, W, gsh, hplanes, sel, w, K, route_scale, shared, out); break;
     }
     return launch_err();
 }

@@ -170,14 +170,14 @@ __global__ __launch_bounds__(256) void k_gen_q4_row(uint8_t *q, float *s, uint64
 
 int sw_launch_gen_normal(hipStream_t st, float *out, int64_t n, uint64_t seed, uint64_t offset, double sigma, int to_bf16) {
     if (n <= 0) return 0;
-    hipLaunchKernelGGL(k_gen_normal, dim3((unsigned)sw_imin64((n + 255) / 256, 65536)), dim3(256), 0, st, out, n, seed,
+    SW_LAUNCH(k_gen_normal, dim3((unsigned)sw_imin64((n + 255) / 256, 65536)), dim3(256), 0, st, out, n, seed,
                        offset, sigma, to_bf16);
     return launch_err();
 }
 
 int sw_launch_gen_bf16(hipStream_t st, uint16_t *out, int64_t n, uint64_t seed, uint64_t offset, double sigma) {
     if (n <= 0) return 0;
-    hipLaunchKernelGGL(k_gen_bf16, dim3((unsigned)sw_imin64((n + 255) / 256, 65536)), dim3(256), 0, st, out, n, seed,
+    SW_LAUNCH(k_gen_bf16, dim3((unsigned)sw_imin64((n + 255) / 256, 65536)), dim3(256), 0, st, out, n, seed,
                        offset, sigma);
     return launch_err();
 }
@@ -188,12 +188,12 @@ int sw_launch_gen_q4(hipStream_t st, uint8_t *q, float *s, uint64_t seed, double
     if (gs > 0) {
         if (gs % 2 || K % gs || gs > 128) return -1;
         const int64_t n = nrows * (K / gs);
-        hipLaunchKernelGGL(k_gen_q4_group, dim3((unsigned)sw_imin64((n + 255) / 256, 65536)), dim3(256), 0, st, q, s, seed,
+        SW_LAUNCH(k_gen_q4_group, dim3((unsigned)sw_imin64((n + 255) / 256, 65536)), dim3(256), 0, st, q, s, seed,
                            sigma, row0, nrows, K, gs);
     } else {
         for (int64_t r0 = 0; r0 < nrows; r0 += 65536) {
             const int64_t nr = sw_imin64(65536, nrows - r0);
-            hipLaunchKernelGGL(k_gen_q4_row, dim3((unsigned)nr), dim3(256), 0, st, q + r0 * (K / 2), s + r0, seed, sigma,
+            SW_LAUNCH(k_gen_q4_row, dim3((unsigned)nr), dim3(256), 0, st, q + r0 * (K / 2), s + r0, seed, sigma,
                                row0 + r0, K);
         }
     }

@@ -29,7 +29,7 @@ __global__ void k_chain_major(const void *__restrict__ W, int w_bf16, int E, int
 int sw_launch_chain_major(hipStream_t st, const void *W, int w_bf16, int E, int D, void *Wc) {
     if (D % 128 || E <= 0) return -1;
     const int64_t n = (int64_t)((E + 3) / 4) * 4 * D;
-    hipLaunchKernelGGL(k_chain_major, dim3((unsigned)sw_imin64((n + 255) / 256, 8192)), dim3(256), 0, st, W, w_bf16, E, D, Wc);
+    SW_LAUNCH(k_chain_major, dim3((unsigned)sw_imin64((n + 255) / 256, 8192)), dim3(256), 0, st, W, w_bf16, E, D, Wc);
     return launch_err();
 }
 
@@ -68,11 +68,11 @@ int sw_launch_router_topk(hipStream_t st, const void *Wc, int w_bf16, const floa
     dim3 grid((unsigned)((E + epb - 1) / epb), (unsigned)S);
     const RouterArgs R = {Wc, x, D, E, logit_bias, logits, route_act, scores, xl, xs, nullptr, 0, 0, 0, nullptr, nullptr, nullptr};
     if (one) {
-        if (w_bf16) hipLaunchKernelGGL((k_router_logits<1, 1>), grid, dim3(nt), router_lds(D), st, R);
-        else hipLaunchKernelGGL((k_router_logits<0, 1>), grid, dim3(nt), router_lds(D), st, R);
+        if (w_bf16) SW_LAUNCH((k_router_logits<1, 1>), grid, dim3(nt), router_lds(D), st, R);
+        else SW_LAUNCH((k_router_logits<0, 1>), grid, dim3(nt), router_lds(D), st, R);
     } else {
-        if (w_bf16) hipLaunchKernelGGL((k_router_logits<1, 0>), grid, dim3(nt), router_lds(D), st, R);
-        else hipLaunchKernelGGL((k_router_logits<0, 0>), grid, dim3(nt), router_lds(D), st, R);
+        if (w_bf16) SW_LAUNCH((k_router_logits<1, 0>), grid, dim3(nt), router_lds(D), st, R);
+        else SW_LAUNCH((k_router_logits<0, 0>), grid, dim3(nt), router_lds(D), st, R);
     }
     if (launch_err()) return -1;
     if (!sel) return 0;                              // logits only
@@ -84,7 +84,7 @@ int sw_launch_gate_topk(hipStream_t st, const float *logits, const float *scores
     if (E <= 0 || E > TK_MAXE || S <= 0 || K <= 0 || K > 64 || K > E || route_act < 0 || route_act > 2) return -1;
     if (route_act != 1 && !scores) return -1;
     const int nper = (E + 63) / 64;
-#define SW_GATE(NP) hipLaunchKernelGGL(k_gate_topk<NP>, dim3((unsigned)S), dim3(64), 0, st, logits, scores, E, K, route_act, \
+#define SW_GATE(NP) SW_LAUNCH(k_gate_topk<NP>, dim3((unsigned)S), dim3(64), 0, st, logits, scores, E, K, route_act, \
                                        corr_bias, use_corr_bias, norm_topk, sel, w)
     if (nper <= 1) SW_GATE(1);
     else if (nper <= 2) SW_GATE(2);
@@ -170,7 +170,7 @@ __global__ __launch_bounds__(BK_THREADS) void k_bucket(const int *__restrict__ s
 int sw_launch_bucket(hipStream_t st, const int *sel, int S, int K, int E, int *gexp, int *gbeg,
                      int *gcnt, int *G, int *grow, int *rowof) {
     if (E <= 0 || E > BK_MAXE || S <= 0 || K <= 0) return -1;
-    hipLaunchKernelGGL(k_bucket, dim3(1), dim3(BK_THREADS), 0, st, sel, S * K, K, E, gexp, gbeg, gcnt, G, grow, rowof);
+    SW_LAUNCH(k_bucket, dim3(1), dim3(BK_THREADS), 0, st, sel, S * K, K, E, gexp, gbeg, gcnt, G, grow, rowof);
     return launch_err();
 }
 
@@ -225,7 +225,7 @@ int sw_launch_combine(hipStream_t st, const float *slots, const int *rowof, cons
                       float route_scale, const float *shared, float *out, int accumulate) {
     if (D % 4 || S <= 0) return -1;
     const int64_t n4 = (int64_t)S * (D / 4);
-    hipLaunchKernelGGL(k_combine, dim3((unsigned)sw_imin64((n4 + 255) / 256, 4096)), dim3(256), 0, st, slots, rowof, w,
+    SW_LAUNCH(k_combine, dim3((unsigned)sw_imin64((n4 + 255) / 256, 4096)), dim3(256), 0, st, slots, rowof, w,
                        S, K, D, route_scale, shared, out, accumulate);
     return launch_err();
 }
@@ -261,7 +261,7 @@ __global__ void k_selftest_libm(float *out, const float *xin, int n) {
 }
 
 int sw_launch_selftest(hipStream_t st, float *out, const float *xin, int n) {
-    hipLaunchKernelGGL(k_selftest_mfma, dim3(1), dim3(64), 0, st, out);
-    if (n > 0) hipLaunchKernelGGL(k_selftest_libm, dim3((unsigned)sw_imin64((n + 255) / 256, 4096)), dim3(256), 0, st, out, xin, n);
+    SW_LAUNCH(k_selftest_mfma, dim3(1), dim3(64), 0, st, out);
+    if (n > 0) SW_LAUNCH(k_selftest_libm, dim3((unsigned)sw_imin64((n + 255) / 256, 4096)), dim3(256), 0, st, out, xin, n);
     return launch_err();
 }

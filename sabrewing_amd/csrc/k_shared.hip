@@ -21,17 +21,17 @@ __global__ __launch_bounds__(SH_NT) void k_sh_down(const uint16_t *__restrict__ 
 int sw_launch_sh_glu(hipStream_t st, const uint16_t *Wg, const uint16_t *Wu, const float *x, int S, int D, int Is, float *h) {
     if (S <= 0 || Is % SH_GLU_O || !sh_shape_ok(D)) return -1;
     if (S >= 2)
-        hipLaunchKernelGGL(k_sh_glu<SH_TT>, dim3((unsigned)sh_glu_blocks(S, Is, SH_TT)), dim3(SH_NT), sh_glu_lds<SH_TT>(D), st, Wg, Wu, x, S, D, Is, h);
+        SW_LAUNCH(k_sh_glu<SH_TT>, dim3((unsigned)sh_glu_blocks(S, Is, SH_TT)), dim3(SH_NT), sh_glu_lds<SH_TT>(D), st, Wg, Wu, x, S, D, Is, h);
     else
-        hipLaunchKernelGGL(k_sh_glu<1>, dim3((unsigned)sh_glu_blocks(S, Is, 1)), dim3(SH_NT), sh_glu_lds<1>(D), st, Wg, Wu, x, S, D, Is, h);
+        SW_LAUNCH(k_sh_glu<1>, dim3((unsigned)sh_glu_blocks(S, Is, 1)), dim3(SH_NT), sh_glu_lds<1>(D), st, Wg, Wu, x, S, D, Is, h);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
 int sw_launch_sh_down(hipStream_t st, const uint16_t *Wd, const float *h, int S, int Is, int D, float *out) {
     if (S <= 0 || D % SH_DN_O || !sh_shape_ok(Is)) return -1;
     if (S >= 2)
-        hipLaunchKernelGGL(k_sh_down<SH_TT>, dim3((unsigned)sh_down_blocks(S, D, SH_TT)), dim3(SH_NT), sh_down_lds<SH_TT>(Is), st, Wd, h, S, Is, D, out);
+        SW_LAUNCH(k_sh_down<SH_TT>, dim3((unsigned)sh_down_blocks(S, D, SH_TT)), dim3(SH_NT), sh_down_lds<SH_TT>(Is), st, Wd, h, S, Is, D, out);
     else
-        hipLaunchKernelGGL(k_sh_down<1>, dim3((unsigned)sh_down_blocks(S, D, 1)), dim3(SH_NT), sh_down_lds<1>(Is), st, Wd, h, S, Is, D, out);
+        SW_LAUNCH(k_sh_down<1>, dim3((unsigned)sh_down_blocks(S, D, 1)), dim3(SH_NT), sh_down_lds<1>(Is), st, Wd, h, S, Is, D, out);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }

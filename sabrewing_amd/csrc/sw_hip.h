@@ -40,6 +40,23 @@ typedef float sw_f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t sw_u32x4 __attribute__((ext_vector_type(4)));
 
 #ifdef __HIPCC__
+#include <hip/hip_ext.h>
+// Per-launch timing for the profile scopes of the backend: while a scope is
+// open (sw_launch_events non-null), SW_LAUNCH records the scope's start event
+// at the first kernel's dispatch and its stop event at each kernel's end
+// (hipExtLaunchKernelGGL), so the pair times the kernels themselves.
+struct SwLaunchEvents { hipEvent_t start, stop; int started; };
+extern thread_local SwLaunchEvents *sw_launch_events;
+#define SW_LAUNCH(kernel, grid, block, lds, st, ...)                                                              \
+    do {                                                                                                          \
+        if (sw_launch_events) {                                                                                   \
+            hipExtLaunchKernelGGL(kernel, grid, block, lds, st, sw_launch_events->started ? nullptr : sw_launch_events->start, \
+                                  sw_launch_events->stop, 0, __VA_ARGS__);                                        \
+            sw_launch_events->started = 1;                                                                        \
+        } else {                                                                                                  \
+            hipLaunchKernelGGL(kernel, grid, block, lds, st, __VA_ARGS__);                                        \
+        }                                                                                                         \
+    } while (0)
 // Mid-block timestamps of the decode kernels, for a build with -DSW_TRACE only:
 // TR_MARKK(k, i) stores s_memrealtime of thread 0 of block b into slot
 // (k, b, i) of sw_trace_mid (one definition per translation unit).
