@@ -1,0 +1,102 @@
+"""Golden vectors of the MoE-block path, made by the compiled reference.
+
+    python tests/golden/make_golden.py        # needs oracle/_ref (built from /root/reference)
+
+Writes one .npz per case into this directory:
+  - kat_q4_rows.npz: the int4 known-answer case of the reference's backend test
+    (c/tests/test_backend_cuda.cu:42,105-110): rows [-8,-1,0,7] and [1,2,3,4]
+    packed low nibble first, scales {1, 0.25}, x[0:4] of that test, result
+    {-34, -2.5}; evaluated again here by the compiled reference's matmul_q4_k
+    (F32 and exact modes).
+  - moe_<case>.npz: a seeded small layer of each contract.  The layer is not
+    stored: its seeds are, and oracle/synth.py regenerates it bit for bit.
+    Stored: the config, the seeds, the token rows x, the residual out0, and the
+    reference's results -- router logits (the SIMD contract of
+    c/moe_matmul.h:25-43 / :92-110), the top-k picks over the gate scores
+    (c/moe_block.h:115-122 + c/moe_arch.h:64-89), and the layer output of
+    moe_block over every row (c/moe_block.h:18-54).
+
+Only the compiled reference computes what is stored; the restatement under
+oracle/ is used for nothing but regenerating the seeded weights.
+"""
+import os
+import sys
+
+from dataclasses import replace
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+sys.path.insert(0, ROOT)
+
+from oracle import synth                      # noqa: E402
+from oracle.oracle import Oracle, Ref         # noqa: E402
+from sabrewing_amd import configs as cf       # noqa: E402
+
+# (base config, scaled shape, seed, rows, corr-bias sigma)
+CASES = {
+    "c1_small": (cf.C1, dict(D=256, E=16, K=4, I=128), 101, 4, 0.0),
+    "c2_sigmoid_small": (cf.C2_SIGMOID, dict(D=256, E=32, K=6, I=128, Is=128), 102, 4, 0.01),
+    "c5_small": (cf.C5_LAYER, dict(D=256, E=32, K=8, I=384), 103, 4, 0.0),
+    "c2_sigmoid_mid": (cf.C2_SIGMOID, dict(D=1024, E=64, K=8, I=256, Is=256), 104, 2, 0.01),
+    "c4_zipf_sigmoid_small": (replace(cf.C2_SIGMOID, zipf=1.1), dict(D=256, E=64, K=10, I=128, Is=128),
+                              106, 4, 0.01),
+}
+# The reference's moe_block takes sigmoid or softmax gates only (c/moe_block.h:26,
+# c/moe_arch.h route_act); a softplus gate has no reference output to store.
+
+
+def ref_scores(ref, cfg, logits):
+    """Gate scores as c/moe_block.h:115-122 forms them, from the reference's own
+    softmax_row / softplusf / expf."""
+    if cfg.route_act == cf.ROUTE_SOFTMAX:
+        return ref.softmax_row(logits)
+    e = np.array([ref.lib.ref_expf(float(-v)) for v in logits], np.float32)
+    return (np.float32(1) / (np.float32(1) + e)).astype(np.float32)
+
+
+def case_config(name):
+    base, shape, seed, rows, cb = CASES[name]
+    return cf.scaled(base, **shape), seed, rows, cb
+
+
+def main():
+    if not Ref.available("avx512"):
+        raise SystemExit("oracle/_ref is not built (make -C oracle ref, with /root/reference present)")
+    ref = Ref("avx512")
+    orc = Oracle()
+
+    # the backend test's int4 known answer, evaluated by the compiled reference
+    x = np.array([[1, -2, 3, -4]], np.float32)
+    q4 = np.array([0x70, 0xF8, 0xA9, 0xCB], np.uint8)
+    s4 = np.array([1.0, 0.25], np.float32)
+    want = np.array([[-34.0, -2.5]], np.float32)
+    got_f32 = ref.matmul_q4(x, q4.reshape(2, 2), s4, 0, 0)
+    got_exact = ref.matmul_q4(x, q4.reshape(2, 2), s4, 0, 1)
+    assert np.array_equal(got_f32, want) and np.array_equal(got_exact, want), (got_f32, got_exact)
+    np.savez(os.path.join(HERE, "kat_q4_rows.npz"), x=x, q4=q4, s4=s4, want=want)
+
+    for name in CASES:
+        cfg, seed, rows, cb = case_config(name)
+        L = synth.make_layer(orc, cfg, seed, corr_bias_sigma=cb)
+        d = synth.desc_of(cfg)
+        xr = synth.make_x(orc, cfg, seed, rows)
+        out0 = synth.make_x(orc, cfg, seed + 1, rows)
+        out = ref.moe_block_rows(d, L, xr, out0)
+        if cfg.router_bf16:
+            logits = ref.matmul_bf16(xr, L.router, 0)
+        else:
+            logits = ref.matmul_f32(xr, L.router, 0)
+        if L.logit_bias is not None:
+            logits = logits + L.logit_bias
+        bias = L.corr_bias if cfg.use_corr_bias else None
+        sel = np.stack([ref.topk(ref_scores(ref, cfg, logits[s]), cfg.K, bias) for s in range(rows)])
+        np.savez(os.path.join(HERE, f"moe_{name}.npz"), seed=np.int64(seed), rows=np.int64(rows),
+                 corr_bias_sigma=np.float64(cb), x=xr, out0=out0, logits=logits.astype(np.float32),
+                 sel=sel.astype(np.int32), out=out)
+        print(f"{name}: out {out.shape}, logits {logits.shape}, sel {sel.shape}")
+
+
+if __name__ == "__main__":
+    main()
