@@ -10,18 +10,20 @@
 // sum_{l=1..NL} d_l 8^-l with signed digits d_l in [-8, 7] (round to nearest,
 // clamp, carry the exact remainder), so
 //     x ~= 2^(e - 3 NL) * D,   D = sum_l d_l 8^(NL - l)   (|error| <= 2^e 8^-NL).
+// With NL = 7, |D| <= 8 (8^7 - 1) / 7 < 2^21.2 and the input error is at most
+// 2^e 8^-7 (~2.4e-7 of the group's largest input, a few f32 ulps).
 // For one weight row and one group, sum_k (n_k - 8) D_k is an exact int32
-// (Horner over the limbs: acc = (acc << 3) + four dot8), turned into f32 once
-// (|acc| < 2^24, exact) and multiplied by s_row,group * 2^(e - 3 NL) (exact
-// power-of-two scaling of the weight scale).  A row's output is then the sum
+// (Horner over the limbs: acc = (acc << 3) + four dot8; |acc| <= 32 * 8 *
+// 2^21.2 < 2^29.2), turned into f32 once (correctly rounded, the same in every
+// launch) and multiplied by s_row,group * 2^(e - 3 NL) (exact power-of-two
+// scaling of the weight scale).  A row's output is then the sum
 // of its group terms in the fixed order of run_sum (sw_gate.h): runs of up to
 // 16 groups, each summed by a butterfly across the lanes holding them, the
 // run sums left to right.  Nothing of it depends on which tokens share a
 // launch, so grouped and per-token results are bit-identical.
 //
-// Per weight byte this is ~2 VALU ops (XOR, dot8, shift over NL = 5 limbs,
-// one fma per 32 weights) against ~3.3 for nibble-to-f16 dequant plus MFMA,
-// and each wave load is 1 KB of one row, contiguous.
+// Per weight dword this is one XOR and NL dot8 (plus NL - 1 shift-adds and one
+// fma per 32 weights), and each wave load is 1 KB of one row, contiguous.
 #include "sw_hip.h"
 #include "sw_libm.h"
 #include "sw_gate.h"
@@ -82,7 +84,8 @@ int sw_launch_limbs(hipStream_t st, const float *x, int rows, int K, sw_u32x4 *x
 
 // exact int32 sum_k (n_k - 8) D_k over one group: a = the group's 16 weight
 // bytes with every nibble XOR 8 (signed nibbles n - 8); the NL limb dots are
-// independent chains, joined by Horner (every partial sum is exact)
+// independent chains, joined by Horner (every partial sum is exact and below
+// 2^29.2 in magnitude)
 __device__ __forceinline__ int dot8_group(sw_u32x4 a, const sw_u32x4 *X) {
     int p[SW_NL];
 #pragma unroll

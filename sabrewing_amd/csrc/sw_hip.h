@@ -141,7 +141,7 @@ int sw_launch_bf16_rows(hipStream_t st, SwBf16 W, const uint16_t *planes, int S,
 int sw_launch_bf16_rows_x(hipStream_t st, SwBf16 W, const float *x, int S, float *Y);
 // activation limbs for the dot8 GEMV (k_dot8.hip): rows x[rows, K] f32 ->
 // xl[rows][K/32][SW_NL] (32 signed nibbles each), xs[rows][K/32] f32
-#define SW_NL 5
+#define SW_NL 7
 int sw_launch_limbs(hipStream_t st, const float *x, int rows, int K, sw_u32x4 *xl, float *xs);
 // SiLU-GLU(gate, up) for every packed row of every group, on the dot8 unit;
 // output h as limbs hl[packed row][I/32][SW_NL], hs[packed row][I/32]

@@ -155,3 +155,21 @@ def test_graph_replay_matches_eager(be, orc, S_):
         for b in (xd, oe, og):
             b.free()
         dl.free()
+
+
+@pytest.mark.parametrize("S_", [2, 33, 200])
+def test_device_bucket_matches_oracle(be, orc, S_):
+    """the device counting sort (A11): groups in ascending expert id, begin
+    offsets and counts equal to the CPU sort of the same picks"""
+    cfg = SMALL[4]
+    L = synth.make_layer(orc, cfg, 61)
+    dl = DeviceLayer.from_host(be, cfg, L)
+    x = synth.make_x(orc, cfg, 62, S_)
+    xd, od = be.upload(x), be.upload(np.zeros_like(x))
+    be.moe_forward(desc_of(cfg), dl.weights(), xd, od, S_)
+    G, gexp, gbeg, gcnt = be.last_groups()
+    _, sel, _ = be.route(desc_of(cfg), dl.weights(), xd, S_)
+    xd.free(); od.free(); dl.free()
+    Gw, gexp_w, gbeg_w, gcnt_w, _, _ = orc.bucket(sel, S_, cfg.K, cfg.E)
+    assert G == Gw
+    assert np.array_equal(gexp, gexp_w) and np.array_equal(gbeg, gbeg_w) and np.array_equal(gcnt, gcnt_w)
