@@ -295,3 +295,34 @@ class RefLaguna:
             np.ascontiguousarray(x, np.float32), h, x.shape[0], exact, group)
         assert rc == 0
         return h
+
+
+class RefLagunaHip:
+    """The reference Laguna engine's lag_moe_rows built with -DCOLI_CUDA and
+    linked against libsabrewing_loader.so (oracle/_ref/libref_laguna_hip.so):
+    the engine's own batched driver calling this backend through lag_cuda_*."""
+
+    def __init__(self):
+        self.lib = C.CDLL(os.path.join(HERE, "_ref", "libref_laguna_hip.so"))
+        f = self.lib.ref_laguna_moe_rows_dev
+        f.restype = C.c_int
+        f.argtypes = ([C.c_int] * 3 + [C.c_float] + [C.c_int] * 3 + [C.c_void_p] * 2 + [C.c_void_p] * 4
+                      + [C.c_void_p] * 3 + [C.c_void_p] * 7 + [F32P, F32P, C.c_int, C.c_int])
+
+    @staticmethod
+    def available():
+        return os.path.exists(os.path.join(HERE, "_ref", "libref_laguna_hip.so"))
+
+    def moe_rows(self, desc, layer, dev, x, h, group=1):
+        """dev: device pointers (ints) gu_q, gu_s, dn_q, dn_s, sg, su, sd"""
+        assert layer.gs == 0 and not layer.router_bf16
+        h = np.ascontiguousarray(h, np.float32).copy()
+        rc = self.lib.ref_laguna_moe_rows_dev(
+            desc.E, desc.K, desc.norm_topk, desc.route_scale, layer.D, layer.I, layer.Is,
+            _ptr(layer.router), _ptr(layer.corr_bias),
+            _ptr(layer.gu_q), _ptr(layer.gu_s), _ptr(layer.dn_q), _ptr(layer.dn_s),
+            _ptr(layer.sg), _ptr(layer.su), _ptr(layer.sd),
+            *[C.c_void_p(int(p)) for p in dev],
+            np.ascontiguousarray(x, np.float32), h, x.shape[0], group)
+        assert rc == 0
+        return h

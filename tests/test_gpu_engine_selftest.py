@@ -12,6 +12,8 @@ lag_cuda_moe_group, with its own bars: bf16 max rel < 5e-3, q4 max rel
 import os
 import subprocess
 
+import numpy as np
+
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -29,3 +31,40 @@ def test_reference_engine_cuda_selftest():
     lines = [l for l in r.stdout.splitlines() if l.startswith("[cuda-test]")]
     assert r.returncode == 0 and lines and lines[-1] == "[cuda-test] ALL PASS", r.stdout
     assert any("BIT-IDENTICAL" in l for l in lines)
+
+
+@pytest.mark.parametrize("S_", [1, 5, 150])
+def test_reference_engine_moe_rows_on_device(be, orc, S_):
+    """The engine's own lag_moe_rows (c/laguna.c:805-824) with a device-resident
+    layer, built against this backend's loader: S == 1 goes through moe_block's
+    expert_batch hook (lag_cuda_moe_experts), S > 1 through the engine's host
+    counting sort and lag_cuda_moe_group (150 rows: two chunks of the engine's
+    128), the shared expert through lag_cuda_matmul_bf16.  Against the same
+    engine on the CPU: within the benchmark tolerance; grouped and per-token
+    device runs bit-identical.  The host copies handed to the device run have
+    zero scales and zero shared weights, so a silent fallback to the engine's
+    CPU path cannot pass."""
+    from dataclasses import replace
+    from oracle import synth
+    from oracle.oracle import RefLaguna, RefLagunaHip
+    from sabrewing_amd import configs as cf
+    if not (RefLagunaHip.available() and RefLaguna.available()):
+        pytest.skip("reference engine libraries not built")
+    cfg = replace(cf.scaled(cf.C2_SIGMOID, D=512, E=32, K=6, I=256, Is=256), gs=0, router_bf16=False)
+    L = synth.make_layer(orc, cfg, 71, corr_bias_sigma=0.01)
+    d = synth.desc_of(cfg)
+    x = synth.make_x(orc, cfg, 72, S_)
+    h0 = synth.make_x(orc, cfg, 73, S_)
+    want = RefLaguna().moe_rows(d, L, x, h0, group=1)
+    bufs = [be.upload(a) for a in (L.gu_q, L.gu_s, L.dn_q, L.dn_s, L.sg, L.su, L.sd)]
+    poisoned = replace(L, gu_s=np.zeros_like(L.gu_s), dn_s=np.zeros_like(L.dn_s), sg=np.zeros_like(L.sg),
+                       su=np.zeros_like(L.su), sd=np.zeros_like(L.sd))
+    lag = RefLagunaHip()
+    got = lag.moe_rows(d, poisoned, [int(b) for b in bufs], x, h0, group=1)
+    got_pt = lag.moe_rows(d, poisoned, [int(b) for b in bufs], x, h0, group=0)
+    for b in bufs:
+        b.free()
+    dg, dw = got - h0, want - h0
+    nw = float(np.max(np.abs(dg - dw))) / float(np.max(np.abs(dw)))
+    assert nw <= 2e-3, nw
+    assert np.array_equal(got.view(np.uint32), got_pt.view(np.uint32))
