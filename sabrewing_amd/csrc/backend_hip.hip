@@ -493,13 +493,20 @@ extern "C" int lag_hip_moe_forward(const LagHipMoeDesc *d, const LagHipMoeWeight
     // E <= 256: one token's gate + top-k runs in every block of the expert stage
     // (no device-scope handoff); several tokens' in the routing stage, each by
     // its last router block; E > 256: a gate + top-k launch
-    const bool fused = E <= 256;
-    const bool in_route = fused && S > 1, in_experts = fused && S == 1;
+    const bool fused = E <= 256 && S == 1;
+    const bool in_route = false, in_experts = fused;
     if (in_route && ensure_cnt(S)) return -1;
+    // S == 1: the shared expert's gate_up and down run as extra blocks of stages 1 and 2;
+    // S > 1: as kernels of their own over token tiles (the same arithmetic per token)
+    const bool sh_in = sh && S == 1;
     { PROF("stage_route");
       if (sw_launch_stage_route(g_st, w->router, d->router_bf16, x, S, D, E, w->logit_bias, f.logits, f.scores, d->route_act,
                                 f.xl, f.xs, in_route ? (int *)g_cnt.p : nullptr, K, w->corr_bias, d->use_corr_bias,
-                                d->norm_topk, f.sel, f.w, sg, su, Is, f.shh)) return fail_msg("routing stage launch"); }
+                                d->norm_topk, f.sel, f.w, sh_in ? sg : nullptr, su, Is, f.shh)) return fail_msg("routing stage launch"); }
+    if (sh && !sh_in) {
+        PROF("shared_glu");
+        if (sw_launch_sh_glu(g_st, sg, su, x, S, D, Is, f.shh)) return fail_msg("shared gate_up launch");
+    }
     if (!fused) {
         PROF("gate_topk");
         if (sw_launch_gate_topk(g_st, f.logits, f.scores, S, E, K, d->route_act, w->corr_bias, d->use_corr_bias,
@@ -521,8 +528,12 @@ extern "C" int lag_hip_moe_forward(const LagHipMoeDesc *d, const LagHipMoeWeight
         SwGroups g = {f.gexp, f.gbeg, f.gcnt, f.grow, f.G, T < E ? T : E, 0};
         { PROF("stage_experts");
           if (sw_launch_stage_experts(g_st, gu, f.xl, f.xs, g, I, f.hl, f.hs, nullptr, K, nullptr, E, d->route_act,
-                                      w->corr_bias, d->use_corr_bias, d->norm_topk, f.w, sd, f.shh, S, Is, D, f.sout))
+                                      w->corr_bias, d->use_corr_bias, d->norm_topk, f.w, nullptr, f.shh, S, Is, D, f.sout))
               return fail_msg("expert stage launch"); }
+        if (sh) {
+            PROF("shared_down");
+            if (sw_launch_sh_down(g_st, sd, f.shh, S, Is, D, f.sout)) return fail_msg("shared down launch");
+        }
         SwGroups gd = g;
         gd.grow = nullptr;                 // the down reads the packed rows directly
         { PROF("q4_down"); if (sw_launch_q4_dot8_rows(g_st, dn, f.hl, f.hs, gd, f.slots)) return fail_msg("down launch"); }

@@ -469,6 +469,7 @@ __global__ __launch_bounds__(256) void k_dot8_rows(Dot8RowsArgs A) {
     TR_END(3);
 }
 template <int PF, int C16>
+#define RW_PF 4
 struct RowsL {
     static void go(dim3 grid, size_t lds, hipStream_t st, const Dot8RowsArgs &A) {
         SW_LAUNCH((k_dot8_rows<PF, DG_TT, C16>), grid, dim3(256), lds, st, A);
@@ -480,7 +481,9 @@ int sw_launch_q4_dot8_rows(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, const flo
     if (!dot8_shape_ok(W.K) || g.ngroups_max <= 0 || W.O <= 0 || !q4_extent_ok(W) || dot8_gsh(W, gsh)) return -1;
     const dim3 grid((unsigned)g.ngroups_max, (unsigned)((W.O + DG_ROWS - 1) / DG_ROWS));
     const Dot8RowsArgs A = {W, gsh, xl, xs, g, Y};
-    dispatch_pf_c16<RowsL>(dg_pf_rows(W.K), dot8_c16(W.K), grid, dot8_glu_lds(W.K, DG_TT), st, A);
+    // a ring of at most RW_PF steps: within 128 VGPRs, four blocks per CU
+    const int pf = dg_pf_rows(W.K) < RW_PF ? dg_pf_rows(W.K) : RW_PF;
+    dispatch_pf_c16<RowsL>(pf, dot8_c16(W.K), grid, dot8_glu_lds(W.K, DG_TT), st, A);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
@@ -667,7 +670,7 @@ int sw_launch_stage_route(hipStream_t st, const void *Wc, int w_bf16, const floa
     const int nbr = (E + router_epb(one, SH_NT) - 1) / router_epb(one, SH_NT);
     const RouterArgs R = {Wc, x, D, E, logit_bias, logits, route_act, scores, xl, xs, cnt, K, use_bias, norm, bias, sel, w};
     const ShGluArgs G = {sg, su, x, S, D, Is, sh_h};
-    const int TT = S >= 2 ? SH_TT : 1;
+    const int TT = S >= 2 && sg ? SH_TT : 1;
     const int nsh = sg ? sh_glu_blocks(S, Is, TT) : 0;
     if (sg && (Is % SH_GLU_O || !sh_shape_ok(D))) return -1;
     const dim3 grid((unsigned)(nbr * S + nsh));
@@ -700,14 +703,16 @@ int sw_launch_stage_experts(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, const fl
     if (sd && (D % SH_DN_O || !sh_shape_ok(Is))) return -1;
     const int nbx = picks ? K : g.ngroups_max;
     const int nglu = nbx * (I / 32);
-    const int TTS = S >= 2 ? SH_TT : 1;
+    const int TTS = S >= 2 && sd ? SH_TT : 1;         // (no shared blocks: the smaller instance)
     const int nsh = sd ? sh_down_blocks(S, D, TTS) : 0;
     const DotRoute rt = route_src ? DotRoute{route_src, bias, E, K, act, use_bias, norm, w} : DotRoute{};
     const Dot8GluArgs A = {W, gsh, xl, xs, g, I, hl, hs, sel, rt};
     const ShDownArgs Sd = {sd, sh_h, S, Is, D, sh_out};
     const dim3 grid((unsigned)(nglu + nsh));
     const size_t shl = sd ? (TTS == SH_TT ? sh_down_lds<SH_TT>(Is) : sh_down_lds<1>(Is)) : 0;
-    const int pf = dg_pf_glu(W.K), c16 = dot8_c16(W.K);
+    const int pf0 = dg_pf_glu(W.K), c16 = dot8_c16(W.K);
+    // groups: a shallower ring (4 steps) keeps the kernel within 128 VGPRs, two blocks per CU
+    const int pf = picks ? pf0 : (pf0 < 4 ? pf0 : 4);
     if (!picks) {
         const size_t lds = lds_max(dot8_glu_lds(W.K, DG_TT), shl);
         if (TTS == SH_TT) dispatch_pf_c16<StageL<0, 0, DG_TT, SH_TT>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd);

@@ -56,6 +56,7 @@ __device__ __forceinline__ void sh_rows_job(RowPtr rowp, int K, const float *__r
                                             float *runs) {
     const int G = K / SH_RG, Gq = run_lanes(G);
     const int CH = Gq < SH_CHG ? Gq : SH_CHG, NC = Gq / CH;
+    const bool c16 = G % SH_CHG == 0;              // no padding lanes (else they add zero terms)
     const int tid = threadIdx.x;
     const int RPS = sh_rps(Gq, NR, NT), NS = NR / RPS;
     const int ro = tid / Gq, gq = tid - ro * Gq, c = gq / CH;
@@ -91,7 +92,7 @@ __device__ __forceinline__ void sh_rows_job(RowPtr rowp, int K, const float *__r
         for (int t = 0; t < TT; t++) {
             if (t < nt) {                              // uniform over the block
                 const float q = bf16_group_chain(w, xv[t]);
-                const float p = CH == SH_CHG ? run_sum16(q) : run_sum(gv ? q : 0.f, CH);
+                const float p = c16 ? run_sum16(q) : run_sum(gv ? q : 0.f, CH);
                 if (lead && s < NS) runs[(lr * TT + t) * NC + c] = p;
             }
         }
@@ -165,5 +166,126 @@ __device__ __forceinline__ void sh_down_block(const uint16_t *__restrict__ Wd, c
 template <int TT>
 __host__ __device__ inline size_t sh_down_lds(int Is) { return (size_t)SH_DN_O * TT * sh_nc(Is) * 4; }
 __host__ __device__ inline int sh_down_blocks(int S, int D, int TT) { return (D / SH_DN_O) * ((S + TT - 1) / TT); }
+
+// ---- batches (S > 1): token tiles staged in LDS ----
+// The same per-(row, token) arithmetic as sh_rows_job (bf16_group_chain over
+// each group of 32 inputs, then run_sum, then the runs left to right), for a
+// tile of up to SHT_T tokens whose inputs are staged once in LDS and read by
+// every row of the block, so a weight row is read once per tile instead of
+// once per token pair.  Block of SHT_NT threads: thread (row slot ro, group g)
+// with Gq = run_lanes(G) lanes per row and RPS = SHT_NT / Gq row slots; slot
+// ro takes rows ro*NS .. ro*NS+NS-1 (NS = ceil(NR / RPS)), in batches of SHT_R
+// rows.  LDS: the tile xt[t][g][8 chunks of 16 bytes],
+// chunk c of group g stored at chunk c ^ (g & 7) (the lanes of a wave read
+// consecutive groups), then runs[NR][SHT_T][NC].
+#define SHT_T 8
+#ifndef SH_TILE_MARK
+#define SH_TILE_MARK(i)
+#endif
+#define SHT_NT 512
+#define SHT_R 4               // rows per batch (one LDS read of a token's inputs serves all)
+#define SHT_XB 8              // tile chunks per thread in flight while staging
+__host__ __device__ inline size_t sh_tile_lds(int K, int NR) {
+    const int G = K / SH_RG, NC = G < SH_CHG ? 1 : run_lanes(G) / SH_CHG;
+    return ((size_t)SHT_T * G * SH_RG + (size_t)NR * SHT_T * NC) * 4;
+}
+template <class RowPtr, class Emit>
+__device__ __forceinline__ void sh_tile_job(RowPtr rowp, int NR, int K, const float *__restrict__ x, int tok0, int nt,
+                                            Emit emit, float *lds) {
+    const int G = K / SH_RG, Gq = run_lanes(G);
+    const int CH = Gq < SH_CHG ? Gq : SH_CHG, NC = Gq / CH;
+    const bool c16 = G % SH_CHG == 0;              // no padding lanes (else they add zero terms)
+    const int tid = threadIdx.x;
+    const int RPS = SHT_NT / Gq, NS = (NR + RPS - 1) / RPS;
+    const int ro = tid / Gq, gq = tid - ro * Gq, c = gq / CH;
+    const bool worker = ro < RPS, lead = worker && (gq & (CH - 1)) == 0, gv = gq < G;
+    const int g = gv ? gq : G - 1;
+    const int roc = worker ? ro : 0;
+    float *xt = lds, *runs = lds + (size_t)SHT_T * G * SH_RG;
+    auto row_of = [&](int s) { const int lr = roc * NS + s; return lr < NR ? lr : NR - 1; };
+    auto wld = [&](int s, sw_u32x4 *w) {
+        const sw_u32x4 *wp = (const sw_u32x4 *)(rowp(row_of(s)) + g * SH_RG);
+#pragma unroll
+        for (int q = 0; q < 4; q++) w[q] = wp[q];
+    };
+    // rows in batches of SHT_R: every 16-byte chunk of a token's inputs read from LDS
+    // feeds the chains of SHT_R rows (each chain still in input order)
+    const int NB = (NS + SHT_R - 1) / SHT_R;
+    sw_u32x4 w[SHT_R][4];
+#pragma unroll
+    for (int r = 0; r < SHT_R; r++) wld(r < NS ? r : NS - 1, w[r]);
+    // the tile: nt tokens x G groups x 8 chunks of 16 bytes, SHT_XB chunks per thread
+    // in flight per pass (loads clamped to the last chunk, stores guarded)
+    const int nch = nt * G * 8;
+    for (int base = 0; base < nch; base += SHT_XB * SHT_NT) {
+        sw_f32x4 v[SHT_XB];
+#pragma unroll
+        for (int u = 0; u < SHT_XB; u++) {
+            const int idx = min(base + u * SHT_NT + tid, nch - 1);
+            const int t = idx / (G * 8), r = idx - t * (G * 8);
+            v[u] = *(const sw_f32x4 *)(x + (int64_t)(tok0 + t) * K + (r >> 3) * SH_RG + 4 * (r & 7));
+        }
+#pragma unroll
+        for (int u = 0; u < SHT_XB; u++) {
+            const int idx = base + u * SHT_NT + tid;
+            if (idx < nch) {
+                const int t = idx / (G * 8), r = idx - t * (G * 8), gg = r >> 3, cc = r & 7;
+                *(sw_f32x4 *)(xt + ((t * G + gg) * 8 + (cc ^ (gg & 7))) * 4) = v[u];
+            }
+        }
+    }
+    __syncthreads();
+    SH_TILE_MARK(1);
+    const float *xg = xt + (size_t)g * 8 * 4;
+    const int sw = g & 7;
+    for (int b = 0; b < NB; b++) {
+        if (b > 0) {
+#pragma unroll
+            for (int r = 0; r < SHT_R; r++) wld(min(b * SHT_R + r, NS - 1), w[r]);
+        }
+        for (int t = 0; t < nt; t++) {                 // uniform over the block
+            const float *xr = xg + (size_t)t * G * 8 * 4;
+            float q[SHT_R];
+#pragma unroll
+            for (int r = 0; r < SHT_R; r++) q[r] = 0.f;
+#pragma unroll
+            for (int qq = 0; qq < 4; qq++) {           // bf16_group_chain, inputs from the tile
+                const sw_f32x4 xa = *(const sw_f32x4 *)(xr + ((2 * qq) ^ sw) * 4);
+                const sw_f32x4 xb = *(const sw_f32x4 *)(xr + ((2 * qq + 1) ^ sw) * 4);
+#pragma unroll
+                for (int r = 0; r < SHT_R; r++) {
+                    const sw_u32x4 v = w[r][qq];
+                    q[r] = __builtin_fmaf(bf16lo(v.x), xa.x, q[r]);
+                    q[r] = __builtin_fmaf(bf16hi(v.x), xa.y, q[r]);
+                    q[r] = __builtin_fmaf(bf16lo(v.y), xa.z, q[r]);
+                    q[r] = __builtin_fmaf(bf16hi(v.y), xa.w, q[r]);
+                    q[r] = __builtin_fmaf(bf16lo(v.z), xb.x, q[r]);
+                    q[r] = __builtin_fmaf(bf16hi(v.z), xb.y, q[r]);
+                    q[r] = __builtin_fmaf(bf16lo(v.w), xb.z, q[r]);
+                    q[r] = __builtin_fmaf(bf16hi(v.w), xb.w, q[r]);
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < SHT_R; r++) {
+                const int s = b * SHT_R + r, lr = roc * NS + s;
+                const float p = c16 ? run_sum16(q[r]) : run_sum(gv ? q[r] : 0.f, CH);
+                if (lead && s < NS && lr < NR) runs[(lr * SHT_T + t) * NC + c] = p;
+            }
+        }
+        SH_TILE_MARK(2 + (b < 3 ? b : 3));
+    }
+    __syncthreads();
+    for (int it = tid; it < NR * nt; it += SHT_NT) {
+        const int lr = it / nt, t = it - lr * nt;
+        const float *rr = runs + (lr * SHT_T + t) * NC;
+        float y = rr[0];
+        for (int cc = 1; cc < NC; cc++) y = y + rr[cc];
+        emit(lr, t, y);
+    }
+}
+// gate_up: SHT_GLU_O outputs i per block (gate rows, then up rows), a tile of tokens
+#define SHT_GLU_O 16
+// down: SHT_DN_O output rows per block
+#define SHT_DN_O 64
 
 #endif
