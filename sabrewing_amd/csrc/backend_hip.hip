@@ -113,13 +113,6 @@ static int grow_dev(Buf &b, size_t need) {
 // per-token arrival counters of the routing stage: their own allocation (no
 // other scratch ever overlaps them), zero between launches (the last block of
 // each token resets its counter)
-static Buf g_cnt;
-static int ensure_cnt(int S) {
-    if ((size_t)S * 4 <= g_cnt.cap) return 0;
-    if (grow_dev(g_cnt, (size_t)S * 4)) return -1;
-    CK(hipMemsetAsync(g_cnt.p, 0, g_cnt.cap, g_st), "counter clear");
-    return 0;
-}
 static int grow_pinned(Buf &b, size_t need) {
     if (need <= b.cap) return 0;
     if (b.p) (void)hipHostFree(b.p);
@@ -407,7 +400,7 @@ extern "C" int lag_hip_router_chain(const void *W, void *Wc, int E, int D, int w
 
 struct FwdScratch {
     float *logits, *scores, *w, *slots, *sout;
-    int *sel, *gexp, *gbeg, *gcnt, *G, *grow, *rowof;
+    int *sel, *gexp, *gbeg, *gcnt, *G, *grow, *rowof, *items, *P;
     sw_u32x4 *hl;           // h of every packed row as dot8 limbs
     float *hs;
     float *shh;             // shared expert h [S, Is]
@@ -436,6 +429,7 @@ static int carve_fwd(const LagHipMoeDesc *d, int S, FwdScratch &f) {
     const size_t o_sel = cv.take((size_t)T * 4), o_w = cv.take((size_t)T * 4);
     const size_t o_gexp = cv.take((size_t)E * 4), o_gbeg = cv.take((size_t)E * 4), o_gcnt = cv.take((size_t)E * 4);
     const size_t o_G = cv.take(4), o_grow = cv.take((size_t)T * 4), o_rowof = cv.take((size_t)T * 4);
+    const size_t o_items = cv.take((size_t)sw_npass_max(T, E, SW_DG_TT) * 4), o_P = cv.take(4);
     const size_t o_hl = cv.take((size_t)T * (I / 32) * SW_NL * 16), o_hs = cv.take((size_t)T * (I / 32) * 4);
     const size_t o_slot = cv.take(S > 1 ? (size_t)T * D * 4 : 4);
     size_t o_sh = 0, o_so = 0;
@@ -445,6 +439,7 @@ static int carve_fwd(const LagHipMoeDesc *d, int S, FwdScratch &f) {
     char *A = (char *)g_arena.p;
     f.logits = (float *)(A + o_lg); f.scores = (float *)(A + o_sc); f.sel = (int *)(A + o_sel); f.w = (float *)(A + o_w);
     f.gexp = (int *)(A + o_gexp); f.gbeg = (int *)(A + o_gbeg); f.gcnt = (int *)(A + o_gcnt); f.G = (int *)(A + o_G);
+    f.items = (int *)(A + o_items); f.P = (int *)(A + o_P);
     f.grow = (int *)(A + o_grow); f.rowof = (int *)(A + o_rowof);
     f.hl = (sw_u32x4 *)(A + o_hl); f.hs = (float *)(A + o_hs); f.slots = (float *)(A + o_slot);
     f.shh = d->shared_mode ? (float *)(A + o_sh) : nullptr;
@@ -471,13 +466,14 @@ extern "C" int lag_hip_route(const LagHipMoeDesc *d, const LagHipMoeWeights *w, 
     return route_dev(d, w, x, S, logits ? logits : f.logits, f.scores, sel, wts);
 }
 
-// One decode step (sabrewing's moe_block over S tokens, device pointers):
-//   stage 1  router logits / scores / limbs, each token's gate + top-k by its
-//            last router block (E > 256: a gate + top-k launch after), and the
-//            shared expert's gate_up; for S > 1 then the counting sort
-//   stage 2  routed gate_up + the shared expert's down
-//   stage 3  S == 1: routed down fused with the rank-order combine;
-//            S > 1: grouped routed down into slots, then the combine
+// One decode step (sabrewing's moe_block over S tokens, device pointers).
+// S == 1, three launches:
+//   stage 1  router logits / scores / limbs of x + the shared expert's gate_up
+//   stage 2  every block re-derives the gate + top-k (E <= 256), then the
+//            routed gate_up; + the shared expert's down
+//   stage 3  routed down fused with the rank-order combine (+ shared, residual)
+// S > 1: routing stage, gate + top-k, shared gate_up over token tiles, the
+// counting sort, grouped gate_up, shared down, grouped down into slots, combine.
 extern "C" int lag_hip_moe_forward(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const float *x, float *out, int S) {
     if (!g_ok || fault_injected()) return -1;
     if (!desc_ok(d, w) || S <= 0) return fail_msg("moe_forward: unsupported descriptor/shape");
@@ -490,24 +486,21 @@ extern "C" int lag_hip_moe_forward(const LagHipMoeDesc *d, const LagHipMoeWeight
     const bool sh = d->shared_mode != 0;
     const uint16_t *sg = sh ? (const uint16_t *)w->sg : nullptr, *su = sh ? (const uint16_t *)w->su : nullptr;
     const uint16_t *sd = sh ? (const uint16_t *)w->sd : nullptr;
-    // E <= 256: one token's gate + top-k runs in every block of the expert stage
-    // (no device-scope handoff); several tokens' in the routing stage, each by
-    // its last router block; E > 256: a gate + top-k launch
-    const bool fused = E <= 256 && S == 1;
-    const bool in_route = false, in_experts = fused;
-    if (in_route && ensure_cnt(S)) return -1;
+    // one token with E <= 256: its gate + top-k runs in every block of the
+    // expert stage (no device-scope handoff); otherwise a gate + top-k launch
+    // after the routing stage
+    const bool in_experts = E <= 256 && S == 1;
     // S == 1: the shared expert's gate_up and down run as extra blocks of stages 1 and 2;
     // S > 1: as kernels of their own over token tiles (the same arithmetic per token)
     const bool sh_in = sh && S == 1;
     { PROF("stage_route");
       if (sw_launch_stage_route(g_st, w->router, d->router_bf16, x, S, D, E, w->logit_bias, f.logits, f.scores, d->route_act,
-                                f.xl, f.xs, in_route ? (int *)g_cnt.p : nullptr, K, w->corr_bias, d->use_corr_bias,
-                                d->norm_topk, f.sel, f.w, sh_in ? sg : nullptr, su, Is, f.shh)) return fail_msg("routing stage launch"); }
+                                f.xl, f.xs, sh_in ? sg : nullptr, su, Is, f.shh)) return fail_msg("routing stage launch"); }
     if (sh && !sh_in) {
         PROF("shared_glu");
         if (sw_launch_sh_glu(g_st, sg, su, x, S, D, Is, f.shh)) return fail_msg("shared gate_up launch");
     }
-    if (!fused) {
+    if (!in_experts) {
         PROF("gate_topk");
         if (sw_launch_gate_topk(g_st, f.logits, f.scores, S, E, K, d->route_act, w->corr_bias, d->use_corr_bias,
                                 d->norm_topk, f.sel, f.w)) return fail_msg("gate/top-k launch");
@@ -524,8 +517,11 @@ extern "C" int lag_hip_moe_forward(const LagHipMoeDesc *d, const LagHipMoeWeight
         g_last_G_dev = 0; g_last_ng = K;
     } else {
         { PROF("bucket");
-          if (sw_launch_bucket(g_st, f.sel, S, K, E, f.gexp, f.gbeg, f.gcnt, f.G, f.grow, f.rowof)) return fail_msg("bucket launch"); }
-        SwGroups g = {f.gexp, f.gbeg, f.gcnt, f.grow, f.G, T < E ? T : E, 0};
+          if (sw_launch_bucket(g_st, f.sel, S, K, E, f.gexp, f.gbeg, f.gcnt, f.G, f.grow, f.rowof, SW_DG_TT, f.items, f.P))
+              return fail_msg("bucket launch"); }
+        // one block per pass of up to SW_DG_TT tokens of a group (the passes of a group
+        // with many tokens spread over blocks instead of queueing in one)
+        SwGroups g = {f.gexp, f.gbeg, f.gcnt, f.grow, f.G, sw_npass_max(T, E, SW_DG_TT), 0, f.items, f.P};
         { PROF("stage_experts");
           if (sw_launch_stage_experts(g_st, gu, f.xl, f.xs, g, I, f.hl, f.hs, nullptr, K, nullptr, E, d->route_act,
                                       w->corr_bias, d->use_corr_bias, d->norm_topk, f.w, nullptr, f.shh, S, Is, D, f.sout))
@@ -648,8 +644,8 @@ extern "C" const char *lag_hip_last_error(void) { return g_err; }
 
 // ------------------------------------------------------------ graphs ----
 // Every device-pointer entry issued between begin and end (moe_forward,
-// route, d2d) is recorded, fork/join of the shared-expert stream included,
-// into one graph replayed by lag_hip_graph_launch with one submission.
+// route, d2d) is recorded into one graph, replayed by lag_hip_graph_launch
+// with one submission.
 extern "C" int lag_hip_graph_begin(void) {
     if (!g_ok || g_capturing) return -1;
     prof_flush();

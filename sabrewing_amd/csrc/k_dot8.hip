@@ -129,6 +129,28 @@ __host__ __device__ inline int dg_rps(int Gq, int cap, int nt) {
     return r;
 }
 
+// the work of grouped block bx: expert e, the group's first packed row beg and
+// its tokens [t0, tend) -- one pass from the pass list, or the whole group
+// (false: nothing to do)
+__device__ __forceinline__ bool grp_work(const SwGroups &grp, int bx, int TT, int &e, int &beg, int &t0, int &tend) {
+    if (grp.items) {
+        if (bx >= *grp.P) return false;
+        const int v = grp.items[bx], gi = v & 1023;
+        t0 = v >> 10;
+        e = grp.gexp[gi];
+        beg = grp.gbeg[gi];
+        tend = min(t0 + TT, grp.gcnt[gi]);
+        return true;
+    }
+    const int gvalid = grp.G ? *grp.G : grp.ngroups_max;
+    if (bx >= gvalid) return false;
+    e = grp.gexp ? grp.gexp[bx] : 0;
+    beg = grp.gbeg ? grp.gbeg[bx] : 0;
+    t0 = 0;
+    tend = grp.gcnt ? grp.gcnt[bx] : grp.cnt_const;
+    return true;
+}
+
 // ------------------------------------------------------------ gate_up ----
 // One block = 32 consecutive intermediate outputs i of one group: gate rows
 // i0..i0+31 and up rows i0..i0+31 (64 weight rows), every input group, for a
@@ -142,7 +164,7 @@ __host__ __device__ inline int dg_rps(int Gq, int cap, int nt) {
 // in flight; a row's run sums go to LDS and the row sums, the SiLU-GLU and
 // the limbs of h (the down projection's input) follow.
 #define DG_ROWS 64
-#define DG_TT 2               // tokens per weight pass in the grouped kernels
+#define DG_TT SW_DG_TT        // tokens per weight pass in the grouped kernels
 #define DG_NT 512             // threads per gate_up block
 // One token (PICK = 1): block (rank a, set of outputs) takes pick a and
 // writes h of packed row a.  With NP = 0 the picks come in sel (from the
@@ -206,11 +228,11 @@ __device__ __forceinline__ void dot8_glu_block(const Dot8GluArgs &A, int bx, int
     const int ng = W.gs > 0 ? K / W.gs : 1;
     const int sg = W.gs > 0 ? (g * RG) >> A.gsh : 0;
     const uint32_t rb = (uint32_t)K / 2, sb = (uint32_t)ng * 4;
-    int e, beg, cnt;
+    int e, beg, tb, tend;
     sw_u32x4 X[TT][SW_NL];
     float xf[TT];
     if constexpr (PICK) {                             // one token: rank bx of its picks
-        beg = bx; cnt = 1;
+        beg = bx; tb = 0; tend = 1;
 #pragma unroll
         for (int l = 0; l < SW_NL; l++) X[0][l] = xl[(int64_t)g * SW_NL + l];
         xf[0] = xs[g];
@@ -225,11 +247,7 @@ __device__ __forceinline__ void dot8_glu_block(const Dot8GluArgs &A, int bx, int
         }
         TR_MARK(0);
     } else {
-        const int gvalid = grp.G ? *grp.G : grp.ngroups_max;
-        if (bx >= gvalid) return;
-        e = grp.gexp ? grp.gexp[bx] : 0;
-        beg = grp.gbeg ? grp.gbeg[bx] : 0;
-        cnt = grp.gcnt ? grp.gcnt[bx] : grp.cnt_const;
+        if (!grp_work(grp, bx, TT, e, beg, tb, tend)) return;
     }
     const sw_rsrc rq = q4_rq(W), rs = q4_rs(W);
     // lane offsets (this thread's first row of a half) and the scalar offset of step s
@@ -239,8 +257,8 @@ __device__ __forceinline__ void dot8_glu_block(const Dot8GluArgs &A, int bx, int
     auto srow = [&](int s) -> uint32_t { return s < NSH ? erow + s : erow + I + (s - NSH); };
     const int NS = 2 * NSH;
     float *myruns = runs + (roc * NSH) * NC + c;      // this lane's run sum of step s: myruns[(t*64 + h*32 + j) * NC]
-    for (int t0 = 0; t0 < cnt; t0 += TT) {
-        const int nt = min(TT, cnt - t0);
+    for (int t0 = tb; t0 < tend; t0 += TT) {
+        const int nt = min(TT, tend - t0);
         if constexpr (PICK == 0) {
 #pragma unroll
             for (int t = 0; t < TT; t++) {
@@ -389,10 +407,8 @@ __device__ __forceinline__ void dot8_rows_block(const Dot8RowsArgs &A, int bx, i
     const bool worker = ro < RPS, lead = worker && (gq & (CH - 1)) == 0, gv = C16 || gq < G;
     const int g = gv ? gq : G - 1;
     const int roc = worker ? ro : 0;
-    const int gvalid = grp.G ? *grp.G : grp.ngroups_max;
-    if (bx >= gvalid) return;
-    const int e = grp.gexp ? grp.gexp[bx] : 0, beg = grp.gbeg ? grp.gbeg[bx] : 0;
-    const int cnt = grp.gcnt ? grp.gcnt[bx] : grp.cnt_const;
+    int e, beg, tb, tend;
+    if (!grp_work(grp, bx, TT, e, beg, tb, tend)) return;
     const int r0 = by * DG_ROWS;
     const int nrows = min(DG_ROWS, O - r0);
     const int ng = W.gs > 0 ? K / W.gs : 1;
@@ -404,8 +420,8 @@ __device__ __forceinline__ void dot8_rows_block(const Dot8RowsArgs &A, int bx, i
     const uint32_t vos = (uint32_t)(roc * NS) * sb + (uint32_t)sg * 4;
     const uint32_t erow = (uint32_t)e * (uint32_t)O + (uint32_t)r0;
     float *myruns = runs + (roc * NS) * NC + c;
-    for (int t0 = 0; t0 < cnt; t0 += TT) {
-        const int nt = min(TT, cnt - t0);
+    for (int t0 = tb; t0 < tend; t0 += TT) {
+        const int nt = min(TT, tend - t0);
         sw_u32x4 X[TT][SW_NL];
         float xf[TT];
 #pragma unroll
@@ -465,7 +481,10 @@ template <int PF, int TT, int C16>
 __global__ __launch_bounds__(256) void k_dot8_rows(Dot8RowsArgs A) {
     extern __shared__ __align__(16) float red[];
     TR_BEGIN();
-    dot8_rows_block<PF, TT, C16>(A, blockIdx.x, blockIdx.y, red);
+    const int nb = (int)(gridDim.x * gridDim.y);
+    const int w = A.grp.items ? sw_xcd_work((int)(blockIdx.x + gridDim.x * blockIdx.y), nb)
+                              : (int)(blockIdx.x + gridDim.x * blockIdx.y);
+    dot8_rows_block<PF, TT, C16>(A, w % (int)gridDim.x, w / (int)gridDim.x, red);
     TR_END(3);
 }
 template <int PF, int C16>
@@ -610,12 +629,12 @@ static size_t lds_max(size_t a, size_t b) { return a > b ? a : b; }
 struct ShGluArgs { const uint16_t *Wg, *Wu; const float *x; int S, D, Is; float *h; };
 struct ShDownArgs { const uint16_t *Wd; const float *h; int S, Is, D; float *out; };
 
-template <int BF16, int TT, int NP, int ONE>
+template <int BF16, int TT, int ONE>
 __global__ __launch_bounds__(SH_NT) void k_stage_route(RouterArgs R, int nbr, int S, ShGluArgs G) {
     extern __shared__ __align__(16) float smem[];
     TR_BEGIN();
     const int b = blockIdx.x;
-    if (b < nbr * S) router_block<BF16, NP, ONE>(R, b % nbr, b / nbr, nbr, smem);
+    if (b < nbr * S) router_block<BF16, ONE>(R, b % nbr, b / nbr, nbr, smem);
     else sh_glu_block<TT>(G.Wg, G.Wu, G.x, G.S, G.D, G.Is, G.h, b - nbr * S, smem);
     TR_END(0);
 }
@@ -626,8 +645,12 @@ __global__ __launch_bounds__(DG_NT) void k_stage_experts(Dot8GluArgs A, int nbx,
     extern __shared__ __align__(16) float smem[];
     TR_BEGIN();
     const int b = blockIdx.x;
-    if (b < nglu) dot8_glu_block<PF, PICK, NP, TTG, C16>(A, b % nbx, b / nbx, smem);
-    else sh_down_block<TTS>(Sd.Wd, Sd.h, Sd.S, Sd.Is, Sd.D, Sd.out, b - nglu, smem);
+    if (b < nglu) {
+        const int w = PICK == 0 && A.grp.items ? sw_xcd_work(b, nglu) : b;
+        dot8_glu_block<PF, PICK, NP, TTG, C16>(A, w % nbx, w / nbx, smem);
+    } else {
+        sh_down_block<TTS>(Sd.Wd, Sd.h, Sd.S, Sd.Is, Sd.D, Sd.out, b - nglu, smem);
+    }
     TR_END(1);
 }
 template <int PICK, int NP, int TTG, int TTS>
@@ -640,48 +663,36 @@ struct StageL {
     };
 };
 
-template <int BF16, int TT, int ONE>
-static void launch_stage_route(int np, dim3 grid, size_t lds, hipStream_t st, const RouterArgs &R, int nbr, int S,
-                               const ShGluArgs &G) {
-    if (np == 0) SW_LAUNCH((k_stage_route<BF16, TT, 0, ONE>), grid, dim3(SH_NT), lds, st, R, nbr, S, G);
-    else if (np == 1) SW_LAUNCH((k_stage_route<BF16, TT, 1, ONE>), grid, dim3(SH_NT), lds, st, R, nbr, S, G);
-    else if (np == 2) SW_LAUNCH((k_stage_route<BF16, TT, 2, ONE>), grid, dim3(SH_NT), lds, st, R, nbr, S, G);
-    else SW_LAUNCH((k_stage_route<BF16, TT, 4, ONE>), grid, dim3(SH_NT), lds, st, R, nbr, S, G);
-}
 template <int TT, int ONE>
-static void launch_stage_route2(int bf16, int np, dim3 grid, size_t lds, hipStream_t st, const RouterArgs &R, int nbr,
-                                int S, const ShGluArgs &G) {
-    if (bf16) launch_stage_route<1, TT, ONE>(np, grid, lds, st, R, nbr, S, G);
-    else launch_stage_route<0, TT, ONE>(np, grid, lds, st, R, nbr, S, G);
+static void launch_stage_route(int bf16, dim3 grid, size_t lds, hipStream_t st, const RouterArgs &R, int nbr, int S,
+                               const ShGluArgs &G) {
+    if (bf16) SW_LAUNCH((k_stage_route<1, TT, ONE>), grid, dim3(SH_NT), lds, st, R, nbr, S, G);
+    else SW_LAUNCH((k_stage_route<0, TT, ONE>), grid, dim3(SH_NT), lds, st, R, nbr, S, G);
 }
 
-// stage 1: router logits / scores and the limbs of x, the gate + top-k of
-// each token when cnt is non-null (E <= 256; picks to sel/w), and the shared
+// stage 1: router logits / scores and the limbs of x, and the shared
 // expert's gate_up when sg is non-null
 int sw_launch_stage_route(hipStream_t st, const void *Wc, int w_bf16, const float *x, int S, int D, int E,
                           const float *logit_bias, float *logits, float *scores, int route_act, sw_u32x4 *xl, float *xs,
-                          int *cnt, int K, const float *bias, int use_bias, int norm, int *sel, float *w,
                           const uint16_t *sg, const uint16_t *su, int Is, float *sh_h) {
     if (D % 128 || E <= 0 || S <= 0 || route_act < 0 || route_act > 2 || (route_act != 1 && !scores)) return -1;
-    if (cnt && (E > 256 || K <= 0 || K > 64 || K > E || !sel || !w)) return -1;
     const int one = router_one(S, E);
     const size_t rl = router_lds(D);
     if (rl > 65536 || D > 4 * RT_XB * (one ? SH_NT - 64 : SH_NT)) return -1;
     const int nbr = (E + router_epb(one, SH_NT) - 1) / router_epb(one, SH_NT);
-    const RouterArgs R = {Wc, x, D, E, logit_bias, logits, route_act, scores, xl, xs, cnt, K, use_bias, norm, bias, sel, w};
+    const RouterArgs R = {Wc, x, D, E, logit_bias, logits, route_act, scores, xl, xs};
     const ShGluArgs G = {sg, su, x, S, D, Is, sh_h};
     const int TT = S >= 2 && sg ? SH_TT : 1;
     const int nsh = sg ? sh_glu_blocks(S, Is, TT) : 0;
     if (sg && (Is % SH_GLU_O || !sh_shape_ok(D))) return -1;
     const dim3 grid((unsigned)(nbr * S + nsh));
     const size_t lds = lds_max(rl, sg ? (TT == SH_TT ? sh_glu_lds<SH_TT>(D) : sh_glu_lds<1>(D)) : 0);
-    const int np = !cnt ? 0 : E <= 64 ? 1 : E <= 128 ? 2 : 4;
     if (TT == SH_TT) {
-        if (one) launch_stage_route2<SH_TT, 1>(w_bf16, np, grid, lds, st, R, nbr, S, G);
-        else launch_stage_route2<SH_TT, 0>(w_bf16, np, grid, lds, st, R, nbr, S, G);
+        if (one) launch_stage_route<SH_TT, 1>(w_bf16, grid, lds, st, R, nbr, S, G);
+        else launch_stage_route<SH_TT, 0>(w_bf16, grid, lds, st, R, nbr, S, G);
     } else {
-        if (one) launch_stage_route2<1, 1>(w_bf16, np, grid, lds, st, R, nbr, S, G);
-        else launch_stage_route2<1, 0>(w_bf16, np, grid, lds, st, R, nbr, S, G);
+        if (one) launch_stage_route<1, 1>(w_bf16, grid, lds, st, R, nbr, S, G);
+        else launch_stage_route<1, 0>(w_bf16, grid, lds, st, R, nbr, S, G);
     }
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }

@@ -52,7 +52,7 @@ __global__ __launch_bounds__(64) void k_gate_topk(const float *__restrict__ logi
 template <int BF16, int ONE>
 __global__ __launch_bounds__(512) void k_router_logits(RouterArgs R) {
     extern __shared__ __align__(16) float smem[];
-    router_block<BF16, 0, ONE>(R, blockIdx.x, blockIdx.y, gridDim.x, smem);
+    router_block<BF16, ONE>(R, blockIdx.x, blockIdx.y, gridDim.x, smem);
 }
 
 int sw_launch_router_topk(hipStream_t st, const void *Wc, int w_bf16, const float *x, int S, int D, int E,
@@ -66,7 +66,7 @@ int sw_launch_router_topk(hipStream_t st, const void *Wc, int w_bf16, const floa
     const int nt = 512, one = router_one(S, E), epb = router_epb(one, nt);
     if (router_lds(D) > 65536 || D > 4 * RT_XB * (one ? nt - 64 : nt)) return -1;
     dim3 grid((unsigned)((E + epb - 1) / epb), (unsigned)S);
-    const RouterArgs R = {Wc, x, D, E, logit_bias, logits, route_act, scores, xl, xs, nullptr, 0, 0, 0, nullptr, nullptr, nullptr};
+    const RouterArgs R = {Wc, x, D, E, logit_bias, logits, route_act, scores, xl, xs};
     if (one) {
         if (w_bf16) SW_LAUNCH((k_router_logits<1, 1>), grid, dim3(nt), router_lds(D), st, R);
         else SW_LAUNCH((k_router_logits<0, 1>), grid, dim3(nt), router_lds(D), st, R);
@@ -106,8 +106,9 @@ int sw_launch_gate_topk(hipStream_t st, const float *logits, const float *scores
 __global__ __launch_bounds__(BK_THREADS) void k_bucket(const int *__restrict__ sel, int T, int K, int E,
                                                        int *__restrict__ gexp, int *__restrict__ gbeg,
                                                        int *__restrict__ gcnt, int *__restrict__ Gout,
-                                                       int *__restrict__ grow, int *__restrict__ rowof) {
-    __shared__ int cnt[BK_MAXE], run[BK_MAXE], sa[BK_MAXE], sb[BK_MAXE];
+                                                       int *__restrict__ grow, int *__restrict__ rowof, int tt,
+                                                       int *__restrict__ items, int *__restrict__ Pout) {
+    __shared__ int cnt[BK_MAXE], run[BK_MAXE], sa[BK_MAXE], sb[BK_MAXE], sp[BK_MAXE];
     __shared__ int wcnt[BK_THREADS / 64][BK_MAXE];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     for (int i = tid; i < E; i += BK_THREADS) {
@@ -117,14 +118,15 @@ __global__ __launch_bounds__(BK_THREADS) void k_bucket(const int *__restrict__ s
     __syncthreads();
     for (int p = tid; p < T; p += BK_THREADS) atomicAdd(&cnt[sel[p]], 1);
     __syncthreads();
-    // exclusive scans of cnt (packed offsets) and of cnt > 0 (group index)
-    for (int i = tid; i < E; i += BK_THREADS) { sa[i] = cnt[i]; sb[i] = cnt[i] > 0; }
+    // exclusive scans of cnt (packed offsets), of cnt > 0 (group index) and of
+    // the passes ceil(cnt / tt) (pass list offsets)
+    for (int i = tid; i < E; i += BK_THREADS) { sa[i] = cnt[i]; sb[i] = cnt[i] > 0; sp[i] = (cnt[i] + tt - 1) / tt; }
     __syncthreads();
     for (int off = 1; off < E; off <<= 1) {
-        int va = 0, vb = 0;
-        if (tid < E && tid >= off) { va = sa[tid - off]; vb = sb[tid - off]; }
+        int va = 0, vb = 0, vp = 0;
+        if (tid < E && tid >= off) { va = sa[tid - off]; vb = sb[tid - off]; vp = sp[tid - off]; }
         __syncthreads();
-        if (tid < E && tid >= off) { sa[tid] += va; sb[tid] += vb; }
+        if (tid < E && tid >= off) { sa[tid] += va; sb[tid] += vb; sp[tid] += vp; }
         __syncthreads();
     }
     if (tid < E) {
@@ -133,6 +135,11 @@ __global__ __launch_bounds__(BK_THREADS) void k_bucket(const int *__restrict__ s
         run[tid] = offx;
         if (c > 0) { gexp[gi] = tid; gbeg[gi] = offx; gcnt[gi] = c; }
         if (tid == E - 1) *Gout = sb[tid];
+        if (items) {
+            const int np = (c + tt - 1) / tt, p0 = sp[tid] - np;
+            for (int k = 0; k < np; k++) items[p0 + k] = ((k * tt) << 10) | gi;
+            if (tid == E - 1) *Pout = sp[tid];
+        }
     }
     __syncthreads();
     int nbits = 0;
@@ -168,9 +175,11 @@ __global__ __launch_bounds__(BK_THREADS) void k_bucket(const int *__restrict__ s
 }
 
 int sw_launch_bucket(hipStream_t st, const int *sel, int S, int K, int E, int *gexp, int *gbeg,
-                     int *gcnt, int *G, int *grow, int *rowof) {
-    if (E <= 0 || E > BK_MAXE || S <= 0 || K <= 0) return -1;
-    SW_LAUNCH(k_bucket, dim3(1), dim3(BK_THREADS), 0, st, sel, S * K, K, E, gexp, gbeg, gcnt, G, grow, rowof);
+                     int *gcnt, int *G, int *grow, int *rowof, int tt, int *items, int *P) {
+    if (E <= 0 || E > BK_MAXE || S <= 0 || K <= 0 || tt <= 0 || (items && !P)) return -1;
+    if ((int64_t)S * K >= (1 << 21)) return -1;      // pass offsets in 21 bits of an item
+    SW_LAUNCH(k_bucket, dim3(1), dim3(BK_THREADS), 0, st, sel, S * K, K, E, gexp, gbeg, gcnt, G, grow, rowof, tt,
+              items, P);
     return launch_err();
 }
 

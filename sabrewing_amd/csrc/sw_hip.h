@@ -96,9 +96,24 @@ struct SwGroups {
     const int *gexp, *gbeg, *gcnt;   // [ngroups]; null gexp/gbeg mean 0, null gcnt means cnt_const
     const int *grow;                 // [T] or null
     const int *G;                    // device count (null: use ngroups_max)
-    int ngroups_max;
+    int ngroups_max;                 // grid extent: groups, or passes when items is set
     int cnt_const;
+    // passes (optional): items[j] = (t0 << 10) | group of pass j, P = the device count;
+    // a block then takes one pass of up to DG_TT tokens from t0 instead of a whole group
+    const int *items;
+    const int *P;
 };
+#define SW_DG_TT 2             // tokens per weight pass of the grouped dot8 kernels
+// the upper bound of the passes of T packed rows in at most min(T, E) groups, tt tokens each
+__host__ __device__ inline int sw_npass_max(int T, int E, int tt) { return (T + (T < E ? T : E) * (tt - 1)) / tt; }
+// XCD-aware block order: launches deal consecutive block ids to the 8 XCDs in
+// turn; work index w gives XCD k the contiguous range [k n/8, (k+1) n/8) of
+// the first n = 8 floor(nb/8) blocks, so neighbouring work (the passes of one
+// group over the same weight rows) shares an L2
+__device__ __forceinline__ int sw_xcd_work(int b, int nb) {
+    const int n8 = nb & ~7;
+    return b < n8 ? (b & 7) * (n8 >> 3) + (b >> 3) : b;
+}
 
 // int4 weight tensor of E experts, O rows each, K inputs
 struct SwQ4 {
@@ -126,8 +141,9 @@ int sw_launch_router_topk(hipStream_t st, const void *Wc, int w_bf16, const floa
 // gate + top-k of S tokens from their logits (act 1) or scores (one wave each)
 int sw_launch_gate_topk(hipStream_t st, const float *logits, const float *scores, int S, int E, int K, int route_act,
                         const float *corr_bias, int use_corr_bias, int norm_topk, int *sel, float *w);
+// counting sort by expert; with items non-null also the pass list of tt tokens (SwGroups)
 int sw_launch_bucket(hipStream_t st, const int *sel, int S, int K, int E, int *gexp, int *gbeg,
-                     int *gcnt, int *G, int *grow, int *rowof);
+                     int *gcnt, int *G, int *grow, int *rowof, int tt, int *items, int *P);
 // out planes of SiLU-GLU(gate, up) for every packed row of every group
 // maxtok: an upper bound of any group's token count (1 for the per-token path)
 // (x: f32 activations [tokens, K], split into hi/lo planes while staged)
@@ -163,15 +179,13 @@ int sw_launch_q4_down_combine(hipStream_t st, SwQ4 W, const _Float16 *hplanes, c
 // out[s] (+)= route_scale * sum_a w[s,a] * slots[rowof[s,a]] (+ shared[s])
 int sw_launch_combine(hipStream_t st, const float *slots, const int *rowof, const float *w, int S, int K, int D,
                       float route_scale, const float *shared, float *out, int accumulate);
-// fused decode stages (k_dot8.hip): stage 1 = router logits/scores/limbs,
-// each token's gate + top-k by its last router block (cnt non-null: S zeroed
-// arrival counters, E <= 256; picks to sel/w) and the shared expert's gate_up
-// (sg null: none); stage 2 = routed gate_up (sel non-null: one token's K
-// picks, from sel or, with route_src, by a gate + top-k in every block; else
-// the groups g) + the shared expert's down (sd null: none)
+// fused decode stages (k_dot8.hip): stage 1 = router logits/scores/limbs
+// and the shared expert's gate_up (sg null: none); stage 2 = routed gate_up
+// (sel non-null: one token's K picks, from sel or, with route_src, by a gate
+// + top-k in every block; else the groups g) + the shared expert's down (sd
+// null: none)
 int sw_launch_stage_route(hipStream_t st, const void *Wc, int w_bf16, const float *x, int S, int D, int E,
                           const float *logit_bias, float *logits, float *scores, int route_act, sw_u32x4 *xl, float *xs,
-                          int *cnt, int K, const float *bias, int use_bias, int norm, int *sel, float *w,
                           const uint16_t *sg, const uint16_t *su, int Is, float *sh_h);
 int sw_launch_stage_experts(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, const float *xs, SwGroups g, int I, sw_u32x4 *hl,
                             float *hs, int *sel, int K, const float *route_src, int E, int act, const float *bias,
@@ -179,6 +193,7 @@ int sw_launch_stage_experts(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, const fl
                             float *sh_out);
 // the shared expert on the VALU (sw_shared.h): h[S, Is] = silu(Wg x) * (Wu x)
 // and out[S, D] = Wd h, bf16 weights, f32 activations
+// the shared expert of a batch over token tiles (k_shared.hip): h = silu(Wg x) * (Wu x); out = Wd h
 int sw_launch_sh_glu(hipStream_t st, const uint16_t *Wg, const uint16_t *Wu, const float *x, int S, int D, int Is, float *h);
 int sw_launch_sh_down(hipStream_t st, const uint16_t *Wd, const float *h, int S, int Is, int D, float *out);
 // synthetic data

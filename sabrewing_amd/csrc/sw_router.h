@@ -33,14 +33,6 @@ struct RouterArgs {
     float *scores;             // [S, E] sigmoid / softplus scores (act != 1) or null
     sw_u32x4 *xl;              // dot8 limbs of x, or null
     float *xs;
-    // gate + top-k by the last router block of each token (cnt non-null):
-    // cnt[s] counts the token's finished blocks (0 between launches; the last
-    // block resets it), picks and weights to sel/w [S, K]
-    int *cnt;
-    int K, use_bias, norm;
-    const float *bias;         // selection bias (e_score_correction_bias) or null
-    int *sel;
-    float *w;
 };
 // experts per router block of nt threads: 4 (ONE: wave 0 runs the chains,
 // the other waves stage x -- the router spread over as many CUs as there are
@@ -50,8 +42,8 @@ __host__ __device__ inline int router_epb(int one, int nt) { return one ? 4 : 4 
 __host__ inline int router_one(int S, int E) { return (int64_t)S * ((E + 3) / 4) <= 256; }
 
 // block bx (of nbx per token) of token s; smem: the dynamic LDS (router_lds
-// bytes); NP > 0: E <= 64 NP and the token's gate + top-k by its last block
-template <int BF16, int NP, int ONE>
+// bytes)
+template <int BF16, int ONE>
 __device__ __forceinline__ void router_block(const RouterArgs &R, int bx, int s, int nbx, float *smem) {
     constexpr int P = BF16 ? 8 : 4;
     __shared__ uint64_t tab[32];                     // expf table for the sigmoid / softplus scores
@@ -180,33 +172,6 @@ __device__ __forceinline__ void router_block(const RouterArgs &R, int bx, int s,
         for (int g = bx * 2 * nw + (tid >> 5); g < G; g += nbx * 2 * nw) {
             const int k = g * SW_RG + (tid & 31);
             limbs_group(xt[(k & 15) * ML + (k >> 4)], tid & 31, R.xl + ((int64_t)s * G + g) * SW_NL, R.xs + (int64_t)s * G + g);
-        }
-    }
-    if constexpr (NP > 0) {
-        // the last of the token's nbx blocks routes it: every block publishes its
-        // logits (device-scope release, then one arrival count); the block that
-        // counts last acquires them all and runs the gate + top-k on one wave
-        __shared__ int last;
-        __threadfence();
-        __syncthreads();
-        if (tid == 0) last = atomicAdd(R.cnt + s, 1) == nbx - 1;
-        __syncthreads();
-        TR_MARKK(0, 2);
-        if (last) {
-            __threadfence();
-            TR_MARKK(0, 3);
-            if (tid < 64) {
-                int sk;
-                float wk;
-                gate_topk_wave<NP>((act == 1 ? R.logits : R.scores) + (int64_t)s * E, E, R.K, act, R.bias, R.use_bias,
-                                   R.norm, tab, sk, wk);
-                if (tid < R.K) {
-                    R.sel[(int64_t)s * R.K + tid] = sk;
-                    R.w[(int64_t)s * R.K + tid] = wk;
-                }
-                if (tid == 0) R.cnt[s] = 0;
-            }
-            TR_MARKK(0, 7);
         }
     }
 }

@@ -126,8 +126,8 @@ def test_device_x_generator(be, orc):
 
 @pytest.mark.parametrize("S_", [1, 5])
 def test_graph_replay_matches_eager(be, orc, S_):
-    """a recorded forward (shared-expert fork/join included) replays bit-identical
-    to the eager call, every time, with eager work and syncs between replays"""
+    """a recorded forward replays bit-identical to the eager call, every time,
+    with eager work and syncs between replays"""
     cfg = SMALL[2]
     L = synth.make_layer(orc, cfg, 51)
     dl = DeviceLayer.from_host(be, cfg, L)
