@@ -71,12 +71,18 @@ int    lag_hip_moe_group_g(float *acc, const float *x, const void *gu_q, const f
                            int S, int K, int I, int D, int gs);
 
 /* ---------------- 3. device-resident MoE block ---------------- */
-enum { LAG_HIP_ROUTE_SIGMOID = 0, LAG_HIP_ROUTE_SOFTMAX = 1, LAG_HIP_ROUTE_SOFTPLUS = 2 };
+enum { LAG_HIP_ROUTE_SIGMOID = 0, LAG_HIP_ROUTE_SOFTMAX = 1, LAG_HIP_ROUTE_SOFTPLUS = 2,
+       LAG_HIP_ROUTE_SOFTMAX_OLMOE = 3, LAG_HIP_ROUTE_SOFTMAX_QWEN = 4 };
 enum { LAG_HIP_SHARED_NONE = 0, LAG_HIP_SHARED_UNSCALED = 1 };
 
-/* MoeDesc (c/moe_arch.h:33-41) plus the layer shape.  route_act SOFTPLUS
- * (x > 20 ? x : log1pf(expf(x)), c/moe_math.h:54) is an extension; the
- * reference wires SIGMOID and SOFTMAX, shared NONE and UNSCALED. */
+/* MoeDesc (c/moe_arch.h:33-41) plus the layer shape.  route_act: SIGMOID and
+ * SOFTMAX are moe_block's (c/moe_block.h:24-26); the others are extensions:
+ * SOFTPLUS x > 20 ? x : log1pf(expf(x)) (c/moe_math.h:54); SOFTMAX_OLMOE the
+ * OLMoE engine's routing (float-sum softmax, each probability divided by the
+ * sum, c/olmoe.c:212-216, 607-632; norm_topk as moe_block's); SOFTMAX_QWEN
+ * qwen35's moe_route (double-sum softmax, (float)(p / sum) in double, the
+ * picks always renormalised in double, c/qwen35.c:558-589; norm_topk and the
+ * correction bias unused).  The reference wires shared NONE and UNSCALED. */
 typedef struct {
     int   n_experts, topk, route_act, use_corr_bias, norm_topk;
     float route_scale;

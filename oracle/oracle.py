@@ -60,6 +60,8 @@ class Oracle:
         for f in ("sw_siluf", "sw_softplusf", "sw_sigmoidf"):
             getattr(L, f).restype = C.c_float; getattr(L, f).argtypes = [C.c_float]
         L.sw_softmax_row.argtypes = [F32P, C.c_int]
+        L.sw_softmax_row_olmoe.argtypes = [F32P, C.c_int]
+        L.sw_moe_route_qwen.argtypes = [F32P, C.c_int, C.c_int, I32P, F32P]
         L.sw_expf_array.argtypes = [F32P, F32P, C.c_int64]
         L.sw_log1pf_array.argtypes = [F32P, F32P, C.c_int64]
         L.sw_moe_topk.argtypes = [F32P, C.c_void_p, C.c_int, C.c_int, C.c_int, I32P]
@@ -68,6 +70,7 @@ class Oracle:
         L.sw_moe_route.argtypes = [C.POINTER(SwMoeDesc), C.POINTER(SwMoeLayer), F32P, C.c_int, C.c_int,
                                    C.c_void_p, I32P, F32P]
         L.sw_moe_block_rows.argtypes = [C.POINTER(SwMoeDesc), C.POINTER(SwMoeLayer), F32P, F32P, C.c_int, C.c_int]
+        L.sw_route_logits.argtypes = [C.POINTER(SwMoeDesc), F32P, C.c_int, I32P, F32P]
         L.sw_moe_group_rows.argtypes = [C.POINTER(SwMoeDesc), C.POINTER(SwMoeLayer), F32P, F32P, C.c_int, C.c_int]
         L.sw_bucket.restype = C.c_int
         L.sw_bucket.argtypes = [I32P, C.c_int, C.c_int, C.c_int, I32P, I32P, I32P, I32P, I32P]
@@ -138,6 +141,24 @@ class Oracle:
         self.lib.sw_softmax_row(x, x.size)
         return x
 
+    def softmax_row_olmoe(self, x):
+        x = np.ascontiguousarray(x, np.float32).copy()
+        self.lib.sw_softmax_row_olmoe(x, x.size)
+        return x
+
+    def route_qwen(self, logits, K):
+        sel = np.empty(K, np.int32); w = np.empty(K, np.float32)
+        self.lib.sw_moe_route_qwen(np.ascontiguousarray(logits, np.float32), logits.size, K, sel, w)
+        return sel, w
+
+    def route_logits(self, desc, logits):
+        """gate + top-k of given logits [S, E] under desc (no correction bias)"""
+        d, _ = self.make(desc, None)
+        S = logits.shape[0]
+        sel = np.empty((S, desc.K), np.int32); w = np.empty((S, desc.K), np.float32)
+        self.lib.sw_route_logits(C.byref(d), np.ascontiguousarray(logits, np.float32), S, sel, w)
+        return sel, w
+
     def expf(self, x):
         x = np.ascontiguousarray(x, np.float32); y = np.empty_like(x)
         self.lib.sw_expf_array(y, x, x.size)
@@ -167,6 +188,8 @@ class Oracle:
     def make(desc, layer):
         d = SwMoeDesc(desc.E, desc.K, desc.route_act, desc.use_corr_bias, desc.norm_topk,
                       desc.route_scale, desc.shared_mode)
+        if layer is None:
+            return d, None
         L = SwMoeLayer(layer.D, layer.I, layer.Is, layer.E, layer.gs, int(layer.router_bf16), 0,
                        _ptr(layer.router), _ptr(layer.corr_bias), _ptr(layer.logit_bias),
                        _ptr(layer.gu_q), _ptr(layer.dn_q), _ptr(layer.gu_s), _ptr(layer.dn_s),
@@ -326,3 +349,37 @@ class RefLagunaHip:
             np.ascontiguousarray(x, np.float32), h, x.shape[0], group)
         assert rc == 0
         return h
+
+
+class RefCallers:
+    """The OLMoE and qwen35 engines' routing from their own sources
+    (oracle/_ref/libref_olmoe_*.so, libref_qwen35_*.so)."""
+
+    def __init__(self):
+        self.olmoe = C.CDLL(os.path.join(HERE, "_ref", "libref_olmoe_avx512.so"))
+        self.qwen = C.CDLL(os.path.join(HERE, "_ref", "libref_qwen35_avx512.so"))
+        self.olmoe.ref_olmoe_route.argtypes = [F32P, C.c_int, C.c_int, C.c_int, I32P, F32P]
+        self.olmoe.ref_olmoe_softmax_row.argtypes = [F32P, C.c_int]
+        self.qwen.ref_qwen35_route.argtypes = [F32P, C.c_int, C.c_int, I32P, F32P]
+
+    @staticmethod
+    def available():
+        return all(os.path.exists(os.path.join(HERE, "_ref", f)) for f in
+                   ("libref_olmoe_avx512.so", "libref_qwen35_avx512.so"))
+
+    def olmoe_route(self, logits, K, norm):
+        E = logits.size
+        sel = np.empty(K, np.int32); w = np.empty(K, np.float32)
+        self.olmoe.ref_olmoe_route(np.ascontiguousarray(logits, np.float32), E, K, norm, sel, w)
+        return sel, w
+
+    def olmoe_softmax_row(self, x):
+        x = np.ascontiguousarray(x, np.float32).copy()
+        self.olmoe.ref_olmoe_softmax_row(x, x.size)
+        return x
+
+    def qwen_route(self, logits, K):
+        E = logits.size
+        sel = np.empty(K, np.int32); w = np.empty(K, np.float32)
+        self.qwen.ref_qwen35_route(np.ascontiguousarray(logits, np.float32), E, K, sel, w)
+        return sel, w

@@ -361,6 +361,34 @@ void sw_softmax_row(float *x, int n) {
     float inv = (float)(1.0 / s); for (int i = 0; i < n; i++) x[i] *= inv;
 }
 
+/* OLMoE's softmax_row (c/olmoe.c:212-216): max from -1e30 by a strict scan,
+ * expf(x-m) summed in float in order, each term divided by the sum */
+void sw_softmax_row_olmoe(float *x, int n) {
+    float m = -1e30f; for (int i = 0; i < n; i++) if (x[i] > m) m = x[i];
+    float s = 0; for (int i = 0; i < n; i++) { x[i] = expf(x[i] - m); s += x[i]; }
+    for (int i = 0; i < n; i++) x[i] /= s;
+}
+
+/* qwen35's moe_route (c/qwen35.c:558-589): max from -inf by a strict scan,
+ * expf(x-mx) summed in double, p = (float)(p / sum) in double; K passes over
+ * the unused experts keeping the first, replaced by a strictly larger p (ties
+ * -> lowest id); w = p of the picks, renormalised by their double sum */
+void sw_moe_route_qwen(const float *logit, int E, int K, int *sel, float *w) {
+    float *p = (float *)malloc((size_t)E * sizeof(float));
+    unsigned char *used = (unsigned char *)calloc((size_t)E, 1);
+    float mx = -INFINITY; for (int e = 0; e < E; e++) if (logit[e] > mx) mx = logit[e];
+    double sum = 0; for (int e = 0; e < E; e++) { p[e] = expf(logit[e] - mx); sum += p[e]; }
+    for (int e = 0; e < E; e++) p[e] = (float)(p[e] / sum);
+    for (int a = 0; a < K; a++) {
+        int best = -1;
+        for (int e = 0; e < E; e++) { if (used[e]) continue; if (best < 0 || p[e] > p[best]) best = e; }
+        used[best] = 1; sel[a] = best; w[a] = p[best];
+    }
+    double tot = 0; for (int a = 0; a < K; a++) tot += w[a];
+    for (int a = 0; a < K; a++) w[a] = (float)(w[a] / tot);
+    free(p); free(used);
+}
+
 /* c/moe_arch.h:64-89: K passes, strict > from -1e30 (ties -> lowest id), bias
  * for selection only, all-non-finite -> lowest unselected expert */
 void sw_moe_topk(const float *score, const float *corr_bias, int use_bias, int E, int K, int *sel) {
@@ -409,12 +437,27 @@ static void router_logits(const SwMoeLayer *L, const float *x, int S, int mode, 
 /* moe_block.h:115-122 (and c/laguna.c:697-706 per row) */
 static void route_row(const SwMoeDesc *d, const SwMoeLayer *L, float *rl, float *sc, int *sel, float *w) {
     int E = d->n_experts, K = d->topk;
-    if (d->route_act == SW_ROUTE_SOFTMAX) { sw_softmax_row(rl, E); for (int e = 0; e < E; e++) sc[e] = rl[e]; }
+    if (d->route_act == SW_ROUTE_SOFTMAX_QWEN) { sw_moe_route_qwen(rl, E, K, sel, w); return; }
+    if (d->route_act == SW_ROUTE_SOFTMAX_OLMOE) {   /* c/olmoe.c:607-632: softmax_row, the moe_topk scan, norm */
+        sw_softmax_row_olmoe(rl, E); for (int e = 0; e < E; e++) sc[e] = rl[e];
+    } else if (d->route_act == SW_ROUTE_SOFTMAX) { sw_softmax_row(rl, E); for (int e = 0; e < E; e++) sc[e] = rl[e]; }
     else if (d->route_act == SW_ROUTE_SOFTPLUS) { for (int e = 0; e < E; e++) sc[e] = sw_softplusf(rl[e]); }
     else for (int e = 0; e < E; e++) sc[e] = 1.f / (1.f + expf(-rl[e]));
     sw_moe_topk(sc, L->corr_bias, d->use_corr_bias, E, K, sel);
     for (int a = 0; a < K; a++) w[a] = sc[sel[a]];
     if (d->norm_topk) { float sm = 0; for (int a = 0; a < K; a++) sm += w[a]; for (int a = 0; a < K; a++) w[a] /= sm; }
+}
+
+/* the gate + top-k of S rows of given logits (route_row on a copy of each) */
+void sw_route_logits(const SwMoeDesc *d, const float *logits, int S, int *sel, float *w) {
+    int E = d->n_experts, K = d->topk;
+    SwMoeLayer L; memset(&L, 0, sizeof L); L.E = E;
+    float *rl = (float *)malloc((size_t)E * sizeof(float)), *sc = (float *)malloc((size_t)E * sizeof(float));
+    for (int s = 0; s < S; s++) {
+        memcpy(rl, logits + (int64_t)s * E, (size_t)E * sizeof(float));
+        route_row(d, &L, rl, sc, sel + s * K, w + s * K);
+    }
+    free(rl); free(sc);
 }
 
 void sw_moe_route(const SwMoeDesc *d, const SwMoeLayer *L, const float *x, int S,

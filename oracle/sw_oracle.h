@@ -64,12 +64,15 @@ float sw_siluf(float x);
 float sw_softplusf(float x);
 float sw_sigmoidf(float x);
 void  sw_softmax_row(float *x, int n);
+void  sw_softmax_row_olmoe(float *x, int n);
+void  sw_moe_route_qwen(const float *logit, int E, int K, int *sel, float *w);
 void  sw_moe_topk(const float *score, const float *corr_bias, int use_bias, int E, int K, int *sel);
 void  sw_rmsnorm_row(float *out, const float *x, const float *w, int D, float eps);
 int   sw_argmax(const float *v, int n);
 
 /* ---------------- MoE block ---------------- */
-enum { SW_ROUTE_SIGMOID = 0, SW_ROUTE_SOFTMAX = 1, SW_ROUTE_SOFTPLUS = 2 };
+enum { SW_ROUTE_SIGMOID = 0, SW_ROUTE_SOFTMAX = 1, SW_ROUTE_SOFTPLUS = 2, SW_ROUTE_SOFTMAX_OLMOE = 3,
+       SW_ROUTE_SOFTMAX_QWEN = 4 };
 enum { SW_SHARED_NONE = 0, SW_SHARED_UNSCALED = 1 };
 
 typedef struct {
@@ -98,6 +101,8 @@ typedef struct {
 enum { SW_MODE_F32 = 0, SW_MODE_IDOT = 1, SW_MODE_EXACT = 2 };
 
 /* routing for S rows: logits (optional out), sel [S*K], w [S*K] */
+/* gate + top-k of S rows of given logits [S,E] (no corr_bias) */
+void sw_route_logits(const SwMoeDesc *d, const float *logits, int S, int *sel, float *w);
 void sw_moe_route(const SwMoeDesc *d, const SwMoeLayer *L, const float *x, int S,
                   int mode, float *logits, int *sel, float *w);
 /* per-token moe_block for each of S rows: out[s] += MoE(x[s]) */

@@ -19,6 +19,8 @@ scale layout).  Weights N(0, 0.02), activations N(0, 1).
 from dataclasses import dataclass, replace
 
 ROUTE_SIGMOID, ROUTE_SOFTMAX, ROUTE_SOFTPLUS = 0, 1, 2
+# other callers' routing contracts (c/olmoe.c:607-632; c/qwen35.c:558-589)
+ROUTE_SOFTMAX_OLMOE, ROUTE_SOFTMAX_QWEN = 3, 4
 SHARED_NONE, SHARED_UNSCALED = 0, 1
 WEIGHT_SIGMA = 0.02
 
@@ -81,7 +83,13 @@ C5_LAYER = MoeConfig("C5-inkling-small", D=4096, E=256, K=8, I=1536, Is=0, route
                      use_corr_bias=0, norm_topk=0, route_scale=1.0, shared_mode=SHARED_NONE)
 C5_LAYERS, C5_BATCH, C5_VOCAB = 48, 8, 32000
 
-CONFIGS = {c.name: c for c in (C1, C2, C2_SIGMOID, C4_ZIPF, C5_LAYER)}
+# C1 routed as the OLMoE engine routes it; a qwen35-style layer (int4 experts through
+# lag_cuda_moe_group, softmax top-8 renormalised in double, c/qwen35.c:600-640)
+C1_OLMOE = replace(C1, name="C1-olmoe-engine-routing", route_act=ROUTE_SOFTMAX_OLMOE, norm_topk=1)
+QWEN = MoeConfig("qwen35-moe", D=2048, E=256, K=8, I=512, Is=0, route_act=ROUTE_SOFTMAX_QWEN,
+                 use_corr_bias=0, norm_topk=0, route_scale=1.0, shared_mode=SHARED_NONE, router_bf16=False,
+                 x_bf16=False)
+CONFIGS = {c.name: c for c in (C1, C2, C2_SIGMOID, C4_ZIPF, C5_LAYER, C1_OLMOE, QWEN)}
 
 
 def scaled(cfg, D=None, E=None, K=None, I=None, Is=None, name=None):

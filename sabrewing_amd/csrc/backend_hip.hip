@@ -489,7 +489,7 @@ extern "C" int lag_hip_moe_forward(const LagHipMoeDesc *d, const LagHipMoeWeight
     // one token with E <= 256: its gate + top-k runs in every block of the
     // expert stage (no device-scope handoff); otherwise a gate + top-k launch
     // after the routing stage
-    const bool in_experts = E <= 256 && S == 1;
+    const bool in_experts = E <= 256 && S == 1 && d->route_act <= 2;   // (the block top-k takes acts 0-2)
     // S == 1: the shared expert's gate_up and down run as extra blocks of stages 1 and 2;
     // S > 1: as kernels of their own over token tiles (the same arithmetic per token)
     const bool sh_in = sh && S == 1;
@@ -508,7 +508,7 @@ extern "C" int lag_hip_moe_forward(const LagHipMoeDesc *d, const LagHipMoeWeight
     if (S == 1) {                        // one token: its K picks in rank order, fused down + combine
         { PROF("stage_experts");
           if (sw_launch_stage_experts(g_st, gu, f.xl, f.xs, SwGroups{}, I, f.hl, f.hs, f.sel, K,
-                                      in_experts ? (d->route_act == 1 ? f.logits : f.scores) : nullptr, E, d->route_act,
+                                      in_experts ? (sw_act_softmax(d->route_act) ? f.logits : f.scores) : nullptr, E, d->route_act,
                                       w->corr_bias, d->use_corr_bias, d->norm_topk, f.w, sd, f.shh, S, Is, D, f.sout))
               return fail_msg("expert stage launch"); }
         { PROF("q4_down_combine");

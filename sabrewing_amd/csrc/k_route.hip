@@ -43,7 +43,7 @@ __global__ __launch_bounds__(64) void k_gate_topk(const float *__restrict__ logi
     const int lane = threadIdx.x, s = blockIdx.x;
     int sk;
     float wk;
-    gate_topk_wave<NPER>((act == 1 ? logits : scores) + (int64_t)s * E, E, K, act, bias, use_bias, norm, tab, sk, wk);
+    gate_topk_wave<NPER>((sw_act_softmax(act) ? logits : scores) + (int64_t)s * E, E, K, act, bias, use_bias, norm, tab, sk, wk);
     if (lane < K) { sel_all[(int64_t)s * K + lane] = sk; w_all[(int64_t)s * K + lane] = wk; }
 }
 
@@ -60,7 +60,7 @@ int sw_launch_router_topk(hipStream_t st, const void *Wc, int w_bf16, const floa
                           const float *corr_bias, int use_corr_bias, int norm_topk, int *sel, float *w,
                           sw_u32x4 *xl, float *xs) {
     if (D % 128 || D > 16384 || E <= 0 || E > TK_MAXE || S <= 0 || K <= 0 || K > 64 || K > E) return -1;
-    if (route_act < 0 || route_act > 2 || (sel && route_act != 1 && !scores)) return -1;
+    if (route_act < 0 || route_act > 4 || (sel && !sw_act_softmax(route_act) && !scores)) return -1;
     // four experts per block (wave 0; the others stage x) while that stays within 256 blocks,
     // else four per wave of eight
     const int nt = 512, one = router_one(S, E), epb = router_epb(one, nt);
@@ -81,8 +81,8 @@ int sw_launch_router_topk(hipStream_t st, const void *Wc, int w_bf16, const floa
 
 int sw_launch_gate_topk(hipStream_t st, const float *logits, const float *scores, int S, int E, int K, int route_act,
                         const float *corr_bias, int use_corr_bias, int norm_topk, int *sel, float *w) {
-    if (E <= 0 || E > TK_MAXE || S <= 0 || K <= 0 || K > 64 || K > E || route_act < 0 || route_act > 2) return -1;
-    if (route_act != 1 && !scores) return -1;
+    if (E <= 0 || E > TK_MAXE || S <= 0 || K <= 0 || K > 64 || K > E || route_act < 0 || route_act > 4) return -1;
+    if (!sw_act_softmax(route_act) && !scores) return -1;
     const int nper = (E + 63) / 64;
 #define SW_GATE(NP) SW_LAUNCH(k_gate_topk<NP>, dim3((unsigned)S), dim3(64), 0, st, logits, scores, E, K, route_act, \
                                        corr_bias, use_corr_bias, norm_topk, sel, w)

@@ -95,7 +95,7 @@ __device__ __forceinline__ float lanef(float v, int l) {
 }
 
 // The routing of one token, by the 64 lanes of one wave (no block barrier):
-// src is the token's logits (act == 1) or its sigmoid/softplus scores; tab is
+// src is the token's logits (a softmax act: 1, 3, 4) or its sigmoid/softplus scores; tab is
 // 32 words of LDS for the expf table (softmax).  On return lane a < K holds
 // pick a (rank order) in sk and its weight in wk.
 template <int NPER>   // expert slots per lane: E <= 64 * NPER
@@ -104,8 +104,8 @@ __device__ void gate_topk_wave(const float *__restrict__ src, int E, int K, int 
     const int lane = threadIdx.x & 63;
     float v[NPER], b[NPER];
     // every load of the token issued before any is used (clamped indices)
-    if (act == 1 && lane < 32) tab[lane] = sw_exp2f_tab[lane];
-    const bool hasb = use_bias && bias;
+    if ((act == 1 || act == 3 || act == 4) && lane < 32) tab[lane] = sw_exp2f_tab[lane];
+    const bool hasb = use_bias && bias && act != 4;       // qwen35 selects on the probabilities alone
 #pragma unroll
     for (int i = 0; i < NPER; i++) {
         const int e = min(lane + 64 * i, E - 1);
@@ -113,7 +113,7 @@ __device__ void gate_topk_wave(const float *__restrict__ src, int E, int K, int 
         b[i] = hasb ? bias[e] : 0.f;
     }
     TR_MARKK(0, 4);
-    if (act == 1) {                                   // softmax
+    if (act == 1) {                                   // softmax (c/moe_math.h:68-72)
         wave_sync();
         float mx = -__builtin_inff();
         bool any = false;
@@ -134,6 +134,37 @@ __device__ void gate_topk_wave(const float *__restrict__ src, int E, int K, int 
         const float inv = (float)(1.0 / sum);
 #pragma unroll
         for (int i = 0; i < NPER; i++) v[i] = v[i] * inv;
+    } else if (act == 3 || act == 4) {
+        // act 3: OLMoE's softmax_row (c/olmoe.c:212-216): max from -1e30 by a strict
+        // scan, a float sum in expert order, each term divided by it.
+        // act 4: qwen35's moe_route (c/qwen35.c:570-574): max from -inf by a
+        // strict scan, a double sum in expert order, each term (float)(p / sum)
+        // in double.  A strict scan skips NaN: the maximum of the other keys.
+        wave_sync();
+        float mx = act == 3 ? -1e30f : -__builtin_inff();
+#pragma unroll
+        for (int i = 0; i < NPER; i++) {
+            const int e = lane + 64 * i;
+            if (e < E && v[i] > mx) mx = v[i];
+        }
+        for (int o = 32; o; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+#pragma unroll
+        for (int i = 0; i < NPER; i++) v[i] = sw_expf_t(v[i] - mx, tab);
+        if (act == 3) {
+            float sum = 0.f;
+#pragma unroll
+            for (int i = 0; i < NPER; i++)
+                for (int l = 0; l < 64 && l + 64 * i < E; l++) sum += lanef(v[i], l);
+#pragma unroll
+            for (int i = 0; i < NPER; i++) v[i] = v[i] / sum;
+        } else {
+            double sum = 0.0;
+#pragma unroll
+            for (int i = 0; i < NPER; i++)
+                for (int l = 0; l < 64 && l + 64 * i < E; l++) sum += (double)lanef(v[i], l);
+#pragma unroll
+            for (int i = 0; i < NPER; i++) v[i] = (float)((double)v[i] / sum);
+        }
     }
     uint32_t ko[NPER];                                // order key, 0 = invalid or taken (valid keys order above 0)
     bool fr[NPER];
@@ -180,7 +211,11 @@ __device__ void gate_topk_wave(const float *__restrict__ src, int E, int K, int 
         if (lane == a) { sk = bi; wk = wb; }
     }
     TR_MARKK(0, 6);
-    if (norm) {                                       // renormalised: summed in rank order
+    if (act == 4) {                                   // qwen35: always, in double (c/qwen35.c:585-587)
+        double tot = 0.0;
+        for (int a = 0; a < K; a++) tot += (double)lanef(wk, a);
+        wk = (float)((double)wk / tot);
+    } else if (norm) {                                // renormalised: summed in rank order
         float sm = 0.f;
         for (int a = 0; a < K; a++) sm += lanef(wk, a);
         wk = wk / sm;

@@ -104,6 +104,10 @@ struct SwGroups {
     const int *P;
 };
 #define SW_DG_TT 2             // tokens per weight pass of the grouped dot8 kernels
+// route activations whose gate is a softmax of the logits (computed with the
+// top-k): 1 moe_block's, 3 OLMoE's, 4 qwen35's; 0 sigmoid and 2 softplus come
+// as scores from the router
+__host__ __device__ inline bool sw_act_softmax(int act) { return act == 1 || act == 3 || act == 4; }
 // the upper bound of the passes of T packed rows in at most min(T, E) groups, tt tokens each
 __host__ __device__ inline int sw_npass_max(int T, int E, int tt) { return (T + (T < E ? T : E) * (tt - 1)) / tt; }
 // XCD-aware block order: launches deal consecutive block ids to the 8 XCDs in

@@ -30,7 +30,7 @@ struct RouterArgs {
     const float *lbias;        // logit bias or null
     float *logits;             // [S, E]
     int act;
-    float *scores;             // [S, E] sigmoid / softplus scores (act != 1) or null
+    float *scores;             // [S, E] sigmoid / softplus scores (act 0, 2) or null
     sw_u32x4 *xl;              // dot8 limbs of x, or null
     float *xs;
 };
@@ -164,7 +164,7 @@ __device__ __forceinline__ void router_block(const RouterArgs &R, int bx, int s,
     if (j == 0 && valid) {
         if (R.lbias) v = v + R.lbias[e];
         R.logits[(int64_t)s * E + e] = v;
-        if (act != 1 && R.scores)
+        if (!sw_act_softmax(act) && R.scores)
             R.scores[(int64_t)s * E + e] = (act == 2) ? sw_softplus_ref_t(v, tab) : sw_sigmoid_ref_t(v, tab);
     }
     if (!ONE && R.xl) {                               // the token's dot8 limbs, half a wave per group, from xt

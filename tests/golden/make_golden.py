@@ -8,6 +8,9 @@ Writes one .npz per case into this directory:
     packed low nibble first, scales {1, 0.25}, x[0:4] of that test, result
     {-34, -2.5}; evaluated again here by the compiled reference's matmul_q4_k
     (F32 and exact modes).
+  - route_callers.npz: the routing of the OLMoE engine (c/olmoe.c:607-632)
+    and of qwen35 (moe_route, c/qwen35.c:558-589), from their own compiled
+    sources, on rows of logits with ties, NaN, -inf and huge values.
   - moe_<case>.npz: a seeded small layer of each contract.  The layer is not
     stored: its seeds are, and oracle/synth.py regenerates it bit for bit.
     Stored: the config, the seeds, the token rows x, the residual out0, and the
@@ -31,7 +34,7 @@ ROOT = os.path.dirname(os.path.dirname(HERE))
 sys.path.insert(0, ROOT)
 
 from oracle import synth                      # noqa: E402
-from oracle.oracle import Oracle, Ref         # noqa: E402
+from oracle.oracle import Oracle, Ref, RefCallers   # noqa: E402
 from sabrewing_amd import configs as cf       # noqa: E402
 
 # (base config, scaled shape, seed, rows, corr-bias sigma)
@@ -76,6 +79,22 @@ def main():
     got_exact = ref.matmul_q4(x, q4.reshape(2, 2), s4, 0, 1)
     assert np.array_equal(got_f32, want) and np.array_equal(got_exact, want), (got_f32, got_exact)
     np.savez(os.path.join(HERE, "kat_q4_rows.npz"), x=x, q4=q4, s4=s4, want=want)
+
+    rc = RefCallers()
+    rng = np.random.default_rng(1707)
+    E, K = 64, 8
+    rows = [(rng.standard_normal(E) * s).astype(np.float32) for s in (0.5, 3.0, 30.0)]
+    t = (rng.standard_normal(E) * 2).astype(np.float32); t[::3] = t[0]; rows.append(t)
+    r = rng.standard_normal(E).astype(np.float32); r[7] = np.nan; rows.append(r)
+    r = rng.standard_normal(E).astype(np.float32); r[:16] = -np.inf; rows.append(r)
+    rows.append(np.full(E, -1e31, np.float32))
+    lg = np.stack(rows)
+    ol = [rc.olmoe_route(row, K, norm) for norm in (0, 1) for row in lg]
+    qw = [rc.qwen_route(row, K) for row in lg]
+    np.savez(os.path.join(HERE, "route_callers.npz"), logits=lg, K=np.int64(K),
+             olmoe_sel=np.stack([s for s, _ in ol]).reshape(2, len(lg), K),
+             olmoe_w=np.stack([w for _, w in ol]).reshape(2, len(lg), K),
+             qwen_sel=np.stack([s for s, _ in qw]), qwen_w=np.stack([w for _, w in qw]))
 
     for name in CASES:
         cfg, seed, rows, cb = case_config(name)

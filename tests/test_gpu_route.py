@@ -53,6 +53,9 @@ CASES = [
     (cf.C4_ZIPF, 0.0),                                             # skew: logit bias
     (cf.C5_LAYER, 0.0),                                            # softmax over 256
     (replace(cf.C2_SIGMOID, name="C2-sigmoid-nonorm", norm_topk=0), 0.02),
+    (cf.C1_OLMOE, 0.0),                                            # OLMoE engine: float-sum softmax, divide
+    (replace(cf.C1_OLMOE, name="C1-olmoe-nonorm", norm_topk=0), 0.0),
+    (cf.QWEN, 0.0),                                                # qwen35: double softmax, double renorm
 ]
 
 

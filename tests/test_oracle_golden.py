@@ -36,6 +36,7 @@ def bits(a):
 def test_fixture_set_complete():
     assert set(CASES) >= {"c1_small", "c2_sigmoid_small", "c5_small", "c2_sigmoid_mid", "c4_zipf_sigmoid_small"}
     assert os.path.exists(os.path.join(GOLD, "kat_q4_rows.npz"))
+    assert os.path.exists(os.path.join(GOLD, "route_callers.npz"))
 
 
 def test_kat_q4_rows(orc):
@@ -85,3 +86,22 @@ def test_planted_mistake_is_caught(orc):
     L.dn_s = L.dn_s.copy()
     L.dn_s[e * cfg.D * ngI:(e * cfg.D + 1) * ngI] *= -1
     assert not np.array_equal(bits(orc.moe_block_rows(d, L, g["x"][:1], g["out0"][:1])), bits(g["out"][:1]))
+
+
+def test_callers_routing_golden(orc):
+    """A17: OLMoE's and qwen35's routing against the fixtures their own
+    compiled sources wrote (tests/golden/route_callers.npz)"""
+    g = np.load(os.path.join(GOLD, "route_callers.npz"))
+    lg, K = g["logits"], int(g["K"])
+    E = lg.shape[1]
+    for norm in (0, 1):
+        d = synth.Desc(E, K, cf.ROUTE_SOFTMAX_OLMOE, 0, norm, 1.0, 0)
+        sel, w = orc.route_logits(d, lg)
+        assert np.array_equal(sel, g["olmoe_sel"][norm]) and np.array_equal(bits(w), bits(g["olmoe_w"][norm]))
+    d = synth.Desc(E, K, cf.ROUTE_SOFTMAX_QWEN, 0, 0, 1.0, 0)
+    sel, w = orc.route_logits(d, lg)
+    assert np.array_equal(sel, g["qwen_sel"]) and np.array_equal(bits(w), bits(g["qwen_w"]))
+    # closed forms: qwen's weights sum to 1 in double within a float rounding each; picks distinct
+    assert all(len(set(r)) == K for r in sel)
+    ok = np.isfinite(w).all(axis=1)
+    assert np.allclose(w[ok].astype(np.float64).sum(axis=1), 1.0, atol=1e-6)

@@ -106,3 +106,40 @@ def test_laguna_engine_path(orc):
     assert bits_equal(orc.moe_block_rows(d, L, x[:1], h0[:1]), lag.moe_rows(d, L, x[:1], h0[:1]))
     for mode in (2,):                                # g_exact: the double-accumulate kernels
         assert bits_equal(orc.moe_block_rows(d, L, x, h0, mode), lag.moe_rows(d, L, x, h0, exact=1, group=0))
+
+
+def _logit_sets(rng, E):
+    """random rows, rows with exact ties, a NaN row, -inf entries, huge logits"""
+    rows = [(rng.standard_normal(E) * s).astype(np.float32) for s in (0.5, 3.0, 30.0)]
+    t = (rng.standard_normal(E) * 2).astype(np.float32)
+    t[::3] = t[0]                                       # ties of the leading value
+    rows.append(t)
+    r = rng.standard_normal(E).astype(np.float32); r[E // 2] = np.nan
+    rows.append(r)
+    r = rng.standard_normal(E).astype(np.float32); r[:E // 4] = -np.inf
+    rows.append(r)
+    rows.append(np.full(E, -1e31, np.float32))          # below OLMoE's -1e30 start
+    rows.append(np.full(E, 5.0, np.float32))            # all equal
+    return np.stack(rows)
+
+
+@pytest.mark.parametrize("E,K", [(64, 8), (256, 8), (60, 6), (8, 8)])
+def test_other_callers_routing_vs_ref(orc, rng, E, K):
+    """A17: the OLMoE engine's routing (c/olmoe.c:607-632) and qwen35's
+    moe_route (c/qwen35.c:558-589), each from its own compiled source"""
+    from oracle.oracle import RefCallers
+    if not RefCallers.available():
+        pytest.skip("compiled reference callers not built")
+    rc = RefCallers()
+    lg = _logit_sets(rng, E)
+    for row in lg:
+        assert bits_equal(orc.softmax_row_olmoe(row), rc.olmoe_softmax_row(row))
+        for norm in (0, 1):
+            d = synth.Desc(E, K, cf.ROUTE_SOFTMAX_OLMOE, 0, norm, 1.0, 0)
+            sel, w = orc.route_logits(d, row[None])
+            rs, rw = rc.olmoe_route(row, K, norm)
+            assert np.array_equal(sel[0], rs) and bits_equal(w[0], rw)
+        d = synth.Desc(E, K, cf.ROUTE_SOFTMAX_QWEN, 0, 0, 1.0, 0)
+        sel, w = orc.route_logits(d, row[None])
+        qs, qw = rc.qwen_route(row, K)
+        assert np.array_equal(sel[0], qs) and bits_equal(w[0], qw)
