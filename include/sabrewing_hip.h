@@ -128,6 +128,22 @@ int    lag_hip_route(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const fl
  * valid until the next forward): G (host out), gexp/gbeg/gcnt [G] host copies */
 int    lag_hip_last_groups(int *G, int *gexp, int *gbeg, int *gcnt, int cap);
 
+/* ---------------- stack glue (device pointers, queued on the backend stream) ----------------
+ * A layer of a stack is h += MoE(rmsnorm(h, w_l)) (lag_hip_rmsnorm, then
+ * lag_hip_moe_forward with x = the normed rows and out = h); a step ends in
+ * rmsnorm, the head and a greedy pick. */
+/* out[s] = x[s] / sqrt(mean(x[s]^2) + eps) * w, the squares summed in double
+ * (rmsnorm_row, c/moe_math.h:58-62); out may be x.  0 = ok */
+int    lag_hip_rmsnorm(const float *x, const float *w, float *out, int S, int D, float eps);
+/* logits[S,V] = x[S,D] . head^T under the 16-lane contract of the head's
+ * resmm -> matmul_bf16 (c/laguna.c:1156-1158; Wc from lag_hip_router_upload
+ * of the [V,D] head), and with tok non-null tok[s] = the greedy pick of
+ * argmax_logits (strict ascending scan: ties to the lowest index,
+ * c/laguna.c:1159).  0 = ok */
+int    lag_hip_head_argmax(const void *Wc, int w_bf16, const float *x, int S, int D, int V, float *logits, int *tok);
+/* tok[s] = argmax_logits' pick over logits[s, 0..V) alone (c/laguna.c:1159).  0 = ok */
+int    lag_hip_argmax(const float *logits, int S, int V, int *tok);
+
 /* ---------------- memory, stream, timing ---------------- */
 void  *lag_hip_alloc(size_t n);
 int    lag_hip_h2d(void *dst, const void *src, size_t n);

@@ -141,6 +141,28 @@ class Oracle:
         self.lib.sw_softmax_row(x, x.size)
         return x
 
+    def rmsnorm_rows(self, x, w, eps):
+        x = np.ascontiguousarray(x, np.float32); w = np.ascontiguousarray(w, np.float32)
+        out = np.empty_like(x)
+        for s in range(x.shape[0]):
+            self.lib.sw_rmsnorm_row(out[s], x[s], w, x.shape[1], eps)
+        return out
+
+    def argmax_rows(self, v):
+        v = np.ascontiguousarray(v, np.float32)
+        return np.array([self.lib.sw_argmax(v[s], v.shape[1]) for s in range(v.shape[0])], np.int32)
+
+    def stack(self, desc, layers, norms, final_norm, head, h0, eps):
+        """h += moe_block(rmsnorm(h, w_l)) per layer, then rmsnorm, the bf16 head
+        (matmul_bf16, the SIMD contract) and the greedy pick: (h, logits, tok)"""
+        h = np.ascontiguousarray(h0, np.float32).copy()
+        for l, L in enumerate(layers):
+            xn = self.rmsnorm_rows(h, norms[l], eps)
+            h = self.moe_block_rows(desc, L, xn, h)
+        xn = self.rmsnorm_rows(h, final_norm, eps)
+        logits = self.matmul_bf16(xn, head)
+        return h, logits, self.argmax_rows(logits)
+
     def softmax_row_olmoe(self, x):
         x = np.ascontiguousarray(x, np.float32).copy()
         self.lib.sw_softmax_row_olmoe(x, x.size)
@@ -279,6 +301,12 @@ class Ref:
         self.lib.ref_moe_topk(np.ascontiguousarray(score, np.float32), _ptr(b), 1 if b is not None else 0,
                               score.size, K, sel)
         return sel
+
+    def rmsnorm_row(self, x, w, eps):
+        out = np.empty(x.size, np.float32)
+        self.lib.ref_rmsnorm_row(out, np.ascontiguousarray(x, np.float32), np.ascontiguousarray(w, np.float32),
+                                 x.size, eps)
+        return out
 
     def moe_block_rows(self, desc, layer, x, out, mode=0, exact=0):
         out = np.ascontiguousarray(out, np.float32).copy()

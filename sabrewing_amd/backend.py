@@ -26,7 +26,8 @@ EXPORTS = [
     "lag_hip_matmul_bf16", "lag_hip_matmul_q4", "lag_hip_expert_q4", "lag_hip_moe_experts", "lag_hip_moe_group",
     "lag_hip_matmul_q4_g", "lag_hip_expert_q4_g", "lag_hip_moe_experts_g", "lag_hip_moe_group_g",
     "lag_hip_router_upload", "lag_hip_router_chain", "lag_hip_moe_forward", "lag_hip_moe_block", "lag_hip_route",
-    "lag_hip_last_groups", "lag_hip_alloc", "lag_hip_h2d", "lag_hip_d2h", "lag_hip_d2d", "lag_hip_memset",
+    "lag_hip_last_groups", "lag_hip_rmsnorm", "lag_hip_head_argmax", "lag_hip_argmax",
+    "lag_hip_alloc", "lag_hip_h2d", "lag_hip_d2h", "lag_hip_d2d", "lag_hip_memset",
     "lag_hip_graph_begin", "lag_hip_graph_end", "lag_hip_graph_launch", "lag_hip_graph_destroy", "lag_hip_sync",
     "lag_hip_event_create", "lag_hip_event_record", "lag_hip_event_elapsed_ms", "lag_hip_event_destroy",
     "lag_hip_profile", "lag_hip_profile_count", "lag_hip_profile_read", "lag_hip_profile_reset",
@@ -92,6 +93,9 @@ def load_library(path=None):
     L.lag_hip_moe_group_g.argtypes = L.lag_hip_moe_group.argtypes + [C.c_int]
     L.lag_hip_router_upload.restype = VP; L.lag_hip_router_upload.argtypes = [VP, C.c_int, C.c_int, C.c_int]
     L.lag_hip_router_chain.argtypes = [VP, VP, C.c_int, C.c_int, C.c_int]
+    L.lag_hip_rmsnorm.argtypes = [VP, VP, VP, C.c_int, C.c_int, C.c_float]
+    L.lag_hip_head_argmax.argtypes = [VP, C.c_int, VP, C.c_int, C.c_int, C.c_int, VP, VP]
+    L.lag_hip_argmax.argtypes = [VP, C.c_int, C.c_int, VP]
     DP, WP = C.POINTER(LagHipMoeDesc), C.POINTER(LagHipMoeWeights)
     L.lag_hip_moe_forward.argtypes = [DP, WP, VP, VP, C.c_int]
     L.lag_hip_moe_block.argtypes = [DP, WP, F32P, F32P, C.c_int]
@@ -233,6 +237,18 @@ class Backend:
         for b in (lg, sel, w):
             b.free()
         return out
+
+    def rmsnorm(self, x_dev, w_dev, out_dev, S, D, eps):
+        self.check(self.lib.lag_hip_rmsnorm(VP(int(x_dev)), VP(int(w_dev)), VP(int(out_dev)), S, D, C.c_float(eps)),
+                   "lag_hip_rmsnorm")
+
+    def head_argmax(self, Wc, w_bf16, x_dev, S, D, V, logits_dev, tok_dev=None):
+        self.check(self.lib.lag_hip_head_argmax(VP(int(Wc)), int(w_bf16), VP(int(x_dev)), S, D, V, VP(int(logits_dev)),
+                                                VP(int(tok_dev)) if tok_dev is not None else None),
+                   "lag_hip_head_argmax")
+
+    def argmax(self, logits_dev, S, V, tok_dev):
+        self.check(self.lib.lag_hip_argmax(VP(int(logits_dev)), S, V, VP(int(tok_dev))), "lag_hip_argmax")
 
     def last_groups(self, cap=4096):
         G = C.c_int(0)

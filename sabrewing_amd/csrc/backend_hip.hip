@@ -542,6 +542,33 @@ extern "C" int lag_hip_moe_forward(const LagHipMoeDesc *d, const LagHipMoeWeight
     return 0;
 }
 
+// ------------------------------------------------------------ stack glue ----
+extern "C" int lag_hip_rmsnorm(const float *x, const float *w, float *out, int S, int D, float eps) {
+    if (!g_ok || fault_injected() || !x || !w || !out) return -1;
+    PROF("rmsnorm");
+    if (sw_launch_rmsnorm(g_st, x, w, out, S, D, eps)) return fail_msg("rmsnorm launch");
+    return 0;
+}
+
+extern "C" int lag_hip_argmax(const float *logits, int S, int V, int *tok) {
+    if (!g_ok || fault_injected() || !logits || !tok) return -1;
+    PROF("argmax");
+    if (sw_launch_argmax(g_st, logits, S, V, tok)) return fail_msg("argmax launch");
+    return 0;
+}
+
+extern "C" int lag_hip_head_argmax(const void *Wc, int w_bf16, const float *x, int S, int D, int V, float *logits, int *tok) {
+    if (!g_ok || fault_injected() || !Wc || !x || !logits || S <= 0 || V <= 0) return -1;
+    { PROF("head_logits");
+      if (sw_launch_router_topk(g_st, Wc, w_bf16, x, S, D, V, nullptr, logits, nullptr, 1, 1, nullptr, 0, 0, nullptr,
+                                nullptr, nullptr, nullptr)) return fail_msg("head launch (shape unsupported?)"); }
+    if (tok) {
+        PROF("argmax");
+        if (sw_launch_argmax(g_st, logits, S, V, tok)) return fail_msg("argmax launch");
+    }
+    return 0;
+}
+
 extern "C" int lag_hip_last_groups(int *G, int *gexp, int *gbeg, int *gcnt, int cap) {
     if (!g_ok) return -1;
     CK(hipStreamSynchronize(g_st), "stream sync");

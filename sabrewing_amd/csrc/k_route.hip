@@ -59,7 +59,8 @@ int sw_launch_router_topk(hipStream_t st, const void *Wc, int w_bf16, const floa
                           const float *logit_bias, float *logits, float *scores, int K, int route_act,
                           const float *corr_bias, int use_corr_bias, int norm_topk, int *sel, float *w,
                           sw_u32x4 *xl, float *xs) {
-    if (D % 128 || D > 16384 || E <= 0 || E > TK_MAXE || S <= 0 || K <= 0 || K > 64 || K > E) return -1;
+    if (D % 128 || D > 16384 || E <= 0 || S <= 0) return -1;
+    if (sel && (E > TK_MAXE || K <= 0 || K > 64 || K > E)) return -1;   // (logits only: any number of rows)
     if (route_act < 0 || route_act > 4 || (sel && !sw_act_softmax(route_act) && !scores)) return -1;
     // four experts per block (wave 0; the others stage x) while that stays within 256 blocks,
     // else four per wave of eight

@@ -197,6 +197,9 @@ int sw_launch_stage_experts(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, const fl
                             float *sh_out);
 // the shared expert on the VALU (sw_shared.h): h[S, Is] = silu(Wg x) * (Wu x)
 // and out[S, D] = Wd h, bf16 weights, f32 activations
+// stack glue (k_glue.hip): RMSNorm rows, greedy argmax rows
+int sw_launch_rmsnorm(hipStream_t st, const float *x, const float *w, float *out, int S, int D, float eps);
+int sw_launch_argmax(hipStream_t st, const float *logits, int S, int V, int *tok);
 // the shared expert of a batch over token tiles (k_shared.hip): h = silu(Wg x) * (Wu x); out = Wd h
 int sw_launch_sh_glu(hipStream_t st, const uint16_t *Wg, const uint16_t *Wu, const float *x, int S, int D, int Is, float *h);
 int sw_launch_sh_down(hipStream_t st, const uint16_t *Wd, const float *h, int S, int Is, int D, float *out);

@@ -1,0 +1,80 @@
+"""The stack glue on the device (A18): RMSNorm rows, the bf16 head's logits
+and the greedy pick, and a small stack of MoE layers end to end, against the
+oracle: RMSNorm, head logits and the pick bit for bit; the stack's residual
+stream within the benchmark tolerance and its greedy tokens identical."""
+import numpy as np
+import pytest
+
+from oracle import synth
+from sabrewing_amd import configs as cf
+from sabrewing_amd.stack import DeviceStack, NORM_EPS, head_bf16, norm_weights
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("D", [512, 4096])
+def test_rmsnorm_bits(be, orc, D):
+    rng = np.random.default_rng(D)
+    x = (rng.standard_normal((5, D)) * np.array([[1e-3], [1.0], [30.0], [1.0], [1e3]])).astype(np.float32)
+    w = (1 + rng.standard_normal(D) * 0.02).astype(np.float32)
+    xd, wd, od = be.upload(x), be.upload(w), be.upload(np.zeros_like(x))
+    be.rmsnorm(xd, wd, od, 5, D, NORM_EPS)
+    got = be.d2h(od, x.shape, np.float32)
+    for b in (xd, wd, od):
+        b.free()
+    assert np.array_equal(got.view(np.uint32), orc.rmsnorm_rows(x, w, NORM_EPS).view(np.uint32))
+
+
+def test_head_logits_and_pick(be, orc):
+    cfg = cf.scaled(cf.C5_LAYER, D=512)
+    V, S = 1000, 4
+    head = head_bf16(orc, cfg, 5, V)
+    x = np.random.default_rng(2).standard_normal((S, cfg.D)).astype(np.float32)
+    Wc = be.router_upload(head, True)
+    xd, ld, td = be.upload(x), be.alloc(S * V * 4), be.alloc(S * 4)
+    be.head_argmax(Wc, True, xd, S, cfg.D, V, ld, td)
+    logits = be.d2h(ld, (S, V), np.float32)
+    tok = be.d2h(td, (S,), np.int32)
+    want = orc.matmul_bf16(x, head)
+    assert np.array_equal(logits.view(np.uint32), want.view(np.uint32))
+    assert np.array_equal(tok, orc.argmax_rows(want))
+    # the pick's rules on planted rows: ties to the lowest index, -0.0 == +0.0, NaN
+    rows = np.full((4, V), -1.0, np.float32)
+    rows[0, [7, 3, 900]] = 5.0
+    rows[1, :] = -2.0; rows[1, 10] = -0.0; rows[1, 4] = 0.0
+    rows[2, 0] = np.nan; rows[2, 5] = 9.0
+    rows[3, 1] = np.nan; rows[3, 600] = 2.0
+    be.h2d(ld, rows)
+    be.argmax(ld, S, V, td)
+    assert np.array_equal(be.d2h(td, (S,), np.int32), [3, 4, 0, 600])
+    assert np.array_equal(orc.argmax_rows(rows), [3, 4, 0, 600])
+    for b in (Wc, xd, ld, td):
+        b.free()
+
+
+@pytest.mark.parametrize("S_", [1, 4])
+def test_small_stack(be, orc, S_):
+    cfg = cf.scaled(cf.C5_LAYER, D=512, E=32, K=8, I=384)
+    n_layers, V, seed = 3, 1000, 77
+    layers = [synth.make_layer(orc, cfg, seed, layer=l) for l in range(n_layers)]
+    nw = norm_weights(orc, cfg, seed, n_layers)
+    head = head_bf16(orc, cfg, seed, V)
+    h0 = synth.make_x(orc, cfg, seed, S_)
+    wh, wlog, wtok = orc.stack(synth.desc_of(cfg), layers, nw[:n_layers], nw[n_layers], head, h0, NORM_EPS)
+    st = DeviceStack.from_host(be, cfg, layers, nw[:n_layers], nw[n_layers], head)
+    hd, xn, ld, td = be.upload(h0), be.alloc(S_ * cfg.D * 4), be.alloc(S_ * V * 4), be.alloc(S_ * 4)
+    st.step(hd, xn, ld, td, S_)
+    h = be.d2h(hd, h0.shape, np.float32)
+    logits = be.d2h(ld, (S_, V), np.float32)
+    tok = be.d2h(td, (S_,), np.int32)
+    st.free()
+    for b in (hd, xn, ld, td):
+        b.free()
+    dw = wh - h0
+    assert float(np.max(np.abs((h - h0) - dw))) / float(np.max(np.abs(dw))) <= 2e-3
+    err = float(np.max(np.abs(logits - wlog)))
+    srt = np.sort(wlog, axis=1)
+    margin = srt[:, -1] - srt[:, -2]
+    clear = margin > 20 * err
+    assert clear.sum() >= max(1, S_ - 1), (margin, err)
+    assert np.array_equal(tok[clear], wtok[clear])

@@ -154,3 +154,38 @@ def test_generator(orc):
     assert abs(big.mean()) < 1e-4 and abs(big.std() - 0.02) < 1e-4
     assert abs(float(((big / 0.02) ** 4).mean()) - 3.0) < 0.05             # normal kurtosis
     assert np.array_equal(orc.normal(100, seed, 0.02, offset=50), big[50:150])
+
+
+def test_rmsnorm_and_argmax(orc):
+    """A18 glue: rmsnorm_row (c/moe_math.h:58-62) bit-exact against the
+    compiled reference when built, and against its closed form in double
+    within one float rounding; argmax (c/laguna.c:1159) against a brute-force
+    strict scan, ties, signed zeros and NaN included"""
+    from oracle.oracle import Ref
+    rng = np.random.default_rng(58)
+    for D in (64, 512, 4096):
+        x = (rng.standard_normal((3, D)) * rng.choice([1e-3, 1.0, 1e3], (3, 1))).astype(np.float32)
+        w = (1 + rng.standard_normal(D) * 0.02).astype(np.float32)
+        got = orc.rmsnorm_rows(x, w, 1e-6)
+        inv = 1.0 / np.sqrt((x.astype(np.float64) ** 2).mean(axis=1, keepdims=True) + 1e-6)
+        assert np.allclose(got, x * inv * w, rtol=4e-7, atol=0)
+        if Ref.available():
+            r = Ref()
+            for s in range(3):
+                assert np.array_equal(got[s].view(np.uint32), r.rmsnorm_row(x[s], w, 1e-6).view(np.uint32))
+
+    def scan(v):
+        b = 0
+        for i in range(1, len(v)):
+            if v[i] > v[b]:
+                b = i
+        return b
+    cases = [rng.standard_normal(100).astype(np.float32),
+             np.array([1, 3, 3, 2, 3], np.float32),
+             np.array([-0.0, 0.0, -1.0], np.float32),
+             np.array([0.0, -0.0, -1.0], np.float32),
+             np.array([np.nan, 5, 7], np.float32),
+             np.array([1, np.nan, 7, 7, np.nan], np.float32),
+             np.array([-np.inf, -np.inf], np.float32)]
+    for v in cases:
+        assert orc.argmax_rows(v[None])[0] == scan(list(v))
