@@ -102,6 +102,57 @@ def cpu_baseline(be, cfg, dl, xs, seconds):
                       f"{isa} build, {dt:.1f} s"}
 
 
+def run_stack(args):
+    """--config C5-stack: the Config-5 decode step -- 48 resident MoE layers
+    (D=4096, E=256, top-8 softmax, I=1536, no shared expert), h += MoE(rmsnorm(h))
+    each, then rmsnorm, the bf16 4096x32000 head and the greedy pick, for a
+    batch of C5_BATCH streams."""
+    from sabrewing_amd import configs as cf
+    from sabrewing_amd.backend import Backend, gen_x
+    from sabrewing_amd.stack import DeviceStack
+    cfg, L, V = cf.C5_LAYER, args.layers_stack, cf.C5_VOCAB
+    B = args.batch or cf.C5_BATCH
+    be = Backend(0)
+    t0 = time.time()
+    st = DeviceStack.generate(be, cfg, L, V, args.seed)
+    log(f"generated the {L}-layer stack ({L * cfg.expert_bytes() * cfg.E / 1e9:.1f} GB of experts) in {time.time() - t0:.1f}s")
+    D = cfg.D
+    nx = args.warmup + args.steps
+    xs = gen_x(be, cfg, args.seed, B * nx)
+    h, xn, lg, tok = be.alloc(B * D * 4), be.alloc(B * D * 4), be.alloc(B * V * 4), be.alloc(B * 4)
+
+    def step(i):
+        be.check(be.lib.lag_hip_d2d(int(h), int(xs) + i * B * D * 4, B * D * 4), "d2d")
+        st.step(h, xn, lg, tok, B)
+
+    for i in range(args.warmup):
+        step(i)
+    be.sync()
+    ev0, ev1 = be.event(), be.event()
+    be.record(ev0)
+    for i in range(args.steps):
+        step(args.warmup + i)
+    be.record(ev1)
+    be.sync()
+    ms = be.elapsed_ms(ev0, ev1) / args.steps
+    be.profile_reset(); be.profile(True)
+    step(0); be.sync()
+    prof = be.profile_read(); be.profile(False)
+    kern = {k: {"avg_us": round(1e3 * v[0] / max(v[1], 1), 2), "launches": v[1]} for k, v in prof.items()}
+    res = {"metric": "Config-5 stack decode tokens/s (48 int4 MoE layers + RMSNorm + bf16 head + greedy pick)",
+           "value": round(B / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+           "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+           "vs_baseline": None, "dtype": "int4 weights (group-32 f32 scales) x f32 activations, f32 accumulate",
+           "data": "synthetic: seeded N(0,0.02) weights generated on device, N(0,1) bf16-valued tokens",
+           "config": {"workload": "C5-stack", "batch": B, "layers": L, "hidden": D, "experts": cfg.E, "topk": cfg.K,
+                      "moe_inter": cfg.I, "vocab": V},
+           "kernels": kern}
+    print(json.dumps(res), flush=True)
+    for b in (h, xn, lg, tok, xs):
+        b.free()
+    st.free()
+
+
 def run(args):
     from sabrewing_amd import configs as cf
     from sabrewing_amd.backend import Backend, DeviceLayer, desc_of, gen_x
@@ -266,7 +317,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--batch", type=int, default=1)
+    ap.add_argument("--batch", type=int, default=None, help="tokens per step (default 1; C5-stack: 8)")
+    ap.add_argument("--layers-stack", type=int, default=48, help="C5-stack: resident MoE layers")
     ap.add_argument("--config", default="C2-laguna-softplus")
     ap.add_argument("--layers", type=int, default=12)
     ap.add_argument("--seed", type=int, default=20261201)
@@ -283,6 +335,10 @@ def main():
         print("bench.py: this build measures one GPU only (the MoE block on one MI355X); "
               "--gpus N > 1 is not supported", file=sys.stderr)
         sys.exit(2)
+    if args.config == "C5-stack":
+        run_stack(args)
+        return
+    args.batch = args.batch or 1
     run(args)
 
 

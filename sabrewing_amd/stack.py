@@ -33,14 +33,21 @@ class DeviceStack:
         return self
 
     @classmethod
-    def generate(cls, be, cfg, n_layers, V, seed, orc):
-        """Device-generated layers and head; norm weights from the host generator (orc)."""
+    def generate(cls, be, cfg, n_layers, V, seed):
+        """Everything generated on the device (the bits of norm_weights / head_bf16)."""
         self = cls(be, cfg, V)
         self.layers = [DeviceLayer.generate(be, cfg, seed, layer=l) for l in range(n_layers)]
-        nw = norm_weights(orc, cfg, seed, n_layers)
-        self.norms = [self._keep(be.upload(nw[l])) for l in range(n_layers)]
-        self.final_norm = self._keep(be.upload(nw[n_layers]))
         D = cfg.D
+        for l in range(n_layers + 1):
+            g = be.alloc(D * 4)
+            be.gen_normal(g, D, synth.tensor_seed(seed, l, synth.T_NORM), WEIGHT_SIGMA)
+            w = (np.float32(1.0) + be.d2h(g, (D,), np.float32)).astype(np.float32)
+            g.free()
+            b = self._keep(be.upload(w))
+            if l < n_layers:
+                self.norms.append(b)
+            else:
+                self.final_norm = b
         tmp = be.alloc(V * D * 2)
         be.gen_bf16(tmp, V * D, synth.tensor_seed(seed, 0, synth.T_HEAD), WEIGHT_SIGMA)
         self.head = self._keep(be.alloc((V + 3) // 4 * 4 * D * 2))
