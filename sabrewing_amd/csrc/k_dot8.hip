@@ -236,12 +236,20 @@ __device__ __forceinline__ void dot8_glu_block(const Dot8GluArgs &A, int bx, int
 #pragma unroll
         for (int l = 0; l < SW_NL; l++) X[0][l] = xl[(int64_t)g * SW_NL + l];
         xf[0] = xs[g];
-        if constexpr (NP > 0) {                       // the token's routing by the whole block
-            __shared__ TopkBlockLDS tk;
+        if constexpr (NP > 0) {                       // the token's routing by wave 0 of the block
+            __shared__ int tk_sk[64];
+            __shared__ float tk_wk[64];
+            __shared__ uint64_t tk_tab[32];
             const DotRoute rt = A.rt;
-            gate_topk_block<DG_NT, NP>(rt.src, rt.E, rt.K, rt.act, rt.bias, rt.use_bias, rt.norm, tk);
-            e = __builtin_amdgcn_readfirstlane(tk.sk[bx]);
-            if (bx == 0 && by == 0 && tid < rt.K) { A.sel[tid] = tk.sk[tid]; rt.w[tid] = tk.wk[tid]; }
+            if (tid < 64) {
+                int sk;
+                float wk;
+                gate_topk_wave<NP>(rt.src, rt.E, rt.K, rt.act, rt.bias, rt.use_bias, rt.norm, tk_tab, sk, wk);
+                if (tid < rt.K) { tk_sk[tid] = sk; tk_wk[tid] = wk; }
+            }
+            __syncthreads();
+            e = __builtin_amdgcn_readfirstlane(tk_sk[bx]);
+            if (bx == 0 && by == 0 && tid < rt.K) { A.sel[tid] = tk_sk[tid]; rt.w[tid] = tk_wk[tid]; }
         } else {
             e = A.sel[bx];
         }
