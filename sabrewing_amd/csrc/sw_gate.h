@@ -176,59 +176,40 @@ __device__ void gate_topk_wave(const float *__restrict__ src, int E, int K, int 
         ko[i] = (e < E && key > -1e30f) ? ord_f32(key) : 0u;
     }
     TR_MARKK(0, 5);
-    // The K picks are the K largest words (ko << 32 | ~e) over e < E: ko desc,
-    // then the lowest id -- the order of moe_topk's K passes, invalid keys (ko
-    // 0) last by id, which is its all-invalid fallback.  T, the K-th largest
-    // ko, by a radix select (one bit per step: count the keys >= prefix|bit);
-    // every key above T is picked, and of those equal to T the lowest ids
-    // until K; the picks, compacted into LDS, rank each other.
-    __shared__ uint64_t pk_word[64];
-    __shared__ float pk_val[64];
-    __shared__ int pk_e[64];
-    __shared__ float pk_w[64];
-    const unsigned long long ltmask = lane ? (~0ull >> (64 - lane)) : 0ull;
-    unsigned long long frm[NPER];                    // the slots of real experts (e < E), per slot
+    sk = 0; wk = 0.f;
+    for (int a = 0; a < K; a++) {
+        uint32_t lm = ko[0];
 #pragma unroll
-    for (int i = 0; i < NPER; i++) frm[i] = __ballot(fr[i]);
-    uint32_t T = 0u;
-#pragma unroll 4
-    for (int bit = 31; bit >= 0; bit--) {
-        const uint32_t cand = T | (1u << bit);
-        int c = 0;
+        for (int i = 1; i < NPER; i++) lm = lm > ko[i] ? lm : ko[i];
+        const uint32_t m = wave_umax(lm);
+        int bi = 0x7fffffff;
+        if (m != 0u) {                                // the lowest id holding the maximum
 #pragma unroll
-        for (int i = 0; i < NPER; i++) c += __popcll(__ballot(ko[i] >= cand) & frm[i]);
-        T = c >= K ? cand : T;
-    }
-    int ngt = 0;
+            for (int i = NPER - 1; i >= 0; i--) {
+                const unsigned long long bal = __ballot(ko[i] == m);
+                if (bal) bi = 64 * i + __builtin_ctzll(bal);
+            }
+        } else {                                      // nothing valid left: the lowest unselected id
 #pragma unroll
-    for (int i = 0; i < NPER; i++) ngt += __popcll(__ballot(ko[i] > T) & frm[i]);
-    const int need = K - ngt;                         // of the keys equal to T, lowest ids first
-    int eq_before = 0, sel_before = 0;
-#pragma unroll
-    for (int i = 0; i < NPER; i++) {
-        const unsigned long long eq = __ballot(fr[i] && ko[i] == T);
-        const bool take = fr[i] && (ko[i] > T || (ko[i] == T && eq_before + __popcll(eq & ltmask) < need));
-        const unsigned long long tk = __ballot(take);
-        if (take) {
-            const int slot = sel_before + __popcll(tk & ltmask);
-            const int e = lane + 64 * i;
-            pk_word[slot] = ((uint64_t)ko[i] << 32) | (0xFFFFFFFFu - (uint32_t)e);
-            pk_val[slot] = v[i];
+            for (int i = NPER - 1; i >= 0; i--) {
+                const unsigned long long bal = __ballot(fr[i]);
+                if (bal) bi = 64 * i + __builtin_ctzll(bal);
+            }
+            if (bi >= E) bi = 0;
         }
-        eq_before += __popcll(eq);
-        sel_before += __popcll(tk);
+        const int slot = bi >> 6, bl = bi & 63;       // uniform
+        float vs = v[0];
+#pragma unroll
+        for (int i = 1; i < NPER; i++)
+            if (i == slot) vs = v[i];
+        const float wb = lanef(vs, bl);               // the pick's weight: its unbiased score
+        if (lane == bl) {
+#pragma unroll
+            for (int i = 0; i < NPER; i++)
+                if (i == slot) { ko[i] = 0u; fr[i] = false; }
+        }
+        if (lane == a) { sk = bi; wk = wb; }
     }
-    wave_sync();
-    if (lane < K) {                                   // rank among the K picks: the larger words
-        const uint64_t mw = pk_word[lane];
-        int r = 0;
-        for (int j = 0; j < K; j++) r += pk_word[j] > mw ? 1 : 0;
-        pk_e[r] = (int)(0xFFFFFFFFu - (uint32_t)(mw & 0xFFFFFFFFull));
-        pk_w[r] = pk_val[lane];
-    }
-    wave_sync();
-    sk = lane < K ? pk_e[lane] : 0;
-    wk = lane < K ? pk_w[lane] : 0.f;
     TR_MARKK(0, 6);
     if (act == 4) {                                   // qwen35: always, in double (c/qwen35.c:585-587)
         double tot = 0.0;
