@@ -44,17 +44,19 @@ def kernel_bytes(cfg, S, G):
     dn_w = G * (D * I // 2 + D * ngI * 4)
     sh_gu = 2 * Is * D * 2 if cfg.shared_mode else 0
     sh_dn = D * Is * 2 if cfg.shared_mode else 0
-    b = {
-        "stage_route": cfg.router_bytes() + S * D * 4 + 2 * S * E * 4 + S * limb(D) + sh_gu + S * Is * 4,
-        "stage_experts": gu_w + S * limb(D) + T * limb(I) + sh_dn + S * Is * 4 + S * D * 4,
-    }
-    if S == 1:
-        b["q4_down_combine"] = dn_w + T * limb(I) + T * 8 + 2 * D * 4 + (D * 4 if cfg.shared_mode else 0)
-    else:
-        b["gate_topk"] = 2 * S * E * 4 + T * 8
-        b["bucket"] = T * 4 * 3 + E * 12
-        b["q4_down"] = dn_w + T * limb(I) + T * D * 4
-        b["combine"] = T * D * 4 + 2 * S * D * 4 + (S * D * 4 if cfg.shared_mode else 0) + T * 8
+    route = cfg.router_bytes() + S * D * 4 + 2 * S * E * 4 + S * limb(D)
+    if S == 1:        # the shared expert rides in stages 1 and 2
+        b = {"stage_route": route + sh_gu + S * Is * 4,
+             "stage_experts": gu_w + S * limb(D) + T * limb(I) + sh_dn + S * Is * 4 + S * D * 4,
+             "q4_down_combine": dn_w + T * limb(I) + T * 8 + 2 * D * 4 + (D * 4 if cfg.shared_mode else 0)}
+    else:             # its own kernels over token tiles
+        b = {"stage_route": route, "gate_topk": 2 * S * E * 4 + T * 8, "bucket": T * 4 * 3 + E * 12,
+             "stage_experts": gu_w + S * limb(D) + T * limb(I),
+             "q4_down": dn_w + T * limb(I) + T * D * 4,
+             "combine": T * D * 4 + 2 * S * D * 4 + (S * D * 4 if cfg.shared_mode else 0) + T * 8}
+        if cfg.shared_mode:
+            b["shared_glu"] = sh_gu + S * D * 4 + S * Is * 4
+            b["shared_down"] = sh_dn + S * Is * 4 + S * D * 4
     return b
 
 
@@ -225,26 +227,29 @@ def run(args):
     if args.timed_only:
         return
 
-    # per-kernel times: the same steps again with every launch bracketed by events
-    be.profile_reset()
-    be.profile(True)
-    G_sum = 0
-    for i in range(args.steps):
+    # distinct experts per step (the bytes a step must read)
+    G_sum, nG = 0, min(args.steps, 20)
+    for i in range(nG):
         step(args.warmup + i)
         if B > 1:
             G_sum += be.last_groups()[0]
+    G = G_sum / nG if B > 1 and G_sum > 0 else cfg.K
+
+    # per-kernel times: the same steps again, each launch bracketed by HIP events
+    # on the backend stream
+    be.profile_reset()
+    be.profile(True)
+    for i in range(args.steps):
+        step(args.warmup + i)
     be.sync()
     prof = be.profile_read()
     be.profile(False)
-    G = G_sum / args.steps if B > 1 else cfg.K
-    if B > 1 and G_sum == 0:
-        G = cfg.K
     kb = kernel_bytes(cfg, B, G)
     kern = {k: {"avg_us": 1e3 * v[0] / max(v[1], 1), "launches": v[1]} for k, v in prof.items()}
     for k, v in kern.items():
         if k in kb:
             v["bytes"] = kb[k]
-            v["GBs"] = kb[k] / (v["avg_us"] * 1e-6) / 1e9
+            v["GBs"] = kb[k] / (v["avg_us"] * 1e-6) / 1e9 if v["avg_us"] > 0 else 0.0
     dom = max(kern, key=lambda k: kern[k]["avg_us"] * kern[k]["launches"])
     dk = kern[dom]
     # HBM bytes per launch of that kernel as rocprofv3 counted them (FETCH_SIZE x2 + WRITE_SIZE,
