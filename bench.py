@@ -115,6 +115,7 @@ def run_stack(args):
     cfg, L, V = cf.C5_LAYER, args.layers_stack, cf.C5_VOCAB
     B = args.batch or cf.C5_BATCH
     be = Backend(0)
+    be.set_grouped_kernel({"auto": 0, "dot8": 1, "mfma": 2}[args.grouped])
     t0 = time.time()
     st = DeviceStack.generate(be, cfg, L, V, args.seed)
     log(f"generated the {L}-layer stack ({L * cfg.expert_bytes() * cfg.E / 1e9:.1f} GB of experts) in {time.time() - t0:.1f}s")
@@ -162,6 +163,7 @@ def run(args):
     cfg = cf.CONFIGS[args.config]
     B = args.batch
     be = Backend(0)
+    be.set_grouped_kernel({"auto": 0, "dot8": 1, "mfma": 2}[args.grouped])
     t0 = time.time()
     layers = []
     for l in range(args.layers):
@@ -327,6 +329,8 @@ def main():
     ap.add_argument("--config", default="C2-laguna-softplus")
     ap.add_argument("--layers", type=int, default=12)
     ap.add_argument("--seed", type=int, default=20261201)
+    ap.add_argument("--grouped", choices=["auto", "dot8", "mfma"], default="auto",
+                    help="grouped expert GEMMs of batches: auto (int8 MFMA at >= 8 tokens per group), dot8, mfma")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--calib-copy-mb", type=int, default=0,

@@ -169,6 +169,13 @@ void  *lag_hip_graph_end(void);          /* NULL on failure */
 int    lag_hip_graph_launch(void *g);
 void   lag_hip_graph_destroy(void *g);
 
+/* Kernel choice for the grouped expert GEMMs of lag_hip_moe_forward with
+ * S > 1: 0 auto (the int8 MFMA when the batch's groups average >= 8 tokens,
+ * else dot8), 1 dot8, 2 int8 MFMA.  Both give the same bits.  Returns the
+ * previous mode, -1 for a bad one.  No counterpart in the reference (one
+ * grouped kernel there, c/backend_cuda.cu:618-700): a tuning switch. */
+int    lag_hip_set_grouped_kernel(int mode);
+
 /* per-kernel timing with events on the backend stream (the analogue of the
  * reference's COLI_CUDA_PROFILE=1, c/backend_cuda.cu:822-940) */
 int    lag_hip_profile(int enable);
@@ -182,8 +189,8 @@ int    lag_hip_gen_bf16(uint16_t *out, int64_t n, uint64_t seed, uint64_t offset
 int    lag_hip_gen_q4(uint8_t *q, float *s, uint64_t seed, double sigma, int64_t row0, int64_t nrows, int K, int gs);
 
 /* ---------------- diagnostics ---------------- */
-/* MFMA lane-layout probe + libm evaluation on n host inputs; out_host gets
- * 512 + 2n floats (see k_route.hip).  0 = ran */
+/* MFMA lane-layout probes (f16, bf16, int8) + libm evaluation on n host
+ * inputs; out_host gets 768 + 2n floats (layout in k_route.hip).  0 = ran */
 int    lag_hip_selftest(float *out_host, const float *xin_host, int n);
 const char *lag_hip_last_error(void);
 

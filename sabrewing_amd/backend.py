@@ -26,7 +26,7 @@ EXPORTS = [
     "lag_hip_matmul_bf16", "lag_hip_matmul_q4", "lag_hip_expert_q4", "lag_hip_moe_experts", "lag_hip_moe_group",
     "lag_hip_matmul_q4_g", "lag_hip_expert_q4_g", "lag_hip_moe_experts_g", "lag_hip_moe_group_g",
     "lag_hip_router_upload", "lag_hip_router_chain", "lag_hip_moe_forward", "lag_hip_moe_block", "lag_hip_route",
-    "lag_hip_last_groups", "lag_hip_rmsnorm", "lag_hip_head_argmax", "lag_hip_argmax",
+    "lag_hip_last_groups", "lag_hip_rmsnorm", "lag_hip_head_argmax", "lag_hip_argmax", "lag_hip_set_grouped_kernel",
     "lag_hip_alloc", "lag_hip_h2d", "lag_hip_d2h", "lag_hip_d2d", "lag_hip_memset",
     "lag_hip_graph_begin", "lag_hip_graph_end", "lag_hip_graph_launch", "lag_hip_graph_destroy", "lag_hip_sync",
     "lag_hip_event_create", "lag_hip_event_record", "lag_hip_event_elapsed_ms", "lag_hip_event_destroy",
@@ -106,6 +106,7 @@ def load_library(path=None):
     L.lag_hip_event_elapsed_ms.restype = C.c_float; L.lag_hip_event_elapsed_ms.argtypes = [VP, VP]
     L.lag_hip_event_destroy.argtypes = [VP]
     L.lag_hip_profile.argtypes = [C.c_int]
+    L.lag_hip_set_grouped_kernel.argtypes = [C.c_int]
     L.lag_hip_profile_read.argtypes = [C.c_int, C.c_char_p, C.c_int, C.POINTER(C.c_double), C.POINTER(C.c_longlong)]
     L.lag_hip_gen_normal.argtypes = [VP, C.c_int64, C.c_uint64, C.c_uint64, C.c_double, C.c_int]
     L.lag_hip_gen_bf16.argtypes = [VP, C.c_int64, C.c_uint64, C.c_uint64, C.c_double]
@@ -296,6 +297,16 @@ class Backend:
     def profile(self, on):
         self.lib.lag_hip_profile(int(on))
 
+    GROUPED_AUTO, GROUPED_DOT8, GROUPED_MFMA = 0, 1, 2
+
+    def set_grouped_kernel(self, mode):
+        """the grouped expert GEMMs of batches: 0 auto, 1 dot8, 2 int8 MFMA
+        (bit-identical); returns the previous mode"""
+        prev = self.lib.lag_hip_set_grouped_kernel(int(mode))
+        if prev < 0:
+            raise BackendError(f"bad grouped-kernel mode {mode}")
+        return prev
+
     def profile_reset(self):
         self.lib.lag_hip_profile_reset()
 
@@ -310,7 +321,7 @@ class Backend:
 
     def selftest(self, xin):
         xin = np.ascontiguousarray(xin, np.float32)
-        out = np.zeros(512 + 2 * xin.size, np.float32)
+        out = np.zeros(768 + 2 * xin.size, np.float32)
         self.check(self.lib.lag_hip_selftest(out, xin, xin.size), "lag_hip_selftest")
         return out
 

@@ -213,6 +213,23 @@ extern "C" int lag_hip_sync(void) {
     return 0;
 }
 
+// The grouped expert GEMMs of a batch: dot8 (k_dot8.hip) or the int8 MFMA
+// (k_mfma.hip), bit-identical; auto takes the MFMA when the groups average at
+// least SW_MF_MIN_AVG tokens (its 16-token tiles are then mostly full)
+static int g_grouped_kernel = 0;        // 0 auto, 1 dot8, 2 MFMA
+#define SW_MF_MIN_AVG 8
+static bool use_mfma(int T, int E, int D, int I) {
+    if (g_grouped_kernel == 1 || D % 128 || I % 128) return false;      // whole chunks of 4 input groups
+    if (g_grouped_kernel == 2) return true;
+    return T >= SW_MF_MIN_AVG * (T < E ? T : E);
+}
+extern "C" int lag_hip_set_grouped_kernel(int mode) {
+    if (mode < 0 || mode > 2) return -1;
+    const int prev = g_grouped_kernel;
+    g_grouped_kernel = mode;
+    return prev;
+}
+
 // the int4 expert pipeline over device groups:
 //   h <- silu_glu(gate_up . x);  slots <- down . h
 // (limbs_ready: xl/xs already hold the limbs of dx)
@@ -237,17 +254,22 @@ static int grouped_host(float *outh, const float *x, int S, const void *gu_q, co
     if (!g_ok || fault_injected()) return -1;
     if (D <= 0 || I <= 0 || G <= 0 || S <= 0) return -1;
     const int T = S * K;
-    const int ngD = gs > 0 ? D / gs : 1, ngI = gs > 0 ? I / gs : 1;
-    (void)ngD; (void)ngI;
+    // the MFMA kernels for prefill-sized groups: tiles of up to 64 tokens, listed here
+    int ntile = 0;
+    for (int i = 0; i < G; i++) ntile += (gcnt[i] + SW_MF_TT - 1) / SW_MF_TT;
+    const bool mf = G < 1024 && T < (1 << 21) && use_mfma(T, G, D, I);
     Carve cv;
-    const size_t o_x = cv.take((size_t)S * D * 4), o_idx = cv.take((size_t)(3 * G + 2 * T) * 4 + (size_t)T * 4);
+    const size_t idxn = (size_t)(3 * G + 2 * T) * 4 + (size_t)T * 4 + (mf ? (size_t)(ntile + 1) * 4 : 0);
+    const size_t o_x = cv.take((size_t)S * D * 4), o_idx = cv.take(idxn);
     const size_t o_hl = cv.take((size_t)T * (I / 32) * SW_NL * 16), o_hs = cv.take((size_t)T * (I / 32) * 4);
     const size_t o_slot = cv.take((size_t)T * D * 4), o_out = cv.take((size_t)S * D * 4);
     const size_t o_xl = cv.take((size_t)S * (D / 32) * SW_NL * 16), o_xs = cv.take((size_t)S * (D / 32) * 4);
+    size_t o_xd = 0, o_hd = 0;
+    if (mf) { o_xd = cv.take((size_t)S * (D / 32) * 128); o_hd = cv.take((size_t)T * (I / 32) * 128); }
     if (grow_dev(g_arena, cv.off)) return -1;
     char *A = (char *)g_arena.p;
-    // one pinned blob: x | gexp gbeg gcnt grow rowof w
-    const size_t xn = (size_t)S * D * 4, idxn = (size_t)(3 * G + 2 * T) * 4 + (size_t)T * 4;
+    // one pinned blob: x | gexp gbeg gcnt grow rowof w [| items P]
+    const size_t xn = (size_t)S * D * 4;
     if (grow_pinned(g_hin, xn + idxn) || grow_pinned(g_hout, (size_t)S * D * 4)) return -1;
     char *H = (char *)g_hin.p;
     memcpy(H, x, xn);
@@ -258,6 +280,12 @@ static int grouped_host(float *outh, const float *x, int S, const void *gu_q, co
     memcpy(hi + 3 * G, grow, (size_t)T * 4);
     memcpy(hi + 3 * G + T, rowof, (size_t)T * 4);
     memcpy(hi + 3 * G + 2 * T, w, (size_t)T * 4);
+    if (mf) {
+        int *it = hi + 3 * G + 3 * T, n = 0;
+        for (int i = 0; i < G; i++)
+            for (int t0 = 0; t0 < gcnt[i]; t0 += SW_MF_TT) it[n++] = (t0 << 10) | i;
+        it[n] = n;
+    }
     CK(hipMemcpyAsync(A + o_x, H, xn, hipMemcpyHostToDevice, g_st), "x upload");
     CK(hipMemcpyAsync(A + o_idx, H + xn, idxn, hipMemcpyHostToDevice, g_st), "index upload");
     const int *d_gexp = (const int *)(A + o_idx), *d_gbeg = d_gexp + G, *d_gcnt = d_gexp + 2 * G;
@@ -273,8 +301,18 @@ static int grouped_host(float *outh, const float *x, int S, const void *gu_q, co
     SwGroups g = {d_gexp, d_gbeg, d_gcnt, d_grow, nullptr, G, 0};
     int maxcnt = 0;
     for (int i = 0; i < G; i++) maxcnt = gcnt[i] > maxcnt ? gcnt[i] : maxcnt;
-    if (run_experts(gu, dn, (const float *)(A + o_x), S, (sw_u32x4 *)(A + o_xl), (float *)(A + o_xs), 0, g, I,
-                    (sw_u32x4 *)(A + o_hl), (float *)(A + o_hs), (float *)(A + o_slot), maxcnt)) return -1;
+    if (mf) {
+        const int *d_items = (const int *)(d_w + T);
+        const SwGroups gt = {d_gexp, d_gbeg, d_gcnt, d_grow, nullptr, ntile, 0, d_items, d_items + ntile};
+        SwGroups gd = gt;
+        gd.grow = nullptr;
+        uint32_t *xd = (uint32_t *)(A + o_xd), *hd = (uint32_t *)(A + o_hd);
+        float *xds = (float *)(A + o_xs), *hds = (float *)(A + o_hs);     // the factors: same sizes as the limbs'
+        { PROF("digits"); if (sw_launch_digits(g_st, (const float *)(A + o_x), S, D, xd, xds)) return fail_msg("digits launch"); }
+        { PROF("mf_glu"); if (sw_launch_mf_glu(g_st, gu, xd, xds, gt, I, hd, hds)) return fail_msg("MFMA gate_up launch (shape unsupported?)"); }
+        { PROF("mf_down"); if (sw_launch_mf_rows(g_st, dn, hd, hds, gd, (float *)(A + o_slot))) return fail_msg("MFMA down launch (shape unsupported?)"); }
+    } else if (run_experts(gu, dn, (const float *)(A + o_x), S, (sw_u32x4 *)(A + o_xl), (float *)(A + o_xs), 0, g, I,
+                           (sw_u32x4 *)(A + o_hl), (float *)(A + o_hs), (float *)(A + o_slot), maxcnt)) return -1;
     const float *res = (const float *)(A + o_slot);
     if (combine) {
         PROF("combine");
@@ -406,6 +444,8 @@ struct FwdScratch {
     float *shh;             // shared expert h [S, Is]
     sw_u32x4 *xl;
     float *xs;
+    uint32_t *xd, *hd;      // MFMA digits of x [S][D/32] and of h [T][I/32] (prefill)
+    float *xds, *hds;
 };
 static int g_last_G_dev = 0;            // 1: last forward's groups live in the arena
 static FwdScratch g_last;
@@ -435,6 +475,11 @@ static int carve_fwd(const LagHipMoeDesc *d, int S, FwdScratch &f) {
     size_t o_sh = 0, o_so = 0;
     if (d->shared_mode) { o_sh = cv.take((size_t)S * Is * 4); o_so = cv.take((size_t)S * D * 4); }
     const size_t o_xl = cv.take((size_t)S * (D / 32) * SW_NL * 16), o_xs = cv.take((size_t)S * (D / 32) * 4);
+    size_t o_xd = 0, o_xds = 0, o_hd = 0, o_hds = 0;
+    if (S > 1) {
+        o_xd = cv.take((size_t)S * (D / 32) * 128); o_xds = cv.take((size_t)S * (D / 32) * 4);
+        o_hd = cv.take((size_t)T * (I / 32) * 128); o_hds = cv.take((size_t)T * (I / 32) * 4);
+    }
     if (grow_dev(g_arena, cv.off)) return -1;
     char *A = (char *)g_arena.p;
     f.logits = (float *)(A + o_lg); f.scores = (float *)(A + o_sc); f.sel = (int *)(A + o_sel); f.w = (float *)(A + o_w);
@@ -445,8 +490,11 @@ static int carve_fwd(const LagHipMoeDesc *d, int S, FwdScratch &f) {
     f.shh = d->shared_mode ? (float *)(A + o_sh) : nullptr;
     f.sout = d->shared_mode ? (float *)(A + o_so) : nullptr;
     f.xl = (sw_u32x4 *)(A + o_xl); f.xs = (float *)(A + o_xs);
+    f.xd = S > 1 ? (uint32_t *)(A + o_xd) : nullptr; f.xds = S > 1 ? (float *)(A + o_xds) : nullptr;
+    f.hd = S > 1 ? (uint32_t *)(A + o_hd) : nullptr; f.hds = S > 1 ? (float *)(A + o_hds) : nullptr;
     return 0;
 }
+
 
 // router logits (+ scores); with sel, gate + top-k; with xl, the dot8 limbs of x
 static int route_dev(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const float *x, int S, float *logits,
@@ -473,7 +521,9 @@ extern "C" int lag_hip_route(const LagHipMoeDesc *d, const LagHipMoeWeights *w, 
 //            routed gate_up; + the shared expert's down
 //   stage 3  routed down fused with the rank-order combine (+ shared, residual)
 // S > 1: routing stage, gate + top-k, shared gate_up over token tiles, the
-// counting sort, grouped gate_up, shared down, grouped down into slots, combine.
+// counting sort, grouped gate_up, shared down, grouped down into slots, combine;
+// the grouped GEMMs on dot8 (passes of 2 tokens) or, for prefill-sized batches,
+// on the int8 MFMA (tiles of 64 tokens, the inputs as MFMA digits).
 extern "C" int lag_hip_moe_forward(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const float *x, float *out, int S) {
     if (!g_ok || fault_injected()) return -1;
     if (!desc_ok(d, w) || S <= 0) return fail_msg("moe_forward: unsupported descriptor/shape");
@@ -493,9 +543,15 @@ extern "C" int lag_hip_moe_forward(const LagHipMoeDesc *d, const LagHipMoeWeight
     // S == 1: the shared expert's gate_up and down run as extra blocks of stages 1 and 2;
     // S > 1: as kernels of their own over token tiles (the same arithmetic per token)
     const bool sh_in = sh && S == 1;
+    const bool mf = S > 1 && use_mfma(T, E, D, I);
     { PROF("stage_route");
       if (sw_launch_stage_route(g_st, w->router, d->router_bf16, x, S, D, E, w->logit_bias, f.logits, f.scores, d->route_act,
-                                f.xl, f.xs, sh_in ? sg : nullptr, su, Is, f.shh)) return fail_msg("routing stage launch"); }
+                                mf ? nullptr : f.xl, f.xs, sh_in ? sg : nullptr, su, Is, f.shh))
+          return fail_msg("routing stage launch"); }
+    if (mf) {
+        PROF("digits");
+        if (sw_launch_digits(g_st, x, S, D, f.xd, f.xds)) return fail_msg("digits launch");
+    }
     if (sh && !sh_in) {
         PROF("shared_glu");
         if (sw_launch_sh_glu(g_st, sg, su, x, S, D, Is, f.shh)) return fail_msg("shared gate_up launch");
@@ -515,6 +571,24 @@ extern "C" int lag_hip_moe_forward(const LagHipMoeDesc *d, const LagHipMoeWeight
           if (sw_launch_q4_dot8_down_combine(g_st, dn, f.hl, f.hs, f.sel, f.w, K, d->route_scale, f.sout, out))
               return fail_msg("down/combine launch"); }
         g_last_G_dev = 0; g_last_ng = K;
+    } else if (mf) {                     // prefill: tiles of up to 64 tokens of a group on the int8 MFMA
+        { PROF("bucket");
+          if (sw_launch_bucket(g_st, f.sel, S, K, E, f.gexp, f.gbeg, f.gcnt, f.G, f.grow, f.rowof, SW_MF_TT, f.items, f.P))
+              return fail_msg("bucket launch"); }
+        SwGroups g = {f.gexp, f.gbeg, f.gcnt, f.grow, f.G, sw_npass_max(T, E, SW_MF_TT), 0, f.items, f.P};
+        { PROF("mf_glu");
+          if (sw_launch_mf_glu(g_st, gu, f.xd, f.xds, g, I, f.hd, f.hds)) return fail_msg("MFMA gate_up launch"); }
+        if (sh) {
+            PROF("shared_down");
+            if (sw_launch_sh_down(g_st, sd, f.shh, S, Is, D, f.sout)) return fail_msg("shared down launch");
+        }
+        SwGroups gd = g;
+        gd.grow = nullptr;                 // the down reads the packed rows directly
+        { PROF("mf_down"); if (sw_launch_mf_rows(g_st, dn, f.hd, f.hds, gd, f.slots)) return fail_msg("MFMA down launch"); }
+        { PROF("combine");
+          if (sw_launch_combine(g_st, f.slots, f.rowof, f.w, S, K, D, d->route_scale, f.sout, out, 1))
+              return fail_msg("combine launch"); }
+        g_last_G_dev = 1; g_last_ng = 0;
     } else {
         { PROF("bucket");
           if (sw_launch_bucket(g_st, f.sel, S, K, E, f.gexp, f.gbeg, f.gcnt, f.G, f.grow, f.rowof, SW_DG_TT, f.items, f.P))
@@ -656,12 +730,12 @@ extern "C" int lag_hip_gen_q4(uint8_t *q, float *s, uint64_t seed, double sigma,
 extern "C" int lag_hip_selftest(float *out_host, const float *xin_host, int n) {
     if (!g_ok || n < 0) return -1;
     float *dout = nullptr, *din = nullptr;
-    CK(hipMalloc(&dout, (size_t)(512 + 2 * n) * 4), "selftest alloc");
+    CK(hipMalloc(&dout, (size_t)(768 + 2 * n) * 4), "selftest alloc");
     if (n > 0 && hipMalloc(&din, (size_t)n * 4) != hipSuccess) { (void)hipFree(dout); return fail_msg("selftest alloc"); }
     if (n > 0) CK(hipMemcpy(din, xin_host, (size_t)n * 4, hipMemcpyHostToDevice), "selftest upload");
     int rc = sw_launch_selftest(g_st, dout, din, n);
     if (rc == 0 && hipStreamSynchronize(g_st) != hipSuccess) rc = -1;
-    if (rc == 0 && hipMemcpy(out_host, dout, (size_t)(512 + 2 * n) * 4, hipMemcpyDeviceToHost) != hipSuccess) rc = -1;
+    if (rc == 0 && hipMemcpy(out_host, dout, (size_t)(768 + 2 * n) * 4, hipMemcpyDeviceToHost) != hipSuccess) rc = -1;
     (void)hipFree(dout);
     if (din) (void)hipFree(din);
     return rc ? fail_msg("selftest") : 0;

@@ -110,18 +110,6 @@ __device__ __forceinline__ float row_term(float p, bool gv, int CH) {
     return run_sum(gv ? p : 0.f, CH);
 }
 
-// The weight tensors are read through buffer descriptors over all E experts
-// (extent E * O * K/2 bytes, and E * O * ng * 4 for the scales).
-static bool q4_extent_ok(const SwQ4 &W) {
-    const int ng = W.gs > 0 ? W.K / W.gs : 1;
-    return W.E > 0 && (uint64_t)W.E * W.O * (W.K / 2) < (1ull << 32) && (uint64_t)W.E * W.O * ng * 4 < (1ull << 32);
-}
-__device__ __forceinline__ sw_rsrc q4_rq(const SwQ4 &W) { return sw_make_rsrc(W.q, (uint32_t)W.E * W.O * (W.K / 2)); }
-__device__ __forceinline__ sw_rsrc q4_rs(const SwQ4 &W) {
-    const int ng = W.gs > 0 ? W.K / W.gs : 1;
-    return sw_make_rsrc(W.s, (uint32_t)W.E * W.O * ng * 4);
-}
-
 // row slots of a block of nt threads: the largest power of two with rps * Gq <= nt, at most cap
 __host__ __device__ inline int dg_rps(int Gq, int cap, int nt) {
     int r = 1;
@@ -129,27 +117,6 @@ __host__ __device__ inline int dg_rps(int Gq, int cap, int nt) {
     return r;
 }
 
-// the work of grouped block bx: expert e, the group's first packed row beg and
-// its tokens [t0, tend) -- one pass from the pass list, or the whole group
-// (false: nothing to do)
-__device__ __forceinline__ bool grp_work(const SwGroups &grp, int bx, int TT, int &e, int &beg, int &t0, int &tend) {
-    if (grp.items) {
-        if (bx >= *grp.P) return false;
-        const int v = grp.items[bx], gi = v & 1023;
-        t0 = v >> 10;
-        e = grp.gexp[gi];
-        beg = grp.gbeg[gi];
-        tend = min(t0 + TT, grp.gcnt[gi]);
-        return true;
-    }
-    const int gvalid = grp.G ? *grp.G : grp.ngroups_max;
-    if (bx >= gvalid) return false;
-    e = grp.gexp ? grp.gexp[bx] : 0;
-    beg = grp.gbeg ? grp.gbeg[bx] : 0;
-    t0 = 0;
-    tend = grp.gcnt ? grp.gcnt[bx] : grp.cnt_const;
-    return true;
-}
 
 // ------------------------------------------------------------ gate_up ----
 // One block = 32 consecutive intermediate outputs i of one group: gate rows
@@ -193,14 +160,6 @@ struct Dot8GluArgs {
 
 // K inputs as G = K/32 groups, G <= 256
 static bool dot8_shape_ok(int K) { return K > 0 && K % RG == 0 && K / RG <= 256; }
-static int dot8_gsh(const SwQ4 &W, int &gsh) {
-    gsh = 0;
-    if (W.gs > 0) {
-        if (W.gs % RG || W.K % W.gs || (W.gs & (W.gs - 1))) return -1;
-        while ((1 << gsh) < W.gs) gsh++;
-    }
-    return 0;
-}
 static int dot8_nc(int K) { const int G = K / RG; return G < CHG ? 1 : run_lanes(G) / CHG; }
 static int dot8_c16(int K) { return (K / RG) % CHG == 0; }
 // steps of weight loads in flight: min(8, steps per half) (a power of two dividing it)
@@ -257,7 +216,7 @@ __device__ __forceinline__ void dot8_glu_block(const Dot8GluArgs &A, int bx, int
     } else {
         if (!grp_work(grp, bx, TT, e, beg, tb, tend)) return;
     }
-    const sw_rsrc rq = q4_rq(W), rs = q4_rs(W);
+    const sw_rsrc rq = sw_q4_rq(W), rs = sw_q4_rs(W);
     // lane offsets (this thread's first row of a half) and the scalar offset of step s
     const uint32_t voq = (uint32_t)(roc * NSH) * rb + (uint32_t)g * 16;
     const uint32_t vos = (uint32_t)(roc * NSH) * sb + (uint32_t)sg * 4;
@@ -363,8 +322,8 @@ struct GluL {
 };
 
 static int dot8_glu_check(SwQ4 W, int I, int &gsh) {
-    if (!dot8_shape_ok(W.K) || I % 32 || W.O != 2 * I || !q4_extent_ok(W)) return -1;
-    return dot8_gsh(W, gsh);
+    if (!dot8_shape_ok(W.K) || I % 32 || W.O != 2 * I || !sw_q4_extent_ok(W)) return -1;
+    return sw_q4_gsh(W, gsh);
 }
 static size_t dot8_glu_lds(int K, int TT) { return (size_t)TT * DG_ROWS * dot8_nc(K) * 4; }
 
@@ -422,7 +381,7 @@ __device__ __forceinline__ void dot8_rows_block(const Dot8RowsArgs &A, int bx, i
     const int ng = W.gs > 0 ? K / W.gs : 1;
     const int sg = W.gs > 0 ? (g * RG) >> A.gsh : 0;
     const uint32_t rb = (uint32_t)K / 2, sb = (uint32_t)ng * 4;
-    const sw_rsrc rq = q4_rq(W), rs = q4_rs(W);
+    const sw_rsrc rq = sw_q4_rq(W), rs = sw_q4_rs(W);
     // rows past O read the next expert's rows (or zeros past the tensor) and are not stored
     const uint32_t voq = (uint32_t)(roc * NS) * rb + (uint32_t)g * 16;
     const uint32_t vos = (uint32_t)(roc * NS) * sb + (uint32_t)sg * 4;
@@ -505,7 +464,7 @@ struct RowsL {
 
 int sw_launch_q4_dot8_rows(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, const float *xs, SwGroups g, float *Y) {
     int gsh;
-    if (!dot8_shape_ok(W.K) || g.ngroups_max <= 0 || W.O <= 0 || !q4_extent_ok(W) || dot8_gsh(W, gsh)) return -1;
+    if (!dot8_shape_ok(W.K) || g.ngroups_max <= 0 || W.O <= 0 || !sw_q4_extent_ok(W) || sw_q4_gsh(W, gsh)) return -1;
     const dim3 grid((unsigned)g.ngroups_max, (unsigned)((W.O + DG_ROWS - 1) / DG_ROWS));
     const Dot8RowsArgs A = {W, gsh, xl, xs, g, Y};
     // a ring of at most RW_PF steps: within 128 VGPRs, four blocks per CU
@@ -569,7 +528,7 @@ __device__ __forceinline__ void dot8_down_combine_block(const Dot8DownArgs &A, i
     for (int l = 0; l < SW_NL; l++) X[l] = hl[((int64_t)ac * G + g) * SW_NL + l];
     const float xf = hs[(int64_t)ac * G + g];
     const uint32_t e = (uint32_t)sel[ac];
-    const sw_rsrc rq = q4_rq(W), rs = q4_rs(W);
+    const sw_rsrc rq = sw_q4_rq(W), rs = sw_q4_rs(W);
     const uint32_t voq = (e * (uint32_t)D + (uint32_t)d0) * rb + (uint32_t)g * 16;
     const uint32_t vos = (e * (uint32_t)D + (uint32_t)d0) * sb + (uint32_t)sg * 4;
     sw_u32x4 ra[DC_RB];
@@ -614,8 +573,8 @@ int sw_launch_q4_dot8_down_combine(hipStream_t st, SwQ4 W, const sw_u32x4 *hl, c
                                    int K, float route_scale, const float *shared, float *out) {
     const int I = W.K, G = I / RG;
     int gsh;
-    if (!dot8_shape_ok(I) || W.O % DC_RB || K <= 0 || K > 64 || K * run_lanes(G) > 1024 || !q4_extent_ok(W) ||
-        dot8_gsh(W, gsh)) return -1;
+    if (!dot8_shape_ok(I) || W.O % DC_RB || K <= 0 || K > 64 || K * run_lanes(G) > 1024 || !sw_q4_extent_ok(W) ||
+        sw_q4_gsh(W, gsh)) return -1;
     const size_t lds = (size_t)K * DC_RB * dot8_nc(I) * 4;
     const int threads = (K * run_lanes(G) + 63) / 64 * 64;
     const Dot8DownArgs A = {W, gsh, hl, hs, sel, w, K, route_scale, shared, out};

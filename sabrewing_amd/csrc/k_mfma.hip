@@ -1,0 +1,416 @@
+// k_mfma.hip -- the grouped int4 expert GEMMs of prefill on the int8 matrix
+// cores, bit-identical to the dot8 kernels of k_dot8.hip.
+//
+// For a weight row and a group of 32 inputs, dot8 forms the exact integer
+// acc = sum_k w_k D_k (w_k = n_k - 8 in [-8, 7], D_k the 7-limb integer of
+// input k, |D_k| < 2^21.2) and the term (float)acc * (s * xf).  Here every D
+// is cut into two 12-bit digits, D = E1 2^12 + E0 with E0 the residue of D
+// mod 4096 in [-2048, 2048), and every E into a low nibble and a signed high
+// byte, E = lo + 16 hi (lo = E & 15, hi = E >> 4; both int8).  One
+// v_mfma_i32_16x16x64_i8 has 64 k-slots: the 32 weights as bytes w against
+// lo, and as bytes 16 w against hi, so it returns
+//     R = sum_k (w_k lo_k + 16 w_k hi_k) = sum_k w_k E_k
+// exactly (|R| < 2^19); the two of E0 and E1 give acc = (R1 << 12) + R0,
+// dot8's int32.  The terms and the canonical row sum (pairwise trees over
+// runs of 16 groups, padded with +0 terms, the runs added left to right)
+// follow dot8's operations one for one, so a token's output has the same
+// bits whichever kernel ran its group.
+//
+// Digits in memory: per (input row, group) 128 bytes, the B operands of the
+// two MFMAs: byte op*64 + (k>>3)*16 + half*8 + (k&1)*4 + ((k&7)>>1) holds
+// input k's lo (half 0) or hi (half 1) digit of E0 (op 0) or E1 (op 1).
+// Lane l of the MFMA (column l % 16, k quarter q = l / 16) reads the 16
+// bytes of quarter q, and its A operand holds the same k-slots of a weight
+// row: [w of k = 8q+0,2,4,6 | w of 8q+1,3,5,7 | 16w of the same | 16w ...],
+// expanded from packed dword q of the row's group (nibble k at bits 4(k&7)).
+//
+// Block: 128 weight rows (8 tiles of 16) x a tile of up to 64 tokens (4
+// tiles of 16) of one group, 8 waves; wave w takes row tiles w&3 and (w&3)+4
+// (for gate_up the gate and the up rows of the same 16 outputs) against
+// token tiles 2(w>>2) and 2(w>>2)+1, so each lane holds 16 (row, token) sums.
+// The operands of 4 input groups at a time -- the rows' weights expanded
+// once for the 8 waves, the tokens' digits, the scales and the token factors
+// -- are staged in LDS in two buffers: while the waves compute one chunk from
+// LDS, the next chunk's loads are in flight in registers.  The inner loop
+// reads LDS only, every wave read a contiguous 1 KB (conflict-free).
+#include "sw_hip.h"
+#include "sw_gate.h"
+
+#define MF_DW 32           // digit dwords per (input row, group)
+#define MF_ROWS 128        // weight rows per block
+#define MF_TT SW_MF_TT     // tokens per block tile (64)
+#define MF_NT 512          // threads per block: 8 waves
+#define MF_CG 4            // input groups per staged chunk
+// one chunk buffer in LDS: expanded weights [g][tile 8][quarter 4][row 16] x 16 B,
+// digits [g][token tile 4][op 2][quarter 4][token 16] x 16 B, scales [g][row],
+// token factors [g][token]
+#define MF_A_OFF 0
+#define MF_B_OFF (MF_A_OFF + MF_CG * MF_ROWS * 64)
+#define MF_S_OFF (MF_B_OFF + MF_CG * MF_TT * 128)
+#define MF_X_OFF (MF_S_OFF + MF_CG * MF_ROWS * 4)
+#define MF_BUF (MF_X_OFF + MF_CG * MF_TT * 4)
+#define MF_HLD 65          // floats per token row of h in the gate_up epilogue
+
+// ------------------------------------------------------------ digits ----
+// one group by the 32 lanes of a half-wave (i = lane in the half): the same
+// exponent and 7 limbs as limbs_group, written as the MFMA digits above;
+// the factor 2^(e - 21) (NaN for a group holding a NaN or an infinity, whose
+// digits are 0) is limbs_group's
+__device__ __forceinline__ void digits_group(float v, int i, uint32_t *__restrict__ dst, float *__restrict__ fdst) {
+    bool bad;
+    const int e = limbs_exp(v, bad);
+    float y = ldexpf(v, -e);
+    int D = 0;
+#pragma unroll
+    for (int l = 0; l < SW_NL; l++) D = D * 8 + (int)limb_digit(y);
+    if (bad) D = 0;
+    const int E0 = ((D + 2048) & 4095) - 2048, E1 = (D - E0) >> 12;
+    const int sh = 8 * ((i & 7) >> 1);
+    uint32_t b[4] = {(uint32_t)(E0 & 15) << sh, (uint32_t)((E0 >> 4) & 255) << sh, (uint32_t)(E1 & 15) << sh,
+                     (uint32_t)((E1 >> 4) & 255) << sh};
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        b[q] |= __shfl_xor(b[q], 2, 32);
+        b[q] |= __shfl_xor(b[q], 4, 32);
+    }
+    if ((i & 6) == 0) {                               // lane 8 kq + par holds the dwords of (kq, par)
+        const int kq = i >> 3, par = i & 1;
+        dst[kq * 4 + par] = b[0];
+        dst[kq * 4 + 2 + par] = b[1];
+        dst[16 + kq * 4 + par] = b[2];
+        dst[16 + kq * 4 + 2 + par] = b[3];
+    }
+    if (i == 0) *fdst = bad ? __builtin_nanf("") : ldexpf(1.0f, e - 3 * SW_NL);
+}
+
+// rows x[r, K] f32 -> digits dg[r][K/32][32 dwords], factors xs[r][K/32]
+__global__ __launch_bounds__(256) void k_digits(const float *__restrict__ x, int K, int rows, uint32_t *__restrict__ dg,
+                                                float *__restrict__ xs) {
+    const int G = K / SW_RG;
+    const int tid = threadIdx.x, g = blockIdx.x * 8 + (tid >> 5), r = blockIdx.y;
+    if (r >= rows || g >= G) return;                  // whole half-waves leave together
+    digits_group(x[(int64_t)r * K + g * SW_RG + (tid & 31)], tid & 31, dg + ((int64_t)r * G + g) * MF_DW,
+                 xs + (int64_t)r * G + g);
+}
+
+int sw_launch_digits(hipStream_t st, const float *x, int rows, int K, uint32_t *dg, float *xs) {
+    if (K % SW_RG || rows <= 0) return -1;
+    const int G = K / SW_RG;
+    SW_LAUNCH(k_digits, dim3((unsigned)((G + 7) / 8), (unsigned)rows), dim3(256), 0, st, x, K, rows, dg, xs);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+// ------------------------------------------------------------ GEMM ----
+struct MfArgs {
+    SwQ4 W;
+    int gsh;
+    const uint32_t *dg;     // input digits [rows][G][MF_DW]
+    const float *xs;        // input factors [rows][G]
+    SwGroups grp;           // tiles: items of up to MF_TT tokens, P live
+    int I;                  // GLU: the intermediate size (W.O == 2 I)
+    int nrb;                // row blocks
+    uint32_t *hdg;          // GLU: h of every packed row as digits [T][I/32][MF_DW]
+    float *hxs;             //      and factors [T][I/32]
+    float *Y;               // rows: [T][O]
+};
+
+// the pairwise tree of a run of CH terms (CH a power of two <= 16), fed one
+// term at a time (gl = the term's index in the run, known at compile time
+// after unrolling): L holds the pending single, pair, quad and eight; the
+// run's sum lands in run after the last term
+template <int CH>
+__device__ __forceinline__ void tree_push(float p, int gl, float (&L)[4], float &run) {
+    if (CH == 1) { run = p; return; }
+    if ((gl & 1) == 0) { L[0] = p; return; }
+    float s = L[0] + p;
+    if (CH == 2) { run = s; return; }
+    if ((gl & 2) == 0) { L[1] = s; return; }
+    s = L[1] + s;
+    if (CH == 4) { run = s; return; }
+    if ((gl & 4) == 0) { L[2] = s; return; }
+    s = L[2] + s;
+    if (CH == 8) { run = s; return; }
+    if ((gl & 8) == 0) { L[3] = s; return; }
+    run = L[3] + s;
+}
+
+// the four int8 operand dwords of packed weight dword w (nibble n = w_k + 8
+// of k = 8q + c at bits 4c): bytes w of the even k, w of the odd k, 16 w of
+// the even k, 16 w of the odd k
+__device__ __forceinline__ sw_i32x4 mf_expand(uint32_t w) {
+    const uint32_t wx = w ^ 0x88888888u;             // nibbles w_k as 4-bit two's complement
+    sw_i32x4 a;
+    a[0] = (int)(((w & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u);          // n + 120 < 256, then bit 7 flipped: n - 8
+    a[1] = (int)((((w >> 4) & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u);
+    a[2] = (int)((wx << 4) & 0xF0F0F0F0u);
+    a[3] = (int)(wx & 0xF0F0F0F0u);
+    return a;
+}
+
+template <int N>
+struct MfIc { static constexpr int v = N; };
+
+template <int GLU, int CH, int FULL>
+__global__ __launch_bounds__(MF_NT, 1) void k_mf(MfArgs A) {
+    extern __shared__ __align__(16) uint8_t mf_lds[];
+    const SwQ4 W = A.W;
+    const SwGroups grp = A.grp;
+    const int K = W.K, G = K / SW_RG, O = W.O;
+    const int NC = G / MF_CG;                              // staged chunks (G % 4 == 0)
+    const int NCV = (G + CH - 1) / CH * (CH / MF_CG);      // chunks of the padded runs
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, col = lane & 15, kq = lane >> 4;
+    const int mp = wave & 3, np = wave >> 2;               // row tiles mp, mp + 4; token tiles 2np, 2np + 1
+
+    // block -> (tile, row block), XCD-aware over the live blocks
+    const int nlive = *grp.P * A.nrb;
+    if ((int)blockIdx.x >= nlive) return;
+    const int wk = sw_xcd_work((int)blockIdx.x, nlive);
+    const int tile = wk / A.nrb, rb = wk - tile * A.nrb;
+    int e, beg, t0, tend;
+    if (!grp_work(grp, tile, MF_TT, e, beg, t0, tend)) return;
+    const int nt = tend - t0;
+    const int i0 = rb * 64, r0 = rb * MF_ROWS;
+    // weight row of local row r (GLU: gate rows i0..i0+63, then the up rows)
+    auto srow = [&](int r) -> uint32_t {
+        if (GLU) return (uint32_t)e * (uint32_t)O + (uint32_t)(r < 64 ? i0 + r : A.I + i0 + r - 64);
+        return (uint32_t)e * (uint32_t)O + (uint32_t)(r0 + r);     // past O: the next expert's rows, not stored
+    };
+    auto token = [&](int t) -> int64_t {                   // input row of tile token t (past the tile: its last)
+        const int pr = beg + t0 + min(t, nt - 1);
+        return grp.grow ? grp.grow[pr] : pr;
+    };
+    const sw_rsrc rq = sw_q4_rq(W), rs = sw_q4_rs(W);
+    const int ng = W.gs > 0 ? K / W.gs : 1;
+    const uint32_t rbytes = (uint32_t)K / 2;
+
+    // ---- staging: this thread's units of a chunk
+    //  weights: row ra = tid & 127 of group tid >> 7 (16 B packed, expanded on the store) + its scale
+    //  digits:  16 B (op, quarter) of token tb of each of the 4 groups
+    //  factors: token tx of group tid >> 6 (threads < 256)
+    const int ra = tid & 127, ga = tid >> 7;
+    const uint32_t rowa = srow(ra);
+    const int tb = ((tid >> 7) & 3) * 16 + (tid & 15), opb = (tid >> 6) & 1, kqb = (tid >> 4) & 3;
+    const uint32_t *__restrict__ dgb = A.dg + token(tb) * G * MF_DW + opb * 16 + kqb * 4;
+    const int tx = tid & 63, gx = tid >> 6;
+    const float *__restrict__ xsx = A.xs + token(tx) * G;
+    sw_u32x4 pka, pkb[MF_CG];
+    float psa = 1.0f, pxf = 0.f;
+    auto stage_load = [&](int c) {
+        const int g0 = c * MF_CG;
+        pka = sw_ld16(rq, rowa * rbytes + (uint32_t)(g0 + ga) * 16, 0);
+        if (W.gs > 0) psa = sw_ld4f(rs, (rowa * (uint32_t)ng + (uint32_t)(((g0 + ga) * SW_RG) >> A.gsh)) * 4, 0);
+#pragma unroll
+        for (int v = 0; v < MF_CG; v++) pkb[v] = *(const sw_u32x4 *)(dgb + (g0 + v) * MF_DW);
+        if (tid < MF_CG * MF_TT) pxf = xsx[g0 + gx];
+    };
+    auto stage_store = [&](int buf) {
+        uint8_t *base = mf_lds + buf * MF_BUF;
+        sw_i32x4 *Al = (sw_i32x4 *)(base + MF_A_OFF);
+        sw_u32x4 *Bl = (sw_u32x4 *)(base + MF_B_OFF);
+        const int m = ra >> 4, i = ra & 15;
+#pragma unroll
+        for (int q = 0; q < 4; q++) Al[((ga * 8 + m) * 4 + q) * 16 + i] = mf_expand(pka[q]);
+        ((float *)(base + MF_S_OFF))[ga * MF_ROWS + ra] = psa;
+#pragma unroll
+        for (int v = 0; v < MF_CG; v++) Bl[v * MF_NT + tid] = pkb[v];
+        if (tid < MF_CG * MF_TT) ((float *)(base + MF_X_OFF))[gx * MF_TT + tx] = pxf;
+    };
+
+    const bool wact = np * 32 < nt;                        // uniform over the wave
+    const bool two = np * 32 + 16 < nt;                    // the wave's second token tile holds tokens
+    float y[2][2][4], L[2][2][4][4], run[2][2][4];
+    // the LDS operands of one group for this wave
+    struct Frag {
+        sw_i32x4 a[2], b[2][2];
+        sw_f32x4 s4[2];
+        float xf[2];
+    };
+    auto fetch = [&](Frag &F, const uint8_t *base, int g) {
+        const sw_i32x4 *Al = (const sw_i32x4 *)(base + MF_A_OFF);
+        const sw_i32x4 *Bl = (const sw_i32x4 *)(base + MF_B_OFF);
+        const float *Sl = (const float *)(base + MF_S_OFF), *Xl = (const float *)(base + MF_X_OFF);
+#pragma unroll
+        for (int mi = 0; mi < 2; mi++) {
+            const int m = mp + 4 * mi;
+            F.a[mi] = Al[((g * 8 + m) * 4 + kq) * 16 + col];
+            F.s4[mi] = *(const sw_f32x4 *)(Sl + g * MF_ROWS + 16 * m + 4 * kq);
+        }
+#pragma unroll
+        for (int ni = 0; ni < 2; ni++) {
+            const int n = 2 * np + ni;
+            F.b[ni][0] = Bl[((g * 4 + n) * 2 + 0) * 64 + lane];
+            F.b[ni][1] = Bl[((g * 4 + n) * 2 + 1) * 64 + lane];
+            F.xf[ni] = Xl[g * MF_TT + 16 * n + col];
+        }
+    };
+    // the terms of one group (zero terms for the padding of a run: REAL = 0) into the trees
+    auto group = [&](const Frag &F, int gl, bool first, auto RC, auto TC) {
+        constexpr bool REAL = decltype(RC)::v, TWO = decltype(TC)::v;
+#pragma unroll
+        for (int ni = 0; ni < (TWO ? 2 : 1); ni++) {
+            sw_i32x4 R0[2], R1[2];
+            if (REAL) {
+                const sw_i32x4 z = {0, 0, 0, 0};
+#pragma unroll
+                for (int mi = 0; mi < 2; mi++) {
+                    R0[mi] = __builtin_amdgcn_mfma_i32_16x16x64_i8(F.a[mi], F.b[ni][0], z, 0, 0, 0);
+                    R1[mi] = __builtin_amdgcn_mfma_i32_16x16x64_i8(F.a[mi], F.b[ni][1], z, 0, 0, 0);
+                }
+            }
+#pragma unroll
+            for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    float p = 0.f;                          // the +0 terms of a padded run
+                    if (REAL) {
+                        const int acc = (R1[mi][j] << 12) + R0[mi][j];
+                        p = (float)acc * (F.s4[mi][j] * F.xf[ni]);
+                    }
+                    tree_push<CH>(p, gl, L[mi][ni][j], run[mi][ni][j]);
+                    if (gl == CH - 1) y[mi][ni][j] = first ? run[mi][ni][j] : y[mi][ni][j] + run[mi][ni][j];
+                }
+        }
+    };
+    // one chunk: its 4 groups at positions Q*4 .. Q*4+3 of the run (Q known at compile time);
+    // the next group's operands are read from LDS before this group's terms are summed
+    auto chunk = [&](auto QC, auto RC, auto TC, int c) {
+        constexpr int Q = decltype(QC)::v;
+        const uint8_t *base = mf_lds + (c & 1) * MF_BUF;
+        const bool first = c < CH / MF_CG;                 // in the first run
+        Frag F[2];
+        if (decltype(RC)::v) fetch(F[0], base, 0);
+#pragma unroll
+        for (int g = 0; g < MF_CG; g++) {
+            if (decltype(RC)::v && g + 1 < MF_CG) fetch(F[(g + 1) & 1], base, g + 1);
+            group(F[g & 1], Q * MF_CG + g, first, RC, TC);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    auto chunk_q = [&](auto RC, auto TC, int c) {
+        switch (c % (CH / MF_CG)) {
+            case 0: chunk(MfIc<0>{}, RC, TC, c); break;
+            case 1: if constexpr (CH / MF_CG > 1) chunk(MfIc<1 % (CH / MF_CG)>{}, RC, TC, c); break;
+            case 2: if constexpr (CH / MF_CG > 2) chunk(MfIc<2 % (CH / MF_CG)>{}, RC, TC, c); break;
+            default: if constexpr (CH / MF_CG > 3) chunk(MfIc<3 % (CH / MF_CG)>{}, RC, TC, c); break;
+        }
+    };
+
+    stage_load(0);
+    stage_store(0);
+    __syncthreads();
+    if (NC > 1) stage_load(1);
+    for (int c = 0; c < NCV; c++) {
+        if (wact) {
+            if (FULL || c < NC) {
+                if (two) chunk_q(MfIc<1>{}, MfIc<1>{}, c);
+                else chunk_q(MfIc<1>{}, MfIc<0>{}, c);
+            } else if constexpr (!FULL) {
+                if (two) chunk_q(MfIc<0>{}, MfIc<1>{}, c);
+                else chunk_q(MfIc<0>{}, MfIc<0>{}, c);
+            }
+        }
+        if (c + 1 < NC) stage_store((c + 1) & 1);          // read by no wave since the last barrier
+        __syncthreads();
+        if (c + 2 < NC) stage_load(c + 2);
+    }
+
+    if constexpr (GLU) {
+        // h = silu(gate) * up per (token, output), through LDS to the digit writers
+        float *hl = (float *)mf_lds;                       // [MF_TT][MF_HLD]; every wave is past its last read
+        const int I = A.I;
+        if (wact) {
+#pragma unroll
+            for (int ni = 0; ni < 2; ni++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const int i = 16 * mp + 4 * kq + j, t = 32 * np + 16 * ni + col;
+                    float yg = y[0][ni][j], yu = y[1][ni][j];
+                    if (W.gs <= 0) {                        // per-row scales after the sum
+                        yg = yg * W.s[(int64_t)e * (2 * I) + i0 + i];
+                        yu = yu * W.s[(int64_t)e * (2 * I) + I + i0 + i];
+                    }
+                    hl[t * MF_HLD + i] = (yg / (1.0f + expf(-yg))) * yu;
+                }
+        }
+        __syncthreads();
+        // the block's 64 outputs are two limb groups of the down projection's input
+        const int GI = I / SW_RG, hw = tid >> 5, i = tid & 31;
+        for (int job = hw; job < 2 * nt; job += MF_NT / 32) {
+            const int t = job >> 1, q = job & 1;
+            const int64_t prow = beg + t0 + t;
+            const int gi = 2 * rb + q;
+            digits_group(hl[t * MF_HLD + 32 * q + i], i, A.hdg + (prow * GI + gi) * MF_DW, A.hxs + prow * GI + gi);
+        }
+    } else {
+        if (wact) {
+#pragma unroll
+            for (int ni = 0; ni < 2; ni++) {
+                const int t = 32 * np + 16 * ni + col;
+                if (t < nt) {
+                    float *yrow = A.Y + (int64_t)(beg + t0 + t) * O;
+#pragma unroll
+                    for (int mi = 0; mi < 2; mi++) {
+                        const int row = r0 + 16 * (mp + 4 * mi) + 4 * kq;
+                        if (row < O) {
+                            sw_f32x4 o;
+#pragma unroll
+                            for (int j = 0; j < 4; j++)
+                                o[j] = W.gs > 0 ? y[mi][ni][j] : y[mi][ni][j] * W.s[(int64_t)e * O + row + j];
+                            *(sw_f32x4 *)(yrow + row) = o;
+                        }
+                    }
+                }
+            }
+        }
+    }
+}
+
+// ------------------------------------------------------------ launch ----
+static size_t mf_lds_bytes() {
+    const size_t h = (size_t)MF_TT * MF_HLD * 4;
+    return 2 * MF_BUF > h ? 2 * MF_BUF : h;
+}
+// dynamic LDS above 64 KB, raised once per kernel, outside any stream work
+template <int GLU, int CH, int FULL>
+static int mf_go(hipStream_t st, unsigned nblocks, const MfArgs &A) {
+    static size_t raised = 0;
+    const size_t lds = mf_lds_bytes();
+    if (lds > raised) {
+        if (hipFuncSetAttribute((const void *)k_mf<GLU, CH, FULL>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
+            hipSuccess) return -1;
+        raised = lds;
+    }
+    SW_LAUNCH((k_mf<GLU, CH, FULL>), dim3(nblocks), dim3(MF_NT), lds, st, A);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+template <int GLU>
+static int mf_dispatch(hipStream_t st, unsigned nblocks, const MfArgs &A) {
+    const int G = A.W.K / SW_RG, Gq = run_lanes(G), CH = Gq < 16 ? Gq : 16;
+    const bool full = G == Gq;
+    if (CH == 16) return full ? mf_go<GLU, 16, 1>(st, nblocks, A) : mf_go<GLU, 16, 0>(st, nblocks, A);
+    if (CH == 8) return full ? mf_go<GLU, 8, 1>(st, nblocks, A) : mf_go<GLU, 8, 0>(st, nblocks, A);
+    if (CH == 4) return full ? mf_go<GLU, 4, 1>(st, nblocks, A) : mf_go<GLU, 4, 0>(st, nblocks, A);
+    return -1;
+}
+// shapes: K a multiple of 128 (whole chunks of 4 input groups), tiles listed (items, P)
+static int mf_check(const SwQ4 &W, const SwGroups &g, int &gsh) {
+    if (W.K % (SW_RG * MF_CG) || !g.items || !g.P || g.ngroups_max <= 0 || !sw_q4_extent_ok(W)) return -1;
+    return sw_q4_gsh(W, gsh);
+}
+
+int sw_launch_mf_glu(hipStream_t st, SwQ4 W, const uint32_t *dg, const float *xs, SwGroups g, int I, uint32_t *hdg,
+                     float *hxs) {
+    int gsh;
+    if (mf_check(W, g, gsh) || I % 64 || W.O != 2 * I) return -1;
+    const int nrb = I / 64;
+    const MfArgs A = {W, gsh, dg, xs, g, I, nrb, hdg, hxs, nullptr};
+    return mf_dispatch<1>(st, (unsigned)(g.ngroups_max * nrb), A);
+}
+
+int sw_launch_mf_rows(hipStream_t st, SwQ4 W, const uint32_t *dg, const float *xs, SwGroups g, float *Y) {
+    int gsh;
+    if (mf_check(W, g, gsh) || W.O % 4) return -1;
+    const int nrb = (W.O + MF_ROWS - 1) / MF_ROWS;
+    const MfArgs A = {W, gsh, dg, xs, g, 0, nrb, nullptr, nullptr, Y};
+    return mf_dispatch<0>(st, (unsigned)(g.ngroups_max * nrb), A);
+}

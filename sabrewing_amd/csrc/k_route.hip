@@ -242,9 +242,13 @@ int sw_launch_combine(hipStream_t st, const float *slots, const int *rowof, cons
 
 // ------------------------------------------------------------ self test ----
 // MFMA lane-layout probe: A[i][k] = 32 i + k, B[k][j] = (k == j), so
-// C[i][j] = 32 i + j under the layout in sw_hip.h; plus glibc-exact libm on
-// host-chosen inputs.  out: [0,256) f16 MFMA C per lane (4 each), [256,512)
-// bf16 MFMA, [512, 512+n) sw_expf(xin), [512+n, 512+2n) sw_log1pf(xin).
+// C[i][j] = 32 i + j under the layout in sw_hip.h; the int8 MFMA on fixed
+// byte patterns (lane l byte b of A: (7 l + 13 b) % 17 - 8, of B:
+// (5 l + 3 b + 1) % 23 - 11), whose C shows which A and B bytes meet; plus
+// glibc-exact libm on host-chosen inputs.  out: [0,256) f16 MFMA C per lane
+// (4 each), [256,512) bf16 MFMA, [512,768) i8 MFMA, [768, 768+n)
+// sw_expf(xin), [768+n, 768+2n) sw_log1pf(xin).
+#define ST_LIBM 768
 __global__ void k_selftest_mfma(float *out) {
     const int l = threadIdx.x;
     sw_half8 a, b;
@@ -261,12 +265,25 @@ __global__ void k_selftest_mfma(float *out) {
     c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
     c2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ab, bb, c2, 0, 0, 0);
     for (int j = 0; j < 4; j++) { out[l * 4 + j] = c[j]; out[256 + l * 4 + j] = c2[j]; }
+    sw_i32x4 ai, bi, ci = {0, 0, 0, 0};
+    for (int d = 0; d < 4; d++) {
+        uint32_t wa = 0, wb = 0;
+        for (int q = 0; q < 4; q++) {
+            const int b = 4 * d + q;
+            wa |= (uint32_t)(uint8_t)(int8_t)((7 * l + 13 * b) % 17 - 8) << (8 * q);
+            wb |= (uint32_t)(uint8_t)(int8_t)((5 * l + 3 * b + 1) % 23 - 11) << (8 * q);
+        }
+        ai[d] = (int)wa;
+        bi[d] = (int)wb;
+    }
+    ci = __builtin_amdgcn_mfma_i32_16x16x64_i8(ai, bi, ci, 0, 0, 0);
+    for (int j = 0; j < 4; j++) out[512 + l * 4 + j] = (float)ci[j];
 }
 
 __global__ void k_selftest_libm(float *out, const float *xin, int n) {
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
-        out[512 + i] = sw_expf(xin[i]);
-        out[512 + n + i] = sw_log1pf(xin[i]);
+        out[ST_LIBM + i] = sw_expf(xin[i]);
+        out[ST_LIBM + n + i] = sw_log1pf(xin[i]);
     }
 }
 

@@ -343,10 +343,12 @@ __device__ void gate_topk_block(const float *__restrict__ src, int E, int K, int
 // 8j + i at bits 4i of dword j, the weights' nibble order); the factor is
 // 2^(e - 3 NL), or NaN for a group holding a NaN or an infinity.
 #define SW_RG 32
-// one group by the 32 lanes of a half-wave; i = lane in the half
-__device__ __forceinline__ void limbs_group(float v, int i, sw_u32x4 *__restrict__ dst, float *__restrict__ fdst) {
+// the group's exponent e (by the 32 lanes of a half-wave, v = this lane's
+// input): 2^e the smallest power of two above max|x|, 0 for an all-zero
+// group; bad = the group holds a NaN or an infinity
+__device__ __forceinline__ int limbs_exp(float v, bool &bad) {
     float m = fabsf(v);
-    bool bad = !(m <= 3.4028235e38f);                // NaN or inf
+    bad = !(m <= 3.4028235e38f);                     // NaN or inf
 #pragma unroll
     for (int o = 1; o < 32; o <<= 1) {
         m = fmaxf(m, __shfl_xor(m, o, 32));
@@ -354,14 +356,26 @@ __device__ __forceinline__ void limbs_group(float v, int i, sw_u32x4 *__restrict
     }
     int e = 0;
     if (m > 0.f && !bad) (void)frexpf(m, &e);        // m = f 2^e, f in [0.5, 1): 2^e > m
+    return e;
+}
+// the next digit of y (|y| <= 1): round to nearest, clamp to [-8, 7]; y keeps
+// the exact remainder (|y| <= 1)
+__device__ __forceinline__ float limb_digit(float &y) {
+    const float t = y * 8.0f;                         // exact
+    float d = rintf(t);
+    d = fminf(fmaxf(d, -8.0f), 7.0f);
+    y = t - d;                                        // exact
+    return d;
+}
+// one group by the 32 lanes of a half-wave; i = lane in the half
+__device__ __forceinline__ void limbs_group(float v, int i, sw_u32x4 *__restrict__ dst, float *__restrict__ fdst) {
+    bool bad;
+    const int e = limbs_exp(v, bad);
     float y = ldexpf(v, -e);                          // exact: |y| < 1
     uint32_t dw[SW_NL];
 #pragma unroll
     for (int l = 0; l < SW_NL; l++) {
-        const float t = y * 8.0f;                     // exact
-        float d = rintf(t);
-        d = fminf(fmaxf(d, -8.0f), 7.0f);
-        y = t - d;                                    // exact, |y| <= 1
+        const float d = limb_digit(y);
         uint32_t nib = ((uint32_t)(int)d & 0xFu) << (4 * (i & 7));
         nib |= __shfl_xor(nib, 1, 32);
         nib |= __shfl_xor(nib, 2, 32);

@@ -38,6 +38,7 @@ typedef _Float16 sw_half2 __attribute__((ext_vector_type(2)));
 typedef __bf16 sw_bf16x8 __attribute__((ext_vector_type(8)));
 typedef float sw_f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t sw_u32x4 __attribute__((ext_vector_type(4)));
+typedef int sw_i32x4 __attribute__((ext_vector_type(4)));
 
 #ifdef __HIPCC__
 #include <hip/hip_ext.h>
@@ -119,6 +120,28 @@ __device__ __forceinline__ int sw_xcd_work(int b, int nb) {
     return b < n8 ? (b & 7) * (n8 >> 3) + (b >> 3) : b;
 }
 
+// the work of grouped block bx: expert e, the group's first packed row beg and
+// its tokens [t0, tend) -- one pass from the pass list, or the whole group
+// (false: nothing to do)
+__device__ __forceinline__ bool grp_work(const SwGroups &grp, int bx, int TT, int &e, int &beg, int &t0, int &tend) {
+    if (grp.items) {
+        if (bx >= *grp.P) return false;
+        const int v = grp.items[bx], gi = v & 1023;
+        t0 = v >> 10;
+        e = grp.gexp[gi];
+        beg = grp.gbeg[gi];
+        tend = min(t0 + TT, grp.gcnt[gi]);
+        return true;
+    }
+    const int gvalid = grp.G ? *grp.G : grp.ngroups_max;
+    if (bx >= gvalid) return false;
+    e = grp.gexp ? grp.gexp[bx] : 0;
+    beg = grp.gbeg ? grp.gbeg[bx] : 0;
+    t0 = 0;
+    tend = grp.gcnt ? grp.gcnt[bx] : grp.cnt_const;
+    return true;
+}
+
 // int4 weight tensor of E experts, O rows each, K inputs
 struct SwQ4 {
     const uint8_t *q;     // [E*O, K/2]
@@ -126,6 +149,27 @@ struct SwQ4 {
     int O, K, gs;         // gs = 0: per-row scale
     int E;                // experts in the tensor (the extent of its buffer descriptors)
 };
+// The int4 tensors are read through buffer descriptors over all E experts
+// (extent E * O * K/2 bytes, and E * O * ng * 4 for the scales).
+static inline bool sw_q4_extent_ok(const SwQ4 &W) {
+    const int ng = W.gs > 0 ? W.K / W.gs : 1;
+    return W.E > 0 && (uint64_t)W.E * W.O * (W.K / 2) < (1ull << 32) && (uint64_t)W.E * W.O * ng * 4 < (1ull << 32);
+}
+__device__ __forceinline__ sw_rsrc sw_q4_rq(const SwQ4 &W) { return sw_make_rsrc(W.q, (uint32_t)W.E * W.O * (W.K / 2)); }
+__device__ __forceinline__ sw_rsrc sw_q4_rs(const SwQ4 &W) {
+    const int ng = W.gs > 0 ? W.K / W.gs : 1;
+    return sw_make_rsrc(W.s, (uint32_t)W.E * W.O * ng * 4);
+}
+// scale groups of gs inputs (a power of two, a multiple of 32): group of
+// input k is k >> gsh; gs <= 0 means one scale per row
+static inline int sw_q4_gsh(const SwQ4 &W, int &gsh) {
+    gsh = 0;
+    if (W.gs > 0) {
+        if (W.gs % 32 || W.K % W.gs || (W.gs & (W.gs - 1))) return -1;
+        while ((1 << gsh) < W.gs) gsh++;
+    }
+    return 0;
+}
 
 // bf16 weight tensor [O, K]
 struct SwBf16 {
@@ -198,6 +242,15 @@ int sw_launch_stage_experts(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, const fl
 // the shared expert on the VALU (sw_shared.h): h[S, Is] = silu(Wg x) * (Wu x)
 // and out[S, D] = Wd h, bf16 weights, f32 activations
 // stack glue (k_glue.hip): RMSNorm rows, greedy argmax rows
+// prefill expert GEMMs on the int8 MFMA (k_mfma.hip), bit-identical to the
+// dot8 ones: activations as MFMA digits dg[rows][K/32][32 dwords] + factors
+// xs[rows][K/32] (the limbs' exponent and integer, recut); tiles of up to 64
+// tokens of a group listed in g.items / g.P (sw_launch_bucket with tt = 64)
+#define SW_MF_TT 64
+int sw_launch_digits(hipStream_t st, const float *x, int rows, int K, uint32_t *dg, float *xs);
+int sw_launch_mf_glu(hipStream_t st, SwQ4 W, const uint32_t *dg, const float *xs, SwGroups g, int I, uint32_t *hdg,
+                     float *hxs);
+int sw_launch_mf_rows(hipStream_t st, SwQ4 W, const uint32_t *dg, const float *xs, SwGroups g, float *Y);
 int sw_launch_rmsnorm(hipStream_t st, const float *x, const float *w, float *out, int S, int D, float eps);
 int sw_launch_argmax(hipStream_t st, const float *logits, int S, int V, int *tok);
 // the shared expert of a batch over token tiles (k_shared.hip): h = silu(Wg x) * (Wu x); out = Wd h

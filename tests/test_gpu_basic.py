@@ -15,6 +15,13 @@ def test_mfma_layout(be):
     row, col = 4 * (lane // 16) + j, lane % 16
     assert np.array_equal(out[:256].reshape(64, 4), (32 * row + col).astype(np.float32))
     assert np.array_equal(out[256:512].reshape(64, 4), (2 * row + (col & 1)).astype(np.float32))
+    # int8 16x16x64: lane l = (row or column l % 16, k quarter l // 16), its 16
+    # bytes meeting the same bytes of the other operand's lane
+    b = np.arange(16)[None, :]
+    A = ((7 * np.arange(64)[:, None] + 13 * b) % 17 - 8).reshape(4, 16, 16)     # [quarter][row][byte]
+    B = ((5 * np.arange(64)[:, None] + 3 * b + 1) % 23 - 11).reshape(4, 16, 16)
+    C = np.einsum("qib,qjb->ij", A, B)
+    assert np.array_equal(out[512:768].reshape(64, 4), C[row, col].astype(np.float32))
 
 
 def test_device_libm_matches_host(be, orc):
@@ -28,7 +35,7 @@ def test_device_libm_matches_host(be, orc):
     xs = xs[~np.isnan(xs)]
     out = be.selftest(xs)
     n = xs.size
-    e_dev, l_dev = out[512:512 + n], out[512 + n:512 + 2 * n]
+    e_dev, l_dev = out[768:768 + n], out[768 + n:768 + 2 * n]
     e_host, l_host = orc.expf(xs), orc.log1pf(xs)
     assert np.array_equal(e_dev.view(np.uint32), e_host.view(np.uint32))
     ok = (l_dev.view(np.uint32) == l_host.view(np.uint32)) | (np.isnan(l_dev) & np.isnan(l_host))
