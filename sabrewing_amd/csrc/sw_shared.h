@@ -214,24 +214,20 @@ __device__ __forceinline__ void sh_tile_job(RowPtr rowp, int NR, int K, const fl
     sw_u32x4 w[SHT_R][4];
 #pragma unroll
     for (int r = 0; r < SHT_R; r++) wld(r < NS ? r : NS - 1, w[r]);
-    // the tile: nt tokens x G groups x 8 chunks of 16 bytes, SHT_XB chunks per thread
-    // in flight per pass (loads clamped to the last chunk, stores guarded)
-    const int nch = nt * G * 8;
-    for (int base = 0; base < nch; base += SHT_XB * SHT_NT) {
-        sw_f32x4 v[SHT_XB];
+    // the tile: nt tokens x G groups x 8 chunks of 16 bytes; per token row, chunk r
+    // by thread r mod SHT_NT, SHT_XB chunks per thread in flight (rows past the tile
+    // load the tile's last row and are not stored)
+    const int rch = G * 8;
+    for (int t0 = 0; t0 < nt; t0 += SHT_XB) {
+        for (int r = tid; r < rch; r += SHT_NT) {
+            const int gg = r >> 3, cc = r & 7;
+            sw_f32x4 v[SHT_XB];
 #pragma unroll
-        for (int u = 0; u < SHT_XB; u++) {
-            const int idx = min(base + u * SHT_NT + tid, nch - 1);
-            const int t = idx / (G * 8), r = idx - t * (G * 8);
-            v[u] = *(const sw_f32x4 *)(x + (int64_t)(tok0 + t) * K + (r >> 3) * SH_RG + 4 * (r & 7));
-        }
+            for (int u = 0; u < SHT_XB; u++)
+                v[u] = *(const sw_f32x4 *)(x + (int64_t)(tok0 + min(t0 + u, nt - 1)) * K + gg * SH_RG + 4 * cc);
 #pragma unroll
-        for (int u = 0; u < SHT_XB; u++) {
-            const int idx = base + u * SHT_NT + tid;
-            if (idx < nch) {
-                const int t = idx / (G * 8), r = idx - t * (G * 8), gg = r >> 3, cc = r & 7;
-                *(sw_f32x4 *)(xt + ((t * G + gg) * 8 + (cc ^ (gg & 7))) * 4) = v[u];
-            }
+            for (int u = 0; u < SHT_XB; u++)
+                if (t0 + u < nt) *(sw_f32x4 *)(xt + (((t0 + u) * G + gg) * 8 + (cc ^ (gg & 7))) * 4) = v[u];
         }
     }
     __syncthreads();
@@ -239,9 +235,22 @@ __device__ __forceinline__ void sh_tile_job(RowPtr rowp, int NR, int K, const fl
     const float *xg = xt + (size_t)g * 8 * 4;
     const int sw = g & 7;
     for (int b = 0; b < NB; b++) {
-        if (b > 0) {
+        // this batch's weights widened once for the tile's tokens; the next batch's in flight
+        float wf[SHT_R][SH_RG];
 #pragma unroll
-            for (int r = 0; r < SHT_R; r++) wld(min(b * SHT_R + r, NS - 1), w[r]);
+        for (int r = 0; r < SHT_R; r++)
+#pragma unroll
+            for (int qq = 0; qq < 4; qq++) {
+                const sw_u32x4 v = w[r][qq];
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    wf[r][8 * qq + 2 * j] = bf16lo(v[j]);
+                    wf[r][8 * qq + 2 * j + 1] = bf16hi(v[j]);
+                }
+            }
+        if (b + 1 < NB) {
+#pragma unroll
+            for (int r = 0; r < SHT_R; r++) wld(min((b + 1) * SHT_R + r, NS - 1), w[r]);
         }
         for (int t = 0; t < nt; t++) {                 // uniform over the block
             const float *xr = xg + (size_t)t * G * 8 * 4;
@@ -254,15 +263,15 @@ __device__ __forceinline__ void sh_tile_job(RowPtr rowp, int NR, int K, const fl
                 const sw_f32x4 xb = *(const sw_f32x4 *)(xr + ((2 * qq + 1) ^ sw) * 4);
 #pragma unroll
                 for (int r = 0; r < SHT_R; r++) {
-                    const sw_u32x4 v = w[r][qq];
-                    q[r] = __builtin_fmaf(bf16lo(v.x), xa.x, q[r]);
-                    q[r] = __builtin_fmaf(bf16hi(v.x), xa.y, q[r]);
-                    q[r] = __builtin_fmaf(bf16lo(v.y), xa.z, q[r]);
-                    q[r] = __builtin_fmaf(bf16hi(v.y), xa.w, q[r]);
-                    q[r] = __builtin_fmaf(bf16lo(v.z), xb.x, q[r]);
-                    q[r] = __builtin_fmaf(bf16hi(v.z), xb.y, q[r]);
-                    q[r] = __builtin_fmaf(bf16lo(v.w), xb.z, q[r]);
-                    q[r] = __builtin_fmaf(bf16hi(v.w), xb.w, q[r]);
+                    const float *wr = wf[r] + 8 * qq;
+                    q[r] = __builtin_fmaf(wr[0], xa.x, q[r]);
+                    q[r] = __builtin_fmaf(wr[1], xa.y, q[r]);
+                    q[r] = __builtin_fmaf(wr[2], xa.z, q[r]);
+                    q[r] = __builtin_fmaf(wr[3], xa.w, q[r]);
+                    q[r] = __builtin_fmaf(wr[4], xb.x, q[r]);
+                    q[r] = __builtin_fmaf(wr[5], xb.y, q[r]);
+                    q[r] = __builtin_fmaf(wr[6], xb.z, q[r]);
+                    q[r] = __builtin_fmaf(wr[7], xb.w, q[r]);
                 }
             }
 #pragma unroll
