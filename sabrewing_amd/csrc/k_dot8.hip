@@ -83,22 +83,29 @@ int sw_launch_limbs(hipStream_t st, const float *x, int rows, int K, sw_u32x4 *x
 }
 
 // exact int32 sum_k (n_k - 8) D_k over one group: a = the group's 16 weight
-// bytes with every nibble XOR 8 (signed nibbles n - 8); the NL limb dots are
-// independent chains, joined by Horner (every partial sum is exact and below
-// 2^29.2 in magnitude)
-__device__ __forceinline__ int dot8_group(sw_u32x4 a, const sw_u32x4 *X) {
-    int p[SW_NL];
+// bytes with every nibble XOR 8 (signed nibbles n - 8).  Horner over the
+// limbs folded into dot8 chains -- acc = (acc << 3), then limb l's four dot8
+// accumulate into it -- as two independent chains (limbs 0..3 and 4..6)
+// joined at the end: acc = (hi << 9) + lo.  Every partial sum is an exact
+// Horner prefix, below 2^29.2 in magnitude.
+__device__ __forceinline__ int dot8_chain(sw_u32x4 a, const sw_u32x4 *X, int l0, int l1) {
+    int acc = __builtin_amdgcn_sdot8((int)a.x, (int)X[l0].x, 0, false);
+    acc = __builtin_amdgcn_sdot8((int)a.y, (int)X[l0].y, acc, false);
+    acc = __builtin_amdgcn_sdot8((int)a.z, (int)X[l0].z, acc, false);
+    acc = __builtin_amdgcn_sdot8((int)a.w, (int)X[l0].w, acc, false);
 #pragma unroll
-    for (int l = 0; l < SW_NL; l++) {
-        int t = __builtin_amdgcn_sdot8((int)a.x, (int)X[l].x, 0, false);
-        t = __builtin_amdgcn_sdot8((int)a.y, (int)X[l].y, t, false);
-        t = __builtin_amdgcn_sdot8((int)a.z, (int)X[l].z, t, false);
-        p[l] = __builtin_amdgcn_sdot8((int)a.w, (int)X[l].w, t, false);
+    for (int l = l0 + 1; l < l1; l++) {
+        acc = __builtin_amdgcn_sdot8((int)a.x, (int)X[l].x, acc << 3, false);
+        acc = __builtin_amdgcn_sdot8((int)a.y, (int)X[l].y, acc, false);
+        acc = __builtin_amdgcn_sdot8((int)a.z, (int)X[l].z, acc, false);
+        acc = __builtin_amdgcn_sdot8((int)a.w, (int)X[l].w, acc, false);
     }
-    int acc = p[0];
-#pragma unroll
-    for (int l = 1; l < SW_NL; l++) acc = (acc << 3) + p[l];
     return acc;
+}
+#define DOT8_SPLIT 4          // limbs of the high chain
+__device__ __forceinline__ int dot8_group(sw_u32x4 a, const sw_u32x4 *X) {
+    const int hi = dot8_chain(a, X, 0, DOT8_SPLIT), lo = dot8_chain(a, X, DOT8_SPLIT, SW_NL);
+    return (hi << (3 * (SW_NL - DOT8_SPLIT))) + lo;
 }
 
 // A row's terms: one per group of 32 inputs, the lanes of a row padded to

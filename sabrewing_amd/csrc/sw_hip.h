@@ -124,21 +124,23 @@ __device__ __forceinline__ int sw_xcd_work(int b, int nb) {
 // its tokens [t0, tend) -- one pass from the pass list, or the whole group
 // (false: nothing to do)
 __device__ __forceinline__ bool grp_work(const SwGroups &grp, int bx, int TT, int &e, int &beg, int &t0, int &tend) {
+    // (uniform over the block: read into scalar registers)
+    auto u = [](int v) { return __builtin_amdgcn_readfirstlane(v); };
     if (grp.items) {
-        if (bx >= *grp.P) return false;
-        const int v = grp.items[bx], gi = v & 1023;
+        if (bx >= u(*grp.P)) return false;
+        const int v = u(grp.items[bx]), gi = v & 1023;
         t0 = v >> 10;
-        e = grp.gexp[gi];
-        beg = grp.gbeg[gi];
-        tend = min(t0 + TT, grp.gcnt[gi]);
+        e = u(grp.gexp[gi]);
+        beg = u(grp.gbeg[gi]);
+        tend = min(t0 + TT, u(grp.gcnt[gi]));
         return true;
     }
-    const int gvalid = grp.G ? *grp.G : grp.ngroups_max;
+    const int gvalid = grp.G ? u(*grp.G) : grp.ngroups_max;
     if (bx >= gvalid) return false;
-    e = grp.gexp ? grp.gexp[bx] : 0;
-    beg = grp.gbeg ? grp.gbeg[bx] : 0;
+    e = grp.gexp ? u(grp.gexp[bx]) : 0;
+    beg = grp.gbeg ? u(grp.gbeg[bx]) : 0;
     t0 = 0;
-    tend = grp.gcnt ? grp.gcnt[bx] : grp.cnt_const;
+    tend = grp.gcnt ? u(grp.gcnt[bx]) : grp.cnt_const;
     return true;
 }
 
