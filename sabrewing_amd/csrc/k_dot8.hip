@@ -452,7 +452,7 @@ __device__ __forceinline__ void dot8_rows_block(const Dot8RowsArgs &A, int bx, i
 }
 
 template <int PF, int TT, int C16>
-__global__ __launch_bounds__(256) void k_dot8_rows(Dot8RowsArgs A) {
+__global__ __launch_bounds__(256, 4) void k_dot8_rows(Dot8RowsArgs A) {
     extern __shared__ __align__(16) float red[];
     TR_BEGIN();
     const int nb = (int)(gridDim.x * gridDim.y);
@@ -615,7 +615,7 @@ __global__ __launch_bounds__(SH_NT) void k_stage_route(RouterArgs R, int nbr, in
 
 // TTG: tokens per pass of the routed gate_up; TTS: of the shared down
 template <int PF, int PICK, int NP, int TTG, int TTS, int C16>
-__global__ __launch_bounds__(DG_NT) void k_stage_experts(Dot8GluArgs A, int nbx, int nglu, ShDownArgs Sd) {
+__global__ __launch_bounds__(DG_NT, PICK ? 1 : 4) void k_stage_experts(Dot8GluArgs A, int nbx, int nglu, ShDownArgs Sd) {
     extern __shared__ __align__(16) float smem[];
     TR_BEGIN();
     const int b = blockIdx.x;
@@ -696,7 +696,8 @@ int sw_launch_stage_experts(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, const fl
     const dim3 grid((unsigned)(nglu + nsh));
     const size_t shl = sd ? (TTS == SH_TT ? sh_down_lds<SH_TT>(Is) : sh_down_lds<1>(Is)) : 0;
     const int pf0 = dg_pf_glu(W.K), c16 = dot8_c16(W.K);
-    // groups: a shallower ring (4 steps) keeps the kernel within 128 VGPRs, two blocks per CU
+    // groups: a 4-step ring, two blocks per CU (four waves per SIMD, 128 VGPRs); an
+    // 8-step ring also fits but measured slower at B=32 (224 vs 215 us)
     const int pf = picks ? pf0 : (pf0 < 4 ? pf0 : 4);
     if (!picks) {
         const size_t lds = lds_max(dot8_glu_lds(W.K, DG_TT), shl);
