@@ -126,18 +126,17 @@ __host__ __device__ inline int dg_rps(int Gq, int cap, int nt) {
 
 
 // ------------------------------------------------------------ gate_up ----
-// One block = 32 consecutive intermediate outputs i of one group: gate rows
-// i0..i0+31 and up rows i0..i0+31 (64 weight rows), every input group, for a
-// tile of up to TT tokens of the group per pass over the block's weights (a
-// group with more tokens takes further passes, which re-read the block's
-// weights from L2).  Thread (row slot ro, input group g): Gq threads per row,
-// RPS row slots; slot ro takes NSH = 32/RPS consecutive gate rows and the
-// same up rows, one row per step (steps 0..NSH-1 gate, NSH..2NSH-1 up), so
-// its addresses are a fixed lane offset plus a per-step scalar one.  The
-// tile's limbs of its group stay in registers; PF steps of weight loads are
-// in flight; a row's run sums go to LDS and the row sums, the SiLU-GLU and
-// the limbs of h (the down projection's input) follow.
-#define DG_ROWS 64
+// One block = RO (32; 128 or 64 for batches) consecutive intermediate outputs i
+// of one group: gate rows i0..i0+RO-1 and up rows i0..i0+RO-1, every input
+// group, for a tile of up to TT tokens of the group per pass over the block's
+// weights (a group with more tokens takes further passes, which re-read the
+// block's weights from L2).  Thread (row slot ro, input group g): Gq threads
+// per row, RPS row slots; slot ro takes NSH = RO/RPS consecutive gate rows
+// and the same up rows, one row per step (steps 0..NSH-1 gate, NSH..2NSH-1
+// up), so its addresses are a fixed lane offset plus a per-step scalar one.
+// The tile's limbs of its group stay in registers; PF steps of weight loads
+// are in flight; a row's run sums go to LDS and the row sums, the SiLU-GLU
+// and the limbs of h (the down projection's input) follow.
 #define DG_TT SW_DG_TT        // tokens per weight pass in the grouped kernels
 #define DG_NT 512             // threads per gate_up block
 // One token (PICK = 1): block (rank a, set of outputs) takes pick a and
@@ -173,11 +172,12 @@ static int dot8_c16(int K) { return (K / RG) % CHG == 0; }
 static int dg_pf_glu(int K) { const int n = 32 / dg_rps(run_lanes(K / RG), 32, DG_NT); return n < 8 ? n : 8; }
 static int dg_pf_rows(int K) { const int n = 64 / dg_rps(run_lanes(K / RG), 64, 256); return n < 8 ? n : 8; }
 
-// block (bx = group or rank, by = set of 32 outputs); runs: the dynamic LDS,
-// [TT][DG_ROWS][NC] floats
-template <int PF, int PICK, int NP, int TT, int C16>
+// block (bx = group or rank, by = set of RO outputs: 32, or up to 128 for groups --
+// fewer, longer blocks per weight byte); runs: the dynamic LDS, [TT][2 RO][NC] floats
+template <int PF, int PICK, int NP, int TT, int C16, int RO>
 __device__ __forceinline__ void dot8_glu_block(const Dot8GluArgs &A, int bx, int by, float *runs) {
     static_assert(PICK == 0 || TT == 1, "picks are of one token");
+    static_assert(RO == 32 || RO == 64 || RO == 128, "1, 2 or 4 limb groups of h per block");
     const SwQ4 W = A.W;
     const int I = A.I;
     const sw_u32x4 *__restrict__ xl = A.xl;
@@ -185,12 +185,12 @@ __device__ __forceinline__ void dot8_glu_block(const Dot8GluArgs &A, int bx, int
     const SwGroups grp = A.grp;
     const int K = W.K, G = K / RG, Gq = C16 ? G : run_lanes(G);
     const int CH = C16 ? CHG : (Gq < CHG ? Gq : CHG), NC = Gq / CH;
-    const int RPS = dg_rps(Gq, 32, DG_NT), NSH = 32 / RPS;    // a row slot: NSH gate rows and NSH up rows
+    const int RPS = dg_rps(Gq, RO, DG_NT), NSH = RO / RPS;    // a row slot: NSH gate rows and NSH up rows
     const int tid = threadIdx.x, ro = tid / Gq, gq = tid - ro * Gq, c = gq / CH;
     const bool worker = ro < RPS, lead = worker && (gq & (CH - 1)) == 0, gv = C16 || gq < G;
     const int g = gv ? gq : G - 1;                   // padding lanes load group G-1 and add 0
     const int roc = worker ? ro : 0;
-    const int i0 = by * (DG_ROWS / 2);
+    const int i0 = by * RO;
     const int ng = W.gs > 0 ? K / W.gs : 1;
     const int sg = W.gs > 0 ? (g * RG) >> A.gsh : 0;
     const uint32_t rb = (uint32_t)K / 2, sb = (uint32_t)ng * 4;
@@ -258,12 +258,12 @@ __device__ __forceinline__ void dot8_glu_block(const Dot8GluArgs &A, int bx, int
                 sa[u] = sw_ld4f(rs, vos, srow(s + PF) * sb);
                 __builtin_amdgcn_sched_barrier(0);
             }
-            const int urow = s < NSH ? s : 32 + s - NSH;                 // local row minus roc * NSH
+            const int urow = s < NSH ? s : RO + s - NSH;                 // local row minus roc * NSH
 #pragma unroll
             for (int t = 0; t < TT; t++) {
                 if (t < nt) {                          // uniform over the block
                     const float p = row_term<C16>((float)dot8_group(w, X[t]) * (sc * xf[t]), gv, CH);
-                    if (lead) myruns[(t * DG_ROWS + urow) * NC] = p;
+                    if (lead) myruns[(t * 2 * RO + urow) * NC] = p;
                 }
             }
         };
@@ -277,10 +277,10 @@ __device__ __forceinline__ void dot8_glu_block(const Dot8GluArgs &A, int bx, int
         TR_MARK(1);
         __syncthreads();
         TR_MARK(2);
-        // token t of the tile by the half-wave of threads 32t..32t+31
-        const int t = tid >> 5, i = tid & 31;
+        // token t of the tile by the threads RO t .. RO t + RO - 1 (a half-wave per limb group)
+        const int t = tid / RO, i = tid - t * RO;
         if (t < nt) {
-            const float *rg = runs + (t * DG_ROWS + i) * NC, *ru = runs + (t * DG_ROWS + 32 + i) * NC;
+            const float *rg = runs + (t * 2 * RO + i) * NC, *ru = runs + (t * 2 * RO + RO + i) * NC;
             float yg = rg[0], yu = ru[0];
             for (int cc = 1; cc < NC; cc++) { yg = yg + rg[cc]; yu = yu + ru[cc]; }
             if (W.gs <= 0) {                            // per-row scales after the sum
@@ -288,19 +288,19 @@ __device__ __forceinline__ void dot8_glu_block(const Dot8GluArgs &A, int bx, int
                 yu = yu * W.s[(int64_t)e * (2 * I) + I + i0 + i];
             }
             const float h = (yg / (1.0f + expf(-yg))) * yu;
-            // the block's 32 outputs are one limb group of the down projection's input
-            const int GI = I / RG, gi_out = i0 / RG;
+            // every 32 of the block's outputs are one limb group of the down projection's input
+            const int GI = I / RG, gi_out = (i0 + i) / RG;
             const int64_t prow = beg + t0 + t;
-            limbs_group(h, i, A.hl + (prow * GI + gi_out) * SW_NL, A.hs + prow * GI + gi_out);
+            limbs_group(h, i & 31, A.hl + (prow * GI + gi_out) * SW_NL, A.hs + prow * GI + gi_out);
         }
         __syncthreads();
     }
 }
 
-template <int PF, int PICK, int TT, int C16>
+template <int PF, int PICK, int TT, int C16, int RO>
 __global__ __launch_bounds__(DG_NT) void k_dot8_glu(Dot8GluArgs A) {
     extern __shared__ __align__(16) float red[];
-    dot8_glu_block<PF, PICK, 0, TT, C16>(A, blockIdx.x, blockIdx.y, red);
+    dot8_glu_block<PF, PICK, 0, TT, C16, RO>(A, blockIdx.x, blockIdx.y, red);
 }
 
 // dispatch on the prefetch depth pf (1, 2, 4 or 8) and C16
@@ -318,29 +318,35 @@ static void dispatch_pf_c16(int pf, int c16, Args &&...args) {
         else L<1, 0>::go(args...);
     }
 }
-template <int PICK, int TT>
+template <int PICK, int TT, int RO>
 struct GluL {
     template <int PF, int C16>
     struct L {
         static void go(dim3 grid, size_t lds, hipStream_t st, const Dot8GluArgs &A) {
-            SW_LAUNCH((k_dot8_glu<PF, PICK, TT, C16>), grid, dim3(DG_NT), lds, st, A);
+            SW_LAUNCH((k_dot8_glu<PF, PICK, TT, C16, RO>), grid, dim3(DG_NT), lds, st, A);
         }
     };
 };
+// outputs per gate_up block of a batch: 128 or 64 when I allows (fewer blocks, so less
+// per-block start and epilogue per weight byte: B=32 gate_up 215 -> 190 us), else 32
+static int dg_ro(int I) { return I % 128 == 0 ? 128 : I % 64 == 0 ? 64 : 32; }
 
 static int dot8_glu_check(SwQ4 W, int I, int &gsh) {
     if (!dot8_shape_ok(W.K) || I % 32 || W.O != 2 * I || !sw_q4_extent_ok(W)) return -1;
     return sw_q4_gsh(W, gsh);
 }
-static size_t dot8_glu_lds(int K, int TT) { return (size_t)TT * DG_ROWS * dot8_nc(K) * 4; }
+static size_t dot8_glu_lds(int K, int TT, int RO = 32) { return (size_t)TT * 2 * RO * dot8_nc(K) * 4; }
 
 int sw_launch_q4_dot8_glu(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, const float *xs, SwGroups g, int I,
                           sw_u32x4 *hl, float *hs) {
     int gsh;
     if (dot8_glu_check(W, I, gsh) || g.ngroups_max <= 0) return -1;
     const Dot8GluArgs A = {W, gsh, xl, xs, g, I, hl, hs, nullptr, DotRoute{}};
-    dispatch_pf_c16<GluL<0, DG_TT>::L>(dg_pf_glu(W.K), dot8_c16(W.K), dim3((unsigned)g.ngroups_max, (unsigned)(I / 32)),
-                                       dot8_glu_lds(W.K, DG_TT), st, A);
+    const int RO = dg_ro(I);
+    const dim3 grid((unsigned)g.ngroups_max, (unsigned)(I / RO));
+    if (RO == 128) dispatch_pf_c16<GluL<0, DG_TT, 128>::L>(dg_pf_glu(W.K), dot8_c16(W.K), grid, dot8_glu_lds(W.K, DG_TT, 128), st, A);
+    else if (RO == 64) dispatch_pf_c16<GluL<0, DG_TT, 64>::L>(dg_pf_glu(W.K), dot8_c16(W.K), grid, dot8_glu_lds(W.K, DG_TT, 64), st, A);
+    else dispatch_pf_c16<GluL<0, DG_TT, 32>::L>(dg_pf_glu(W.K), dot8_c16(W.K), grid, dot8_glu_lds(W.K, DG_TT, 32), st, A);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
@@ -349,16 +355,17 @@ int sw_launch_q4_dot8_glu_picks(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, cons
     int gsh;
     if (dot8_glu_check(W, I, gsh) || K <= 0 || K > 64 || !sel) return -1;
     const Dot8GluArgs A = {W, gsh, xl, xs, SwGroups{}, I, hl, hs, const_cast<int *>(sel), DotRoute{}};
-    dispatch_pf_c16<GluL<1, 1>::L>(dg_pf_glu(W.K), dot8_c16(W.K), dim3((unsigned)K, (unsigned)(I / 32)), dot8_glu_lds(W.K, 1), st, A);
+    dispatch_pf_c16<GluL<1, 1, 32>::L>(dg_pf_glu(W.K), dot8_c16(W.K), dim3((unsigned)K, (unsigned)(I / 32)), dot8_glu_lds(W.K, 1), st, A);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
 // ------------------------------------------------------------ rows ----
 // Y[packed row, O] = W_e . x for every packed row of every group (the down
-// projection of the grouped path): block = 64 consecutive output rows of one
-// group, a tile of up to DG_TT tokens per weight pass; thread (row slot ro,
-// input group g) takes NS = 64/RPS consecutive rows, one per step; same
-// fixed-order row sums, f32 rows out.
+// projection of the grouped path): block = RB (128, or 64 when O is not a
+// multiple of 128) consecutive output rows of one group, a tile of up to
+// DG_TT tokens per weight pass; thread (row slot ro, input group g) takes
+// NS = RB/RPS consecutive rows, one per step; same fixed-order row sums, f32
+// rows out.
 struct Dot8RowsArgs {
     SwQ4 W;
     int gsh;
@@ -367,7 +374,7 @@ struct Dot8RowsArgs {
     SwGroups grp;
     float *Y;
 };
-template <int PF, int TT, int C16>
+template <int PF, int TT, int C16, int RB>
 __device__ __forceinline__ void dot8_rows_block(const Dot8RowsArgs &A, int bx, int by, float *runs) {
     const SwQ4 W = A.W;
     const sw_u32x4 *__restrict__ xl = A.xl;
@@ -376,15 +383,15 @@ __device__ __forceinline__ void dot8_rows_block(const Dot8RowsArgs &A, int bx, i
     float *__restrict__ Y = A.Y;
     const int K = W.K, G = K / RG, O = W.O, Gq = C16 ? G : run_lanes(G);
     const int CH = C16 ? CHG : (Gq < CHG ? Gq : CHG), NC = Gq / CH;
-    const int RPS = dg_rps(Gq, 64, 256), NS = DG_ROWS / RPS;
+    const int RPS = dg_rps(Gq, RB, 256), NS = RB / RPS;
     const int tid = threadIdx.x, ro = tid / Gq, gq = tid - ro * Gq, c = gq / CH;
     const bool worker = ro < RPS, lead = worker && (gq & (CH - 1)) == 0, gv = C16 || gq < G;
     const int g = gv ? gq : G - 1;
     const int roc = worker ? ro : 0;
     int e, beg, tb, tend;
     if (!grp_work(grp, bx, TT, e, beg, tb, tend)) return;
-    const int r0 = by * DG_ROWS;
-    const int nrows = min(DG_ROWS, O - r0);
+    const int r0 = by * RB;
+    const int nrows = min(RB, O - r0);
     const int ng = W.gs > 0 ? K / W.gs : 1;
     const int sg = W.gs > 0 ? (g * RG) >> A.gsh : 0;
     const uint32_t rb = (uint32_t)K / 2, sb = (uint32_t)ng * 4;
@@ -425,7 +432,7 @@ __device__ __forceinline__ void dot8_rows_block(const Dot8RowsArgs &A, int bx, i
             for (int t = 0; t < TT; t++) {
                 if (t < nt) {                          // uniform over the block
                     const float p = row_term<C16>((float)dot8_group(w, X[t]) * (sc * xf[t]), gv, CH);
-                    if (lead) myruns[(t * DG_ROWS + s) * NC] = p;
+                    if (lead) myruns[(t * RB + s) * NC] = p;
                 }
             }
         };
@@ -437,8 +444,8 @@ __device__ __forceinline__ void dot8_rows_block(const Dot8RowsArgs &A, int bx, i
 #pragma unroll
         for (int u = 0; u < PF; u++) step(s0 + u, u, false);
         __syncthreads();
-        for (int it = tid; it < TT * DG_ROWS; it += 256) {
-            const int t = it / DG_ROWS, r = it - t * DG_ROWS;
+        for (int it = tid; it < TT * RB; it += 256) {
+            const int t = it / RB, r = it - t * RB;
             if (t < nt && r < nrows) {
                 const float *rr = runs + it * NC;
                 float y = rr[0];
@@ -451,32 +458,40 @@ __device__ __forceinline__ void dot8_rows_block(const Dot8RowsArgs &A, int bx, i
     }
 }
 
-template <int PF, int TT, int C16>
+template <int PF, int TT, int C16, int RB>
 __global__ __launch_bounds__(256, 4) void k_dot8_rows(Dot8RowsArgs A) {
     extern __shared__ __align__(16) float red[];
     TR_BEGIN();
     const int nb = (int)(gridDim.x * gridDim.y);
     const int w = A.grp.items ? sw_xcd_work((int)(blockIdx.x + gridDim.x * blockIdx.y), nb)
                               : (int)(blockIdx.x + gridDim.x * blockIdx.y);
-    dot8_rows_block<PF, TT, C16>(A, w % (int)gridDim.x, w / (int)gridDim.x, red);
+    dot8_rows_block<PF, TT, C16, RB>(A, w % (int)gridDim.x, w / (int)gridDim.x, red);
     TR_END(3);
 }
-template <int PF, int C16>
 #define RW_PF 4
+template <int RB>
 struct RowsL {
-    static void go(dim3 grid, size_t lds, hipStream_t st, const Dot8RowsArgs &A) {
-        SW_LAUNCH((k_dot8_rows<PF, DG_TT, C16>), grid, dim3(256), lds, st, A);
-    }
+    template <int PF, int C16>
+    struct L {
+        static void go(dim3 grid, size_t lds, hipStream_t st, const Dot8RowsArgs &A) {
+            SW_LAUNCH((k_dot8_rows<PF, DG_TT, C16, RB>), grid, dim3(256), lds, st, A);
+        }
+    };
 };
 
 int sw_launch_q4_dot8_rows(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, const float *xs, SwGroups g, float *Y) {
     int gsh;
     if (!dot8_shape_ok(W.K) || g.ngroups_max <= 0 || W.O <= 0 || !sw_q4_extent_ok(W) || sw_q4_gsh(W, gsh)) return -1;
-    const dim3 grid((unsigned)g.ngroups_max, (unsigned)((W.O + DG_ROWS - 1) / DG_ROWS));
+    // 128 rows per block when O allows (half the blocks: half the per-block start and
+    // epilogue per weight byte), else 64
+    const int RB = W.O % 128 == 0 ? 128 : 64;          // (256 rows measured no faster at B=32)
+    const dim3 grid((unsigned)g.ngroups_max, (unsigned)((W.O + RB - 1) / RB));
     const Dot8RowsArgs A = {W, gsh, xl, xs, g, Y};
     // a ring of at most RW_PF steps: within 128 VGPRs, four blocks per CU
     const int pf = dg_pf_rows(W.K) < RW_PF ? dg_pf_rows(W.K) : RW_PF;
-    dispatch_pf_c16<RowsL>(pf, dot8_c16(W.K), grid, dot8_glu_lds(W.K, DG_TT), st, A);
+    const size_t lds = (size_t)DG_TT * RB * dot8_nc(W.K) * 4;
+    if (RB == 128) dispatch_pf_c16<RowsL<128>::L>(pf, dot8_c16(W.K), grid, lds, st, A);
+    else dispatch_pf_c16<RowsL<64>::L>(pf, dot8_c16(W.K), grid, lds, st, A);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
@@ -614,25 +629,25 @@ __global__ __launch_bounds__(SH_NT) void k_stage_route(RouterArgs R, int nbr, in
 }
 
 // TTG: tokens per pass of the routed gate_up; TTS: of the shared down
-template <int PF, int PICK, int NP, int TTG, int TTS, int C16>
+template <int PF, int PICK, int NP, int TTG, int TTS, int C16, int RO>
 __global__ __launch_bounds__(DG_NT, PICK ? 1 : 4) void k_stage_experts(Dot8GluArgs A, int nbx, int nglu, ShDownArgs Sd) {
     extern __shared__ __align__(16) float smem[];
     TR_BEGIN();
     const int b = blockIdx.x;
     if (b < nglu) {
         const int w = PICK == 0 && A.grp.items ? sw_xcd_work(b, nglu) : b;
-        dot8_glu_block<PF, PICK, NP, TTG, C16>(A, w % nbx, w / nbx, smem);
+        dot8_glu_block<PF, PICK, NP, TTG, C16, RO>(A, w % nbx, w / nbx, smem);
     } else {
         sh_down_block<TTS>(Sd.Wd, Sd.h, Sd.S, Sd.Is, Sd.D, Sd.out, b - nglu, smem);
     }
     TR_END(1);
 }
-template <int PICK, int NP, int TTG, int TTS>
+template <int PICK, int NP, int TTG, int TTS, int RO = 32>
 struct StageL {
     template <int PF, int C16>
     struct L {
         static void go(dim3 grid, size_t lds, hipStream_t st, const Dot8GluArgs &A, int nbx, int nglu, const ShDownArgs &Sd) {
-            SW_LAUNCH((k_stage_experts<PF, PICK, NP, TTG, TTS, C16>), grid, dim3(DG_NT), lds, st, A, nbx, nglu, Sd);
+            SW_LAUNCH((k_stage_experts<PF, PICK, NP, TTG, TTS, C16, RO>), grid, dim3(DG_NT), lds, st, A, nbx, nglu, Sd);
         }
     };
 };
@@ -687,7 +702,8 @@ int sw_launch_stage_experts(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, const fl
     if (!picks && g.ngroups_max <= 0) return -1;
     if (sd && (D % SH_DN_O || !sh_shape_ok(Is))) return -1;
     const int nbx = picks ? K : g.ngroups_max;
-    const int nglu = nbx * (I / 32);
+    const int RO = picks || (sd && S >= 2) ? 32 : dg_ro(I);   // outputs per gate_up block
+    const int nglu = nbx * (I / RO);
     const int TTS = S >= 2 && sd ? SH_TT : 1;         // (no shared blocks: the smaller instance)
     const int nsh = sd ? sh_down_blocks(S, D, TTS) : 0;
     const DotRoute rt = route_src ? DotRoute{route_src, bias, E, K, act, use_bias, norm, w} : DotRoute{};
@@ -700,8 +716,10 @@ int sw_launch_stage_experts(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, const fl
     // 8-step ring also fits but measured slower at B=32 (224 vs 215 us)
     const int pf = picks ? pf0 : (pf0 < 4 ? pf0 : 4);
     if (!picks) {
-        const size_t lds = lds_max(dot8_glu_lds(W.K, DG_TT), shl);
+        const size_t lds = lds_max(dot8_glu_lds(W.K, DG_TT, RO), shl);
         if (TTS == SH_TT) dispatch_pf_c16<StageL<0, 0, DG_TT, SH_TT>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd);
+        else if (RO == 128) dispatch_pf_c16<StageL<0, 0, DG_TT, 1, 128>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd);
+        else if (RO == 64) dispatch_pf_c16<StageL<0, 0, DG_TT, 1, 64>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd);
         else dispatch_pf_c16<StageL<0, 0, DG_TT, 1>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd);
     } else {
         const size_t lds = lds_max(dot8_glu_lds(W.K, 1), shl);
