@@ -357,6 +357,14 @@ class DeviceLayer:
         return self
 
     @classmethod
+    def from_container(cls, be, snap, i):
+        """MoE layer i of a Laguna int4 snapshot (sabrewing_amd.container.Snapshot);
+        the layer's descriptor is self.cfg"""
+        from .container import load_layer
+        cfg, L = load_layer(snap, i)
+        return cls.from_host(be, cfg, L)
+
+    @classmethod
     def generate(cls, be, cfg, base_seed, layer=0):
         """Generate a seeded layer directly in HBM (same bits as the host generator)."""
         self = cls(be, cfg)

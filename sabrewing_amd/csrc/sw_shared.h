@@ -45,7 +45,9 @@ __host__ __device__ inline bool sh_shape_ok(int K) { return K > 0 && K % SH_RG =
 // NS = NR/RPS consecutive rows, one per step, SH_PF steps of loads in flight,
 // the group's inputs of every token of the tile in registers.  LDS:
 // runs[NR * TT * NC] floats, NC = Gq / min(Gq, 16).
+#ifndef SH_PF
 #define SH_PF 2
+#endif
 __host__ __device__ inline int sh_rps(int Gq, int NR, int NT) {
     int r = 1;
     while (r * 2 * Gq <= NT && r < NR) r *= 2;
@@ -122,7 +124,9 @@ __host__ __device__ inline int sh_nc(int K) { return K / SH_RG < SH_CHG ? 1 : ru
 // shared expert gate_up: SH_GLU_O outputs i per block; local rows 0..O-1 are
 // gate rows i0.., rows O..2O-1 the up rows; h[tok][i] = silu(gate) * up (f32)
 #define SH_NT 512              // threads per block of the shared-expert jobs
+#ifndef SH_GLU_O
 #define SH_GLU_O 8
+#endif
 template <int TT>
 __device__ __forceinline__ void sh_glu_block(const uint16_t *__restrict__ Wg, const uint16_t *__restrict__ Wu,
                                              const float *__restrict__ x, int S, int D, int Is, float *__restrict__ h,
