@@ -176,6 +176,16 @@ void   lag_hip_graph_destroy(void *g);
  * grouped kernel there, c/backend_cuda.cu:618-700): a tuning switch. */
 int    lag_hip_set_grouped_kernel(int mode);
 
+/* The int4 activation contract of lag_hip_moe_forward / lag_hip_moe_block for
+ * per-row scales (gs == 0): 0 (default) this build's exact-integer digits,
+ * 1 the reference's IDOT contract -- activations to int8 per 32-block
+ * (amax/127, lrintf), exact int8 x int4 block dots, acc = fma(s_b, dot_b, acc)
+ * in block order, x row scale (c/moe_quant.h:48-82, 141-182) -- which gives
+ * the bits of the CPU tier under LAG_IDOT=1 (c/laguna.c:204-207).  Returns
+ * the previous mode, -1 for a bad one; descriptors with gs > 0 ignore it (the
+ * reference's grouped kernel has no IDOT form, c/quant.h:168-203). */
+int    lag_hip_set_q4_mode(int mode);
+
 /* per-kernel timing with events on the backend stream (the analogue of the
  * reference's COLI_CUDA_PROFILE=1, c/backend_cuda.cu:822-940) */
 int    lag_hip_profile(int enable);

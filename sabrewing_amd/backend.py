@@ -27,6 +27,7 @@ EXPORTS = [
     "lag_hip_matmul_q4_g", "lag_hip_expert_q4_g", "lag_hip_moe_experts_g", "lag_hip_moe_group_g",
     "lag_hip_router_upload", "lag_hip_router_chain", "lag_hip_moe_forward", "lag_hip_moe_block", "lag_hip_route",
     "lag_hip_last_groups", "lag_hip_rmsnorm", "lag_hip_head_argmax", "lag_hip_argmax", "lag_hip_set_grouped_kernel",
+    "lag_hip_set_q4_mode",
     "lag_hip_alloc", "lag_hip_h2d", "lag_hip_d2h", "lag_hip_d2d", "lag_hip_memset",
     "lag_hip_graph_begin", "lag_hip_graph_end", "lag_hip_graph_launch", "lag_hip_graph_destroy", "lag_hip_sync",
     "lag_hip_event_create", "lag_hip_event_record", "lag_hip_event_elapsed_ms", "lag_hip_event_destroy",
@@ -107,6 +108,7 @@ def load_library(path=None):
     L.lag_hip_event_destroy.argtypes = [VP]
     L.lag_hip_profile.argtypes = [C.c_int]
     L.lag_hip_set_grouped_kernel.argtypes = [C.c_int]
+    L.lag_hip_set_q4_mode.argtypes = [C.c_int]
     L.lag_hip_profile_read.argtypes = [C.c_int, C.c_char_p, C.c_int, C.POINTER(C.c_double), C.POINTER(C.c_longlong)]
     L.lag_hip_gen_normal.argtypes = [VP, C.c_int64, C.c_uint64, C.c_uint64, C.c_double, C.c_int]
     L.lag_hip_gen_bf16.argtypes = [VP, C.c_int64, C.c_uint64, C.c_uint64, C.c_double]
@@ -305,6 +307,17 @@ class Backend:
         prev = self.lib.lag_hip_set_grouped_kernel(int(mode))
         if prev < 0:
             raise BackendError(f"bad grouped-kernel mode {mode}")
+        return prev
+
+    Q4_DOT8, Q4_IDOT = 0, 1
+
+    def set_q4_mode(self, mode):
+        """the int4 activation contract of moe_forward for per-row scales: 0 this
+        build's exact-integer form, 1 the reference's IDOT (LAG_IDOT=1); returns the
+        previous mode"""
+        prev = self.lib.lag_hip_set_q4_mode(int(mode))
+        if prev < 0:
+            raise BackendError(f"bad q4 mode {mode}")
         return prev
 
     def profile_reset(self):

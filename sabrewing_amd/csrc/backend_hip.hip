@@ -230,6 +230,17 @@ extern "C" int lag_hip_set_grouped_kernel(int mode) {
     return prev;
 }
 
+// The int4 activation contract of the device-resident layer for per-row scales
+// (gs == 0): 0 this build's exact-integer dot8/MFMA form, 1 the reference's IDOT
+// (int8 activations per 32-block, c/moe_quant.h:48-82; its LAG_IDOT=1, c/laguna.c:204-207).
+static int g_q4_mode = 0;
+extern "C" int lag_hip_set_q4_mode(int mode) {
+    if (mode < 0 || mode > 1) return -1;
+    const int prev = g_q4_mode;
+    g_q4_mode = mode;
+    return prev;
+}
+
 // the int4 expert pipeline over device groups:
 //   h <- silu_glu(gate_up . x);  slots <- down . h
 // (limbs_ready: xl/xs already hold the limbs of dx)
@@ -446,6 +457,8 @@ struct FwdScratch {
     float *xs;
     uint32_t *xd, *hd;      // MFMA digits of x [S][D/32] and of h [T][I/32] (prefill)
     float *xds, *hds;
+    uint32_t *xq, *hq;      // IDOT int8 activations of x [S][D/32][8] and of h [T][I/32][8]
+    float *xqs, *hqs, *hf;  // their block scales; h [T][I] f32
 };
 static int g_last_G_dev = 0;            // 1: last forward's groups live in the arena
 static FwdScratch g_last;
@@ -461,7 +474,7 @@ static int desc_ok(const LagHipMoeDesc *d, const LagHipMoeWeights *w) {
     return 1;
 }
 
-static int carve_fwd(const LagHipMoeDesc *d, int S, FwdScratch &f) {
+static int carve_fwd(const LagHipMoeDesc *d, int S, FwdScratch &f, bool idot = false) {
     const int E = d->n_experts, K = d->topk, D = d->hidden, I = d->moe_inter, Is = d->shared_inter;
     const int T = S * K;
     Carve cv;
@@ -471,7 +484,7 @@ static int carve_fwd(const LagHipMoeDesc *d, int S, FwdScratch &f) {
     const size_t o_G = cv.take(4), o_grow = cv.take((size_t)T * 4), o_rowof = cv.take((size_t)T * 4);
     const size_t o_items = cv.take((size_t)sw_npass_max(T, E, SW_DG_TT) * 4), o_P = cv.take(4);
     const size_t o_hl = cv.take((size_t)T * (I / 32) * SW_NL * 16), o_hs = cv.take((size_t)T * (I / 32) * 4);
-    const size_t o_slot = cv.take(S > 1 ? (size_t)T * D * 4 : 4);
+    const size_t o_slot = cv.take(S > 1 || idot ? (size_t)T * D * 4 : 4);
     size_t o_sh = 0, o_so = 0;
     if (d->shared_mode) { o_sh = cv.take((size_t)S * Is * 4); o_so = cv.take((size_t)S * D * 4); }
     const size_t o_xl = cv.take((size_t)S * (D / 32) * SW_NL * 16), o_xs = cv.take((size_t)S * (D / 32) * 4);
@@ -480,8 +493,17 @@ static int carve_fwd(const LagHipMoeDesc *d, int S, FwdScratch &f) {
         o_xd = cv.take((size_t)S * (D / 32) * 128); o_xds = cv.take((size_t)S * (D / 32) * 4);
         o_hd = cv.take((size_t)T * (I / 32) * 128); o_hds = cv.take((size_t)T * (I / 32) * 4);
     }
+    size_t o_xq = 0, o_xqs = 0, o_hq = 0, o_hqs = 0, o_hf = 0;
+    if (idot) {
+        o_xq = cv.take((size_t)S * (D / 32) * 32); o_xqs = cv.take((size_t)S * (D / 32) * 4);
+        o_hq = cv.take((size_t)T * (I / 32) * 32); o_hqs = cv.take((size_t)T * (I / 32) * 4);
+        o_hf = cv.take((size_t)T * I * 4);
+    }
     if (grow_dev(g_arena, cv.off)) return -1;
     char *A = (char *)g_arena.p;
+    f.xq = idot ? (uint32_t *)(A + o_xq) : nullptr; f.xqs = idot ? (float *)(A + o_xqs) : nullptr;
+    f.hq = idot ? (uint32_t *)(A + o_hq) : nullptr; f.hqs = idot ? (float *)(A + o_hqs) : nullptr;
+    f.hf = idot ? (float *)(A + o_hf) : nullptr;
     f.logits = (float *)(A + o_lg); f.scores = (float *)(A + o_sc); f.sel = (int *)(A + o_sel); f.w = (float *)(A + o_w);
     f.gexp = (int *)(A + o_gexp); f.gbeg = (int *)(A + o_gbeg); f.gcnt = (int *)(A + o_gcnt); f.G = (int *)(A + o_G);
     f.items = (int *)(A + o_items); f.P = (int *)(A + o_P);
@@ -514,6 +536,49 @@ extern "C" int lag_hip_route(const LagHipMoeDesc *d, const LagHipMoeWeights *w, 
     return route_dev(d, w, x, S, logits ? logits : f.logits, f.scores, sel, wts);
 }
 
+// The layer in the IDOT contract (any S): router, gate + top-k, the counting sort, int8
+// activations, grouped gate_up GLU, int8 h, grouped down into slots, combine; the
+// shared expert as in batches (the same arithmetic as the decode stages).
+static int forward_idot(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const float *x, float *out, int S) {
+    const int E = d->n_experts, K = d->topk, D = d->hidden, I = d->moe_inter, Is = d->shared_inter;
+    FwdScratch f;
+    if (carve_fwd(d, S, f, true) || ensure_consts(K)) return -1;
+    SwQ4 gu = {(const uint8_t *)w->gu_q, w->gu_s, 2 * I, D, 0, E};
+    SwQ4 dn = {(const uint8_t *)w->dn_q, w->dn_s, D, I, 0, E};
+    const bool sh = d->shared_mode != 0;
+    { PROF("stage_route");
+      if (sw_launch_stage_route(g_st, w->router, d->router_bf16, x, S, D, E, w->logit_bias, f.logits, f.scores, d->route_act,
+                                nullptr, f.xs, nullptr, nullptr, Is, f.shh)) return fail_msg("routing stage launch"); }
+    if (sh) {
+        PROF("shared_glu");
+        if (sw_launch_sh_glu(g_st, (const uint16_t *)w->sg, (const uint16_t *)w->su, x, S, D, Is, f.shh))
+            return fail_msg("shared gate_up launch");
+    }
+    { PROF("gate_topk");
+      if (sw_launch_gate_topk(g_st, f.logits, f.scores, S, E, K, d->route_act, w->corr_bias, d->use_corr_bias, d->norm_topk,
+                              f.sel, f.w)) return fail_msg("gate/top-k launch"); }
+    { PROF("bucket");
+      if (sw_launch_bucket(g_st, f.sel, S, K, E, f.gexp, f.gbeg, f.gcnt, f.G, f.grow, f.rowof, 1, nullptr, nullptr))
+          return fail_msg("bucket launch"); }
+    const SwGroups g = {f.gexp, f.gbeg, f.gcnt, f.grow, f.G, S * K < E ? S * K : E, 0, nullptr, nullptr};
+    SwGroups gd = g;
+    gd.grow = nullptr;                     // the down reads the packed rows directly
+    { PROF("idot_quant"); if (sw_launch_idot_quant(g_st, x, S, D, f.xq, f.xqs)) return fail_msg("IDOT quant launch"); }
+    { PROF("idot_glu"); if (sw_launch_idot_glu(g_st, gu, f.xq, f.xqs, g, I, f.hf)) return fail_msg("IDOT gate_up launch"); }
+    if (sh) {
+        PROF("shared_down");
+        if (sw_launch_sh_down(g_st, (const uint16_t *)w->sd, f.shh, S, Is, D, f.sout)) return fail_msg("shared down launch");
+    }
+    { PROF("idot_quant"); if (sw_launch_idot_quant(g_st, f.hf, S * K, I, f.hq, f.hqs)) return fail_msg("IDOT quant launch"); }
+    { PROF("idot_down"); if (sw_launch_idot_rows(g_st, dn, f.hq, f.hqs, gd, f.slots)) return fail_msg("IDOT down launch"); }
+    { PROF("combine");
+      if (sw_launch_combine(g_st, f.slots, f.rowof, f.w, S, K, D, d->route_scale, f.sout, out, 1))
+          return fail_msg("combine launch"); }
+    g_last_G_dev = 1; g_last_ng = 0;
+    g_last = f;
+    return 0;
+}
+
 // One decode step (sabrewing's moe_block over S tokens, device pointers).
 // S == 1, three launches:
 //   stage 1  router logits / scores / limbs of x + the shared expert's gate_up
@@ -527,6 +592,7 @@ extern "C" int lag_hip_route(const LagHipMoeDesc *d, const LagHipMoeWeights *w, 
 extern "C" int lag_hip_moe_forward(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const float *x, float *out, int S) {
     if (!g_ok || fault_injected()) return -1;
     if (!desc_ok(d, w) || S <= 0) return fail_msg("moe_forward: unsupported descriptor/shape");
+    if (g_q4_mode == 1 && d->gs == 0) return forward_idot(d, w, x, out, S);
     const int E = d->n_experts, K = d->topk, D = d->hidden, I = d->moe_inter, Is = d->shared_inter;
     const int T = S * K;
     FwdScratch f;

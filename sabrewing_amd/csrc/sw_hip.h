@@ -253,6 +253,11 @@ int sw_launch_digits(hipStream_t st, const float *x, int rows, int K, uint32_t *
 int sw_launch_mf_glu(hipStream_t st, SwQ4 W, const uint32_t *dg, const float *xs, SwGroups g, int I, uint32_t *hdg,
                      float *hxs);
 int sw_launch_mf_rows(hipStream_t st, SwQ4 W, const uint32_t *dg, const float *xs, SwGroups g, float *Y);
+// the reference's IDOT int4 contract (k_idot.hip, per-row scales): int8 activations
+// per 32-block xi[rows][K/32][8 dwords] + xs[rows][K/32], then grouped rows (whole groups)
+int sw_launch_idot_quant(hipStream_t st, const float *x, int rows, int K, uint32_t *xi, float *xs);
+int sw_launch_idot_glu(hipStream_t st, SwQ4 W, const uint32_t *xi, const float *xs, SwGroups g, int I, float *h);
+int sw_launch_idot_rows(hipStream_t st, SwQ4 W, const uint32_t *xi, const float *xs, SwGroups g, float *Y);
 int sw_launch_rmsnorm(hipStream_t st, const float *x, const float *w, float *out, int S, int D, float eps);
 int sw_launch_argmax(hipStream_t st, const float *logits, int S, int V, int *tok);
 // the shared expert of a batch over token tiles (k_shared.hip): h = silu(Wg x) * (Wu x); out = Wd h

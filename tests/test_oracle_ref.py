@@ -108,6 +108,41 @@ def test_laguna_engine_path(orc):
         assert bits_equal(orc.moe_block_rows(d, L, x, h0, mode), lag.moe_rows(d, L, x, h0, exact=1, group=0))
 
 
+_IDOT_CHILD = r"""
+import sys
+import numpy as np
+from dataclasses import replace
+from oracle import synth
+from oracle.oracle import Oracle, RefLaguna
+from sabrewing_amd import configs as cf
+orc, lag = Oracle(), RefLaguna()
+cfg = replace(cf.scaled(cf.C2_SIGMOID, D=256, E=32, K=6, I=128, Is=128), gs=0, router_bf16=False)
+L = synth.make_layer(orc, cfg, 17, corr_bias_sigma=0.01)
+d = synth.desc_of(cfg)
+x, h0 = synth.make_x(orc, cfg, 18, 5), synth.make_x(orc, cfg, 19, 5)
+a = orc.moe_block_rows(d, L, x, h0, 1).view(np.uint32)
+b = lag.moe_rows(d, L, x, h0, group=0).view(np.uint32)
+c = lag.moe_rows(d, L, x, h0, group=1).view(np.uint32)
+f = orc.moe_block_rows(d, L, x, h0, 0).view(np.uint32)
+print("IDOT-OK" if np.array_equal(a, b) and np.array_equal(a, c) and not np.array_equal(a, f) else "IDOT-MISMATCH")
+"""
+
+
+def test_laguna_engine_idot():
+    """the oracle's IDOT layer (mode 1) against the reference engine's CPU tier under
+    LAG_IDOT=1 (c/laguna.c:204-207, read once per process: a child process), per-token
+    and grouped (c/laguna.c:739), bit for bit; the f32 contract differs"""
+    import os
+    import subprocess
+    import sys
+    if not RefLaguna.available():
+        pytest.skip("compiled reference engine not built")
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ, LAG_IDOT="1", PYTHONPATH=root)
+    r = subprocess.run([sys.executable, "-c", _IDOT_CHILD], env=env, cwd=root, capture_output=True, text=True, timeout=300)
+    assert "IDOT-OK" in r.stdout, r.stdout + r.stderr
+
+
 def _logit_sets(rng, E):
     """random rows, rows with exact ties, a NaN row, -inf entries, huge logits"""
     rows = [(rng.standard_normal(E) * s).astype(np.float32) for s in (0.5, 3.0, 30.0)]
