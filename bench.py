@@ -104,6 +104,67 @@ def cpu_baseline(be, cfg, dl, xs, seconds):
                       f"{isa} build, {dt:.1f} s"}
 
 
+def per_row_modes(be, cfg, dl, xs, seconds, steps):
+    """Side figures for the per-row-scale (gs = 0) contracts: the reference CPU moe_block
+    in its F32 and IDOT activation modes (c/moe_quant.h:45-125; LAG_IDOT), and the device
+    layer at B = 1 in its default and IDOT modes, on one per-row-quantised copy of the
+    workload's layer (generated on the device)."""
+    from dataclasses import replace
+    from oracle.oracle import Ref
+    from oracle import synth as osyn
+    isa = "avx512" if "avx512f" in open("/proc/cpuinfo").read() else "avx2"
+    if not Ref.available(isa):
+        return None
+    from sabrewing_amd.backend import DeviceLayer
+    c0 = replace(cfg, gs=0, name=cfg.name + "-gs0")
+    seed0 = dl.seed + 7
+    d0 = DeviceLayer.generate(be, c0, seed0)
+    ref = Ref(isa)
+    ref.lib.ref_omp_autotune()
+    D, I, E = c0.D, c0.I, c0.E
+    get = lambda b, shape, dt: be.d2h(b, shape, dt)
+    from sabrewing_amd import synth as S
+    from oracle.oracle import Oracle
+    r = Oracle().normal(E * D, S.tensor_seed(seed0, 0, S.T_ROUTER), 0.02).reshape(E, D)
+    L = osyn.Layer(D, I, c0.Is, E, 0, c0.router_bf16, Oracle().to_bf16(r) if c0.router_bf16 else r,
+                   np.zeros(E, np.float32) if c0.use_corr_bias else None, None,
+                   get(d0.gu_q, E * 2 * I * D // 2, np.uint8), get(d0.gu_s, E * 2 * I, np.float32),
+                   get(d0.dn_q, E * D * I // 2, np.uint8), get(d0.dn_s, E * D, np.float32),
+                   get(d0.sg, (c0.Is, D), np.uint16) if c0.shared_mode else None,
+                   get(d0.su, (c0.Is, D), np.uint16) if c0.shared_mode else None,
+                   get(d0.sd, (D, c0.Is), np.uint16) if c0.shared_mode else None)
+    d = osyn.desc_of(replace(c0, route_act=0) if c0.route_act == 2 else c0)
+    out = {}
+    o = np.zeros((1, D), np.float32)
+    for name, mode in (("cpu_f32", 0), ("cpu_idot", 1)):
+        ref.moe_block_rows(d, L, xs[0:1], o, mode)
+        n, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < seconds and n < 100000:
+            ref.moe_block_rows(d, L, xs[n % len(xs):n % len(xs) + 1], o, mode)
+            n += 1
+        out[name] = round(n / (time.perf_counter() - t0), 1)
+    xb, ob = be.upload(xs[:1]), be.alloc(D * 4)
+    for name, mode in (("device", be.Q4_DOT8), ("device_idot", be.Q4_IDOT)):
+        prev = be.set_q4_mode(mode)
+        try:
+            for _ in range(10):
+                be.moe_forward(d0.desc(), d0.weights(), xb, ob, 1)
+            be.sync()
+            e0, e1 = be.event(), be.event()
+            be.record(e0)
+            for _ in range(steps):
+                be.moe_forward(d0.desc(), d0.weights(), xb, ob, 1)
+            be.record(e1)
+            be.sync()
+            out[name] = round(steps / (be.elapsed_ms(e0, e1) * 1e-3), 1)
+        finally:
+            be.set_q4_mode(prev)
+    xb.free(); ob.free(); d0.free()
+    out["unit"] = "tokens/s (B=1, eager)"
+    out["sample"] = f"{c0.name}: per-row int4, {isa} reference with one thread per physical core, ~{seconds:.0f} s per CPU mode"
+    return out
+
+
 def run_stack(args):
     """--config C5-stack: the Config-5 decode step -- 48 resident MoE layers
     (D=4096, E=256, top-8 softmax, I=1536, no shared expert), h += MoE(rmsnorm(h))
@@ -284,6 +345,7 @@ def run(args):
     log(f"host-buffer entry (PCIe-inclusive, synchronous): {pcie_ms * 1e3:.1f} us/step, {B / (pcie_ms * 1e-3):.0f} tokens/s")
 
     cpu = None
+    modes = None
     if not args.no_cpu:
         rng_x = gen_x(be, cfg, args.seed + 1, 64)
         xs = be.d2h(rng_x, (64, cfg.D), np.float32)
@@ -292,6 +354,12 @@ def run(args):
             cpu = cpu_baseline(be, cfg, layers[0], xs, args.cpu_seconds)
         except Exception as e:                      # the baseline is reported, never required
             log("cpu baseline failed:", repr(e))
+        if B == 1 and cfg.gs > 0:
+            try:
+                modes = per_row_modes(be, cfg, layers[0], xs, args.cpu_seconds / 3, args.steps)
+                log("per-row (gs=0) contracts:", json.dumps(modes))
+            except Exception as e:
+                log("per-row modes failed:", repr(e))
 
     res = {
         "metric": "MoE-layer tokens/s + % peak HBM GB/s, int4 experts, batch 1 and batch 32",
@@ -309,6 +377,7 @@ def run(args):
                    "layer_hbm_frac": round(layer_gbs / HBM_PEAK_GBS, 4)},
         "roofline": roof,
         "cpu_baseline": cpu,
+        "per_row_modes": modes,
         "kernels": {k: {kk: (round(vv, 2) if isinstance(vv, float) else vv) for kk, vv in v.items()} for k, v in kern.items()},
     }
     print(json.dumps(res), flush=True)
