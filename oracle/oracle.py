@@ -72,6 +72,8 @@ class Oracle:
         L.sw_moe_block_rows.argtypes = [C.POINTER(SwMoeDesc), C.POINTER(SwMoeLayer), F32P, F32P, C.c_int, C.c_int]
         L.sw_route_logits.argtypes = [C.POINTER(SwMoeDesc), F32P, C.c_int, I32P, F32P]
         L.sw_moe_group_rows.argtypes = [C.POINTER(SwMoeDesc), C.POINTER(SwMoeLayer), F32P, F32P, C.c_int, C.c_int]
+        L.sw_glm_logits.argtypes = [F32P, F32P, F32P, C.c_int, C.c_int, F32P, F32P]
+        L.sw_glm_matmul.argtypes = [F32P, F32P, F32P] + [C.c_int] * 3
         L.sw_bucket.restype = C.c_int
         L.sw_bucket.argtypes = [I32P, C.c_int, C.c_int, C.c_int, I32P, I32P, I32P, I32P, I32P]
 
@@ -181,6 +183,73 @@ class Oracle:
         self.lib.sw_route_logits(C.byref(d), np.ascontiguousarray(logits, np.float32), S, sel, w)
         return sel, w
 
+    # ---- the GLM engine's routing (c/colibri.c:2871-2999, plain path) ----
+    def glm_matmul(self, x, W):
+        """c/quant.h:98-102 as GCC -O3 builds it for AVX-512: inputs ascending, rounded products
+        added in order, the last I % 8 as an fma chain"""
+        x = np.ascontiguousarray(x, np.float32); W = np.ascontiguousarray(W, np.float32)
+        y = np.empty((x.shape[0], W.shape[0]), np.float32)
+        self.lib.sw_glm_matmul(y, x, W, x.shape[0], x.shape[1], W.shape[0])
+        return y
+
+    def glm_logits(self, x, W, bias):
+        """(logit, choice) of one row: sigmoidf of the chain (c/colibri.c:833, 2873), + bias"""
+        E, D = W.shape
+        lg = np.empty(E, np.float32); ch = np.empty(E, np.float32)
+        self.lib.sw_glm_logits(np.ascontiguousarray(x, np.float32), np.ascontiguousarray(W, np.float32),
+                               np.ascontiguousarray(bias, np.float32), D, E, lg, ch)
+        return lg, ch
+
+    @staticmethod
+    def glm_select(logit, choice, Ksel, topp=0.0, norm_topk=1, routed_scale=1.0):
+        """(idx[Ksel], w[Ksel], keff): Ksel passes of the first strict maximum of choice over the
+        experts not yet taken (from -1e30, so NaN and <= -1e30 never win; none: kk < E ? kk : 0,
+        c/colibri.c:2776-2782, 2955-2961); with 0 < topp < 1 the stable descending insertion sort
+        and the cumulative cut (:2979-2984); norm_topk (:2997) and routed_scale (:2998) over the
+        kept ones.  Every operation in float32, in the reference's order."""
+        f = np.float32
+        E = len(choice)
+        idx, w, taken = [], [], set()
+        for kk in range(Ksel):
+            best, bv = -1, f(-1e30)
+            for e in range(E):
+                if e not in taken and choice[e] > bv:
+                    bv, best = choice[e], e
+            if best < 0:
+                best = kk if kk < E else 0
+            idx.append(best); w.append(f(logit[best])); taken.add(best)
+        Ke = Ksel
+        topp = f(topp)
+        if f(0) < topp < f(1):
+            for a in range(1, Ksel):
+                ii, ww, b = idx[a], w[a], a - 1
+                while b >= 0 and w[b] < ww:
+                    w[b + 1] = w[b]; idx[b + 1] = idx[b]; b -= 1
+                w[b + 1] = ww; idx[b + 1] = ii
+            tot = f(1e-20)
+            for v in w:
+                tot = f(tot + v)
+            cum = f(0)
+            for kk in range(Ksel):
+                cum = f(cum + w[kk])
+                if cum >= f(topp * tot):
+                    Ke = kk + 1
+                    break
+        if norm_topk:
+            sm = f(0)
+            for kk in range(Ke):
+                sm = f(sm + w[kk])
+            sm = f(sm + f(1e-20))
+            for kk in range(Ke):
+                w[kk] = f(w[kk] / sm)
+        for kk in range(Ke):
+            w[kk] = f(w[kk] * f(routed_scale))
+        return np.array(idx, np.int32), np.array(w, np.float32), Ke
+
+    def glm_route(self, x, W, bias, Ksel, topp=0.0, norm_topk=1, routed_scale=1.0):
+        lg, ch = self.glm_logits(x, W, bias)
+        return self.glm_select(lg, ch, Ksel, topp, norm_topk, routed_scale)
+
     def expf(self, x):
         x = np.ascontiguousarray(x, np.float32); y = np.empty_like(x)
         self.lib.sw_expf_array(y, x, x.size)
@@ -238,6 +307,24 @@ class Oracle:
         out = np.ascontiguousarray(out, np.float32).copy()
         self.lib.sw_moe_group_rows(C.byref(d), C.byref(L), np.ascontiguousarray(x, np.float32), out, x.shape[0], mode)
         return out
+
+
+class RefGlm:
+    """The GLM engine's router GEMV (c/quant.h matmul), compiled from the reference."""
+
+    def __init__(self):
+        self.lib = C.CDLL(os.path.join(HERE, "_ref", "libref_glm_avx512.so"))
+        self.lib.ref_glm_matmul.argtypes = [F32P, F32P, F32P] + [C.c_int] * 3
+
+    @staticmethod
+    def available():
+        return os.path.exists(os.path.join(HERE, "_ref", "libref_glm_avx512.so"))
+
+    def matmul(self, x, W):
+        x = np.ascontiguousarray(x, np.float32); W = np.ascontiguousarray(W, np.float32)
+        y = np.empty((x.shape[0], W.shape[0]), np.float32)
+        self.lib.ref_glm_matmul(y, x, W, x.shape[0], x.shape[1], W.shape[0])
+        return y
 
 
 class Ref:

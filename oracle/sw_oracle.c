@@ -182,6 +182,32 @@ static float hsum8(const float *v) {            /* hsum256, c/quant.h:20-24 */
 
 /* ======================= GEMV / GEMM contracts ======================= */
 
+/* GLM router (c/colibri.c:2871-2874): logits by c/quant.h:98-102's f32 matmul,
+ * `a += xs[i] * w[i]` for i ascending.  As GCC -O3 builds it for AVX-512 the
+ * products of the first I - I % 8 inputs are vectorised (16 and 8 wide) and
+ * rounded, then added in order; the last I % 8 are a scalar fma chain.  The
+ * sum order is the source's either way.  Then sigmoidf (c/colibri.c:833) with
+ * glibc expf and the selection score logit + bias. */
+static float glm_dot(const float *x, const float *w, int I) {
+    const int nv = I - I % 8;
+    float a = 0.f;
+    for (int i = 0; i < nv; i++) { const float p = x[i] * w[i]; a = a + p; }
+    for (int i = nv; i < I; i++) a = fmaf(x[i], w[i], a);
+    return a;
+}
+void sw_glm_logits(const float *x, const float *W, const float *bias, int D, int E, float *logit, float *choice) {
+    for (int e = 0; e < E; e++) {
+        const float lg = 1.f / (1.f + expf(-glm_dot(x, W + (int64_t)e * D, D)));
+        logit[e] = lg;
+        choice[e] = lg + bias[e];
+    }
+}
+/* the dot alone (to compare with the compiled c/quant.h matmul) */
+void sw_glm_matmul(float *y, const float *x, const float *W, int S, int I, int O) {
+    for (int o = 0; o < O; o++)
+        for (int s = 0; s < S; s++) y[(int64_t)s * O + o] = glm_dot(x + (int64_t)s * I, W + (int64_t)o * I, I);
+}
+
 /* c/moe_matmul.h:25-55.  SIMD: lane j sums i = j mod 16 ascending with FMA,
  * reduce16, then the scalar tail fused into the sum.  exact: double sum. */
 void sw_matmul_f32(float *y, const float *x, const float *W, int S, int I, int O, int exact) {

@@ -52,6 +52,8 @@ void sw_gen_q4(uint8_t *packed, float *scale, uint64_t seed, double sigma,
 
 /* ---------------- kernels (reference contracts) ---------------- */
 void sw_matmul_f32(float *y, const float *x, const float *W, int S, int I, int O, int exact);
+void sw_glm_logits(const float *x, const float *W, const float *bias, int D, int E, float *logit, float *choice);
+void sw_glm_matmul(float *y, const float *x, const float *W, int S, int I, int O);
 void sw_matmul_bf16(float *y, const float *x, const uint16_t *W, int S, int I, int O, int exact);
 enum { SW_Q4_F32 = 0, SW_Q4_IDOT = 1 };
 void sw_matmul_q4(float *y, const float *x, const uint8_t *packed, const float *scale,

@@ -162,6 +162,7 @@ struct Dot8GluArgs {
     float *hs;
     int *sel;
     DotRoute rt;
+    const SwTab *tab;          // per-group tensors (the _tab launch) or null
 };
 
 // K inputs as G = K/32 groups, G <= 256
@@ -174,8 +175,9 @@ static int dg_pf_rows(int K) { const int n = 64 / dg_rps(run_lanes(K / RG), 64, 
 
 // block (bx = group or rank, by = set of RO outputs: 32, or up to 128 for groups --
 // fewer, longer blocks per weight byte); runs: the dynamic LDS, [TT][2 RO][NC] floats
-template <int PF, int PICK, int NP, int TT, int C16, int RO>
+template <int PF, int PICK, int NP, int TT, int C16, int RO, int PT = 0>
 __device__ __forceinline__ void dot8_glu_block(const Dot8GluArgs &A, int bx, int by, float *runs) {
+    static_assert(PT == 0 || PICK == 0, "per-group tensors come with groups");
     static_assert(PICK == 0 || TT == 1, "picks are of one token");
     static_assert(RO == 32 || RO == 64 || RO == 128, "1, 2 or 4 limb groups of h per block");
     const SwQ4 W = A.W;
@@ -223,12 +225,28 @@ __device__ __forceinline__ void dot8_glu_block(const Dot8GluArgs &A, int bx, int
     } else {
         if (!grp_work(grp, bx, TT, e, beg, tb, tend)) return;
     }
-    const sw_rsrc rq = sw_q4_rq(W), rs = sw_q4_rs(W);
+    // gate rows through (rq, rs), up rows through (rq2, rs2): one [E*2I] tensor, or the
+    // group's own gate and up tensors (PT)
+    sw_rsrc rq, rs, rq2, rs2;
+    uint32_t erow;
+    if constexpr (PT) {
+        const SwTab tb_ = A.tab[e];
+        rq = sw_make_rsrc(tb_.g, (uint32_t)I * rb);
+        rq2 = sw_make_rsrc(tb_.u, (uint32_t)I * rb);
+        rs = sw_make_rsrc(tb_.gs, (uint32_t)I * sb);
+        rs2 = sw_make_rsrc(tb_.us, (uint32_t)I * sb);
+        erow = (uint32_t)i0;
+    } else {
+        rq = rq2 = sw_q4_rq(W);
+        rs = rs2 = sw_q4_rs(W);
+        erow = (uint32_t)e * (uint32_t)(2 * I) + (uint32_t)i0;
+    }
     // lane offsets (this thread's first row of a half) and the scalar offset of step s
     const uint32_t voq = (uint32_t)(roc * NSH) * rb + (uint32_t)g * 16;
     const uint32_t vos = (uint32_t)(roc * NSH) * sb + (uint32_t)sg * 4;
-    const uint32_t erow = (uint32_t)e * (uint32_t)(2 * I) + (uint32_t)i0;
-    auto srow = [&](int s) -> uint32_t { return s < NSH ? erow + s : erow + I + (s - NSH); };
+    auto srow = [&](int s) -> uint32_t { return s < NSH ? erow + s : erow + (PT ? 0 : I) + (s - NSH); };
+    auto wq = [&](int s) -> const sw_rsrc & { return s < NSH ? rq : rq2; };
+    auto ws = [&](int s) -> const sw_rsrc & { return s < NSH ? rs : rs2; };
     const int NS = 2 * NSH;
     float *myruns = runs + (roc * NSH) * NC + c;      // this lane's run sum of step s: myruns[(t*64 + h*32 + j) * NC]
     for (int t0 = tb; t0 < tend; t0 += TT) {
@@ -247,15 +265,15 @@ __device__ __forceinline__ void dot8_glu_block(const Dot8GluArgs &A, int bx, int
         float sa[PF];
 #pragma unroll
         for (int u = 0; u < PF; u++) {
-            ra[u] = sw_ld16(rq, voq, srow(u) * rb);
-            sa[u] = sw_ld4f(rs, vos, srow(u) * sb);
+            ra[u] = sw_ld16(wq(u), voq, srow(u) * rb);
+            sa[u] = sw_ld4f(ws(u), vos, srow(u) * sb);
         }
         auto step = [&](int s, int u, bool refill) {
             const sw_u32x4 w = ra[u] ^ 0x88888888u;
             const float sc = W.gs > 0 ? sa[u] : 1.0f;
             if (refill) {
-                ra[u] = sw_ld16(rq, voq, srow(s + PF) * rb);
-                sa[u] = sw_ld4f(rs, vos, srow(s + PF) * sb);
+                ra[u] = sw_ld16(wq(s + PF), voq, srow(s + PF) * rb);
+                sa[u] = sw_ld4f(ws(s + PF), vos, srow(s + PF) * sb);
                 __builtin_amdgcn_sched_barrier(0);
             }
             const int urow = s < NSH ? s : RO + s - NSH;                 // local row minus roc * NSH
@@ -284,8 +302,13 @@ __device__ __forceinline__ void dot8_glu_block(const Dot8GluArgs &A, int bx, int
             float yg = rg[0], yu = ru[0];
             for (int cc = 1; cc < NC; cc++) { yg = yg + rg[cc]; yu = yu + ru[cc]; }
             if (W.gs <= 0) {                            // per-row scales after the sum
-                yg = yg * W.s[(int64_t)e * (2 * I) + i0 + i];
-                yu = yu * W.s[(int64_t)e * (2 * I) + I + i0 + i];
+                if constexpr (PT) {
+                    yg = yg * A.tab[e].gs[i0 + i];
+                    yu = yu * A.tab[e].us[i0 + i];
+                } else {
+                    yg = yg * W.s[(int64_t)e * (2 * I) + i0 + i];
+                    yu = yu * W.s[(int64_t)e * (2 * I) + I + i0 + i];
+                }
             }
             const float h = (yg / (1.0f + expf(-yg))) * yu;
             // every 32 of the block's outputs are one limb group of the down projection's input
@@ -373,8 +396,9 @@ struct Dot8RowsArgs {
     const float *xs;
     SwGroups grp;
     float *Y;
+    const SwTab *tab;          // per-group tensors (the _tab launch) or null
 };
-template <int PF, int TT, int C16, int RB>
+template <int PF, int TT, int C16, int RB, int PT = 0>
 __device__ __forceinline__ void dot8_rows_block(const Dot8RowsArgs &A, int bx, int by, float *runs) {
     const SwQ4 W = A.W;
     const sw_u32x4 *__restrict__ xl = A.xl;
@@ -395,11 +419,18 @@ __device__ __forceinline__ void dot8_rows_block(const Dot8RowsArgs &A, int bx, i
     const int ng = W.gs > 0 ? K / W.gs : 1;
     const int sg = W.gs > 0 ? (g * RG) >> A.gsh : 0;
     const uint32_t rb = (uint32_t)K / 2, sb = (uint32_t)ng * 4;
-    const sw_rsrc rq = sw_q4_rq(W), rs = sw_q4_rs(W);
+    sw_rsrc rq, rs;
+    if constexpr (PT) {                                  // the group's own down tensor
+        rq = sw_make_rsrc(A.tab[e].d, (uint32_t)O * rb);
+        rs = sw_make_rsrc(A.tab[e].ds, (uint32_t)O * sb);
+    } else {
+        rq = sw_q4_rq(W);
+        rs = sw_q4_rs(W);
+    }
     // rows past O read the next expert's rows (or zeros past the tensor) and are not stored
     const uint32_t voq = (uint32_t)(roc * NS) * rb + (uint32_t)g * 16;
     const uint32_t vos = (uint32_t)(roc * NS) * sb + (uint32_t)sg * 4;
-    const uint32_t erow = (uint32_t)e * (uint32_t)O + (uint32_t)r0;
+    const uint32_t erow = (PT ? 0u : (uint32_t)e * (uint32_t)O) + (uint32_t)r0;
     float *myruns = runs + (roc * NS) * NC + c;
     for (int t0 = tb; t0 < tend; t0 += TT) {
         const int nt = min(TT, tend - t0);
@@ -450,7 +481,7 @@ __device__ __forceinline__ void dot8_rows_block(const Dot8RowsArgs &A, int bx, i
                 const float *rr = runs + it * NC;
                 float y = rr[0];
                 for (int cc = 1; cc < NC; cc++) y = y + rr[cc];
-                if (W.gs <= 0) y = y * W.s[(int64_t)e * O + r0 + r];
+                if (W.gs <= 0) y = y * (PT ? A.tab[e].ds[r0 + r] : W.s[(int64_t)e * O + r0 + r]);
                 Y[(int64_t)(beg + t0 + t) * O + r0 + r] = y;
             }
         }
@@ -492,6 +523,69 @@ int sw_launch_q4_dot8_rows(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, const flo
     const size_t lds = (size_t)DG_TT * RB * dot8_nc(W.K) * 4;
     if (RB == 128) dispatch_pf_c16<RowsL<128>::L>(pf, dot8_c16(W.K), grid, lds, st, A);
     else dispatch_pf_c16<RowsL<64>::L>(pf, dot8_c16(W.K), grid, lds, st, A);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+// ------------------------------------------------ per-group tensors (coli table) ----
+// The two grouped kernels with group c's gate/up/down read from tab[gexp[c]]: the
+// same blocks, steps and fixed-order sums, so a group's outputs are bit-identical to
+// the same expert's outputs from the one-tensor launches above.
+template <int PF, int C16, int RO>
+__global__ __launch_bounds__(DG_NT) void k_dot8_glu_tab(Dot8GluArgs A) {
+    extern __shared__ __align__(16) float red[];
+    dot8_glu_block<PF, 0, 0, DG_TT, C16, RO, 1>(A, blockIdx.x, blockIdx.y, red);
+}
+template <int RO>
+struct GluTabL {
+    template <int PF, int C16>
+    struct L {
+        static void go(dim3 grid, size_t lds, hipStream_t st, const Dot8GluArgs &A) {
+            SW_LAUNCH((k_dot8_glu_tab<PF, C16, RO>), grid, dim3(DG_NT), lds, st, A);
+        }
+    };
+};
+int sw_launch_q4_dot8_glu_tab(hipStream_t st, SwQ4 W, const SwTab *tab, const sw_u32x4 *xl, const float *xs, SwGroups g,
+                              int I, sw_u32x4 *hl, float *hs) {
+    int gsh;
+    W.E = 1;                                              // each tensor holds one expert
+    if (!tab || dot8_glu_check(W, I, gsh) || g.ngroups_max <= 0 || g.items) return -1;
+    const Dot8GluArgs A = {W, gsh, xl, xs, g, I, hl, hs, nullptr, DotRoute{}, tab};
+    const int RO = dg_ro(I);
+    const dim3 grid((unsigned)g.ngroups_max, (unsigned)(I / RO));
+    if (RO == 128) dispatch_pf_c16<GluTabL<128>::L>(dg_pf_glu(W.K), dot8_c16(W.K), grid, dot8_glu_lds(W.K, DG_TT, 128), st, A);
+    else if (RO == 64) dispatch_pf_c16<GluTabL<64>::L>(dg_pf_glu(W.K), dot8_c16(W.K), grid, dot8_glu_lds(W.K, DG_TT, 64), st, A);
+    else dispatch_pf_c16<GluTabL<32>::L>(dg_pf_glu(W.K), dot8_c16(W.K), grid, dot8_glu_lds(W.K, DG_TT, 32), st, A);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+template <int PF, int C16, int RB>
+__global__ __launch_bounds__(256, 4) void k_dot8_rows_tab(Dot8RowsArgs A) {
+    extern __shared__ __align__(16) float red[];
+    dot8_rows_block<PF, DG_TT, C16, RB, 1>(A, blockIdx.x, blockIdx.y, red);
+}
+template <int RB>
+struct RowsTabL {
+    template <int PF, int C16>
+    struct L {
+        static void go(dim3 grid, size_t lds, hipStream_t st, const Dot8RowsArgs &A) {
+            SW_LAUNCH((k_dot8_rows_tab<PF, C16, RB>), grid, dim3(256), lds, st, A);
+        }
+    };
+};
+int sw_launch_q4_dot8_rows_tab(hipStream_t st, SwQ4 W, const SwTab *tab, const sw_u32x4 *xl, const float *xs, SwGroups g,
+                               float *Y) {
+    int gsh;
+    W.E = 1;
+    if (!tab || !dot8_shape_ok(W.K) || g.ngroups_max <= 0 || g.items || W.O <= 0 || !sw_q4_extent_ok(W) ||
+        sw_q4_gsh(W, gsh))
+        return -1;
+    const int RB = W.O % 128 == 0 ? 128 : 64;
+    const dim3 grid((unsigned)g.ngroups_max, (unsigned)((W.O + RB - 1) / RB));
+    const Dot8RowsArgs A = {W, gsh, xl, xs, g, Y, tab};
+    const int pf = dg_pf_rows(W.K) < RW_PF ? dg_pf_rows(W.K) : RW_PF;
+    const size_t lds = (size_t)DG_TT * RB * dot8_nc(W.K) * 4;
+    if (RB == 128) dispatch_pf_c16<RowsTabL<128>::L>(pf, dot8_c16(W.K), grid, lds, st, A);
+    else dispatch_pf_c16<RowsTabL<64>::L>(pf, dot8_c16(W.K), grid, lds, st, A);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

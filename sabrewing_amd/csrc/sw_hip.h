@@ -157,6 +157,13 @@ static inline bool sw_q4_extent_ok(const SwQ4 &W) {
     const int ng = W.gs > 0 ? W.K / W.gs : 1;
     return W.E > 0 && (uint64_t)W.E * W.O * (W.K / 2) < (1ull << 32) && (uint64_t)W.E * W.O * ng * 4 < (1ull << 32);
 }
+// One group's expert as three separate int4 tensors (the coli table's gate, up and
+// down ColiCudaTensor, c/backend_cuda.cu:785-943): a group's rows address these
+// instead of expert e of one [E*O] tensor.  Scales are [rows][ng] as in SwQ4.
+struct SwTab {
+    const uint8_t *g, *u, *d;
+    const float *gs, *us, *ds;
+};
 __device__ __forceinline__ sw_rsrc sw_q4_rq(const SwQ4 &W) { return sw_make_rsrc(W.q, (uint32_t)W.E * W.O * (W.K / 2)); }
 __device__ __forceinline__ sw_rsrc sw_q4_rs(const SwQ4 &W) {
     const int ng = W.gs > 0 ? W.K / W.gs : 1;
@@ -218,6 +225,12 @@ int sw_launch_q4_dot8_glu_picks(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, cons
                                 const int *sel, int K);
 // Y[packed row, O] f32 for every group, input as limbs (the grouped down projection)
 int sw_launch_q4_dot8_rows(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, const float *xs, SwGroups g, float *Y);
+// the same two grouped kernels over per-group tensors: W gives O, K and gs (its q, s
+// and E are unused); group c's tensors are tab[gexp[c]]
+int sw_launch_q4_dot8_glu_tab(hipStream_t st, SwQ4 W, const SwTab *tab, const sw_u32x4 *xl, const float *xs, SwGroups g,
+                              int I, sw_u32x4 *hl, float *hs);
+int sw_launch_q4_dot8_rows_tab(hipStream_t st, SwQ4 W, const SwTab *tab, const sw_u32x4 *xl, const float *xs, SwGroups g,
+                               float *Y);
 // the dot8 down projection fused with the rank-order combine for one token
 // (h as limbs of the K packed rows in rank order)
 int sw_launch_q4_dot8_down_combine(hipStream_t st, SwQ4 W, const sw_u32x4 *hl, const float *hs, const int *sel, const float *w,

@@ -18,7 +18,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 def header_functions(path):
     src = open(path).read()
     src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
-    return set(re.findall(r"\b(lag_(?:hip|cuda)_\w+|sabrewing_loader_\w+)\s*\(", src))
+    return set(re.findall(r"\b((?:lag|coli)_(?:hip|cuda)_\w+|sabrewing_loader_\w+)\s*\(", src))
 
 
 def exported(path):
@@ -37,10 +37,24 @@ def test_hip_library_exports_header():
         assert hasattr(lib, name)
 
 
+def test_coli_library_exports_header():
+    """every slot of the coli table (c/backend_cuda.h:28-169) is exported and bound"""
+    from sabrewing_amd.coli import COLI_EXPORTS
+    decl = header_functions(os.path.join(ROOT, "include", "sabrewing_coli.h"))
+    assert decl == set(COLI_EXPORTS) and len(decl) == 46
+    assert not decl - exported(B.LIB_PATH)
+
+
 def test_loader_exports_header():
+    from sabrewing_amd.coli import COLI_EXPORTS
     decl = header_functions(os.path.join(ROOT, "include", "sabrewing_loader.h"))
-    assert decl == set(B.LOADER_EXPORTS)
+    coli = {n.replace("coli_hip_", "coli_cuda_") for n in COLI_EXPORTS}
+    assert decl == set(B.LOADER_EXPORTS) | coli | {"sabrewing_loader_coli_available"}
     assert not decl - exported(B.LOADER_PATH)
+    # the reference's own coli_cuda_* declarations (c/backend_cuda.h) are exactly these
+    ref = "/root/reference/c/backend_cuda.h"
+    if os.path.exists(ref):
+        assert set(re.findall(r"\b(coli_cuda_\w+)\s*\(", open(ref).read())) == coli
 
 
 LOADER_PROBE = textwrap.dedent("""
@@ -49,9 +63,13 @@ LOADER_PROBE = textwrap.dedent("""
     L.lag_cuda_upload.restype = C.c_void_p
     L.sabrewing_loader_path.restype = C.c_char_p
     L.lag_cuda_free_bytes.restype = C.c_size_t
+    L.coli_cuda_expert_group_take.restype = C.c_void_p
+    L.coli_cuda_pipe_alloc.restype = C.c_void_p
     print(L.sabrewing_loader_available(), L.lag_cuda_init(0), L.lag_cuda_upload(None, 16),
           L.lag_cuda_free_bytes(), L.lag_cuda_matmul_q8(None, None, None, 1, 1, 1),
-          L.sabrewing_loader_path().decode())
+          L.sabrewing_loader_path().decode(),
+          L.sabrewing_loader_coli_available(), L.coli_cuda_device_count(), L.coli_cuda_device_at(0),
+          L.coli_cuda_expert_group_take(0), L.coli_cuda_pipe_alloc(0, 16), L.coli_cuda_tensor_device(None))
 """)
 
 
@@ -68,6 +86,8 @@ def test_loader_unavailable_sentinels(tmp_path):
     out, _ = run_probe(str(tmp_path / "absent.so"))
     assert out[:5] == ["0", "-1", "None", "0", "-1"]
     assert out[5] == str(tmp_path / "absent.so")
+    # the coli table's sentinels (c/backend_loader.c:261-512): 0 / -1 / NULL
+    assert out[6:] == ["0", "0", "-1", "None", "None", "-1"]
 
 
 def test_loader_all_or_nothing(tmp_path):
