@@ -80,8 +80,8 @@ class Tensor:
 
 
 class Coli:
-    def __init__(self, devices=(0,)):
-        self.lib = B.load_library()
+    def __init__(self, devices=(0,), path=None):
+        self.lib = B.load_library(path)
         self.f = _Fns(self.lib)
         devs = np.asarray(devices, np.int32)
         if not self.f.init(devs.ctypes.data, len(devs)):

@@ -550,7 +550,8 @@ int sw_launch_q4_dot8_glu_tab(hipStream_t st, SwQ4 W, const SwTab *tab, const sw
     W.E = 1;                                              // each tensor holds one expert
     if (!tab || dot8_glu_check(W, I, gsh) || g.ngroups_max <= 0 || g.items) return -1;
     const Dot8GluArgs A = {W, gsh, xl, xs, g, I, hl, hs, nullptr, DotRoute{}, tab};
-    const int RO = dg_ro(I);
+    // a decode-sized call (few groups) takes 32-output blocks, so the grid still fills the chip
+    const int RO = g.ngroups_max * (I / 128) < 512 ? 32 : dg_ro(I);
     const dim3 grid((unsigned)g.ngroups_max, (unsigned)(I / RO));
     if (RO == 128) dispatch_pf_c16<GluTabL<128>::L>(dg_pf_glu(W.K), dot8_c16(W.K), grid, dot8_glu_lds(W.K, DG_TT, 128), st, A);
     else if (RO == 64) dispatch_pf_c16<GluTabL<64>::L>(dg_pf_glu(W.K), dot8_c16(W.K), grid, dot8_glu_lds(W.K, DG_TT, 64), st, A);
@@ -579,7 +580,7 @@ int sw_launch_q4_dot8_rows_tab(hipStream_t st, SwQ4 W, const SwTab *tab, const s
     if (!tab || !dot8_shape_ok(W.K) || g.ngroups_max <= 0 || g.items || W.O <= 0 || !sw_q4_extent_ok(W) ||
         sw_q4_gsh(W, gsh))
         return -1;
-    const int RB = W.O % 128 == 0 ? 128 : 64;
+    const int RB = W.O % 128 == 0 && g.ngroups_max * (W.O / 128) >= 512 ? 128 : 64;
     const dim3 grid((unsigned)g.ngroups_max, (unsigned)((W.O + RB - 1) / RB));
     const Dot8RowsArgs A = {W, gsh, xl, xs, g, Y, tab};
     const int pf = dg_pf_rows(W.K) < RW_PF ? dg_pf_rows(W.K) : RW_PF;
