@@ -598,7 +598,9 @@ int sw_launch_q4_dot8_rows_tab(hipStream_t st, SwQ4 W, const SwTab *tab, const s
 // fixed-order row sum of the grouped rows kernel (so it is bit-identical to
 // that kernel's slot value) and the ranks are summed in order with one fma
 // each, the operation sequence of k_combine.
-#define DC_RB 8
+#ifndef DC_RB
+#define DC_RB 8            // 4 and 16 measured slower at B=1 (10.2 and 10.9 us against 9.8)
+#endif
 struct Dot8DownArgs {
     SwQ4 W;
     int gsh;
