@@ -151,22 +151,28 @@ int collect(ColiHipTensor *const *gates, ColiHipTensor *const *ups, ColiHipTenso
     return 1;
 }
 
-// device scratch of a group call over T rows: x | gexp gbeg gcnt grow | tab | limbs | h limbs | y
+// device scratch of a group call over T rows: x | gexp gbeg gcnt grow/items | tab |
+// limbs (dot8) or digits (MFMA) of x and of h, with their factors | y
 struct GLay { size_t x, ints, tab, xl, xs, hl, hs, y, end; };
-GLay glay(const Groups &G, int T, int xrows) {
+// (T rows through the projections, xrows rows of x, ints: 3 per group + nextra)
+GLay glay(const Groups &G, int T, int xrows, int nextra = 0, bool mf = false) {
     Carve cv;
     GLay L;
+    const size_t per_group = mf ? (size_t)SW_MF_DIGIT_BYTES : (size_t)SW_NL * 16;
     L.x = cv.take((size_t)xrows * G.D * 4);
-    L.ints = cv.take((size_t)(3 * G.count + T) * 4);
+    L.ints = cv.take((size_t)(3 * G.count + nextra) * 4);
     L.tab = cv.take((size_t)G.count * sizeof(SwTab));
-    L.xl = cv.take((size_t)xrows * (G.D / 32) * SW_NL * 16);
+    L.xl = cv.take((size_t)xrows * (G.D / 32) * per_group);
     L.xs = cv.take((size_t)xrows * (G.D / 32) * 4);
-    L.hl = cv.take((size_t)T * (G.I / 32) * SW_NL * 16);
+    L.hl = cv.take((size_t)T * (G.I / 32) * per_group);
     L.hs = cv.take((size_t)T * (G.I / 32) * 4);
     L.y = cv.take((size_t)T * G.D * 4);
     L.end = cv.off;
     return L;
 }
+// the int8 MFMA GEMMs for prefill-sized groups (16-token tiles mostly full), as
+// the lag family's automatic choice: whole chunks of 4 input groups, >= 8 rows per group
+bool use_mf(const Groups &G) { return G.D % 128 == 0 && G.I % 128 == 0 && G.total >= 8 * G.count; }
 size_t meta_bytes(const Groups &G, int T) { return (size_t)(3 * G.count + T) * 4 + (size_t)G.count * sizeof(SwTab); }
 // the host image of the ints and the table: gexp = 0..count-1 (the table index),
 // gbeg, gcnt, grow (or nothing), then the table
@@ -202,6 +208,23 @@ void count_group(const Groups &G) {
     g_grows += (uint64_t)G.total;
 }
 
+// the MFMA form of the group: digits of x, gate/up + GLU, down, over 64-token tiles
+// (items[j] = (t0 << 10) | group, then their count) listed after gexp gbeg gcnt
+int launch_group_mf(Ctx *c, const Groups &G, char *A, const GLay &L, int ntile) {
+    const int *d = (const int *)(A + L.ints);
+    const int *items = d + 3 * G.count;
+    const SwTab *tab = (const SwTab *)(A + L.tab);
+    const SwGroups gt = {d, d + G.count, d + 2 * G.count, nullptr, nullptr, ntile, 0, items, items + ntile};
+    const SwQ4 gu = {nullptr, nullptr, 2 * G.I, G.D, G.gs_gu, 1};
+    const SwQ4 dn = {nullptr, nullptr, G.D, G.I, G.gs_d, 1};
+    uint32_t *xd = (uint32_t *)(A + L.xl), *hd = (uint32_t *)(A + L.hl);
+    float *xds = (float *)(A + L.xs), *hds = (float *)(A + L.hs);
+    if (sw_launch_digits(c->st, (const float *)(A + L.x), G.total, G.D, xd, xds)) return 0;
+    if (sw_launch_mf_glu_tab(c->st, gu, tab, xd, xds, gt, G.I, hd, hds)) return 0;
+    if (sw_launch_mf_rows_tab(c->st, dn, tab, hd, hds, gt, (float *)(A + L.y))) return 0;
+    return ok(hipGetLastError(), "expert group launch");
+}
+
 // the synchronous group (expert_group, expert_mlp, shared_mlp_w4a16)
 int group_sync(const Groups &G, float *y, const float *x) {
     Ctx *c = find_ctx(G.device);
@@ -209,8 +232,16 @@ int group_sync(const Groups &G, float *y, const float *x) {
     std::lock_guard<std::mutex> lk(mu_of(c));
     if (!select_ctx(c)) return 0;
     const int T = G.total;
-    const GLay L = glay(G, T, T);
-    const size_t xb = (size_t)T * G.D * 4, mb = meta_bytes(G, 0);
+    const bool mf = use_mf(G);
+    std::vector<int> items;
+    if (mf) {
+        for (int g = 0; g < G.count; g++)
+            for (int t0 = 0; t0 < G.cnt[g]; t0 += SW_MF_TT) items.push_back((t0 << 10) | g);
+        items.push_back((int)items.size());
+    }
+    const int ni = (int)items.size();
+    const GLay L = glay(G, T, T, ni, mf);
+    const size_t xb = (size_t)T * G.D * 4, ib = (size_t)(3 * G.count + ni) * 4, mb = ib + (size_t)G.count * sizeof(SwTab);
     if (!grow(c, c->arena, L.end) || !grow_pinned(c, c->hin, c->hin_cap, xb + mb) ||
         !grow_pinned(c, c->hout, c->hout_cap, xb))
         return 0;
@@ -221,17 +252,20 @@ int group_sync(const Groups &G, float *y, const float *x) {
         for (auto &e : c->prof)
             if (!ok(hipEventCreate(&e), "profile event")) return 0;
     memcpy(H, x, xb);
-    pack_meta(G, nullptr, 0, H + xb);
+    pack_meta(G, nullptr, 0, H + xb);                      // gexp gbeg gcnt, then the table
+    if (mf) {                                              // the tiles between the ints and the table
+        memmove(H + xb + ib, H + xb + (size_t)(3 * G.count) * 4, (size_t)G.count * sizeof(SwTab));
+        memcpy(H + xb + (size_t)(3 * G.count) * 4, items.data(), (size_t)ni * 4);
+    }
     if (prof) (void)hipEventRecord(c->prof[0], c->st);
     // the table follows the ints in the image; in the arena it has its own aligned slot
     if (!ok(hipMemcpyAsync(A + L.x, H, xb, hipMemcpyHostToDevice, c->st), "expert group input upload") ||
-        !ok(hipMemcpyAsync(A + L.ints, H + xb, (size_t)(3 * G.count) * 4, hipMemcpyHostToDevice, c->st),
-            "expert group descriptors") ||
-        !ok(hipMemcpyAsync(A + L.tab, H + xb + (size_t)(3 * G.count) * 4, (size_t)G.count * sizeof(SwTab),
-                           hipMemcpyHostToDevice, c->st), "expert group table"))
+        !ok(hipMemcpyAsync(A + L.ints, H + xb, ib, hipMemcpyHostToDevice, c->st), "expert group descriptors") ||
+        !ok(hipMemcpyAsync(A + L.tab, H + xb + ib, (size_t)G.count * sizeof(SwTab), hipMemcpyHostToDevice, c->st),
+            "expert group table"))
         return 0;
     if (prof) (void)hipEventRecord(c->prof[1], c->st);
-    if (!launch_group(c, G, A, L, T, T, false)) return 0;
+    if (mf ? !launch_group_mf(c, G, A, L, ni - 1) : !launch_group(c, G, A, L, T, T, false)) return 0;
     if (prof) (void)hipEventRecord(c->prof[2], c->st);
     if (!ok(hipMemcpyAsync(c->hout, A + L.y, xb, hipMemcpyDeviceToHost, c->st), "expert group output download")) return 0;
     if (prof) (void)hipEventRecord(c->prof[3], c->st);
@@ -651,8 +685,8 @@ extern "C" int coli_hip_expert_group_resident_issue(ColiHipTensor *const *gates,
     // scratch for the 64-expert cap at this (D, I), so a later issue never regrows it under queued work
     Groups cap = G;
     cap.count = 64;
-    const GLay Lc = glay(cap, 64, 1);
-    const GLay L = glay(G, T, 1);
+    const GLay Lc = glay(cap, 64, 1, 64);
+    const GLay L = glay(G, T, 1, T);
     if (!grow(c, c->res, Lc.end + (size_t)G.D * 4 + 256)) return 0;
     // the pinned meta image: wait until the previous issue's copy of it has run
     if (c->ev_res_live && !ok(hipEventSynchronize(c->ev_res), "resident meta wait")) return 0;

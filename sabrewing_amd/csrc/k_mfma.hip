@@ -112,6 +112,7 @@ struct MfArgs {
     uint32_t *hdg;          // GLU: h of every packed row as digits [T][I/32][MF_DW]
     float *hxs;             //      and factors [T][I/32]
     float *Y;               // rows: [T][O]
+    const SwTab *tab;       // per-group tensors (the _tab launches) or null
 };
 
 // the pairwise tree of a run of CH terms (CH a power of two <= 16), fed one
@@ -150,7 +151,7 @@ __device__ __forceinline__ sw_i32x4 mf_expand(uint32_t w) {
 template <int N>
 struct MfIc { static constexpr int v = N; };
 
-template <int GLU, int CH, int FULL>
+template <int GLU, int CH, int FULL, int PT>
 __global__ __launch_bounds__(MF_NT, 1) void k_mf(MfArgs A) {
     extern __shared__ __align__(16) uint8_t mf_lds[];
     const SwQ4 W = A.W;
@@ -171,17 +172,34 @@ __global__ __launch_bounds__(MF_NT, 1) void k_mf(MfArgs A) {
     const int nt = tend - t0;
     const int i0 = rb * 64, r0 = rb * MF_ROWS;
     // weight row of local row r (GLU: gate rows i0..i0+63, then the up rows)
+    // (PT: row r of the group's own gate, up or down tensor)
     auto srow = [&](int r) -> uint32_t {
-        if (GLU) return (uint32_t)e * (uint32_t)O + (uint32_t)(r < 64 ? i0 + r : A.I + i0 + r - 64);
-        return (uint32_t)e * (uint32_t)O + (uint32_t)(r0 + r);     // past O: the next expert's rows, not stored
+        const uint32_t eo = PT ? 0u : (uint32_t)e * (uint32_t)O;
+        if (GLU) return eo + (uint32_t)(r < 64 ? i0 + r : (PT ? 0 : A.I) + i0 + r - 64);
+        return eo + (uint32_t)(r0 + r);     // past O: the next expert's rows (PT: zeros), not stored
     };
     auto token = [&](int t) -> int64_t {                   // input row of tile token t (past the tile: its last)
         const int pr = beg + t0 + min(t, nt - 1);
         return grp.grow ? grp.grow[pr] : pr;
     };
-    const sw_rsrc rq = sw_q4_rq(W), rs = sw_q4_rs(W);
     const int ng = W.gs > 0 ? K / W.gs : 1;
     const uint32_t rbytes = (uint32_t)K / 2;
+    sw_rsrc rq, rs;
+    if constexpr (PT) {
+        // a staging thread's row ra = tid & 127 is an up row iff (tid >> 6) & 1: uniform per wave
+        const SwTab tb_ = A.tab[e];
+        if (GLU) {
+            const bool up = __builtin_amdgcn_readfirstlane((tid >> 6) & 1);
+            rq = sw_make_rsrc(up ? tb_.u : tb_.g, (uint32_t)A.I * rbytes);
+            rs = sw_make_rsrc(up ? tb_.us : tb_.gs, (uint32_t)A.I * (uint32_t)ng * 4);
+        } else {
+            rq = sw_make_rsrc(tb_.d, (uint32_t)O * rbytes);
+            rs = sw_make_rsrc(tb_.ds, (uint32_t)O * (uint32_t)ng * 4);
+        }
+    } else {
+        rq = sw_q4_rq(W);
+        rs = sw_q4_rs(W);
+    }
 
     // ---- staging: this thread's units of a chunk
     //  weights: row ra = tid & 127 of group tid >> 7 (16 B packed, expanded on the store) + its scale
@@ -326,8 +344,13 @@ __global__ __launch_bounds__(MF_NT, 1) void k_mf(MfArgs A) {
                     const int i = 16 * mp + 4 * kq + j, t = 32 * np + 16 * ni + col;
                     float yg = y[0][ni][j], yu = y[1][ni][j];
                     if (W.gs <= 0) {                        // per-row scales after the sum
-                        yg = yg * W.s[(int64_t)e * (2 * I) + i0 + i];
-                        yu = yu * W.s[(int64_t)e * (2 * I) + I + i0 + i];
+                        if constexpr (PT) {
+                            yg = yg * A.tab[e].gs[i0 + i];
+                            yu = yu * A.tab[e].us[i0 + i];
+                        } else {
+                            yg = yg * W.s[(int64_t)e * (2 * I) + i0 + i];
+                            yu = yu * W.s[(int64_t)e * (2 * I) + I + i0 + i];
+                        }
                     }
                     hl[t * MF_HLD + i] = (yg / (1.0f + expf(-yg))) * yu;
                 }
@@ -355,7 +378,8 @@ __global__ __launch_bounds__(MF_NT, 1) void k_mf(MfArgs A) {
                             sw_f32x4 o;
 #pragma unroll
                             for (int j = 0; j < 4; j++)
-                                o[j] = W.gs > 0 ? y[mi][ni][j] : y[mi][ni][j] * W.s[(int64_t)e * O + row + j];
+                                o[j] = W.gs > 0 ? y[mi][ni][j]
+                                                : y[mi][ni][j] * (PT ? A.tab[e].ds[row + j] : W.s[(int64_t)e * O + row + j]);
                             *(sw_f32x4 *)(yrow + row) = o;
                         }
                     }
@@ -371,25 +395,25 @@ static size_t mf_lds_bytes() {
     return 2 * MF_BUF > h ? 2 * MF_BUF : h;
 }
 // dynamic LDS above 64 KB, raised once per kernel, outside any stream work
-template <int GLU, int CH, int FULL>
+template <int GLU, int CH, int FULL, int PT>
 static int mf_go(hipStream_t st, unsigned nblocks, const MfArgs &A) {
     static size_t raised = 0;
     const size_t lds = mf_lds_bytes();
     if (lds > raised) {
-        if (hipFuncSetAttribute((const void *)k_mf<GLU, CH, FULL>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
-            hipSuccess) return -1;
+        if (hipFuncSetAttribute((const void *)k_mf<GLU, CH, FULL, PT>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)lds) != hipSuccess) return -1;
         raised = lds;
     }
-    SW_LAUNCH((k_mf<GLU, CH, FULL>), dim3(nblocks), dim3(MF_NT), lds, st, A);
+    SW_LAUNCH((k_mf<GLU, CH, FULL, PT>), dim3(nblocks), dim3(MF_NT), lds, st, A);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
-template <int GLU>
+template <int GLU, int PT = 0>
 static int mf_dispatch(hipStream_t st, unsigned nblocks, const MfArgs &A) {
     const int G = A.W.K / SW_RG, Gq = run_lanes(G), CH = Gq < 16 ? Gq : 16;
     const bool full = G == Gq;
-    if (CH == 16) return full ? mf_go<GLU, 16, 1>(st, nblocks, A) : mf_go<GLU, 16, 0>(st, nblocks, A);
-    if (CH == 8) return full ? mf_go<GLU, 8, 1>(st, nblocks, A) : mf_go<GLU, 8, 0>(st, nblocks, A);
-    if (CH == 4) return full ? mf_go<GLU, 4, 1>(st, nblocks, A) : mf_go<GLU, 4, 0>(st, nblocks, A);
+    if (CH == 16) return full ? mf_go<GLU, 16, 1, PT>(st, nblocks, A) : mf_go<GLU, 16, 0, PT>(st, nblocks, A);
+    if (CH == 8) return full ? mf_go<GLU, 8, 1, PT>(st, nblocks, A) : mf_go<GLU, 8, 0, PT>(st, nblocks, A);
+    if (CH == 4) return full ? mf_go<GLU, 4, 1, PT>(st, nblocks, A) : mf_go<GLU, 4, 0, PT>(st, nblocks, A);
     return -1;
 }
 // shapes: K a multiple of 128 (whole chunks of 4 input groups), tiles listed (items, P)
@@ -413,4 +437,25 @@ int sw_launch_mf_rows(hipStream_t st, SwQ4 W, const uint32_t *dg, const float *x
     const int nrb = (W.O + MF_ROWS - 1) / MF_ROWS;
     const MfArgs A = {W, gsh, dg, xs, g, 0, nrb, nullptr, nullptr, Y};
     return mf_dispatch<0>(st, (unsigned)(g.ngroups_max * nrb), A);
+}
+
+// the same two GEMMs over per-group tensors: group c's gate/up/down are tab[gexp[c]]
+// (W gives O, K and gs; each tensor holds one expert)
+int sw_launch_mf_glu_tab(hipStream_t st, SwQ4 W, const SwTab *tab, const uint32_t *dg, const float *xs, SwGroups g,
+                         int I, uint32_t *hdg, float *hxs) {
+    int gsh;
+    W.E = 1;
+    if (!tab || !hdg || !hxs || mf_check(W, g, gsh) || I % 64 || W.O != 2 * I) return -1;
+    const int nrb = I / 64;
+    const MfArgs A = {W, gsh, dg, xs, g, I, nrb, hdg, hxs, nullptr, tab};
+    return mf_dispatch<1, 1>(st, (unsigned)(g.ngroups_max * nrb), A);
+}
+int sw_launch_mf_rows_tab(hipStream_t st, SwQ4 W, const SwTab *tab, const uint32_t *dg, const float *xs, SwGroups g,
+                          float *Y) {
+    int gsh;
+    W.E = 1;
+    if (!tab || !Y || mf_check(W, g, gsh) || W.O % 4) return -1;
+    const int nrb = (W.O + MF_ROWS - 1) / MF_ROWS;
+    const MfArgs A = {W, gsh, dg, xs, g, 0, nrb, nullptr, nullptr, Y, tab};
+    return mf_dispatch<0, 1>(st, (unsigned)(g.ngroups_max * nrb), A);
 }

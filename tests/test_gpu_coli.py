@@ -2,9 +2,10 @@
 sabrewing_amd/csrc/coli_hip.hip) against the oracle and against the lag family.
 
   * expert groups: each row equals the same expert's lag_hip_expert_q4 output bit
-    for bit (the same dot8 kernels, reading the group's three tensors through a
-    per-group table) and the oracle's int4 expert (c/moe_quant.h / c/quant.h
-    numerics) within the lag family's bounds;
+    for bit (the same dot8 kernels, or for prefill-sized groups the int8 MFMA
+    GEMMs, reading the group's three tensors through a per-group table) and the
+    oracle's int4 expert (c/moe_quant.h / c/quant.h numerics) within the lag
+    family's bounds;
   * issue/take, expert_mlp and the shared MLP are the same computation;
   * the resident pair: one fma per expert in call order, slots summed in order;
   * the router: idx, weights and the kept count equal the oracle's restatement of
@@ -112,6 +113,28 @@ def test_expert_group_equals_lag_and_oracle(coli, be, orc, gs):
     n = (C.c_uint64 * 3)()
     coli.f.group_stats(C.addressof(n), C.addressof(n) + 8, C.addressof(n) + 16, None, None, None)
     assert n[0] >= 1 and n[1] >= 5 and n[2] >= T
+    ex.free()
+
+
+@pytest.mark.parametrize("gs", [0, 32])
+def test_prefill_group_on_the_mfma(coli, be, orc, gs):
+    """groups averaging >= 8 rows take the int8 MFMA GEMMs (64-token tiles, partial tiles,
+    one group over two tiles): still each row's lag expert output bit for bit"""
+    L = layer(orc, gs, seed=21)
+    ex = Experts(coli, L, gs)
+    ids, rows = [3, 1, 4, 0], [40, 70, 9, 130]
+    T = sum(rows)
+    x = np.random.default_rng(7).standard_normal((T, D)).astype(np.float32)
+    y = coli.expert_group(*ex.lists(ids), rows, x)
+    dev = [be.upload(a) for a in (L.gu_q, L.gu_s, L.dn_q, L.dn_s)]
+    owner = np.repeat(ids, rows)
+    for r in list(range(0, T, 7)) + [39, 40, 109, 110, 118, 119, 182, 183, T - 1]:
+        e = int(owner[r])
+        assert np.array_equal(bits(y[r]), bits(lag_expert(be, dev, L, e, x[r], gs))), (e, r)
+        if r % 35 == 0:
+            assert normwise(y[r], cpu_expert(orc, L, e, x[r], gs)) < (2e-4 if gs == 0 else 2e-3)
+    for b in dev:
+        b.free()
     ex.free()
 
 
