@@ -72,7 +72,7 @@ int    lag_hip_moe_group_g(float *acc, const float *x, const void *gu_q, const f
 
 /* ---------------- 3. device-resident MoE block ---------------- */
 enum { LAG_HIP_ROUTE_SIGMOID = 0, LAG_HIP_ROUTE_SOFTMAX = 1, LAG_HIP_ROUTE_SOFTPLUS = 2,
-       LAG_HIP_ROUTE_SOFTMAX_OLMOE = 3, LAG_HIP_ROUTE_SOFTMAX_QWEN = 4 };
+       LAG_HIP_ROUTE_SOFTMAX_OLMOE = 3, LAG_HIP_ROUTE_SOFTMAX_QWEN = 4, LAG_HIP_ROUTE_SQRT_SOFTPLUS = 5 };
 enum { LAG_HIP_SHARED_NONE = 0, LAG_HIP_SHARED_UNSCALED = 1 };
 
 /* MoeDesc (c/moe_arch.h:33-41) plus the layer shape.  route_act: SIGMOID and
@@ -82,7 +82,9 @@ enum { LAG_HIP_SHARED_NONE = 0, LAG_HIP_SHARED_UNSCALED = 1 };
  * sum, c/olmoe.c:212-216, 607-632; norm_topk as moe_block's); SOFTMAX_QWEN
  * qwen35's moe_route (double-sum softmax, (float)(p / sum) in double, the
  * picks always renormalised in double, c/qwen35.c:558-589; norm_topk and the
- * correction bias unused).  The reference wires shared NONE and UNSCALED. */
+ * correction bias unused); SQRT_SOFTPLUS sqrtf(softplusf(x)), DeepSeek-V4's
+ * router score (c/deepseek.c:854), selected and weighted as moe_block's
+ * sigmoid scores.  The reference wires shared NONE and UNSCALED. */
 typedef struct {
     int   n_experts, topk, route_act, use_corr_bias, norm_topk;
     float route_scale;
@@ -200,7 +202,7 @@ int    lag_hip_gen_q4(uint8_t *q, float *s, uint64_t seed, double sigma, int64_t
 
 /* ---------------- diagnostics ---------------- */
 /* MFMA lane-layout probes (f16, bf16, int8) + libm evaluation on n host
- * inputs; out_host gets 768 + 2n floats (layout in k_route.hip).  0 = ran */
+ * inputs; out_host gets 768 + 3n floats (layout in k_route.hip).  0 = ran */
 int    lag_hip_selftest(float *out_host, const float *xin_host, int n);
 const char *lag_hip_last_error(void);
 

@@ -468,6 +468,9 @@ static void route_row(const SwMoeDesc *d, const SwMoeLayer *L, float *rl, float 
         sw_softmax_row_olmoe(rl, E); for (int e = 0; e < E; e++) sc[e] = rl[e];
     } else if (d->route_act == SW_ROUTE_SOFTMAX) { sw_softmax_row(rl, E); for (int e = 0; e < E; e++) sc[e] = rl[e]; }
     else if (d->route_act == SW_ROUTE_SOFTPLUS) { for (int e = 0; e < E; e++) sc[e] = sw_softplusf(rl[e]); }
+    else if (d->route_act == SW_ROUTE_SQRT_SOFTPLUS) {   /* c/deepseek.c:854 */
+        for (int e = 0; e < E; e++) sc[e] = sqrtf(sw_softplusf(rl[e]));
+    }
     else for (int e = 0; e < E; e++) sc[e] = 1.f / (1.f + expf(-rl[e]));
     sw_moe_topk(sc, L->corr_bias, d->use_corr_bias, E, K, sel);
     for (int a = 0; a < K; a++) w[a] = sc[sel[a]];

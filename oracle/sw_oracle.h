@@ -74,7 +74,7 @@ int   sw_argmax(const float *v, int n);
 
 /* ---------------- MoE block ---------------- */
 enum { SW_ROUTE_SIGMOID = 0, SW_ROUTE_SOFTMAX = 1, SW_ROUTE_SOFTPLUS = 2, SW_ROUTE_SOFTMAX_OLMOE = 3,
-       SW_ROUTE_SOFTMAX_QWEN = 4 };
+       SW_ROUTE_SOFTMAX_QWEN = 4, SW_ROUTE_SQRT_SOFTPLUS = 5 };
 enum { SW_SHARED_NONE = 0, SW_SHARED_UNSCALED = 1 };
 
 typedef struct {

@@ -334,7 +334,7 @@ class Backend:
 
     def selftest(self, xin):
         xin = np.ascontiguousarray(xin, np.float32)
-        out = np.zeros(768 + 2 * xin.size, np.float32)
+        out = np.zeros(768 + 3 * xin.size, np.float32)
         self.check(self.lib.lag_hip_selftest(out, xin, xin.size), "lag_hip_selftest")
         return out
 

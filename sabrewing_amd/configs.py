@@ -21,6 +21,8 @@ from dataclasses import dataclass, replace
 ROUTE_SIGMOID, ROUTE_SOFTMAX, ROUTE_SOFTPLUS = 0, 1, 2
 # other callers' routing contracts (c/olmoe.c:607-632; c/qwen35.c:558-589)
 ROUTE_SOFTMAX_OLMOE, ROUTE_SOFTMAX_QWEN = 3, 4
+# DeepSeek-V4's router score sqrtf(softplusf(x)) (c/deepseek.c:854) as a moe_block gate
+ROUTE_SQRT_SOFTPLUS = 5
 SHARED_NONE, SHARED_UNSCALED = 0, 1
 WEIGHT_SIGMA = 0.02
 
@@ -85,6 +87,9 @@ C5_LAYERS, C5_BATCH, C5_VOCAB = 48, 8, 32000
 
 # C1 routed as the OLMoE engine routes it; a qwen35-style layer (int4 experts through
 # lag_cuda_moe_group, softmax top-8 renormalised in double, c/qwen35.c:600-640)
+# a DeepSeek-V4-shaped gate (c/deepseek.c:854): sqrt(softplus) scores with the correction
+# bias in the selection, on the C2 layer shape (a parity case, not a bench config)
+C2_SQRTSP = replace(C2, name="C2-sqrt-softplus", route_act=ROUTE_SQRT_SOFTPLUS)
 C1_OLMOE = replace(C1, name="C1-olmoe-engine-routing", route_act=ROUTE_SOFTMAX_OLMOE, norm_topk=1)
 QWEN = MoeConfig("qwen35-moe", D=2048, E=256, K=8, I=512, Is=0, route_act=ROUTE_SOFTMAX_QWEN,
                  use_corr_bias=0, norm_topk=0, route_scale=1.0, shared_mode=SHARED_NONE, router_bf16=False,

@@ -467,6 +467,7 @@ static int g_last_ng = 0;
 static int desc_ok(const LagHipMoeDesc *d, const LagHipMoeWeights *w) {
     if (!d || !w) return 0;
     if (d->n_experts <= 0 || d->topk <= 0 || d->topk > d->n_experts || d->topk > 64) return 0;
+    if (d->route_act < 0 || d->route_act > SW_ROUTE_ACT_MAX) return 0;
     if (d->hidden % 128 || d->moe_inter % 128) return 0;
     if (d->gs > 0 && (d->gs % 32 || d->hidden % d->gs || d->moe_inter % d->gs)) return 0;
     if (d->shared_mode && (!w->sg || !w->su || !w->sd || d->shared_inter % 128)) return 0;
@@ -605,7 +606,7 @@ extern "C" int lag_hip_moe_forward(const LagHipMoeDesc *d, const LagHipMoeWeight
     // one token with E <= 256: its gate + top-k runs in every block of the
     // expert stage (no device-scope handoff); otherwise a gate + top-k launch
     // after the routing stage
-    const bool in_experts = E <= 256 && S == 1 && d->route_act <= 2;   // (the block top-k takes acts 0-2)
+    const bool in_experts = E <= 256 && S == 1 && (d->route_act == 1 || sw_act_scores(d->route_act));
     // S == 1: the shared expert's gate_up and down run as extra blocks of stages 1 and 2;
     // S > 1: as kernels of their own over token tiles (the same arithmetic per token)
     const bool sh_in = sh && S == 1;
@@ -796,12 +797,12 @@ extern "C" int lag_hip_gen_q4(uint8_t *q, float *s, uint64_t seed, double sigma,
 extern "C" int lag_hip_selftest(float *out_host, const float *xin_host, int n) {
     if (!g_ok || n < 0) return -1;
     float *dout = nullptr, *din = nullptr;
-    CK(hipMalloc(&dout, (size_t)(768 + 2 * n) * 4), "selftest alloc");
+    CK(hipMalloc(&dout, (size_t)(768 + 3 * n) * 4), "selftest alloc");
     if (n > 0 && hipMalloc(&din, (size_t)n * 4) != hipSuccess) { (void)hipFree(dout); return fail_msg("selftest alloc"); }
     if (n > 0) CK(hipMemcpy(din, xin_host, (size_t)n * 4, hipMemcpyHostToDevice), "selftest upload");
     int rc = sw_launch_selftest(g_st, dout, din, n);
     if (rc == 0 && hipStreamSynchronize(g_st) != hipSuccess) rc = -1;
-    if (rc == 0 && hipMemcpy(out_host, dout, (size_t)(768 + 2 * n) * 4, hipMemcpyDeviceToHost) != hipSuccess) rc = -1;
+    if (rc == 0 && hipMemcpy(out_host, dout, (size_t)(768 + 3 * n) * 4, hipMemcpyDeviceToHost) != hipSuccess) rc = -1;
     (void)hipFree(dout);
     if (din) (void)hipFree(din);
     return rc ? fail_msg("selftest") : 0;

@@ -761,7 +761,7 @@ static void launch_stage_route(int bf16, dim3 grid, size_t lds, hipStream_t st, 
 int sw_launch_stage_route(hipStream_t st, const void *Wc, int w_bf16, const float *x, int S, int D, int E,
                           const float *logit_bias, float *logits, float *scores, int route_act, sw_u32x4 *xl, float *xs,
                           const uint16_t *sg, const uint16_t *su, int Is, float *sh_h) {
-    if (D % 128 || E <= 0 || S <= 0 || route_act < 0 || route_act > 4 || (!sw_act_softmax(route_act) && !scores)) return -1;
+    if (D % 128 || E <= 0 || S <= 0 || route_act < 0 || route_act > SW_ROUTE_ACT_MAX || (!sw_act_softmax(route_act) && !scores)) return -1;
     const int one = router_one(S, E);
     const size_t rl = router_lds(D);
     if (rl > 65536 || D > 4 * RT_XB * (one ? SH_NT - 64 : SH_NT)) return -1;
@@ -795,7 +795,7 @@ int sw_launch_stage_experts(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, const fl
     if (dot8_glu_check(W, I, gsh)) return -1;
     const bool picks = sel != nullptr;
     if (picks && (S != 1 || K <= 0 || K > 64)) return -1;
-    if (picks && route_src && (E <= 0 || E > 256 || K > E || !w || act < 0 || act > 2)) return -1;
+    if (picks && route_src && (E <= 0 || E > 256 || K > E || !w || !(act == 1 || sw_act_scores(act)))) return -1;
     if (!picks && g.ngroups_max <= 0) return -1;
     if (sd && (D % SH_DN_O || !sh_shape_ok(Is))) return -1;
     const int nbx = picks ? K : g.ngroups_max;

@@ -61,7 +61,7 @@ int sw_launch_router_topk(hipStream_t st, const void *Wc, int w_bf16, const floa
                           sw_u32x4 *xl, float *xs) {
     if (D % 128 || D > 16384 || E <= 0 || S <= 0) return -1;
     if (sel && (E > TK_MAXE || K <= 0 || K > 64 || K > E)) return -1;   // (logits only: any number of rows)
-    if (route_act < 0 || route_act > 4 || (sel && !sw_act_softmax(route_act) && !scores)) return -1;
+    if (route_act < 0 || route_act > SW_ROUTE_ACT_MAX || (sel && !sw_act_softmax(route_act) && !scores)) return -1;
     // four experts per block (wave 0; the others stage x) while that stays within 256 blocks,
     // else four per wave of eight
     const int nt = 512, one = router_one(S, E), epb = router_epb(one, nt);
@@ -82,7 +82,7 @@ int sw_launch_router_topk(hipStream_t st, const void *Wc, int w_bf16, const floa
 
 int sw_launch_gate_topk(hipStream_t st, const float *logits, const float *scores, int S, int E, int K, int route_act,
                         const float *corr_bias, int use_corr_bias, int norm_topk, int *sel, float *w) {
-    if (E <= 0 || E > TK_MAXE || S <= 0 || K <= 0 || K > 64 || K > E || route_act < 0 || route_act > 4) return -1;
+    if (E <= 0 || E > TK_MAXE || S <= 0 || K <= 0 || K > 64 || K > E || route_act < 0 || route_act > SW_ROUTE_ACT_MAX) return -1;
     if (!sw_act_softmax(route_act) && !scores) return -1;
     const int nper = (E + 63) / 64;
 #define SW_GATE(NP) SW_LAUNCH(k_gate_topk<NP>, dim3((unsigned)S), dim3(64), 0, st, logits, scores, E, K, route_act, \
@@ -247,7 +247,7 @@ int sw_launch_combine(hipStream_t st, const float *slots, const int *rowof, cons
 // (5 l + 3 b + 1) % 23 - 11), whose C shows which A and B bytes meet; plus
 // glibc-exact libm on host-chosen inputs.  out: [0,256) f16 MFMA C per lane
 // (4 each), [256,512) bf16 MFMA, [512,768) i8 MFMA, [768, 768+n)
-// sw_expf(xin), [768+n, 768+2n) sw_log1pf(xin).
+// sw_expf(xin), [768+n, 768+2n) sw_log1pf(xin), [768+2n, 768+3n) sw_sqrt_rn(xin).
 #define ST_LIBM 768
 __global__ void k_selftest_mfma(float *out) {
     const int l = threadIdx.x;
@@ -284,6 +284,7 @@ __global__ void k_selftest_libm(float *out, const float *xin, int n) {
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
         out[ST_LIBM + i] = sw_expf(xin[i]);
         out[ST_LIBM + n + i] = sw_log1pf(xin[i]);
+        out[ST_LIBM + 2 * n + i] = sw_sqrt_rn(xin[i]);
     }
 }
 

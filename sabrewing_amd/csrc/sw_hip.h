@@ -109,6 +109,10 @@ struct SwGroups {
 // top-k): 1 moe_block's, 3 OLMoE's, 4 qwen35's; 0 sigmoid and 2 softplus come
 // as scores from the router
 __host__ __device__ inline bool sw_act_softmax(int act) { return act == 1 || act == 3 || act == 4; }
+// the gates whose router scores are selected by moe_topk and weighted as moe_block's
+// sigmoid (c/moe_block.h:115-122): sigmoid, softplus, sqrt(softplus)
+__host__ __device__ inline bool sw_act_scores(int act) { return act == 0 || act == 2 || act == 5; }
+#define SW_ROUTE_ACT_MAX 5
 // the upper bound of the passes of T packed rows in at most min(T, E) groups, tt tokens each
 __host__ __device__ inline int sw_npass_max(int T, int E, int tt) { return (T + (T < E ? T : E) * (tt - 1)) / tt; }
 // XCD-aware block order: launches deal consecutive block ids to the 8 XCDs in

@@ -148,4 +148,25 @@ __host__ __device__ static inline float sw_softplus_ref_t(float x, const uint64_
 __host__ __device__ static inline float sw_sigmoid_ref(float x) { return sw_sigmoid_ref_t(x, sw_exp2f_tab); }
 __host__ __device__ static inline float sw_softplus_ref(float x) { return sw_softplus_ref_t(x, sw_exp2f_tab); }
 
+// IEEE sqrtf (round to nearest) from the hardware estimate: the result is the
+// float whose rounding interval holds sqrt(x), decided by comparing x with the
+// squares of the midpoints to its neighbours.  A midpoint has 25 significant
+// bits, so its square is exact in double; sqrt(x) of a float x is never a
+// midpoint.  Two corrections cover an estimate within 2 ulp.
+__device__ static inline float sw_sqrt_rn(float x) {
+    if (!(x > 0.f) || x == __builtin_inff()) return __builtin_sqrtf(x);   // +-0, negative, NaN, inf
+    float sc = 1.f;
+    if (x < 1.17549435e-38f) { x *= 18446744073709551616.0f; sc = 2.3283064365386963e-10f; }  // subnormal: x 2^64, result 2^-32 (exact)
+    float r = __builtin_sqrtf(x);
+    const double xd = x;
+    for (int it = 0; it < 2; it++) {
+        const float d = __uint_as_float(__float_as_uint(r) - 1u), u = __uint_as_float(__float_as_uint(r) + 1u);
+        const double md = 0.5 * ((double)d + (double)r), mu = 0.5 * ((double)r + (double)u);
+        if (md * md > xd) r = d;
+        else if (mu * mu < xd) r = u;
+        else break;
+    }
+    return r * sc;
+}
+
 #endif

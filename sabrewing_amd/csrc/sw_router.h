@@ -165,7 +165,9 @@ __device__ __forceinline__ void router_block(const RouterArgs &R, int bx, int s,
         if (R.lbias) v = v + R.lbias[e];
         R.logits[(int64_t)s * E + e] = v;
         if (!sw_act_softmax(act) && R.scores)
-            R.scores[(int64_t)s * E + e] = (act == 2) ? sw_softplus_ref_t(v, tab) : sw_sigmoid_ref_t(v, tab);
+            R.scores[(int64_t)s * E + e] = act == 2   ? sw_softplus_ref_t(v, tab)
+                                           : act == 5 ? sw_sqrt_rn(sw_softplus_ref_t(v, tab))   // c/deepseek.c:854
+                                                      : sw_sigmoid_ref_t(v, tab);
     }
     if (!ONE && R.xl) {                               // the token's dot8 limbs, half a wave per group, from xt
         const int G = D / SW_RG;

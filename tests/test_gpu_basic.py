@@ -40,6 +40,12 @@ def test_device_libm_matches_host(be, orc):
     assert np.array_equal(e_dev.view(np.uint32), e_host.view(np.uint32))
     ok = (l_dev.view(np.uint32) == l_host.view(np.uint32)) | (np.isnan(l_dev) & np.isnan(l_host))
     assert ok.all()
+    # sqrt rounded to nearest (the SQRT_SOFTPLUS gate): numpy's float32 sqrt is IEEE, and the
+    # positive inputs include subnormals and every exponent
+    pos = xs >= 0
+    s_dev, s_host = out[768 + 2 * n:768 + 3 * n], np.sqrt(np.where(pos, xs, np.float32(0)))
+    assert np.array_equal(s_dev[pos].view(np.uint32), s_host[pos].view(np.uint32))
+    assert np.isnan(s_dev[xs < 0]).all()
 
 
 def test_generator_matches_host(be, orc):

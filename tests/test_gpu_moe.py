@@ -33,7 +33,8 @@ SMALL = [cf.scaled(cf.C1, D=512, E=16, K=4, I=256),
          replace(cf.scaled(cf.C2_SIGMOID, D=512, E=32, K=6, I=256, Is=256), name="C2-small-gs0", gs=0),
          cf.scaled(cf.C2_SIGMOID, D=768, E=32, K=6, I=384, Is=384, name="C2-D768"),     # 24 groups: padded runs of 16
          cf.scaled(cf.C1_OLMOE, D=512, E=64, K=8, I=256, name="C1-olmoe-engine"),
-         cf.scaled(cf.QWEN, D=512, E=64, K=8, I=256, name="qwen35-small")]
+         cf.scaled(cf.QWEN, D=512, E=64, K=8, I=256, name="qwen35-small"),
+         cf.scaled(cf.C2_SQRTSP, D=512, E=32, K=6, I=256, Is=256, name="C2-sqrt-softplus-small")]
 
 
 @pytest.mark.parametrize("cfg", SMALL, ids=lambda c: c.name)

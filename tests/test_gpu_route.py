@@ -56,6 +56,7 @@ CASES = [
     (cf.C1_OLMOE, 0.0),                                            # OLMoE engine: float-sum softmax, divide
     (replace(cf.C1_OLMOE, name="C1-olmoe-nonorm", norm_topk=0), 0.0),
     (cf.QWEN, 0.0),                                                # qwen35: double softmax, double renorm
+    (cf.C2_SQRTSP, 0.01),                                          # DeepSeek-V4's sqrt(softplus) + correction bias
 ]
 
 

@@ -178,3 +178,22 @@ def test_other_callers_routing_vs_ref(orc, rng, E, K):
         sel, w = orc.route_logits(d, row[None])
         qs, qw = rc.qwen_route(row, K)
         assert np.array_equal(sel[0], qs) and bits_equal(w[0], qw)
+
+
+def test_sqrt_softplus_gate(orc, ref, rng):
+    """route_act 5: the oracle's scores are the compiled reference's softplusf then an
+    IEEE sqrt (c/deepseek.c:854), selected with the correction bias by moe_topk and
+    weighted as moe_block's sigmoid scores, renormalised (c/moe_block.h:115-122)"""
+    from oracle.oracle import Ref
+    cfg = cf.scaled(cf.C2_SQRTSP, D=512, E=64, K=6, I=256, Is=256)
+    L = synth.make_layer(orc, cfg, 31, corr_bias_sigma=0.01)
+    x = synth.make_x(orc, cfg, 32, 7)
+    lg, sel, w = orc.route(synth.desc_of(cfg), L, x)
+    for s in range(x.shape[0]):
+        sp = np.array([ref.lib.ref_softplusf(float(v)) for v in lg[s]], np.float32)
+        sc = np.sqrt(sp)                                   # float32 sqrt: correctly rounded
+        choice = sc + L.corr_bias
+        order = sorted(range(cfg.E), key=lambda e: (-float(choice[e]), e))[:cfg.K]
+        assert list(sel[s]) == order
+        want = sc[order] / np.float32(sum(np.float32(v) for v in sc[order]))   # route_scale: after the combine
+        assert np.allclose(w[s], want, rtol=2e-7, atol=0)
