@@ -217,6 +217,69 @@ def run_stack(args):
     st.free()
 
 
+def run_coli(args):
+    """--config GLM-coli: the GLM engine's coli_cuda_expert_group on GLM-4.5-shaped experts
+    (D=5120, I=1536, per-row int4, separate gate/up/down tensors), a side figure: decode
+    (8 experts x 1 row) and prefill (8 experts x 256 rows).  Four sets of 8 experts (378 MB)
+    rotate so the Infinity Cache cannot serve a call's weights.  Device time is the
+    reference's own COLI_CUDA_PROFILE accounting (events around the launches,
+    c/backend_cuda.cu:822-940); the host figure includes the PCIe copies and the sync."""
+    import ctypes as C
+    os.environ["COLI_CUDA_PROFILE"] = "1"
+    from sabrewing_amd.coli import Coli
+    D, I, NE, NSET = 5120, 1536, 8, 4
+    c = Coli([0])
+    rng = np.random.default_rng(args.seed)
+    sets = []
+    for _ in range(NSET):
+        ts = []
+        for _ in range(NE):
+            g = rng.integers(0, 256, (I, D // 2), dtype=np.uint8)
+            u = rng.integers(0, 256, (I, D // 2), dtype=np.uint8)
+            d = rng.integers(0, 256, (D, I // 2), dtype=np.uint8)
+            ts.append((c.upload(g, np.full(I, 2e-3, np.float32), D, I), c.upload(u, np.full(I, 2e-3, np.float32), D, I),
+                       c.upload(d, np.full(D, 2e-3, np.float32), I, D)))
+        sets.append(([t[0] for t in ts], [t[1] for t in ts], [t[2] for t in ts]))
+    wbytes = NE * (3 * I * D // 2 + (2 * I + D) * 4)
+
+    def stats():
+        v = (C.c_uint64 * 3)(); f = (C.c_double * 3)()
+        c.f.group_stats(C.addressof(v), C.addressof(v) + 8, C.addressof(v) + 16, C.addressof(f), C.addressof(f) + 8,
+                        C.addressof(f) + 16)
+        return v[0], f[1]
+
+    res = {}
+    for name, rows, n in (("decode", 1, max(args.steps, 40)), ("prefill", 256, max(args.steps // 10, 8))):
+        x = rng.standard_normal((NE * rows, D)).astype(np.float32)
+        for i in range(4):
+            c.expert_group(*sets[i % NSET], [rows] * NE, x)
+        c0, k0 = stats()
+        t0 = time.perf_counter()
+        for i in range(n):
+            c.expert_group(*sets[i % NSET], [rows] * NE, x)
+        dt = (time.perf_counter() - t0) / n
+        c1, k1 = stats()
+        kern_us = 1e3 * (k1 - k0) / max(c1 - c0, 1)
+        res[name] = {"experts": NE, "rows_per_expert": rows, "calls": n, "host_us_per_call": round(dt * 1e6, 1),
+                     "device_us_per_call": round(kern_us, 1), "weight_bytes": wbytes,
+                     "weight_GBs_device": round(wbytes / (kern_us * 1e-6) / 1e9, 1),
+                     "expert_rows_per_s_host": round(NE * rows / dt, 1),
+                     "tera_ops_device": round(2 * 3 * I * D * NE * rows / (kern_us * 1e-6) / 1e12, 2),
+                     "kernel": "int8 MFMA" if rows >= 8 else "dot8 grouped"}
+        log(f"GLM-coli {name}: {dt * 1e6:.1f} us/call host, {kern_us:.1f} us device "
+            f"({wbytes / (kern_us * 1e-6) / 1e9:.0f} GB/s of expert weights)")
+    print(json.dumps({"metric": "coli_cuda_expert_group (GLM-4.5-shaped experts) side figure", "unit": "us/call",
+                      "n_gpus": 1, "higher_is_better": False, "dtype": "int4 per-row weights x f32 activations",
+                      "data": "synthetic: uniform random int4 bytes, N(0,1) rows",
+                      "config": {"workload": "GLM-coli", "hidden": D, "moe_inter": I, "sets_rotated": NSET}, **res}),
+          flush=True)
+    for st in sets:
+        for ts in st:
+            for t in ts:
+                t.free()
+    c.close()
+
+
 def run(args):
     from sabrewing_amd import configs as cf
     from sabrewing_amd.backend import Backend, DeviceLayer, desc_of, gen_x
@@ -415,6 +478,9 @@ def main():
         sys.exit(2)
     if args.config == "C5-stack":
         run_stack(args)
+        return
+    if args.config == "GLM-coli":
+        run_coli(args)
         return
     args.batch = args.batch or 1
     run(args)
