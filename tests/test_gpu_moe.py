@@ -97,10 +97,11 @@ def host_layer_for(orc, cfg, seed, x):
     return L, sel
 
 
-@pytest.mark.parametrize("cfg", [cf.C1, cf.C2, cf.C2_SIGMOID], ids=lambda c: c.name)
-@pytest.mark.parametrize("S_", [1, 4])
+@pytest.mark.parametrize("cfg,S_", [(c, s) for c in (cf.C1, cf.C2, cf.C2_SIGMOID) for s in (1, 4)] + [(cf.C2, 32)],
+                         ids=lambda v: v.name if hasattr(v, "name") else str(v))
 def test_layer_full_size(be, orc, cfg, S_):
-    """benchmark shapes: device-generated layer vs the oracle on the same bits"""
+    """benchmark shapes, the bench's B = 1 and B = 32 workloads included: device-generated
+    layer vs the oracle on the same bits"""
     seed = 555
     x = synth.make_x(orc, cfg, seed, S_)
     L, sel_w = host_layer_for(orc, cfg, seed, x)
