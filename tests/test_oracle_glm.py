@@ -3,7 +3,8 @@ the contract of coli_hip_pipe_router, pinned on the CPU:
 
   * the logits GEMV equals the reference's own c/quant.h matmul, compiled from
     the reference (oracle/_ref/libref_glm_avx512.so), bit for bit at every
-    input count 1..80 and at the GLM shapes (its vector body and scalar tail);
+    input count 1..80 and at the GLM shapes (its vector body and scalar tail),
+    and the committed vectors written from it (tests/golden/glm_router.npz);
   * the selection against what the mathematics fixes: a brute-force ranking
     (value descending, then id), ties to the lowest id, NaN and values at or
     below -1e30 never chosen, the fallback of an empty pass, the top-p cut at
@@ -29,6 +30,16 @@ def test_logits_equal_compiled_reference(o):
         W = (rng.standard_normal((17, D)) * 0.05).astype(np.float32)
         a, b = o.glm_matmul(x, W), r.matmul(x, W)
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), D
+
+
+def test_logits_equal_golden(o):
+    """the committed vectors of the compiled c/quant.h matmul (tests/golden/make_glm_golden.py):
+    the pin without the reference present"""
+    import os
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", "glm_router.npz"))
+    for D in (5, 13, 37, 5120, 5127):
+        got = o.glm_matmul(g[f"x_{D}"], g[f"w_{D}"])
+        assert np.array_equal(got.view(np.uint32), g[f"y_{D}"].view(np.uint32)), D
 
 
 def test_logits_are_sigmoid_of_the_dot(o):
