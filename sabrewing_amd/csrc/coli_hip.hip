@@ -193,7 +193,7 @@ int launch_group(Ctx *c, const Groups &G, char *A, const GLay &L, int T, int xro
     const SwQ4 gu = {nullptr, nullptr, 2 * G.I, G.D, G.gs_gu, 1};
     const SwQ4 dn = {nullptr, nullptr, G.D, G.I, G.gs_d, 1};
     if (sw_launch_limbs(c->st, (const float *)(A + L.x), xrows, G.D, xl, xs)) return 0;
-    if (sw_launch_q4_dot8_glu_tab(c->st, gu, tab, xl, xs, g, G.I, hl, hs)) return 0;
+    if (sw_launch_q4_dot8_glu_tab(c->st, gu, tab, xl, xs, g, G.I, hl, hs, G.total == G.count)) return 0;
     SwGroups gd = g;
     gd.grow = nullptr;
     if (sw_launch_q4_dot8_rows_tab(c->st, dn, tab, hl, hs, gd, (float *)(A + L.y))) return 0;

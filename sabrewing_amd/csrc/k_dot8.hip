@@ -530,22 +530,23 @@ int sw_launch_q4_dot8_rows(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, const flo
 // The two grouped kernels with group c's gate/up/down read from tab[gexp[c]]: the
 // same blocks, steps and fixed-order sums, so a group's outputs are bit-identical to
 // the same expert's outputs from the one-tensor launches above.
-template <int PF, int C16, int RO>
+template <int PF, int C16, int RO, int TT>
 __global__ __launch_bounds__(DG_NT) void k_dot8_glu_tab(Dot8GluArgs A) {
     extern __shared__ __align__(16) float red[];
-    dot8_glu_block<PF, 0, 0, DG_TT, C16, RO, 1>(A, blockIdx.x, blockIdx.y, red);
+    dot8_glu_block<PF, 0, 0, TT, C16, RO, 1>(A, blockIdx.x, blockIdx.y, red);
 }
-template <int RO>
+template <int RO, int TT>
 struct GluTabL {
     template <int PF, int C16>
     struct L {
         static void go(dim3 grid, size_t lds, hipStream_t st, const Dot8GluArgs &A) {
-            SW_LAUNCH((k_dot8_glu_tab<PF, C16, RO>), grid, dim3(DG_NT), lds, st, A);
+            SW_LAUNCH((k_dot8_glu_tab<PF, C16, RO, TT>), grid, dim3(DG_NT), lds, st, A);
         }
     };
 };
+// one_row: every group holds one row (decode), so a weight pass carries one token
 int sw_launch_q4_dot8_glu_tab(hipStream_t st, SwQ4 W, const SwTab *tab, const sw_u32x4 *xl, const float *xs, SwGroups g,
-                              int I, sw_u32x4 *hl, float *hs) {
+                              int I, sw_u32x4 *hl, float *hs, int one_row) {
     int gsh;
     W.E = 1;                                              // each tensor holds one expert
     if (!tab || dot8_glu_check(W, I, gsh) || g.ngroups_max <= 0 || g.items) return -1;
@@ -553,9 +554,11 @@ int sw_launch_q4_dot8_glu_tab(hipStream_t st, SwQ4 W, const SwTab *tab, const sw
     // a decode-sized call (few groups) takes 32-output blocks, so the grid still fills the chip
     const int RO = g.ngroups_max * (I / 128) < 512 ? 32 : dg_ro(I);
     const dim3 grid((unsigned)g.ngroups_max, (unsigned)(I / RO));
-    if (RO == 128) dispatch_pf_c16<GluTabL<128>::L>(dg_pf_glu(W.K), dot8_c16(W.K), grid, dot8_glu_lds(W.K, DG_TT, 128), st, A);
-    else if (RO == 64) dispatch_pf_c16<GluTabL<64>::L>(dg_pf_glu(W.K), dot8_c16(W.K), grid, dot8_glu_lds(W.K, DG_TT, 64), st, A);
-    else dispatch_pf_c16<GluTabL<32>::L>(dg_pf_glu(W.K), dot8_c16(W.K), grid, dot8_glu_lds(W.K, DG_TT, 32), st, A);
+    const int pf = dg_pf_glu(W.K), c16 = dot8_c16(W.K);
+    if (one_row && RO == 32) dispatch_pf_c16<GluTabL<32, 1>::L>(pf, c16, grid, dot8_glu_lds(W.K, 1, 32), st, A);
+    else if (RO == 128) dispatch_pf_c16<GluTabL<128, DG_TT>::L>(pf, c16, grid, dot8_glu_lds(W.K, DG_TT, 128), st, A);
+    else if (RO == 64) dispatch_pf_c16<GluTabL<64, DG_TT>::L>(pf, c16, grid, dot8_glu_lds(W.K, DG_TT, 64), st, A);
+    else dispatch_pf_c16<GluTabL<32, DG_TT>::L>(pf, c16, grid, dot8_glu_lds(W.K, DG_TT, 32), st, A);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

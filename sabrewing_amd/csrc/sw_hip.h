@@ -232,7 +232,7 @@ int sw_launch_q4_dot8_rows(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, const flo
 // the same two grouped kernels over per-group tensors: W gives O, K and gs (its q, s
 // and E are unused); group c's tensors are tab[gexp[c]]
 int sw_launch_q4_dot8_glu_tab(hipStream_t st, SwQ4 W, const SwTab *tab, const sw_u32x4 *xl, const float *xs, SwGroups g,
-                              int I, sw_u32x4 *hl, float *hs);
+                              int I, sw_u32x4 *hl, float *hs, int one_row);
 int sw_launch_q4_dot8_rows_tab(hipStream_t st, SwQ4 W, const SwTab *tab, const sw_u32x4 *xl, const float *xs, SwGroups g,
                                float *Y);
 // the dot8 down projection fused with the rank-order combine for one token
