@@ -26,6 +26,17 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+# what the kernels compute in: int4 weights and their f32 group scales against the
+# activations written per 32 inputs as 7 signed base-8 digits under a power-of-two
+# factor (exact integer dots, |input error| <= 2^-21 of the group's largest input);
+# f32 accumulation; the router and the shared expert in f32 fma chains on bf16 weights
+DTYPE = ("int4 x int4-digit activations (7 base-8 limbs per 32 inputs, 2^-21 of the group max), "
+         "exact int32 dots, f32 scales and accumulation; f32 router and shared expert on bf16 weights")
+# the reference CPU baseline's OpenMP placement (c/moe_util.h:78-86 sets one thread per
+# physical core; the pinning is the reference's measured setting); read when the
+# OpenMP runtime first starts, so set before any OpenMP library loads
+os.environ.setdefault("OMP_PROC_BIND", "spread")
+os.environ.setdefault("OMP_PLACES", "cores")
 
 
 def log(*a):
@@ -135,14 +146,6 @@ def per_row_modes(be, cfg, dl, xs, seconds, steps):
                    get(d0.sd, (D, c0.Is), np.uint16) if c0.shared_mode else None)
     d = osyn.desc_of(replace(c0, route_act=0) if c0.route_act == 2 else c0)
     out = {}
-    o = np.zeros((1, D), np.float32)
-    for name, mode in (("cpu_f32", 0), ("cpu_idot", 1)):
-        ref.moe_block_rows(d, L, xs[0:1], o, mode)
-        n, t0 = 0, time.perf_counter()
-        while time.perf_counter() - t0 < seconds and n < 100000:
-            ref.moe_block_rows(d, L, xs[n % len(xs):n % len(xs) + 1], o, mode)
-            n += 1
-        out[name] = round(n / (time.perf_counter() - t0), 1)
     xb, ob = be.upload(xs[:1]), be.alloc(D * 4)
     for name, mode in (("device", be.Q4_DOT8), ("device_idot", be.Q4_IDOT)):
         prev = be.set_q4_mode(mode)
@@ -159,6 +162,15 @@ def per_row_modes(be, cfg, dl, xs, seconds, steps):
             out[name] = round(steps / (be.elapsed_ms(e0, e1) * 1e-3), 1)
         finally:
             be.set_q4_mode(prev)
+    # the CPU modes after the device ones (the OpenMP team pins the host thread)
+    o = np.zeros((1, D), np.float32)
+    for name, mode in (("cpu_f32", 0), ("cpu_idot", 1)):
+        ref.moe_block_rows(d, L, xs[0:1], o, mode)
+        n, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < seconds and n < 100000:
+            ref.moe_block_rows(d, L, xs[n % len(xs):n % len(xs) + 1], o, mode)
+            n += 1
+        out[name] = round(n / (time.perf_counter() - t0), 1)
     xb.free(); ob.free(); d0.free()
     out["unit"] = "tokens/s (B=1, eager)"
     out["sample"] = f"{c0.name}: per-row int4, {isa} reference with one thread per physical core, ~{seconds:.0f} s per CPU mode"
@@ -206,7 +218,7 @@ def run_stack(args):
     res = {"metric": "Config-5 stack decode tokens/s (48 int4 MoE layers + RMSNorm + bf16 head + greedy pick)",
            "value": round(B / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
            "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
-           "vs_baseline": None, "dtype": "int4 weights (group-32 f32 scales) x f32 activations, f32 accumulate",
+           "vs_baseline": None, "dtype": DTYPE,
            "data": "synthetic: seeded N(0,0.02) weights generated on device, N(0,1) bf16-valued tokens",
            "config": {"workload": "C5-stack", "batch": B, "layers": L, "hidden": D, "experts": cfg.E, "topk": cfg.K,
                       "moe_inter": cfg.I, "vocab": V},
@@ -280,23 +292,30 @@ def run_coli(args):
     c.close()
 
 
-def run(args):
-    from sabrewing_amd import configs as cf
-    from sabrewing_amd.backend import Backend, DeviceLayer, desc_of, gen_x
+def host_facts():
+    """the CPU baseline's host: model, sockets, NUMA nodes, CPUs, glibc (read before
+    any OpenMP team binds the process's threads)"""
+    import glob
+    info = open("/proc/cpuinfo").read().splitlines()
+    model = next((l.split(":", 1)[1].strip() for l in info if l.startswith("model name")), "unknown")
+    sockets = len({l.split(":", 1)[1].strip() for l in info if l.startswith("physical id")}) or 1
+    try:
+        glibc = os.confstr("CS_GNU_LIBC_VERSION")
+    except (ValueError, OSError):
+        glibc = None
+    return {"cpu_model": model, "sockets": sockets,
+            "numa_nodes": len(glob.glob("/sys/devices/system/node/node[0-9]*")) or 1,
+            "logical_cpus": os.cpu_count(), "cpus_allowed": len(os.sched_getaffinity(0)), "glibc": glibc,
+            "omp": {k: os.environ.get(k) for k in ("OMP_PROC_BIND", "OMP_PLACES")}}
 
-    cfg = cf.CONFIGS[args.config]
-    B = args.batch
-    be = Backend(0)
-    be.set_grouped_kernel({"auto": 0, "dot8": 1, "mfma": 2}[args.grouped])
-    t0 = time.time()
-    layers = []
-    for l in range(args.layers):
-        dl = DeviceLayer.generate(be, cfg, args.seed, layer=l)
-        dl.seed, dl.layer = args.seed, l
-        layers.append(dl)
-    log(f"generated {args.layers} x {cfg.name} layers in {time.time() - t0:.1f}s")
+
+def measure(be, cfg, layers, B, args, seed, profile=True):
+    """One batch size: W eager warmup steps, K timed steps (eager, then the same
+    steps recorded as one graph and replayed), then the distinct experts per step
+    and, with profile, each kernel's average launch time from HIP events."""
+    from sabrewing_amd.backend import desc_of, gen_x
     nx = args.warmup + args.steps
-    xbuf = gen_x(be, cfg, args.seed, B * nx)
+    xbuf = gen_x(be, cfg, seed, B * nx)
     outs = [be.alloc(B * cfg.D * 4) for _ in layers]
     for o in outs:
         be.lib.lag_hip_memset(int(o), 0, B * cfg.D * 4)
@@ -308,6 +327,129 @@ def run(args):
         l = i % len(layers)
         be.moe_forward(desc, wts[l], xptr(i), outs[l], B)
 
+    r = {"B": B}
+    try:
+        for i in range(args.warmup):
+            step(i)
+        be.sync()
+        ev0, ev1 = be.event(), be.event()
+        be.record(ev0)
+        h0 = time.perf_counter()
+        for i in range(args.steps):
+            step(args.warmup + i)
+        r["host_us"] = (time.perf_counter() - h0) * 1e6 / args.steps
+        be.record(ev1)
+        be.sync()
+        r["ms_eager"] = be.elapsed_ms(ev0, ev1) / args.steps
+        log(f"{cfg.name} B={B} eager: {r['ms_eager'] * 1e3:.1f} us/step, {B / (r['ms_eager'] * 1e-3):.0f} tokens/s "
+            f"(host enqueue {r['host_us']:.1f} us/step)")
+        r["ms"] = r["ms_eager"]
+        if not args.eager:
+            # the same K steps recorded once and replayed with one submission: the
+            # device time of the steps without the host's per-launch cost
+            be.graph_begin()
+            for i in range(args.steps):
+                step(args.warmup + i)
+            g = be.graph_end()
+            be.graph_launch(g)
+            be.sync()
+            be.record(ev0)
+            be.graph_launch(g)
+            be.record(ev1)
+            be.sync()
+            be.graph_destroy(g)
+            r["ms"] = be.elapsed_ms(ev0, ev1) / args.steps
+        r["tok_s"] = B / (r["ms"] * 1e-3)
+        log(f"{cfg.name} B={B}: {r['ms'] * 1e3:.1f} us/step, {r['tok_s']:.0f} tokens/s "
+            f"({'eager' if args.eager else 'graph replay'})")
+        if not profile:
+            return r
+        # distinct experts per step (the bytes a step must read)
+        G_sum, nG = 0, min(args.steps, 20)
+        for i in range(nG):
+            step(args.warmup + i)
+            if B > 1:
+                G_sum += be.last_groups()[0]
+        G = G_sum / nG if B > 1 and G_sum > 0 else cfg.K
+        # per-kernel times: the same steps again, each launch bracketed by HIP events
+        # on the backend stream
+        be.profile_reset()
+        be.profile(True)
+        for i in range(args.steps):
+            step(args.warmup + i)
+        be.sync()
+        prof = be.profile_read()
+        be.profile(False)
+        kb = kernel_bytes(cfg, B, G)
+        kern = {k: {"avg_us": 1e3 * v[0] / max(v[1], 1), "launches": v[1]} for k, v in prof.items()}
+        for k, v in kern.items():
+            if k in kb:
+                v["bytes"] = kb[k]
+                v["GBs"] = kb[k] / (v["avg_us"] * 1e-6) / 1e9 if v["avg_us"] > 0 else 0.0
+        dom = max(kern, key=lambda k: kern[k]["avg_us"] * kern[k]["launches"])
+        dk = kern[dom]
+        # HBM bytes per launch of that kernel as rocprofv3 counted them (FETCH_SIZE x2 + WRITE_SIZE,
+        # calibrated on a device copy; profiles/decode_kernels_*.md), when a profile covers this workload
+        traffic = None
+        try:
+            with open(os.path.join(ROOT, "profiles", "traffic.json")) as f:
+                traffic = json.load(f).get(cfg.name, {}).get(str(B), {}).get(dom, {}).get("traffic_bytes")
+        except (OSError, ValueError):
+            pass
+        r["G"] = G
+        r["layer_bytes"] = cfg.step_bytes(B, G)
+        r["layer_gbs"] = r["layer_bytes"] / (r["ms"] * 1e-3) / 1e9
+        r["roofline"] = {"bound": "hbm", "kernel": dom, "achieved": round(dk.get("GBs", 0.0), 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(dk.get("GBs", 0.0) / HBM_PEAK_GBS, 4), "traffic": traffic,
+                         "bytes_per_launch": dk.get("bytes"), "avg_launch_us": round(dk["avg_us"], 2)}
+        r["kernels"] = {k: {kk: (round(vv, 2) if isinstance(vv, float) else vv) for kk, vv in v.items()}
+                        for k, v in kern.items()}
+        log(f"B={B} kernels:", json.dumps(r["kernels"]))
+        if B == args.batch:
+            # the host-buffer boundary (lag_hip_moe_block: x and out in host memory, copied
+            # over PCIe each call, synchronous): a side figure, never `value`
+            hx = be.d2h(xbuf, (B, cfg.D), np.float32)
+            hout = np.zeros((B, cfg.D), np.float32)
+            for i in range(5):
+                be.moe_block(desc, wts[i % len(wts)], hx, hout)
+            nh = max(20, min(args.steps, 200))
+            h0 = time.perf_counter()
+            for i in range(nh):
+                be.moe_block(desc, wts[i % len(wts)], hx, hout)
+            r["pcie_ms"] = (time.perf_counter() - h0) * 1e3 / nh
+            log(f"host-buffer entry (PCIe-inclusive, synchronous): {r['pcie_ms'] * 1e3:.1f} us/step, "
+                f"{B / (r['pcie_ms'] * 1e-3):.0f} tokens/s")
+        return r
+    finally:
+        for o in outs:
+            o.free()
+        xbuf.free()
+
+
+def batch_summary(cfg, r):
+    return {"batch": r["B"], "ms_per_step": round(r["ms"], 5), "tokens_per_s": round(r["tok_s"], 1),
+            "distinct_experts_per_step": round(r["G"], 2), "layer_bytes_per_step": int(r["layer_bytes"]),
+            "layer_hbm_GBs": round(r["layer_gbs"], 1), "layer_hbm_frac": round(r["layer_gbs"] / HBM_PEAK_GBS, 4),
+            "roofline": r["roofline"]}
+
+
+def run(args):
+    from sabrewing_amd import configs as cf
+    from sabrewing_amd.backend import Backend, DeviceLayer, gen_x
+
+    cfg = cf.CONFIGS[args.config]
+    B = args.batch
+    facts = host_facts()
+    be = Backend(0)
+    be.set_grouped_kernel({"auto": 0, "dot8": 1, "mfma": 2}[args.grouped])
+    t0 = time.time()
+    layers = []
+    for l in range(args.layers):
+        dl = DeviceLayer.generate(be, cfg, args.seed, layer=l)
+        dl.seed, dl.layer = args.seed, l
+        layers.append(dl)
+    log(f"generated {args.layers} x {cfg.name} layers in {time.time() - t0:.1f}s")
+
     if args.calib_copy_mb:
         # a plain device copy of known size, for scaling the FETCH_SIZE / WRITE_SIZE counters
         n = args.calib_copy_mb << 20
@@ -318,135 +460,71 @@ def run(args):
         a_.free(); b_.free()
         log(f"calibration copy: {args.calib_copy_mb} MiB device-to-device")
 
-    for i in range(args.warmup):
-        step(i)
-    be.sync()
-    ev0, ev1 = be.event(), be.event()
-    be.record(ev0)
-    h0 = time.perf_counter()
-    for i in range(args.steps):
-        step(args.warmup + i)
-    host_us = (time.perf_counter() - h0) * 1e6 / args.steps
-    be.record(ev1)
-    be.sync()
-    ms_eager = be.elapsed_ms(ev0, ev1) / args.steps
-    log(f"{cfg.name} B={B} eager: {ms_eager * 1e3:.1f} us/step, {B / (ms_eager * 1e-3):.0f} tokens/s "
-        f"(host enqueue {host_us:.1f} us/step)")
-    ms = ms_eager
-    if not args.eager:
-        # the same K steps recorded once and replayed with one submission: the
-        # device time of the steps without the host's per-launch cost
-        be.graph_begin()
-        for i in range(args.steps):
-            step(args.warmup + i)
-        g = be.graph_end()
-        be.graph_launch(g)
-        be.sync()
-        be.record(ev0)
-        be.graph_launch(g)
-        be.record(ev1)
-        be.sync()
-        be.graph_destroy(g)
-        ms = be.elapsed_ms(ev0, ev1) / args.steps
-    tok_s = B / (ms * 1e-3)
-    log(f"{cfg.name} B={B}: {ms * 1e3:.1f} us/step, {tok_s:.0f} tokens/s ({'eager' if args.eager else 'graph replay'})")
+    main_r = measure(be, cfg, layers, B, args, args.seed, profile=not args.timed_only)
     if args.timed_only:
         return
+    # the batched-decode sweep of the same layer: B = 8, 32, 64
+    sweep = {}
+    if not args.no_sweep and B == 1:
+        for b in (8, 32, 64):
+            sweep[b] = measure(be, cfg, layers, b, args, args.seed + 101 * b)
 
-    # distinct experts per step (the bytes a step must read)
-    G_sum, nG = 0, min(args.steps, 20)
-    for i in range(nG):
-        step(args.warmup + i)
-        if B > 1:
-            G_sum += be.last_groups()[0]
-    G = G_sum / nG if B > 1 and G_sum > 0 else cfg.K
-
-    # per-kernel times: the same steps again, each launch bracketed by HIP events
-    # on the backend stream
-    be.profile_reset()
-    be.profile(True)
-    for i in range(args.steps):
-        step(args.warmup + i)
-    be.sync()
-    prof = be.profile_read()
-    be.profile(False)
-    kb = kernel_bytes(cfg, B, G)
-    kern = {k: {"avg_us": 1e3 * v[0] / max(v[1], 1), "launches": v[1]} for k, v in prof.items()}
-    for k, v in kern.items():
-        if k in kb:
-            v["bytes"] = kb[k]
-            v["GBs"] = kb[k] / (v["avg_us"] * 1e-6) / 1e9 if v["avg_us"] > 0 else 0.0
-    dom = max(kern, key=lambda k: kern[k]["avg_us"] * kern[k]["launches"])
-    dk = kern[dom]
-    # HBM bytes per launch of that kernel as rocprofv3 counted them (FETCH_SIZE x2 + WRITE_SIZE,
-    # calibrated on a device copy; profiles/decode_kernels_*.md), when a profile covers this workload
-    traffic = None
-    try:
-        with open(os.path.join(ROOT, "profiles", "traffic.json")) as f:
-            traffic = json.load(f).get(cfg.name, {}).get(str(B), {}).get(dom, {}).get("traffic_bytes")
-    except (OSError, ValueError):
-        pass
-    layer_bytes = cfg.step_bytes(B, G)
-    roof = {"bound": "hbm", "kernel": dom, "achieved": round(dk.get("GBs", 0.0), 1), "peak": HBM_PEAK_GBS,
-            "unit": "GB/s", "frac": round(dk.get("GBs", 0.0) / HBM_PEAK_GBS, 4), "traffic": traffic,
-            "bytes_per_launch": dk.get("bytes"), "avg_launch_us": round(dk["avg_us"], 2)}
-    layer_gbs = layer_bytes / (ms * 1e-3) / 1e9
-    log("kernels:", json.dumps({k: {kk: (round(vv, 2) if isinstance(vv, float) else vv) for kk, vv in v.items()}
-                                for k, v in kern.items()}))
-
-    # the host-buffer boundary (lag_hip_moe_block: x and out in host memory, copied over
-    # PCIe each call, synchronous): a side figure, never `value`
-    hx = be.d2h(xbuf, (B, cfg.D), np.float32)
-    hout = np.zeros((B, cfg.D), np.float32)
-    for i in range(5):
-        be.moe_block(desc, wts[i % len(wts)], hx, hout)
-    nh = max(20, min(args.steps, 200))
-    h0 = time.perf_counter()
-    for i in range(nh):
-        be.moe_block(desc, wts[i % len(wts)], hx, hout)
-    pcie_ms = (time.perf_counter() - h0) * 1e3 / nh
-    log(f"host-buffer entry (PCIe-inclusive, synchronous): {pcie_ms * 1e3:.1f} us/step, {B / (pcie_ms * 1e-3):.0f} tokens/s")
-
+    # the CPU side last: the OpenMP team it starts pins the host thread (OMP_PROC_BIND)
     cpu = None
     modes = None
     if not args.no_cpu:
         rng_x = gen_x(be, cfg, args.seed + 1, 64)
         xs = be.d2h(rng_x, (64, cfg.D), np.float32)
         rng_x.free()
-        try:
-            cpu = cpu_baseline(be, cfg, layers[0], xs, args.cpu_seconds)
-        except Exception as e:                      # the baseline is reported, never required
-            log("cpu baseline failed:", repr(e))
         if B == 1 and cfg.gs > 0:
             try:
                 modes = per_row_modes(be, cfg, layers[0], xs, args.cpu_seconds / 3, args.steps)
                 log("per-row (gs=0) contracts:", json.dumps(modes))
             except Exception as e:
                 log("per-row modes failed:", repr(e))
+        try:
+            cpu = cpu_baseline(be, cfg, layers[0], xs, args.cpu_seconds)
+            if cpu:
+                cpu["host"] = facts
+        except Exception as e:                      # the baseline is reported, never required
+            log("cpu baseline failed:", repr(e))
 
+    r = main_r
     res = {
         "metric": "MoE-layer tokens/s + % peak HBM GB/s, int4 experts, batch 1 and batch 32",
-        "value": round(tok_s, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "value": round(r["tok_s"], 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(r["ms"], 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "submission": "eager" if args.eager else "graph replay of the timed steps",
-        "eager_value": round(B / (ms_eager * 1e-3), 1), "eager_host_enqueue_us": round(host_us, 1),
-        "host_buffer_value": round(B / (pcie_ms * 1e-3), 1),
-        "dtype": "int4 weights (group-32 f32 scales) x f32 activations, f32 accumulate",
+        "eager_value": round(B / (r["ms_eager"] * 1e-3), 1), "eager_host_enqueue_us": round(r["host_us"], 1),
+        "host_buffer_value": round(B / (r["pcie_ms"] * 1e-3), 1) if "pcie_ms" in r else None,
+        "dtype": DTYPE,
         "data": "synthetic: seeded N(0,0.02) int4 weights generated on device, N(0,1) bf16-valued tokens",
         "config": {"workload": cfg.name, "batch": B, "hidden": cfg.D, "experts": cfg.E, "topk": cfg.K,
-                   "moe_inter": cfg.I, "shared_inter": cfg.Is, "gs": cfg.gs, "gate": ["sigmoid", "softmax", "softplus"][cfg.route_act],
-                   "layers_rotated": args.layers, "distinct_experts_per_step": round(G, 2),
-                   "layer_bytes_per_step": int(layer_bytes), "layer_hbm_GBs": round(layer_gbs, 1),
-                   "layer_hbm_frac": round(layer_gbs / HBM_PEAK_GBS, 4)},
-        "roofline": roof,
+                   "moe_inter": cfg.I, "shared_inter": cfg.Is, "gs": cfg.gs,
+                   "gate": ["sigmoid", "softmax", "softplus", "softmax-olmoe", "softmax-qwen", "sqrt-softplus"][cfg.route_act],
+                   "layers_rotated": args.layers, "distinct_experts_per_step": round(r["G"], 2),
+                   "layer_bytes_per_step": int(r["layer_bytes"]), "layer_hbm_GBs": round(r["layer_gbs"], 1),
+                   "layer_hbm_frac": round(r["layer_gbs"] / HBM_PEAK_GBS, 4)},
+        "roofline": r["roofline"],
         "cpu_baseline": cpu,
         "per_row_modes": modes,
-        "kernels": {k: {kk: (round(vv, 2) if isinstance(vv, float) else vv) for kk, vv in v.items()} for k, v in kern.items()},
+        "kernels": r["kernels"],
     }
+    if 32 in sweep:
+        b32 = sweep[32]
+        per_tok1 = r["layer_bytes"] / B
+        per_tok32 = b32["layer_bytes"] / 32
+        res["batch32"] = {**batch_summary(cfg, b32), "kernels": b32["kernels"],
+                          "tokens_per_s_vs_batch1": round(b32["tok_s"] / r["tok_s"], 3),
+                          # bytes per token fall only this much with G distinct experts, so
+                          # this is the ratio at equal HBM efficiency; F7's ceiling puts B=1
+                          # at 70 % and B=32 at 100 % of peak
+                          "ratio_at_equal_hbm_frac": round(per_tok1 / per_tok32, 3),
+                          "ratio_ceiling_b1_70pct_b32_100pct": round(per_tok1 / per_tok32 / 0.7, 3),
+                          "target_ratio": 8.0}
+    if sweep:
+        res["batch_sweep"] = {str(b): batch_summary(cfg, v) for b, v in sweep.items()}
     print(json.dumps(res), flush=True)
-    for o in outs:
-        o.free()
-    xbuf.free()
     for dl in layers:
         dl.free()
 
@@ -469,6 +547,7 @@ def main():
                     help="one device-to-device copy of this many MiB before the timed steps (counter calibration)")
     ap.add_argument("--eager", action="store_true",
                     help="time the per-call submission only (default: also record the steps as one graph and time its replay)")
+    ap.add_argument("--no-sweep", action="store_true", help="B=1 only (no batch 8/32/64 objects)")
     ap.add_argument("--timed-only", action="store_true",
                     help="stop after the timed steps (no per-kernel pass, no CPU baseline, no JSON line)")
     args = ap.parse_args()

@@ -163,8 +163,11 @@ void   lag_hip_event_destroy(void *ev);
  * lag_hip_d2d) issued between begin and end into one graph, replayed with a
  * single submission by lag_hip_graph_launch (async on the backend stream).
  * Pointers and shapes are fixed at recording; scratch must already be large
- * enough (issue the same shapes once first), else the entry fails.  No
- * counterpart in the reference (its decode loop launches per layer): this
+ * enough (issue the same shapes once first), else the entry fails.  A
+ * finished recording owns the backend scratch it was recorded over until
+ * lag_hip_graph_destroy (which waits for the stream, then frees it); later
+ * calls of any size allocate their own, so they never disturb a live graph.
+ * No counterpart in the reference (its decode loop launches per layer): this
  * is the launch-overhead-free way to drive a decode step. */
 int    lag_hip_graph_begin(void);
 void  *lag_hip_graph_end(void);          /* NULL on failure */

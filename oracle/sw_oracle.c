@@ -15,6 +15,7 @@
  * tests/test_oracle_golden.py against the committed golden vectors, and
  * tests/test_oracle_math.py against closed forms and brute force. */
 #include "sw_oracle.h"
+#include <immintrin.h>
 #include <math.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -208,26 +209,82 @@ void sw_glm_matmul(float *y, const float *x, const float *W, int S, int I, int O
         for (int s = 0; s < S; s++) y[(int64_t)s * O + o] = glm_dot(x + (int64_t)s * I, W + (int64_t)o * I, I);
 }
 
+/* ---- row tiles for the lane contracts below ----
+ * A batch of S rows re-reads every weight row once per token, so the
+ * restatements walk tiles of MT weight rows (widened once into f32) against
+ * one token at a time, four rows side by side.  _mm256_fmadd_ps is eight
+ * independent fmaf() (one rounding each), so lane j of a vector accumulator
+ * is exactly the scalar chain ln[j] of the contract; the reductions are the
+ * scalar reduce16 / hsum8 on the stored lanes.  Tiling changes which rows
+ * are computed when, never the operations of one (token, row) pair. */
+#define MT 16
+static void store16(float *ln, __m256 lo, __m256 hi) { _mm256_storeu_ps(ln, lo); _mm256_storeu_ps(ln + 8, hi); }
+
+/* 16-lane SIMD contract of c/moe_matmul.h:25-43 for four widened rows w0..w3 */
+static void lane16_rows4(float *y4, const float *xs, const float *w, int I) {
+    __m256 lo[4], hi[4];
+    for (int r = 0; r < 4; r++) { lo[r] = _mm256_setzero_ps(); hi[r] = _mm256_setzero_ps(); }
+    int i = 0;
+    for (; i + 16 <= I; i += 16) {
+        const __m256 xa = _mm256_loadu_ps(xs + i), xb = _mm256_loadu_ps(xs + i + 8);
+        for (int r = 0; r < 4; r++) {
+            lo[r] = _mm256_fmadd_ps(xa, _mm256_loadu_ps(w + (int64_t)r * I + i), lo[r]);
+            hi[r] = _mm256_fmadd_ps(xb, _mm256_loadu_ps(w + (int64_t)r * I + i + 8), hi[r]);
+        }
+    }
+    for (int r = 0; r < 4; r++) {
+        float ln[16];
+        store16(ln, lo[r], hi[r]);
+        float sm = reduce16(ln);
+        for (int k = i; k < I; k++) sm = fmaf(xs[k], w[(int64_t)r * I + k], sm);
+        y4[r] = sm;
+    }
+}
+
+/* y[s, o] for rows o of W (widened by `widen` into MT-row tiles) under the
+ * 16-lane contract */
+static void lane16_matmul(float *y, const float *x, int S, int I, int O,
+                          void (*widen)(float *dst, const void *W, int64_t o0, int n, int I), const void *W) {
+    const int nt = (O + MT - 1) / MT;
+    #pragma omp parallel if((int64_t)S * O >= 512)
+    {
+        float *wv = (float *)aligned_alloc(64, ((size_t)MT * I * 4 + 63) / 64 * 64);
+        #pragma omp for schedule(static)
+        for (int t = 0; t < nt; t++) {
+            const int o0 = t * MT, no = O - o0 < MT ? O - o0 : MT;
+            widen(wv, W, o0, no, I);
+            memset(wv + (int64_t)no * I, 0, (size_t)(MT - no) * I * 4);
+            for (int s = 0; s < S; s++) {
+                const float *xs = x + (int64_t)s * I;
+                for (int r0 = 0; r0 < no; r0 += 4) {
+                    float y4[4];
+                    lane16_rows4(y4, xs, wv + (int64_t)r0 * I, I);
+                    for (int r = 0; r < 4 && r0 + r < no; r++) y[(int64_t)s * O + o0 + r0 + r] = y4[r];
+                }
+            }
+        }
+        free(wv);
+    }
+}
+static void widen_f32(float *dst, const void *W, int64_t o0, int n, int I) {
+    memcpy(dst, (const float *)W + o0 * I, (size_t)n * I * 4);
+}
+static void widen_bf16(float *dst, const void *W, int64_t o0, int n, int I) {
+    const uint16_t *w = (const uint16_t *)W + o0 * I;
+    for (int64_t k = 0; k < (int64_t)n * I; k++) dst[k] = sw_bf16_to_f32(w[k]);
+}
+
 /* c/moe_matmul.h:25-55.  SIMD: lane j sums i = j mod 16 ascending with FMA,
  * reduce16, then the scalar tail fused into the sum.  exact: double sum. */
 void sw_matmul_f32(float *y, const float *x, const float *W, int S, int I, int O, int exact) {
+    if (!exact) { lane16_matmul(y, x, S, I, O, widen_f32, W); return; }
     #pragma omp parallel for schedule(static) if((int64_t)S * O >= 512)
     for (int o = 0; o < O; o++) {
         const float *w = W + (int64_t)o * I;
         for (int s = 0; s < S; s++) {
             const float *xs = x + (int64_t)s * I;
-            if (exact) {
-                double sm = 0; for (int i = 0; i < I; i++) sm += (double)xs[i] * w[i];
-                y[(int64_t)s * O + o] = (float)sm;
-                continue;
-            }
-            float ln[16] = {0};
-            int i = 0;
-            for (; i + 16 <= I; i += 16)
-                for (int j = 0; j < 16; j++) ln[j] = fmaf(xs[i + j], w[i + j], ln[j]);
-            float sm = reduce16(ln);
-            for (; i < I; i++) sm = fmaf(xs[i], w[i], sm);
-            y[(int64_t)s * O + o] = sm;
+            double sm = 0; for (int i = 0; i < I; i++) sm += (double)xs[i] * w[i];
+            y[(int64_t)s * O + o] = (float)sm;
         }
     }
 }
@@ -236,23 +293,14 @@ void sw_matmul_f32(float *y, const float *x, const float *W, int S, int I, int O
  * lane contract as matmul_f32 (so a bf16 router equals an f32 router holding
  * the widened values, c/laguna.c:126-128). */
 void sw_matmul_bf16(float *y, const float *x, const uint16_t *W, int S, int I, int O, int exact) {
+    if (!exact) { lane16_matmul(y, x, S, I, O, widen_bf16, W); return; }
     #pragma omp parallel for schedule(static) if((int64_t)S * O >= 512)
     for (int o = 0; o < O; o++) {
         const uint16_t *w = W + (int64_t)o * I;
         for (int s = 0; s < S; s++) {
             const float *xs = x + (int64_t)s * I;
-            if (exact) {
-                double sm = 0; for (int i = 0; i < I; i++) sm += (double)xs[i] * sw_bf16_to_f32(w[i]);
-                y[(int64_t)s * O + o] = (float)sm;
-                continue;
-            }
-            float ln[16] = {0};
-            int i = 0;
-            for (; i + 16 <= I; i += 16)
-                for (int j = 0; j < 16; j++) ln[j] = fmaf(xs[i + j], sw_bf16_to_f32(w[i + j]), ln[j]);
-            float sm = reduce16(ln);
-            for (; i < I; i++) sm = fmaf(xs[i], sw_bf16_to_f32(w[i]), sm);
-            y[(int64_t)s * O + o] = sm;
+            double sm = 0; for (int i = 0; i < I; i++) sm += (double)xs[i] * sw_bf16_to_f32(w[i]);
+            y[(int64_t)s * O + o] = (float)sm;
         }
     }
 }
@@ -337,9 +385,71 @@ void sw_matmul_q4(float *y, const float *x, const uint8_t *packed, const float *
 /* group-scale int4, c/quant.h:168-203 (AVX2 body): per group an 8-lane FMA
  * chain, two FMAs per 16 columns (cols i..i+7 then i+8..i+15), hsum256, then
  * a = fma(h, scale, a); scalar tail for a group length not divisible by 16. */
+/* the AVX2 body of c/quant.h:168-203 for four rows of decoded nibble values
+ * w (n - 8 as floats, row r at w + r*I) and one token, when every group is a
+ * whole number of 16-column steps: lane j of a group's accumulator is the
+ * fmaf chain ln[j] over cols i+j then i+8+j, hsum8, a = fma(h, scale, a) */
+static void i4g_rows4(float *y4, const float *xs, const float *w, const float *sc, int ng, int I, int gs) {
+    float a[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int g = 0; g < ng; g++) {
+        const int base = g * gs;
+        __m256 ln[4];
+        for (int r = 0; r < 4; r++) ln[r] = _mm256_setzero_ps();
+        for (int i = base; i < base + gs; i += 16) {
+            const __m256 xa = _mm256_loadu_ps(xs + i), xb = _mm256_loadu_ps(xs + i + 8);
+            for (int r = 0; r < 4; r++) {
+                ln[r] = _mm256_fmadd_ps(xa, _mm256_loadu_ps(w + (int64_t)r * I + i), ln[r]);
+                ln[r] = _mm256_fmadd_ps(xb, _mm256_loadu_ps(w + (int64_t)r * I + i + 8), ln[r]);
+            }
+        }
+        for (int r = 0; r < 4; r++) {
+            float v[8];
+            _mm256_storeu_ps(v, ln[r]);
+            a[r] = fmaf(hsum8(v), sc[(int64_t)r * ng + g], a[r]);
+        }
+    }
+    for (int r = 0; r < 4; r++) y4[r] = a[r];
+}
+
+/* byte b -> {low nibble - 8, high nibble - 8} as floats (the even, odd column) */
+static float nib_pair[256][2];
+static void nib_pair_init(void) {
+    for (int b = 0; b < 256; b++) { nib_pair[b][0] = (float)((b & 0xF) - 8); nib_pair[b][1] = (float)((b >> 4) - 8); }
+}
+
 void sw_matmul_i4_grouped(float *y, const float *x, const uint8_t *q4, const float *scale,
                           int S, int I, int O, int gs) {
     int rb = (I + 1) / 2, ng = (I + gs - 1) / gs;
+    if (gs % 16 == 0 && I % gs == 0) {              /* tiles of MT rows, decoded once */
+        if (nib_pair[0][0] == 0.f) nib_pair_init();
+        const int nt = (O + MT - 1) / MT;
+        #pragma omp parallel
+        {
+            float *wv = (float *)aligned_alloc(64, ((size_t)MT * I * 4 + 63) / 64 * 64);
+            float *sv = (float *)malloc((size_t)MT * ng * 4);
+            #pragma omp for schedule(static)
+            for (int t = 0; t < nt; t++) {
+                const int o0 = t * MT, no = O - o0 < MT ? O - o0 : MT;
+                for (int r = 0; r < MT; r++) {
+                    const uint8_t *w = q4 + (int64_t)(o0 + r) * rb;
+                    float *d = wv + (int64_t)r * I;
+                    if (r < no) for (int c = 0; c < I / 2; c++) memcpy(d + 2 * c, nib_pair[w[c]], 8);
+                    else memset(d, 0, (size_t)I * 4);
+                    for (int g = 0; g < ng; g++) sv[r * ng + g] = r < no ? scale[(int64_t)(o0 + r) * ng + g] : 0.f;
+                }
+                for (int s = 0; s < S; s++) {
+                    const float *xs = x + (int64_t)s * I;
+                    for (int r0 = 0; r0 < no; r0 += 4) {
+                        float y4[4];
+                        i4g_rows4(y4, xs, wv + (int64_t)r0 * I, sv + r0 * ng, ng, I, gs);
+                        for (int r = 0; r < 4 && r0 + r < no; r++) y[(int64_t)s * O + o0 + r0 + r] = y4[r];
+                    }
+                }
+            }
+            free(wv); free(sv);
+        }
+        return;
+    }
     #pragma omp parallel for schedule(static)
     for (int o = 0; o < O; o++) {
         const uint8_t *w = q4 + (int64_t)o * rb;

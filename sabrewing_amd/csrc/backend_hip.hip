@@ -121,29 +121,13 @@ static int grow_pinned(Buf &b, size_t need) {
     b.cap = need * 2;
     return 0;
 }
-static Buf g_arena, g_hin, g_hout, g_consts;
-static int g_consts_k = 0;
+static Buf g_arena, g_hin, g_hout;
 
 // carve aligned sub-buffers out of the arena
 struct Carve {
     size_t off = 0;
     size_t take(size_t n) { size_t o = (off + 255) & ~(size_t)255; off = o + n; return o; }
 };
-
-static int ensure_consts(int K) {   // iota[K], ones[K], zeros[K]
-    if (K <= g_consts_k) return 0;
-    if (g_capturing) return fail_msg("constants not set up while recording a graph (run the same shapes once first)");
-    int k = K < 64 ? 64 : K;
-    if (grow_dev(g_consts, (size_t)3 * k * sizeof(int))) return -1;
-    std::vector<int> h((size_t)3 * k);
-    for (int i = 0; i < k; i++) { h[i] = i; h[k + i] = 1; h[2 * k + i] = 0; }
-    CK(hipMemcpy(g_consts.p, h.data(), h.size() * sizeof(int), hipMemcpyHostToDevice), "constant upload");
-    g_consts_k = k;
-    return 0;
-}
-static const int *c_iota(void) { return (const int *)g_consts.p; }
-static const int *c_ones(void) { return (const int *)g_consts.p + g_consts_k; }
-static const int *c_zeros(void) { return (const int *)g_consts.p + 2 * g_consts_k; }
 
 // ------------------------------------------------------------ lag family ----
 extern "C" int lag_hip_init(int dev) {
@@ -466,7 +450,8 @@ static int g_last_ng = 0;
 
 static int desc_ok(const LagHipMoeDesc *d, const LagHipMoeWeights *w) {
     if (!d || !w) return 0;
-    if (d->n_experts <= 0 || d->topk <= 0 || d->topk > d->n_experts || d->topk > 64) return 0;
+    // (E <= 1024: the gate/top-k wave and the counting sort hold every expert on chip)
+    if (d->n_experts <= 0 || d->n_experts > 1024 || d->topk <= 0 || d->topk > d->n_experts || d->topk > 64) return 0;
     if (d->route_act < 0 || d->route_act > SW_ROUTE_ACT_MAX) return 0;
     if (d->hidden % 128 || d->moe_inter % 128) return 0;
     if (d->gs > 0 && (d->gs % 32 || d->hidden % d->gs || d->moe_inter % d->gs)) return 0;
@@ -475,7 +460,12 @@ static int desc_ok(const LagHipMoeDesc *d, const LagHipMoeWeights *w) {
     return 1;
 }
 
-static int carve_fwd(const LagHipMoeDesc *d, int S, FwdScratch &f, bool idot = false) {
+// Where a forward's scratch comes from: the growing arena (fixed null), or a
+// caller-provided region of fixed capacity that nothing may outgrow.
+struct ScratchSrc { char *fixed; size_t cap; };
+static const ScratchSrc kArena = {nullptr, 0};
+
+static int carve_fwd(const LagHipMoeDesc *d, int S, FwdScratch &f, const ScratchSrc &src, bool idot = false) {
     const int E = d->n_experts, K = d->topk, D = d->hidden, I = d->moe_inter, Is = d->shared_inter;
     const int T = S * K;
     Carve cv;
@@ -500,8 +490,18 @@ static int carve_fwd(const LagHipMoeDesc *d, int S, FwdScratch &f, bool idot = f
         o_hq = cv.take((size_t)T * (I / 32) * 32); o_hqs = cv.take((size_t)T * (I / 32) * 4);
         o_hf = cv.take((size_t)T * I * 4);
     }
-    if (grow_dev(g_arena, cv.off)) return -1;
-    char *A = (char *)g_arena.p;
+    char *A;
+    if (src.fixed) {
+        if (cv.off > src.cap) {
+            snprintf(g_err, sizeof g_err, "moe_forward: S=%d needs %zu bytes of scratch, above the fixed region's %zu",
+                     S, cv.off, src.cap);
+            return -1;
+        }
+        A = src.fixed;
+    } else {
+        if (grow_dev(g_arena, cv.off)) return -1;
+        A = (char *)g_arena.p;
+    }
     f.xq = idot ? (uint32_t *)(A + o_xq) : nullptr; f.xqs = idot ? (float *)(A + o_xqs) : nullptr;
     f.hq = idot ? (uint32_t *)(A + o_hq) : nullptr; f.hqs = idot ? (float *)(A + o_hqs) : nullptr;
     f.hf = idot ? (float *)(A + o_hf) : nullptr;
@@ -533,17 +533,18 @@ extern "C" int lag_hip_route(const LagHipMoeDesc *d, const LagHipMoeWeights *w, 
                              float *logits, int *sel, float *wts) {
     if (!g_ok || fault_injected() || !desc_ok(d, w) || S <= 0) return -1;
     FwdScratch f;
-    if (carve_fwd(d, S, f)) return -1;
+    if (carve_fwd(d, S, f, kArena)) return -1;
     return route_dev(d, w, x, S, logits ? logits : f.logits, f.scores, sel, wts);
 }
 
 // The layer in the IDOT contract (any S): router, gate + top-k, the counting sort, int8
 // activations, grouped gate_up GLU, int8 h, grouped down into slots, combine; the
 // shared expert as in batches (the same arithmetic as the decode stages).
-static int forward_idot(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const float *x, float *out, int S) {
+static int forward_idot(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const float *x, float *out, int S,
+                        const ScratchSrc &sc) {
     const int E = d->n_experts, K = d->topk, D = d->hidden, I = d->moe_inter, Is = d->shared_inter;
     FwdScratch f;
-    if (carve_fwd(d, S, f, true) || ensure_consts(K)) return -1;
+    if (carve_fwd(d, S, f, sc, true)) return -1;
     SwQ4 gu = {(const uint8_t *)w->gu_q, w->gu_s, 2 * I, D, 0, E};
     SwQ4 dn = {(const uint8_t *)w->dn_q, w->dn_s, D, I, 0, E};
     const bool sh = d->shared_mode != 0;
@@ -590,14 +591,15 @@ static int forward_idot(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const
 // counting sort, grouped gate_up, shared down, grouped down into slots, combine;
 // the grouped GEMMs on dot8 (passes of 2 tokens) or, for prefill-sized batches,
 // on the int8 MFMA (tiles of 64 tokens, the inputs as MFMA digits).
-extern "C" int lag_hip_moe_forward(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const float *x, float *out, int S) {
+static int forward(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const float *x, float *out, int S,
+                   const ScratchSrc &sc) {
     if (!g_ok || fault_injected()) return -1;
     if (!desc_ok(d, w) || S <= 0) return fail_msg("moe_forward: unsupported descriptor/shape");
-    if (g_q4_mode == 1 && d->gs == 0) return forward_idot(d, w, x, out, S);
+    if (g_q4_mode == 1 && d->gs == 0) return forward_idot(d, w, x, out, S, sc);
     const int E = d->n_experts, K = d->topk, D = d->hidden, I = d->moe_inter, Is = d->shared_inter;
     const int T = S * K;
     FwdScratch f;
-    if (carve_fwd(d, S, f) || ensure_consts(K)) return -1;
+    if (carve_fwd(d, S, f, sc)) return -1;
     SwQ4 gu = {(const uint8_t *)w->gu_q, w->gu_s, 2 * I, D, d->gs, E};
     SwQ4 dn = {(const uint8_t *)w->dn_q, w->dn_s, D, I, d->gs, E};
     const bool sh = d->shared_mode != 0;
@@ -681,6 +683,10 @@ extern "C" int lag_hip_moe_forward(const LagHipMoeDesc *d, const LagHipMoeWeight
     }
     g_last = f;
     return 0;
+}
+
+extern "C" int lag_hip_moe_forward(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const float *x, float *out, int S) {
+    return forward(d, w, x, out, S, kArena);
 }
 
 // ------------------------------------------------------------ stack glue ----
@@ -813,7 +819,12 @@ extern "C" const char *lag_hip_last_error(void) { return g_err; }
 // ------------------------------------------------------------ graphs ----
 // Every device-pointer entry issued between begin and end (moe_forward,
 // route, d2d) is recorded into one graph, replayed by lag_hip_graph_launch
-// with one submission.
+// with one submission.  The recorded kernels hold raw pointers into the
+// scratch arena, so a finished recording takes the arena with it (freed by
+// lag_hip_graph_destroy) and the next eager call allocates a fresh one: no
+// later call, whatever its size, can free or move memory that a live graph
+// replays over.
+struct GraphRec { hipGraphExec_t exec; Buf arena; };
 extern "C" int lag_hip_graph_begin(void) {
     if (!g_ok || g_capturing) return -1;
     prof_flush();
@@ -831,13 +842,22 @@ extern "C" void *lag_hip_graph_end(void) {
     e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
     (void)hipGraphDestroy(graph);
     if (e != hipSuccess) { fail("graph instantiate", e); return nullptr; }
-    return (void *)exec;
+    GraphRec *r = new GraphRec{exec, g_arena};
+    g_arena = Buf{};
+    g_last_G_dev = 0;                   // the last groups now live in the graph's arena
+    g_last_ng = 0;
+    return (void *)r;
 }
 extern "C" int lag_hip_graph_launch(void *g) {
     if (!g_ok || !g || g_capturing) return -1;
-    CK(hipGraphLaunch((hipGraphExec_t)g, g_st), "graph launch");
+    CK(hipGraphLaunch(((GraphRec *)g)->exec, g_st), "graph launch");
     return 0;
 }
 extern "C" void lag_hip_graph_destroy(void *g) {
-    if (g) (void)hipGraphExecDestroy((hipGraphExec_t)g);
+    if (!g) return;
+    GraphRec *r = (GraphRec *)g;
+    (void)hipStreamSynchronize(g_st);   // no replay may still be reading the buffers
+    (void)hipGraphExecDestroy(r->exec);
+    if (r->arena.p) (void)hipFree(r->arena.p);
+    delete r;
 }

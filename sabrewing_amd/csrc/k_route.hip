@@ -101,16 +101,17 @@ int sw_launch_gate_topk(hipStream_t st, const float *logits, const float *scores
 // groups in ascending expert id, packed rows stable in (token, rank) order.
 // One block of 1024 threads; pairs are taken 1024 at a time in order, and a
 // pair's rank among earlier pairs of its expert comes from per-wave ballot
-// match masks plus per-wave counts of the earlier waves.
+// match masks plus per-wave counts of the earlier waves (a wave holds at most
+// 64 pairs of an expert, so each count is one byte: 16 KB for 1024 experts).
 #define BK_THREADS 1024
-#define BK_MAXE 512
+#define BK_MAXE 1024
 __global__ __launch_bounds__(BK_THREADS) void k_bucket(const int *__restrict__ sel, int T, int K, int E,
                                                        int *__restrict__ gexp, int *__restrict__ gbeg,
                                                        int *__restrict__ gcnt, int *__restrict__ Gout,
                                                        int *__restrict__ grow, int *__restrict__ rowof, int tt,
                                                        int *__restrict__ items, int *__restrict__ Pout) {
     __shared__ int cnt[BK_MAXE], run[BK_MAXE], sa[BK_MAXE], sb[BK_MAXE], sp[BK_MAXE];
-    __shared__ int wcnt[BK_THREADS / 64][BK_MAXE];
+    __shared__ uint8_t wcnt[BK_THREADS / 64][BK_MAXE];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     for (int i = tid; i < E; i += BK_THREADS) {
         cnt[i] = 0;
@@ -156,7 +157,7 @@ __global__ __launch_bounds__(BK_THREADS) void k_bucket(const int *__restrict__ s
             peers &= ((e >> b) & 1) ? m : ~m;
         }
         const int rank = __popcll(peers & lt);
-        if (act && rank == 0) wcnt[wave][e] = __popcll(peers);
+        if (act && rank == 0) wcnt[wave][e] = (uint8_t)__popcll(peers);
         __syncthreads();
         if (act) {
             int pre = 0;

@@ -1,0 +1,58 @@
+"""Helpers of the full-size parity tests: host copies of device-generated layers.
+
+A full-size layer is generated in HBM by the device generator (bit-identical to
+the host generator: tests/test_gpu_kernels.py pins it), and the oracle gets a
+host copy of it one layer at a time.  Only the experts the oracle's own routing
+picks are copied back (moe_block never reads the others), into zero-filled
+arrays whose untouched pages cost no host memory.  The router, the correction
+and Zipf biases and the norms are small and regenerated on the host."""
+import ctypes as C
+
+import numpy as np
+
+from oracle import synth
+from sabrewing_amd import synth as S
+
+
+def _d2h_into(be, dst, src, src_off):
+    """dst[:] <- device bytes at int(src) + src_off"""
+    dst = np.ascontiguousarray(dst)
+    be.check(be.lib.lag_hip_d2h(dst.ctypes.data_as(C.c_void_p), C.c_void_p(int(src) + src_off), dst.nbytes), "d2h")
+
+
+def host_layer(be, orc, cfg, dl, seed, x, layer=0):
+    """(host Layer with the experts routed by x copied from device layer dl, sel [S, K])"""
+    D, I, E, gs = cfg.D, cfg.I, cfg.E, cfg.gs
+    ngD, ngI = (D // gs, I // gs) if gs else (1, 1)
+    ts = lambda tid: S.tensor_seed(seed, layer, tid)
+    r = orc.normal(E * D, ts(S.T_ROUTER), 0.02).reshape(E, D)
+    router = orc.to_bf16(r) if cfg.router_bf16 else r
+    corr = np.zeros(E, np.float32) if cfg.use_corr_bias else None
+    lb = S.zipf_bias(E, cfg.zipf, ts(S.T_ROUTER) ^ 0x5A5A) if cfg.zipf > 0 else None
+    gu_q = np.zeros((E * 2 * I, D // 2), np.uint8)
+    gu_s = np.zeros((E * 2 * I, ngD), np.float32)
+    dn_q = np.zeros((E * D, I // 2), np.uint8)
+    dn_s = np.zeros((E * D, ngI), np.float32)
+    sg = su = sd = None
+    if cfg.shared_mode:
+        sg = be.d2h(dl.sg, (cfg.Is, D), np.uint16)
+        su = be.d2h(dl.su, (cfg.Is, D), np.uint16)
+        sd = be.d2h(dl.sd, (D, cfg.Is), np.uint16)
+    L = synth.Layer(D, I, cfg.Is, E, gs, cfg.router_bf16, router, corr, lb, gu_q.reshape(-1), gu_s.reshape(-1),
+                    dn_q.reshape(-1), dn_s.reshape(-1), sg, su, sd)
+    _, sel, _ = orc.route(synth.desc_of(cfg), L, x)
+    for e in np.unique(sel):
+        e = int(e)
+        r0, r1 = e * 2 * I, (e + 1) * 2 * I
+        _d2h_into(be, gu_q[r0:r1], dl.gu_q, r0 * (D // 2))
+        _d2h_into(be, gu_s[r0:r1], dl.gu_s, r0 * ngD * 4)
+        r0, r1 = e * D, (e + 1) * D
+        _d2h_into(be, dn_q[r0:r1], dl.dn_q, r0 * (I // 2))
+        _d2h_into(be, dn_s[r0:r1], dl.dn_s, r0 * ngI * 4)
+    return L, sel
+
+
+def normwise(got, want, base):
+    """max |(got - base) - (want - base)| / max |want - base|: the MoE update's error"""
+    dw = want - base
+    return float(np.max(np.abs((got - base) - dw))) / float(np.max(np.abs(dw)))

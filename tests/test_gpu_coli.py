@@ -117,6 +117,25 @@ def test_expert_group_equals_lag_and_oracle(coli, be, orc, gs):
 
 
 @pytest.mark.parametrize("gs", [0, 32])
+def test_expert_group_one_row_each(coli, be, orc, gs):
+    """groups of one row each (decode) take the one-token weight passes; each row
+    still equals the same expert's lag_hip_expert_q4 output bit for bit and the
+    oracle's expert within the lag family's bounds"""
+    L = layer(orc, gs, seed=7)
+    ex = Experts(coli, L, gs)
+    ids, rows = [2, 0, 5, 3], [1, 1, 1, 1]
+    x = np.random.default_rng(11).standard_normal((4, D)).astype(np.float32)
+    y = coli.expert_group(*ex.lists(ids), rows, x)
+    dev = [be.upload(a) for a in (L.gu_q, L.gu_s, L.dn_q, L.dn_s)]
+    for r, e in enumerate(ids):
+        assert np.array_equal(bits(y[r]), bits(lag_expert(be, dev, L, e, x[r], gs))), (e, r)
+        assert normwise(y[r], cpu_expert(orc, L, e, x[r], gs)) < (2e-4 if gs == 0 else 2e-3)
+    for b in dev:
+        b.free()
+    ex.free()
+
+
+@pytest.mark.parametrize("gs", [0, 32])
 def test_prefill_group_on_the_mfma(coli, be, orc, gs):
     """groups averaging >= 8 rows take the int8 MFMA GEMMs (64-token tiles, partial tiles,
     one group over two tiles): still each row's lag expert output bit for bit"""

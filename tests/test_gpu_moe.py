@@ -162,6 +162,46 @@ def test_graph_replay_matches_eager(be, orc, S_):
         dl.free()
 
 
+def test_graph_survives_larger_eager_calls(be, orc):
+    """a live recording keeps the scratch it was recorded over: eager calls of a
+    larger shape between replays (which need a larger arena) leave its replays
+    bit-identical to the eager result"""
+    cfg = SMALL[2]
+    L = synth.make_layer(orc, cfg, 53)
+    dl = DeviceLayer.from_host(be, cfg, L)
+    x1 = synth.make_x(orc, cfg, 54, 1)
+    xb = synth.make_x(orc, cfg, 55, 300)
+    z1, zb = np.zeros_like(x1), np.zeros_like(xb)
+    xd, oe, og = be.upload(x1), be.upload(z1), be.upload(z1)
+    xbd, obd = be.upload(xb), be.upload(zb)
+    be.moe_forward(desc_of(cfg), dl.weights(), xd, oe, 1)
+    be.sync()
+    want = be.d2h(oe, x1.shape, np.float32)
+    be.graph_begin()
+    be.moe_forward(desc_of(cfg), dl.weights(), xd, og, 1)
+    g = be.graph_end()
+    try:
+        for rep in range(3):
+            be.h2d(obd, zb)                                         # a larger eager call first
+            be.moe_forward(desc_of(cfg), dl.weights(), xbd, obd, 300 - 50 * rep)
+            be.sync()
+            be.h2d(og, z1)
+            be.graph_launch(g)
+            be.sync()
+            got = be.d2h(og, x1.shape, np.float32)
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), rep
+    finally:
+        be.graph_destroy(g)
+    # after the graph is gone the eager path still works
+    be.h2d(oe, z1)
+    be.moe_forward(desc_of(cfg), dl.weights(), xd, oe, 1)
+    be.sync()
+    assert np.array_equal(be.d2h(oe, x1.shape, np.float32).view(np.uint32), want.view(np.uint32))
+    for b in (xd, oe, og, xbd, obd):
+        b.free()
+    dl.free()
+
+
 @pytest.mark.parametrize("S_", [2, 33, 200])
 def test_device_bucket_matches_oracle(be, orc, S_):
     """the device counting sort (A11): groups in ascending expert id, begin
@@ -178,3 +218,24 @@ def test_device_bucket_matches_oracle(be, orc, S_):
     Gw, gexp_w, gbeg_w, gcnt_w, _, _ = orc.bucket(sel, S_, cfg.K, cfg.E)
     assert G == Gw
     assert np.array_equal(gexp, gexp_w) and np.array_equal(gbeg, gbeg_w) and np.array_equal(gcnt, gcnt_w)
+
+
+@pytest.mark.parametrize("S_", [1, 2, 5])
+def test_layer_1024_experts(be, orc, S_):
+    """E = 1024 (the descriptor's limit): the gate/top-k launch and the counting sort
+    hold every expert; routing identical and the layer within tolerance at S = 1 and
+    on the grouped path"""
+    cfg = cf.scaled(cf.C1, D=512, E=1024, K=8, I=256, name="C1-E1024")
+    L = synth.make_layer(orc, cfg, 71)
+    x = synth.make_x(orc, cfg, 72, S_)
+    base = synth.make_x(orc, cfg, 73, S_)
+    want = orc.moe_block_rows(synth.desc_of(cfg), L, x, base)
+    dl = DeviceLayer.from_host(be, cfg, L)
+    got = be.moe_block(desc_of(cfg), dl.weights(), x, base)
+    xd = be.upload(x)
+    _, sel, _ = be.route(desc_of(cfg), dl.weights(), xd, S_)
+    xd.free(); dl.free()
+    _, sel_w, _ = orc.route(synth.desc_of(cfg), L, x)
+    assert np.array_equal(sel, sel_w)
+    nw, el = errs(got, want, base)
+    assert nw <= TOL, (nw, el)
