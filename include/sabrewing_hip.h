@@ -121,6 +121,19 @@ int    lag_hip_router_chain(const void *W, void *Wc, int E, int D, int w_bf16);
  * backend stream; S == 1 runs the per-token path, S > 1 the grouped path
  * (bit-identical per token).  0 = ok. */
 int    lag_hip_moe_forward(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const float *x, float *out, int S);
+/* lag_hip_moe_forward without any allocation.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * The scratch of the forward lives in a static device array of
+ * LAG_HIP_NOALLOC_SCRATCH_BYTES on each device (held from library load until
+ * the process ends) instead of the growing arena; the call makes no
+ * hipMalloc/hipFree and no other allocation.  A shape whose scratch does not
+ * fit returns -1 before any launch (lag_hip_last_error gives the bytes it
+ * needed): the C2 layer (D=4096, E=256, K=10, I=Is=1024) fits up to S = 64.
+ * Same results, bit for bit, as lag_hip_moe_forward.  Every call on a device
+ * shares that device's array, so calls that overlap on one device race. */
+#define LAG_HIP_NOALLOC_SCRATCH_BYTES ((size_t)24 << 20)
+int    lag_hip_moe_forward_noalloc(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const float *x, float *out, int S);
 /* the same with host x/out; synchronous */
 int    lag_hip_moe_block(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const float *x, float *out, int S);
 /* routing only (device pointers): logits [S,E] (may be NULL), sel [S,K], w [S,K] */

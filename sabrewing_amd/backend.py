@@ -25,7 +25,8 @@ EXPORTS = [
     "lag_hip_init", "lag_hip_free_bytes", "lag_hip_total_bytes", "lag_hip_upload", "lag_hip_free",
     "lag_hip_matmul_bf16", "lag_hip_matmul_q4", "lag_hip_expert_q4", "lag_hip_moe_experts", "lag_hip_moe_group",
     "lag_hip_matmul_q4_g", "lag_hip_expert_q4_g", "lag_hip_moe_experts_g", "lag_hip_moe_group_g",
-    "lag_hip_router_upload", "lag_hip_router_chain", "lag_hip_moe_forward", "lag_hip_moe_block", "lag_hip_route",
+    "lag_hip_router_upload", "lag_hip_router_chain", "lag_hip_moe_forward", "lag_hip_moe_forward_noalloc",
+    "lag_hip_moe_block", "lag_hip_route",
     "lag_hip_last_groups", "lag_hip_rmsnorm", "lag_hip_head_argmax", "lag_hip_argmax", "lag_hip_set_grouped_kernel",
     "lag_hip_set_q4_mode",
     "lag_hip_alloc", "lag_hip_h2d", "lag_hip_d2h", "lag_hip_d2d", "lag_hip_memset",
@@ -99,6 +100,7 @@ def load_library(path=None):
     L.lag_hip_argmax.argtypes = [VP, C.c_int, C.c_int, VP]
     DP, WP = C.POINTER(LagHipMoeDesc), C.POINTER(LagHipMoeWeights)
     L.lag_hip_moe_forward.argtypes = [DP, WP, VP, VP, C.c_int]
+    L.lag_hip_moe_forward_noalloc.argtypes = [DP, WP, VP, VP, C.c_int]
     L.lag_hip_moe_block.argtypes = [DP, WP, F32P, F32P, C.c_int]
     L.lag_hip_route.argtypes = [DP, WP, VP, C.c_int, VP, VP, VP]
     L.lag_hip_last_groups.argtypes = [C.POINTER(C.c_int), I32P, I32P, I32P, C.c_int]
@@ -225,6 +227,11 @@ class Backend:
     def moe_forward(self, desc, weights, x_dev, out_dev, S):
         self.check(self.lib.lag_hip_moe_forward(C.byref(desc), C.byref(weights), VP(int(x_dev)), VP(int(out_dev)), S),
                    "lag_hip_moe_forward")
+
+    def moe_forward_noalloc(self, desc, weights, x_dev, out_dev, S):
+        """the allocation-free forward (scratch in the library's static device array)"""
+        self.check(self.lib.lag_hip_moe_forward_noalloc(C.byref(desc), C.byref(weights), VP(int(x_dev)),
+                                                        VP(int(out_dev)), S), "lag_hip_moe_forward_noalloc")
 
     def moe_block(self, desc, weights, x, out):
         x = np.ascontiguousarray(x, np.float32); out = np.ascontiguousarray(out, np.float32).copy()

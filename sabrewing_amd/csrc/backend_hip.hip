@@ -129,6 +129,8 @@ struct Carve {
     size_t take(size_t n) { size_t o = (off + 255) & ~(size_t)255; off = o + n; return o; }
 };
 
+static int noalloc_setup(int dev);
+
 // ------------------------------------------------------------ lag family ----
 extern "C" int lag_hip_init(int dev) {
     if (g_ok && dev == g_dev) return 0;
@@ -137,6 +139,7 @@ extern "C" int lag_hip_init(int dev) {
     void *probe = nullptr;
     CK(hipMalloc(&probe, 1 << 20), "probe allocation");
     (void)hipFree(probe);
+    if (noalloc_setup(dev)) return -1;
     g_dev = dev;
     g_ok = 1;
     return 0;
@@ -687,6 +690,40 @@ static int forward(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const floa
 
 extern "C" int lag_hip_moe_forward(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const float *x, float *out, int S) {
     return forward(d, w, x, out, S, kArena);
+}
+
+// ------------------------------------------------- the allocation-free forward ----
+// lag_hip_moe_forward with its scratch in a file-scope device array instead of
+// the arena: no allocation of any kind, for callers that cannot allocate (code
+// under graph capture, tight serving loops).  Each device holds its own copy of
+// the array; the host name `scratch` is only a stand-in, so its device address
+// is looked up once per device (lag_hip_init, with that device current) and
+// only that address is ever handed to kernels.  Nothing in it must start at
+// zero: every word a launch reads was written earlier in the same call.
+// Calls that overlap on one device share the array and race.
+#define SW_NOALLOC_MAX_DEV 64
+#define SW_NOALLOC_SCRATCH_BYTES LAG_HIP_NOALLOC_SCRATCH_BYTES
+static __device__ __align__(256) char scratch[SW_NOALLOC_SCRATCH_BYTES];
+static char *g_scratch_ptr[SW_NOALLOC_MAX_DEV];
+
+static int noalloc_setup(int dev) {
+    if (dev < 0 || dev >= SW_NOALLOC_MAX_DEV) return fail_msg("device index beyond the static scratch table");
+    if (g_scratch_ptr[dev]) return 0;
+    void *p = nullptr;
+    CK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "static scratch address");
+    g_scratch_ptr[dev] = (char *)p;
+    return 0;
+}
+
+extern "C" int lag_hip_moe_forward_noalloc(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const float *x, float *out,
+                                           int S) {
+    if (!g_ok || g_dev < 0 || g_dev >= SW_NOALLOC_MAX_DEV || !g_scratch_ptr[g_dev])
+        return fail_msg("moe_forward_noalloc: backend not initialised");
+    const int prof = g_prof;
+    g_prof = 0;                                  // the per-launch timing pool allocates events
+    const int rc = forward(d, w, x, out, S, ScratchSrc{g_scratch_ptr[g_dev], SW_NOALLOC_SCRATCH_BYTES});
+    g_prof = prof;
+    return rc;
 }
 
 // ------------------------------------------------------------ stack glue ----
