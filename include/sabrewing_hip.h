@@ -57,6 +57,24 @@ int    lag_hip_moe_group(float *acc, const float *x, const void *gu_q, const flo
                          const int *gcnt, int G, const int *grow, const int *rowof, const float *w,
                          int S, int K, int I, int D);
 
+/* lag_cuda_matmul_q8 (:36): int8 weights [O,I] followed in the same buffer by
+ * their f32 row scales [O] (c/backend_cuda_laguna.cu:125-126) */
+int    lag_hip_matmul_q8(float *y, const float *x, const void *W, int S, int I, int O);
+/* ink_cuda_matmul_q8 (c/backend_cuda_ink.h:27-28): the same with the scales in
+ * their own buffer */
+int    lag_hip_matmul_q8_s(float *y, const float *x, const void *q8, const void *scale, int S, int I, int O);
+/* ink_cuda_matmul_bf16 (c/backend_cuda_ink.h:17-18): activations rounded to bf16
+ * (c/backend_cuda_ink.cu:63-64), in the lane order of the CPU's matmul_h
+ * (c/moe_matmul.h:66-89, vdpbf16ps); I % 32 != 0 takes the f32-activation
+ * contract, as the CPU does */
+int    lag_hip_matmul_bf16_rx(float *y, const float *x, const void *W, int S, int I, int O);
+/* Numerics of the host-activation matmuls: calls of up to 64 rows reproduce the
+ * reference CPU's SIMD contracts bit for bit -- matmul_bf16 the 16 f32-activation
+ * lanes of c/moe_matmul.h:92-110, matmul_q4 (per-row scales) matmul_q4_k's F32
+ * lanes (c/moe_quant.h:85-109), matmul_q8 matmul_q8_k's F32 lanes
+ * (c/moe_quant.h:378-391), matmul_bf16_rx the vdpbf16ps lanes; larger calls of
+ * matmul_bf16 / matmul_q4 run on the MFMA GEMMs (within 1e-5 relative). */
+
 /* ---------------- 2. group-scaled int4 forms (scale[o*ng + g], ng = I/gs) ---------------- */
 int    lag_hip_matmul_q4_g(float *y, const float *x, const void *packed, const void *scale,
                            int S, int I, int O, int gs);

@@ -10,8 +10,11 @@
  * every table slot must resolve or the library is unloaded again, and while
  * the backend is unavailable every wrapper returns the "not initialised"
  * value (-1 / NULL / 0), so the engine keeps its CPU path.  Entries with no
- * MI355X counterpart (int8 residents, fp4 experts) always return -1.
- * An engine links this object in place of backend_cuda_laguna.o. */
+ * MI355X counterpart (the fp4 experts) always return -1.  The Inkling
+ * engine's ink_cuda_* table (c/backend_cuda_ink.h:14-34) is exported too, with
+ * its own all-or-nothing resolution.
+ * An engine links this object in place of backend_cuda_laguna.o (or
+ * backend_cuda_ink.o). */
 #ifndef SABREWING_LOADER_H
 #define SABREWING_LOADER_H
 #include <stddef.h>
@@ -39,6 +42,22 @@ int    lag_cuda_matmul_fp4(float *y, const float *x, const void *packed, const v
 int    lag_cuda_moe_experts_fp4(float *out, const float *x, const void *gu_q, const void *gu_es,
                                 const void *dn_q, const void *dn_es, const int *sel, const float *w, int K,
                                 int I, int D, float limit);
+
+/* The Inkling engine's table (c/backend_cuda_ink.h:14-34, 0 ok / -1 fail), each
+ * slot forwarded to its lag_hip_* entry: init, memory and upload as the lag
+ * family's; matmul_bf16 rounds the activations to bf16 (c/backend_cuda_ink.cu:63-64)
+ * -- lag_hip_matmul_bf16_rx, the CPU's matmul_h lane order; matmul_q4 and
+ * expert_q4 the lag family's per-row int4; matmul_q8 int8 weights with their
+ * row scales in a separate buffer (lag_hip_matmul_q8_s). */
+int    ink_cuda_init(int dev);
+size_t ink_cuda_free_bytes(void);
+size_t ink_cuda_total_bytes(void);
+void  *ink_cuda_upload(const void *h, size_t n);
+int    ink_cuda_matmul_bf16(float *y, const float *x, const void *W, int S, int I, int O);
+int    ink_cuda_matmul_q4(float *y, const float *x, const void *packed, const void *scale, int S, int I, int O);
+int    ink_cuda_matmul_q8(float *y, const float *x, const void *q8, const void *scale, int S, int I, int O);
+int    ink_cuda_expert_q4(float *out, const float *x, const void *p13, const void *s13,
+                          const void *p2, const void *s2, int I, int D);
 
 /* The GLM engine's table (c/backend_cuda.h:28-169, 1 ok / 0 fail), the slots of
  * the reference's Windows loader (c/backend_loader.c:99-150), each forwarded to
@@ -96,6 +115,8 @@ int coli_cuda_pipe_router(int device, const float *x_dev, const void *rw_dev, co
 int    sabrewing_loader_available(void);
 /* the same for the coli slots */
 int    sabrewing_loader_coli_available(void);
+/* the same for the ink slots */
+int    sabrewing_loader_ink_available(void);
 /* the absolute path tried (or "" before the first attempt) */
 const char *sabrewing_loader_path(void);
 

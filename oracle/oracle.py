@@ -13,6 +13,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 F32P = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
 U8P = np.ctypeslib.ndpointer(np.uint8, flags="C_CONTIGUOUS")
 U16P = np.ctypeslib.ndpointer(np.uint16, flags="C_CONTIGUOUS")
+I8P = np.ctypeslib.ndpointer(np.int8, flags="C_CONTIGUOUS")
 I32P = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
 
 ROUTE_SIGMOID, ROUTE_SOFTMAX, ROUTE_SOFTPLUS = 0, 1, 2
@@ -56,6 +57,9 @@ class Oracle:
         L.sw_matmul_f32.argtypes = [F32P, F32P, F32P] + [C.c_int] * 4
         L.sw_matmul_bf16.argtypes = [F32P, F32P, U16P] + [C.c_int] * 4
         L.sw_matmul_q4.argtypes = [F32P, F32P, U8P, F32P] + [C.c_int] * 5
+        L.sw_matmul_bf16_rx.argtypes = [F32P, F32P, U16P] + [C.c_int] * 3
+        L.sw_f32_to_bf16_ne.restype = C.c_uint16; L.sw_f32_to_bf16_ne.argtypes = [C.c_float]
+        L.sw_matmul_q8.argtypes = [F32P, F32P, I8P, F32P] + [C.c_int] * 4
         L.sw_matmul_i4_grouped.argtypes = [F32P, F32P, U8P, F32P] + [C.c_int] * 4
         for f in ("sw_siluf", "sw_softplusf", "sw_sigmoidf"):
             getattr(L, f).restype = C.c_float; getattr(L, f).argtypes = [C.c_float]
@@ -124,6 +128,20 @@ class Oracle:
         S, I = x.shape; O = Wb.shape[0]
         y = np.empty((S, O), np.float32)
         self.lib.sw_matmul_bf16(y, np.ascontiguousarray(x), np.ascontiguousarray(Wb), S, I, O, exact)
+        return y
+
+    def matmul_bf16_rx(self, x, Wb):
+        """bf16 weights against bf16-rounded activations (the vdpbf16ps contract)"""
+        S, I = x.shape; O = Wb.shape[0]
+        y = np.empty((S, O), np.float32)
+        self.lib.sw_matmul_bf16_rx(y, np.ascontiguousarray(x, np.float32), np.ascontiguousarray(Wb), S, I, O)
+        return y
+
+    def matmul_q8(self, x, q, s, mode=0):
+        S, I = x.shape; O = q.shape[0]
+        y = np.empty((S, O), np.float32)
+        self.lib.sw_matmul_q8(y, np.ascontiguousarray(x, np.float32), np.ascontiguousarray(q, np.int8),
+                              np.ascontiguousarray(s, np.float32), S, I, O, mode)
         return y
 
     def matmul_q4(self, x, p, s, mode=0, exact=0):
@@ -337,6 +355,7 @@ class Ref:
         L.ref_matmul_f32.argtypes = [F32P, F32P, F32P] + [C.c_int] * 4
         L.ref_matmul_bf16.argtypes = [F32P, F32P, U16P] + [C.c_int] * 5
         L.ref_matmul_q4_kb.argtypes = [F32P, F32P, U8P, F32P] + [C.c_int] * 5
+        L.ref_matmul_q8.argtypes = [F32P, F32P, I8P, F32P] + [C.c_int] * 3
         L.ref_matmul_i4_grouped.argtypes = [F32P, F32P, U8P, F32P] + [C.c_int] * 4
         L.ref_softmax_row.argtypes = [F32P, C.c_int]
         L.ref_moe_topk.argtypes = [F32P, C.c_void_p, C.c_int, C.c_int, C.c_int, I32P]
@@ -363,6 +382,15 @@ class Ref:
         S, I = x.shape; O = Wb.shape[0]
         y = np.empty((S, O), np.float32)
         self.lib.ref_matmul_bf16(y, np.ascontiguousarray(x), np.ascontiguousarray(Wb), S, I, O, round_x, exact)
+        return y
+
+    def matmul_q8(self, x, q, s, mode=0):
+        """matmul_q8_k, one row of x at a time (the reference kernel is single-row)"""
+        S, I = x.shape; O = q.shape[0]
+        y = np.empty((S, O), np.float32)
+        for r in range(S):
+            self.lib.ref_matmul_q8(y[r], np.ascontiguousarray(x[r], np.float32), np.ascontiguousarray(q, np.int8),
+                                   np.ascontiguousarray(s, np.float32), I, O, mode)
         return y
 
     def matmul_q4(self, x, p, s, mode=0, exact=0):

@@ -20,6 +20,7 @@
 
 void ref_matmul_f32(float *y, const float *x, const float *W, int S, int I, int O, int exact) { matmul_f32(y, x, W, S, I, O, exact); }
 void ref_matmul_bf16(float *y, const float *x, const uint16_t *W, int S, int I, int O, int round_x, int exact) { matmul_bf16_k(y, x, W, S, I, O, round_x, exact); }
+void ref_matmul_q8(float *y, const float *x, const int8_t *q, const float *s, int I, int O, int mode) { matmul_q8_k(y, x, q, s, I, O, mode, 0); }
 void ref_matmul_q4_kb(float *y, const float *x, const uint8_t *p, const float *s, int S, int I, int O, int mode, int exact) { matmul_q4_kb(y, x, p, s, S, I, O, mode, exact); }
 void ref_matmul_i4_grouped(float *y, const float *x, const uint8_t *p, const float *s, int S, int I, int O, int gs) { matmul_i4_grouped(y, x, p, s, S, I, O, gs); }
 void ref_softmax_row(float *x, int n) { softmax_row(x, n); }

@@ -305,6 +305,107 @@ void sw_matmul_bf16(float *y, const float *x, const uint16_t *W, int S, int I, i
     }
 }
 
+/* ---- the bf16 activation contract (round_x = 1) ----
+ * c/moe_matmul.h:64-90 on an AVX512-BF16 host, inkling's matmul_h
+ * (c/inkling.c:166-169): every activation rounded to bf16 by vcvtne2ps2bf16,
+ * then per row 16 lanes, lane j taking the bf16 pair (2j, 2j+1) of each
+ * 32-column chunk through vdpbf16ps -- two FMAs in a row, the odd column
+ * first, each with denormal inputs read as zero and a denormal result
+ * flushed to zero (Intel SDM, VDPBF16PS) -- then _mm512_reduce_add_ps.
+ * With I % 32 != 0 the reference takes its f32-activation path instead. */
+static float daz(float v) {
+    uint32_t u; memcpy(&u, &v, 4);
+    if ((u & 0x7F800000u) == 0 && (u & 0x007FFFFFu)) { u &= 0x80000000u; memcpy(&v, &u, 4); }
+    return v;
+}
+/* vcvtne2ps2bf16 of one float: NaN quieted, denormal to a signed zero, else RNE */
+uint16_t sw_f32_to_bf16_ne(float f) {
+    uint32_t u; memcpy(&u, &f, 4);
+    if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x007FFFFFu)) return (uint16_t)((u >> 16) | 0x40);
+    if ((u & 0x7F800000u) == 0) return (uint16_t)((u >> 16) & 0x8000);
+    u += 0x7FFF + ((u >> 16) & 1);
+    return (uint16_t)(u >> 16);
+}
+static float dp_step(float acc, float a, float b) { return daz(fmaf(daz(a), daz(b), daz(acc))); }
+
+void sw_matmul_bf16_rx(float *y, const float *x, const uint16_t *W, int S, int I, int O) {
+    if (I % 32) { sw_matmul_bf16(y, x, W, S, I, O, 0); return; }
+    float *xb = (float *)malloc((size_t)S * I * 4);
+    for (int64_t k = 0; k < (int64_t)S * I; k++) xb[k] = sw_bf16_to_f32(sw_f32_to_bf16_ne(x[k]));
+    #pragma omp parallel for schedule(static) if((int64_t)S * O >= 512)
+    for (int o = 0; o < O; o++) {
+        const uint16_t *w = W + (int64_t)o * I;
+        for (int s = 0; s < S; s++) {
+            const float *xs = xb + (int64_t)s * I;
+            float ln[16] = {0};
+            for (int c = 0; c < I; c += 32)
+                for (int j = 0; j < 16; j++) {
+                    ln[j] = dp_step(ln[j], xs[c + 2 * j + 1], sw_bf16_to_f32(w[c + 2 * j + 1]));
+                    ln[j] = dp_step(ln[j], xs[c + 2 * j], sw_bf16_to_f32(w[c + 2 * j]));
+                }
+            y[(int64_t)s * O + o] = reduce16(ln);
+        }
+    }
+    free(xb);
+}
+
+/* int8 weights [O,I] with f32 row scales, c/moe_quant.h:346-400 (matmul_q8_k),
+ * each of the S rows of x on its own.  F32: 16 lanes fmaf(x, (float)w) over
+ * i = j mod 16, reduce16, the scalar tail fused, * scale.  IDOT: x to int8 per
+ * 32-block (amax/127, lrintf), exact int dot per block, acc = fma(xs_b, dot,
+ * acc) in block order, * scale (I % 32 == 0, I <= 8192).  An IDOT call of
+ * another shape takes the scalar route: a double sum, (float)(sum * scale). */
+void sw_matmul_q8(float *y, const float *x, const int8_t *q, const float *scale, int S, int I, int O, int mode) {
+    if (mode == SW_Q4_IDOT && !(I % 32 == 0 && I <= 8192)) {
+        for (int o = 0; o < O; o++)
+            for (int s = 0; s < S; s++) {
+                const int8_t *w = q + (int64_t)o * I; const float *xs = x + (int64_t)s * I;
+                double sm = 0; for (int i = 0; i < I; i++) sm += (double)xs[i] * w[i];
+                y[(int64_t)s * O + o] = (float)(sm * scale[o]);
+            }
+        return;
+    }
+    if (mode == SW_Q4_IDOT && I % 32 == 0 && I <= 8192) {
+        const int nb = I / 32;
+        for (int s = 0; s < S; s++) {
+            const float *xr = x + (int64_t)s * I;
+            int8_t xi[8192]; float xsb[256];
+            for (int b = 0; b < nb; b++) {
+                float am = 0.f; for (int i = 0; i < 32; i++) { float a = fabsf(xr[b * 32 + i]); if (a > am) am = a; }
+                float sc = am / 127.f; if (sc < 1e-12f) sc = 1e-12f;
+                xsb[b] = sc; float inv = 1.f / sc;
+                for (int i = 0; i < 32; i++) xi[b * 32 + i] = (int8_t)lrintf(xr[b * 32 + i] * inv);
+            }
+            #pragma omp parallel for schedule(static)
+            for (int o = 0; o < O; o++) {
+                const int8_t *w = q + (int64_t)o * I;
+                float acc = 0.f;
+                for (int b = 0; b < nb; b++) {
+                    int dot = 0;
+                    for (int i = 0; i < 32; i++) dot += (int)xi[b * 32 + i] * (int)w[b * 32 + i];
+                    acc = fmaf(xsb[b], (float)dot, acc);
+                }
+                y[(int64_t)s * O + o] = acc * scale[o];
+            }
+        }
+        return;
+    }
+    #pragma omp parallel for schedule(static) if((int64_t)S * O >= 512)
+    for (int o = 0; o < O; o++) {
+        const int8_t *w = q + (int64_t)o * I;
+        for (int s = 0; s < S; s++) {
+            const float *xs = x + (int64_t)s * I;
+            float ln[16] = {0};
+            int i = 0;
+            for (; i + 16 <= I; i += 16)
+                for (int j = 0; j < 16; j++) ln[j] = fmaf(xs[i + j], (float)w[i + j], ln[j]);
+            float sm = reduce16(ln);
+            for (; i < I; i++) sm = fmaf(xs[i], (float)w[i], sm);
+            y[(int64_t)s * O + o] = sm * scale[o];
+        }
+    }
+}
+
 static inline int nib_at(const uint8_t *p, int col) {
     uint8_t b = p[col >> 1];
     return (col & 1) ? (b >> 4) : (b & 0xF);

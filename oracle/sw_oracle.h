@@ -55,7 +55,12 @@ void sw_matmul_f32(float *y, const float *x, const float *W, int S, int I, int O
 void sw_glm_logits(const float *x, const float *W, const float *bias, int D, int E, float *logit, float *choice);
 void sw_glm_matmul(float *y, const float *x, const float *W, int S, int I, int O);
 void sw_matmul_bf16(float *y, const float *x, const uint16_t *W, int S, int I, int O, int exact);
+/* bf16 weights against bf16-rounded activations (inkling's matmul_h contract) */
+void sw_matmul_bf16_rx(float *y, const float *x, const uint16_t *W, int S, int I, int O);
+uint16_t sw_f32_to_bf16_ne(float f);
 enum { SW_Q4_F32 = 0, SW_Q4_IDOT = 1 };
+/* int8 weights + f32 row scales (mode SW_Q4_F32 / SW_Q4_IDOT: the same two contracts) */
+void sw_matmul_q8(float *y, const float *x, const int8_t *q, const float *scale, int S, int I, int O, int mode);
 void sw_matmul_q4(float *y, const float *x, const uint8_t *packed, const float *scale,
                   int S, int I, int O, int mode, int exact);
 void sw_matmul_i4_grouped(float *y, const float *x, const uint8_t *q4, const float *scale,

@@ -24,6 +24,7 @@ VP = C.c_void_p
 EXPORTS = [
     "lag_hip_init", "lag_hip_free_bytes", "lag_hip_total_bytes", "lag_hip_upload", "lag_hip_free",
     "lag_hip_matmul_bf16", "lag_hip_matmul_q4", "lag_hip_expert_q4", "lag_hip_moe_experts", "lag_hip_moe_group",
+    "lag_hip_matmul_q8", "lag_hip_matmul_q8_s", "lag_hip_matmul_bf16_rx",
     "lag_hip_matmul_q4_g", "lag_hip_expert_q4_g", "lag_hip_moe_experts_g", "lag_hip_moe_group_g",
     "lag_hip_router_upload", "lag_hip_router_chain", "lag_hip_moe_forward", "lag_hip_moe_forward_noalloc",
     "lag_hip_moe_block", "lag_hip_route",
@@ -40,6 +41,11 @@ LOADER_EXPORTS = [
     "lag_cuda_matmul_bf16", "lag_cuda_matmul_q8", "lag_cuda_matmul_q4", "lag_cuda_expert_q4",
     "lag_cuda_moe_experts", "lag_cuda_moe_group", "lag_cuda_matmul_fp4", "lag_cuda_moe_experts_fp4",
     "sabrewing_loader_available", "sabrewing_loader_path",
+]
+# the Inkling engine's table (c/backend_cuda_ink.h:14-34), exported by the loader
+INK_EXPORTS = [
+    "ink_cuda_init", "ink_cuda_free_bytes", "ink_cuda_total_bytes", "ink_cuda_upload", "ink_cuda_matmul_bf16",
+    "ink_cuda_matmul_q4", "ink_cuda_matmul_q8", "ink_cuda_expert_q4", "sabrewing_loader_ink_available",
 ]
 
 
@@ -88,6 +94,9 @@ def load_library(path=None):
     L.lag_hip_matmul_q4_g.argtypes = [F32P, F32P, VP, VP, C.c_int, C.c_int, C.c_int, C.c_int]
     L.lag_hip_expert_q4.argtypes = [F32P, F32P, VP, VP, VP, VP, C.c_int, C.c_int]
     L.lag_hip_expert_q4_g.argtypes = [F32P, F32P, VP, VP, VP, VP, C.c_int, C.c_int, C.c_int]
+    L.lag_hip_matmul_q8.argtypes = [F32P, F32P, VP, C.c_int, C.c_int, C.c_int]
+    L.lag_hip_matmul_q8_s.argtypes = [F32P, F32P, VP, VP, C.c_int, C.c_int, C.c_int]
+    L.lag_hip_matmul_bf16_rx.argtypes = [F32P, F32P, VP, C.c_int, C.c_int, C.c_int]
     L.lag_hip_moe_experts.argtypes = [F32P, F32P, VP, VP, VP, VP, I32P, F32P, C.c_int, C.c_int, C.c_int]
     L.lag_hip_moe_experts_g.argtypes = [F32P, F32P, VP, VP, VP, VP, I32P, F32P, C.c_int, C.c_int, C.c_int, C.c_int]
     L.lag_hip_moe_group.argtypes = [F32P, F32P, VP, VP, VP, VP, I32P, I32P, I32P, C.c_int, I32P, I32P, F32P,
@@ -181,6 +190,18 @@ class Backend:
         x = np.ascontiguousarray(x, np.float32); S, I = x.shape
         y = np.empty((S, O), np.float32)
         self.check(self.lib.lag_hip_matmul_bf16(y, x, VP(int(W)), S, I, O), "lag_hip_matmul_bf16")
+        return y
+
+    def matmul_bf16_rx(self, x, W, O):
+        x = np.ascontiguousarray(x, np.float32); S, I = x.shape
+        y = np.empty((S, O), np.float32)
+        self.check(self.lib.lag_hip_matmul_bf16_rx(y, x, VP(int(W)), S, I, O), "lag_hip_matmul_bf16_rx")
+        return y
+
+    def matmul_q8(self, x, q, s, O):
+        x = np.ascontiguousarray(x, np.float32); S, I = x.shape
+        y = np.empty((S, O), np.float32)
+        self.check(self.lib.lag_hip_matmul_q8_s(y, x, VP(int(q)), VP(int(s)), S, I, O), "lag_hip_matmul_q8_s")
         return y
 
     def matmul_q4(self, x, p, s, O, gs=0):

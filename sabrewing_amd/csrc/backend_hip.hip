@@ -366,8 +366,48 @@ extern "C" int lag_hip_expert_q4(float *out, const float *x, const void *p13, co
     return lag_hip_expert_q4_g(out, x, p13, s13, p2, s2, I, D, 0);
 }
 
+// The reference CPU's 16-lane GEMV contracts, bit for bit (k_lanes.hip): host
+// x and y, device weights.  Every row of every call takes them, so a token's
+// result does not depend on how many rows share its call (an engine's
+// per-token and chunked paths agree bit for bit, as on the CPU).
+static int lanes_host(float *y, const float *x, const void *W, int wkind, int dp, const void *scale, int S, int I, int O,
+                      int gs = 0) {
+    if (!g_ok || fault_injected()) return -1;
+    if (S <= 0 || I <= 0 || O <= 0 || !W) return -1;
+    Carve cv;
+    const size_t o_x = cv.take((size_t)S * I * 4), o_y = cv.take((size_t)S * O * 4);
+    if (grow_dev(g_arena, cv.off) || grow_pinned(g_hin, (size_t)S * I * 4) || grow_pinned(g_hout, (size_t)S * O * 4)) return -1;
+    char *A = (char *)g_arena.p;
+    memcpy(g_hin.p, x, (size_t)S * I * 4);
+    CK(hipMemcpyAsync(A + o_x, g_hin.p, (size_t)S * I * 4, hipMemcpyHostToDevice, g_st), "x upload");
+    { PROF("lanes16");
+      if (sw_launch_lanes16(g_st, W, wkind, dp, (const float *)scale, (const float *)(A + o_x), S, I, O, (float *)(A + o_y), gs))
+          return fail_msg("lanes launch (shape unsupported?)"); }
+    CK(hipMemcpyAsync(g_hout.p, A + o_y, (size_t)S * O * 4, hipMemcpyDeviceToHost, g_st), "result download");
+    CK(hipStreamSynchronize(g_st), "stream sync");
+    memcpy(y, g_hout.p, (size_t)S * O * 4);
+    if (g_prof) prof_flush();
+    return 0;
+}
+
+extern "C" int lag_hip_matmul_bf16_rx(float *y, const float *x, const void *W, int S, int I, int O) {
+    return lanes_host(y, x, W, 0, I % 32 == 0, nullptr, S, I, O);
+}
+extern "C" int lag_hip_matmul_q8_s(float *y, const float *x, const void *q8, const void *scale, int S, int I, int O) {
+    if (!scale) return -1;
+    return lanes_host(y, x, q8, 1, 0, scale, S, I, O);
+}
+extern "C" int lag_hip_matmul_q8(float *y, const float *x, const void *W, int S, int I, int O) {
+    if (!W) return -1;
+    return lag_hip_matmul_q8_s(y, x, W, (const char *)W + (size_t)I * O, S, I, O);
+}
+
 extern "C" int lag_hip_matmul_q4_g(float *y, const float *x, const void *packed, const void *scale,
                                    int S, int I, int O, int gs) {
+    if (gs <= 0 && !(I & 1)) return lanes_host(y, x, packed, 2, 0, scale, S, I, O);
+    // group scales: matmul_i4_grouped's lanes, the scales applied in f32 per group
+    if (gs >= 16 && gs % 16 == 0 && gs <= 256 && 256 % gs == 0 && I % gs == 0)
+        return lanes_host(y, x, packed, 3, 0, scale, S, I, O, gs);
     if (!g_ok || fault_injected()) return -1;
     if (S <= 0 || I <= 0 || O <= 0) return -1;
     Carve cv;
@@ -396,21 +436,7 @@ extern "C" int lag_hip_matmul_q4(float *y, const float *x, const void *packed, c
 }
 
 extern "C" int lag_hip_matmul_bf16(float *y, const float *x, const void *W, int S, int I, int O) {
-    if (!g_ok || fault_injected() || (I & 1)) return -1;
-    if (S <= 0 || I <= 0 || O <= 0) return -1;
-    Carve cv;
-    const size_t o_x = cv.take((size_t)S * I * 4), o_y = cv.take((size_t)S * O * 4);
-    if (grow_dev(g_arena, cv.off) || grow_pinned(g_hin, (size_t)S * I * 4) || grow_pinned(g_hout, (size_t)S * O * 4)) return -1;
-    char *A = (char *)g_arena.p;
-    memcpy(g_hin.p, x, (size_t)S * I * 4);
-    CK(hipMemcpyAsync(A + o_x, g_hin.p, (size_t)S * I * 4, hipMemcpyHostToDevice, g_st), "x upload");
-    SwBf16 Wt = {(const uint16_t *)W, O, I};
-    { PROF("bf16_rows"); if (sw_launch_bf16_rows_x(g_st, Wt, (const float *)(A + o_x), S, (float *)(A + o_y))) return fail_msg("bf16 launch (shape unsupported?)"); }
-    CK(hipMemcpyAsync(g_hout.p, A + o_y, (size_t)S * O * 4, hipMemcpyDeviceToHost, g_st), "result download");
-    CK(hipStreamSynchronize(g_st), "stream sync");
-    memcpy(y, g_hout.p, (size_t)S * O * 4);
-    if (g_prof) prof_flush();
-    return 0;
+    return lanes_host(y, x, W, 0, 0, nullptr, S, I, O);
 }
 
 // ------------------------------------------------------------ device MoE block ----

@@ -36,6 +36,7 @@ static struct {
     fn_free free_;
     fn_mm_bf16 matmul_bf16;
     fn_mm_q4 matmul_q4;
+    fn_mm_bf16 matmul_q8;
     fn_expert expert_q4;
     fn_experts moe_experts;
     fn_group moe_group;
@@ -75,6 +76,7 @@ static void load_once(void) {
         RESOLVE(free_, "lag_hip_free");
         RESOLVE(matmul_bf16, "lag_hip_matmul_bf16");
         RESOLVE(matmul_q4, "lag_hip_matmul_q4");
+        RESOLVE(matmul_q8, "lag_hip_matmul_q8");
         RESOLVE(expert_q4, "lag_hip_expert_q4");
         RESOLVE(moe_experts, "lag_hip_moe_experts");
         RESOLVE(moe_group, "lag_hip_moe_group");
@@ -100,7 +102,7 @@ int lag_cuda_matmul_bf16(float *y, const float *x, const void *W, int S, int I, 
     load_once(); return T.available ? T.matmul_bf16(y, x, W, S, I, O) : -1;
 }
 int lag_cuda_matmul_q8(float *y, const float *x, const void *W, int S, int I, int O) {
-    (void)y; (void)x; (void)W; (void)S; (void)I; (void)O; return -1;          /* int8 residents: CPU path */
+    load_once(); return T.available ? T.matmul_q8(y, x, W, S, I, O) : -1;
 }
 int lag_cuda_matmul_q4(float *y, const float *x, const void *packed, const void *scale, int S, int I, int O) {
     load_once(); return T.available ? T.matmul_q4(y, x, packed, scale, S, I, O) : -1;
@@ -125,6 +127,75 @@ int lag_cuda_moe_experts_fp4(float *out, const float *x, const void *gu_q, const
                              const void *dn_es, const int *sel, const float *w, int K, int I, int D, float limit) {
     (void)out; (void)x; (void)gu_q; (void)gu_es; (void)dn_q; (void)dn_es; (void)sel; (void)w; (void)K; (void)I;
     (void)D; (void)limit; return -1;
+}
+
+/* ---- the Inkling family (c/backend_cuda_ink.h:14-34): its own table over the
+ * same library, all of its eight slots or none; -1 / NULL / 0 while unavailable.
+ * The same device and stream as the lag family (one backend per process). ---- */
+typedef int (*fn_mm_q8s)(float *, const float *, const void *, const void *, int, int, int);
+static struct {
+    int loaded, available;
+    void *lib;
+    fn_init init;
+    fn_bytes free_bytes, total_bytes;
+    fn_upload upload;
+    fn_mm_bf16 matmul_bf16_rx;
+    fn_mm_q4 matmul_q4;
+    fn_mm_q8s matmul_q8_s;
+    fn_expert expert_q4;
+} K;
+
+#define RESOLVE_K(field, name)                                     \
+    do {                                                           \
+        *(void **)(&K.field) = dlsym(K.lib, name);                 \
+        if (!K.field) { missing = name; goto unload; }             \
+    } while (0)
+
+static void ink_load_once(void) {
+    if (K.loaded) return;
+    K.loaded = 1;
+    if (!T.path[0]) resolve_path();
+    if (!T.path[0]) return;
+    K.lib = dlopen(T.path, RTLD_NOW | RTLD_LOCAL);
+    if (!K.lib) return;
+    {
+        const char *missing = NULL;
+        RESOLVE_K(init, "lag_hip_init");
+        RESOLVE_K(free_bytes, "lag_hip_free_bytes");
+        RESOLVE_K(total_bytes, "lag_hip_total_bytes");
+        RESOLVE_K(upload, "lag_hip_upload");
+        RESOLVE_K(matmul_bf16_rx, "lag_hip_matmul_bf16_rx");
+        RESOLVE_K(matmul_q4, "lag_hip_matmul_q4");
+        RESOLVE_K(matmul_q8_s, "lag_hip_matmul_q8_s");
+        RESOLVE_K(expert_q4, "lag_hip_expert_q4");
+        K.available = 1;
+        return;
+    unload:
+        fprintf(stderr, "[sabrewing-loader] %s: missing symbol %s; inkling backend unavailable\n", T.path, missing);
+        dlclose(K.lib);
+        memset(&K.init, 0, sizeof K - ((char *)&K.init - (char *)&K));
+        K.lib = NULL;
+    }
+}
+
+int sabrewing_loader_ink_available(void) { ink_load_once(); return K.available; }
+int ink_cuda_init(int dev) { ink_load_once(); return K.available ? K.init(dev) : -1; }
+size_t ink_cuda_free_bytes(void) { ink_load_once(); return K.available ? K.free_bytes() : 0; }
+size_t ink_cuda_total_bytes(void) { ink_load_once(); return K.available ? K.total_bytes() : 0; }
+void *ink_cuda_upload(const void *h, size_t n) { ink_load_once(); return K.available ? K.upload(h, n) : NULL; }
+/* bf16 weights against bf16-rounded activations (c/backend_cuda_ink.cu:63-64; the CPU's matmul_h) */
+int ink_cuda_matmul_bf16(float *y, const float *x, const void *W, int S, int I, int O) {
+    ink_load_once(); return K.available ? K.matmul_bf16_rx(y, x, W, S, I, O) : -1;
+}
+int ink_cuda_matmul_q4(float *y, const float *x, const void *packed, const void *scale, int S, int I, int O) {
+    ink_load_once(); return K.available ? K.matmul_q4(y, x, packed, scale, S, I, O) : -1;
+}
+int ink_cuda_matmul_q8(float *y, const float *x, const void *q8, const void *scale, int S, int I, int O) {
+    ink_load_once(); return K.available ? K.matmul_q8_s(y, x, q8, scale, S, I, O) : -1;
+}
+int ink_cuda_expert_q4(float *out, const float *x, const void *p13, const void *s13, const void *p2, const void *s2,
+                       int I, int D) {
+    ink_load_once(); return K.available ? K.expert_q4(out, x, p13, s13, p2, s2, I, D) : -1;
 }
 
 /* ---- the coli family (c/backend_loader.c:99-512): its own table over the same

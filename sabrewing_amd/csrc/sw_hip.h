@@ -216,6 +216,12 @@ int sw_launch_q4_rows_x(hipStream_t st, SwQ4 W, const float *x, SwGroups g, floa
 int sw_launch_bf16_gateup(hipStream_t st, SwBf16 Wg, SwBf16 Wu, const float *x, int S, uint16_t *hplanes);
 int sw_launch_bf16_rows(hipStream_t st, SwBf16 W, const uint16_t *planes, int S, float *Y);
 int sw_launch_bf16_rows_x(hipStream_t st, SwBf16 W, const float *x, int S, float *Y);
+// the reference CPU's 16-lane GEMV contracts (k_lanes.hip), bit for bit: wkind 0 bf16,
+// 1 int8 (+ row scale), 2 per-row int4 (+ row scale), 3 group-scaled int4 (+ scales
+// [O][I/gs], matmul_i4_grouped's lanes); dp: bf16-rounded activations through the
+// vdpbf16ps lane order
+int sw_launch_lanes16(hipStream_t st, const void *W, int wkind, int dp, const float *scale, const float *x, int S,
+                      int I, int O, float *y, int gs);
 // activation limbs for the dot8 GEMV (k_dot8.hip): rows x[rows, K] f32 ->
 // xl[rows][K/32][SW_NL] (32 signed nibbles each), xs[rows][K/32] f32
 #define SW_NL 7

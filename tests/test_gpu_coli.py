@@ -260,9 +260,10 @@ def test_matmul_and_pipe_gemm(coli, be, orc, gs):
     t = coli.upload(g, gsc, D, I, 0, gs)
     x = np.random.default_rng(6).standard_normal((5, D)).astype(np.float32)
     y = coli.matmul(t, x)
-    pg, ps = be.upload(np.ascontiguousarray(g)), be.upload(np.ascontiguousarray(gsc))
-    assert np.array_equal(bits(y), bits(be.matmul_q4(x, pg, ps, I, gs)))
-    pg.free(); ps.free()
+    # the GLM engine's int4 matmul has no single CPU contract (its IDOT and f32 routes
+    # are chosen at run time): the MFMA GEMM is held to the f32 route within its bound
+    want = orc.matmul_i4_grouped(x, g, gsc, gs) if gs else orc.matmul_q4(x, g, gsc)
+    assert normwise(y, want) < (1e-5 if gs == 0 else 1e-3)
     xd, yd = coli.dev_put(x), coli.f.pipe_alloc(0, 5 * I * 4)
     assert coli.f.pipe_gemm(t.ptr, yd, xd, 5)
     assert np.array_equal(bits(coli.dev_get(yd, (5, I))), bits(y))

@@ -33,6 +33,27 @@ def test_reference_engine_cuda_selftest():
     assert any("BIT-IDENTICAL" in l for l in lines)
 
 
+INKLING = os.path.join(ROOT, "oracle", "_ref", "inkling_hip")
+
+
+def test_reference_inkling_cuda_q4_test(tmp_path):
+    """The Inkling engine (c/inkling.c built with -DCOLI_CUDA against the loader's
+    ink_cuda_* table) and its own --cuda-q4-test (c/inkling.c:1789-1862): int4
+    GEMM, int8 GEMM and the fused int4 expert at 6144 x 6144 against its CPU
+    kernels, each to a scaled error below 1e-3.  IDOT=0 selects the CPU's f32
+    activation route, the reference run the test's own comment names."""
+    if not os.path.exists(INKLING):
+        pytest.skip("inkling engine binary not built (make -C oracle ref, with the reference sources present)")
+    env = dict(os.environ, SNAP=str(tmp_path), IDOT="0", OMP_NUM_THREADS=os.environ.get("OMP_NUM_THREADS", "8"))
+    r = subprocess.run([INKLING, "--cuda-q4-test"], env=env, stdout=subprocess.PIPE, stderr=subprocess.STDOUT,
+                       text=True, timeout=110)
+    print(r.stdout)
+    oks = [l for l in r.stdout.splitlines() if l.endswith("[OK]")]
+    assert r.returncode == 0 and len(oks) == 3, r.stdout
+    assert any(l.startswith("q4 GPU") for l in oks) and any(l.startswith("q8 GPU") for l in oks)
+    assert any(l.startswith("fused-expert GPU") for l in oks)
+
+
 @pytest.mark.parametrize("S_", [1, 5, 150])
 def test_reference_engine_moe_rows_on_device(be, orc, S_):
     """The engine's own lag_moe_rows (c/laguna.c:805-824) with a device-resident

@@ -22,8 +22,8 @@ def q4_case(orc, O, I, gs, seed):
     return p, s
 
 
-@pytest.mark.parametrize("gs", [0, 32, 64])
-@pytest.mark.parametrize("S_", [1, 3, 17])
+@pytest.mark.parametrize("gs", [0, 32, 64, 256])
+@pytest.mark.parametrize("S_", [1, 3, 17, 70])
 def test_matmul_q4(be, orc, gs, S_):
     O, I = 512, 2048
     p, s = q4_case(orc, O, I, gs, 11 + gs)
@@ -32,9 +32,9 @@ def test_matmul_q4(be, orc, gs, S_):
     dp, ds = be.upload(p), be.upload(s)
     got = be.matmul_q4(x, dp, ds, O, gs)
     dp.free(); ds.free()
-    # per-row scales keep the weights exact (f32 scale after the sum); group scales
-    # are folded into f16 weights (one rounding, 2^-11 relative)
-    assert normwise(got, want) < (1e-5 if gs == 0 else 1e-3)
+    # per-row scales: matmul_q4_k's F32 lanes; group scales: matmul_i4_grouped's lanes with
+    # the scales applied in f32 per group -- bit for bit at every S
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
 def test_nibble_kat(be):
@@ -51,17 +51,55 @@ def test_nibble_kat(be):
     assert y[0, 0] == -34.0 and y[0, 1] == -2.5 and np.all(y[0, 2:] == 0)
 
 
-@pytest.mark.parametrize("S_", [1, 4, 40])
+@pytest.mark.parametrize("S_", [1, 4, 40, 64, 65])
 def test_matmul_bf16(be, orc, S_):
+    """decode sizes (S <= 64) reproduce the CPU's 16-lane f32-activation contract bit
+    for bit, |x| up to 1e5 and tiny values included; larger calls take the MFMA GEMM"""
     O, I = 256, 1024
     rng = np.random.default_rng(3)
     Wb = orc.to_bf16((rng.standard_normal((O, I)) * 0.02).astype(np.float32))
     x = rng.standard_normal((S_, I)).astype(np.float32)
+    x[0, :8] *= 1e5
+    x[-1, 8:16] *= 1e-30
     want = orc.matmul_bf16(x, Wb)
     dW = be.upload(Wb)
     got = be.matmul_bf16(x, dW, O)
     dW.free()
-    assert normwise(got, want) < 1e-4
+    if S_ <= 64:
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    else:
+        assert normwise(got, want) < 1e-4
+
+
+@pytest.mark.parametrize("S_,I,O", [(1, 1024, 256), (5, 4096, 100), (3, 40, 17), (9, 6144, 64)])
+def test_matmul_bf16_round_x(be, orc, S_, I, O):
+    """inkling's matmul_h contract (ink_cuda_matmul_bf16): bf16-rounded activations in
+    the vdpbf16ps lane order, bit for bit, denormals and huge values included; I = 40
+    takes the f32-activation lanes, as the CPU does"""
+    rng = np.random.default_rng(I + S_)
+    Wb = orc.to_bf16((rng.standard_normal((O, I)) * 0.05).astype(np.float32))
+    Wb[0, :4] = [0x0001, 0x8003, 0x7F7F, 0x0080]
+    x = rng.standard_normal((S_, I)).astype(np.float32)
+    x[0, :5] = [1e-39, -1e-40, 3e38, np.float32(1.0000001), -0.0]
+    want = orc.matmul_bf16_rx(x, Wb)
+    dW = be.upload(Wb)
+    got = be.matmul_bf16_rx(x, dW, O)
+    dW.free()
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("S_,I,O", [(1, 6144, 64), (4, 1000, 33), (2, 40, 7)])
+def test_matmul_q8(be, orc, S_, I, O):
+    """int8 weights + row scales (lag/ink matmul_q8): matmul_q8_k's F32 lanes, bit for bit"""
+    rng = np.random.default_rng(I)
+    q = rng.integers(-127, 128, (O, I), dtype=np.int8)
+    sc = (rng.random(O) * 1e-3).astype(np.float32)
+    x = rng.standard_normal((S_, I)).astype(np.float32)
+    want = orc.matmul_q8(x, q, sc, 0)
+    dq, ds = be.upload(q), be.upload(sc)
+    got = be.matmul_q8(x, dq, ds, O)
+    dq.free(); ds.free()
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
 def layer_small(orc, gs, seed=5, E=6, D=1024, I=512):

@@ -18,7 +18,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 def header_functions(path):
     src = open(path).read()
     src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
-    return set(re.findall(r"\b((?:lag|coli)_(?:hip|cuda)_\w+|sabrewing_loader_\w+)\s*\(", src))
+    return set(re.findall(r"\b((?:lag|coli|ink)_(?:hip|cuda)_\w+|sabrewing_loader_\w+)\s*\(", src))
 
 
 def exported(path):
@@ -49,12 +49,16 @@ def test_loader_exports_header():
     from sabrewing_amd.coli import COLI_EXPORTS
     decl = header_functions(os.path.join(ROOT, "include", "sabrewing_loader.h"))
     coli = {n.replace("coli_hip_", "coli_cuda_") for n in COLI_EXPORTS}
-    assert decl == set(B.LOADER_EXPORTS) | coli | {"sabrewing_loader_coli_available"}
+    assert decl == set(B.LOADER_EXPORTS) | coli | {"sabrewing_loader_coli_available"} | set(B.INK_EXPORTS)
     assert not decl - exported(B.LOADER_PATH)
     # the reference's own coli_cuda_* declarations (c/backend_cuda.h) are exactly these
     ref = "/root/reference/c/backend_cuda.h"
     if os.path.exists(ref):
         assert set(re.findall(r"\b(coli_cuda_\w+)\s*\(", open(ref).read())) == coli
+    # and its ink_cuda_* declarations (c/backend_cuda_ink.h) these eight
+    ref = "/root/reference/c/backend_cuda_ink.h"
+    if os.path.exists(ref):
+        assert set(re.findall(r"\b(ink_cuda_\w+)\s*\(", open(ref).read())) == set(B.INK_EXPORTS[:-1])
 
 
 LOADER_PROBE = textwrap.dedent("""
@@ -65,11 +69,16 @@ LOADER_PROBE = textwrap.dedent("""
     L.lag_cuda_free_bytes.restype = C.c_size_t
     L.coli_cuda_expert_group_take.restype = C.c_void_p
     L.coli_cuda_pipe_alloc.restype = C.c_void_p
+    L.ink_cuda_upload.restype = C.c_void_p
+    L.ink_cuda_free_bytes.restype = C.c_size_t
     print(L.sabrewing_loader_available(), L.lag_cuda_init(0), L.lag_cuda_upload(None, 16),
           L.lag_cuda_free_bytes(), L.lag_cuda_matmul_q8(None, None, None, 1, 1, 1),
           L.sabrewing_loader_path().decode(),
           L.sabrewing_loader_coli_available(), L.coli_cuda_device_count(), L.coli_cuda_device_at(0),
-          L.coli_cuda_expert_group_take(0), L.coli_cuda_pipe_alloc(0, 16), L.coli_cuda_tensor_device(None))
+          L.coli_cuda_expert_group_take(0), L.coli_cuda_pipe_alloc(0, 16), L.coli_cuda_tensor_device(None),
+          L.sabrewing_loader_ink_available(), L.ink_cuda_init(0), L.ink_cuda_upload(None, 16),
+          L.ink_cuda_free_bytes(), L.ink_cuda_matmul_bf16(None, None, None, 1, 1, 1),
+          L.ink_cuda_matmul_q8(None, None, None, None, 1, 1, 1))
 """)
 
 
@@ -87,7 +96,9 @@ def test_loader_unavailable_sentinels(tmp_path):
     assert out[:5] == ["0", "-1", "None", "0", "-1"]
     assert out[5] == str(tmp_path / "absent.so")
     # the coli table's sentinels (c/backend_loader.c:261-512): 0 / -1 / NULL
-    assert out[6:] == ["0", "0", "-1", "None", "None", "-1"]
+    assert out[6:12] == ["0", "0", "-1", "None", "None", "-1"]
+    # the ink table's: -1 / NULL / 0
+    assert out[12:] == ["0", "-1", "None", "0", "-1", "-1"]
 
 
 def test_loader_all_or_nothing(tmp_path):
@@ -98,6 +109,7 @@ def test_loader_all_or_nothing(tmp_path):
     subprocess.run(["gcc", "-shared", "-fPIC", str(src), "-o", str(so)], check=True)
     out, err = run_probe(str(so))
     assert out[:2] == ["0", "-1"] and "missing symbol" in err
+    assert out[12:14] == ["0", "-1"] and "inkling backend unavailable" in err
 
 
 def test_loader_relative_path_refused(tmp_path):

@@ -53,6 +53,31 @@ def test_q4_rows(orc, ref, rng, S, I, O):
         assert bits_equal(orc.matmul_q4(x, p, s, mode, exact), ref.matmul_q4(x, p, s, mode, exact)), (mode, exact)
 
 
+@pytest.mark.parametrize("S,I,O", [(1, 64, 5), (3, 4096, 37), (2, 96, 7), (2, 40, 3), (1, 6144, 64)])
+def test_bf16_round_x(orc, ref, rng, S, I, O):
+    """inkling's matmul_h contract (bf16-rounded activations, vdpbf16ps lanes), with
+    denormal, huge and halfway activations and denormal / extreme bf16 weights; I = 40
+    takes the reference's f32-activation route"""
+    x = rng.standard_normal((S, I)).astype(np.float32)
+    x[0, :5] = [1e-39, -1e-40, 3e38, np.float32(1.0000001), -0.0]
+    W = orc.to_bf16((rng.standard_normal((O, I)) * 0.05).astype(np.float32))
+    W[0, :4] = [0x0001, 0x8003, 0x7F7F, 0x0080]
+    assert bits_equal(orc.matmul_bf16_rx(x, W), ref.matmul_bf16(x, W, round_x=1))
+    tiny = np.full((1, 64), 1e-20, np.float32)         # products below the normal range: flushed
+    Wt = orc.to_bf16(np.full((3, 64), 1e-20, np.float32))
+    assert bits_equal(orc.matmul_bf16_rx(tiny, Wt), ref.matmul_bf16(tiny, Wt, round_x=1))
+
+
+@pytest.mark.parametrize("S,I,O", [(1, 64, 5), (3, 4096, 37), (2, 96, 7), (2, 40, 3), (1, 6144, 64)])
+def test_q8_rows(orc, ref, rng, S, I, O):
+    """int8 weights with row scales (matmul_q8_k), both activation contracts"""
+    x = rng.standard_normal((S, I)).astype(np.float32)
+    q = rng.integers(-127, 128, (O, I), dtype=np.int8)
+    sc = (rng.random(O) * 1e-3).astype(np.float32)
+    for mode in (0, 1):
+        assert bits_equal(orc.matmul_q8(x, q, sc, mode), ref.matmul_q8(x, q, sc, mode)), mode
+
+
 def test_softmax_topk(orc, ref, rng):
     for n in (8, 64, 256):
         v = (rng.standard_normal(n) * 3).astype(np.float32)
