@@ -90,8 +90,9 @@ int    lag_hip_moe_group_g(float *acc, const float *x, const void *gu_q, const f
 
 /* ---------------- 3. device-resident MoE block ---------------- */
 enum { LAG_HIP_ROUTE_SIGMOID = 0, LAG_HIP_ROUTE_SOFTMAX = 1, LAG_HIP_ROUTE_SOFTPLUS = 2,
-       LAG_HIP_ROUTE_SOFTMAX_OLMOE = 3, LAG_HIP_ROUTE_SOFTMAX_QWEN = 4, LAG_HIP_ROUTE_SQRT_SOFTPLUS = 5 };
-enum { LAG_HIP_SHARED_NONE = 0, LAG_HIP_SHARED_UNSCALED = 1 };
+       LAG_HIP_ROUTE_SOFTMAX_OLMOE = 3, LAG_HIP_ROUTE_SOFTMAX_QWEN = 4, LAG_HIP_ROUTE_SQRT_SOFTPLUS = 5,
+       LAG_HIP_ROUTE_INKLING = 6 };
+enum { LAG_HIP_SHARED_NONE = 0, LAG_HIP_SHARED_UNSCALED = 1, LAG_HIP_SHARED_GATED = 3 };
 
 /* MoeDesc (c/moe_arch.h:33-41) plus the layer shape.  route_act: SIGMOID and
  * SOFTMAX are moe_block's (c/moe_block.h:24-26); the others are extensions:
@@ -102,13 +103,24 @@ enum { LAG_HIP_SHARED_NONE = 0, LAG_HIP_SHARED_UNSCALED = 1 };
  * picks always renormalised in double, c/qwen35.c:558-589; norm_topk and the
  * correction bias unused); SQRT_SOFTPLUS sqrtf(softplusf(x)), DeepSeek-V4's
  * router score (c/deepseek.c:854), selected and weighted as moe_block's
- * sigmoid scores.  The reference wires shared NONE and UNSCALED. */
+ * sigmoid scores; INKLING the Inkling engine's moe() routing (c/inkling.c:
+ * 1027-1043): a router of n_experts + n_shared rows, the routed sigmoids
+ * selected by moe_topk with the correction bias, weights the sigmoids of the
+ * K picks and of the n_shared shared gates, each * route_scale / (their float
+ * sum), route_scale being the engine's route_scale * gate.global_scale formed
+ * in float (norm_topk unused; the routed sum is not scaled again).  The
+ * reference wires shared NONE and UNSCALED; GATED (moe_arch.h's
+ * MOE_SHARED_GATED, with INKLING only) adds n_shared shared experts after the
+ * routed ranks, each output times its gate's weight (c/inkling.c:1166-1183),
+ * their matmuls in inkling's matmul_h contract (bf16 weights, bf16-rounded
+ * activations): sg and su [n_shared*Is, D], sd [n_shared*D, Is]. */
 typedef struct {
     int   n_experts, topk, route_act, use_corr_bias, norm_topk;
     float route_scale;
     int   shared_mode;
     int   hidden, moe_inter, shared_inter, gs;   /* D, I, Is; gs = 0: per-row int4 scale */
     int   router_bf16;                           /* router element type: 1 bf16, 0 f32 */
+    int   n_shared;                              /* INKLING: shared gate rows / GATED experts (else 0) */
 } LagHipMoeDesc;
 
 /* Device pointers of one layer.  Experts in the reference container layout
@@ -154,7 +166,9 @@ int    lag_hip_moe_forward(const LagHipMoeDesc *d, const LagHipMoeWeights *w, co
 int    lag_hip_moe_forward_noalloc(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const float *x, float *out, int S);
 /* the same with host x/out; synchronous */
 int    lag_hip_moe_block(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const float *x, float *out, int S);
-/* routing only (device pointers): logits [S,E] (may be NULL), sel [S,K], w [S,K] */
+/* routing only (device pointers): logits [S,E] (may be NULL), sel [S,K], w [S,K];
+ * INKLING: logits [S, E + n_shared], w [S, K + n_shared] (the picks' weights,
+ * then the shared gates') */
 int    lag_hip_route(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const float *x, int S,
                      float *logits, int *sel, float *wts);
 /* last routing's expert groups (device pointers of the backend's scratch;

@@ -26,10 +26,17 @@ def _ptr(a):
     return None if a is None else a.ctypes.data_as(C.c_void_p)
 
 
+def route_shape(desc):
+    """(router rows, weights per token): Inkling's routing (act 6) adds its
+    n_shared shared-expert gates to both"""
+    ns = getattr(desc, "n_shared", 0) if desc.route_act == 6 else 0
+    return desc.E + ns, desc.K + ns
+
+
 class SwMoeDesc(C.Structure):
     _fields_ = [("n_experts", C.c_int), ("topk", C.c_int), ("route_act", C.c_int),
                 ("use_corr_bias", C.c_int), ("norm_topk", C.c_int), ("route_scale", C.c_float),
-                ("shared_mode", C.c_int)]
+                ("shared_mode", C.c_int), ("n_shared", C.c_int)]
 
 
 class SwMoeLayer(C.Structure):
@@ -194,10 +201,10 @@ class Oracle:
         return sel, w
 
     def route_logits(self, desc, logits):
-        """gate + top-k of given logits [S, E] under desc (no correction bias)"""
+        """gate + top-k of given logits [S, R] under desc (no correction bias)"""
         d, _ = self.make(desc, None)
         S = logits.shape[0]
-        sel = np.empty((S, desc.K), np.int32); w = np.empty((S, desc.K), np.float32)
+        sel = np.empty((S, desc.K), np.int32); w = np.empty((S, route_shape(desc)[1]), np.float32)
         self.lib.sw_route_logits(C.byref(d), np.ascontiguousarray(logits, np.float32), S, sel, w)
         return sel, w
 
@@ -296,7 +303,7 @@ class Oracle:
     @staticmethod
     def make(desc, layer):
         d = SwMoeDesc(desc.E, desc.K, desc.route_act, desc.use_corr_bias, desc.norm_topk,
-                      desc.route_scale, desc.shared_mode)
+                      desc.route_scale, desc.shared_mode, getattr(desc, "n_shared", 0))
         if layer is None:
             return d, None
         L = SwMoeLayer(layer.D, layer.I, layer.Is, layer.E, layer.gs, int(layer.router_bf16), 0,
@@ -308,8 +315,9 @@ class Oracle:
     def route(self, desc, layer, x, mode=MODE_F32):
         d, L = self.make(desc, layer)
         S = x.shape[0]
-        sel = np.empty((S, desc.K), np.int32); w = np.empty((S, desc.K), np.float32)
-        lg = np.empty((S, desc.E), np.float32)
+        R, W = route_shape(desc)
+        sel = np.empty((S, desc.K), np.int32); w = np.empty((S, W), np.float32)
+        lg = np.empty((S, R), np.float32)
         self.lib.sw_moe_route(C.byref(d), C.byref(L), np.ascontiguousarray(x, np.float32), S, mode,
                               lg.ctypes.data_as(C.c_void_p), sel, w)
         return lg, sel, w
@@ -324,6 +332,33 @@ class Oracle:
         d, L = self.make(desc, layer)
         out = np.ascontiguousarray(out, np.float32).copy()
         self.lib.sw_moe_group_rows(C.byref(d), C.byref(L), np.ascontiguousarray(x, np.float32), out, x.shape[0], mode)
+        return out
+
+
+class RefInkling:
+    """The Inkling engine's own moe() (c/inkling.c:1011-1185, compiled in
+    oracle/_ref/libref_inkling_avx512.so by ref_inkling.c) on host weights.  Its
+    routed matmuls take IDOT from the environment once per process."""
+
+    def __init__(self):
+        self.lib = C.CDLL(os.path.join(HERE, "_ref", "libref_inkling_avx512.so"))
+        self.lib.ref_inkling_moe.restype = C.c_int
+        self.lib.ref_inkling_moe.argtypes = ([C.c_int] * 3 + [C.c_float] * 2 + [C.c_int] * 2 + [C.c_void_p] * 9
+                                             + [F32P, F32P, C.c_int])
+
+    @staticmethod
+    def available():
+        return os.path.exists(os.path.join(HERE, "_ref", "libref_inkling_avx512.so"))
+
+    def moe(self, E, K, ns, route_scale, gscale, layer, x):
+        """out[S, D] = moe(x) with out starting at zero"""
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.zeros_like(x)
+        L = layer
+        rc = self.lib.ref_inkling_moe(E, K, ns, route_scale, gscale, L.D, L.I, _ptr(L.router), _ptr(L.corr_bias),
+                                      _ptr(L.gu_q), _ptr(L.gu_s), _ptr(L.dn_q), _ptr(L.dn_s),
+                                      _ptr(L.sg), _ptr(L.su), _ptr(L.sd), x, out, x.shape[0])
+        assert rc == 0
         return out
 
 

@@ -663,18 +663,32 @@ int sw_argmax(const float *v, int n) {
 
 /* ======================= MoE block ======================= */
 
-static void router_logits(const SwMoeLayer *L, const float *x, int S, int mode, float *rl) {
-    int exact = mode == SW_MODE_EXACT;
-    if (L->router_bf16) sw_matmul_bf16(rl, x, (const uint16_t *)L->router, S, L->D, L->E, exact);
-    else sw_matmul_f32(rl, x, (const float *)L->router, S, L->D, L->E, exact);
+/* router rows: the E routed experts, plus Inkling's shared-expert gate rows */
+static int router_rows(const SwMoeDesc *d, int E) { return E + (d->route_act == SW_ROUTE_INKLING ? d->n_shared : 0); }
+/* weights per token: K, plus Inkling's shared-expert weights */
+static int weight_cols(const SwMoeDesc *d) { return d->topk + (d->route_act == SW_ROUTE_INKLING ? d->n_shared : 0); }
+
+static void router_logits(const SwMoeDesc *d, const SwMoeLayer *L, const float *x, int S, int mode, float *rl) {
+    int exact = mode == SW_MODE_EXACT, R = router_rows(d, L->E);
+    if (L->router_bf16) sw_matmul_bf16(rl, x, (const uint16_t *)L->router, S, L->D, R, exact);
+    else sw_matmul_f32(rl, x, (const float *)L->router, S, L->D, R, exact);
     if (L->logit_bias)
-        for (int s = 0; s < S; s++) for (int e = 0; e < L->E; e++) rl[(int64_t)s * L->E + e] += L->logit_bias[e];
+        for (int s = 0; s < S; s++) for (int e = 0; e < L->E; e++) rl[(int64_t)s * R + e] += L->logit_bias[e];
 }
 
 /* moe_block.h:115-122 (and c/laguna.c:697-706 per row) */
 static void route_row(const SwMoeDesc *d, const SwMoeLayer *L, float *rl, float *sc, int *sel, float *w) {
     int E = d->n_experts, K = d->topk;
     if (d->route_act == SW_ROUTE_SOFTMAX_QWEN) { sw_moe_route_qwen(rl, E, K, sel, w); return; }
+    if (d->route_act == SW_ROUTE_INKLING) {         /* c/inkling.c:1027-1043; w gets K + n_shared */
+        for (int e = 0; e < E; e++) sc[e] = sw_sigmoidf(rl[e]);
+        sw_moe_topk(sc, L->corr_bias, d->use_corr_bias, E, K, sel);
+        float sum = 0.f;
+        for (int a = 0; a < K; a++) { w[a] = sw_sigmoidf(rl[sel[a]]); sum += w[a]; }
+        for (int j = 0; j < d->n_shared; j++) { w[K + j] = sw_sigmoidf(rl[E + j]); sum += w[K + j]; }
+        for (int a = 0; a < K + d->n_shared; a++) w[a] *= d->route_scale / sum;
+        return;
+    }
     if (d->route_act == SW_ROUTE_SOFTMAX_OLMOE) {   /* c/olmoe.c:607-632: softmax_row, the moe_topk scan, norm */
         sw_softmax_row_olmoe(rl, E); for (int e = 0; e < E; e++) sc[e] = rl[e];
     } else if (d->route_act == SW_ROUTE_SOFTMAX) { sw_softmax_row(rl, E); for (int e = 0; e < E; e++) sc[e] = rl[e]; }
@@ -690,23 +704,23 @@ static void route_row(const SwMoeDesc *d, const SwMoeLayer *L, float *rl, float 
 
 /* the gate + top-k of S rows of given logits (route_row on a copy of each) */
 void sw_route_logits(const SwMoeDesc *d, const float *logits, int S, int *sel, float *w) {
-    int E = d->n_experts, K = d->topk;
+    int E = d->n_experts, K = d->topk, R = router_rows(d, E), W = weight_cols(d);
     SwMoeLayer L; memset(&L, 0, sizeof L); L.E = E;
-    float *rl = (float *)malloc((size_t)E * sizeof(float)), *sc = (float *)malloc((size_t)E * sizeof(float));
+    float *rl = (float *)malloc((size_t)R * sizeof(float)), *sc = (float *)malloc((size_t)E * sizeof(float));
     for (int s = 0; s < S; s++) {
-        memcpy(rl, logits + (int64_t)s * E, (size_t)E * sizeof(float));
-        route_row(d, &L, rl, sc, sel + s * K, w + s * K);
+        memcpy(rl, logits + (int64_t)s * R, (size_t)R * sizeof(float));
+        route_row(d, &L, rl, sc, sel + s * K, w + s * W);
     }
     free(rl); free(sc);
 }
 
 void sw_moe_route(const SwMoeDesc *d, const SwMoeLayer *L, const float *x, int S,
                   int mode, float *logits, int *sel, float *w) {
-    int E = d->n_experts, K = d->topk;
-    float *rl = (float *)malloc((size_t)S * E * sizeof(float)), *sc = (float *)malloc((size_t)E * sizeof(float));
-    router_logits(L, x, S, mode, rl);
-    if (logits) memcpy(logits, rl, (size_t)S * E * sizeof(float));
-    for (int s = 0; s < S; s++) route_row(d, L, rl + (int64_t)s * E, sc, sel + s * K, w + s * K);
+    int E = d->n_experts, K = d->topk, R = router_rows(d, E), W = weight_cols(d);
+    float *rl = (float *)malloc((size_t)S * R * sizeof(float)), *sc = (float *)malloc((size_t)E * sizeof(float));
+    router_logits(d, L, x, S, mode, rl);
+    if (logits) memcpy(logits, rl, (size_t)S * R * sizeof(float));
+    for (int s = 0; s < S; s++) route_row(d, L, rl + (int64_t)s * R, sc, sel + s * K, w + s * W);
     free(rl); free(sc);
 }
 
@@ -750,24 +764,48 @@ static void shared_rows(const SwMoeLayer *L, const float *x, int S, float *out, 
     free(sg); free(su);
 }
 
-/* moe_block.h:109-145 with laguna's hooks (c/laguna.c:574-617) */
+/* shared expert j of Inkling's gated pool over S rows (c/inkling.c:1177-1181):
+ * gate and up rows j*Is.., SiLU-GLU, down block j, all through matmul_h */
+static void gated_rows(const SwMoeLayer *L, int j, const float *x, int S, float *out) {
+    int D = L->D, SI = L->Is;
+    const uint16_t *sg = (const uint16_t *)L->sg + (int64_t)j * SI * D, *su = (const uint16_t *)L->su + (int64_t)j * SI * D;
+    const uint16_t *sd = (const uint16_t *)L->sd + (int64_t)j * D * SI;
+    float *g = (float *)malloc((size_t)S * SI * 4), *u = (float *)malloc((size_t)S * SI * 4);
+    sw_matmul_bf16_rx(g, x, sg, S, D, SI);
+    sw_matmul_bf16_rx(u, x, su, S, D, SI);
+    for (int64_t i = 0; i < (int64_t)S * SI; i++) g[i] = sw_siluf(g[i]) * u[i];
+    sw_matmul_bf16_rx(out, g, sd, S, SI, D);
+    free(g); free(u);
+}
+
+/* moe_block.h:109-145 with laguna's hooks (c/laguna.c:574-617); with
+ * SW_ROUTE_INKLING the weights already hold the route scale (no scaling of the
+ * routed sum) and SW_SHARED_GATED adds the gated shared experts after the
+ * routed ranks (c/inkling.c:1011-1183) */
 void sw_moe_block_rows(const SwMoeDesc *d, const SwMoeLayer *L, const float *x, float *out, int S, int mode) {
     int E = d->n_experts, K = d->topk, D = L->D, I = L->I;
-    float *rl = (float *)malloc((size_t)E * 4), *sc = (float *)malloc((size_t)E * 4), *w = (float *)malloc((size_t)K * 4);
+    const int inkling = d->route_act == SW_ROUTE_INKLING;
+    float *rl = (float *)malloc((size_t)router_rows(d, E) * 4), *sc = (float *)malloc((size_t)E * 4);
+    float *w = (float *)malloc((size_t)weight_cols(d) * 4);
     int *sel = (int *)malloc((size_t)K * sizeof(int));
     float *scr = (float *)malloc((size_t)D * 4), *acc = (float *)malloc((size_t)D * 4);
     float *gu = (float *)malloc((size_t)2 * I * 4), *glu = (float *)malloc((size_t)I * 4);
     for (int s = 0; s < S; s++) {
         const float *xs = x + (int64_t)s * D; float *os = out + (int64_t)s * D;
-        router_logits(L, xs, 1, mode, rl);
+        router_logits(d, L, xs, 1, mode, rl);
         route_row(d, L, rl, sc, sel, w);
         for (int i = 0; i < D; i++) acc[i] = 0;
         for (int a = 0; a < K; a++) {
             expert_rows(L, sel[a], xs, 1, scr, mode, gu, glu);
             for (int i = 0; i < D; i++) acc[i] = fmaf(w[a], scr[i], acc[i]);
         }
-        for (int i = 0; i < D; i++) acc[i] *= d->route_scale;
-        if (d->shared_mode != SW_SHARED_NONE) {
+        if (!inkling) for (int i = 0; i < D; i++) acc[i] *= d->route_scale;
+        if (d->shared_mode == SW_SHARED_GATED) {
+            for (int j = 0; j < d->n_shared; j++) {
+                gated_rows(L, j, xs, 1, scr);
+                for (int i = 0; i < D; i++) acc[i] = fmaf(w[K + j], scr[i], acc[i]);
+            }
+        } else if (d->shared_mode != SW_SHARED_NONE) {
             shared_rows(L, xs, 1, scr, mode);
             for (int i = 0; i < D; i++) acc[i] += scr[i];
         }
@@ -797,8 +835,9 @@ int sw_bucket(const int *sel, int S, int K, int E, int *gexp, int *gbeg, int *gc
 
 /* lag_moe_group, c/laguna.c:689-786 (CPU tier) */
 void sw_moe_group_rows(const SwMoeDesc *d, const SwMoeLayer *L, const float *x, float *out, int S, int mode) {
-    int E = d->n_experts, K = d->topk, D = L->D, I = L->I, T = S * K;
-    float *w = (float *)malloc((size_t)T * 4);
+    int E = d->n_experts, K = d->topk, D = L->D, I = L->I, T = S * K, W = weight_cols(d);
+    const int inkling = d->route_act == SW_ROUTE_INKLING;
+    float *w = (float *)malloc((size_t)S * W * 4);
     int *sel = (int *)malloc((size_t)T * sizeof(int));
     sw_moe_route(d, L, x, S, mode, NULL, sel, w);
     int *gexp = (int *)malloc((size_t)E * sizeof(int)), *gbeg = (int *)malloc((size_t)E * sizeof(int));
@@ -817,12 +856,21 @@ void sw_moe_group_rows(const SwMoeDesc *d, const SwMoeLayer *L, const float *x, 
         float *o = acc + (int64_t)s * D;
         for (int i = 0; i < D; i++) o[i] = 0;
         for (int a = 0; a < K; a++) {
-            const float *v = slots + (int64_t)rowof[s * K + a] * D; float wa = w[s * K + a];
+            const float *v = slots + (int64_t)rowof[s * K + a] * D; float wa = w[(int64_t)s * W + a];
             for (int i = 0; i < D; i++) o[i] = fmaf(wa, v[i], o[i]);
         }
     }
-    for (int64_t i = 0; i < (int64_t)S * D; i++) acc[i] *= d->route_scale;
-    if (d->shared_mode != SW_SHARED_NONE) {
+    if (!inkling) for (int64_t i = 0; i < (int64_t)S * D; i++) acc[i] *= d->route_scale;
+    if (d->shared_mode == SW_SHARED_GATED) {
+        float *so = (float *)malloc((size_t)S * D * 4);
+        for (int j = 0; j < d->n_shared; j++) {
+            gated_rows(L, j, x, S, so);
+            for (int s = 0; s < S; s++)
+                for (int i = 0; i < D; i++) acc[(int64_t)s * D + i] = fmaf(w[(int64_t)s * W + K + j], so[(int64_t)s * D + i], acc[(int64_t)s * D + i]);
+        }
+        for (int64_t i = 0; i < (int64_t)S * D; i++) out[i] += acc[i];
+        free(so);
+    } else if (d->shared_mode != SW_SHARED_NONE) {
         float *so = (float *)malloc((size_t)S * D * 4);
         shared_rows(L, x, S, so, mode);
         for (int64_t i = 0; i < (int64_t)S * D; i++) out[i] += acc[i] + so[i];

@@ -78,14 +78,24 @@ void  sw_rmsnorm_row(float *out, const float *x, const float *w, int D, float ep
 int   sw_argmax(const float *v, int n);
 
 /* ---------------- MoE block ---------------- */
+/* SW_ROUTE_INKLING: the Inkling engine's moe() routing (c/inkling.c:1027-1043):
+ * logits over E routed + n_shared shared rows; selection by moe_topk on the
+ * routed sigmoids plus the correction bias; weights the sigmoids of the K
+ * picks' and the n_shared shared logits, their float sum (ranks, then the
+ * shared) s, each times route_scale / s (route_scale = the engine's
+ * route_scale * gate.global_scale, formed by the caller in float).
+ * SW_SHARED_GATED: the n_shared shared experts take those weights, after the
+ * routed ranks, with no further scale (c/inkling.c:1166-1183); their matmuls
+ * are inkling's matmul_h (bf16 weights, bf16-rounded activations). */
 enum { SW_ROUTE_SIGMOID = 0, SW_ROUTE_SOFTMAX = 1, SW_ROUTE_SOFTPLUS = 2, SW_ROUTE_SOFTMAX_OLMOE = 3,
-       SW_ROUTE_SOFTMAX_QWEN = 4, SW_ROUTE_SQRT_SOFTPLUS = 5 };
-enum { SW_SHARED_NONE = 0, SW_SHARED_UNSCALED = 1 };
+       SW_ROUTE_SOFTMAX_QWEN = 4, SW_ROUTE_SQRT_SOFTPLUS = 5, SW_ROUTE_INKLING = 6 };
+enum { SW_SHARED_NONE = 0, SW_SHARED_UNSCALED = 1, SW_SHARED_GATED = 3 };
 
 typedef struct {
     int   n_experts, topk, route_act, use_corr_bias, norm_topk;
     float route_scale;
     int   shared_mode;
+    int   n_shared;            /* SW_ROUTE_INKLING: shared logit rows / SW_SHARED_GATED experts */
 } SwMoeDesc;
 
 /* Host weights of one MoE layer, in the reference container layout
@@ -93,7 +103,9 @@ typedef struct {
  *   gu_q [E*2I, D/2] (gate rows then up rows per expert), gu_s [E*2I*ngD]
  *   dn_q [E*D, I/2], dn_s [E*D*ngI]   (ng = 1 when gs == 0)
  *   router: f32 [E,D] or bf16 [E,D] (router_bf16)
- *   shared: bf16 [Is,D],[Is,D],[D,Is] (or f32 when shared_f32)        */
+ *   shared: bf16 [Is,D],[Is,D],[D,Is] (or f32 when shared_f32); GATED:
+ *           n_shared experts stacked, [ns*Is,D],[ns*Is,D],[ns,D,Is]
+ *   SW_ROUTE_INKLING: router [E + n_shared, D]                          */
 typedef struct {
     int D, I, Is, E, gs;
     int router_bf16, shared_f32;

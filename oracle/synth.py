@@ -20,6 +20,7 @@ class Desc:
     norm_topk: int
     route_scale: float
     shared_mode: int
+    n_shared: int = 0
 
 
 @dataclass
@@ -48,21 +49,23 @@ class Layer:
 
 
 def desc_of(cfg):
-    return Desc(cfg.E, cfg.K, cfg.route_act, cfg.use_corr_bias, cfg.norm_topk, cfg.route_scale, cfg.shared_mode)
+    return Desc(cfg.E, cfg.K, cfg.route_act, cfg.use_corr_bias, cfg.norm_topk, cfg.route_scale, cfg.shared_mode,
+                cfg.n_shared)
 
 
 def make_layer(orc, cfg, base_seed, layer=0, corr_bias_sigma=0.0):
     D, I, Is, E, gs = cfg.D, cfg.I, cfg.Is, cfg.E, cfg.gs
     ts = lambda tid: S.tensor_seed(base_seed, layer, tid)
-    r = orc.normal(E * D, ts(S.T_ROUTER), WEIGHT_SIGMA).reshape(E, D)
+    R, ns = cfg.router_rows, cfg.n_shared_experts
+    r = orc.normal(R * D, ts(S.T_ROUTER), WEIGHT_SIGMA).reshape(R, D)
     router = orc.to_bf16(r) if cfg.router_bf16 else r
     gu_q, gu_s = orc.gen_q4(ts(S.T_GATE_UP), WEIGHT_SIGMA, E * 2 * I, D, gs)
     dn_q, dn_s = orc.gen_q4(ts(S.T_DOWN), WEIGHT_SIGMA, E * D, I, gs)
     sg = su = sd = None
-    if cfg.shared_mode:
-        sg = orc.to_bf16(orc.normal(Is * D, ts(S.T_SH_GATE), WEIGHT_SIGMA)).reshape(Is, D)
-        su = orc.to_bf16(orc.normal(Is * D, ts(S.T_SH_UP), WEIGHT_SIGMA)).reshape(Is, D)
-        sd = orc.to_bf16(orc.normal(D * Is, ts(S.T_SH_DOWN), WEIGHT_SIGMA)).reshape(D, Is)
+    if cfg.shared_mode:                  # ns experts stacked: [ns*Is, D], [ns*Is, D], [ns*D, Is]
+        sg = orc.to_bf16(orc.normal(ns * Is * D, ts(S.T_SH_GATE), WEIGHT_SIGMA)).reshape(ns * Is, D)
+        su = orc.to_bf16(orc.normal(ns * Is * D, ts(S.T_SH_UP), WEIGHT_SIGMA)).reshape(ns * Is, D)
+        sd = orc.to_bf16(orc.normal(ns * D * Is, ts(S.T_SH_DOWN), WEIGHT_SIGMA)).reshape(ns * D, Is)
     corr = None
     if cfg.use_corr_bias:
         corr = (orc.normal(E, ts(S.T_CORR_BIAS), corr_bias_sigma) if corr_bias_sigma > 0

@@ -53,7 +53,7 @@ class LagHipMoeDesc(C.Structure):
     _fields_ = [("n_experts", C.c_int), ("topk", C.c_int), ("route_act", C.c_int), ("use_corr_bias", C.c_int),
                 ("norm_topk", C.c_int), ("route_scale", C.c_float), ("shared_mode", C.c_int),
                 ("hidden", C.c_int), ("moe_inter", C.c_int), ("shared_inter", C.c_int), ("gs", C.c_int),
-                ("router_bf16", C.c_int)]
+                ("router_bf16", C.c_int), ("n_shared", C.c_int)]
 
 
 class LagHipMoeWeights(C.Structure):
@@ -63,7 +63,7 @@ class LagHipMoeWeights(C.Structure):
 
 def desc_of(cfg):
     return LagHipMoeDesc(cfg.E, cfg.K, cfg.route_act, cfg.use_corr_bias, cfg.norm_topk, cfg.route_scale,
-                         cfg.shared_mode, cfg.D, cfg.I, cfg.Is, cfg.gs, int(cfg.router_bf16))
+                         cfg.shared_mode, cfg.D, cfg.I, cfg.Is, cfg.gs, int(cfg.router_bf16), cfg.n_shared)
 
 
 class BackendError(RuntimeError):
@@ -260,11 +260,15 @@ class Backend:
         return out
 
     def route(self, desc, weights, x_dev, S):
-        E, K = desc.n_experts, desc.topk
-        lg, sel, w = self.alloc(S * E * 4), self.alloc(S * K * 4), self.alloc(S * K * 4)
+        """(logits [S, R], sel [S, K], w [S, W]); Inkling's routing (act 6) has R = E + n_shared
+        router rows and W = K + n_shared weights (the picks', then the shared gates')"""
+        K = desc.topk
+        ns = desc.n_shared if desc.route_act == 6 else 0
+        R, W = desc.n_experts + ns, K + ns
+        lg, sel, w = self.alloc(S * R * 4), self.alloc(S * K * 4), self.alloc(S * W * 4)
         self.check(self.lib.lag_hip_route(C.byref(desc), C.byref(weights), VP(int(x_dev)), S, VP(int(lg)),
                                           VP(int(sel)), VP(int(w))), "lag_hip_route")
-        out = (self.d2h(lg, (S, E), np.float32), self.d2h(sel, (S, K), np.int32), self.d2h(w, (S, K), np.float32))
+        out = (self.d2h(lg, (S, R), np.float32), self.d2h(sel, (S, K), np.int32), self.d2h(w, (S, W), np.float32))
         for b in (lg, sel, w):
             b.free()
         return out
@@ -414,13 +418,14 @@ class DeviceLayer:
         ngD = D // gs if gs > 0 else 1
         ngI = I // gs if gs > 0 else 1
         rb = 2 if cfg.router_bf16 else 4
-        tmp = be.alloc(E * D * rb)
+        R = cfg.router_rows                      # Inkling: the shared gate rows follow the E routed
+        tmp = be.alloc(R * D * rb)
         if cfg.router_bf16:
-            be.gen_bf16(tmp, E * D, ts(synth.T_ROUTER), WEIGHT_SIGMA)
+            be.gen_bf16(tmp, R * D, ts(synth.T_ROUTER), WEIGHT_SIGMA)
         else:
-            be.gen_normal(tmp, E * D, ts(synth.T_ROUTER), WEIGHT_SIGMA)
-        self.router = self._keep(be.alloc((E + 3) // 4 * 4 * D * rb))    # streaming order
-        be.check(be.lib.lag_hip_router_chain(VP(int(tmp)), VP(int(self.router)), E, D, int(cfg.router_bf16)), "router chain")
+            be.gen_normal(tmp, R * D, ts(synth.T_ROUTER), WEIGHT_SIGMA)
+        self.router = self._keep(be.alloc((R + 3) // 4 * 4 * D * rb))    # streaming order
+        be.check(be.lib.lag_hip_router_chain(VP(int(tmp)), VP(int(self.router)), R, D, int(cfg.router_bf16)), "router chain")
         be.sync()
         tmp.free()
         self.gu_q, self.gu_s = self._keep(be.alloc(E * 2 * I * D // 2)), self._keep(be.alloc(E * 2 * I * ngD * 4))
@@ -433,11 +438,12 @@ class DeviceLayer:
         if cfg.zipf > 0:
             lb = synth.zipf_bias(E, cfg.zipf, ts(synth.T_ROUTER) ^ 0x5A5A)
             self.logit_bias = self._keep(be.upload(lb))
-        if cfg.shared_mode:
-            self.sg, self.su, self.sd = (self._keep(be.alloc(Is * D * 2)) for _ in range(3))
-            be.gen_bf16(self.sg, Is * D, ts(synth.T_SH_GATE), WEIGHT_SIGMA)
-            be.gen_bf16(self.su, Is * D, ts(synth.T_SH_UP), WEIGHT_SIGMA)
-            be.gen_bf16(self.sd, D * Is, ts(synth.T_SH_DOWN), WEIGHT_SIGMA)
+        if cfg.shared_mode:                       # ns shared experts stacked (GATED: Inkling's pool)
+            ns = cfg.n_shared_experts
+            self.sg, self.su, self.sd = (self._keep(be.alloc(ns * Is * D * 2)) for _ in range(3))
+            be.gen_bf16(self.sg, ns * Is * D, ts(synth.T_SH_GATE), WEIGHT_SIGMA)
+            be.gen_bf16(self.su, ns * Is * D, ts(synth.T_SH_UP), WEIGHT_SIGMA)
+            be.gen_bf16(self.sd, ns * D * Is, ts(synth.T_SH_DOWN), WEIGHT_SIGMA)
         be.sync()
         return self
 

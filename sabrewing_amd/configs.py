@@ -23,7 +23,11 @@ ROUTE_SIGMOID, ROUTE_SOFTMAX, ROUTE_SOFTPLUS = 0, 1, 2
 ROUTE_SOFTMAX_OLMOE, ROUTE_SOFTMAX_QWEN = 3, 4
 # DeepSeek-V4's router score sqrtf(softplusf(x)) (c/deepseek.c:854) as a moe_block gate
 ROUTE_SQRT_SOFTPLUS = 5
-SHARED_NONE, SHARED_UNSCALED = 0, 1
+# the Inkling engine's routing (c/inkling.c:1027-1043): sigmoid + bias selection, weights
+# normalised over the K picks and the n_shared shared-expert gates, x route_scale
+ROUTE_INKLING = 6
+# Inkling's shared experts, weighted from that pool (c/inkling.c:1166-1183)
+SHARED_NONE, SHARED_UNSCALED, SHARED_GATED = 0, 1, 3
 WEIGHT_SIGMA = 0.02
 
 
@@ -44,6 +48,7 @@ class MoeConfig:
     router_bf16: bool = True
     x_bf16: bool = True
     zipf: float = 0.0          # >0: per-expert logit bias -zipf*ln(rank) (skew variant)
+    n_shared: int = 0          # ROUTE_INKLING: shared gate rows after the E routed ones; SHARED_GATED: experts
 
     @property
     def ngD(self):
@@ -59,11 +64,19 @@ class MoeConfig:
         sc = 4 * (2 * self.I * self.ngD + self.D * self.ngI)
         return nib + sc
 
+    @property
+    def router_rows(self):
+        return self.E + (self.n_shared if self.route_act == ROUTE_INKLING else 0)
+
+    @property
+    def n_shared_experts(self):
+        return self.n_shared if self.shared_mode == SHARED_GATED else (1 if self.shared_mode else 0)
+
     def router_bytes(self):
-        return self.E * self.D * (2 if self.router_bf16 else 4)
+        return self.router_rows * self.D * (2 if self.router_bf16 else 4)
 
     def shared_bytes(self):
-        return 3 * self.D * self.Is * 2 if self.shared_mode else 0
+        return 3 * self.D * self.Is * 2 * self.n_shared_experts
 
     def step_bytes(self, S, G):
         """Algorithmic HBM bytes of one layer pass over S tokens touching G
@@ -94,7 +107,13 @@ C1_OLMOE = replace(C1, name="C1-olmoe-engine-routing", route_act=ROUTE_SOFTMAX_O
 QWEN = MoeConfig("qwen35-moe", D=2048, E=256, K=8, I=512, Is=0, route_act=ROUTE_SOFTMAX_QWEN,
                  use_corr_bias=0, norm_topk=0, route_scale=1.0, shared_mode=SHARED_NONE, router_bf16=False,
                  x_bf16=False)
-CONFIGS = {c.name: c for c in (C1, C2, C2_SIGMOID, C4_ZIPF, C5_LAYER, C1_OLMOE, QWEN)}
+# an Inkling-shaped layer (c/inkling.c:1011-1183; docs/inkling.md): f32 router over E + 2 rows,
+# sigmoid + correction-bias selection, 2 gated bf16 shared experts, per-row int4 experts,
+# route_scale 8 x a gate.global_scale of 1 (a parity case, not a bench config)
+INKLING = MoeConfig("inkling-gated", D=4096, E=256, K=6, I=2048, Is=2048, route_act=ROUTE_INKLING,
+                    use_corr_bias=1, norm_topk=0, route_scale=8.0, shared_mode=SHARED_GATED, gs=0,
+                    router_bf16=False, x_bf16=False, n_shared=2)
+CONFIGS = {c.name: c for c in (C1, C2, C2_SIGMOID, C4_ZIPF, C5_LAYER, C1_OLMOE, QWEN, INKLING)}
 
 
 def scaled(cfg, D=None, E=None, K=None, I=None, Is=None, name=None):

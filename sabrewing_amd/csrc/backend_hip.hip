@@ -462,6 +462,8 @@ extern "C" int lag_hip_router_chain(const void *W, void *Wc, int E, int D, int w
 
 struct FwdScratch {
     float *logits, *scores, *w, *slots, *sout;
+    float *wsh;             // Inkling: the shared gates' weights [S, ns]
+    float *shu;             // GATED: the shared experts' up rows [S, ns * Is]
     int *sel, *gexp, *gbeg, *gcnt, *G, *grow, *rowof, *items, *P;
     sw_u32x4 *hl;           // h of every packed row as dot8 limbs
     float *hs;
@@ -477,8 +479,25 @@ static int g_last_G_dev = 0;            // 1: last forward's groups live in the 
 static FwdScratch g_last;
 static int g_last_ng = 0;
 
+// router rows and the Inkling gate pool; the shared experts of a layer
+static int ink_ns(const LagHipMoeDesc *d) { return d->route_act == SW_ROUTE_INKLING ? d->n_shared : 0; }
+static int router_rows(const LagHipMoeDesc *d) { return d->n_experts + ink_ns(d); }
+static int shared_count(const LagHipMoeDesc *d) {
+    return d->shared_mode == LAG_HIP_SHARED_GATED ? d->n_shared : d->shared_mode ? 1 : 0;
+}
+// the scale the combine applies to the routed sum: Inkling's weights already hold it
+static float combine_scale(const LagHipMoeDesc *d) { return d->route_act == SW_ROUTE_INKLING ? 1.0f : d->route_scale; }
+
 static int desc_ok(const LagHipMoeDesc *d, const LagHipMoeWeights *w) {
     if (!d || !w) return 0;
+    if (d->shared_mode != LAG_HIP_SHARED_NONE && d->shared_mode != LAG_HIP_SHARED_UNSCALED &&
+        d->shared_mode != LAG_HIP_SHARED_GATED) return 0;
+    if (d->route_act == SW_ROUTE_INKLING) {          // its own gate pool; no router-hook bias
+        if (d->n_shared < 0 || d->n_shared > 64 || w->logit_bias) return 0;
+        if (d->shared_mode == LAG_HIP_SHARED_UNSCALED) return 0;
+        if (d->n_experts + d->n_shared > 1024) return 0;
+    }
+    if (d->shared_mode == LAG_HIP_SHARED_GATED && (d->route_act != SW_ROUTE_INKLING || d->n_shared < 1)) return 0;
     // (E <= 1024: the gate/top-k wave and the counting sort hold every expert on chip)
     if (d->n_experts <= 0 || d->n_experts > 1024 || d->topk <= 0 || d->topk > d->n_experts || d->topk > 64) return 0;
     if (d->route_act < 0 || d->route_act > SW_ROUTE_ACT_MAX) return 0;
@@ -496,17 +515,19 @@ static const ScratchSrc kArena = {nullptr, 0};
 
 static int carve_fwd(const LagHipMoeDesc *d, int S, FwdScratch &f, const ScratchSrc &src, bool idot = false) {
     const int E = d->n_experts, K = d->topk, D = d->hidden, I = d->moe_inter, Is = d->shared_inter;
-    const int T = S * K;
+    const int T = S * K, R = router_rows(d), nsx = shared_count(d);
     Carve cv;
-    const size_t o_lg = cv.take((size_t)S * E * 4), o_sc = cv.take((size_t)S * E * 4);
+    const size_t o_lg = cv.take((size_t)S * R * 4), o_sc = cv.take((size_t)S * R * 4);
+    const size_t o_wsh = cv.take((size_t)S * (ink_ns(d) > 0 ? ink_ns(d) : 1) * 4);
     const size_t o_sel = cv.take((size_t)T * 4), o_w = cv.take((size_t)T * 4);
     const size_t o_gexp = cv.take((size_t)E * 4), o_gbeg = cv.take((size_t)E * 4), o_gcnt = cv.take((size_t)E * 4);
     const size_t o_G = cv.take(4), o_grow = cv.take((size_t)T * 4), o_rowof = cv.take((size_t)T * 4);
     const size_t o_items = cv.take((size_t)sw_npass_max(T, E, SW_DG_TT) * 4), o_P = cv.take(4);
     const size_t o_hl = cv.take((size_t)T * (I / 32) * SW_NL * 16), o_hs = cv.take((size_t)T * (I / 32) * 4);
     const size_t o_slot = cv.take(S > 1 || idot ? (size_t)T * D * 4 : 4);
-    size_t o_sh = 0, o_so = 0;
-    if (d->shared_mode) { o_sh = cv.take((size_t)S * Is * 4); o_so = cv.take((size_t)S * D * 4); }
+    size_t o_sh = 0, o_so = 0, o_su = 0;
+    if (d->shared_mode) { o_sh = cv.take((size_t)S * nsx * Is * 4); o_so = cv.take((size_t)S * nsx * D * 4); }
+    if (d->shared_mode == LAG_HIP_SHARED_GATED) o_su = cv.take((size_t)S * nsx * Is * 4);
     const size_t o_xl = cv.take((size_t)S * (D / 32) * SW_NL * 16), o_xs = cv.take((size_t)S * (D / 32) * 4);
     size_t o_xd = 0, o_xds = 0, o_hd = 0, o_hds = 0;
     if (S > 1) {
@@ -541,6 +562,8 @@ static int carve_fwd(const LagHipMoeDesc *d, int S, FwdScratch &f, const Scratch
     f.hl = (sw_u32x4 *)(A + o_hl); f.hs = (float *)(A + o_hs); f.slots = (float *)(A + o_slot);
     f.shh = d->shared_mode ? (float *)(A + o_sh) : nullptr;
     f.sout = d->shared_mode ? (float *)(A + o_so) : nullptr;
+    f.shu = d->shared_mode == LAG_HIP_SHARED_GATED ? (float *)(A + o_su) : nullptr;
+    f.wsh = (float *)(A + o_wsh);
     f.xl = (sw_u32x4 *)(A + o_xl); f.xs = (float *)(A + o_xs);
     f.xd = S > 1 ? (uint32_t *)(A + o_xd) : nullptr; f.xds = S > 1 ? (float *)(A + o_xds) : nullptr;
     f.hd = S > 1 ? (uint32_t *)(A + o_hd) : nullptr; f.hds = S > 1 ? (float *)(A + o_hds) : nullptr;
@@ -552,9 +575,38 @@ static int carve_fwd(const LagHipMoeDesc *d, int S, FwdScratch &f, const Scratch
 static int route_dev(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const float *x, int S, float *logits,
                      float *scores, int *sel, float *wts, sw_u32x4 *xl = nullptr, float *xs = nullptr) {
     PROF("router_topk");
+    // Inkling: the picks' weights then the shared gates' in one row of K + ns
+    const int ns = ink_ns(d), K = d->topk;
+    const SwGateOpt o = {router_rows(d), ns, d->route_scale, K + ns, ns ? wts + K : nullptr, K + ns};
     if (sw_launch_router_topk(g_st, w->router, d->router_bf16, x, S, d->hidden, d->n_experts, w->logit_bias, logits,
                               scores, d->topk, d->route_act, w->corr_bias, d->use_corr_bias, d->norm_topk,
-                              sel, wts, xl, xs)) return fail_msg("router launch");
+                              sel, wts, xl, xs, &o)) return fail_msg("router launch");
+    return 0;
+}
+
+// the gate + top-k launch of the forward: weights [S, K], Inkling's shared gates' to f.wsh
+static int gate_dev(const LagHipMoeDesc *d, const LagHipMoeWeights *w, int S, FwdScratch &f) {
+    PROF("gate_topk");
+    const int ns = ink_ns(d);
+    const SwGateOpt o = {router_rows(d), ns, d->route_scale, d->topk, ns ? f.wsh : nullptr, ns};
+    if (sw_launch_gate_topk(g_st, f.logits, f.scores, S, d->n_experts, d->topk, d->route_act, w->corr_bias,
+                            d->use_corr_bias, d->norm_topk, f.sel, f.w, &o)) return fail_msg("gate/top-k launch");
+    return 0;
+}
+
+// Inkling's gated shared experts over S rows (c/inkling.c:1166-1183) in matmul_h's
+// contract: gate and up rows of all ns experts, SiLU-GLU, then expert j's down into
+// sout[s][j][D]
+static int gated_shared(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const float *x, int S, FwdScratch &f) {
+    PROF("gated_shared");
+    const int D = d->hidden, Is = d->shared_inter, ns = d->n_shared;
+    if (sw_launch_lanes16(g_st, w->sg, 0, 1, nullptr, x, S, D, ns * Is, f.shh, 0) ||
+        sw_launch_lanes16(g_st, w->su, 0, 1, nullptr, x, S, D, ns * Is, f.shu, 0) ||
+        sw_launch_silu_mul(g_st, f.shh, f.shu, (int64_t)S * ns * Is, f.shh)) return fail_msg("gated shared gate/up launch");
+    for (int j = 0; j < ns; j++)
+        if (sw_launch_lanes16_ld(g_st, (const uint16_t *)w->sd + (size_t)j * D * Is, 0, 1, nullptr, f.shh + (size_t)j * Is,
+                                 ns * Is, S, Is, D, f.sout + (size_t)j * D, ns * D, 0))
+            return fail_msg("gated shared down launch");
     return 0;
 }
 
@@ -576,18 +628,17 @@ static int forward_idot(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const
     if (carve_fwd(d, S, f, sc, true)) return -1;
     SwQ4 gu = {(const uint8_t *)w->gu_q, w->gu_s, 2 * I, D, 0, E};
     SwQ4 dn = {(const uint8_t *)w->dn_q, w->dn_s, D, I, 0, E};
-    const bool sh = d->shared_mode != 0;
+    const bool sh = d->shared_mode == LAG_HIP_SHARED_UNSCALED, gated = d->shared_mode == LAG_HIP_SHARED_GATED;
     { PROF("stage_route");
-      if (sw_launch_stage_route(g_st, w->router, d->router_bf16, x, S, D, E, w->logit_bias, f.logits, f.scores, d->route_act,
-                                nullptr, f.xs, nullptr, nullptr, Is, f.shh)) return fail_msg("routing stage launch"); }
+      if (sw_launch_stage_route(g_st, w->router, d->router_bf16, x, S, D, router_rows(d), w->logit_bias, f.logits, f.scores,
+                                d->route_act, nullptr, f.xs, nullptr, nullptr, Is, f.shh)) return fail_msg("routing stage launch"); }
     if (sh) {
         PROF("shared_glu");
         if (sw_launch_sh_glu(g_st, (const uint16_t *)w->sg, (const uint16_t *)w->su, x, S, D, Is, f.shh))
             return fail_msg("shared gate_up launch");
     }
-    { PROF("gate_topk");
-      if (sw_launch_gate_topk(g_st, f.logits, f.scores, S, E, K, d->route_act, w->corr_bias, d->use_corr_bias, d->norm_topk,
-                              f.sel, f.w)) return fail_msg("gate/top-k launch"); }
+    if (gated && gated_shared(d, w, x, S, f)) return -1;
+    if (gate_dev(d, w, S, f)) return -1;
     { PROF("bucket");
       if (sw_launch_bucket(g_st, f.sel, S, K, E, f.gexp, f.gbeg, f.gcnt, f.G, f.grow, f.rowof, 1, nullptr, nullptr))
           return fail_msg("bucket launch"); }
@@ -603,7 +654,8 @@ static int forward_idot(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const
     { PROF("idot_quant"); if (sw_launch_idot_quant(g_st, f.hf, S * K, I, f.hq, f.hqs)) return fail_msg("IDOT quant launch"); }
     { PROF("idot_down"); if (sw_launch_idot_rows(g_st, dn, f.hq, f.hqs, gd, f.slots)) return fail_msg("IDOT down launch"); }
     { PROF("combine");
-      if (sw_launch_combine(g_st, f.slots, f.rowof, f.w, S, K, D, d->route_scale, f.sout, out, 1))
+      if (sw_launch_combine(g_st, f.slots, f.rowof, f.w, S, K, D, combine_scale(d), f.sout, out, 1,
+                            gated ? f.wsh : nullptr, gated ? d->n_shared : 0))
           return fail_msg("combine launch"); }
     g_last_G_dev = 1; g_last_ng = 0;
     g_last = f;
@@ -631,9 +683,13 @@ static int forward(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const floa
     if (carve_fwd(d, S, f, sc)) return -1;
     SwQ4 gu = {(const uint8_t *)w->gu_q, w->gu_s, 2 * I, D, d->gs, E};
     SwQ4 dn = {(const uint8_t *)w->dn_q, w->dn_s, D, I, d->gs, E};
-    const bool sh = d->shared_mode != 0;
+    // sh: moe_block's unscaled shared expert (the laguna contract); gated: Inkling's pool
+    const bool sh = d->shared_mode == LAG_HIP_SHARED_UNSCALED, gated = d->shared_mode == LAG_HIP_SHARED_GATED;
     const uint16_t *sg = sh ? (const uint16_t *)w->sg : nullptr, *su = sh ? (const uint16_t *)w->su : nullptr;
     const uint16_t *sd = sh ? (const uint16_t *)w->sd : nullptr;
+    const float rs_c = combine_scale(d);
+    const float *wsh = gated ? f.wsh : nullptr;
+    const int nsg = gated ? d->n_shared : 0;
     // one token with E <= 256: its gate + top-k runs in every block of the
     // expert stage (no device-scope handoff); otherwise a gate + top-k launch
     // after the routing stage
@@ -643,9 +699,10 @@ static int forward(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const floa
     const bool sh_in = sh && S == 1;
     const bool mf = S > 1 && use_mfma(T, E, D, I);
     { PROF("stage_route");
-      if (sw_launch_stage_route(g_st, w->router, d->router_bf16, x, S, D, E, w->logit_bias, f.logits, f.scores, d->route_act,
-                                mf ? nullptr : f.xl, f.xs, sh_in ? sg : nullptr, su, Is, f.shh))
+      if (sw_launch_stage_route(g_st, w->router, d->router_bf16, x, S, D, router_rows(d), w->logit_bias, f.logits, f.scores,
+                                d->route_act, mf ? nullptr : f.xl, f.xs, sh_in ? sg : nullptr, su, Is, f.shh))
           return fail_msg("routing stage launch"); }
+    if (gated && gated_shared(d, w, x, S, f)) return -1;
     if (mf) {
         PROF("digits");
         if (sw_launch_digits(g_st, x, S, D, f.xd, f.xds)) return fail_msg("digits launch");
@@ -654,11 +711,7 @@ static int forward(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const floa
         PROF("shared_glu");
         if (sw_launch_sh_glu(g_st, sg, su, x, S, D, Is, f.shh)) return fail_msg("shared gate_up launch");
     }
-    if (!in_experts) {
-        PROF("gate_topk");
-        if (sw_launch_gate_topk(g_st, f.logits, f.scores, S, E, K, d->route_act, w->corr_bias, d->use_corr_bias,
-                                d->norm_topk, f.sel, f.w)) return fail_msg("gate/top-k launch");
-    }
+    if (!in_experts && gate_dev(d, w, S, f)) return -1;
     if (S == 1) {                        // one token: its K picks in rank order, fused down + combine
         { PROF("stage_experts");
           if (sw_launch_stage_experts(g_st, gu, f.xl, f.xs, SwGroups{}, I, f.hl, f.hs, f.sel, K,
@@ -666,7 +719,8 @@ static int forward(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const floa
                                       w->corr_bias, d->use_corr_bias, d->norm_topk, f.w, sd, f.shh, S, Is, D, f.sout))
               return fail_msg("expert stage launch"); }
         { PROF("q4_down_combine");
-          if (sw_launch_q4_dot8_down_combine(g_st, dn, f.hl, f.hs, f.sel, f.w, K, d->route_scale, f.sout, out))
+          if (sw_launch_q4_dot8_down_combine(g_st, dn, f.hl, f.hs, f.sel, f.w, K, rs_c, sh || gated ? f.sout : nullptr, out,
+                                             wsh, nsg))
               return fail_msg("down/combine launch"); }
         g_last_G_dev = 0; g_last_ng = K;
     } else if (mf) {                     // prefill: tiles of up to 64 tokens of a group on the int8 MFMA
@@ -684,7 +738,7 @@ static int forward(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const floa
         gd.grow = nullptr;                 // the down reads the packed rows directly
         { PROF("mf_down"); if (sw_launch_mf_rows(g_st, dn, f.hd, f.hds, gd, f.slots)) return fail_msg("MFMA down launch"); }
         { PROF("combine");
-          if (sw_launch_combine(g_st, f.slots, f.rowof, f.w, S, K, D, d->route_scale, f.sout, out, 1))
+          if (sw_launch_combine(g_st, f.slots, f.rowof, f.w, S, K, D, rs_c, sh || gated ? f.sout : nullptr, out, 1, wsh, nsg))
               return fail_msg("combine launch"); }
         g_last_G_dev = 1; g_last_ng = 0;
     } else {
@@ -706,7 +760,7 @@ static int forward(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const floa
         gd.grow = nullptr;                 // the down reads the packed rows directly
         { PROF("q4_down"); if (sw_launch_q4_dot8_rows(g_st, dn, f.hl, f.hs, gd, f.slots)) return fail_msg("down launch"); }
         { PROF("combine");
-          if (sw_launch_combine(g_st, f.slots, f.rowof, f.w, S, K, D, d->route_scale, f.sout, out, 1))
+          if (sw_launch_combine(g_st, f.slots, f.rowof, f.w, S, K, D, rs_c, sh || gated ? f.sout : nullptr, out, 1, wsh, nsg))
               return fail_msg("combine launch"); }
         g_last_G_dev = 1; g_last_ng = 0;
     }

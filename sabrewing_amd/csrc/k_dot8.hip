@@ -615,6 +615,8 @@ struct Dot8DownArgs {
     float route_scale;
     const float *shared;
     float *out;
+    const float *wsh;          // Inkling's gated shared experts: shared [ns][D] weighted by wsh[ns], or null
+    int ns;
 };
 // block bx of DC_RB output rows; runs: [K][DC_RB][NC] floats
 template <int C16>
@@ -643,7 +645,7 @@ __device__ __forceinline__ void dot8_down_combine_block(const Dot8DownArgs &A, i
     float sh_d = 0.f, out_d = 0.f;
     if (tid < DC_RB) {
         out_d = out[d0 + tid];
-        if (shared) sh_d = shared[d0 + tid];
+        if (shared && !A.wsh) sh_d = shared[d0 + tid];
     }
     sw_u32x4 X[SW_NL];
 #pragma unroll
@@ -678,7 +680,11 @@ __device__ __forceinline__ void dot8_down_combine_block(const Dot8DownArgs &A, i
             acc = __builtin_fmaf(wk[aa], y, acc);
         }
         acc = acc * route_scale;
-        if (shared) acc = acc + sh_d;
+        if (A.wsh) {                                  // c/inkling.c:1176-1182: after the routed ranks
+            for (int j = 0; j < A.ns; j++) acc = __builtin_fmaf(A.wsh[j], shared[(int64_t)j * D + d0 + tid], acc);
+        } else if (shared) {
+            acc = acc + sh_d;
+        }
         out[d0 + tid] = out_d + acc;
     }
 }
@@ -692,14 +698,15 @@ __global__ __launch_bounds__(1024) void k_dot8_down_combine(Dot8DownArgs A) {
 }
 
 int sw_launch_q4_dot8_down_combine(hipStream_t st, SwQ4 W, const sw_u32x4 *hl, const float *hs, const int *sel, const float *w,
-                                   int K, float route_scale, const float *shared, float *out) {
+                                   int K, float route_scale, const float *shared, float *out, const float *wsh, int ns) {
     const int I = W.K, G = I / RG;
     int gsh;
     if (!dot8_shape_ok(I) || W.O % DC_RB || K <= 0 || K > 64 || K * run_lanes(G) > 1024 || !sw_q4_extent_ok(W) ||
         sw_q4_gsh(W, gsh)) return -1;
     const size_t lds = (size_t)K * DC_RB * dot8_nc(I) * 4;
     const int threads = (K * run_lanes(G) + 63) / 64 * 64;
-    const Dot8DownArgs A = {W, gsh, hl, hs, sel, w, K, route_scale, shared, out};
+    if (wsh && (!shared || ns <= 0)) return -1;
+    const Dot8DownArgs A = {W, gsh, hl, hs, sel, w, K, route_scale, shared, out, wsh, ns};
     if (dot8_c16(I)) SW_LAUNCH(k_dot8_down_combine<1>, dim3((unsigned)(W.O / DC_RB)), dim3(threads), lds, st, A);
     else SW_LAUNCH(k_dot8_down_combine<0>, dim3((unsigned)(W.O / DC_RB)), dim3(threads), lds, st, A);
     return hipGetLastError() == hipSuccess ? 0 : -1;

@@ -30,6 +30,7 @@
 // rows (coalesced 16-byte loads) and of up to TS tokens go through LDS, and
 // each token's chains stay in registers across tiles.
 #include "sw_hip.h"
+#include "sw_libm.h"
 
 #define LN_ROWS 16
 #define LN_CC 256                  // columns per LDS tile
@@ -77,6 +78,7 @@ struct LanesArgs {
     float *y;               // [S, O]
     int S, I, O;
     int gs;                 // I4G: columns per scale group (16..256, dividing I)
+    int ldx, ldy;           // row strides of x and y
 };
 
 // reduce16 over the 16 lanes of a row (xor partners stay inside the row)
@@ -126,7 +128,7 @@ __global__ __launch_bounds__(256) void k_lanes16(LanesArgs A) {
         }
         for (int p = tid; p < TS * cn; p += 256) {
             const int t = p / cn, cc = p - t * cn;
-            float v = t < ns ? A.x[(size_t)(s0 + t) * I + c0 + cc] : 0.f;
+            float v = t < ns ? A.x[(size_t)(s0 + t) * A.ldx + c0 + cc] : 0.f;
             xt[t * LN_CC + cc] = DP ? round_bf16_ne(v) : v;
         }
         __syncthreads();
@@ -189,7 +191,7 @@ __global__ __launch_bounds__(256) void k_lanes16(LanesArgs A) {
     for (int t = 0; t < TS; t++) {
         float sm = WK == WK_I4G ? acc[t] : reduce16_lanes(acc[t]);    // I4G: lane 0 holds the row's sum
         if (j == 0 && t < ns && o < O) {
-            const float *xs = A.x + (size_t)(s0 + t) * I;
+            const float *xs = A.x + (size_t)(s0 + t) * A.ldx;
             const uint8_t *wr = W + (size_t)o * rowb;
             if constexpr (WK == WK_I4) {               // the byte tail of c/moe_quant.h:105-108
                 for (int i = imain; i + 1 < I; i += 2) {
@@ -204,7 +206,7 @@ __global__ __launch_bounds__(256) void k_lanes16(LanesArgs A) {
                 }
             }
             if (WK != WK_I4G && A.scale) sm = sm * A.scale[o];
-            A.y[(size_t)(s0 + t) * O + o] = sm;
+            A.y[(size_t)(s0 + t) * A.ldy + o] = sm;
         }
     }
 }
@@ -224,17 +226,38 @@ static void launch_lanes(hipStream_t st, const LanesArgs &A) {
 // contract (bf16 weights, I % 32 == 0)
 int sw_launch_lanes16(hipStream_t st, const void *W, int wkind, int dp, const float *scale, const float *x, int S,
                       int I, int O, float *y, int gs) {
-    if (!W || !x || !y || S <= 0 || I <= 0 || O <= 0) return -1;
+    return sw_launch_lanes16_ld(st, W, wkind, dp, scale, x, I, S, I, O, y, O, gs);
+}
+
+int sw_launch_lanes16_ld(hipStream_t st, const void *W, int wkind, int dp, const float *scale, const float *x, int ldx,
+                         int S, int I, int O, float *y, int ldy, int gs) {
+    if (!W || !x || !y || S <= 0 || I <= 0 || O <= 0 || ldx < I || ldy < O) return -1;
     if (dp && (wkind != WK_BF16 || I % 32)) return -1;
     if ((wkind == WK_I4 || wkind == WK_I4G) && (I & 1)) return -1;
     if (wkind == WK_I4G && (gs < 16 || gs % 16 || gs > LN_CC || LN_CC % gs || I % gs)) return -1;
     if (wkind != WK_BF16 && !scale) return -1;
-    const LanesArgs A = {W, wkind == WK_BF16 ? nullptr : scale, x, y, S, I, O, gs};
+    const LanesArgs A = {W, wkind == WK_BF16 ? nullptr : scale, x, y, S, I, O, gs, ldx, ldy};
     if (dp) launch_lanes<WK_BF16, 1>(st, A);
     else if (wkind == WK_BF16) launch_lanes<WK_BF16, 0>(st, A);
     else if (wkind == WK_I8) launch_lanes<WK_I8, 0>(st, A);
     else if (wkind == WK_I4) launch_lanes<WK_I4, 0>(st, A);
     else if (wkind == WK_I4G) launch_lanes<WK_I4G, 0>(st, A);
     else return -1;
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+// ------------------------------------------------------------ SiLU-GLU ----
+// h = siluf(g) * u elementwise, siluf(x) = x / (1 + expf(-x)) with the glibc-exact
+// expf (c/moe_math.h:53): the bits of the CPU's `g[i] = siluf(g[i]) * u[i]`
+__global__ void k_silu_mul(const float *__restrict__ g, const float *__restrict__ u, int64_t n, float *__restrict__ h) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+        const float v = g[i];
+        h[i] = (v / (1.0f + sw_expf(-v))) * u[i];
+    }
+}
+
+int sw_launch_silu_mul(hipStream_t st, const float *g, const float *u, int64_t n, float *h) {
+    if (!g || !u || !h || n <= 0) return -1;
+    SW_LAUNCH(k_silu_mul, dim3((unsigned)sw_imin64((n + 255) / 256, 4096)), dim3(256), 0, st, g, u, n, h);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }

@@ -38,13 +38,15 @@ int sw_launch_chain_major(hipStream_t st, const void *W, int w_bf16, int E, int 
 template <int NPER>   // expert slots per lane: E <= 64 * NPER
 __global__ __launch_bounds__(64) void k_gate_topk(const float *__restrict__ logits, const float *__restrict__ scores,
                                                   int E, int K, int act, const float *__restrict__ bias, int use_bias,
-                                                  int norm, int *__restrict__ sel_all, float *__restrict__ w_all) {
+                                                  int norm, int *__restrict__ sel_all, float *__restrict__ w_all,
+                                                  SwGateOpt o) {
     __shared__ uint64_t tab[32];
     const int lane = threadIdx.x, s = blockIdx.x;
     int sk;
     float wk;
-    gate_topk_wave<NPER>((sw_act_softmax(act) ? logits : scores) + (int64_t)s * E, E, K, act, bias, use_bias, norm, tab, sk, wk);
-    if (lane < K) { sel_all[(int64_t)s * K + lane] = sk; w_all[(int64_t)s * K + lane] = wk; }
+    gate_topk_wave<NPER>((sw_act_softmax(act) ? logits : scores) + (int64_t)s * o.ld, E, K, act, bias, use_bias, norm, tab,
+                         sk, wk, o.ns, o.rs, o.wsh ? o.wsh + (int64_t)s * o.wshld : nullptr);
+    if (lane < K) { sel_all[(int64_t)s * K + lane] = sk; w_all[(int64_t)s * o.wld + lane] = wk; }
 }
 
 #include "sw_router.h"
@@ -58,9 +60,12 @@ __global__ __launch_bounds__(512) void k_router_logits(RouterArgs R) {
 int sw_launch_router_topk(hipStream_t st, const void *Wc, int w_bf16, const float *x, int S, int D, int E,
                           const float *logit_bias, float *logits, float *scores, int K, int route_act,
                           const float *corr_bias, int use_corr_bias, int norm_topk, int *sel, float *w,
-                          sw_u32x4 *xl, float *xs) {
+                          sw_u32x4 *xl, float *xs, const SwGateOpt *opt) {
     if (D % 128 || D > 16384 || E <= 0 || S <= 0) return -1;
-    if (sel && (E > TK_MAXE || K <= 0 || K > 64 || K > E)) return -1;   // (logits only: any number of rows)
+    // (logits only: any number of rows; with Inkling's ns shared gates the router has E + ns)
+    const int ns = opt ? opt->ns : 0;
+    if (sel && (E > TK_MAXE || K <= 0 || K > 64 || K > E)) return -1;
+    E += ns;
     if (route_act < 0 || route_act > SW_ROUTE_ACT_MAX || (sel && !sw_act_softmax(route_act) && !scores)) return -1;
     // four experts per block (wave 0; the others stage x) while that stays within 256 blocks,
     // else four per wave of eight
@@ -77,16 +82,18 @@ int sw_launch_router_topk(hipStream_t st, const void *Wc, int w_bf16, const floa
     }
     if (launch_err()) return -1;
     if (!sel) return 0;                              // logits only
-    return sw_launch_gate_topk(st, logits, scores, S, E, K, route_act, corr_bias, use_corr_bias, norm_topk, sel, w);
+    return sw_launch_gate_topk(st, logits, scores, S, E - ns, K, route_act, corr_bias, use_corr_bias, norm_topk, sel, w, opt);
 }
 
 int sw_launch_gate_topk(hipStream_t st, const float *logits, const float *scores, int S, int E, int K, int route_act,
-                        const float *corr_bias, int use_corr_bias, int norm_topk, int *sel, float *w) {
+                        const float *corr_bias, int use_corr_bias, int norm_topk, int *sel, float *w, const SwGateOpt *opt) {
     if (E <= 0 || E > TK_MAXE || S <= 0 || K <= 0 || K > 64 || K > E || route_act < 0 || route_act > SW_ROUTE_ACT_MAX) return -1;
     if (!sw_act_softmax(route_act) && !scores) return -1;
+    const SwGateOpt o = opt ? *opt : SwGateOpt{E, 0, 1.f, K, nullptr, 0};
+    if (o.ld < E + o.ns || o.wld < K || o.ns < 0 || o.ns > 64 || (o.ns && route_act != SW_ROUTE_INKLING)) return -1;
     const int nper = (E + 63) / 64;
 #define SW_GATE(NP) SW_LAUNCH(k_gate_topk<NP>, dim3((unsigned)S), dim3(64), 0, st, logits, scores, E, K, route_act, \
-                                       corr_bias, use_corr_bias, norm_topk, sel, w)
+                                       corr_bias, use_corr_bias, norm_topk, sel, w, o)
     if (nper <= 1) SW_GATE(1);
     else if (nper <= 2) SW_GATE(2);
     else if (nper <= 4) SW_GATE(4);
@@ -192,7 +199,7 @@ int sw_launch_bucket(hipStream_t st, const int *sel, int S, int K, int E, int *g
 // reference build compiles it (c/moe_block.h:124-142; c/laguna.c:761-782).
 __global__ void k_combine(const float *__restrict__ slots, const int *__restrict__ rowof, const float *__restrict__ w,
                           int S, int K, int D, float route_scale, const float *__restrict__ shared,
-                          float *__restrict__ out, int accumulate) {
+                          float *__restrict__ out, int accumulate, const float *__restrict__ wsh, int ns) {
     const int64_t n4 = (int64_t)S * (D / 4);
     for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n4; i += (int64_t)gridDim.x * blockDim.x) {
         const int64_t s = i / (D / 4), d = (i % (D / 4)) * 4;
@@ -215,7 +222,14 @@ __global__ void k_combine(const float *__restrict__ slots, const int *__restrict
         }
 #pragma unroll
         for (int c = 0; c < 4; c++) acc[c] = acc[c] * route_scale;
-        if (shared) {
+        if (wsh) {                                    // Inkling's gated shared experts, in order
+            for (int j = 0; j < ns; j++) {
+                const float wj = wsh[s * ns + j];
+                const sw_f32x4 sh = *(const sw_f32x4 *)(shared + (s * ns + j) * D + d);
+#pragma unroll
+                for (int c = 0; c < 4; c++) acc[c] = __builtin_fmaf(wj, sh[c], acc[c]);
+            }
+        } else if (shared) {
             const sw_f32x4 sh = *(const sw_f32x4 *)(shared + s * D + d);
 #pragma unroll
             for (int c = 0; c < 4; c++) acc[c] = acc[c] + sh[c];
@@ -233,11 +247,11 @@ __global__ void k_combine(const float *__restrict__ slots, const int *__restrict
 }
 
 int sw_launch_combine(hipStream_t st, const float *slots, const int *rowof, const float *w, int S, int K, int D,
-                      float route_scale, const float *shared, float *out, int accumulate) {
-    if (D % 4 || S <= 0) return -1;
+                      float route_scale, const float *shared, float *out, int accumulate, const float *wsh, int ns) {
+    if (D % 4 || S <= 0 || (wsh && (!shared || ns <= 0))) return -1;
     const int64_t n4 = (int64_t)S * (D / 4);
     SW_LAUNCH(k_combine, dim3((unsigned)sw_imin64((n4 + 255) / 256, 4096)), dim3(256), 0, st, slots, rowof, w,
-                       S, K, D, route_scale, shared, out, accumulate);
+                       S, K, D, route_scale, shared, out, accumulate, wsh, ns);
     return launch_err();
 }
 

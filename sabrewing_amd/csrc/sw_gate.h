@@ -100,7 +100,8 @@ __device__ __forceinline__ float lanef(float v, int l) {
 // pick a (rank order) in sk and its weight in wk.
 template <int NPER>   // expert slots per lane: E <= 64 * NPER
 __device__ void gate_topk_wave(const float *__restrict__ src, int E, int K, int act, const float *__restrict__ bias,
-                               int use_bias, int norm, uint64_t *tab, int &sk, float &wk) {
+                               int use_bias, int norm, uint64_t *tab, int &sk, float &wk, int ns = 0, float rs = 1.f,
+                               float *__restrict__ wsh = nullptr) {
     const int lane = threadIdx.x & 63;
     float v[NPER], b[NPER];
     // every load of the token issued before any is used (clamped indices)
@@ -215,6 +216,13 @@ __device__ void gate_topk_wave(const float *__restrict__ src, int E, int K, int 
         double tot = 0.0;
         for (int a = 0; a < K; a++) tot += (double)lanef(wk, a);
         wk = (float)((double)wk / tot);
+    } else if (act == SW_ROUTE_INKLING) {             // c/inkling.c:1040-1043: the picks' and the shared
+        float sum = 0.f;                              // gates' sigmoids summed in that order, each
+        for (int a = 0; a < K; a++) sum += lanef(wk, a);   // * (route_scale * global_scale) / sum
+        for (int j = 0; j < ns; j++) sum += src[E + j];
+        const float f = rs / sum;
+        wk = wk * f;
+        if (wsh && lane < ns) wsh[lane] = src[E + lane] * f;
     } else if (norm) {                                // renormalised: summed in rank order
         float sm = 0.f;
         for (int a = 0; a < K; a++) sm += lanef(wk, a);

@@ -112,7 +112,15 @@ __host__ __device__ inline bool sw_act_softmax(int act) { return act == 1 || act
 // the gates whose router scores are selected by moe_topk and weighted as moe_block's
 // sigmoid (c/moe_block.h:115-122): sigmoid, softplus, sqrt(softplus)
 __host__ __device__ inline bool sw_act_scores(int act) { return act == 0 || act == 2 || act == 5; }
-#define SW_ROUTE_ACT_MAX 5
+// the Inkling engine's routing (c/inkling.c:1027-1043): sigmoid scores selected as moe_topk
+// does, weights normalised over the K picks and the n_shared shared-expert gates
+#define SW_ROUTE_INKLING 6
+#define SW_ROUTE_ACT_MAX 6
+// extra layout of the gate + top-k: src rows of ld logits/scores (E routed first); with
+// ns > 0 (Inkling) the ns shared gates follow them, the weights end in * rs / sum over
+// the K picks and those gates, and the gates' weights go to wsh (row stride wshld);
+// the pick weights to w with row stride wld
+struct SwGateOpt { int ld, ns; float rs; int wld; float *wsh; int wshld; };
 // the upper bound of the passes of T packed rows in at most min(T, E) groups, tt tokens each
 __host__ __device__ inline int sw_npass_max(int T, int E, int tt) { return (T + (T < E ? T : E) * (tt - 1)) / tt; }
 // XCD-aware block order: launches deal consecutive block ids to the 8 XCDs in
@@ -198,10 +206,11 @@ struct SwBf16 {
 int sw_launch_router_topk(hipStream_t st, const void *Wc, int w_bf16, const float *x, int S, int D, int E,
                           const float *logit_bias, float *logits, float *scores, int K, int route_act,
                           const float *corr_bias, int use_corr_bias, int norm_topk, int *sel, float *w,
-                          sw_u32x4 *xl, float *xs);
+                          sw_u32x4 *xl, float *xs, const SwGateOpt *opt = nullptr);
 // gate + top-k of S tokens from their logits (act 1) or scores (one wave each)
 int sw_launch_gate_topk(hipStream_t st, const float *logits, const float *scores, int S, int E, int K, int route_act,
-                        const float *corr_bias, int use_corr_bias, int norm_topk, int *sel, float *w);
+                        const float *corr_bias, int use_corr_bias, int norm_topk, int *sel, float *w,
+                        const SwGateOpt *opt = nullptr);
 // counting sort by expert; with items non-null also the pass list of tt tokens (SwGroups)
 int sw_launch_bucket(hipStream_t st, const int *sel, int S, int K, int E, int *gexp, int *gbeg,
                      int *gcnt, int *G, int *grow, int *rowof, int tt, int *items, int *P);
@@ -222,6 +231,11 @@ int sw_launch_bf16_rows_x(hipStream_t st, SwBf16 W, const float *x, int S, float
 // vdpbf16ps lane order
 int sw_launch_lanes16(hipStream_t st, const void *W, int wkind, int dp, const float *scale, const float *x, int S,
                       int I, int O, float *y, int gs);
+// the same with row strides: x row s at x + s*ldx, y row s at y + s*ldy
+int sw_launch_lanes16_ld(hipStream_t st, const void *W, int wkind, int dp, const float *scale, const float *x, int ldx,
+                         int S, int I, int O, float *y, int ldy, int gs);
+// h[i] = siluf(g[i]) * u[i] with the glibc-exact expf (c/moe_math.h:53)
+int sw_launch_silu_mul(hipStream_t st, const float *g, const float *u, int64_t n, float *h);
 // activation limbs for the dot8 GEMV (k_dot8.hip): rows x[rows, K] f32 ->
 // xl[rows][K/32][SW_NL] (32 signed nibbles each), xs[rows][K/32] f32
 #define SW_NL 7
@@ -243,15 +257,20 @@ int sw_launch_q4_dot8_rows_tab(hipStream_t st, SwQ4 W, const SwTab *tab, const s
                                float *Y);
 // the dot8 down projection fused with the rank-order combine for one token
 // (h as limbs of the K packed rows in rank order)
+// (wsh non-null: ns gated shared outputs shared[ns][D], added after the ranks as
+// fma(wsh[j], shared[j], acc), Inkling's pass 3; route_scale 1)
 int sw_launch_q4_dot8_down_combine(hipStream_t st, SwQ4 W, const sw_u32x4 *hl, const float *hs, const int *sel, const float *w,
-                                   int K, float route_scale, const float *shared, float *out);
+                                   int K, float route_scale, const float *shared, float *out,
+                                   const float *wsh = nullptr, int ns = 0);
 // the int4 down projection fused with the rank-order combine for one token:
 // out[d] += (sum_a w[a] * down_{sel[a]}(h_a)[d]) * route_scale (+ shared[d])
 int sw_launch_q4_down_combine(hipStream_t st, SwQ4 W, const _Float16 *hplanes, const int *sel, const float *w, int K,
                               float route_scale, const float *shared, float *out);
 // out[s] (+)= route_scale * sum_a w[s,a] * slots[rowof[s,a]] (+ shared[s])
+// (wsh non-null: shared [S][ns][D] gated by wsh [S][ns] after the ranks, as above)
 int sw_launch_combine(hipStream_t st, const float *slots, const int *rowof, const float *w, int S, int K, int D,
-                      float route_scale, const float *shared, float *out, int accumulate);
+                      float route_scale, const float *shared, float *out, int accumulate,
+                      const float *wsh = nullptr, int ns = 0);
 // fused decode stages (k_dot8.hip): stage 1 = router logits/scores/limbs
 // and the shared expert's gate_up (sg null: none); stage 2 = routed gate_up
 // (sel non-null: one token's K picks, from sel or, with route_src, by a gate

@@ -25,7 +25,8 @@ def host_layer(be, orc, cfg, dl, seed, x, layer=0):
     D, I, E, gs = cfg.D, cfg.I, cfg.E, cfg.gs
     ngD, ngI = (D // gs, I // gs) if gs else (1, 1)
     ts = lambda tid: S.tensor_seed(seed, layer, tid)
-    r = orc.normal(E * D, ts(S.T_ROUTER), 0.02).reshape(E, D)
+    R, ns = cfg.router_rows, cfg.n_shared_experts
+    r = orc.normal(R * D, ts(S.T_ROUTER), 0.02).reshape(R, D)
     router = orc.to_bf16(r) if cfg.router_bf16 else r
     corr = np.zeros(E, np.float32) if cfg.use_corr_bias else None
     lb = S.zipf_bias(E, cfg.zipf, ts(S.T_ROUTER) ^ 0x5A5A) if cfg.zipf > 0 else None
@@ -35,9 +36,9 @@ def host_layer(be, orc, cfg, dl, seed, x, layer=0):
     dn_s = np.zeros((E * D, ngI), np.float32)
     sg = su = sd = None
     if cfg.shared_mode:
-        sg = be.d2h(dl.sg, (cfg.Is, D), np.uint16)
-        su = be.d2h(dl.su, (cfg.Is, D), np.uint16)
-        sd = be.d2h(dl.sd, (D, cfg.Is), np.uint16)
+        sg = be.d2h(dl.sg, (ns * cfg.Is, D), np.uint16)
+        su = be.d2h(dl.su, (ns * cfg.Is, D), np.uint16)
+        sd = be.d2h(dl.sd, (ns * D, cfg.Is), np.uint16)
     L = synth.Layer(D, I, cfg.Is, E, gs, cfg.router_bf16, router, corr, lb, gu_q.reshape(-1), gu_s.reshape(-1),
                     dn_q.reshape(-1), dn_s.reshape(-1), sg, su, sd)
     _, sel, _ = orc.route(synth.desc_of(cfg), L, x)

@@ -105,3 +105,31 @@ def test_callers_routing_golden(orc):
     assert all(len(set(r)) == K for r in sel)
     ok = np.isfinite(w).all(axis=1)
     assert np.allclose(w[ok].astype(np.float64).sum(axis=1), 1.0, atol=1e-6)
+
+
+def test_inkling_layer_golden(orc):
+    """The oracle's Inkling contract (route_act 6 + gated shared experts) reproduces the
+    Inkling engine's own moe() bit for bit, on both of its activation routes (fixture
+    written by tests/golden/make_inkling_golden.py from the compiled engine)"""
+    import importlib.util
+    from dataclasses import replace
+    spec = importlib.util.spec_from_file_location("mig", os.path.join(GOLD, "make_inkling_golden.py"))
+    mig = importlib.util.module_from_spec(spec); spec.loader.exec_module(mig)
+    g = np.load(os.path.join(GOLD, "inkling_moe.npz"))
+    assert int(g["seed"]) == mig.SEED and int(g["rows"]) == mig.ROWS
+    cfg, L, x = mig.layer_and_x(orc)
+    assert np.array_equal(bits(x), bits(g["x"]))
+    # the engine's route_scale * gate.global_scale, formed in float
+    d = synth.desc_of(replace(cfg, route_scale=float(np.float32(cfg.route_scale) * g["gscale"])))
+    z = np.zeros_like(x)
+    for mode, key in ((1, "out_idot"), (0, "out_f32")):
+        assert np.array_equal(bits(orc.moe_block_rows(d, L, x, z, mode)), bits(g[key])), key
+        assert np.array_equal(bits(orc.moe_group_rows(d, L, x, z, mode)), bits(g[key])), key
+    # the routing itself against a brute-force reading of c/inkling.c:1027-1043
+    lg, sel, w = orc.route(d, L, x)
+    assert lg.shape == (x.shape[0], cfg.E + cfg.n_shared) and w.shape == (x.shape[0], cfg.K + cfg.n_shared)
+    sig = lambda v: np.float32(1) / (np.float32(1) + np.exp(-v.astype(np.float64)).astype(np.float32))
+    for s in range(x.shape[0]):
+        key = sig(lg[s, :cfg.E]) + L.corr_bias
+        assert set(sel[s]) == set(np.argsort(-key, kind="stable")[:cfg.K])
+        assert abs(float(np.sum(w[s])) - d.route_scale) < 1e-5 * d.route_scale

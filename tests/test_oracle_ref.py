@@ -222,3 +222,44 @@ def test_sqrt_softplus_gate(orc, ref, rng):
         assert list(sel[s]) == order
         want = sc[order] / np.float32(sum(np.float32(v) for v in sc[order]))   # route_scale: after the combine
         assert np.allclose(w[s], want, rtol=2e-7, atol=0)
+
+
+INK_CHILD = """
+import sys, numpy as np
+sys.path.insert(0, sys.argv[1])
+from oracle.oracle import RefInkling
+z = np.load(sys.argv[2])
+from types import SimpleNamespace
+L = SimpleNamespace(**{k: (z[k] if z[k].size else None) for k in ("router", "corr_bias", "gu_q", "gu_s", "dn_q", "dn_s", "sg", "su", "sd")}, D=int(z["D"]), I=int(z["I"]))
+np.save(sys.argv[3], RefInkling().moe(int(z["E"]), int(z["K"]), int(z["ns"]), float(z["rs"]), float(z["gs"]), L, z["x"]))
+"""
+
+
+@pytest.mark.parametrize("S_", [1, 4])
+def test_inkling_moe_vs_engine(orc, tmp_path, S_):
+    """the oracle's Inkling layer against the engine's own moe() (oracle/_ref,
+    compiled from c/inkling.c), bit for bit: the engine's default int8 activation
+    route in this process, its f32 route (IDOT=0) in a child process (the engine
+    reads IDOT once)"""
+    import os, subprocess, sys
+    from oracle.oracle import RefInkling
+    if not RefInkling.available():
+        pytest.skip("compiled Inkling engine (oracle/_ref) not built")
+    cfg = cf.scaled(cf.INKLING, D=512, E=64, K=6, I=256, Is=256, name="inkling-pin")
+    gsc = 0.75
+    L = synth.make_layer(orc, cfg, 131 + S_, corr_bias_sigma=0.02)
+    x = synth.make_x(orc, cfg, 132, S_)
+    d = synth.desc_of(replace(cfg, route_scale=float(np.float32(cfg.route_scale) * np.float32(gsc))))
+    z = np.zeros_like(x)
+    if "IDOT" not in os.environ:
+        want = RefInkling().moe(cfg.E, cfg.K, cfg.n_shared, cfg.route_scale, gsc, L, x)
+        assert bits_equal(orc.moe_block_rows(d, L, x, z, 1), want)
+        assert bits_equal(orc.moe_group_rows(d, L, x, z, 1), want)
+    f = tmp_path / "layer.npz"
+    np.savez(f, x=x, D=L.D, I=L.I, E=cfg.E, K=cfg.K, ns=cfg.n_shared, rs=cfg.route_scale, gs=gsc,
+             **{k: getattr(L, k) for k in ("router", "corr_bias", "gu_q", "gu_s", "dn_q", "dn_s", "sg", "su", "sd")})
+    env = dict(os.environ, IDOT="0")
+    out = tmp_path / "out.npy"
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    subprocess.run([sys.executable, "-c", INK_CHILD, root, str(f), str(out)], env=env, check=True)
+    assert bits_equal(orc.moe_block_rows(d, L, x, z, 0), np.load(out))
