@@ -694,7 +694,8 @@ static int forward(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const floa
     // expert stage (no device-scope handoff); otherwise a gate + top-k launch
     // after the routing stage
     const bool in_experts = E <= 256 && S == 1 && (d->route_act == 1 || sw_act_scores(d->route_act));
-    // S == 1: the shared expert's gate_up and down run as extra blocks of stages 1 and 2;
+    // S == 1: the shared expert's gate_up and down run as extra blocks of stages 1 and 2
+    // (they fill the chip while the routed chain waits on its router and top-k);
     // S > 1: as kernels of their own over token tiles (the same arithmetic per token)
     const bool sh_in = sh && S == 1;
     const bool mf = S > 1 && use_mfma(T, E, D, I);
@@ -716,7 +717,8 @@ static int forward(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const floa
         { PROF("stage_experts");
           if (sw_launch_stage_experts(g_st, gu, f.xl, f.xs, SwGroups{}, I, f.hl, f.hs, f.sel, K,
                                       in_experts ? (sw_act_softmax(d->route_act) ? f.logits : f.scores) : nullptr, E, d->route_act,
-                                      w->corr_bias, d->use_corr_bias, d->norm_topk, f.w, sd, f.shh, S, Is, D, f.sout))
+                                      w->corr_bias, d->use_corr_bias, d->norm_topk, f.w, sh_in ? sd : nullptr, f.shh, S, Is, D,
+                                      f.sout))
               return fail_msg("expert stage launch"); }
         { PROF("q4_down_combine");
           if (sw_launch_q4_dot8_down_combine(g_st, dn, f.hl, f.hs, f.sel, f.w, K, rs_c, sh || gated ? f.sout : nullptr, out,

@@ -16,9 +16,8 @@
 // summed in rank order (c/moe_block.h:121-122).
 //
 // A pass is one wave-wide max of the order-preserving bits of key + 0.0
-// (invalid or taken experts are 0), then the lowest id holding that maximum
-// found with one ballot per slot: a larger key wins, equal keys go to the
-// lower id.
+// (invalid or taken experts are 0), then the lowest id holding that maximum:
+// a larger key wins, equal keys go to the lower id.
 #define TK_MAXE 1024
 
 // LDS ordering between the lanes of one wave (its LDS operations run in order)
@@ -98,6 +97,13 @@ __device__ __forceinline__ float lanef(float v, int l) {
 // src is the token's logits (a softmax act: 1, 3, 4) or its sigmoid/softplus scores; tab is
 // 32 words of LDS for the expf table (softmax).  On return lane a < K holds
 // pick a (rank order) in sk and its weight in wk.
+//
+// Lane l holds the NPER consecutive experts NPER l .. NPER l + NPER - 1, so a
+// lower lane holds lower ids and the lowest id holding the maximum is the
+// lowest such lane's first such slot: one ballot per pass.  Each lane keeps
+// its own best slot and the state it leaves when that slot is taken ready
+// before the wave maximum is known, so a pass is the maximum, one ballot and
+// the winner's update.
 template <int NPER>   // expert slots per lane: E <= 64 * NPER
 __device__ void gate_topk_wave(const float *__restrict__ src, int E, int K, int act, const float *__restrict__ bias,
                                int use_bias, int norm, uint64_t *tab, int &sk, float &wk, int ns = 0, float rs = 1.f,
@@ -109,29 +115,45 @@ __device__ void gate_topk_wave(const float *__restrict__ src, int E, int K, int 
     const bool hasb = use_bias && bias && act != 4;       // qwen35 selects on the probabilities alone
 #pragma unroll
     for (int i = 0; i < NPER; i++) {
-        const int e = min(lane + 64 * i, E - 1);
+        const int e = min(NPER * lane + i, E - 1);
         v[i] = src[e];
         b[i] = hasb ? bias[e] : 0.f;
     }
     TR_MARKK(0, 4);
+    // the sums of the softmax paths in expert order: lane l's slots, then lane l + 1's
+    auto sum_f = [&](float *p) {
+        float sum = 0.f;
+        for (int l = 0; l < 64 && NPER * l < E; l++) {
+#pragma unroll
+            for (int i = 0; i < NPER; i++)
+                if (NPER * l + i < E) sum += lanef(p[i], l);
+        }
+        return sum;
+    };
+    auto sum_d = [&](float *p) {
+        double sum = 0.0;
+        for (int l = 0; l < 64 && NPER * l < E; l++) {
+#pragma unroll
+            for (int i = 0; i < NPER; i++)
+                if (NPER * l + i < E) sum += (double)lanef(p[i], l);
+        }
+        return sum;
+    };
     if (act == 1) {                                   // softmax (c/moe_math.h:68-72)
         wave_sync();
         float mx = -__builtin_inff();
         bool any = false;
 #pragma unroll
         for (int i = 0; i < NPER; i++) {
-            const int e = lane + 64 * i;
+            const int e = NPER * lane + i;
             if (e < E && v[i] == v[i]) { mx = any ? fmaxf(mx, v[i]) : v[i]; any = true; }
         }
         for (int o = 32; o; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-        const float r0 = __shfl(v[0], 0);
+        const float r0 = __shfl(v[0], 0);             // expert 0
         if (r0 != r0) mx = r0;                        // a NaN in slot 0 propagates, as in the scan
 #pragma unroll
         for (int i = 0; i < NPER; i++) v[i] = sw_expf_t(v[i] - mx, tab);
-        double sum = 0.0;                             // in expert order, in double (every lane the same)
-#pragma unroll
-        for (int i = 0; i < NPER; i++)
-            for (int l = 0; l < 64 && l + 64 * i < E; l++) sum += (double)lanef(v[i], l);
+        const double sum = sum_d(v);                  // in expert order, in double (every lane the same)
         const float inv = (float)(1.0 / sum);
 #pragma unroll
         for (int i = 0; i < NPER; i++) v[i] = v[i] * inv;
@@ -145,71 +167,72 @@ __device__ void gate_topk_wave(const float *__restrict__ src, int E, int K, int 
         float mx = act == 3 ? -1e30f : -__builtin_inff();
 #pragma unroll
         for (int i = 0; i < NPER; i++) {
-            const int e = lane + 64 * i;
+            const int e = NPER * lane + i;
             if (e < E && v[i] > mx) mx = v[i];
         }
         for (int o = 32; o; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
 #pragma unroll
         for (int i = 0; i < NPER; i++) v[i] = sw_expf_t(v[i] - mx, tab);
         if (act == 3) {
-            float sum = 0.f;
-#pragma unroll
-            for (int i = 0; i < NPER; i++)
-                for (int l = 0; l < 64 && l + 64 * i < E; l++) sum += lanef(v[i], l);
+            const float sum = sum_f(v);
 #pragma unroll
             for (int i = 0; i < NPER; i++) v[i] = v[i] / sum;
         } else {
-            double sum = 0.0;
-#pragma unroll
-            for (int i = 0; i < NPER; i++)
-                for (int l = 0; l < 64 && l + 64 * i < E; l++) sum += (double)lanef(v[i], l);
+            const double sum = sum_d(v);
 #pragma unroll
             for (int i = 0; i < NPER; i++) v[i] = (float)((double)v[i] / sum);
         }
     }
     uint32_t ko[NPER];                                // order key, 0 = invalid or taken (valid keys order above 0)
-    bool fr[NPER];
+    uint32_t frm = 0;                                 // bit i: slot i is an expert with an invalid key
 #pragma unroll
     for (int i = 0; i < NPER; i++) {
-        const int e = lane + 64 * i;
+        const int e = NPER * lane + i;
         const float key = v[i] + b[i];
-        fr[i] = e < E;
         ko[i] = (e < E && key > -1e30f) ? ord_f32(key) : 0u;
+        if (e < E && ko[i] == 0u) frm |= 1u << i;
     }
     TR_MARKK(0, 5);
     sk = 0; wk = 0.f;
-    for (int a = 0; a < K; a++) {
+    // the passes that find a valid key (as many as there are valid experts), then the
+    // all-invalid fallback for the rest: by then every valid expert is taken, so the
+    // unselected ones are those of frm
+    int nv = 0;
+#pragma unroll
+    for (int i = 0; i < NPER; i++) nv += __builtin_popcountll(__ballot(ko[i] != 0u));
+    const int kv = K < nv ? K : nv;
+    int a = 0;
+    for (; a < kv; a++) {
+        // this lane's best: the largest key, its first slot and that slot's weight
         uint32_t lm = ko[0];
 #pragma unroll
         for (int i = 1; i < NPER; i++) lm = lm > ko[i] ? lm : ko[i];
-        const uint32_t m = wave_umax(lm);
-        int bi = 0x7fffffff;
-        if (m != 0u) {                                // the lowest id holding the maximum
+        int ls = NPER - 1;
 #pragma unroll
-            for (int i = NPER - 1; i >= 0; i--) {
-                const unsigned long long bal = __ballot(ko[i] == m);
-                if (bal) bi = 64 * i + __builtin_ctzll(bal);
-            }
-        } else {                                      // nothing valid left: the lowest unselected id
-#pragma unroll
-            for (int i = NPER - 1; i >= 0; i--) {
-                const unsigned long long bal = __ballot(fr[i]);
-                if (bal) bi = 64 * i + __builtin_ctzll(bal);
-            }
-            if (bi >= E) bi = 0;
-        }
-        const int slot = bi >> 6, bl = bi & 63;       // uniform
+        for (int i = NPER - 2; i >= 0; i--) ls = ko[i] == lm ? i : ls;
         float vs = v[0];
 #pragma unroll
-        for (int i = 1; i < NPER; i++)
-            if (i == slot) vs = v[i];
+        for (int i = 1; i < NPER; i++) vs = ls == i ? v[i] : vs;
+        const uint32_t m = wave_umax(lm);
+        const int bl = __builtin_ctzll(__ballot(lm == m));    // the lowest lane holding the maximum
+        const int slot = __builtin_amdgcn_readlane(ls, bl);
         const float wb = lanef(vs, bl);               // the pick's weight: its unbiased score
-        if (lane == bl) {
+        const bool win = lane == bl;
 #pragma unroll
-            for (int i = 0; i < NPER; i++)
-                if (i == slot) { ko[i] = 0u; fr[i] = false; }
-        }
-        if (lane == a) { sk = bi; wk = wb; }
+        for (int i = 0; i < NPER; i++) ko[i] = (win && ls == i) ? 0u : ko[i];
+        if (lane == a) { sk = NPER * bl + slot; wk = wb; }
+    }
+    for (; a < K; a++) {                              // nothing valid left: the lowest unselected id
+        const unsigned long long bal = __ballot(frm != 0u);
+        const int ls = frm ? __builtin_ctz(frm) : 0;
+        const int bl = bal ? __builtin_ctzll(bal) : 0;
+        float vs = v[0];
+#pragma unroll
+        for (int i = 1; i < NPER; i++) vs = ls == i ? v[i] : vs;
+        const int slot = __builtin_amdgcn_readlane(ls, bl);
+        const float wb = lanef(vs, bl);
+        if (lane == bl) frm &= ~(1u << ls);
+        if (lane == a) { sk = NPER * bl + slot; wk = wb; }
     }
     TR_MARKK(0, 6);
     if (act == 4) {                                   // qwen35: always, in double (c/qwen35.c:585-587)

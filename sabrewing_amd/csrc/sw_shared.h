@@ -156,7 +156,9 @@ __host__ __device__ inline size_t sh_glu_lds(int D) {
 __host__ __device__ inline int sh_glu_blocks(int S, int Is, int TT) { return (Is / SH_GLU_O) * ((S + TT - 1) / TT); }
 
 // shared expert down: SH_DN_O output rows d per block, out[tok][d] (f32)
+#ifndef SH_DN_O
 #define SH_DN_O 32
+#endif
 template <int TT>
 __device__ __forceinline__ void sh_down_block(const uint16_t *__restrict__ Wd, const float *__restrict__ h, int S, int Is,
                                               int D, float *__restrict__ out, int bid, float *red) {
