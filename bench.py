@@ -61,7 +61,8 @@ def kernel_bytes(cfg, S, G):
              "stage_experts": gu_w + S * limb(D) + T * limb(I) + sh_dn + S * Is * 4 + S * D * 4,
              "q4_down_combine": dn_w + T * limb(I) + T * 8 + 2 * D * 4 + (D * 4 if cfg.shared_mode else 0)}
     else:             # its own kernels over token tiles
-        b = {"stage_route": route, "gate_topk": 2 * S * E * 4 + T * 8, "bucket": T * 4 * 3 + E * 12,
+        b = {"stage_route": route, "router_tiles": cfg.router_bytes() + S * D * 4 + 2 * S * E * 4,
+             "limbs": S * D * 4 + S * limb(D), "gate_topk": 2 * S * E * 4 + T * 8, "bucket": T * 4 * 3 + E * 12,
              "stage_experts": gu_w + S * limb(D) + T * limb(I),
              "q4_down": dn_w + T * limb(I) + T * D * 4,
              "combine": T * D * 4 + 2 * S * D * 4 + (S * D * 4 if cfg.shared_mode else 0) + T * 8}

@@ -467,7 +467,8 @@ struct FwdScratch {
     int *sel, *gexp, *gbeg, *gcnt, *G, *grow, *rowof, *items, *P;
     sw_u32x4 *hl;           // h of every packed row as dot8 limbs
     float *hs;
-    float *shh;             // shared expert h [S, Is]
+    float *shh;             // shared expert h [S, Is] (one token: f32)
+    uint16_t *shx, *shp;    // a batch's shared expert: the bf16 parts of x [S][D/32][3][32] and of h
     sw_u32x4 *xl;
     float *xs;
     uint32_t *xd, *hd;      // MFMA digits of x [S][D/32] and of h [T][I/32] (prefill)
@@ -528,6 +529,10 @@ static int carve_fwd(const LagHipMoeDesc *d, int S, FwdScratch &f, const Scratch
     size_t o_sh = 0, o_so = 0, o_su = 0;
     if (d->shared_mode) { o_sh = cv.take((size_t)S * nsx * Is * 4); o_so = cv.take((size_t)S * nsx * D * 4); }
     if (d->shared_mode == LAG_HIP_SHARED_GATED) o_su = cv.take((size_t)S * nsx * Is * 4);
+    // the batch kernels of the unscaled shared expert (also the IDOT forward's at S = 1)
+    const bool shb = d->shared_mode == LAG_HIP_SHARED_UNSCALED && (S > 1 || idot);
+    size_t o_shx = 0, o_shp = 0;
+    if (shb) { o_shx = cv.take((size_t)S * D * 6); o_shp = cv.take((size_t)S * Is * 6); }
     const size_t o_xl = cv.take((size_t)S * (D / 32) * SW_NL * 16), o_xs = cv.take((size_t)S * (D / 32) * 4);
     size_t o_xd = 0, o_xds = 0, o_hd = 0, o_hds = 0;
     if (S > 1) {
@@ -563,6 +568,8 @@ static int carve_fwd(const LagHipMoeDesc *d, int S, FwdScratch &f, const Scratch
     f.shh = d->shared_mode ? (float *)(A + o_sh) : nullptr;
     f.sout = d->shared_mode ? (float *)(A + o_so) : nullptr;
     f.shu = d->shared_mode == LAG_HIP_SHARED_GATED ? (float *)(A + o_su) : nullptr;
+    f.shx = shb ? (uint16_t *)(A + o_shx) : nullptr;
+    f.shp = shb ? (uint16_t *)(A + o_shp) : nullptr;
     f.wsh = (float *)(A + o_wsh);
     f.xl = (sw_u32x4 *)(A + o_xl); f.xs = (float *)(A + o_xs);
     f.xd = S > 1 ? (uint32_t *)(A + o_xd) : nullptr; f.xds = S > 1 ? (float *)(A + o_xds) : nullptr;
@@ -571,6 +578,23 @@ static int carve_fwd(const LagHipMoeDesc *d, int S, FwdScratch &f, const Scratch
 }
 
 
+// A prefill-sized batch's router, and a head-sized one (R rows), run over token tiles
+// (each weight slice read once per tile, the same bits as the per-token blocks), then
+// the limbs of x as a kernel of their own; smaller batches keep the fused routing stage
+// (B = 32: 11 us against 22 + 4 us tiled, the tiles' x chunks waiting on one wave per CU)
+static bool router_tiled(int S, int D, int R) { return S >= 2 && D % 256 == 0 && (S >= 512 || R >= 4096); }
+static int router_batch(const void *Wc, int w_bf16, const float *x, int S, int D, int R, const float *lbias,
+                        float *logits, float *scores, int act, sw_u32x4 *xl, float *xs) {
+    { PROF("router_tiles");
+      if (sw_launch_router_tiles(g_st, Wc, w_bf16, x, S, D, R, lbias, logits, scores, act))
+          return fail_msg("router launch (shape unsupported?)"); }
+    if (xl) {
+        PROF("limbs");
+        if (sw_launch_limbs(g_st, x, S, D, xl, xs)) return fail_msg("limbs launch");
+    }
+    return 0;
+}
+
 // router logits (+ scores); with sel, gate + top-k; with xl, the dot8 limbs of x
 static int route_dev(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const float *x, int S, float *logits,
                      float *scores, int *sel, float *wts, sw_u32x4 *xl = nullptr, float *xs = nullptr) {
@@ -578,6 +602,13 @@ static int route_dev(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const fl
     // Inkling: the picks' weights then the shared gates' in one row of K + ns
     const int ns = ink_ns(d), K = d->topk;
     const SwGateOpt o = {router_rows(d), ns, d->route_scale, K + ns, ns ? wts + K : nullptr, K + ns};
+    if (router_tiled(S, d->hidden, router_rows(d))) {
+        if (router_batch(w->router, d->router_bf16, x, S, d->hidden, router_rows(d), w->logit_bias, logits, scores,
+                         d->route_act, xl, xs)) return -1;
+        if (sel && sw_launch_gate_topk(g_st, logits, scores, S, d->n_experts, K, d->route_act, w->corr_bias,
+                                       d->use_corr_bias, d->norm_topk, sel, wts, &o)) return fail_msg("gate/top-k launch");
+        return 0;
+    }
     if (sw_launch_router_topk(g_st, w->router, d->router_bf16, x, S, d->hidden, d->n_experts, w->logit_bias, logits,
                               scores, d->topk, d->route_act, w->corr_bias, d->use_corr_bias, d->norm_topk,
                               sel, wts, xl, xs, &o)) return fail_msg("router launch");
@@ -591,6 +622,17 @@ static int gate_dev(const LagHipMoeDesc *d, const LagHipMoeWeights *w, int S, Fw
     const SwGateOpt o = {router_rows(d), ns, d->route_scale, d->topk, ns ? f.wsh : nullptr, ns};
     if (sw_launch_gate_topk(g_st, f.logits, f.scores, S, d->n_experts, d->topk, d->route_act, w->corr_bias,
                             d->use_corr_bias, d->norm_topk, f.sel, f.w, &o)) return fail_msg("gate/top-k launch");
+    return 0;
+}
+
+// a batch's unscaled shared expert, gate_up: the parts of x (unless the routing stage
+// wrote them), then h's parts (f.shp)
+static int shared_glu_batch(const LagHipMoeWeights *w, const float *x, int S, int D, int Is, FwdScratch &f,
+                            bool have_parts = false) {
+    PROF("shared_glu");
+    if (!have_parts && sw_launch_sh_parts(g_st, x, S, D, f.shx)) return fail_msg("shared parts launch");
+    if (sw_launch_sh_glu(g_st, (const uint16_t *)w->sg, (const uint16_t *)w->su, f.shx, S, D, Is, f.shp))
+        return fail_msg("shared gate_up launch (shape unsupported?)");
     return 0;
 }
 
@@ -629,14 +671,15 @@ static int forward_idot(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const
     SwQ4 gu = {(const uint8_t *)w->gu_q, w->gu_s, 2 * I, D, 0, E};
     SwQ4 dn = {(const uint8_t *)w->dn_q, w->dn_s, D, I, 0, E};
     const bool sh = d->shared_mode == LAG_HIP_SHARED_UNSCALED, gated = d->shared_mode == LAG_HIP_SHARED_GATED;
-    { PROF("stage_route");
-      if (sw_launch_stage_route(g_st, w->router, d->router_bf16, x, S, D, router_rows(d), w->logit_bias, f.logits, f.scores,
-                                d->route_act, nullptr, f.xs, nullptr, nullptr, Is, f.shh)) return fail_msg("routing stage launch"); }
-    if (sh) {
-        PROF("shared_glu");
-        if (sw_launch_sh_glu(g_st, (const uint16_t *)w->sg, (const uint16_t *)w->su, x, S, D, Is, f.shh))
-            return fail_msg("shared gate_up launch");
+    if (router_tiled(S, D, router_rows(d))) {
+        if (router_batch(w->router, d->router_bf16, x, S, D, router_rows(d), w->logit_bias, f.logits, f.scores,
+                         d->route_act, nullptr, nullptr)) return -1;
+    } else {
+        PROF("stage_route");
+        if (sw_launch_stage_route(g_st, w->router, d->router_bf16, x, S, D, router_rows(d), w->logit_bias, f.logits, f.scores,
+                                  d->route_act, nullptr, f.xs, nullptr, nullptr, Is, f.shh)) return fail_msg("routing stage launch");
     }
+    if (sh && shared_glu_batch(w, x, S, D, Is, f)) return -1;
     if (gated && gated_shared(d, w, x, S, f)) return -1;
     if (gate_dev(d, w, S, f)) return -1;
     { PROF("bucket");
@@ -649,7 +692,7 @@ static int forward_idot(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const
     { PROF("idot_glu"); if (sw_launch_idot_glu(g_st, gu, f.xq, f.xqs, g, I, f.hf)) return fail_msg("IDOT gate_up launch"); }
     if (sh) {
         PROF("shared_down");
-        if (sw_launch_sh_down(g_st, (const uint16_t *)w->sd, f.shh, S, Is, D, f.sout)) return fail_msg("shared down launch");
+        if (sw_launch_sh_down(g_st, (const uint16_t *)w->sd, f.shp, S, Is, D, f.sout)) return fail_msg("shared down launch");
     }
     { PROF("idot_quant"); if (sw_launch_idot_quant(g_st, f.hf, S * K, I, f.hq, f.hqs)) return fail_msg("IDOT quant launch"); }
     { PROF("idot_down"); if (sw_launch_idot_rows(g_st, dn, f.hq, f.hqs, gd, f.slots)) return fail_msg("IDOT down launch"); }
@@ -699,19 +742,22 @@ static int forward(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const floa
     // S > 1: as kernels of their own over token tiles (the same arithmetic per token)
     const bool sh_in = sh && S == 1;
     const bool mf = S > 1 && use_mfma(T, E, D, I);
-    { PROF("stage_route");
-      if (sw_launch_stage_route(g_st, w->router, d->router_bf16, x, S, D, router_rows(d), w->logit_bias, f.logits, f.scores,
-                                d->route_act, mf ? nullptr : f.xl, f.xs, sh_in ? sg : nullptr, su, Is, f.shh))
-          return fail_msg("routing stage launch"); }
+    if (router_tiled(S, D, router_rows(d))) {
+        if (router_batch(w->router, d->router_bf16, x, S, D, router_rows(d), w->logit_bias, f.logits, f.scores,
+                         d->route_act, mf ? nullptr : f.xl, f.xs)) return -1;
+    } else {
+        PROF("stage_route");
+        if (sw_launch_stage_route(g_st, w->router, d->router_bf16, x, S, D, router_rows(d), w->logit_bias, f.logits, f.scores,
+                                  d->route_act, mf ? nullptr : f.xl, f.xs, sh_in ? sg : nullptr, su, Is, f.shh,
+                                  sh && !sh_in ? f.shx : nullptr))
+            return fail_msg("routing stage launch");
+    }
     if (gated && gated_shared(d, w, x, S, f)) return -1;
     if (mf) {
         PROF("digits");
         if (sw_launch_digits(g_st, x, S, D, f.xd, f.xds)) return fail_msg("digits launch");
     }
-    if (sh && !sh_in) {
-        PROF("shared_glu");
-        if (sw_launch_sh_glu(g_st, sg, su, x, S, D, Is, f.shh)) return fail_msg("shared gate_up launch");
-    }
+    if (sh && !sh_in && shared_glu_batch(w, x, S, D, Is, f, !router_tiled(S, D, router_rows(d)))) return -1;
     if (!in_experts && gate_dev(d, w, S, f)) return -1;
     if (S == 1) {                        // one token: its K picks in rank order, fused down + combine
         { PROF("stage_experts");
@@ -734,7 +780,7 @@ static int forward(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const floa
           if (sw_launch_mf_glu(g_st, gu, f.xd, f.xds, g, I, f.hd, f.hds)) return fail_msg("MFMA gate_up launch"); }
         if (sh) {
             PROF("shared_down");
-            if (sw_launch_sh_down(g_st, sd, f.shh, S, Is, D, f.sout)) return fail_msg("shared down launch");
+            if (sw_launch_sh_down(g_st, sd, f.shp, S, Is, D, f.sout)) return fail_msg("shared down launch");
         }
         SwGroups gd = g;
         gd.grow = nullptr;                 // the down reads the packed rows directly
@@ -756,7 +802,7 @@ static int forward(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const floa
               return fail_msg("expert stage launch"); }
         if (sh) {
             PROF("shared_down");
-            if (sw_launch_sh_down(g_st, sd, f.shh, S, Is, D, f.sout)) return fail_msg("shared down launch");
+            if (sw_launch_sh_down(g_st, sd, f.shp, S, Is, D, f.sout)) return fail_msg("shared down launch");
         }
         SwGroups gd = g;
         gd.grow = nullptr;                 // the down reads the packed rows directly
@@ -826,8 +872,10 @@ extern "C" int lag_hip_argmax(const float *logits, int S, int V, int *tok) {
 extern "C" int lag_hip_head_argmax(const void *Wc, int w_bf16, const float *x, int S, int D, int V, float *logits, int *tok) {
     if (!g_ok || fault_injected() || !Wc || !x || !logits || S <= 0 || V <= 0) return -1;
     { PROF("head_logits");
-      if (sw_launch_router_topk(g_st, Wc, w_bf16, x, S, D, V, nullptr, logits, nullptr, 1, 1, nullptr, 0, 0, nullptr,
-                                nullptr, nullptr, nullptr)) return fail_msg("head launch (shape unsupported?)"); }
+      if (router_tiled(S, D, V) ? sw_launch_router_tiles(g_st, Wc, w_bf16, x, S, D, V, nullptr, logits, nullptr, 1)
+                             : sw_launch_router_topk(g_st, Wc, w_bf16, x, S, D, V, nullptr, logits, nullptr, 1, 1, nullptr, 0, 0,
+                                                     nullptr, nullptr, nullptr, nullptr))
+          return fail_msg("head launch (shape unsupported?)"); }
     if (tok) {
         PROF("argmax");
         if (sw_launch_argmax(g_st, logits, S, V, tok)) return fail_msg("argmax launch");

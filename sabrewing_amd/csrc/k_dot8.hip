@@ -722,21 +722,21 @@ int sw_launch_q4_dot8_down_combine(hipStream_t st, SwQ4 W, const sw_u32x4 *hl, c
 // instead of running as its own launches.
 static size_t lds_max(size_t a, size_t b) { return a > b ? a : b; }
 
-struct ShGluArgs { const uint16_t *Wg, *Wu; const float *x; int S, D, Is; float *h; };
-struct ShDownArgs { const uint16_t *Wd; const float *h; int S, Is, D; float *out; };
+struct ShGluArgs { const uint16_t *Wg, *Wu; const float *x; int D, Is; float *h; };
+struct ShDownArgs { const uint16_t *Wd; const float *h; int Is, D; float *out; };
 
-template <int BF16, int TT, int ONE>
+template <int BF16, int ONE>
 __global__ __launch_bounds__(SH_NT) void k_stage_route(RouterArgs R, int nbr, int S, ShGluArgs G) {
     extern __shared__ __align__(16) float smem[];
     TR_BEGIN();
     const int b = blockIdx.x;
     if (b < nbr * S) router_block<BF16, ONE>(R, b % nbr, b / nbr, nbr, smem);
-    else sh_glu_block<TT>(G.Wg, G.Wu, G.x, G.S, G.D, G.Is, G.h, b - nbr * S, smem);
+    else sh_glu_block(G.Wg, G.Wu, G.x, G.D, G.Is, G.h, b - nbr * S, smem);
     TR_END(0);
 }
 
-// TTG: tokens per pass of the routed gate_up; TTS: of the shared down
-template <int PF, int PICK, int NP, int TTG, int TTS, int C16, int RO>
+// TTG: tokens per pass of the routed gate_up
+template <int PF, int PICK, int NP, int TTG, int C16, int RO>
 __global__ __launch_bounds__(DG_NT, PICK ? 1 : 4) void k_stage_experts(Dot8GluArgs A, int nbx, int nglu, ShDownArgs Sd) {
     extern __shared__ __align__(16) float smem[];
     TR_BEGIN();
@@ -745,51 +745,48 @@ __global__ __launch_bounds__(DG_NT, PICK ? 1 : 4) void k_stage_experts(Dot8GluAr
         const int w = PICK == 0 && A.grp.items ? sw_xcd_work(b, nglu) : b;
         dot8_glu_block<PF, PICK, NP, TTG, C16, RO>(A, w % nbx, w / nbx, smem);
     } else {
-        sh_down_block<TTS>(Sd.Wd, Sd.h, Sd.S, Sd.Is, Sd.D, Sd.out, b - nglu, smem);
+        sh_down_block(Sd.Wd, Sd.h, Sd.Is, Sd.D, Sd.out, b - nglu, smem);
     }
     TR_END(1);
 }
-template <int PICK, int NP, int TTG, int TTS, int RO = 32>
+template <int PICK, int NP, int TTG, int RO = 32>
 struct StageL {
     template <int PF, int C16>
     struct L {
         static void go(dim3 grid, size_t lds, hipStream_t st, const Dot8GluArgs &A, int nbx, int nglu, const ShDownArgs &Sd) {
-            SW_LAUNCH((k_stage_experts<PF, PICK, NP, TTG, TTS, C16, RO>), grid, dim3(DG_NT), lds, st, A, nbx, nglu, Sd);
+            SW_LAUNCH((k_stage_experts<PF, PICK, NP, TTG, C16, RO>), grid, dim3(DG_NT), lds, st, A, nbx, nglu, Sd);
         }
     };
 };
 
-template <int TT, int ONE>
+template <int ONE>
 static void launch_stage_route(int bf16, dim3 grid, size_t lds, hipStream_t st, const RouterArgs &R, int nbr, int S,
                                const ShGluArgs &G) {
-    if (bf16) SW_LAUNCH((k_stage_route<1, TT, ONE>), grid, dim3(SH_NT), lds, st, R, nbr, S, G);
-    else SW_LAUNCH((k_stage_route<0, TT, ONE>), grid, dim3(SH_NT), lds, st, R, nbr, S, G);
+    if (bf16) SW_LAUNCH((k_stage_route<1, ONE>), grid, dim3(SH_NT), lds, st, R, nbr, S, G);
+    else SW_LAUNCH((k_stage_route<0, ONE>), grid, dim3(SH_NT), lds, st, R, nbr, S, G);
 }
 
 // stage 1: router logits / scores and the limbs of x, and the shared
 // expert's gate_up when sg is non-null
 int sw_launch_stage_route(hipStream_t st, const void *Wc, int w_bf16, const float *x, int S, int D, int E,
                           const float *logit_bias, float *logits, float *scores, int route_act, sw_u32x4 *xl, float *xs,
-                          const uint16_t *sg, const uint16_t *su, int Is, float *sh_h) {
+                          const uint16_t *sg, const uint16_t *su, int Is, float *sh_h, uint16_t *xp) {
     if (D % 128 || E <= 0 || S <= 0 || route_act < 0 || route_act > SW_ROUTE_ACT_MAX || (!sw_act_softmax(route_act) && !scores)) return -1;
+    if (xp && !sh_shape_ok(D)) return -1;
     const int one = router_one(S, E);
     const size_t rl = router_lds(D);
     if (rl > 65536 || D > 4 * RT_XB * (one ? SH_NT - 64 : SH_NT)) return -1;
     const int nbr = (E + router_epb(one, SH_NT) - 1) / router_epb(one, SH_NT);
-    const RouterArgs R = {Wc, x, D, E, logit_bias, logits, route_act, scores, xl, xs};
-    const ShGluArgs G = {sg, su, x, S, D, Is, sh_h};
-    const int TT = S >= 2 && sg ? SH_TT : 1;
-    const int nsh = sg ? sh_glu_blocks(S, Is, TT) : 0;
-    if (sg && (Is % SH_GLU_O || !sh_shape_ok(D))) return -1;
+    const RouterArgs R = {Wc, x, D, E, logit_bias, logits, route_act, scores, xl, xs, xp};
+    const ShGluArgs G = {sg, su, x, D, Is, sh_h};
+    // the shared expert's blocks are single-token jobs
+    if (sg && (S != 1 || !su || !sh_h || Is % SH_GLU_O || !sh_shape_ok(D))) return -1;
+    const int nsh = sg ? sh_glu_blocks(Is) : 0;
     const dim3 grid((unsigned)(nbr * S + nsh));
-    const size_t lds = lds_max(rl, sg ? (TT == SH_TT ? sh_glu_lds<SH_TT>(D) : sh_glu_lds<1>(D)) : 0);
-    if (TT == SH_TT) {
-        if (one) launch_stage_route<SH_TT, 1>(w_bf16, grid, lds, st, R, nbr, S, G);
-        else launch_stage_route<SH_TT, 0>(w_bf16, grid, lds, st, R, nbr, S, G);
-    } else {
-        if (one) launch_stage_route<1, 1>(w_bf16, grid, lds, st, R, nbr, S, G);
-        else launch_stage_route<1, 0>(w_bf16, grid, lds, st, R, nbr, S, G);
-    }
+    const size_t lds = lds_max(rl, sg ? sh_glu_lds(D) : 0);
+    if (lds > 65536) return -1;
+    if (one) launch_stage_route<1>(w_bf16, grid, lds, st, R, nbr, S, G);
+    else launch_stage_route<0>(w_bf16, grid, lds, st, R, nbr, S, G);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
@@ -807,33 +804,33 @@ int sw_launch_stage_experts(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, const fl
     if (picks && (S != 1 || K <= 0 || K > 64)) return -1;
     if (picks && route_src && (E <= 0 || E > 256 || K > E || !w || !(act == 1 || sw_act_scores(act)))) return -1;
     if (!picks && g.ngroups_max <= 0) return -1;
-    if (sd && (D % SH_DN_O || !sh_shape_ok(Is))) return -1;
+    // the shared expert's down blocks are single-token jobs
+    if (sd && (S != 1 || !sh_h || !sh_out || D % SH_DN_O || !sh_shape_ok(Is))) return -1;
     const int nbx = picks ? K : g.ngroups_max;
-    const int RO = picks || (sd && S >= 2) ? 32 : dg_ro(I);   // outputs per gate_up block
+    const int RO = picks ? 32 : dg_ro(I);             // outputs per gate_up block
     const int nglu = nbx * (I / RO);
-    const int TTS = S >= 2 && sd ? SH_TT : 1;         // (no shared blocks: the smaller instance)
-    const int nsh = sd ? sh_down_blocks(S, D, TTS) : 0;
+    const int nsh = sd ? sh_down_blocks(D) : 0;
     const DotRoute rt = route_src ? DotRoute{route_src, bias, E, K, act, use_bias, norm, w} : DotRoute{};
     const Dot8GluArgs A = {W, gsh, xl, xs, g, I, hl, hs, sel, rt};
-    const ShDownArgs Sd = {sd, sh_h, S, Is, D, sh_out};
+    const ShDownArgs Sd = {sd, sh_h, Is, D, sh_out};
     const dim3 grid((unsigned)(nglu + nsh));
-    const size_t shl = sd ? (TTS == SH_TT ? sh_down_lds<SH_TT>(Is) : sh_down_lds<1>(Is)) : 0;
+    const size_t shl = sd ? sh_down_lds(Is) : 0;
+    if (shl > 65536) return -1;
     const int pf0 = dg_pf_glu(W.K), c16 = dot8_c16(W.K);
     // groups: a 4-step ring, two blocks per CU (four waves per SIMD, 128 VGPRs); an
     // 8-step ring also fits but measured slower at B=32 (224 vs 215 us)
     const int pf = picks ? pf0 : (pf0 < 4 ? pf0 : 4);
     if (!picks) {
         const size_t lds = lds_max(dot8_glu_lds(W.K, DG_TT, RO), shl);
-        if (TTS == SH_TT) dispatch_pf_c16<StageL<0, 0, DG_TT, SH_TT>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd);
-        else if (RO == 128) dispatch_pf_c16<StageL<0, 0, DG_TT, 1, 128>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd);
-        else if (RO == 64) dispatch_pf_c16<StageL<0, 0, DG_TT, 1, 64>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd);
-        else dispatch_pf_c16<StageL<0, 0, DG_TT, 1>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd);
+        if (RO == 128) dispatch_pf_c16<StageL<0, 0, DG_TT, 128>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd);
+        else if (RO == 64) dispatch_pf_c16<StageL<0, 0, DG_TT, 64>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd);
+        else dispatch_pf_c16<StageL<0, 0, DG_TT>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd);
     } else {
         const size_t lds = lds_max(dot8_glu_lds(W.K, 1), shl);
-        if (!route_src) dispatch_pf_c16<StageL<1, 0, 1, 1>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd);
-        else if (E <= 64) dispatch_pf_c16<StageL<1, 1, 1, 1>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd);
-        else if (E <= 128) dispatch_pf_c16<StageL<1, 2, 1, 1>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd);
-        else dispatch_pf_c16<StageL<1, 4, 1, 1>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd);
+        if (!route_src) dispatch_pf_c16<StageL<1, 0, 1>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd);
+        else if (E <= 64) dispatch_pf_c16<StageL<1, 1, 1>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd);
+        else if (E <= 128) dispatch_pf_c16<StageL<1, 2, 1>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd);
+        else dispatch_pf_c16<StageL<1, 4, 1>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd);
     }
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }

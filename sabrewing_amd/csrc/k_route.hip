@@ -57,6 +57,36 @@ __global__ __launch_bounds__(512) void k_router_logits(RouterArgs R) {
     router_block<BF16, ONE>(R, blockIdx.x, blockIdx.y, gridDim.x, smem);
 }
 
+template <int BF16, int TT, int NW>
+__global__ __launch_bounds__(64 * NW) void k_router_tiles(RouterArgs R, int S) {
+    router_tile_block<BF16, TT, NW>(R, S, blockIdx.x, blockIdx.y);
+}
+
+// token tile and waves per block: 16 tokens on 4 waves (16 experts) for prefill-sized
+// batches, else 8 tokens on one wave (a head-sized router has rows for thousands of waves)
+static void router_tile_shape(int S, int &tt, int &nw) {
+    if (S >= 512) { tt = 16; nw = 4; } else { tt = 8; nw = 1; }
+}
+
+int sw_launch_router_tiles(hipStream_t st, const void *Wc, int w_bf16, const float *x, int S, int D, int E,
+                           const float *logit_bias, float *logits, float *scores, int route_act) {
+    if (D % RT_CK || D > 65536 || E <= 0 || S <= 0 || route_act < 0 || route_act > SW_ROUTE_ACT_MAX) return -1;
+    if ((int64_t)((E + 3) / 4) * 4 * D * (w_bf16 ? 2 : 4) > 0xFFFFFFFFll) return -1;
+    int tt, nw;
+    router_tile_shape(S, tt, nw);
+    const RouterArgs R = {Wc, x, D, E, logit_bias, logits, route_act, scores, nullptr, nullptr, nullptr};
+    const int ng4 = (E + 3) / 4;
+    const dim3 grid((unsigned)((ng4 + nw - 1) / nw), (unsigned)((S + tt - 1) / tt));
+#define SW_RT(B, T, W) SW_LAUNCH((k_router_tiles<B, T, W>), grid, dim3(64 * W), 0, st, R, S)
+    if (w_bf16) {
+        if (tt == 16) SW_RT(1, 16, 4); else SW_RT(1, 8, 1);
+    } else {
+        if (tt == 16) SW_RT(0, 16, 4); else SW_RT(0, 8, 1);
+    }
+#undef SW_RT
+    return launch_err();
+}
+
 int sw_launch_router_topk(hipStream_t st, const void *Wc, int w_bf16, const float *x, int S, int D, int E,
                           const float *logit_bias, float *logits, float *scores, int K, int route_act,
                           const float *corr_bias, int use_corr_bias, int norm_topk, int *sel, float *w,
@@ -72,7 +102,7 @@ int sw_launch_router_topk(hipStream_t st, const void *Wc, int w_bf16, const floa
     const int nt = 512, one = router_one(S, E), epb = router_epb(one, nt);
     if (router_lds(D) > 65536 || D > 4 * RT_XB * (one ? nt - 64 : nt)) return -1;
     dim3 grid((unsigned)((E + epb - 1) / epb), (unsigned)S);
-    const RouterArgs R = {Wc, x, D, E, logit_bias, logits, route_act, scores, xl, xs};
+    const RouterArgs R = {Wc, x, D, E, logit_bias, logits, route_act, scores, xl, xs, nullptr};
     if (one) {
         if (w_bf16) SW_LAUNCH((k_router_logits<1, 1>), grid, dim3(nt), router_lds(D), st, R);
         else SW_LAUNCH((k_router_logits<0, 1>), grid, dim3(nt), router_lds(D), st, R);

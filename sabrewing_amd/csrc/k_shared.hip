@@ -1,89 +1,257 @@
-// k_shared.hip -- the shared expert for batches (S > 1): gate_up + SiLU-GLU
-// and down as standalone kernels over token tiles staged in LDS
-// (sh_tile_job, sw_shared.h).  Per (row, token) the arithmetic is that of
-// the single-token block jobs the decode stages run, so a token's shared
-// expert output does not depend on the batch it came in.
+// k_shared.hip -- the shared expert for batches (S > 1) on the bf16 MFMA: the
+// three bf16 parts of the inputs, gate_up + SiLU-GLU (writing the parts of h),
+// and down.  Per (row, token) the arithmetic is that of the single-token jobs
+// of the decode stages (sw_shared.h), so a token's shared expert output does
+// not depend on the batch it came in.
+//
+// Block: 4 waves; wave w takes two 16-row tiles and two 16-token column tiles
+// (32 rows x 32 tokens) over all of K, its weight words and its tokens' part
+// words loaded from global memory one step ahead; the four waves of a block
+// share their tokens (the same part words, from L1), so a block covers 128
+// rows (the down) or 64 outputs of gate and up (the gate_up) x 32 tokens.
 #include "sw_hip.h"
-
-// Per-block timeline, for a build with -DSW_TRACE only: kernel k (0 gate_up,
-// 1 down), linear block b: marks (0 start, 1 tile staged, 2.. row batches
-// done, 7 end) in sw_trace_mid[(k, b)].
-#ifdef SW_TRACE
-#define TS_MARK(k, i)                                                                         \
-    do {                                                                                      \
-        const unsigned b_ = blockIdx.x + gridDim.x * blockIdx.y;                              \
-        if (threadIdx.x == 0 && b_ < SW_TRACE_SLOT)                                           \
-            sw_trace_mid[((k) * SW_TRACE_SLOT + b_) * 8 + (i)] = wall_clock64();              \
-    } while (0)
-#define SH_TILE_MARK(i) TS_MARK(NR == 32 ? 0 : 1, i)     // gate_up jobs have 2 * 16 rows
-extern "C" int sw_trace_read_mid_shared(void *dst, size_t n) {
-    return hipMemcpyFromSymbol(dst, HIP_SYMBOL(sw_trace_mid), n) == hipSuccess ? 0 : -1;
-}
-#else
-#define TS_MARK(k, i)
-#endif
 #include "sw_shared.h"
 
-// block (set of SHT_GLU_O outputs, token tile): h[tok][i] = silu(gate) * up
-__global__ __launch_bounds__(SHT_NT) void k_sh_glu_tile(const uint16_t *__restrict__ Wg, const uint16_t *__restrict__ Wu,
-                                                      const float *__restrict__ x, int S, int D, int Is,
-                                                      float *__restrict__ h) {
-    extern __shared__ __align__(16) float lds[];
-    __shared__ float ys[2 * SHT_GLU_O * SHT_T];
-    TS_MARK(0, 0);
-    const int i0 = blockIdx.x * SHT_GLU_O, tok0 = blockIdx.y * SHT_T;
-    const int nt = min(SHT_T, S - tok0);
-    sh_tile_job([&](int lr) { return (lr < SHT_GLU_O ? Wg : Wu) + (int64_t)(i0 + (lr & (SHT_GLU_O - 1))) * D; },
-                2 * SHT_GLU_O, D, x, tok0, nt, [&](int lr, int t, float y) { ys[lr * SHT_T + t] = y; }, lds);
+#define SHB_TOK 32             // tokens per block
+
+// parts of the rows of x [S, K] f32 -> [S][K/32][3][32] bf16, 8 inputs per thread
+__global__ __launch_bounds__(256) void k_sh_parts(const float *__restrict__ x, int64_t n8, int K,
+                                                  uint16_t *__restrict__ parts) {
+    const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (c >= n8) return;
+    const int k8 = K / 8;
+    const int64_t tok = c / k8;
+    const int cc = (int)(c - tok * k8);
+    const sw_f32x4 *xv = (const sw_f32x4 *)(x + tok * K + 8 * cc);
+    sw_u32x4 p0, p1, p2;
+    sh_split8(xv[0], xv[1], p0, p1, p2);
+    uint16_t *dst = parts + tok * K * 3 + (cc >> 2) * 3 * SH_RG + (cc & 3) * 8;
+    *(sw_u32x4 *)dst = p0;
+    *(sw_u32x4 *)(dst + SH_RG) = p1;
+    *(sw_u32x4 *)(dst + 2 * SH_RG) = p2;
+}
+
+// the wave's two row tiles (row m of tile t at rowp(t, m)) x two column tiles (tokens
+// tok0 + 16 c + lane % 16) over all of K, the segments folded left to right
+template <class RowPtr>
+__device__ __forceinline__ void sh_wave_tiles(RowPtr rowp, const uint16_t *__restrict__ xp, int S, int K, int tok0,
+                                              sw_f32x4 tot[2][2]) {
+    const int lane = threadIdx.x & 63, m = lane & 15, kq = lane >> 4;
+    const int G = K / SH_RG, GS = G / sh_nseg(G);
+    const uint16_t *wr[2], *br[2];
+#pragma unroll
+    for (int t = 0; t < 2; t++) wr[t] = rowp(t, m) + 8 * kq;
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+        const int tok = min(tok0 + 16 * c + m, S - 1);
+        br[c] = xp + (int64_t)tok * K * 3 + 8 * kq;
+    }
+    struct Step { sw_u32x4 a[2], b[2][3]; };
+    auto load = [&](int g, Step &st) {
+#pragma unroll
+        for (int t = 0; t < 2; t++) st.a[t] = *(const sw_u32x4 *)(wr[t] + (int64_t)g * SH_RG);
+#pragma unroll
+        for (int c = 0; c < 2; c++)
+#pragma unroll
+            for (int p = 0; p < 3; p++) st.b[c][p] = *(const sw_u32x4 *)(br[c] + (g * 3 + p) * SH_RG);
+    };
+    const sw_f32x4 z = {0.f, 0.f, 0.f, 0.f};
+    sw_f32x4 acc[2][2];
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int c = 0; c < 2; c++) { acc[t][c] = z; tot[t][c] = z; }
+    Step cur, nxt;
+    load(0, cur);
+    for (int g = 0; g < G; g++) {
+        load(min(g + 1, G - 1), nxt);
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int c = 0; c < 2; c++) acc[t][c] = sh_mfma3(cur.a[t], cur.b[c][0], cur.b[c][1], cur.b[c][2], acc[t][c]);
+        if ((g + 1) % GS == 0) {                       // a segment ends: fold it in
+#pragma unroll
+            for (int t = 0; t < 2; t++)
+#pragma unroll
+                for (int c = 0; c < 2; c++) {
+                    tot[t][c] = g + 1 == GS ? acc[t][c] : tot[t][c] + acc[t][c];
+                    acc[t][c] = z;
+                }
+        }
+        cur = nxt;
+    }
+}
+
+// block (64 outputs i0 = 64 bx.., 32 tokens): wave w's tile t holds gate rows i0 + 16 w + 8 t
+// + 0..7 (tile rows 0-7) and the same up rows (8-15); h's parts [S][Is/32][3][32]
+__global__ __launch_bounds__(256) void k_sh_glu_mf(const uint16_t *__restrict__ Wg, const uint16_t *__restrict__ Wu,
+                                                   const uint16_t *__restrict__ xp, int S, int D, int Is,
+                                                   uint16_t *__restrict__ hp) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, m = lane & 15, kq = lane >> 4;
+    const int ib = blockIdx.x * 64 + 16 * wave, tok0 = blockIdx.y * SHB_TOK;
+    sw_f32x4 tot[2][2];
+    sh_wave_tiles([&](int t, int r) {
+        const int i = ib + 8 * t + (r & 7);
+        return (r < 8 ? Wg : Wu) + (int64_t)i * D;
+    }, xp, S, D, tok0, tot);
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int c = 0; c < 2; c++) {
+            // lanes kq < 2 hold gate rows 4 kq + r; lane + 32 holds the up rows of the same outputs
+            float hv[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const float yg = tot[t][c][r], yu = __shfl_xor(tot[t][c][r], 32);
+                hv[r] = (yg / (1.0f + expf(-yg))) * yu;
+            }
+            const int tok = tok0 + 16 * c + m;
+            if (kq < 2 && tok < S) {
+                const int i = ib + 8 * t + 4 * kq;      // four consecutive outputs of one group
+                uint32_t pa[4], pb[4], pc[4];
+#pragma unroll
+                for (int r = 0; r < 4; r++) sh_split3(hv[r], pa[r], pb[r], pc[r]);
+                uint16_t *dst = hp + (int64_t)tok * Is * 3 + (i >> 5) * 3 * SH_RG + (i & 31);
+                *(uint2 *)dst = make_uint2(pa[0] | (pa[1] << 16), pa[2] | (pa[3] << 16));
+                *(uint2 *)(dst + SH_RG) = make_uint2(pb[0] | (pb[1] << 16), pb[2] | (pb[3] << 16));
+                *(uint2 *)(dst + 2 * SH_RG) = make_uint2(pc[0] | (pc[1] << 16), pc[2] | (pc[3] << 16));
+            }
+        }
+}
+
+// block (128 rows d0 = 128 bx.., 32 tokens): out[tok][d] f32
+__global__ __launch_bounds__(256) void k_sh_down_mf(const uint16_t *__restrict__ Wd, const uint16_t *__restrict__ hp, int S,
+                                                    int Is, int D, float *__restrict__ out) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, m = lane & 15, kq = lane >> 4;
+    const int db = blockIdx.x * 128 + 32 * wave, tok0 = blockIdx.y * SHB_TOK;
+    sw_f32x4 tot[2][2];
+    sh_wave_tiles([&](int t, int r) { return Wd + (int64_t)(db + 16 * t + r) * Is; }, hp, S, Is, tok0, tot);
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int c = 0; c < 2; c++) {
+            const int tok = tok0 + 16 * c + m;
+            if (tok < S) *(sw_f32x4 *)(out + (int64_t)tok * D + db + 16 * t + 4 * kq) = tot[t][c];
+        }
+}
+
+// ---- decode-sized batches: K split over the waves ----
+// Block (16-row tile, NC column tiles of 16 tokens): wave w runs segment w of the K
+// inputs (the MFMA chain of that segment, as sh_seg_wave), the segment results go
+// to LDS and are folded left to right there, so a token gets the bits of the
+// single-token jobs while 8 waves stream one tile's weights.  Gate_up tiles: rows
+// 0-7 the gate rows of outputs 8 bx .. +7, rows 8-15 the up rows.
+#define SHK_NT 512
+template <int GLU, int NC>
+__global__ __launch_bounds__(SHK_NT) void k_sh_sk(const uint16_t *__restrict__ W0, const uint16_t *__restrict__ W1,
+                                                 const uint16_t *__restrict__ xp, int S, int K, int O,
+                                                 void *__restrict__ outp) {
+    __shared__ float red[8 * 16 * 16 * NC];                // [segment][row][token]
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, m = lane & 15, kq = lane >> 4;
+    const int G = K / SH_RG, nseg = sh_nseg(G), GS = G / nseg;
+    const int r0 = blockIdx.x * (GLU ? 8 : 16), tok0 = blockIdx.y * 16 * NC;
+    if (wave < nseg) {
+        const uint16_t *wr = GLU ? (m < 8 ? W0 + (int64_t)(r0 + m) * K : W1 + (int64_t)(r0 + m - 8) * K)
+                                 : W0 + (int64_t)(r0 + m) * K;
+        wr += 8 * kq;
+        const uint16_t *br[NC];
+#pragma unroll
+        for (int c = 0; c < NC; c++) br[c] = xp + (int64_t)min(tok0 + 16 * c + m, S - 1) * K * 3 + 8 * kq;
+        const int g0 = wave * GS;
+        struct Step { sw_u32x4 a, b[NC][3]; };
+        auto load = [&](int s, Step &st) {
+            const int g = g0 + min(s, GS - 1);
+            st.a = *(const sw_u32x4 *)(wr + (int64_t)g * SH_RG);
+#pragma unroll
+            for (int c = 0; c < NC; c++)
+#pragma unroll
+                for (int p = 0; p < 3; p++) st.b[c][p] = *(const sw_u32x4 *)(br[c] + (g * 3 + p) * SH_RG);
+        };
+        sw_f32x4 acc[NC];
+#pragma unroll
+        for (int c = 0; c < NC; c++) acc[c] = sw_f32x4{0.f, 0.f, 0.f, 0.f};
+        constexpr int SHK_PF = NC == 1 ? 6 : 3;     // steps in flight (weight and part words)
+        Step ring[SHK_PF];
+#pragma unroll
+        for (int u = 0; u < SHK_PF; u++) load(u, ring[u]);
+        for (int s0 = 0; s0 < GS; s0 += SHK_PF) {
+#pragma unroll
+            for (int u = 0; u < SHK_PF; u++) {
+                if (s0 + u < GS) {                         // uniform
+#pragma unroll
+                    for (int c = 0; c < NC; c++)
+                        acc[c] = sh_mfma3(ring[u].a, ring[u].b[c][0], ring[u].b[c][1], ring[u].b[c][2], acc[c]);
+                    load(s0 + u + SHK_PF, ring[u]);
+                }
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < NC; c++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) red[(wave * 16 + 4 * kq + r) * 16 * NC + 16 * c + m] = acc[c][r];
+    }
     __syncthreads();
     const int tid = threadIdx.x;
-    if (tid < SHT_GLU_O * SHT_T) {
-        const int lr = tid / SHT_T, t = tid - lr * SHT_T;
-        if (t < nt) {
-            const float yg = ys[lr * SHT_T + t], yu = ys[(SHT_GLU_O + lr) * SHT_T + t];
-            h[(int64_t)(tok0 + t) * Is + i0 + lr] = (yg / (1.0f + expf(-yg))) * yu;
+    if (GLU) {
+        for (int it = tid; it < 8 * 16 * NC; it += SHK_NT) {
+            const int r = it / (16 * NC), t = it - r * 16 * NC, tok = tok0 + t;
+            float yg = red[r * 16 * NC + t], yu = red[(8 + r) * 16 * NC + t];
+            for (int sg = 1; sg < nseg; sg++) {
+                yg = yg + red[(sg * 16 + r) * 16 * NC + t];
+                yu = yu + red[(sg * 16 + 8 + r) * 16 * NC + t];
+            }
+            if (tok < S) {
+                const int i = r0 + r;
+                uint32_t pa, pb, pc;
+                sh_split3((yg / (1.0f + expf(-yg))) * yu, pa, pb, pc);
+                uint16_t *dst = (uint16_t *)outp + (int64_t)tok * O * 3 + (i >> 5) * 3 * SH_RG + (i & 31);
+                dst[0] = (uint16_t)pa;
+                dst[SH_RG] = (uint16_t)pb;
+                dst[2 * SH_RG] = (uint16_t)pc;
+            }
+        }
+    } else {
+        for (int it = tid; it < 16 * 16 * NC; it += SHK_NT) {
+            const int r = it / (16 * NC), t = it - r * 16 * NC, tok = tok0 + t;
+            float y = red[r * 16 * NC + t];
+            for (int sg = 1; sg < nseg; sg++) y = y + red[(sg * 16 + r) * 16 * NC + t];
+            if (tok < S) ((float *)outp)[(int64_t)tok * O + r0 + r] = y;
         }
     }
-    TS_MARK(0, 7);
 }
-
-// block (set of SHT_DN_O output rows, token tile): out[tok][d]
-__global__ __launch_bounds__(SHT_NT) void k_sh_down_tile(const uint16_t *__restrict__ Wd, const float *__restrict__ h,
-                                                       int S, int Is, int D, float *__restrict__ out) {
-    extern __shared__ __align__(16) float lds[];
-    TS_MARK(1, 0);
-    const int d0 = blockIdx.x * SHT_DN_O, tok0 = blockIdx.y * SHT_T;
-    const int nt = min(SHT_T, S - tok0);
-    sh_tile_job([&](int lr) { return Wd + (int64_t)(d0 + lr) * Is; }, SHT_DN_O, Is, h, tok0, nt,
-                [&](int lr, int t, float y) { out[(int64_t)(tok0 + t) * D + d0 + lr] = y; }, lds);
-    TS_MARK(1, 7);
-}
-
-// dynamic LDS above 64 KB (gfx950 gives a workgroup up to 160 KB): raised once per
-// kernel to the largest size asked so far, outside any stream work
-static int set_lds(const void *fn, size_t bytes, size_t &raised) {
-    if (bytes > 160 * 1024) return -1;
-    if (bytes <= raised) return 0;
-    if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes) != hipSuccess) return -1;
-    raised = bytes;
-    return 0;
-}
-static size_t g_glu_lds = 0, g_down_lds = 0;
-
-int sw_launch_sh_glu(hipStream_t st, const uint16_t *Wg, const uint16_t *Wu, const float *x, int S, int D, int Is, float *h) {
-    if (S <= 0 || Is % SHT_GLU_O || !sh_shape_ok(D) || run_lanes(D / SH_RG) > SHT_NT) return -1;
-    const size_t lds = sh_tile_lds(D, 2 * SHT_GLU_O);
-    if (set_lds((const void *)k_sh_glu_tile, lds, g_glu_lds)) return -1;
-    const dim3 grid((unsigned)(Is / SHT_GLU_O), (unsigned)((S + SHT_T - 1) / SHT_T));
-    SW_LAUNCH(k_sh_glu_tile, grid, dim3(SHT_NT), lds, st, Wg, Wu, x, S, D, Is, h);
+// decode-sized batches take the split-K blocks: the gate_up 16-token column tiles up to
+// 32 tokens (the grid then fills the chip), else 32-token tiles
+#define SHK_MAX_S 128
+template <int GLU>
+static int launch_sk(hipStream_t st, const uint16_t *W0, const uint16_t *W1, const uint16_t *xp, int S, int K, int O,
+                     int nrow, void *out) {
+    const int nc = GLU && S <= 32 ? 1 : 2;      // (the down's segments are short: 32-token tiles)
+    const dim3 grid((unsigned)nrow, (unsigned)((S + 16 * nc - 1) / (16 * nc)));
+    if (nc == 1) SW_LAUNCH((k_sh_sk<GLU, 1>), grid, dim3(SHK_NT), 0, st, W0, W1, xp, S, K, O, out);
+    else SW_LAUNCH((k_sh_sk<GLU, 2>), grid, dim3(SHK_NT), 0, st, W0, W1, xp, S, K, O, out);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
-int sw_launch_sh_down(hipStream_t st, const uint16_t *Wd, const float *h, int S, int Is, int D, float *out) {
-    if (S <= 0 || D % SHT_DN_O || !sh_shape_ok(Is) || run_lanes(Is / SH_RG) > SHT_NT) return -1;
-    const size_t lds = sh_tile_lds(Is, SHT_DN_O);
-    if (set_lds((const void *)k_sh_down_tile, lds, g_down_lds)) return -1;
-    const dim3 grid((unsigned)(D / SHT_DN_O), (unsigned)((S + SHT_T - 1) / SHT_T));
-    SW_LAUNCH(k_sh_down_tile, grid, dim3(SHT_NT), lds, st, Wd, h, S, Is, D, out);
+int sw_launch_sh_parts(hipStream_t st, const float *x, int S, int K, uint16_t *parts) {
+    if (S <= 0 || !sh_shape_ok(K)) return -1;
+    const int64_t n8 = (int64_t)S * (K / 8);
+    SW_LAUNCH(k_sh_parts, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, st, x, n8, K, parts);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int sw_launch_sh_glu(hipStream_t st, const uint16_t *Wg, const uint16_t *Wu, const uint16_t *xp, int S, int D, int Is,
+                     uint16_t *hp) {
+    if (S <= 0 || Is % 64 || !sh_shape_ok(D)) return -1;
+    if (S <= SHK_MAX_S) return launch_sk<1>(st, Wg, Wu, xp, S, D, Is, Is / 8, hp);
+    const dim3 grid((unsigned)(Is / 64), (unsigned)((S + SHB_TOK - 1) / SHB_TOK));
+    SW_LAUNCH(k_sh_glu_mf, grid, dim3(256), 0, st, Wg, Wu, xp, S, D, Is, hp);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int sw_launch_sh_down(hipStream_t st, const uint16_t *Wd, const uint16_t *hp, int S, int Is, int D, float *out) {
+    if (S <= 0 || D % 128 || !sh_shape_ok(Is)) return -1;
+    if (S <= SHK_MAX_S) return launch_sk<0>(st, Wd, nullptr, hp, S, Is, D, D / 16, out);
+    const dim3 grid((unsigned)(D / 128), (unsigned)((S + SHB_TOK - 1) / SHB_TOK));
+    SW_LAUNCH(k_sh_down_mf, grid, dim3(256), 0, st, Wd, hp, S, Is, D, out);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }

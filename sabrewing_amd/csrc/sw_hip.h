@@ -207,6 +207,10 @@ int sw_launch_router_topk(hipStream_t st, const void *Wc, int w_bf16, const floa
                           const float *logit_bias, float *logits, float *scores, int K, int route_act,
                           const float *corr_bias, int use_corr_bias, int norm_topk, int *sel, float *w,
                           sw_u32x4 *xl, float *xs, const SwGateOpt *opt = nullptr);
+// the router logits and scores alone (no limbs, no top-k) over tiles of tokens: one
+// pass over the weights per tile, the same bits as sw_launch_router_topk; D % 256 == 0
+int sw_launch_router_tiles(hipStream_t st, const void *Wc, int w_bf16, const float *x, int S, int D, int E,
+                           const float *logit_bias, float *logits, float *scores, int route_act);
 // gate + top-k of S tokens from their logits (act 1) or scores (one wave each)
 int sw_launch_gate_topk(hipStream_t st, const float *logits, const float *scores, int S, int E, int K, int route_act,
                         const float *corr_bias, int use_corr_bias, int norm_topk, int *sel, float *w,
@@ -272,13 +276,14 @@ int sw_launch_combine(hipStream_t st, const float *slots, const int *rowof, cons
                       float route_scale, const float *shared, float *out, int accumulate,
                       const float *wsh = nullptr, int ns = 0);
 // fused decode stages (k_dot8.hip): stage 1 = router logits/scores/limbs
-// and the shared expert's gate_up (sg null: none); stage 2 = routed gate_up
-// (sel non-null: one token's K picks, from sel or, with route_src, by a gate
-// + top-k in every block; else the groups g) + the shared expert's down (sd
-// null: none)
+// and the shared expert's gate_up (sg null: none; one token), with xp
+// non-null also the bf16 parts of x (a batch's shared expert, sw_shared.h);
+// stage 2 = routed gate_up (sel non-null: one token's K picks, from sel or,
+// with route_src, by a gate + top-k in every block; else the groups g) + the
+// shared expert's down (sd null: none; one token)
 int sw_launch_stage_route(hipStream_t st, const void *Wc, int w_bf16, const float *x, int S, int D, int E,
                           const float *logit_bias, float *logits, float *scores, int route_act, sw_u32x4 *xl, float *xs,
-                          const uint16_t *sg, const uint16_t *su, int Is, float *sh_h);
+                          const uint16_t *sg, const uint16_t *su, int Is, float *sh_h, uint16_t *xp = nullptr);
 int sw_launch_stage_experts(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, const float *xs, SwGroups g, int I, sw_u32x4 *hl,
                             float *hs, int *sel, int K, const float *route_src, int E, int act, const float *bias,
                             int use_bias, int norm, float *w, const uint16_t *sd, const float *sh_h, int S, int Is, int D,
@@ -307,9 +312,12 @@ int sw_launch_idot_glu(hipStream_t st, SwQ4 W, const uint32_t *xi, const float *
 int sw_launch_idot_rows(hipStream_t st, SwQ4 W, const uint32_t *xi, const float *xs, SwGroups g, float *Y);
 int sw_launch_rmsnorm(hipStream_t st, const float *x, const float *w, float *out, int S, int D, float eps);
 int sw_launch_argmax(hipStream_t st, const float *logits, int S, int V, int *tok);
-// the shared expert of a batch over token tiles (k_shared.hip): h = silu(Wg x) * (Wu x); out = Wd h
-int sw_launch_sh_glu(hipStream_t st, const uint16_t *Wg, const uint16_t *Wu, const float *x, int S, int D, int Is, float *h);
-int sw_launch_sh_down(hipStream_t st, const uint16_t *Wd, const float *h, int S, int Is, int D, float *out);
+// the shared expert of a batch on the bf16 MFMA (k_shared.hip): the three bf16 parts of
+// rows of x ([S][K/32][3][32]); h = silu(Wg x) * (Wu x) as its parts; out = Wd h (f32)
+int sw_launch_sh_parts(hipStream_t st, const float *x, int S, int K, uint16_t *parts);
+int sw_launch_sh_glu(hipStream_t st, const uint16_t *Wg, const uint16_t *Wu, const uint16_t *xp, int S, int D, int Is,
+                     uint16_t *hp);
+int sw_launch_sh_down(hipStream_t st, const uint16_t *Wd, const uint16_t *hp, int S, int Is, int D, float *out);
 // synthetic data
 int sw_launch_gen_normal(hipStream_t st, float *out, int64_t n, uint64_t seed, uint64_t offset, double sigma, int to_bf16);
 int sw_launch_gen_bf16(hipStream_t st, uint16_t *out, int64_t n, uint64_t seed, uint64_t offset, double sigma);

@@ -5,6 +5,7 @@
 #include "sw_hip.h"
 #include "sw_libm.h"
 #include "sw_gate.h"
+#include "sw_shared.h"
 
 // logits[s,e] = sum_i x[s,i] W[e,i] under the contract of the reference's
 // AVX-512 router (c/moe_matmul.h:25-43; bf16 weights c/moe_matmul.h:92-110):
@@ -33,6 +34,7 @@ struct RouterArgs {
     float *scores;             // [S, E] sigmoid / softplus scores (act 0, 2) or null
     sw_u32x4 *xl;              // dot8 limbs of x, or null
     float *xs;
+    uint16_t *xp;              // the bf16 parts of x for the shared expert's MFMA (sw_shared.h), or null
 };
 // experts per router block of nt threads: 4 (ONE: wave 0 runs the chains,
 // the other waves stage x -- the router spread over as many CUs as there are
@@ -169,6 +171,17 @@ __device__ __forceinline__ void router_block(const RouterArgs &R, int bx, int s,
                                            : act == 5 ? sw_sqrt_rn(sw_softplus_ref_t(v, tab))   // c/deepseek.c:854
                                                       : sw_sigmoid_ref_t(v, tab);
     }
+    if (R.xp && bx == 0) {                            // the token's bf16 parts, by its first block
+        for (int c = tid; c < D / 8; c += nt) {
+            const sw_f32x4 *xv = (const sw_f32x4 *)(xr + 8 * c);
+            sw_u32x4 p0, p1, p2;
+            sh_split8(xv[0], xv[1], p0, p1, p2);
+            uint16_t *dst = R.xp + (int64_t)s * D * 3 + (c >> 2) * 3 * SH_RG + (c & 3) * 8;
+            *(sw_u32x4 *)dst = p0;
+            *(sw_u32x4 *)(dst + SH_RG) = p1;
+            *(sw_u32x4 *)(dst + 2 * SH_RG) = p2;
+        }
+    }
     if (!ONE && R.xl) {                               // the token's dot8 limbs, half a wave per group, from xt
         const int G = D / SW_RG;
         for (int g = bx * 2 * nw + (tid >> 5); g < G; g += nbx * 2 * nw) {
@@ -178,6 +191,130 @@ __device__ __forceinline__ void router_block(const RouterArgs &R, int bx, int s,
     }
 }
 __host__ inline size_t router_lds(int D) { return (size_t)16 * (D / 16 + 4) * 4; }
+
+// The same logits and scores for a tile of TT tokens per pass over the
+// weights: wave w of block (bx, by) runs the 16 chains of each of the four
+// experts of group bx * NW + w, for tokens TT by .. TT by + TT - 1 (lane
+// 16 q + j keeps chain j of expert 4 (bx NW + w) + q, one accumulator per
+// token), so a router slice is loaded once per TT tokens instead of once per
+// token.  x goes through LDS in chunks of 256 inputs (16 elements of every
+// chain), staged transposed, xt[t][j][m] = x[t][256 c + 16 m + j] (rows of
+// 20 floats: the 16 lanes of a row read 16 bytes each from distinct banks);
+// the next chunk's x is loaded into registers while this one is used, and
+// RT_TPF slices of each lane's chain are in flight.  Every chain is the same
+// fma sequence as router_block's, so the results are the same bits.
+#define RT_CK 256
+#define RT_XS 20
+#define RT_TPF 8
+template <int BF16, int TT, int NW>
+__device__ __forceinline__ void router_tile_block(const RouterArgs &R, int S, int bx, int by) {
+    constexpr int P = BF16 ? 8 : 4, SPC = 16 / P, NTH = 64 * NW;
+    constexpr int XR4 = TT * RT_CK / 4 / NTH;          // float4 of x per thread per chunk
+    static_assert(XR4 >= 1 && XR4 * 4 * NTH == TT * RT_CK, "x chunk splits evenly over the block");
+    static_assert(RT_TPF % SPC == 0, "whole chunks in flight");
+    constexpr int CPR = RT_TPF / SPC;                  // chunks per ring turn
+    __shared__ __align__(16) float xt[TT * 16 * RT_XS];
+    __shared__ uint64_t tab[32];
+    const int D = R.D, E = R.E, act = R.act;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, j = lane & 15;
+    const int eg = bx * NW + wave, e = eg * 4 + (lane >> 4);
+    const int ng4 = (E + 3) / 4, egc = eg < ng4 ? eg : ng4 - 1;
+    const int s0 = by * TT, nt = min(TT, S - s0);
+    const int M = D / 16, NQ = M / P, NCH = D / RT_CK;
+    const sw_rsrc rw = sw_make_rsrc(R.Wc, (uint32_t)ng4 * 4u * (uint32_t)D * (BF16 ? 2u : 4u));
+    const uint32_t voff = ((uint32_t)egc * NQ * 64 + lane) * 16;
+    auto slice = [&](int q) { return sw_ld16(rw, voff, (uint32_t)min(q, NQ - 1) * 1024u); };
+    // x float4 f of a chunk: token f / 64, inputs 4 (f % 64) .. +3 of the chunk
+    auto xload = [&](int c, sw_f32x4 *xr) {
+#pragma unroll
+        for (int u = 0; u < XR4; u++) {
+            const int f = u * NTH + tid, t = f >> 6, k4 = f & 63;
+            const int tok = s0 + (t < nt ? t : nt - 1);
+            xr[u] = *(const sw_f32x4 *)(R.x + (int64_t)tok * D + c * RT_CK + 4 * k4);
+        }
+    };
+    auto xstore = [&](const sw_f32x4 *xr) {
+#pragma unroll
+        for (int u = 0; u < XR4; u++) {
+            const int f = u * NTH + tid, t = f >> 6, k4 = f & 63;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int k = 4 * k4 + i;
+                xt[(t * 16 + (k & 15)) * RT_XS + (k >> 4)] = xr[u][i];
+            }
+        }
+    };
+    float acc[TT];
+#pragma unroll
+    for (int t = 0; t < TT; t++) acc[t] = 0.f;
+    sw_u32x4 ring[RT_TPF];
+#pragma unroll
+    for (int u = 0; u < RT_TPF; u++) ring[u] = slice(u);
+    sw_f32x4 xr[XR4];
+    xload(0, xr);
+    // element p of slice sl of the chunk against the tile's tokens
+    auto use = [&](int sl, const sw_u32x4 &w) {
+        const float *xj = xt + j * RT_XS + sl * P;
+#pragma unroll
+        for (int t = 0; t < TT; t++) {
+            const float *xp = xj + t * 16 * RT_XS;
+            if constexpr (BF16) {
+                const sw_f32x4 xa = *(const sw_f32x4 *)xp, xb = *(const sw_f32x4 *)(xp + 4);
+                acc[t] = __builtin_fmaf(xa.x, __builtin_bit_cast(float, w.x << 16), acc[t]);
+                acc[t] = __builtin_fmaf(xa.y, __builtin_bit_cast(float, w.x & 0xFFFF0000u), acc[t]);
+                acc[t] = __builtin_fmaf(xa.z, __builtin_bit_cast(float, w.y << 16), acc[t]);
+                acc[t] = __builtin_fmaf(xa.w, __builtin_bit_cast(float, w.y & 0xFFFF0000u), acc[t]);
+                acc[t] = __builtin_fmaf(xb.x, __builtin_bit_cast(float, w.z << 16), acc[t]);
+                acc[t] = __builtin_fmaf(xb.y, __builtin_bit_cast(float, w.z & 0xFFFF0000u), acc[t]);
+                acc[t] = __builtin_fmaf(xb.z, __builtin_bit_cast(float, w.w << 16), acc[t]);
+                acc[t] = __builtin_fmaf(xb.w, __builtin_bit_cast(float, w.w & 0xFFFF0000u), acc[t]);
+            } else {
+                const sw_f32x4 xa = *(const sw_f32x4 *)xp, wf = __builtin_bit_cast(sw_f32x4, w);
+                acc[t] = __builtin_fmaf(xa.x, wf.x, acc[t]);
+                acc[t] = __builtin_fmaf(xa.y, wf.y, acc[t]);
+                acc[t] = __builtin_fmaf(xa.z, wf.z, acc[t]);
+                acc[t] = __builtin_fmaf(xa.w, wf.w, acc[t]);
+            }
+        }
+    };
+    for (int c0 = 0; c0 < NCH; c0 += CPR) {
+#pragma unroll
+        for (int cc = 0; cc < CPR; cc++) {
+            const int c = c0 + cc;
+            if (c < NCH) {                                // uniform
+                __syncthreads();                          // the previous chunk's reads are done
+                xstore(xr);
+                if (c + 1 < NCH) xload(c + 1, xr);
+                __syncthreads();
+#pragma unroll
+                for (int sl = 0; sl < SPC; sl++) {
+                    const int u = cc * SPC + sl;          // ring slot of slice c * SPC + sl
+                    use(sl, ring[u]);
+                    ring[u] = slice(c * SPC + sl + RT_TPF);
+                }
+            }
+        }
+    }
+    tab[lane & 31] = sw_exp2f_tab[lane & 31];         // every wave writes the whole table (equal values)
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < TT; t++) {
+        float v = acc[t];
+        v = v + __shfl_down(v, 8, 16);
+        v = v + __shfl_down(v, 4, 16);
+        v = v + __shfl_down(v, 2, 16);
+        v = v + __shfl_down(v, 1, 16);
+        if (j == 0 && e < E && t < nt) {
+            const int64_t s = s0 + t;
+            if (R.lbias) v = v + R.lbias[e];
+            R.logits[s * E + e] = v;
+            if (!sw_act_softmax(act) && R.scores)
+                R.scores[s * E + e] = act == 2   ? sw_softplus_ref_t(v, tab)
+                                      : act == 5 ? sw_sqrt_rn(sw_softplus_ref_t(v, tab))
+                                                 : sw_sigmoid_ref_t(v, tab);
+        }
+    }
+}
 
 
 #endif
