@@ -4,15 +4,8 @@
 // of the decode stages (sw_shared.h), so a token's shared expert output does
 // not depend on the batch it came in.
 //
-// Block: 4 waves; wave w takes two 16-row tiles and two 16-token column tiles
-// (32 rows x 32 tokens) over all of K, its weight words and its tokens' part
-// words loaded from global memory one step ahead; the four waves of a block
-// share their tokens (the same part words, from L1), so a block covers 128
-// rows (the down) or 64 outputs of gate and up (the gate_up) x 32 tokens.
 #include "sw_hip.h"
 #include "sw_shared.h"
-
-#define SHB_TOK 32             // tokens per block
 
 // parts of the rows of x [S, K] f32 -> [S][K/32][3][32] bf16, 8 inputs per thread
 __global__ __launch_bounds__(256) void k_sh_parts(const float *__restrict__ x, int64_t n8, int K,
@@ -31,73 +24,107 @@ __global__ __launch_bounds__(256) void k_sh_parts(const float *__restrict__ x, i
     *(sw_u32x4 *)(dst + 2 * SH_RG) = p2;
 }
 
-// the wave's two row tiles (row m of tile t at rowp(t, m)) x two column tiles (tokens
-// tok0 + 16 c + lane % 16) over all of K, the segments folded left to right
+// Prefill-sized batches.  Block: 4 waves, 128 rows x 64 tokens; wave w takes rows
+// 32 w .. +31 (two 16-row tiles) against the four 16-token column tiles.  The
+// tokens' part words of a step go through LDS (two buffers: the next step's
+// loads are in flight in registers while the waves read this one), each
+// token's 192 bytes at a padded stride; the waves' weight words come from
+// global memory a step ahead.  The fold starts from -0.0, the identity of
+// f32 addition (-0 + y == y bit for bit), so every segment is added the same way.
+#define SHB_TOK 64             // tokens per block
+#define SHB_TS 208             // LDS bytes per token and step: 192 + 16 of padding
+#define SHB_STAGE (SHB_TOK * SHB_TS)
+#define SHB_CH (SHB_TOK * 12 / 256)   // 16-byte chunks staged per thread per step
 template <class RowPtr>
-__device__ __forceinline__ void sh_wave_tiles(RowPtr rowp, const uint16_t *__restrict__ xp, int S, int K, int tok0,
-                                              sw_f32x4 tot[2][2]) {
-    const int lane = threadIdx.x & 63, m = lane & 15, kq = lane >> 4;
+__device__ __forceinline__ void sh_block_tiles(RowPtr rowp, const uint16_t *__restrict__ xp, int S, int K, int tok0,
+                                               uint8_t *lds, sw_f32x4 tot[2][4]) {
+    const int tid = threadIdx.x, lane = tid & 63, m = lane & 15, kq = lane >> 4;
     const int G = K / SH_RG, GS = G / sh_nseg(G);
-    const uint16_t *wr[2], *br[2];
+    const uint16_t *wr[2];
 #pragma unroll
     for (int t = 0; t < 2; t++) wr[t] = rowp(t, m) + 8 * kq;
+    // staging: chunk q = u * 256 + tid of a step -> token q / 12, chunk q % 12
+    const uint16_t *sp[SHB_CH];
+    int so[SHB_CH];
 #pragma unroll
-    for (int c = 0; c < 2; c++) {
-        const int tok = min(tok0 + 16 * c + m, S - 1);
-        br[c] = xp + (int64_t)tok * K * 3 + 8 * kq;
+    for (int u = 0; u < SHB_CH; u++) {
+        const int q = u * 256 + tid, tk = q / 12, ch = q - tk * 12;
+        sp[u] = xp + (int64_t)min(tok0 + tk, S - 1) * G * 3 * SH_RG + ch * 8;
+        so[u] = tk * SHB_TS + ch * 16;
     }
-    struct Step { sw_u32x4 a[2], b[2][3]; };
-    auto load = [&](int g, Step &st) {
+    auto stage_load = [&](int g, sw_u32x4 *r) {
 #pragma unroll
-        for (int t = 0; t < 2; t++) st.a[t] = *(const sw_u32x4 *)(wr[t] + (int64_t)g * SH_RG);
-#pragma unroll
-        for (int c = 0; c < 2; c++)
-#pragma unroll
-            for (int p = 0; p < 3; p++) st.b[c][p] = *(const sw_u32x4 *)(br[c] + (g * 3 + p) * SH_RG);
+        for (int u = 0; u < SHB_CH; u++) r[u] = *(const sw_u32x4 *)(sp[u] + (int64_t)g * 3 * SH_RG);
     };
-    const sw_f32x4 z = {0.f, 0.f, 0.f, 0.f};
-    sw_f32x4 acc[2][2];
+    auto stage_store = [&](int buf, const sw_u32x4 *r) {
+#pragma unroll
+        for (int u = 0; u < SHB_CH; u++) *(sw_u32x4 *)(lds + buf * SHB_STAGE + so[u]) = r[u];
+    };
+    auto ald = [&](int t, int g) { return *(const sw_u32x4 *)(wr[t] + (int64_t)min(g, G - 1) * SH_RG); };
+    sw_f32x4 acc[2][4];
 #pragma unroll
     for (int t = 0; t < 2; t++)
 #pragma unroll
-        for (int c = 0; c < 2; c++) { acc[t][c] = z; tot[t][c] = z; }
-    Step cur, nxt;
-    load(0, cur);
+        for (int c = 0; c < 4; c++) {
+            acc[t][c] = sw_f32x4{0.f, 0.f, 0.f, 0.f};
+            tot[t][c] = sw_f32x4{-0.f, -0.f, -0.f, -0.f};
+        }
+    sw_u32x4 an[2] = {ald(0, 0), ald(1, 0)};
+    sw_u32x4 sr[SHB_CH];
+    stage_load(0, sr);
+    stage_store(0, sr);
+    __syncthreads();
+    if (G > 1) stage_load(1, sr);
     for (int g = 0; g < G; g++) {
-        load(min(g + 1, G - 1), nxt);
+        const uint8_t *base = lds + (g & 1) * SHB_STAGE + m * SHB_TS + kq * 16;
+        const sw_u32x4 a0 = an[0], a1 = an[1];
+        an[0] = ald(0, g + 1);
+        an[1] = ald(1, g + 1);
+        // column tile c's part words from LDS, tile c + 1's read while c's MFMAs run
+        sw_u32x4 b[2][3];
+        auto bld = [&](int c, sw_u32x4 *bb) {
 #pragma unroll
-        for (int t = 0; t < 2; t++)
+            for (int p = 0; p < 3; p++) bb[p] = *(const sw_u32x4 *)(base + 16 * c * SHB_TS + 64 * p);
+        };
+        bld(0, b[0]);
 #pragma unroll
-            for (int c = 0; c < 2; c++) acc[t][c] = sh_mfma3(cur.a[t], cur.b[c][0], cur.b[c][1], cur.b[c][2], acc[t][c]);
+        for (int c = 0; c < 4; c++) {
+            if (c + 1 < 4) bld(c + 1, b[(c + 1) & 1]);
+            acc[0][c] = sh_mfma3(a0, b[c & 1][0], b[c & 1][1], b[c & 1][2], acc[0][c]);
+            acc[1][c] = sh_mfma3(a1, b[c & 1][0], b[c & 1][1], b[c & 1][2], acc[1][c]);
+        }
         if ((g + 1) % GS == 0) {                       // a segment ends: fold it in
 #pragma unroll
             for (int t = 0; t < 2; t++)
 #pragma unroll
-                for (int c = 0; c < 2; c++) {
-                    tot[t][c] = g + 1 == GS ? acc[t][c] : tot[t][c] + acc[t][c];
-                    acc[t][c] = z;
+                for (int c = 0; c < 4; c++) {
+                    tot[t][c] = tot[t][c] + acc[t][c];
+                    acc[t][c] = sw_f32x4{0.f, 0.f, 0.f, 0.f};
                 }
         }
-        cur = nxt;
+        if (g + 1 < G) stage_store((g + 1) & 1, sr);     // read by no wave since the last barrier
+        __syncthreads();
+        if (g + 2 < G) stage_load(g + 2, sr);
     }
 }
 
-// block (64 outputs i0 = 64 bx.., 32 tokens): wave w's tile t holds gate rows i0 + 16 w + 8 t
+// block (64 outputs i0 = 64 bx.., 64 tokens): wave w's tile t holds gate rows i0 + 16 w + 8 t
 // + 0..7 (tile rows 0-7) and the same up rows (8-15); h's parts [S][Is/32][3][32]
 __global__ __launch_bounds__(256) void k_sh_glu_mf(const uint16_t *__restrict__ Wg, const uint16_t *__restrict__ Wu,
                                                    const uint16_t *__restrict__ xp, int S, int D, int Is,
                                                    uint16_t *__restrict__ hp) {
+    __shared__ __align__(16) uint8_t lds[2 * SHB_STAGE];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, m = lane & 15, kq = lane >> 4;
     const int ib = blockIdx.x * 64 + 16 * wave, tok0 = blockIdx.y * SHB_TOK;
-    sw_f32x4 tot[2][2];
-    sh_wave_tiles([&](int t, int r) {
+    sw_f32x4 tot[2][4];
+    sh_block_tiles([&](int t, int r) {
         const int i = ib + 8 * t + (r & 7);
         return (r < 8 ? Wg : Wu) + (int64_t)i * D;
-    }, xp, S, D, tok0, tot);
+    }, xp, S, D, tok0, lds, tot);
 #pragma unroll
     for (int t = 0; t < 2; t++)
 #pragma unroll
-        for (int c = 0; c < 2; c++) {
+        for (int c = 0; c < 4; c++) {
             // lanes kq < 2 hold gate rows 4 kq + r; lane + 32 holds the up rows of the same outputs
             float hv[4];
 #pragma unroll
@@ -119,17 +146,18 @@ __global__ __launch_bounds__(256) void k_sh_glu_mf(const uint16_t *__restrict__ 
         }
 }
 
-// block (128 rows d0 = 128 bx.., 32 tokens): out[tok][d] f32
+// block (128 rows d0 = 128 bx.., 64 tokens): out[tok][d] f32
 __global__ __launch_bounds__(256) void k_sh_down_mf(const uint16_t *__restrict__ Wd, const uint16_t *__restrict__ hp, int S,
                                                     int Is, int D, float *__restrict__ out) {
+    __shared__ __align__(16) uint8_t lds[2 * SHB_STAGE];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, m = lane & 15, kq = lane >> 4;
     const int db = blockIdx.x * 128 + 32 * wave, tok0 = blockIdx.y * SHB_TOK;
-    sw_f32x4 tot[2][2];
-    sh_wave_tiles([&](int t, int r) { return Wd + (int64_t)(db + 16 * t + r) * Is; }, hp, S, Is, tok0, tot);
+    sw_f32x4 tot[2][4];
+    sh_block_tiles([&](int t, int r) { return Wd + (int64_t)(db + 16 * t + r) * Is; }, hp, S, Is, tok0, lds, tot);
 #pragma unroll
     for (int t = 0; t < 2; t++)
 #pragma unroll
-        for (int c = 0; c < 2; c++) {
+        for (int c = 0; c < 4; c++) {
             const int tok = tok0 + 16 * c + m;
             if (tok < S) *(sw_f32x4 *)(out + (int64_t)tok * D + db + 16 * t + 4 * kq) = tot[t][c];
         }
@@ -195,8 +223,8 @@ __global__ __launch_bounds__(SHK_NT) void k_sh_sk(const uint16_t *__restrict__ W
     if (GLU) {
         for (int it = tid; it < 8 * 16 * NC; it += SHK_NT) {
             const int r = it / (16 * NC), t = it - r * 16 * NC, tok = tok0 + t;
-            float yg = red[r * 16 * NC + t], yu = red[(8 + r) * 16 * NC + t];
-            for (int sg = 1; sg < nseg; sg++) {
+            float yg = -0.0f, yu = -0.0f;
+            for (int sg = 0; sg < nseg; sg++) {
                 yg = yg + red[(sg * 16 + r) * 16 * NC + t];
                 yu = yu + red[(sg * 16 + 8 + r) * 16 * NC + t];
             }
@@ -213,8 +241,8 @@ __global__ __launch_bounds__(SHK_NT) void k_sh_sk(const uint16_t *__restrict__ W
     } else {
         for (int it = tid; it < 16 * 16 * NC; it += SHK_NT) {
             const int r = it / (16 * NC), t = it - r * 16 * NC, tok = tok0 + t;
-            float y = red[r * 16 * NC + t];
-            for (int sg = 1; sg < nseg; sg++) y = y + red[(sg * 16 + r) * 16 * NC + t];
+            float y = -0.0f;
+            for (int sg = 0; sg < nseg; sg++) y = y + red[(sg * 16 + r) * 16 * NC + t];
             if (tok < S) ((float *)outp)[(int64_t)tok * O + r0 + r] = y;
         }
     }

@@ -10,7 +10,8 @@
 // NSEG contiguous segments (NSEG: the largest power of two <= 8 dividing G);
 // a segment is one chain of v_mfma_f32_16x16x32_bf16 from zero over its
 // 32-input steps in order, each step three MFMAs against the parts 0, 1, 2;
-// the row is the segments folded left to right.  A row's result depends only
+// the row is the segments folded left to right, from -0.0 (which leaves the first
+// segment's bits as they are).  A row's result depends only
 // on its weights and its token's inputs (an MFMA output element is the dot of
 // its own row and column), so the single-token blocks and the batch kernels
 // give a token the same bits whatever batch it came in.
@@ -144,9 +145,11 @@ __device__ __forceinline__ void sh_seg_store(const sw_f32x4 *acc, int seg, float
             for (int r = 0; r < 4; r++) red[seg * 32 + 16 * t + 4 * (lane >> 4) + r] = acc[t][r];
     }
 }
+// the segments folded left to right from -0.0 (the identity of f32 addition, so the
+// first segment is added like the others)
 __device__ __forceinline__ float sh_fold(const float *red, int row, int nseg) {
-    float y = red[row];
-    for (int s = 1; s < nseg; s++) y = y + red[s * 32 + row];
+    float y = -0.0f;
+    for (int s = 0; s < nseg; s++) y = y + red[s * 32 + row];
     return y;
 }
 
