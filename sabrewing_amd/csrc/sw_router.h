@@ -201,18 +201,16 @@ __host__ inline size_t router_lds(int D) { return (size_t)16 * (D / 16 + 4) * 4;
 // chain), staged transposed, xt[t][j][m] = x[t][256 c + 16 m + j] (rows of
 // 20 floats: the 16 lanes of a row read 16 bytes each from distinct banks);
 // the next chunk's x is loaded into registers while this one is used, and
-// RT_TPF slices of each lane's chain are in flight.  Every chain is the same
+// the slices of RT_TCH chunks of each lane's chain are in flight.  Every chain is the same
 // fma sequence as router_block's, so the results are the same bits.
 #define RT_CK 256
 #define RT_XS 20
-#define RT_TPF 8
+#define RT_TCH 3           // chunks of router slices in flight
 template <int BF16, int TT, int NW>
 __device__ __forceinline__ void router_tile_block(const RouterArgs &R, int S, int bx, int by) {
     constexpr int P = BF16 ? 8 : 4, SPC = 16 / P, NTH = 64 * NW;
     constexpr int XR4 = TT * RT_CK / 4 / NTH;          // float4 of x per thread per chunk
     static_assert(XR4 >= 1 && XR4 * 4 * NTH == TT * RT_CK, "x chunk splits evenly over the block");
-    static_assert(RT_TPF % SPC == 0, "whole chunks in flight");
-    constexpr int CPR = RT_TPF / SPC;                  // chunks per ring turn
     __shared__ __align__(16) float xt[TT * 16 * RT_XS];
     __shared__ uint64_t tab[32];
     const int D = R.D, E = R.E, act = R.act;
@@ -247,53 +245,58 @@ __device__ __forceinline__ void router_tile_block(const RouterArgs &R, int S, in
     float acc[TT];
 #pragma unroll
     for (int t = 0; t < TT; t++) acc[t] = 0.f;
-    sw_u32x4 ring[RT_TPF];
+    // the slices of chunks c, c + 1 and c + 2 in flight (RT_TCH chunks ahead of their use)
+    sw_u32x4 wc[RT_TCH][SPC];
 #pragma unroll
-    for (int u = 0; u < RT_TPF; u++) ring[u] = slice(u);
+    for (int u = 0; u < RT_TCH; u++)
+#pragma unroll
+        for (int sl = 0; sl < SPC; sl++) wc[u][sl] = slice(u * SPC + sl);
     sw_f32x4 xr[XR4];
     xload(0, xr);
-    // element p of slice sl of the chunk against the tile's tokens
+    // element p of slice sl of the chunk against the tile's tokens: the slice widened once,
+    // then the tokens' x read from LDS four tokens at a time (so the reads in flight stay few)
     auto use = [&](int sl, const sw_u32x4 &w) {
         const float *xj = xt + j * RT_XS + sl * P;
+        float wf[P];
+        if constexpr (BF16) {
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                wf[2 * q] = __builtin_bit_cast(float, w[q] << 16);
+                wf[2 * q + 1] = __builtin_bit_cast(float, w[q] & 0xFFFF0000u);
+            }
+        } else {
+            // the whole vector is cast (a bit_cast of one element lvalue reads element 0)
+            const sw_f32x4 wv = __builtin_bit_cast(sw_f32x4, w);
+#pragma unroll
+            for (int q = 0; q < 4; q++) wf[q] = wv[q];
+        }
 #pragma unroll
         for (int t = 0; t < TT; t++) {
             const float *xp = xj + t * 16 * RT_XS;
-            if constexpr (BF16) {
-                const sw_f32x4 xa = *(const sw_f32x4 *)xp, xb = *(const sw_f32x4 *)(xp + 4);
-                acc[t] = __builtin_fmaf(xa.x, __builtin_bit_cast(float, w.x << 16), acc[t]);
-                acc[t] = __builtin_fmaf(xa.y, __builtin_bit_cast(float, w.x & 0xFFFF0000u), acc[t]);
-                acc[t] = __builtin_fmaf(xa.z, __builtin_bit_cast(float, w.y << 16), acc[t]);
-                acc[t] = __builtin_fmaf(xa.w, __builtin_bit_cast(float, w.y & 0xFFFF0000u), acc[t]);
-                acc[t] = __builtin_fmaf(xb.x, __builtin_bit_cast(float, w.z << 16), acc[t]);
-                acc[t] = __builtin_fmaf(xb.y, __builtin_bit_cast(float, w.z & 0xFFFF0000u), acc[t]);
-                acc[t] = __builtin_fmaf(xb.z, __builtin_bit_cast(float, w.w << 16), acc[t]);
-                acc[t] = __builtin_fmaf(xb.w, __builtin_bit_cast(float, w.w & 0xFFFF0000u), acc[t]);
-            } else {
-                const sw_f32x4 xa = *(const sw_f32x4 *)xp, wf = __builtin_bit_cast(sw_f32x4, w);
-                acc[t] = __builtin_fmaf(xa.x, wf.x, acc[t]);
-                acc[t] = __builtin_fmaf(xa.y, wf.y, acc[t]);
-                acc[t] = __builtin_fmaf(xa.z, wf.z, acc[t]);
-                acc[t] = __builtin_fmaf(xa.w, wf.w, acc[t]);
+#pragma unroll
+            for (int h = 0; h < P / 4; h++) {
+                const sw_f32x4 xa = *(const sw_f32x4 *)(xp + 4 * h);
+                acc[t] = __builtin_fmaf(xa.x, wf[4 * h], acc[t]);
+                acc[t] = __builtin_fmaf(xa.y, wf[4 * h + 1], acc[t]);
+                acc[t] = __builtin_fmaf(xa.z, wf[4 * h + 2], acc[t]);
+                acc[t] = __builtin_fmaf(xa.w, wf[4 * h + 3], acc[t]);
             }
+            if ((t & 3) == 3) __builtin_amdgcn_sched_barrier(0);
         }
     };
-    for (int c0 = 0; c0 < NCH; c0 += CPR) {
+    for (int c = 0; c < NCH; c++) {
+        __syncthreads();                              // the previous chunk's reads are done
+        xstore(xr);
+        xload(min(c + 1, NCH - 1), xr);
+        __syncthreads();
 #pragma unroll
-        for (int cc = 0; cc < CPR; cc++) {
-            const int c = c0 + cc;
-            if (c < NCH) {                                // uniform
-                __syncthreads();                          // the previous chunk's reads are done
-                xstore(xr);
-                if (c + 1 < NCH) xload(c + 1, xr);
-                __syncthreads();
+        for (int sl = 0; sl < SPC; sl++) use(sl, wc[0][sl]);
 #pragma unroll
-                for (int sl = 0; sl < SPC; sl++) {
-                    const int u = cc * SPC + sl;          // ring slot of slice c * SPC + sl
-                    use(sl, ring[u]);
-                    ring[u] = slice(c * SPC + sl + RT_TPF);
-                }
-            }
-        }
+        for (int u = 0; u + 1 < RT_TCH; u++)
+#pragma unroll
+            for (int sl = 0; sl < SPC; sl++) wc[u][sl] = wc[u + 1][sl];
+#pragma unroll
+        for (int sl = 0; sl < SPC; sl++) wc[RT_TCH - 1][sl] = slice((c + RT_TCH) * SPC + sl);
     }
     tab[lane & 31] = sw_exp2f_tab[lane & 31];         // every wave writes the whole table (equal values)
     __syncthreads();
