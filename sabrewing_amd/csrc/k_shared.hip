@@ -165,7 +165,7 @@ __global__ __launch_bounds__(256) void k_sh_down_mf(const uint16_t *__restrict__
 
 // ---- decode-sized batches: K split over the waves ----
 // Block (16-row tile, NC column tiles of 16 tokens): wave w runs segment w of the K
-// inputs (the MFMA chain of that segment, as sh_seg_wave), the segment results go
+// inputs (the MFMA chain of that segment, as ShSegWave), the segment results go
 // to LDS and are folded left to right there, so a token gets the bits of the
 // single-token jobs while 8 waves stream one tile's weights.  Gate_up tiles: rows
 // 0-7 the gate rows of outputs 8 bx .. +7, rows 8-15 the up rows.

@@ -97,42 +97,53 @@ __device__ __forceinline__ void sh_stage_parts(const float *__restrict__ x, int 
 
 // wave `seg` of the block: NRT 16-row tiles (row m of tile t at rowp(t, m)) over segment
 // seg of the staged token; lane l keeps rows 4 (l / 16) .. +3 of column l % 16 (only
-// column 0 holds the token; the other columns multiply zeros)
-template <int NRT, class RowPtr>
-__device__ __forceinline__ void sh_seg_wave(RowPtr rowp, int K, const uint16_t *pl, int seg, int nseg, sw_f32x4 *acc) {
-    const int lane = threadIdx.x & 63, m = lane & 15, kq = lane >> 4;
-    const int GS = K / SH_RG / nseg, g0 = seg * GS;
+// column 0 holds the token; the other columns multiply zeros).  start() issues the
+// first SH_PF steps' weight loads (before the block stages the token's parts, so the
+// loads' latency overlaps that work); run() waits for the parts in LDS.
+template <int NRT>
+struct ShSegWave {
     const uint16_t *wr[NRT];
-#pragma unroll
-    for (int t = 0; t < NRT; t++) {
-        wr[t] = rowp(t, m) + 8 * kq;
-        acc[t] = sw_f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-    auto ld = [&](int t, int s) { return *(const sw_u32x4 *)(wr[t] + (int64_t)(g0 + min(s, GS - 1)) * SH_RG); };
+    int GS, g0;
     sw_u32x4 ring[NRT][SH_PF];
+    __device__ __forceinline__ sw_u32x4 ld(int t, int s) const {
+        return *(const sw_u32x4 *)(wr[t] + (int64_t)(g0 + min(s, GS - 1)) * SH_RG);
+    }
+    template <class RowPtr>
+    __device__ __forceinline__ void start(RowPtr rowp, int K, int seg, int nseg) {
+        const int lane = threadIdx.x & 63, m = lane & 15, kq = lane >> 4;
+        GS = K / SH_RG / nseg;
+        g0 = seg * GS;
 #pragma unroll
-    for (int u = 0; u < SH_PF; u++)
+        for (int t = 0; t < NRT; t++) wr[t] = rowp(t, m) + 8 * kq;
 #pragma unroll
-        for (int t = 0; t < NRT; t++) ring[t][u] = ld(t, u);
-    const sw_u32x4 z = {0u, 0u, 0u, 0u};
-    for (int s0 = 0; s0 < GS; s0 += SH_PF) {
+        for (int u = 0; u < SH_PF; u++)
 #pragma unroll
-        for (int u = 0; u < SH_PF; u++) {
-            const int s = s0 + u;
-            if (s < GS) {                              // uniform
-                const uint16_t *pp = pl + (g0 + s) * 3 * SH_RG + 8 * kq;
-                const sw_u32x4 b0 = *(const sw_u32x4 *)pp, b1 = *(const sw_u32x4 *)(pp + SH_RG),
-                               b2 = *(const sw_u32x4 *)(pp + 2 * SH_RG);
-                const bool col0 = m == 0;
+            for (int t = 0; t < NRT; t++) ring[t][u] = ld(t, u);
+    }
+    __device__ __forceinline__ void run(const uint16_t *pl, sw_f32x4 *acc) {
+        const int lane = threadIdx.x & 63, m = lane & 15, kq = lane >> 4;
 #pragma unroll
-                for (int t = 0; t < NRT; t++) {
-                    acc[t] = sh_mfma3(ring[t][u], col0 ? b0 : z, col0 ? b1 : z, col0 ? b2 : z, acc[t]);
-                    ring[t][u] = ld(t, s + SH_PF);
+        for (int t = 0; t < NRT; t++) acc[t] = sw_f32x4{0.f, 0.f, 0.f, 0.f};
+        const sw_u32x4 z = {0u, 0u, 0u, 0u};
+        for (int s0 = 0; s0 < GS; s0 += SH_PF) {
+#pragma unroll
+            for (int u = 0; u < SH_PF; u++) {
+                const int s = s0 + u;
+                if (s < GS) {                          // uniform
+                    const uint16_t *pp = pl + (g0 + s) * 3 * SH_RG + 8 * kq;
+                    const sw_u32x4 b0 = *(const sw_u32x4 *)pp, b1 = *(const sw_u32x4 *)(pp + SH_RG),
+                                   b2 = *(const sw_u32x4 *)(pp + 2 * SH_RG);
+                    const bool col0 = m == 0;
+#pragma unroll
+                    for (int t = 0; t < NRT; t++) {
+                        acc[t] = sh_mfma3(ring[t][u], col0 ? b0 : z, col0 ? b1 : z, col0 ? b2 : z, acc[t]);
+                        ring[t][u] = ld(t, s + SH_PF);
+                    }
                 }
             }
         }
     }
-}
+};
 
 // the segment results of column 0 (rows 16 t + r) into red[seg][32], by the lanes holding them
 template <int NRT>
@@ -161,12 +172,15 @@ __device__ __forceinline__ void sh_glu_block(const uint16_t *__restrict__ Wg, co
     uint16_t *pl = (uint16_t *)smem;
     float *red = smem + (size_t)D * 6 / 4;
     const int i0 = bid * SH_GLU_O, nseg = sh_nseg(D / SH_RG), wave = threadIdx.x >> 6;
+    ShSegWave<1> sw;
+    if (wave < nseg)
+        sw.start([&](int, int m) { return (m < 8 ? Wg + (int64_t)(i0 + m) * D : Wu + (int64_t)(i0 + m - 8) * D); }, D,
+                 wave, nseg);
     sh_stage_parts(x, D, pl);
     __syncthreads();
     if (wave < nseg) {
         sw_f32x4 acc[1];
-        sh_seg_wave<1>([&](int, int m) { return (m < 8 ? Wg + (int64_t)(i0 + m) * D : Wu + (int64_t)(i0 + m - 8) * D); },
-                       D, pl, wave, nseg, acc);
+        sw.run(pl, acc);
         sh_seg_store<1>(acc, wave, red);
     }
     __syncthreads();
@@ -183,11 +197,13 @@ __device__ __forceinline__ void sh_down_block(const uint16_t *__restrict__ Wd, c
     uint16_t *pl = (uint16_t *)smem;
     float *red = smem + (size_t)Is * 6 / 4;
     const int d0 = bid * SH_DN_O, nseg = sh_nseg(Is / SH_RG), wave = threadIdx.x >> 6;
+    ShSegWave<2> sw;
+    if (wave < nseg) sw.start([&](int t, int m) { return Wd + (int64_t)(d0 + 16 * t + m) * Is; }, Is, wave, nseg);
     sh_stage_parts(h, Is, pl);
     __syncthreads();
     if (wave < nseg) {
         sw_f32x4 acc[2];
-        sh_seg_wave<2>([&](int t, int m) { return Wd + (int64_t)(d0 + 16 * t + m) * Is; }, Is, pl, wave, nseg, acc);
+        sw.run(pl, acc);
         sh_seg_store<2>(acc, wave, red);
     }
     __syncthreads();
