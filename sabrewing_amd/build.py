@@ -19,7 +19,7 @@ from concurrent.futures import ThreadPoolExecutor
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
-HIP_SOURCES = ["backend_hip.hip", "k_gemm.hip", "k_dot8.hip", "k_mfma.hip", "k_idot.hip", "k_shared.hip", "k_route.hip", "coli_hip.hip",
+HIP_SOURCES = ["backend_hip.hip", "k_dot8.hip", "k_mfma.hip", "k_idot.hip", "k_shared.hip", "k_route.hip", "coli_hip.hip",
                "k_gen.hip", "k_glue.hip", "k_lanes.hip"]
 HIP_LIB = os.path.join(HERE, "libsabrewing_hip.so")
 LOADER_LIB = os.path.join(HERE, "libsabrewing_loader.so")

@@ -404,31 +404,12 @@ extern "C" int lag_hip_matmul_q8(float *y, const float *x, const void *W, int S,
 
 extern "C" int lag_hip_matmul_q4_g(float *y, const float *x, const void *packed, const void *scale,
                                    int S, int I, int O, int gs) {
-    if (gs <= 0 && !(I & 1)) return lanes_host(y, x, packed, 2, 0, scale, S, I, O);
-    // group scales: matmul_i4_grouped's lanes, the scales applied in f32 per group
-    if (gs >= 16 && gs % 16 == 0 && gs <= 256 && 256 % gs == 0 && I % gs == 0)
-        return lanes_host(y, x, packed, 3, 0, scale, S, I, O, gs);
-    if (!g_ok || fault_injected()) return -1;
-    if (S <= 0 || I <= 0 || O <= 0) return -1;
-    Carve cv;
-    const size_t o_x = cv.take((size_t)S * I * 4), o_idx = cv.take(16);
-    const size_t o_y = cv.take((size_t)S * O * 4);
-    if (grow_dev(g_arena, cv.off) || grow_pinned(g_hin, (size_t)S * I * 4 + 16) || grow_pinned(g_hout, (size_t)S * O * 4)) return -1;
-    char *A = (char *)g_arena.p, *H = (char *)g_hin.p;
-    memcpy(H, x, (size_t)S * I * 4);
-    int *hi = (int *)(H + (size_t)S * I * 4);
-    hi[0] = 0; hi[1] = 0; hi[2] = S;
-    CK(hipMemcpyAsync(A + o_x, H, (size_t)S * I * 4, hipMemcpyHostToDevice, g_st), "x upload");
-    CK(hipMemcpyAsync(A + o_idx, hi, 12, hipMemcpyHostToDevice, g_st), "index upload");
-    const int *d = (const int *)(A + o_idx);
-    SwGroups g = {d, d + 1, d + 2, nullptr, nullptr, 1, 0};
-    SwQ4 W = {(const uint8_t *)packed, (const float *)scale, O, I, gs, 1};
-    { PROF("q4_rows"); if (sw_launch_q4_rows_x(g_st, W, (const float *)(A + o_x), g, (float *)(A + o_y), S)) return fail_msg("q4 launch (shape unsupported?)"); }
-    CK(hipMemcpyAsync(g_hout.p, A + o_y, (size_t)S * O * 4, hipMemcpyDeviceToHost, g_st), "result download");
-    CK(hipStreamSynchronize(g_st), "stream sync");
-    memcpy(y, g_hout.p, (size_t)S * O * 4);
-    if (g_prof) prof_flush();
-    return 0;
+    // per-row scales: matmul_q4_k's lanes; group scales: matmul_i4_grouped's lanes, the
+    // scales applied in f32 per group
+    if (gs <= 0) return (I & 1) ? -1 : lanes_host(y, x, packed, 2, 0, scale, S, I, O);
+    if (gs % 16 || I % gs || (gs <= 256 ? 256 % gs : gs % 256))
+        return fail_msg("matmul_q4_g: group size unsupported (a multiple of 16 dividing 256, or of 256, dividing I)");
+    return lanes_host(y, x, packed, 3, 0, scale, S, I, O, gs);
 }
 extern "C" int lag_hip_matmul_q4(float *y, const float *x, const void *packed, const void *scale, int S, int I, int O) {
     if (I & 1) return -1;

@@ -559,11 +559,12 @@ extern "C" int coli_hip_tensor_update(ColiHipTensor *t, const void *weights, con
 
 // =============================================================== compute ====
 namespace {
-// y_dev[S][O] = x_dev[S][I] . W^T on the context's stream
+// y_dev[S][O] = x_dev[S][I] . W^T on the context's stream, in the CPU's f32 contract:
+// matmul_q4_k (per-row scales, fmt 2) or matmul_i4_grouped (group scales, fmt 4), the
+// 16-lane kernels of k_lanes.hip
 int gemm_dev(Ctx *c, const ColiHipTensor *t, float *y, const float *x, int S) {
-    const SwQ4 W = {(const uint8_t *)t->w, t->s, t->O, t->I, t->gs, 1};
-    const SwGroups g = {nullptr, nullptr, nullptr, nullptr, nullptr, 1, S};
-    if (sw_launch_q4_rows_x(c->st, W, x, g, y, S)) return 0;
+    const int gs = t->fmt == 4 ? t->gs : 0;
+    if (sw_launch_lanes16(c->st, t->w, gs > 0 ? 3 : 2, 0, t->s, x, S, t->I, t->O, y, gs)) return ok(hipErrorInvalidValue, "matmul launch (shape unsupported?)");
     return ok(hipGetLastError(), "matmul launch");
 }
 }  // namespace

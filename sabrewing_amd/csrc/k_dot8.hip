@@ -33,38 +33,6 @@
 #define RG SW_RG              // inputs per limb group
 #define CHG 16                // groups per run of the fixed row-sum order
 
-// Per-block timeline of the decode kernels, for a build with -DSW_TRACE only:
-// block b of kernel slot k writes its start and end (s_memrealtime, 100 MHz)
-// and hardware id to sw_trace[3 * (k * SW_TRACE_SLOT + b)].
-#ifdef SW_TRACE
-static __device__ unsigned long long sw_trace[5 * SW_TRACE_SLOT * 3];
-#define TR_BEGIN() const unsigned long long tr_t0 = wall_clock64()
-#define TR_END(k)                                                                                  \
-    do {                                                                                           \
-        __syncthreads();                                                                           \
-        if (threadIdx.x == 0 && blockIdx.x + gridDim.x * blockIdx.y < SW_TRACE_SLOT) {             \
-            unsigned long long *tp = sw_trace + 3 * ((k) * SW_TRACE_SLOT + blockIdx.x + gridDim.x * blockIdx.y); \
-            tp[0] = tr_t0; tp[1] = wall_clock64();                                                 \
-            tp[2] = (unsigned long long)__smid() | ((unsigned long long)__builtin_amdgcn_s_getreg((20 << 0) | (0 << 6) | (3 << 11)) << 32); \
-        }                                                                                          \
-    } while (0)
-#define TR_MARK(i) TR_MARKK(1, i)
-extern "C" int sw_trace_read(void *dst, size_t n) {
-    return hipMemcpyFromSymbol(dst, HIP_SYMBOL(sw_trace), n) == hipSuccess ? 0 : -1;
-}
-extern "C" int sw_trace_read_mid(void *dst, size_t n) {
-    return hipMemcpyFromSymbol(dst, HIP_SYMBOL(sw_trace_mid), n) == hipSuccess ? 0 : -1;
-}
-extern "C" int sw_trace_clear() {
-    static unsigned long long z[5 * SW_TRACE_SLOT * 3];
-    return hipMemcpyToSymbol(HIP_SYMBOL(sw_trace), z, sizeof(z)) == hipSuccess ? 0 : -1;
-}
-#else
-#define TR_BEGIN()
-#define TR_END(k)
-#define TR_MARK(i)
-#endif
-
 // ------------------------------------------------------------ limbs ----
 // rows x[r, K] f32 -> limbs (limbs_group in sw_gate.h), half a wave per group
 __global__ __launch_bounds__(256) void k_limbs(const float *__restrict__ x, int K, int rows, sw_u32x4 *__restrict__ xl,
@@ -221,7 +189,6 @@ __device__ __forceinline__ void dot8_glu_block(const Dot8GluArgs &A, int bx, int
         } else {
             e = A.sel[bx];
         }
-        TR_MARK(0);
     } else {
         if (!grp_work(grp, bx, TT, e, beg, tb, tend)) return;
     }
@@ -292,9 +259,7 @@ __device__ __forceinline__ void dot8_glu_block(const Dot8GluArgs &A, int bx, int
         }
 #pragma unroll
         for (int u = 0; u < PF; u++) step(s0 + u, u, false);
-        TR_MARK(1);
         __syncthreads();
-        TR_MARK(2);
         // token t of the tile by the threads RO t .. RO t + RO - 1 (a half-wave per limb group)
         const int t = tid / RO, i = tid - t * RO;
         if (t < nt) {
@@ -492,12 +457,10 @@ __device__ __forceinline__ void dot8_rows_block(const Dot8RowsArgs &A, int bx, i
 template <int PF, int TT, int C16, int RB>
 __global__ __launch_bounds__(256, 4) void k_dot8_rows(Dot8RowsArgs A) {
     extern __shared__ __align__(16) float red[];
-    TR_BEGIN();
     const int nb = (int)(gridDim.x * gridDim.y);
     const int w = A.grp.items ? sw_xcd_work((int)(blockIdx.x + gridDim.x * blockIdx.y), nb)
                               : (int)(blockIdx.x + gridDim.x * blockIdx.y);
     dot8_rows_block<PF, TT, C16, RB>(A, w % (int)gridDim.x, w / (int)gridDim.x, red);
-    TR_END(3);
 }
 #define RW_PF 4
 template <int RB>
@@ -692,9 +655,7 @@ __device__ __forceinline__ void dot8_down_combine_block(const Dot8DownArgs &A, i
 template <int C16>
 __global__ __launch_bounds__(1024) void k_dot8_down_combine(Dot8DownArgs A) {
     extern __shared__ __align__(16) float red[];
-    TR_BEGIN();
     dot8_down_combine_block<C16>(A, blockIdx.x, red);
-    TR_END(2);
 }
 
 int sw_launch_q4_dot8_down_combine(hipStream_t st, SwQ4 W, const sw_u32x4 *hl, const float *hs, const int *sel, const float *w,
@@ -728,18 +689,15 @@ struct ShDownArgs { const uint16_t *Wd; const float *h; int Is, D; float *out; }
 template <int BF16, int ONE>
 __global__ __launch_bounds__(SH_NT) void k_stage_route(RouterArgs R, int nbr, int S, ShGluArgs G) {
     extern __shared__ __align__(16) float smem[];
-    TR_BEGIN();
     const int b = blockIdx.x;
     if (b < nbr * S) router_block<BF16, ONE>(R, b % nbr, b / nbr, nbr, smem);
     else sh_glu_block(G.Wg, G.Wu, G.x, G.D, G.Is, G.h, b - nbr * S, smem);
-    TR_END(0);
 }
 
 // TTG: tokens per pass of the routed gate_up
 template <int PF, int PICK, int NP, int TTG, int C16, int RO>
 __global__ __launch_bounds__(DG_NT, PICK ? 1 : 4) void k_stage_experts(Dot8GluArgs A, int nbx, int nglu, ShDownArgs Sd) {
     extern __shared__ __align__(16) float smem[];
-    TR_BEGIN();
     const int b = blockIdx.x;
     if (b < nglu) {
         const int w = PICK == 0 && A.grp.items ? sw_xcd_work(b, nglu) : b;
@@ -747,7 +705,6 @@ __global__ __launch_bounds__(DG_NT, PICK ? 1 : 4) void k_stage_experts(Dot8GluAr
     } else {
         sh_down_block(Sd.Wd, Sd.h, Sd.Is, Sd.D, Sd.out, b - nglu, smem);
     }
-    TR_END(1);
 }
 template <int PICK, int NP, int TTG, int RO = 32>
 struct StageL {

@@ -22,7 +22,9 @@
 //         then a = fma(h, scale[o][g], a) over the groups in order.  The 16
 //         lanes of a row take two groups at a time (lanes 0-7 the even, 8-15
 //         the odd one); the group sums go through LDS to the row's lane 0,
-//         which runs the ordered scale chain.
+//         which runs the ordered scale chain.  A group wider than a tile (gs a
+//         multiple of 256) is taken by lanes 0-7 alone, their chains carried
+//         across its tiles.
 // Each (row, token) is one lane chain, so a result never depends on the
 // shape of the launch that computed it.
 //
@@ -105,9 +107,9 @@ __global__ __launch_bounds__(256) void k_lanes16(LanesArgs A) {
     const int imain = DP || WK == WK_I4G ? I : (WK == WK_I4 ? I & ~31 : I & ~15);
     const uint8_t *W = (const uint8_t *)A.W;
     const size_t rowb = (size_t)I * EB / 8;
-    float acc[TS];
+    float acc[TS], lg[TS];                             // lg: the lane chains of a group wider than a tile
 #pragma unroll
-    for (int t = 0; t < TS; t++) acc[t] = 0.f;
+    for (int t = 0; t < TS; t++) { acc[t] = 0.f; lg[t] = 0.f; }
     for (int c0 = 0; c0 < imain; c0 += LN_CC) {
         const int cn = min(LN_CC, imain - c0);         // a multiple of 16 (32 for DP and int4)
         // the 16 rows' tile: cn * EB / 8 bytes each, in 16-byte pieces (rows past O: zeros)
@@ -146,6 +148,32 @@ __global__ __launch_bounds__(256) void k_lanes16(LanesArgs A) {
         } else if constexpr (WK == WK_I4G) {
             const int gs = A.gs, ngt = cn / gs, half = j >> 3, jj = j & 7;
             float *hrow = hg + r * TS * (LN_CC / 16);
+            if (gs > LN_CC) {
+                // a group spans gs / LN_CC whole tiles: lanes 0-7 carry its chains across them,
+                // and its hsum8 and scale fma follow its last tile
+                if (half == 0) {
+                    for (int i = 0; i < cn; i += 16) {
+                        const float w0 = w_at<WK_I4>(row, i + jj), w1 = w_at<WK_I4>(row, i + 8 + jj);
+#pragma unroll
+                        for (int t = 0; t < TS; t++) {
+                            lg[t] = __builtin_fmaf(xt[t * LN_CC + i + jj], w0, lg[t]);
+                            lg[t] = __builtin_fmaf(xt[t * LN_CC + i + 8 + jj], w1, lg[t]);
+                        }
+                    }
+                }
+                if ((c0 + cn) % gs == 0) {                 // uniform
+                    const int o = o0 + r;
+                    const float sg = A.scale[(size_t)(o < O ? o : 0) * (I / gs) + (c0 + cn) / gs - 1];
+#pragma unroll
+                    for (int t = 0; t < TS; t++) {
+                        float v = lg[t] + __shfl_xor(lg[t], 4, 8);
+                        v = v + __shfl_xor(v, 2, 8);
+                        v = v + __shfl_xor(v, 1, 8);
+                        if (j == 0) acc[t] = __builtin_fmaf(v, sg, acc[t]);
+                        lg[t] = 0.f;
+                    }
+                }
+            }
             for (int g = half; g < ngt; g += 2) {          // this half's groups of the tile
                 float ln[TS];
 #pragma unroll
@@ -222,7 +250,8 @@ static void launch_lanes(hipStream_t st, const LanesArgs &A) {
 }
 
 // wkind 0 bf16, 1 int8 (+ scale), 2 per-row int4 (+ scale), 3 group-scaled int4
-// (+ scale [O][I/gs]; gs a multiple of 16 up to 256 dividing I); dp: the vdpbf16ps
+// (+ scale [O][I/gs]; gs dividing I, a multiple of 16 dividing 256 or a multiple of
+// 256); dp: the vdpbf16ps
 // contract (bf16 weights, I % 32 == 0)
 int sw_launch_lanes16(hipStream_t st, const void *W, int wkind, int dp, const float *scale, const float *x, int S,
                       int I, int O, float *y, int gs) {
@@ -234,7 +263,7 @@ int sw_launch_lanes16_ld(hipStream_t st, const void *W, int wkind, int dp, const
     if (!W || !x || !y || S <= 0 || I <= 0 || O <= 0 || ldx < I || ldy < O) return -1;
     if (dp && (wkind != WK_BF16 || I % 32)) return -1;
     if ((wkind == WK_I4 || wkind == WK_I4G) && (I & 1)) return -1;
-    if (wkind == WK_I4G && (gs < 16 || gs % 16 || gs > LN_CC || LN_CC % gs || I % gs)) return -1;
+    if (wkind == WK_I4G && (gs < 16 || gs % 16 || (gs <= LN_CC ? LN_CC % gs : gs % LN_CC) || I % gs)) return -1;
     if (wkind != WK_BF16 && !scale) return -1;
     const LanesArgs A = {W, wkind == WK_BF16 ? nullptr : scale, x, y, S, I, O, gs, ldx, ldy};
     if (dp) launch_lanes<WK_BF16, 1>(st, A);

@@ -119,7 +119,6 @@ __device__ void gate_topk_wave(const float *__restrict__ src, int E, int K, int 
         v[i] = src[e];
         b[i] = hasb ? bias[e] : 0.f;
     }
-    TR_MARKK(0, 4);
     // the sums of the softmax paths in expert order: lane l's slots, then lane l + 1's
     auto sum_f = [&](float *p) {
         float sum = 0.f;
@@ -192,7 +191,6 @@ __device__ void gate_topk_wave(const float *__restrict__ src, int E, int K, int 
         ko[i] = (e < E && key > -1e30f) ? ord_f32(key) : 0u;
         if (e < E && ko[i] == 0u) frm |= 1u << i;
     }
-    TR_MARKK(0, 5);
     sk = 0; wk = 0.f;
     // the passes that find a valid key (as many as there are valid experts), then the
     // all-invalid fallback for the rest: by then every valid expert is taken, so the
@@ -234,7 +232,6 @@ __device__ void gate_topk_wave(const float *__restrict__ src, int E, int K, int 
         if (lane == bl) frm &= ~(1u << ls);
         if (lane == a) { sk = NPER * bl + slot; wk = wb; }
     }
-    TR_MARKK(0, 6);
     if (act == 4) {                                   // qwen35: always, in double (c/qwen35.c:585-587)
         double tot = 0.0;
         for (int a = 0; a < K; a++) tot += (double)lanef(wk, a);
@@ -251,117 +248,6 @@ __device__ void gate_topk_wave(const float *__restrict__ src, int E, int K, int 
         for (int a = 0; a < K; a++) sm += lanef(wk, a);
         wk = wk / sm;
     }
-}
-
-// The same routing by a whole block of NT threads (E <= NT), by counting
-// instead of K dependent passes.  Expert e gets the 64-bit word (order bits of
-// key + 0.0, ~e) when its key is valid (> -1e30; a NaN is not) and (0, ~e)
-// when not, so a larger word means a larger key, equal keys go to the lower
-// id and the invalid experts come last in id order -- the order in which the
-// K passes of moe_topk, with their all-invalid fallback to the lowest
-// unselected id, pick -- and pick a is the expert with exactly a larger
-// words.  On return the picks and weights (renormalised if norm) are in
-// sh.sk[0..K), sh.wk[0..K).
-typedef unsigned long long sw_u64x2 __attribute__((ext_vector_type(2)));
-struct TopkBlockLDS {
-    alignas(16) uint64_t key[256];
-    float val[256];
-    int part[512];
-    int sk[64];
-    float wk[64];
-    uint64_t tab[32];
-};
-template <int NT, int NPER>   // NPER: E <= 64 NPER (the softmax by one wave)
-__device__ void gate_topk_block(const float *__restrict__ src, int E, int K, int act, const float *__restrict__ bias,
-                                int use_bias, int norm, TopkBlockLDS &sh) {
-    const int tid = threadIdx.x, lane = tid & 63;
-    float v = 0.f, b = 0.f;
-    if (tid < E) {
-        v = src[tid];
-        b = (use_bias && bias) ? bias[tid] : 0.f;
-    }
-    TR_MARKK(1, 3);
-    if (act == 1) {                                   // softmax on wave 0, the scan's expressions
-        if (tid < 32) sh.tab[tid] = sw_exp2f_tab[tid];
-        if (tid < E) sh.val[tid] = v;
-        __syncthreads();
-        if (tid < 64) {
-            float p[NPER];
-#pragma unroll
-            for (int i = 0; i < NPER; i++) p[i] = sh.val[min(lane + 64 * i, E - 1)];
-            float mx = -__builtin_inff();
-            bool any = false;
-#pragma unroll
-            for (int i = 0; i < NPER; i++) {
-                const int e = lane + 64 * i;
-                if (e < E && p[i] == p[i]) { mx = any ? fmaxf(mx, p[i]) : p[i]; any = true; }
-            }
-            for (int o = 32; o; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-            const float r0 = __shfl(p[0], 0);
-            if (r0 != r0) mx = r0;                    // a NaN in slot 0 propagates, as in the scan
-#pragma unroll
-            for (int i = 0; i < NPER; i++) p[i] = sw_expf_t(p[i] - mx, sh.tab);
-            double sum = 0.0;                         // in expert order, in double
-#pragma unroll
-            for (int i = 0; i < NPER; i++)
-                for (int l = 0; l < 64 && l + 64 * i < E; l++) sum += (double)lanef(p[i], l);
-            const float inv = (float)(1.0 / sum);
-#pragma unroll
-            for (int i = 0; i < NPER; i++) {
-                const int e = lane + 64 * i;
-                if (e < E) sh.val[e] = p[i] * inv;
-            }
-        }
-        __syncthreads();
-        if (tid < E) v = sh.val[tid];
-    }
-    uint64_t mykey = 0ull;
-    if (tid < E) {
-        const float key = v + b;
-        const uint32_t lo = 0xFFFFFFFFu - (uint32_t)tid;
-        mykey = key > -1e30f ? (((uint64_t)ord_f32(key) << 32) | lo) : (uint64_t)lo;
-        sh.key[tid] = mykey;
-        sh.val[tid] = v;
-    }
-    __syncthreads();
-    TR_MARKK(1, 4);
-    // H threads per expert, each counting the larger words in its E/H of them
-    const int H = NT / E, per = (E + H - 1) / H;
-    const int e = tid % E, h = tid / E;
-    if (h < H) {
-        const uint64_t kk = sh.key[e];
-        const int j0 = h * per, j1 = min(E, j0 + per);
-        int c = 0, jj = j0;
-        // 32 words per batch in sixteen 16-byte reads (one address per wave: a
-        // broadcast), all in flight before the compares
-        if ((j0 & 1) == 0) {
-            for (; jj + 32 <= j1; jj += 32) {
-                sw_u64x2 w2[16];
-#pragma unroll
-                for (int q = 0; q < 16; q++) w2[q] = *(const sw_u64x2 *)(sh.key + jj + 2 * q);
-#pragma unroll
-                for (int q = 0; q < 16; q++) c += (w2[q].x > kk ? 1 : 0) + (w2[q].y > kk ? 1 : 0);
-            }
-        }
-        for (; jj < j1; jj++) c += sh.key[jj] > kk ? 1 : 0;
-        sh.part[h * E + e] = c;
-    }
-    __syncthreads();
-    TR_MARKK(1, 5);
-    if (tid < E) {
-        int rank = 0;
-        for (int hh = 0; hh < H; hh++) rank += sh.part[hh * E + tid];
-        if (rank < K) { sh.sk[rank] = tid; sh.wk[rank] = v; }
-    }
-    __syncthreads();
-    TR_MARKK(1, 6);
-    if (tid < 64 && norm) {                           // renormalised: summed in rank order
-        float wk = tid < K ? sh.wk[tid] : 0.f;
-        float sm = 0.f;
-        for (int a = 0; a < K; a++) sm += lanef(wk, a);
-        if (tid < K) sh.wk[tid] = wk / sm;
-    }
-    __syncthreads();
 }
 
 // ------------------------------------------------------------ limbs ----

@@ -7,26 +7,18 @@
 //              down [E*D, I/2], scales [E*D, I/gs]; bf16 shared expert
 //              [Is,D],[Is,D],[D,Is]; router in "chain-major" order (see below).
 //   x, out     f32 [S, D] (out is accumulated into: out += MoE(x)).
-//   f16 planes activations feeding the int4 MFMA GEMMs as two f16 rows per
-//              token, hi = RN(v) and lo = RN(v - hi) ([2S, K] f16, row 2t hi,
-//              row 2t+1 lo), each 8-element block stored in the order
-//              0,4,1,5,2,6,3,7 so one 16-byte load is one MFMA B fragment.
-//   bf16 planes the same split for the bf16 (shared-expert) GEMMs, natural order.
+//   activations of the int4 GEMMs as dot8 limbs (k_dot8.hip) or MFMA digits
+//              (k_mfma.hip) per group of 32 inputs; of the bf16 shared expert
+//              as three exact bf16 parts (sw_shared.h).
 //
 // MFMA operand convention for v_mfma_f32_16x16x32_{f16,bf16} (lane l):
 //   A: row l%16, hardware k 8*(l/16)+h for element h of the 8-vector
 //   B: col l%16, same k;   C: col l%16, rows 4*(l/16)+j, j = 0..3
 // (checked on the device by lag_hip_selftest).
 //
-// Per-output reduction contract of every int4 / bf16 GEMM here (B = 1
-// per-token, grouped decode and prefill kernels alike): K is walked in
-// 128-wide super-steps ss, each split into four 32-k MFMAs q = 0..3 (k =
-// 128 ss + 32 kb + 8 q + {0,4,1,5,2,6,3,7} for lane group kb), accumulated
-// in order into one f32 chain per column; the hi and lo columns of a token
-// are added at the end (hi + lo), then scaled (2^-8 weight prescale for group
-// scales, the f32 row scale for per-row scales).  Because no kernel splits K,
-// a token's output does not depend on which other tokens share its launch:
-// the grouped path is bit-identical to the per-token path.
+// Every reduction here is fixed by the operation and its shape alone, never
+// by the batch: a token's output does not depend on which other tokens share
+// its launch, so the grouped paths are bit-identical to the per-token path.
 #ifndef SW_HIP_H
 #define SW_HIP_H
 #include <hip/hip_runtime.h>
@@ -58,16 +50,6 @@ extern thread_local SwLaunchEvents *sw_launch_events;
             hipLaunchKernelGGL(kernel, grid, block, lds, st, __VA_ARGS__);                                        \
         }                                                                                                         \
     } while (0)
-// Mid-block timestamps of the decode kernels, for a build with -DSW_TRACE only:
-// TR_MARKK(k, i) stores s_memrealtime of thread 0 of block b into slot
-// (k, b, i) of sw_trace_mid (one definition per translation unit).
-#ifdef SW_TRACE
-#define SW_TRACE_SLOT 16384
-static __device__ unsigned long long sw_trace_mid[2 * SW_TRACE_SLOT * 8];
-#define TR_MARKK(k, i) do { if (threadIdx.x == 0 && blockIdx.x < SW_TRACE_SLOT) sw_trace_mid[((k) * SW_TRACE_SLOT + blockIdx.x) * 8 + (i)] = wall_clock64(); } while (0)
-#else
-#define TR_MARKK(k, i)
-#endif
 // Raw buffer access: a tensor is one descriptor (base and byte extent in
 // scalar registers); each lane adds a 32-bit offset and each step a scalar
 // one; a load past the extent returns 0 and touches no memory.
@@ -192,12 +174,6 @@ static inline int sw_q4_gsh(const SwQ4 &W, int &gsh) {
     return 0;
 }
 
-// bf16 weight tensor [O, K]
-struct SwBf16 {
-    const uint16_t *w;
-    int O, K;
-};
-
 // ---- kernels (launch wrappers, all async on `st`) ----
 // router logits [S,E] (exact 16-lane FMA-chain contract; Wc chain-major), the
 // sigmoid / softplus scores [S,E] next to them, with xl non-null the dot8
@@ -218,20 +194,10 @@ int sw_launch_gate_topk(hipStream_t st, const float *logits, const float *scores
 // counting sort by expert; with items non-null also the pass list of tt tokens (SwGroups)
 int sw_launch_bucket(hipStream_t st, const int *sel, int S, int K, int E, int *gexp, int *gbeg,
                      int *gcnt, int *G, int *grow, int *rowof, int tt, int *items, int *P);
-// out planes of SiLU-GLU(gate, up) for every packed row of every group
-// maxtok: an upper bound of any group's token count (1 for the per-token path)
-// (x: f32 activations [tokens, K], split into hi/lo planes while staged)
-int sw_launch_q4_gateup(hipStream_t st, SwQ4 W, const float *x, SwGroups g, int I, _Float16 *hplanes, int maxtok);
-// Y[packed row, O] (f32) for every group, from f16 planes or from f32 rows
-int sw_launch_q4_rows(hipStream_t st, SwQ4 W, const _Float16 *planes, SwGroups g, float *Y, int maxtok);
-int sw_launch_q4_rows_x(hipStream_t st, SwQ4 W, const float *x, SwGroups g, float *Y, int maxtok);
-// bf16 weights, one implicit group of S tokens, K split in four quarters
-int sw_launch_bf16_gateup(hipStream_t st, SwBf16 Wg, SwBf16 Wu, const float *x, int S, uint16_t *hplanes);
-int sw_launch_bf16_rows(hipStream_t st, SwBf16 W, const uint16_t *planes, int S, float *Y);
-int sw_launch_bf16_rows_x(hipStream_t st, SwBf16 W, const float *x, int S, float *Y);
 // the reference CPU's 16-lane GEMV contracts (k_lanes.hip), bit for bit: wkind 0 bf16,
 // 1 int8 (+ row scale), 2 per-row int4 (+ row scale), 3 group-scaled int4 (+ scales
-// [O][I/gs], matmul_i4_grouped's lanes); dp: bf16-rounded activations through the
+// [O][I/gs], matmul_i4_grouped's lanes; gs a multiple of 16 dividing 256, or of 256);
+// dp: bf16-rounded activations through the
 // vdpbf16ps lane order
 int sw_launch_lanes16(hipStream_t st, const void *W, int wkind, int dp, const float *scale, const float *x, int S,
                       int I, int O, float *y, int gs);
@@ -268,8 +234,6 @@ int sw_launch_q4_dot8_down_combine(hipStream_t st, SwQ4 W, const sw_u32x4 *hl, c
                                    const float *wsh = nullptr, int ns = 0);
 // the int4 down projection fused with the rank-order combine for one token:
 // out[d] += (sum_a w[a] * down_{sel[a]}(h_a)[d]) * route_scale (+ shared[d])
-int sw_launch_q4_down_combine(hipStream_t st, SwQ4 W, const _Float16 *hplanes, const int *sel, const float *w, int K,
-                              float route_scale, const float *shared, float *out);
 // out[s] (+)= route_scale * sum_a w[s,a] * slots[rowof[s,a]] (+ shared[s])
 // (wsh non-null: shared [S][ns][D] gated by wsh [S][ns] after the ranks, as above)
 int sw_launch_combine(hipStream_t st, const float *slots, const int *rowof, const float *w, int S, int K, int D,

@@ -106,9 +106,7 @@ __device__ __forceinline__ void router_block(const RouterArgs &R, int bx, int s,
         for (int u = 0; u < RT_PF; u++) ring[u] = slice(u);
         stage_x_store(xv);
     }
-    TR_MARKK(0, 7);
     __syncthreads();
-    TR_MARKK(0, 0);
     const float *xj = xt + j * ML;
     float acc = 0.f;
     auto chain4 = [&](int q, const sw_u32x4 &w) {
@@ -155,7 +153,6 @@ __device__ __forceinline__ void router_block(const RouterArgs &R, int bx, int s,
         for (int u = 0; u < RT_PF; u++)
             if (q0 + u < NQ) chain4(q0 + u, ring[u]);
     }
-    TR_MARKK(0, 1);
     tab[lane & 31] = tabv;                            // every wave writes the whole table (equal values)
     wave_sync();
     float v = acc;

@@ -22,7 +22,7 @@ def q4_case(orc, O, I, gs, seed):
     return p, s
 
 
-@pytest.mark.parametrize("gs", [0, 32, 64, 256])
+@pytest.mark.parametrize("gs", [0, 32, 64, 256, 512, 2048])
 @pytest.mark.parametrize("S_", [1, 3, 17, 70])
 def test_matmul_q4(be, orc, gs, S_):
     O, I = 512, 2048
@@ -33,7 +33,8 @@ def test_matmul_q4(be, orc, gs, S_):
     got = be.matmul_q4(x, dp, ds, O, gs)
     dp.free(); ds.free()
     # per-row scales: matmul_q4_k's F32 lanes; group scales: matmul_i4_grouped's lanes with
-    # the scales applied in f32 per group -- bit for bit at every S
+    # the scales applied in f32 per group (groups wider than the kernel's 256-column tile
+    # too) -- bit for bit at every S
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
