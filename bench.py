@@ -30,8 +30,9 @@ HBM_PEAK_GBS = 8000.0
 # activations written per 32 inputs as 7 signed base-8 digits under a power-of-two
 # factor (exact integer dots, |input error| <= 2^-21 of the group's largest input);
 # f32 accumulation; the router and the shared expert in f32 fma chains on bf16 weights
-DTYPE = ("int4 x int4-digit activations (7 base-8 limbs per 32 inputs, 2^-21 of the group max), "
-         "exact int32 dots, f32 scales and accumulation; f32 router and shared expert on bf16 weights")
+DTYPE = ("int4 weights x 7-digit base-8 activation limbs per 32 inputs (2^-21 of the group max), "
+         "exact int32 dots, f32 scales and accumulation; router f32 FMA chains on bf16 weights; "
+         "shared expert bf16 weights x f32 inputs split exactly into three bf16 parts on the MFMA")
 # the reference CPU baseline's OpenMP placement (c/moe_util.h:78-86 sets one thread per
 # physical core; the pinning is the reference's measured setting); read when the
 # OpenMP runtime first starts, so set before any OpenMP library loads

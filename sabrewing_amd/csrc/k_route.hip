@@ -57,9 +57,12 @@ __global__ __launch_bounds__(512) void k_router_logits(RouterArgs R) {
     router_block<BF16, ONE>(R, blockIdx.x, blockIdx.y, gridDim.x, smem);
 }
 
+// a 1-D grid of (expert block, token tile) pairs, dealt so that an XCD runs whole
+// token tiles (all their expert blocks), whose x then comes from its L2
 template <int BF16, int TT, int NW>
-__global__ __launch_bounds__(64 * NW) void k_router_tiles(RouterArgs R, int S) {
-    router_tile_block<BF16, TT, NW>(R, S, blockIdx.x, blockIdx.y);
+__global__ __launch_bounds__(64 * NW) void k_router_tiles(RouterArgs R, int S, int nbx) {
+    const int w = sw_xcd_work((int)blockIdx.x, (int)gridDim.x);
+    router_tile_block<BF16, TT, NW>(R, S, w % nbx, w / nbx);
 }
 
 // token tile and waves per block (4 experts each, sharing the tile's x in LDS): 16 tokens
@@ -77,8 +80,9 @@ int sw_launch_router_tiles(hipStream_t st, const void *Wc, int w_bf16, const flo
     router_tile_shape(S, tt, nw);
     const RouterArgs R = {Wc, x, D, E, logit_bias, logits, route_act, scores, nullptr, nullptr, nullptr};
     const int ng4 = (E + 3) / 4;
-    const dim3 grid((unsigned)((ng4 + nw - 1) / nw), (unsigned)((S + tt - 1) / tt));
-#define SW_RT(B, T, W) SW_LAUNCH((k_router_tiles<B, T, W>), grid, dim3(64 * W), 0, st, R, S)
+    const int nbx = (ng4 + nw - 1) / nw;
+    const dim3 grid((unsigned)((int64_t)nbx * ((S + tt - 1) / tt)));
+#define SW_RT(B, T, W) SW_LAUNCH((k_router_tiles<B, T, W>), grid, dim3(64 * W), 0, st, R, S, nbx)
     if (w_bf16) {
         if (tt == 16) SW_RT(1, 16, 4); else SW_RT(1, 8, 8);
     } else {

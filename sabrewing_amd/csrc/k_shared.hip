@@ -29,7 +29,9 @@ __global__ __launch_bounds__(256) void k_sh_parts(const float *__restrict__ x, i
 // tokens' part words of a step go through LDS (two buffers: the next step's
 // loads are in flight in registers while the waves read this one), each
 // token's 192 bytes at a padded stride; the waves' weight words come from
-// global memory a step ahead.  The fold starts from -0.0, the identity of
+// global memory a step ahead.  Blocks are dealt so that an XCD runs whole
+// token tiles (all their row blocks), whose part words then come from its L2.
+// The fold starts from -0.0, the identity of
 // f32 addition (-0 + y == y bit for bit), so every segment is added the same way.
 #define SHB_TOK 64             // tokens per block
 #define SHB_TS 208             // LDS bytes per token and step: 192 + 16 of padding
@@ -115,7 +117,8 @@ __global__ __launch_bounds__(256) void k_sh_glu_mf(const uint16_t *__restrict__ 
                                                    uint16_t *__restrict__ hp) {
     __shared__ __align__(16) uint8_t lds[2 * SHB_STAGE];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, m = lane & 15, kq = lane >> 4;
-    const int ib = blockIdx.x * 64 + 16 * wave, tok0 = blockIdx.y * SHB_TOK;
+    const int nrb = Is / 64, w = sw_xcd_work((int)blockIdx.x, (int)gridDim.x);   // an XCD's blocks: whole token tiles
+    const int ib = (w % nrb) * 64 + 16 * wave, tok0 = (w / nrb) * SHB_TOK;
     sw_f32x4 tot[2][4];
     sh_block_tiles([&](int t, int r) {
         const int i = ib + 8 * t + (r & 7);
@@ -151,7 +154,8 @@ __global__ __launch_bounds__(256) void k_sh_down_mf(const uint16_t *__restrict__
                                                     int Is, int D, float *__restrict__ out) {
     __shared__ __align__(16) uint8_t lds[2 * SHB_STAGE];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, m = lane & 15, kq = lane >> 4;
-    const int db = blockIdx.x * 128 + 32 * wave, tok0 = blockIdx.y * SHB_TOK;
+    const int nrb = D / 128, w = sw_xcd_work((int)blockIdx.x, (int)gridDim.x);
+    const int db = (w % nrb) * 128 + 32 * wave, tok0 = (w / nrb) * SHB_TOK;
     sw_f32x4 tot[2][4];
     sh_block_tiles([&](int t, int r) { return Wd + (int64_t)(db + 16 * t + r) * Is; }, hp, S, Is, tok0, lds, tot);
 #pragma unroll
@@ -271,7 +275,7 @@ int sw_launch_sh_glu(hipStream_t st, const uint16_t *Wg, const uint16_t *Wu, con
                      uint16_t *hp) {
     if (S <= 0 || Is % 64 || !sh_shape_ok(D)) return -1;
     if (S <= SHK_MAX_S) return launch_sk<1>(st, Wg, Wu, xp, S, D, Is, Is / 8, hp);
-    const dim3 grid((unsigned)(Is / 64), (unsigned)((S + SHB_TOK - 1) / SHB_TOK));
+    const dim3 grid((unsigned)(Is / 64 * ((S + SHB_TOK - 1) / SHB_TOK)));
     SW_LAUNCH(k_sh_glu_mf, grid, dim3(256), 0, st, Wg, Wu, xp, S, D, Is, hp);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
@@ -279,7 +283,7 @@ int sw_launch_sh_glu(hipStream_t st, const uint16_t *Wg, const uint16_t *Wu, con
 int sw_launch_sh_down(hipStream_t st, const uint16_t *Wd, const uint16_t *hp, int S, int Is, int D, float *out) {
     if (S <= 0 || D % 128 || !sh_shape_ok(Is)) return -1;
     if (S <= SHK_MAX_S) return launch_sk<0>(st, Wd, nullptr, hp, S, Is, D, D / 16, out);
-    const dim3 grid((unsigned)(D / 128), (unsigned)((S + SHB_TOK - 1) / SHB_TOK));
+    const dim3 grid((unsigned)(D / 128 * ((S + SHB_TOK - 1) / SHB_TOK)));
     SW_LAUNCH(k_sh_down_mf, grid, dim3(256), 0, st, Wd, hp, S, Is, D, out);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
