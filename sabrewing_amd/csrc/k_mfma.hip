@@ -25,21 +25,23 @@
 // expanded from packed dword q of the row's group (nibble k at bits 4(k&7)).
 //
 // Block: 128 weight rows (8 tiles of 16) x a tile of up to 64 tokens (4
-// tiles of 16) of one group, 8 waves; wave w takes row tiles w&3 and (w&3)+4
+// tiles of 16) of one group, 16 waves; wave w takes row tiles w&3 and (w&3)+4
 // (for gate_up the gate and the up rows of the same 16 outputs) against
-// token tiles 2(w>>2) and 2(w>>2)+1, so each lane holds 16 (row, token) sums.
-// The operands of 4 input groups at a time -- the rows' weights expanded
-// once for the 8 waves, the tokens' digits, the scales and the token factors
-// -- are staged in LDS in two buffers: while the waves compute one chunk from
-// LDS, the next chunk's loads are in flight in registers.  The inner loop
-// reads LDS only, every wave read a contiguous 1 KB (conflict-free).
+// token tile w>>2, so each lane holds 8 (row, token) sums and a wave stays
+// within 128 registers: four waves per SIMD, which hide each other's MFMA,
+// LDS and barrier waits.  The operands of 4 input groups at a time -- the
+// rows' weights expanded once for the 16 waves, the tokens' digits, the
+// scales and the token factors -- are staged in LDS in two buffers: while the
+// waves compute one chunk from LDS, the next chunk's loads are in flight in
+// registers.  The inner loop reads LDS only, every wave read a contiguous 1 KB
+// (conflict-free).
 #include "sw_hip.h"
 #include "sw_gate.h"
 
 #define MF_DW 32           // digit dwords per (input row, group)
 #define MF_ROWS 128        // weight rows per block
 #define MF_TT SW_MF_TT     // tokens per block tile (64)
-#define MF_NT 512          // threads per block: 8 waves
+#define MF_NT 1024         // threads per block: 16 waves
 #define MF_CG 4            // input groups per staged chunk
 // one chunk buffer in LDS: expanded weights [g][tile 8][quarter 4][row 16] x 16 B,
 // digits [g][token tile 4][op 2][quarter 4][token 16] x 16 B, scales [g][row],
@@ -153,6 +155,7 @@ struct MfIc { static constexpr int v = N; };
 
 template <int GLU, int CH, int FULL, int PT>
 __global__ __launch_bounds__(MF_NT, 1) void k_mf(MfArgs A) {
+    static_assert(MF_NT == 1024 && MF_CG * MF_ROWS == 512 && MF_CG * MF_TT * 8 == 2 * MF_NT, "staging map");
     extern __shared__ __align__(16) uint8_t mf_lds[];
     const SwQ4 W = A.W;
     const SwGroups grp = A.grp;
@@ -160,7 +163,7 @@ __global__ __launch_bounds__(MF_NT, 1) void k_mf(MfArgs A) {
     const int NC = G / MF_CG;                              // staged chunks (G % 4 == 0)
     const int NCV = (G + CH - 1) / CH * (CH / MF_CG);      // chunks of the padded runs
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, col = lane & 15, kq = lane >> 4;
-    const int mp = wave & 3, np = wave >> 2;               // row tiles mp, mp + 4; token tiles 2np, 2np + 1
+    const int mp = wave & 3, tt = wave >> 2;               // row tiles mp, mp + 4; token tile tt
 
     // block -> (tile, row block), XCD-aware over the live blocks
     const int nlive = *grp.P * A.nrb;
@@ -201,47 +204,54 @@ __global__ __launch_bounds__(MF_NT, 1) void k_mf(MfArgs A) {
         rs = sw_q4_rs(W);
     }
 
-    // ---- staging: this thread's units of a chunk
-    //  weights: row ra = tid & 127 of group tid >> 7 (16 B packed, expanded on the store) + its scale
-    //  digits:  16 B (op, quarter) of token tb of each of the 4 groups
-    //  factors: token tx of group tid >> 6 (threads < 256)
-    const int ra = tid & 127, ga = tid >> 7;
+    // ---- staging: this thread's units of a chunk (u = tid & 511 within a group of 512 units)
+    //  weights (threads < 512): row ra = tid & 127 of group tid >> 7 (16 B packed, expanded on
+    //           the store) + its scale
+    //  digits:  16 B (op, quarter) of token tb of groups tid >> 9 and (tid >> 9) + 2: unit u of a
+    //           group is token tile u >> 7, op (u >> 6) & 1, quarter (u >> 4) & 3, token u & 15
+    //  factors (threads < 256): token tx of group tid >> 6
+    constexpr int DG_PER = MF_CG * MF_TT * 8 / MF_NT;      // digit units per thread (2)
+    const bool wst = tid < MF_CG * MF_ROWS;                // uniform per wave
+    const int ra = tid & 127, ga = (tid >> 7) & 3;
     const uint32_t rowa = srow(ra);
-    const int tb = ((tid >> 7) & 3) * 16 + (tid & 15), opb = (tid >> 6) & 1, kqb = (tid >> 4) & 3;
+    const int tb = ((tid >> 7) & 3) * 16 + (tid & 15), opb = (tid >> 6) & 1, kqb = (tid >> 4) & 3, gb = tid >> 9;
     const uint32_t *__restrict__ dgb = A.dg + token(tb) * G * MF_DW + opb * 16 + kqb * 4;
-    const int tx = tid & 63, gx = tid >> 6;
+    const int tx = tid & 63, gx = (tid >> 6) & 3;
     const float *__restrict__ xsx = A.xs + token(tx) * G;
-    sw_u32x4 pka, pkb[MF_CG];
+    sw_u32x4 pka, pkb[DG_PER];
     float psa = 1.0f, pxf = 0.f;
     auto stage_load = [&](int c) {
         const int g0 = c * MF_CG;
-        pka = sw_ld16(rq, rowa * rbytes + (uint32_t)(g0 + ga) * 16, 0);
-        if (W.gs > 0) psa = sw_ld4f(rs, (rowa * (uint32_t)ng + (uint32_t)(((g0 + ga) * SW_RG) >> A.gsh)) * 4, 0);
+        if (wst) {
+            pka = sw_ld16(rq, rowa * rbytes + (uint32_t)(g0 + ga) * 16, 0);
+            if (W.gs > 0) psa = sw_ld4f(rs, (rowa * (uint32_t)ng + (uint32_t)(((g0 + ga) * SW_RG) >> A.gsh)) * 4, 0);
+        }
 #pragma unroll
-        for (int v = 0; v < MF_CG; v++) pkb[v] = *(const sw_u32x4 *)(dgb + (g0 + v) * MF_DW);
+        for (int v = 0; v < DG_PER; v++) pkb[v] = *(const sw_u32x4 *)(dgb + (g0 + gb + 2 * v) * MF_DW);
         if (tid < MF_CG * MF_TT) pxf = xsx[g0 + gx];
     };
     auto stage_store = [&](int buf) {
         uint8_t *base = mf_lds + buf * MF_BUF;
         sw_i32x4 *Al = (sw_i32x4 *)(base + MF_A_OFF);
         sw_u32x4 *Bl = (sw_u32x4 *)(base + MF_B_OFF);
-        const int m = ra >> 4, i = ra & 15;
+        if (wst) {
+            const int m = ra >> 4, i = ra & 15;
 #pragma unroll
-        for (int q = 0; q < 4; q++) Al[((ga * 8 + m) * 4 + q) * 16 + i] = mf_expand(pka[q]);
-        ((float *)(base + MF_S_OFF))[ga * MF_ROWS + ra] = psa;
+            for (int q = 0; q < 4; q++) Al[((ga * 8 + m) * 4 + q) * 16 + i] = mf_expand(pka[q]);
+            ((float *)(base + MF_S_OFF))[ga * MF_ROWS + ra] = psa;
+        }
 #pragma unroll
-        for (int v = 0; v < MF_CG; v++) Bl[v * MF_NT + tid] = pkb[v];
+        for (int v = 0; v < DG_PER; v++) Bl[v * MF_NT + tid] = pkb[v];
         if (tid < MF_CG * MF_TT) ((float *)(base + MF_X_OFF))[gx * MF_TT + tx] = pxf;
     };
 
-    const bool wact = np * 32 < nt;                        // uniform over the wave
-    const bool two = np * 32 + 16 < nt;                    // the wave's second token tile holds tokens
-    float y[2][2][4], L[2][2][4][4], run[2][2][4];
+    const bool wact = tt * 16 < nt;                        // uniform over the wave
+    float y[2][4], L[2][4][4], run[2][4];
     // the LDS operands of one group for this wave
     struct Frag {
-        sw_i32x4 a[2], b[2][2];
+        sw_i32x4 a[2], b[2];
         sw_f32x4 s4[2];
-        float xf[2];
+        float xf;
     };
     auto fetch = [&](Frag &F, const uint8_t *base, int g) {
         const sw_i32x4 *Al = (const sw_i32x4 *)(base + MF_A_OFF);
@@ -253,63 +263,56 @@ __global__ __launch_bounds__(MF_NT, 1) void k_mf(MfArgs A) {
             F.a[mi] = Al[((g * 8 + m) * 4 + kq) * 16 + col];
             F.s4[mi] = *(const sw_f32x4 *)(Sl + g * MF_ROWS + 16 * m + 4 * kq);
         }
-#pragma unroll
-        for (int ni = 0; ni < 2; ni++) {
-            const int n = 2 * np + ni;
-            F.b[ni][0] = Bl[((g * 4 + n) * 2 + 0) * 64 + lane];
-            F.b[ni][1] = Bl[((g * 4 + n) * 2 + 1) * 64 + lane];
-            F.xf[ni] = Xl[g * MF_TT + 16 * n + col];
-        }
+        F.b[0] = Bl[((g * 4 + tt) * 2 + 0) * 64 + lane];
+        F.b[1] = Bl[((g * 4 + tt) * 2 + 1) * 64 + lane];
+        F.xf = Xl[g * MF_TT + 16 * tt + col];
     };
     // the terms of one group (zero terms for the padding of a run: REAL = 0) into the trees
-    auto group = [&](const Frag &F, int gl, bool first, auto RC, auto TC) {
-        constexpr bool REAL = decltype(RC)::v, TWO = decltype(TC)::v;
+    auto group = [&](const Frag &F, int gl, bool first, auto RC) {
+        constexpr bool REAL = decltype(RC)::v;
+        sw_i32x4 R0[2], R1[2];
+        if (REAL) {
+            const sw_i32x4 z = {0, 0, 0, 0};
 #pragma unroll
-        for (int ni = 0; ni < (TWO ? 2 : 1); ni++) {
-            sw_i32x4 R0[2], R1[2];
-            if (REAL) {
-                const sw_i32x4 z = {0, 0, 0, 0};
-#pragma unroll
-                for (int mi = 0; mi < 2; mi++) {
-                    R0[mi] = __builtin_amdgcn_mfma_i32_16x16x64_i8(F.a[mi], F.b[ni][0], z, 0, 0, 0);
-                    R1[mi] = __builtin_amdgcn_mfma_i32_16x16x64_i8(F.a[mi], F.b[ni][1], z, 0, 0, 0);
-                }
+            for (int mi = 0; mi < 2; mi++) {
+                R0[mi] = __builtin_amdgcn_mfma_i32_16x16x64_i8(F.a[mi], F.b[0], z, 0, 0, 0);
+                R1[mi] = __builtin_amdgcn_mfma_i32_16x16x64_i8(F.a[mi], F.b[1], z, 0, 0, 0);
             }
-#pragma unroll
-            for (int mi = 0; mi < 2; mi++)
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    float p = 0.f;                          // the +0 terms of a padded run
-                    if (REAL) {
-                        const int acc = (R1[mi][j] << 12) + R0[mi][j];
-                        p = (float)acc * (F.s4[mi][j] * F.xf[ni]);
-                    }
-                    tree_push<CH>(p, gl, L[mi][ni][j], run[mi][ni][j]);
-                    if (gl == CH - 1) y[mi][ni][j] = first ? run[mi][ni][j] : y[mi][ni][j] + run[mi][ni][j];
-                }
         }
+#pragma unroll
+        for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                float p = 0.f;                              // the +0 terms of a padded run
+                if (REAL) {
+                    const int acc = (R1[mi][j] << 12) + R0[mi][j];
+                    p = (float)acc * (F.s4[mi][j] * F.xf);
+                }
+                tree_push<CH>(p, gl, L[mi][j], run[mi][j]);
+                if (gl == CH - 1) y[mi][j] = first ? run[mi][j] : y[mi][j] + run[mi][j];
+            }
     };
-    // one chunk: its 4 groups at positions Q*4 .. Q*4+3 of the run (Q known at compile time);
-    // the next group's operands are read from LDS before this group's terms are summed
-    auto chunk = [&](auto QC, auto RC, auto TC, int c) {
+    // one chunk: its 4 groups at positions Q*4 .. Q*4+3 of the run (Q known at compile time)
+    auto chunk = [&](auto QC, auto RC, int c) {
         constexpr int Q = decltype(QC)::v;
         const uint8_t *base = mf_lds + (c & 1) * MF_BUF;
         const bool first = c < CH / MF_CG;                 // in the first run
-        Frag F[2];
-        if (decltype(RC)::v) fetch(F[0], base, 0);
+        // (one group's operands at a time: a second set for the next group measured slower,
+        // its registers spill at 128)
 #pragma unroll
         for (int g = 0; g < MF_CG; g++) {
-            if (decltype(RC)::v && g + 1 < MF_CG) fetch(F[(g + 1) & 1], base, g + 1);
-            group(F[g & 1], Q * MF_CG + g, first, RC, TC);
+            Frag F;
+            if (decltype(RC)::v) fetch(F, base, g);
+            group(F, Q * MF_CG + g, first, RC);
             __builtin_amdgcn_sched_barrier(0);
         }
     };
-    auto chunk_q = [&](auto RC, auto TC, int c) {
+    auto chunk_q = [&](auto RC, int c) {
         switch (c % (CH / MF_CG)) {
-            case 0: chunk(MfIc<0>{}, RC, TC, c); break;
-            case 1: if constexpr (CH / MF_CG > 1) chunk(MfIc<1 % (CH / MF_CG)>{}, RC, TC, c); break;
-            case 2: if constexpr (CH / MF_CG > 2) chunk(MfIc<2 % (CH / MF_CG)>{}, RC, TC, c); break;
-            default: if constexpr (CH / MF_CG > 3) chunk(MfIc<3 % (CH / MF_CG)>{}, RC, TC, c); break;
+            case 0: chunk(MfIc<0>{}, RC, c); break;
+            case 1: if constexpr (CH / MF_CG > 1) chunk(MfIc<1 % (CH / MF_CG)>{}, RC, c); break;
+            case 2: if constexpr (CH / MF_CG > 2) chunk(MfIc<2 % (CH / MF_CG)>{}, RC, c); break;
+            default: if constexpr (CH / MF_CG > 3) chunk(MfIc<3 % (CH / MF_CG)>{}, RC, c); break;
         }
     };
 
@@ -319,13 +322,8 @@ __global__ __launch_bounds__(MF_NT, 1) void k_mf(MfArgs A) {
     if (NC > 1) stage_load(1);
     for (int c = 0; c < NCV; c++) {
         if (wact) {
-            if (FULL || c < NC) {
-                if (two) chunk_q(MfIc<1>{}, MfIc<1>{}, c);
-                else chunk_q(MfIc<1>{}, MfIc<0>{}, c);
-            } else if constexpr (!FULL) {
-                if (two) chunk_q(MfIc<0>{}, MfIc<1>{}, c);
-                else chunk_q(MfIc<0>{}, MfIc<0>{}, c);
-            }
+            if (FULL || c < NC) chunk_q(MfIc<1>{}, c);
+            else if constexpr (!FULL) chunk_q(MfIc<0>{}, c);
         }
         if (c + 1 < NC) stage_store((c + 1) & 1);          // read by no wave since the last barrier
         __syncthreads();
@@ -338,11 +336,9 @@ __global__ __launch_bounds__(MF_NT, 1) void k_mf(MfArgs A) {
         const int I = A.I;
         if (wact) {
 #pragma unroll
-            for (int ni = 0; ni < 2; ni++)
-#pragma unroll
                 for (int j = 0; j < 4; j++) {
-                    const int i = 16 * mp + 4 * kq + j, t = 32 * np + 16 * ni + col;
-                    float yg = y[0][ni][j], yu = y[1][ni][j];
+                    const int i = 16 * mp + 4 * kq + j, t = 16 * tt + col;
+                    float yg = y[0][j], yu = y[1][j];
                     if (W.gs <= 0) {                        // per-row scales after the sum
                         if constexpr (PT) {
                             yg = yg * A.tab[e].gs[i0 + i];
@@ -366,22 +362,18 @@ __global__ __launch_bounds__(MF_NT, 1) void k_mf(MfArgs A) {
         }
     } else {
         if (wact) {
+            const int t = 16 * tt + col;
+            if (t < nt) {
+                float *yrow = A.Y + (int64_t)(beg + t0 + t) * O;
 #pragma unroll
-            for (int ni = 0; ni < 2; ni++) {
-                const int t = 32 * np + 16 * ni + col;
-                if (t < nt) {
-                    float *yrow = A.Y + (int64_t)(beg + t0 + t) * O;
+                for (int mi = 0; mi < 2; mi++) {
+                    const int row = r0 + 16 * (mp + 4 * mi) + 4 * kq;
+                    if (row < O) {
+                        sw_f32x4 o;
 #pragma unroll
-                    for (int mi = 0; mi < 2; mi++) {
-                        const int row = r0 + 16 * (mp + 4 * mi) + 4 * kq;
-                        if (row < O) {
-                            sw_f32x4 o;
-#pragma unroll
-                            for (int j = 0; j < 4; j++)
-                                o[j] = W.gs > 0 ? y[mi][ni][j]
-                                                : y[mi][ni][j] * (PT ? A.tab[e].ds[row + j] : W.s[(int64_t)e * O + row + j]);
-                            *(sw_f32x4 *)(yrow + row) = o;
-                        }
+                        for (int j = 0; j < 4; j++)
+                            o[j] = W.gs > 0 ? y[mi][j] : y[mi][j] * (PT ? A.tab[e].ds[row + j] : W.s[(int64_t)e * O + row + j]);
+                        *(sw_f32x4 *)(yrow + row) = o;
                     }
                 }
             }

@@ -118,7 +118,8 @@ struct ShSegWave {
 #pragma unroll
         for (int u = 0; u < SH_PF; u++)
 #pragma unroll
-            for (int t = 0; t < NRT; t++) ring[t][u] = ld(t, u);
+            for (int t = 0; t < NRT; t++)
+                if (u < GS) ring[t][u] = ld(t, u);          // uniform
     }
     __device__ __forceinline__ void run(const uint16_t *pl, sw_f32x4 *acc) {
         const int lane = threadIdx.x & 63, m = lane & 15, kq = lane >> 4;
@@ -137,7 +138,7 @@ struct ShSegWave {
 #pragma unroll
                     for (int t = 0; t < NRT; t++) {
                         acc[t] = sh_mfma3(ring[t][u], col0 ? b0 : z, col0 ? b1 : z, col0 ? b2 : z, acc[t]);
-                        ring[t][u] = ld(t, s + SH_PF);
+                        if (s + SH_PF < GS) ring[t][u] = ld(t, s + SH_PF);
                     }
                 }
             }
