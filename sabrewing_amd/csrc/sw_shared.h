@@ -126,23 +126,28 @@ struct ShSegWave {
 #pragma unroll
         for (int t = 0; t < NRT; t++) acc[t] = sw_f32x4{0.f, 0.f, 0.f, 0.f};
         const sw_u32x4 z = {0u, 0u, 0u, 0u};
-        for (int s0 = 0; s0 < GS; s0 += SH_PF) {
+        const bool col0 = m == 0;
+        auto use = [&](int s, int u) {
+            const uint16_t *pp = pl + (g0 + s) * 3 * SH_RG + 8 * kq;
+            const sw_u32x4 b0 = *(const sw_u32x4 *)pp, b1 = *(const sw_u32x4 *)(pp + SH_RG),
+                           b2 = *(const sw_u32x4 *)(pp + 2 * SH_RG);
+#pragma unroll
+            for (int t = 0; t < NRT; t++) acc[t] = sh_mfma3(ring[t][u], col0 ? b0 : z, col0 ? b1 : z, col0 ? b2 : z, acc[t]);
+        };
+        // full rounds with unconditional refills (clamped past the end), then the last
+        // round without: no branch join inside a round, so the waits stay per step
+        int s0 = 0;
+        for (; s0 + SH_PF < GS; s0 += SH_PF) {
 #pragma unroll
             for (int u = 0; u < SH_PF; u++) {
-                const int s = s0 + u;
-                if (s < GS) {                          // uniform
-                    const uint16_t *pp = pl + (g0 + s) * 3 * SH_RG + 8 * kq;
-                    const sw_u32x4 b0 = *(const sw_u32x4 *)pp, b1 = *(const sw_u32x4 *)(pp + SH_RG),
-                                   b2 = *(const sw_u32x4 *)(pp + 2 * SH_RG);
-                    const bool col0 = m == 0;
+                use(s0 + u, u);
 #pragma unroll
-                    for (int t = 0; t < NRT; t++) {
-                        acc[t] = sh_mfma3(ring[t][u], col0 ? b0 : z, col0 ? b1 : z, col0 ? b2 : z, acc[t]);
-                        if (s + SH_PF < GS) ring[t][u] = ld(t, s + SH_PF);
-                    }
-                }
+                for (int t = 0; t < NRT; t++) ring[t][u] = ld(t, s0 + u + SH_PF);
             }
         }
+#pragma unroll
+        for (int u = 0; u < SH_PF; u++)
+            if (s0 + u < GS) use(s0 + u, u);               // uniform
     }
 };
 
