@@ -7,6 +7,7 @@
 // launch loop, no host bounce of intermediate results), and the device-side
 // forward keeps routing, bucketing and the combine on the GPU.
 #include "sw_hip.h"
+#include "sw_shared.h"
 #include "../../include/sabrewing_hip.h"
 #include <stdio.h>
 #include <stdlib.h>
@@ -723,14 +724,17 @@ static int forward(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const floa
     // S > 1: as kernels of their own over token tiles (the same arithmetic per token)
     const bool sh_in = sh && S == 1;
     const bool mf = S > 1 && use_mfma(T, E, D, I);
+    // a decode-sized batch on the dot8 kernels: the shared expert's split-K blocks ride
+    // in the routing stage (gate_up) and the expert stage (down)
+    const bool sh_fused = sh && S > 1 && !mf && S <= SH_SK_MAX_S && !router_tiled(S, D, router_rows(d));
     if (router_tiled(S, D, router_rows(d))) {
         if (router_batch(w->router, d->router_bf16, x, S, D, router_rows(d), w->logit_bias, f.logits, f.scores,
                          d->route_act, mf ? nullptr : f.xl, f.xs)) return -1;
     } else {
         PROF("stage_route");
         if (sw_launch_stage_route(g_st, w->router, d->router_bf16, x, S, D, router_rows(d), w->logit_bias, f.logits, f.scores,
-                                  d->route_act, mf ? nullptr : f.xl, f.xs, sh_in ? sg : nullptr, su, Is, f.shh,
-                                  sh && !sh_in ? f.shx : nullptr))
+                                  d->route_act, mf ? nullptr : f.xl, f.xs, sh_in || sh_fused ? sg : nullptr, su, Is, f.shh,
+                                  sh && !sh_in && !sh_fused ? f.shx : nullptr, sh_fused ? f.shp : nullptr))
             return fail_msg("routing stage launch");
     }
     if (gated && gated_shared(d, w, x, S, f)) return -1;
@@ -738,7 +742,7 @@ static int forward(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const floa
         PROF("digits");
         if (sw_launch_digits(g_st, x, S, D, f.xd, f.xds)) return fail_msg("digits launch");
     }
-    if (sh && !sh_in && shared_glu_batch(w, x, S, D, Is, f, !router_tiled(S, D, router_rows(d)))) return -1;
+    if (sh && !sh_in && !sh_fused && shared_glu_batch(w, x, S, D, Is, f, !router_tiled(S, D, router_rows(d)))) return -1;
     if (!in_experts && gate_dev(d, w, S, f)) return -1;
     if (S == 1) {                        // one token: its K picks in rank order, fused down + combine
         { PROF("stage_experts");
@@ -779,9 +783,10 @@ static int forward(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const floa
         SwGroups g = {f.gexp, f.gbeg, f.gcnt, f.grow, f.G, sw_npass_max(T, E, SW_DG_TT), 0, f.items, f.P};
         { PROF("stage_experts");
           if (sw_launch_stage_experts(g_st, gu, f.xl, f.xs, g, I, f.hl, f.hs, nullptr, K, nullptr, E, d->route_act,
-                                      w->corr_bias, d->use_corr_bias, d->norm_topk, f.w, nullptr, f.shh, S, Is, D, f.sout))
+                                      w->corr_bias, d->use_corr_bias, d->norm_topk, f.w, sh_fused ? sd : nullptr, f.shh, S,
+                                      Is, D, f.sout, sh_fused ? f.shp : nullptr))
               return fail_msg("expert stage launch"); }
-        if (sh) {
+        if (sh && !sh_fused) {
             PROF("shared_down");
             if (sw_launch_sh_down(g_st, sd, f.shp, S, Is, D, f.sout)) return fail_msg("shared down launch");
         }

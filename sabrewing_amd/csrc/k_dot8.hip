@@ -686,48 +686,62 @@ static size_t lds_max(size_t a, size_t b) { return a > b ? a : b; }
 struct ShGluArgs { const uint16_t *Wg, *Wu; const float *x; int D, Is; float *h; };
 struct ShDownArgs { const uint16_t *Wd; const float *h; int Is, D; float *out; };
 
-template <int BF16, int ONE>
-__global__ __launch_bounds__(SH_NT) void k_stage_route(RouterArgs R, int nbr, int S, ShGluArgs G) {
+// SK: the extra blocks are a batch's shared gate_up over column tiles of SK x 16 tokens
+// (sh_sk_block, inputs split from x), else the single token's (sh_glu_block)
+template <int BF16, int ONE, int SK>
+__global__ __launch_bounds__(SH_NT) void k_stage_route(RouterArgs R, int nbr, int S, ShGluArgs G, ShSkArgs Sk) {
     extern __shared__ __align__(16) float smem[];
     const int b = blockIdx.x;
-    if (b < nbr * S) router_block<BF16, ONE>(R, b % nbr, b / nbr, nbr, smem);
-    else sh_glu_block(G.Wg, G.Wu, G.x, G.D, G.Is, G.h, b - nbr * S, smem);
+    if (b < nbr * S) {
+        router_block<BF16, ONE>(R, b % nbr, b / nbr, nbr, smem);
+    } else if constexpr (SK > 0) {
+        const int w = b - nbr * S, nrb = sh_sk_rows(1, Sk.O);
+        sh_sk_block<1, SK, 1>(Sk, w % nrb, w / nrb, smem);
+    } else {
+        sh_glu_block(G.Wg, G.Wu, G.x, G.D, G.Is, G.h, b - nbr * S, smem);
+    }
 }
 
-// TTG: tokens per pass of the routed gate_up
-template <int PF, int PICK, int NP, int TTG, int C16, int RO>
-__global__ __launch_bounds__(DG_NT, PICK ? 1 : 4) void k_stage_experts(Dot8GluArgs A, int nbx, int nglu, ShDownArgs Sd) {
+// TTG: tokens per pass of the routed gate_up.  The extra blocks: the single token's
+// shared down (sh_down_block), or with SKD a batch's (sh_sk_block over the parts of h)
+template <int PF, int PICK, int NP, int TTG, int C16, int RO, int SKD>
+__global__ __launch_bounds__(DG_NT, PICK ? 1 : 4) void k_stage_experts(Dot8GluArgs A, int nbx, int nglu, ShDownArgs Sd,
+                                                                    ShSkArgs Skd) {
     extern __shared__ __align__(16) float smem[];
     const int b = blockIdx.x;
     if (b < nglu) {
         const int w = PICK == 0 && A.grp.items ? sw_xcd_work(b, nglu) : b;
         dot8_glu_block<PF, PICK, NP, TTG, C16, RO>(A, w % nbx, w / nbx, smem);
+    } else if constexpr (SKD) {
+        const int w = b - nglu, nrb = sh_sk_rows(0, Skd.O);
+        sh_sk_block<0, 2, 0>(Skd, w % nrb, w / nrb, smem);
     } else {
         sh_down_block(Sd.Wd, Sd.h, Sd.Is, Sd.D, Sd.out, b - nglu, smem);
     }
 }
-template <int PICK, int NP, int TTG, int RO = 32>
+template <int PICK, int NP, int TTG, int RO = 32, int SKD = 0>
 struct StageL {
     template <int PF, int C16>
     struct L {
-        static void go(dim3 grid, size_t lds, hipStream_t st, const Dot8GluArgs &A, int nbx, int nglu, const ShDownArgs &Sd) {
-            SW_LAUNCH((k_stage_experts<PF, PICK, NP, TTG, C16, RO>), grid, dim3(DG_NT), lds, st, A, nbx, nglu, Sd);
+        static void go(dim3 grid, size_t lds, hipStream_t st, const Dot8GluArgs &A, int nbx, int nglu, const ShDownArgs &Sd,
+                       const ShSkArgs &Skd) {
+            SW_LAUNCH((k_stage_experts<PF, PICK, NP, TTG, C16, RO, SKD>), grid, dim3(DG_NT), lds, st, A, nbx, nglu, Sd, Skd);
         }
     };
 };
 
-template <int ONE>
+template <int ONE, int SK>
 static void launch_stage_route(int bf16, dim3 grid, size_t lds, hipStream_t st, const RouterArgs &R, int nbr, int S,
-                               const ShGluArgs &G) {
-    if (bf16) SW_LAUNCH((k_stage_route<1, ONE>), grid, dim3(SH_NT), lds, st, R, nbr, S, G);
-    else SW_LAUNCH((k_stage_route<0, ONE>), grid, dim3(SH_NT), lds, st, R, nbr, S, G);
+                               const ShGluArgs &G, const ShSkArgs &Sk) {
+    if (bf16) SW_LAUNCH((k_stage_route<1, ONE, SK>), grid, dim3(SH_NT), lds, st, R, nbr, S, G, Sk);
+    else SW_LAUNCH((k_stage_route<0, ONE, SK>), grid, dim3(SH_NT), lds, st, R, nbr, S, G, Sk);
 }
 
 // stage 1: router logits / scores and the limbs of x, and the shared
 // expert's gate_up when sg is non-null
 int sw_launch_stage_route(hipStream_t st, const void *Wc, int w_bf16, const float *x, int S, int D, int E,
                           const float *logit_bias, float *logits, float *scores, int route_act, sw_u32x4 *xl, float *xs,
-                          const uint16_t *sg, const uint16_t *su, int Is, float *sh_h, uint16_t *xp) {
+                          const uint16_t *sg, const uint16_t *su, int Is, float *sh_h, uint16_t *xp, uint16_t *sh_hp) {
     if (D % 128 || E <= 0 || S <= 0 || route_act < 0 || route_act > SW_ROUTE_ACT_MAX || (!sw_act_softmax(route_act) && !scores)) return -1;
     if (xp && !sh_shape_ok(D)) return -1;
     const int one = router_one(S, E);
@@ -736,14 +750,27 @@ int sw_launch_stage_route(hipStream_t st, const void *Wc, int w_bf16, const floa
     const int nbr = (E + router_epb(one, SH_NT) - 1) / router_epb(one, SH_NT);
     const RouterArgs R = {Wc, x, D, E, logit_bias, logits, route_act, scores, xl, xs, xp};
     const ShGluArgs G = {sg, su, x, D, Is, sh_h};
-    // the shared expert's blocks are single-token jobs
-    if (sg && (S != 1 || !su || !sh_h || Is % SH_GLU_O || !sh_shape_ok(D))) return -1;
-    const int nsh = sg ? sh_glu_blocks(Is) : 0;
+    // the shared expert's gate_up: one token's blocks (h to sh_h), or with sh_hp a batch's
+    // split-K blocks (h's parts to sh_hp)
+    if (sg && (!su || Is % 64 || !sh_shape_ok(D))) return -1;
+    if (sg && !(S == 1 ? sh_h && !sh_hp : sh_hp && S <= SH_SK_MAX_S)) return -1;
+    const int nc = sh_sk_nc(1, S);
+    const ShSkArgs Sk = {sg, su, nullptr, x, S, D, Is, sh_hp};
+    const int nsh = !sg ? 0 : S == 1 ? sh_glu_blocks(Is) : sh_sk_rows(1, Is) * sh_sk_cols(S, nc);
     const dim3 grid((unsigned)(nbr * S + nsh));
-    const size_t lds = lds_max(rl, sg ? sh_glu_lds(D) : 0);
+    const size_t lds = lds_max(rl, !sg ? 0 : S == 1 ? sh_glu_lds(D) : sh_sk_lds(nc));
     if (lds > 65536) return -1;
-    if (one) launch_stage_route<1>(w_bf16, grid, lds, st, R, nbr, S, G);
-    else launch_stage_route<0>(w_bf16, grid, lds, st, R, nbr, S, G);
+    const int sk = sg && S > 1 ? nc : 0;
+    if (one) {
+        if (sk) launch_stage_route<1, 1>(w_bf16, grid, lds, st, R, nbr, S, G, Sk);   // (ONE: S <= 4, so nc = 1)
+        else launch_stage_route<1, 0>(w_bf16, grid, lds, st, R, nbr, S, G, Sk);
+    } else if (sk == 1) {
+        launch_stage_route<0, 1>(w_bf16, grid, lds, st, R, nbr, S, G, Sk);
+    } else if (sk == 2) {
+        launch_stage_route<0, 2>(w_bf16, grid, lds, st, R, nbr, S, G, Sk);
+    } else {
+        launch_stage_route<0, 0>(w_bf16, grid, lds, st, R, nbr, S, G, Sk);
+    }
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
@@ -754,24 +781,28 @@ int sw_launch_stage_route(hipStream_t st, const void *Wc, int w_bf16, const floa
 int sw_launch_stage_experts(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, const float *xs, SwGroups g, int I, sw_u32x4 *hl,
                             float *hs, int *sel, int K, const float *route_src, int E, int act, const float *bias,
                             int use_bias, int norm, float *w, const uint16_t *sd, const float *sh_h, int S, int Is, int D,
-                            float *sh_out) {
+                            float *sh_out, const uint16_t *sh_hp) {
     int gsh;
     if (dot8_glu_check(W, I, gsh)) return -1;
     const bool picks = sel != nullptr;
     if (picks && (S != 1 || K <= 0 || K > 64)) return -1;
     if (picks && route_src && (E <= 0 || E > 256 || K > E || !w || !(act == 1 || sw_act_scores(act)))) return -1;
     if (!picks && g.ngroups_max <= 0) return -1;
-    // the shared expert's down blocks are single-token jobs
-    if (sd && (S != 1 || !sh_h || !sh_out || D % SH_DN_O || !sh_shape_ok(Is))) return -1;
+    // the shared expert's down: one token's blocks (from h in sh_h), or with sh_hp a
+    // batch's split-K blocks (from h's parts); out to sh_out
+    if (sd && (!sh_out || D % SH_DN_O || !sh_shape_ok(Is))) return -1;
+    if (sd && !(S == 1 ? sh_h && !sh_hp : sh_hp && !picks && S <= SH_SK_MAX_S)) return -1;
+    const bool skd = sd && S > 1;
     const int nbx = picks ? K : g.ngroups_max;
     const int RO = picks ? 32 : dg_ro(I);             // outputs per gate_up block
     const int nglu = nbx * (I / RO);
-    const int nsh = sd ? sh_down_blocks(D) : 0;
+    const int nsh = !sd ? 0 : skd ? sh_sk_rows(0, D) * sh_sk_cols(S, 2) : sh_down_blocks(D);
     const DotRoute rt = route_src ? DotRoute{route_src, bias, E, K, act, use_bias, norm, w} : DotRoute{};
     const Dot8GluArgs A = {W, gsh, xl, xs, g, I, hl, hs, sel, rt};
     const ShDownArgs Sd = {sd, sh_h, Is, D, sh_out};
+    const ShSkArgs Skd = {sd, nullptr, sh_hp, nullptr, S, Is, D, sh_out};
     const dim3 grid((unsigned)(nglu + nsh));
-    const size_t shl = sd ? sh_down_lds(Is) : 0;
+    const size_t shl = !sd ? 0 : skd ? sh_sk_lds(2) : sh_down_lds(Is);
     if (shl > 65536) return -1;
     const int pf0 = dg_pf_glu(W.K), c16 = dot8_c16(W.K);
     // groups: a 4-step ring, two blocks per CU (four waves per SIMD, 128 VGPRs); an
@@ -779,15 +810,21 @@ int sw_launch_stage_experts(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, const fl
     const int pf = picks ? pf0 : (pf0 < 4 ? pf0 : 4);
     if (!picks) {
         const size_t lds = lds_max(dot8_glu_lds(W.K, DG_TT, RO), shl);
-        if (RO == 128) dispatch_pf_c16<StageL<0, 0, DG_TT, 128>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd);
-        else if (RO == 64) dispatch_pf_c16<StageL<0, 0, DG_TT, 64>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd);
-        else dispatch_pf_c16<StageL<0, 0, DG_TT>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd);
+        if (skd) {
+            if (RO == 128) dispatch_pf_c16<StageL<0, 0, DG_TT, 128, 1>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd, Skd);
+            else if (RO == 64) dispatch_pf_c16<StageL<0, 0, DG_TT, 64, 1>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd, Skd);
+            else dispatch_pf_c16<StageL<0, 0, DG_TT, 32, 1>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd, Skd);
+        } else {
+            if (RO == 128) dispatch_pf_c16<StageL<0, 0, DG_TT, 128>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd, Skd);
+            else if (RO == 64) dispatch_pf_c16<StageL<0, 0, DG_TT, 64>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd, Skd);
+            else dispatch_pf_c16<StageL<0, 0, DG_TT>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd, Skd);
+        }
     } else {
         const size_t lds = lds_max(dot8_glu_lds(W.K, 1), shl);
-        if (!route_src) dispatch_pf_c16<StageL<1, 0, 1>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd);
-        else if (E <= 64) dispatch_pf_c16<StageL<1, 1, 1>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd);
-        else if (E <= 128) dispatch_pf_c16<StageL<1, 2, 1>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd);
-        else dispatch_pf_c16<StageL<1, 4, 1>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd);
+        if (!route_src) dispatch_pf_c16<StageL<1, 0, 1>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd, Skd);
+        else if (E <= 64) dispatch_pf_c16<StageL<1, 1, 1>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd, Skd);
+        else if (E <= 128) dispatch_pf_c16<StageL<1, 2, 1>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd, Skd);
+        else dispatch_pf_c16<StageL<1, 4, 1>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd, Skd);
     }
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }

@@ -167,109 +167,22 @@ __global__ __launch_bounds__(256) void k_sh_down_mf(const uint16_t *__restrict__
         }
 }
 
-// ---- decode-sized batches: K split over the waves ----
-// Block (16-row tile, NC column tiles of 16 tokens): wave w runs segment w of the K
-// inputs (the MFMA chain of that segment, as ShSegWave), the segment results go
-// to LDS and are folded left to right there, so a token gets the bits of the
-// single-token jobs while 8 waves stream one tile's weights.  Gate_up tiles: rows
-// 0-7 the gate rows of outputs 8 bx .. +7, rows 8-15 the up rows.
-#define SHK_NT 512
+// ---- decode-sized batches: K split over the waves (sh_sk_block, sw_shared.h) ----
 template <int GLU, int NC>
-__global__ __launch_bounds__(SHK_NT) void k_sh_sk(const uint16_t *__restrict__ W0, const uint16_t *__restrict__ W1,
-                                                 const uint16_t *__restrict__ xp, int S, int K, int O,
-                                                 void *__restrict__ outp) {
+__global__ __launch_bounds__(SH_SK_NT) void k_sh_sk(ShSkArgs A) {
     __shared__ float red[8 * 16 * 16 * NC];                // [segment][row][token]
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, m = lane & 15, kq = lane >> 4;
-    const int G = K / SH_RG, nseg = sh_nseg(G), GS = G / nseg;
-    const int r0 = blockIdx.x * (GLU ? 8 : 16), tok0 = blockIdx.y * 16 * NC;
-    if (wave < nseg) {
-        const uint16_t *wr = GLU ? (m < 8 ? W0 + (int64_t)(r0 + m) * K : W1 + (int64_t)(r0 + m - 8) * K)
-                                 : W0 + (int64_t)(r0 + m) * K;
-        wr += 8 * kq;
-        const uint16_t *br[NC];
-#pragma unroll
-        for (int c = 0; c < NC; c++) br[c] = xp + (int64_t)min(tok0 + 16 * c + m, S - 1) * K * 3 + 8 * kq;
-        const int g0 = wave * GS;
-        struct Step { sw_u32x4 a, b[NC][3]; };
-        auto load = [&](int s, Step &st) {
-            const int g = g0 + min(s, GS - 1);
-            st.a = *(const sw_u32x4 *)(wr + (int64_t)g * SH_RG);
-#pragma unroll
-            for (int c = 0; c < NC; c++)
-#pragma unroll
-                for (int p = 0; p < 3; p++) st.b[c][p] = *(const sw_u32x4 *)(br[c] + (g * 3 + p) * SH_RG);
-        };
-        sw_f32x4 acc[NC];
-#pragma unroll
-        for (int c = 0; c < NC; c++) acc[c] = sw_f32x4{0.f, 0.f, 0.f, 0.f};
-        // steps in flight (weight and part words): 8 and 4 measured best at B = 8, 32, 64
-        // (6 / 3 before: 21.2 / 12.7 us for B = 32's gate_up / down, now 16.6 / 8.4 us)
-        constexpr int SHK_PF = NC == 1 ? 8 : 4;
-        Step ring[SHK_PF];
-#pragma unroll
-        for (int u = 0; u < SHK_PF; u++) load(u, ring[u]);
-        auto use = [&](const Step &st) {
-#pragma unroll
-            for (int c = 0; c < NC; c++) acc[c] = sh_mfma3(st.a, st.b[c][0], st.b[c][1], st.b[c][2], acc[c]);
-        };
-        // full rounds with unconditional refills (past the end they re-read the last step),
-        // then the last round without: no branch join inside a round, so the waits stay
-        // per step instead of draining the ring at every round
-        int s0 = 0;
-        for (; s0 + SHK_PF < GS; s0 += SHK_PF) {
-#pragma unroll
-            for (int u = 0; u < SHK_PF; u++) {
-                use(ring[u]);
-                load(s0 + u + SHK_PF, ring[u]);
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < SHK_PF; u++)
-            if (s0 + u < GS) use(ring[u]);
-#pragma unroll
-        for (int c = 0; c < NC; c++)
-#pragma unroll
-            for (int r = 0; r < 4; r++) red[(wave * 16 + 4 * kq + r) * 16 * NC + 16 * c + m] = acc[c][r];
-    }
-    __syncthreads();
-    const int tid = threadIdx.x;
-    if (GLU) {
-        for (int it = tid; it < 8 * 16 * NC; it += SHK_NT) {
-            const int r = it / (16 * NC), t = it - r * 16 * NC, tok = tok0 + t;
-            float yg = -0.0f, yu = -0.0f;
-            for (int sg = 0; sg < nseg; sg++) {
-                yg = yg + red[(sg * 16 + r) * 16 * NC + t];
-                yu = yu + red[(sg * 16 + 8 + r) * 16 * NC + t];
-            }
-            if (tok < S) {
-                const int i = r0 + r;
-                uint32_t pa, pb, pc;
-                sh_split3((yg / (1.0f + expf(-yg))) * yu, pa, pb, pc);
-                uint16_t *dst = (uint16_t *)outp + (int64_t)tok * O * 3 + (i >> 5) * 3 * SH_RG + (i & 31);
-                dst[0] = (uint16_t)pa;
-                dst[SH_RG] = (uint16_t)pb;
-                dst[2 * SH_RG] = (uint16_t)pc;
-            }
-        }
-    } else {
-        for (int it = tid; it < 16 * 16 * NC; it += SHK_NT) {
-            const int r = it / (16 * NC), t = it - r * 16 * NC, tok = tok0 + t;
-            float y = -0.0f;
-            for (int sg = 0; sg < nseg; sg++) y = y + red[(sg * 16 + r) * 16 * NC + t];
-            if (tok < S) ((float *)outp)[(int64_t)tok * O + r0 + r] = y;
-        }
-    }
+    sh_sk_block<GLU, NC, 0>(A, blockIdx.x, blockIdx.y, red);
 }
 // decode-sized batches take the split-K blocks: the gate_up 16-token column tiles up to
 // 32 tokens (the grid then fills the chip), else 32-token tiles
-#define SHK_MAX_S 128
 template <int GLU>
 static int launch_sk(hipStream_t st, const uint16_t *W0, const uint16_t *W1, const uint16_t *xp, int S, int K, int O,
-                     int nrow, void *out) {
-    const int nc = GLU && S <= 32 ? 1 : 2;      // (the down's segments are short: 32-token tiles)
-    const dim3 grid((unsigned)nrow, (unsigned)((S + 16 * nc - 1) / (16 * nc)));
-    if (nc == 1) SW_LAUNCH((k_sh_sk<GLU, 1>), grid, dim3(SHK_NT), 0, st, W0, W1, xp, S, K, O, out);
-    else SW_LAUNCH((k_sh_sk<GLU, 2>), grid, dim3(SHK_NT), 0, st, W0, W1, xp, S, K, O, out);
+                     void *out) {
+    const int nc = sh_sk_nc(GLU, S);
+    const dim3 grid((unsigned)sh_sk_rows(GLU, O), (unsigned)sh_sk_cols(S, nc));
+    const ShSkArgs A = {W0, W1, xp, nullptr, S, K, O, out};
+    if (nc == 1) SW_LAUNCH((k_sh_sk<GLU, 1>), grid, dim3(SH_SK_NT), 0, st, A);
+    else SW_LAUNCH((k_sh_sk<GLU, 2>), grid, dim3(SH_SK_NT), 0, st, A);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
@@ -283,7 +196,7 @@ int sw_launch_sh_parts(hipStream_t st, const float *x, int S, int K, uint16_t *p
 int sw_launch_sh_glu(hipStream_t st, const uint16_t *Wg, const uint16_t *Wu, const uint16_t *xp, int S, int D, int Is,
                      uint16_t *hp) {
     if (S <= 0 || Is % 64 || !sh_shape_ok(D)) return -1;
-    if (S <= SHK_MAX_S) return launch_sk<1>(st, Wg, Wu, xp, S, D, Is, Is / 8, hp);
+    if (S <= SH_SK_MAX_S) return launch_sk<1>(st, Wg, Wu, xp, S, D, Is, hp);
     const dim3 grid((unsigned)(Is / 64 * ((S + SHB_TOK - 1) / SHB_TOK)));
     SW_LAUNCH(k_sh_glu_mf, grid, dim3(256), 0, st, Wg, Wu, xp, S, D, Is, hp);
     return hipGetLastError() == hipSuccess ? 0 : -1;
@@ -291,7 +204,7 @@ int sw_launch_sh_glu(hipStream_t st, const uint16_t *Wg, const uint16_t *Wu, con
 
 int sw_launch_sh_down(hipStream_t st, const uint16_t *Wd, const uint16_t *hp, int S, int Is, int D, float *out) {
     if (S <= 0 || D % 128 || !sh_shape_ok(Is)) return -1;
-    if (S <= SHK_MAX_S) return launch_sk<0>(st, Wd, nullptr, hp, S, Is, D, D / 16, out);
+    if (S <= SH_SK_MAX_S) return launch_sk<0>(st, Wd, nullptr, hp, S, Is, D, out);
     const dim3 grid((unsigned)(D / 128 * ((S + SHB_TOK - 1) / SHB_TOK)));
     SW_LAUNCH(k_sh_down_mf, grid, dim3(256), 0, st, Wd, hp, S, Is, D, out);
     return hipGetLastError() == hipSuccess ? 0 : -1;

@@ -240,18 +240,20 @@ int sw_launch_combine(hipStream_t st, const float *slots, const int *rowof, cons
                       float route_scale, const float *shared, float *out, int accumulate,
                       const float *wsh = nullptr, int ns = 0);
 // fused decode stages (k_dot8.hip): stage 1 = router logits/scores/limbs
-// and the shared expert's gate_up (sg null: none; one token), with xp
-// non-null also the bf16 parts of x (a batch's shared expert, sw_shared.h);
-// stage 2 = routed gate_up (sel non-null: one token's K picks, from sel or,
-// with route_src, by a gate + top-k in every block; else the groups g) + the
-// shared expert's down (sd null: none; one token)
+// and the shared expert's gate_up (sg null: none; one token's h to sh_h, or a
+// batch's split-K blocks writing h's parts to sh_hp), with xp non-null also the
+// bf16 parts of x (sw_shared.h); stage 2 = routed gate_up (sel non-null: one
+// token's K picks, from sel or, with route_src, by a gate + top-k in every
+// block; else the groups g) + the shared expert's down (sd null: none; from
+// one token's h in sh_h, or a batch's from h's parts in sh_hp)
 int sw_launch_stage_route(hipStream_t st, const void *Wc, int w_bf16, const float *x, int S, int D, int E,
                           const float *logit_bias, float *logits, float *scores, int route_act, sw_u32x4 *xl, float *xs,
-                          const uint16_t *sg, const uint16_t *su, int Is, float *sh_h, uint16_t *xp = nullptr);
+                          const uint16_t *sg, const uint16_t *su, int Is, float *sh_h, uint16_t *xp = nullptr,
+                          uint16_t *sh_hp = nullptr);
 int sw_launch_stage_experts(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, const float *xs, SwGroups g, int I, sw_u32x4 *hl,
                             float *hs, int *sel, int K, const float *route_src, int E, int act, const float *bias,
                             int use_bias, int norm, float *w, const uint16_t *sd, const float *sh_h, int S, int Is, int D,
-                            float *sh_out);
+                            float *sh_out, const uint16_t *sh_hp = nullptr);
 // the shared expert on the VALU (sw_shared.h): h[S, Is] = silu(Wg x) * (Wu x)
 // and out[S, D] = Wd h, bf16 weights, f32 activations
 // stack glue (k_glue.hip): RMSNorm rows, greedy argmax rows

@@ -217,4 +217,135 @@ __device__ __forceinline__ void sh_down_block(const uint16_t *__restrict__ Wd, c
     if (tid < SH_DN_O) out[d0 + tid] = sh_fold(red, tid, nseg);
 }
 
+// ---- decode-sized batches: K split over the waves ----
+// Block (bx, by) = (16-row tile, NC column tiles of 16 tokens), 8 waves: wave w runs
+// segment w of the K inputs (the MFMA chain of that segment, as ShSegWave), the
+// segment results go to LDS (red: [8][16][16 NC] floats) and are folded left to right
+// there, so a token gets the bits of the single-token jobs while 8 waves stream one
+// tile's weights.  Gate_up tiles: rows 0-7 the gate rows of outputs 8 bx .. +7,
+// rows 8-15 the up rows.  The inputs come as parts (xp) or, FX, as f32 rows (xf)
+// split into their parts at each step.  Run by k_sh_sk (k_shared.hip) and as extra
+// blocks of the decode stage launches (k_dot8.hip).
+struct ShSkArgs {
+    const uint16_t *W0, *W1;   // gate and up rows (GLU), or the down rows
+    const uint16_t *xp;        // the inputs' parts [S][K/32][3][32]
+    const float *xf;           // FX: the inputs [S][K] f32
+    int S, K, O;
+    void *out;                 // GLU: h's parts [S][O/32][3][32]; else [S][O] f32
+};
+#define SH_SK_NT 512
+#define SH_SK_MAX_S 128        // batches up to this many tokens take these blocks
+// column tiles of 16 tokens per block: gate_up 1 up to 32 tokens (the grid then fills
+// the chip), else 2; the down's segments are short: always 2
+__host__ __device__ inline int sh_sk_nc(int GLU, int S) { return GLU && S <= 32 ? 1 : 2; }
+__host__ __device__ inline int sh_sk_rows(int GLU, int O) { return GLU ? O / 8 : O / 16; }
+__host__ __device__ inline int sh_sk_cols(int S, int nc) { return (S + 16 * nc - 1) / (16 * nc); }
+__host__ __device__ inline size_t sh_sk_lds(int nc) { return (size_t)8 * 16 * 16 * nc * 4; }
+template <int GLU, int NC, int FX>
+__device__ __forceinline__ void sh_sk_block(const ShSkArgs &A, int bx, int by, float *red) {
+    const uint16_t *__restrict__ W0 = A.W0, *__restrict__ W1 = A.W1, *__restrict__ xp = A.xp;
+    const int S = A.S, K = A.K, O = A.O;
+    void *__restrict__ outp = A.out;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, m = lane & 15, kq = lane >> 4;
+    const int G = K / SH_RG, nseg = sh_nseg(G), GS = G / nseg;
+    const int r0 = bx * (GLU ? 8 : 16), tok0 = by * 16 * NC;
+    if (wave < nseg) {
+        const uint16_t *wr = GLU ? (m < 8 ? W0 + (int64_t)(r0 + m) * K : W1 + (int64_t)(r0 + m - 8) * K)
+                                 : W0 + (int64_t)(r0 + m) * K;
+        wr += 8 * kq;
+        const uint16_t *br[NC];
+        const float *bf[NC];
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            const int64_t tok = min(tok0 + 16 * c + m, S - 1);
+            if (FX) bf[c] = A.xf + tok * K + 8 * kq;
+            else br[c] = xp + tok * K * 3 + 8 * kq;
+        }
+        const int g0 = wave * GS;
+        // a step's words: the weights and, per column tile, the 3 part words (or the 8 f32
+        // inputs they are split from)
+        struct Step { sw_u32x4 a, b[NC][FX ? 2 : 3]; };
+        auto load = [&](int s, Step &st) {
+            const int g = g0 + min(s, GS - 1);
+            st.a = *(const sw_u32x4 *)(wr + (int64_t)g * SH_RG);
+#pragma unroll
+            for (int c = 0; c < NC; c++) {
+                if (FX) {
+                    st.b[c][0] = *(const sw_u32x4 *)(bf[c] + g * SH_RG);
+                    st.b[c][1] = *(const sw_u32x4 *)(bf[c] + g * SH_RG + 4);
+                } else {
+#pragma unroll
+                    for (int p = 0; p < 3; p++) st.b[c][p] = *(const sw_u32x4 *)(br[c] + (g * 3 + p) * SH_RG);
+                }
+            }
+        };
+        sw_f32x4 acc[NC];
+#pragma unroll
+        for (int c = 0; c < NC; c++) acc[c] = sw_f32x4{0.f, 0.f, 0.f, 0.f};
+        // steps in flight (weight and part words): 8 and 4 measured best at B = 8, 32 and 64
+        constexpr int SHK_PF = NC == 1 ? 8 : 4;
+        Step ring[SHK_PF];
+#pragma unroll
+        for (int u = 0; u < SHK_PF; u++) load(u, ring[u]);
+        auto use = [&](const Step &st) {
+#pragma unroll
+            for (int c = 0; c < NC; c++) {
+                if (FX) {
+                    sw_u32x4 p0, p1, p2;
+                    sh_split8(__builtin_bit_cast(sw_f32x4, st.b[c][0]), __builtin_bit_cast(sw_f32x4, st.b[c][1]), p0, p1, p2);
+                    acc[c] = sh_mfma3(st.a, p0, p1, p2, acc[c]);
+                } else {
+                    acc[c] = sh_mfma3(st.a, st.b[c][0], st.b[c][1], st.b[c][2], acc[c]);
+                }
+            }
+        };
+        // full rounds with unconditional refills (past the end they re-read the last step),
+        // then the last round without: no branch join inside a round, so the waits stay
+        // per step instead of draining the ring at every round
+        int s0 = 0;
+        for (; s0 + SHK_PF < GS; s0 += SHK_PF) {
+#pragma unroll
+            for (int u = 0; u < SHK_PF; u++) {
+                use(ring[u]);
+                load(s0 + u + SHK_PF, ring[u]);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < SHK_PF; u++)
+            if (s0 + u < GS) use(ring[u]);
+#pragma unroll
+        for (int c = 0; c < NC; c++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) red[(wave * 16 + 4 * kq + r) * 16 * NC + 16 * c + m] = acc[c][r];
+    }
+    __syncthreads();
+    const int tid = threadIdx.x;
+    if (GLU) {
+        for (int it = tid; it < 8 * 16 * NC; it += SH_SK_NT) {
+            const int r = it / (16 * NC), t = it - r * 16 * NC, tok = tok0 + t;
+            float yg = -0.0f, yu = -0.0f;
+            for (int sg = 0; sg < nseg; sg++) {
+                yg = yg + red[(sg * 16 + r) * 16 * NC + t];
+                yu = yu + red[(sg * 16 + 8 + r) * 16 * NC + t];
+            }
+            if (tok < S) {
+                const int i = r0 + r;
+                uint32_t pa, pb, pc;
+                sh_split3((yg / (1.0f + expf(-yg))) * yu, pa, pb, pc);
+                uint16_t *dst = (uint16_t *)outp + (int64_t)tok * O * 3 + (i >> 5) * 3 * SH_RG + (i & 31);
+                dst[0] = (uint16_t)pa;
+                dst[SH_RG] = (uint16_t)pb;
+                dst[2 * SH_RG] = (uint16_t)pc;
+            }
+        }
+    } else {
+        for (int it = tid; it < 16 * 16 * NC; it += SH_SK_NT) {
+            const int r = it / (16 * NC), t = it - r * 16 * NC, tok = tok0 + t;
+            float y = -0.0f;
+            for (int sg = 0; sg < nseg; sg++) y = y + red[(sg * 16 + r) * 16 * NC + t];
+            if (tok < S) ((float *)outp)[(int64_t)tok * O + r0 + r] = y;
+        }
+    }
+}
+
 #endif
