@@ -564,7 +564,10 @@ static int carve_fwd(const LagHipMoeDesc *d, int S, FwdScratch &f, const Scratch
 // (each weight slice read once per tile, the same bits as the per-token blocks), then
 // the limbs of x as a kernel of their own; smaller batches keep the fused routing stage
 // (B = 32: 11 us against 22 + 4 us tiled, the tiles' x chunks waiting on one wave per CU)
-static bool router_tiled(int S, int D, int R) { return S >= 2 && D % 256 == 0 && (S >= 512 || R >= 4096); }
+#ifndef SW_RT_MIN_S
+#define SW_RT_MIN_S 512
+#endif
+static bool router_tiled(int S, int D, int R) { return S >= 2 && D % 256 == 0 && (S >= SW_RT_MIN_S || R >= 4096); }
 static int router_batch(const void *Wc, int w_bf16, const float *x, int S, int D, int R, const float *lbias,
                         float *logits, float *scores, int act, sw_u32x4 *xl, float *xs) {
     { PROF("router_tiles");
@@ -724,17 +727,21 @@ static int forward(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const floa
     // S > 1: as kernels of their own over token tiles (the same arithmetic per token)
     const bool sh_in = sh && S == 1;
     const bool mf = S > 1 && use_mfma(T, E, D, I);
-    // a decode-sized batch on the dot8 kernels: the shared expert's split-K blocks ride
-    // in the routing stage (gate_up) and the expert stage (down)
+    // a decode-sized batch on the dot8 kernels: the shared expert's split-K blocks ride in
+    // other launches -- up to 32 tokens in the expert stage (gate_up) and the combine
+    // (down); beyond, in the routing stage (gate_up) and the expert stage (down), where
+    // the down's 32-token tiles re-read its weights less often than the combine's would
     const bool sh_fused = sh && S > 1 && !mf && S <= SH_SK_MAX_S && !router_tiled(S, D, router_rows(d));
+    const bool sh_late = sh_fused && S <= 32;
     if (router_tiled(S, D, router_rows(d))) {
         if (router_batch(w->router, d->router_bf16, x, S, D, router_rows(d), w->logit_bias, f.logits, f.scores,
                          d->route_act, mf ? nullptr : f.xl, f.xs)) return -1;
     } else {
         PROF("stage_route");
         if (sw_launch_stage_route(g_st, w->router, d->router_bf16, x, S, D, router_rows(d), w->logit_bias, f.logits, f.scores,
-                                  d->route_act, mf ? nullptr : f.xl, f.xs, sh_in || sh_fused ? sg : nullptr, su, Is, f.shh,
-                                  sh && !sh_in && !sh_fused ? f.shx : nullptr, sh_fused ? f.shp : nullptr))
+                                  d->route_act, mf ? nullptr : f.xl, f.xs, sh_in || (sh_fused && !sh_late) ? sg : nullptr, su,
+                                  Is, f.shh, sh && !sh_in && !sh_fused ? f.shx : nullptr,
+                                  sh_fused && !sh_late ? f.shp : nullptr))
             return fail_msg("routing stage launch");
     }
     if (gated && gated_shared(d, w, x, S, f)) return -1;
@@ -783,8 +790,8 @@ static int forward(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const floa
         SwGroups g = {f.gexp, f.gbeg, f.gcnt, f.grow, f.G, sw_npass_max(T, E, SW_DG_TT), 0, f.items, f.P};
         { PROF("stage_experts");
           if (sw_launch_stage_experts(g_st, gu, f.xl, f.xs, g, I, f.hl, f.hs, nullptr, K, nullptr, E, d->route_act,
-                                      w->corr_bias, d->use_corr_bias, d->norm_topk, f.w, sh_fused ? sd : nullptr, f.shh, S,
-                                      Is, D, f.sout, sh_fused ? f.shp : nullptr))
+                                      w->corr_bias, d->use_corr_bias, d->norm_topk, f.w, sh_fused && !sh_late ? sd : nullptr,
+                                      f.shh, S, Is, D, f.sout, sh_fused ? f.shp : nullptr, sh_late ? sg : nullptr, su, x))
               return fail_msg("expert stage launch"); }
         if (sh && !sh_fused) {
             PROF("shared_down");
@@ -793,9 +800,15 @@ static int forward(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const floa
         SwGroups gd = g;
         gd.grow = nullptr;                 // the down reads the packed rows directly
         { PROF("q4_down"); if (sw_launch_q4_dot8_rows(g_st, dn, f.hl, f.hs, gd, f.slots)) return fail_msg("down launch"); }
-        { PROF("combine");
-          if (sw_launch_combine(g_st, f.slots, f.rowof, f.w, S, K, D, rs_c, sh || gated ? f.sout : nullptr, out, 1, wsh, nsg))
-              return fail_msg("combine launch"); }
+        if (sh_late) {
+            PROF("shared_down_combine");
+            if (sw_launch_sh_combine(g_st, sd, f.shp, S, Is, D, f.sout, f.slots, f.rowof, f.w, K, rs_c, out))
+                return fail_msg("shared down + combine launch");
+        } else {
+            PROF("combine");
+            if (sw_launch_combine(g_st, f.slots, f.rowof, f.w, S, K, D, rs_c, sh || gated ? f.sout : nullptr, out, 1, wsh, nsg))
+                return fail_msg("combine launch");
+        }
         g_last_G_dev = 1; g_last_ng = 0;
     }
     g_last = f;

@@ -703,7 +703,9 @@ __global__ __launch_bounds__(SH_NT) void k_stage_route(RouterArgs R, int nbr, in
 }
 
 // TTG: tokens per pass of the routed gate_up.  The extra blocks: the single token's
-// shared down (sh_down_block), or with SKD a batch's (sh_sk_block over the parts of h)
+// shared down (sh_down_block), or with SKD a batch's shared expert: 1 its down
+// (sh_sk_block over the parts of h), 2 its gate_up over column tiles of 16 tokens
+// (sh_sk_block, inputs split from x)
 template <int PF, int PICK, int NP, int TTG, int C16, int RO, int SKD>
 __global__ __launch_bounds__(DG_NT, PICK ? 1 : 4) void k_stage_experts(Dot8GluArgs A, int nbx, int nglu, ShDownArgs Sd,
                                                                     ShSkArgs Skd) {
@@ -712,9 +714,12 @@ __global__ __launch_bounds__(DG_NT, PICK ? 1 : 4) void k_stage_experts(Dot8GluAr
     if (b < nglu) {
         const int w = PICK == 0 && A.grp.items ? sw_xcd_work(b, nglu) : b;
         dot8_glu_block<PF, PICK, NP, TTG, C16, RO>(A, w % nbx, w / nbx, smem);
-    } else if constexpr (SKD) {
+    } else if constexpr (SKD == 1) {
         const int w = b - nglu, nrb = sh_sk_rows(0, Skd.O);
         sh_sk_block<0, 2, 0>(Skd, w % nrb, w / nrb, smem);
+    } else if constexpr (SKD == 2) {
+        const int w = b - nglu, nrb = sh_sk_rows(1, Skd.O);
+        sh_sk_block<1, 1, 1, 6>(Skd, w % nrb, w / nrb, smem);   // (a 6-step ring: within 128 registers)
     } else {
         sh_down_block(Sd.Wd, Sd.h, Sd.Is, Sd.D, Sd.out, b - nglu, smem);
     }
@@ -781,7 +786,7 @@ int sw_launch_stage_route(hipStream_t st, const void *Wc, int w_bf16, const floa
 int sw_launch_stage_experts(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, const float *xs, SwGroups g, int I, sw_u32x4 *hl,
                             float *hs, int *sel, int K, const float *route_src, int E, int act, const float *bias,
                             int use_bias, int norm, float *w, const uint16_t *sd, const float *sh_h, int S, int Is, int D,
-                            float *sh_out, const uint16_t *sh_hp) {
+                            float *sh_out, uint16_t *sh_hp, const uint16_t *sg, const uint16_t *su, const float *x) {
     int gsh;
     if (dot8_glu_check(W, I, gsh)) return -1;
     const bool picks = sel != nullptr;
@@ -792,17 +797,23 @@ int sw_launch_stage_experts(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, const fl
     // batch's split-K blocks (from h's parts); out to sh_out
     if (sd && (!sh_out || D % SH_DN_O || !sh_shape_ok(Is))) return -1;
     if (sd && !(S == 1 ? sh_h && !sh_hp : sh_hp && !picks && S <= SH_SK_MAX_S)) return -1;
-    const bool skd = sd && S > 1;
+    // or a batch's shared gate_up split-K blocks over 16-token column tiles (sg, su over x;
+    // h's parts to sh_hp; up to 32 tokens), not both
+    if (sg && (sd || picks || S > 32 || !su || !x || !sh_hp || Is % 64 || !sh_shape_ok(D))) return -1;
+    const int gnc = 1;
+    const int skd = sd && S > 1 ? 1 : sg ? 2 : 0;
     const int nbx = picks ? K : g.ngroups_max;
     const int RO = picks ? 32 : dg_ro(I);             // outputs per gate_up block
     const int nglu = nbx * (I / RO);
-    const int nsh = !sd ? 0 : skd ? sh_sk_rows(0, D) * sh_sk_cols(S, 2) : sh_down_blocks(D);
+    const int nsh = skd == 1 ? sh_sk_rows(0, D) * sh_sk_cols(S, 2) : skd ? sh_sk_rows(1, Is) * sh_sk_cols(S, gnc)
+                    : sd ? sh_down_blocks(D) : 0;
     const DotRoute rt = route_src ? DotRoute{route_src, bias, E, K, act, use_bias, norm, w} : DotRoute{};
     const Dot8GluArgs A = {W, gsh, xl, xs, g, I, hl, hs, sel, rt};
     const ShDownArgs Sd = {sd, sh_h, Is, D, sh_out};
-    const ShSkArgs Skd = {sd, nullptr, sh_hp, nullptr, S, Is, D, sh_out};
+    const ShSkArgs Skd = skd == 1 ? ShSkArgs{sd, nullptr, sh_hp, nullptr, S, Is, D, sh_out}
+                                  : ShSkArgs{sg, su, nullptr, x, S, D, Is, sh_hp};
     const dim3 grid((unsigned)(nglu + nsh));
-    const size_t shl = !sd ? 0 : skd ? sh_sk_lds(2) : sh_down_lds(Is);
+    const size_t shl = skd == 1 ? sh_sk_lds(2) : skd ? sh_sk_lds(gnc) : sd ? sh_down_lds(Is) : 0;
     if (shl > 65536) return -1;
     const int pf0 = dg_pf_glu(W.K), c16 = dot8_c16(W.K);
     // groups: a 4-step ring, two blocks per CU (four waves per SIMD, 128 VGPRs); an
@@ -810,15 +821,16 @@ int sw_launch_stage_experts(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, const fl
     const int pf = picks ? pf0 : (pf0 < 4 ? pf0 : 4);
     if (!picks) {
         const size_t lds = lds_max(dot8_glu_lds(W.K, DG_TT, RO), shl);
-        if (skd) {
-            if (RO == 128) dispatch_pf_c16<StageL<0, 0, DG_TT, 128, 1>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd, Skd);
-            else if (RO == 64) dispatch_pf_c16<StageL<0, 0, DG_TT, 64, 1>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd, Skd);
-            else dispatch_pf_c16<StageL<0, 0, DG_TT, 32, 1>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd, Skd);
-        } else {
-            if (RO == 128) dispatch_pf_c16<StageL<0, 0, DG_TT, 128>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd, Skd);
-            else if (RO == 64) dispatch_pf_c16<StageL<0, 0, DG_TT, 64>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd, Skd);
-            else dispatch_pf_c16<StageL<0, 0, DG_TT>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd, Skd);
-        }
+#define SW_STG(K_) \
+    do { \
+        if (RO == 128) dispatch_pf_c16<StageL<0, 0, DG_TT, 128, K_>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd, Skd); \
+        else if (RO == 64) dispatch_pf_c16<StageL<0, 0, DG_TT, 64, K_>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd, Skd); \
+        else dispatch_pf_c16<StageL<0, 0, DG_TT, 32, K_>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd, Skd); \
+    } while (0)
+        if (skd == 1) SW_STG(1);
+        else if (skd == 2) SW_STG(2);
+        else SW_STG(0);
+#undef SW_STG
     } else {
         const size_t lds = lds_max(dot8_glu_lds(W.K, 1), shl);
         if (!route_src) dispatch_pf_c16<StageL<1, 0, 1>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd, Skd);

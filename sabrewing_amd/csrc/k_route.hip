@@ -68,8 +68,12 @@ __global__ __launch_bounds__(64 * NW) void k_router_tiles(RouterArgs R, int S, i
 // token tile and waves per block (4 experts each, sharing the tile's x in LDS): 16 tokens
 // on 4 waves for prefill-sized batches (C4: 113 us against 122 on 8 waves), else 8 tokens
 // on 8 waves (a head-sized router: 32 rows per x tile; C5 head 75 us against 92 on one wave)
+#ifndef SW_RT_TT_S
+#define SW_RT_TT_S 8
+#define SW_RT_NW_S 8
+#endif
 static void router_tile_shape(int S, int &tt, int &nw) {
-    if (S >= 512) { tt = 16; nw = 4; } else { tt = 8; nw = 8; }
+    if (S >= 512) { tt = 16; nw = 4; } else { tt = SW_RT_TT_S; nw = SW_RT_NW_S; }
 }
 
 int sw_launch_router_tiles(hipStream_t st, const void *Wc, int w_bf16, const float *x, int S, int D, int E,
@@ -84,9 +88,9 @@ int sw_launch_router_tiles(hipStream_t st, const void *Wc, int w_bf16, const flo
     const dim3 grid((unsigned)((int64_t)nbx * ((S + tt - 1) / tt)));
 #define SW_RT(B, T, W) SW_LAUNCH((k_router_tiles<B, T, W>), grid, dim3(64 * W), 0, st, R, S, nbx)
     if (w_bf16) {
-        if (tt == 16) SW_RT(1, 16, 4); else SW_RT(1, 8, 8);
+        if (tt == 16) SW_RT(1, 16, 4); else SW_RT(1, SW_RT_TT_S, SW_RT_NW_S);
     } else {
-        if (tt == 16) SW_RT(0, 16, 4); else SW_RT(0, 8, 8);
+        if (tt == 16) SW_RT(0, 16, 4); else SW_RT(0, SW_RT_TT_S, SW_RT_NW_S);
     }
 #undef SW_RT
     return launch_err();
@@ -228,56 +232,15 @@ int sw_launch_bucket(hipStream_t st, const int *sel, int S, int K, int E, int *g
 }
 
 // ------------------------------------------------------------ combine ----
-// out[s,d] (+)= (sum_a w[s,a] * slots[rowof[s,a], d]) * route_scale (+ shared[s,d])
-// The sum runs in rank order from 0 with one fused multiply-add per rank,
-// the operation sequence of moe_block's `acc[i] += w[a] * scr[i]` as the
-// reference build compiles it (c/moe_block.h:124-142; c/laguna.c:761-782).
+// every (token, 4 outputs) by combine4 (sw_hip.h)
 __global__ void k_combine(const float *__restrict__ slots, const int *__restrict__ rowof, const float *__restrict__ w,
                           int S, int K, int D, float route_scale, const float *__restrict__ shared,
                           float *__restrict__ out, int accumulate, const float *__restrict__ wsh, int ns) {
     const int64_t n4 = (int64_t)S * (D / 4);
     for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n4; i += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t s = i / (D / 4), d = (i % (D / 4)) * 4;
-        sw_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        for (int a0 = 0; a0 < K; a0 += 8) {
-            sw_f32x4 v[8];
-            float wa[8];
-#pragma unroll
-            for (int u = 0; u < 8; u++) {
-                if (a0 + u < K) {
-                    wa[u] = w[s * K + a0 + u];
-                    v[u] = *(const sw_f32x4 *)(slots + (int64_t)rowof[s * K + a0 + u] * D + d);
-                }
-            }
-#pragma unroll
-            for (int u = 0; u < 8; u++)
-                if (a0 + u < K)
-#pragma unroll
-                    for (int c = 0; c < 4; c++) acc[c] = __builtin_fmaf(wa[u], v[u][c], acc[c]);
-        }
-#pragma unroll
-        for (int c = 0; c < 4; c++) acc[c] = acc[c] * route_scale;
-        if (wsh) {                                    // Inkling's gated shared experts, in order
-            for (int j = 0; j < ns; j++) {
-                const float wj = wsh[s * ns + j];
-                const sw_f32x4 sh = *(const sw_f32x4 *)(shared + (s * ns + j) * D + d);
-#pragma unroll
-                for (int c = 0; c < 4; c++) acc[c] = __builtin_fmaf(wj, sh[c], acc[c]);
-            }
-        } else if (shared) {
-            const sw_f32x4 sh = *(const sw_f32x4 *)(shared + s * D + d);
-#pragma unroll
-            for (int c = 0; c < 4; c++) acc[c] = acc[c] + sh[c];
-        }
-        sw_f32x4 *o = (sw_f32x4 *)(out + s * D + d);
-        if (accumulate) {
-            sw_f32x4 cur = *o;
-#pragma unroll
-            for (int c = 0; c < 4; c++) cur[c] = cur[c] + acc[c];
-            *o = cur;
-        } else {
-            *o = acc;
-        }
+        const int64_t s = i / (D / 4);
+        const int d = (int)(i % (D / 4)) * 4;
+        combine4(slots, rowof, w, s, K, D, d, route_scale, shared, out, accumulate, wsh, ns);
     }
 }
 

@@ -173,6 +173,24 @@ __global__ __launch_bounds__(SH_SK_NT) void k_sh_sk(ShSkArgs A) {
     __shared__ float red[8 * 16 * 16 * NC];                // [segment][row][token]
     sh_sk_block<GLU, NC, 0>(A, blockIdx.x, blockIdx.y, red);
 }
+// The shared expert's down fused with the rank-order combine of a decode-sized batch:
+// block (bx, by) runs the down of rows 16 bx .. +15 for the 32 tokens of column tile
+// by (sh_sk_block, written to shared [S][D]), then combines those outputs of those
+// tokens (combine4, the combine launch's arithmetic) into out.
+__global__ __launch_bounds__(SH_SK_NT) void k_sh_combine(ShSkArgs A, const float *__restrict__ slots,
+                                                        const int *__restrict__ rowof, const float *__restrict__ w, int K,
+                                                        float route_scale, float *__restrict__ out) {
+    __shared__ float red[8 * 16 * 16 * 2];
+    sh_sk_block<0, 2, 0>(A, blockIdx.x, blockIdx.y, red);
+    __syncthreads();                                    // the tile's shared outputs are written
+    const int tid = threadIdx.x;
+    if (tid < 32 * 4) {
+        const int64_t s = (int64_t)blockIdx.y * 32 + (tid >> 2);
+        if (s < A.S) combine4(slots, rowof, w, s, K, A.O, blockIdx.x * 16 + 4 * (tid & 3), route_scale,
+                              (const float *)A.out, out, 1, nullptr, 0);
+    }
+}
+
 // decode-sized batches take the split-K blocks: the gate_up 16-token column tiles up to
 // 32 tokens (the grid then fills the chip), else 32-token tiles
 template <int GLU>
@@ -207,5 +225,14 @@ int sw_launch_sh_down(hipStream_t st, const uint16_t *Wd, const uint16_t *hp, in
     if (S <= SH_SK_MAX_S) return launch_sk<0>(st, Wd, nullptr, hp, S, Is, D, out);
     const dim3 grid((unsigned)(D / 128 * ((S + SHB_TOK - 1) / SHB_TOK)));
     SW_LAUNCH(k_sh_down_mf, grid, dim3(256), 0, st, Wd, hp, S, Is, D, out);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int sw_launch_sh_combine(hipStream_t st, const uint16_t *Wd, const uint16_t *hp, int S, int Is, int D, float *shared,
+                         const float *slots, const int *rowof, const float *w, int K, float route_scale, float *out) {
+    if (S <= 0 || S > SH_SK_MAX_S || D % 16 || K <= 0 || !sh_shape_ok(Is)) return -1;
+    const ShSkArgs A = {Wd, nullptr, hp, nullptr, S, Is, D, shared};
+    const dim3 grid((unsigned)sh_sk_rows(0, D), (unsigned)sh_sk_cols(S, 2));
+    SW_LAUNCH(k_sh_combine, grid, dim3(SH_SK_NT), 0, st, A, slots, rowof, w, K, route_scale, out);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }

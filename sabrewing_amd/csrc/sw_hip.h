@@ -63,13 +63,62 @@ __device__ __forceinline__ sw_u32x4 sw_ld16(sw_rsrc r, uint32_t voff, uint32_t s
 __device__ __forceinline__ float sw_ld4f(sw_rsrc r, uint32_t voff, uint32_t soff) {
     return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
 }
+// The rank-order combine of token s at outputs d .. d+3:
+// out[s,d] (+)= (sum_a w[s,a] * slots[rowof[s,a], d]) * route_scale (+ shared[s,d])
+// The sum runs in rank order from 0 with one fused multiply-add per rank, the
+// operation sequence of moe_block's `acc[i] += w[a] * scr[i]` as the reference
+// build compiles it (c/moe_block.h:124-142; c/laguna.c:761-782); with wsh,
+// Inkling's ns gated shared outputs shared[s][ns][D] follow as fma(wsh[s,j], .).
+__device__ __forceinline__ void combine4(const float *__restrict__ slots, const int *__restrict__ rowof,
+                                         const float *__restrict__ w, int64_t s, int K, int D, int d, float route_scale,
+                                         const float *__restrict__ shared, float *__restrict__ out, int accumulate,
+                                         const float *__restrict__ wsh, int ns) {
+    sw_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int a0 = 0; a0 < K; a0 += 8) {
+        sw_f32x4 v[8];
+        float wa[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            if (a0 + u < K) {
+                wa[u] = w[s * K + a0 + u];
+                v[u] = *(const sw_f32x4 *)(slots + (int64_t)rowof[s * K + a0 + u] * D + d);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            if (a0 + u < K)
+#pragma unroll
+                for (int c = 0; c < 4; c++) acc[c] = __builtin_fmaf(wa[u], v[u][c], acc[c]);
+    }
+#pragma unroll
+    for (int c = 0; c < 4; c++) acc[c] = acc[c] * route_scale;
+    if (wsh) {
+        for (int j = 0; j < ns; j++) {
+            const float wj = wsh[s * ns + j];
+            const sw_f32x4 sh = *(const sw_f32x4 *)(shared + (s * ns + j) * D + d);
+#pragma unroll
+            for (int c = 0; c < 4; c++) acc[c] = __builtin_fmaf(wj, sh[c], acc[c]);
+        }
+    } else if (shared) {
+        const sw_f32x4 sh = *(const sw_f32x4 *)(shared + s * D + d);
+#pragma unroll
+        for (int c = 0; c < 4; c++) acc[c] = acc[c] + sh[c];
+    }
+    sw_f32x4 *o = (sw_f32x4 *)(out + s * D + d);
+    if (accumulate) {
+        sw_f32x4 cur = *o;
+#pragma unroll
+        for (int c = 0; c < 4; c++) cur[c] = cur[c] + acc[c];
+        *o = cur;
+    } else {
+        *o = acc;
+    }
+}
 #endif
 
 #define SW_WAVE 64
 
 static inline int64_t sw_imin64(int64_t a, int64_t b) { return a < b ? a : b; }
-#define SW_WPRESCALE 256.0f          // group-scale weights are stored as f16(s * 2^8 * (n-8))
-#define SW_WPRESCALE_INV 0.00390625f
 
 // ---- work description for the grouped GEMMs ----
 // A "group" is one expert applied to gcnt consecutive packed rows starting at
@@ -236,6 +285,10 @@ int sw_launch_q4_dot8_down_combine(hipStream_t st, SwQ4 W, const sw_u32x4 *hl, c
 // out[d] += (sum_a w[a] * down_{sel[a]}(h_a)[d]) * route_scale (+ shared[d])
 // out[s] (+)= route_scale * sum_a w[s,a] * slots[rowof[s,a]] (+ shared[s])
 // (wsh non-null: shared [S][ns][D] gated by wsh [S][ns] after the ranks, as above)
+// the shared expert's down of h's parts hp fused with the combine (accumulating into
+// out, shared [S][D] its scratch): decode-sized batches (k_shared.hip)
+int sw_launch_sh_combine(hipStream_t st, const uint16_t *Wd, const uint16_t *hp, int S, int Is, int D, float *shared,
+                         const float *slots, const int *rowof, const float *w, int K, float route_scale, float *out);
 int sw_launch_combine(hipStream_t st, const float *slots, const int *rowof, const float *w, int S, int K, int D,
                       float route_scale, const float *shared, float *out, int accumulate,
                       const float *wsh = nullptr, int ns = 0);
@@ -245,7 +298,8 @@ int sw_launch_combine(hipStream_t st, const float *slots, const int *rowof, cons
 // bf16 parts of x (sw_shared.h); stage 2 = routed gate_up (sel non-null: one
 // token's K picks, from sel or, with route_src, by a gate + top-k in every
 // block; else the groups g) + the shared expert's down (sd null: none; from
-// one token's h in sh_h, or a batch's from h's parts in sh_hp)
+// one token's h in sh_h, or a batch's from h's parts in sh_hp) or a batch's
+// shared gate_up (sg, su over x; h's parts to sh_hp)
 int sw_launch_stage_route(hipStream_t st, const void *Wc, int w_bf16, const float *x, int S, int D, int E,
                           const float *logit_bias, float *logits, float *scores, int route_act, sw_u32x4 *xl, float *xs,
                           const uint16_t *sg, const uint16_t *su, int Is, float *sh_h, uint16_t *xp = nullptr,
@@ -253,7 +307,8 @@ int sw_launch_stage_route(hipStream_t st, const void *Wc, int w_bf16, const floa
 int sw_launch_stage_experts(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, const float *xs, SwGroups g, int I, sw_u32x4 *hl,
                             float *hs, int *sel, int K, const float *route_src, int E, int act, const float *bias,
                             int use_bias, int norm, float *w, const uint16_t *sd, const float *sh_h, int S, int Is, int D,
-                            float *sh_out, const uint16_t *sh_hp = nullptr);
+                            float *sh_out, uint16_t *sh_hp = nullptr, const uint16_t *sg = nullptr,
+                            const uint16_t *su = nullptr, const float *x = nullptr);
 // the shared expert on the VALU (sw_shared.h): h[S, Is] = silu(Wg x) * (Wu x)
 // and out[S, D] = Wd h, bf16 weights, f32 activations
 // stack glue (k_glue.hip): RMSNorm rows, greedy argmax rows

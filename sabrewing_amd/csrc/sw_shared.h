@@ -241,7 +241,9 @@ __host__ __device__ inline int sh_sk_nc(int GLU, int S) { return GLU && S <= 32 
 __host__ __device__ inline int sh_sk_rows(int GLU, int O) { return GLU ? O / 8 : O / 16; }
 __host__ __device__ inline int sh_sk_cols(int S, int nc) { return (S + 16 * nc - 1) / (16 * nc); }
 __host__ __device__ inline size_t sh_sk_lds(int nc) { return (size_t)8 * 16 * 16 * nc * 4; }
-template <int GLU, int NC, int FX>
+// PF: steps in flight (weight and part words); 0: 8 with one column tile, else 4 (measured
+// best at B = 8, 32 and 64)
+template <int GLU, int NC, int FX, int PF = 0>
 __device__ __forceinline__ void sh_sk_block(const ShSkArgs &A, int bx, int by, float *red) {
     const uint16_t *__restrict__ W0 = A.W0, *__restrict__ W1 = A.W1, *__restrict__ xp = A.xp;
     const int S = A.S, K = A.K, O = A.O;
@@ -258,7 +260,7 @@ __device__ __forceinline__ void sh_sk_block(const ShSkArgs &A, int bx, int by, f
 #pragma unroll
         for (int c = 0; c < NC; c++) {
             const int64_t tok = min(tok0 + 16 * c + m, S - 1);
-            if (FX) bf[c] = A.xf + tok * K + 8 * kq;
+            if constexpr (FX) bf[c] = A.xf + tok * K + 8 * kq;
             else br[c] = xp + tok * K * 3 + 8 * kq;
         }
         const int g0 = wave * GS;
@@ -270,7 +272,7 @@ __device__ __forceinline__ void sh_sk_block(const ShSkArgs &A, int bx, int by, f
             st.a = *(const sw_u32x4 *)(wr + (int64_t)g * SH_RG);
 #pragma unroll
             for (int c = 0; c < NC; c++) {
-                if (FX) {
+                if constexpr (FX) {
                     st.b[c][0] = *(const sw_u32x4 *)(bf[c] + g * SH_RG);
                     st.b[c][1] = *(const sw_u32x4 *)(bf[c] + g * SH_RG + 4);
                 } else {
@@ -282,15 +284,14 @@ __device__ __forceinline__ void sh_sk_block(const ShSkArgs &A, int bx, int by, f
         sw_f32x4 acc[NC];
 #pragma unroll
         for (int c = 0; c < NC; c++) acc[c] = sw_f32x4{0.f, 0.f, 0.f, 0.f};
-        // steps in flight (weight and part words): 8 and 4 measured best at B = 8, 32 and 64
-        constexpr int SHK_PF = NC == 1 ? 8 : 4;
+        constexpr int SHK_PF = PF ? PF : NC == 1 ? 8 : 4;
         Step ring[SHK_PF];
 #pragma unroll
         for (int u = 0; u < SHK_PF; u++) load(u, ring[u]);
         auto use = [&](const Step &st) {
 #pragma unroll
             for (int c = 0; c < NC; c++) {
-                if (FX) {
+                if constexpr (FX) {
                     sw_u32x4 p0, p1, p2;
                     sh_split8(__builtin_bit_cast(sw_f32x4, st.b[c][0]), __builtin_bit_cast(sw_f32x4, st.b[c][1]), p0, p1, p2);
                     acc[c] = sh_mfma3(st.a, p0, p1, p2, acc[c]);
