@@ -129,7 +129,23 @@ __device__ void gate_topk_wave(const float *__restrict__ src, int E, int K, int 
         }
         return sum;
     };
+    // (in double, for terms in [0, 1]: when every nonzero term is at least 2^-19, all terms
+    // are multiples of 2^-42 and every partial sum of at most 1024 of them is below 2^11,
+    // so each addition is exact and any order gives the sequential sum's bits -- a wave
+    // tree then replaces the 64-step scan; a NaN or a smaller term takes the scan)
     auto sum_d = [&](float *p) {
+        bool small = false;
+#pragma unroll
+        for (int i = 0; i < NPER; i++)
+            if (NPER * lane + i < E && !(p[i] == 0.f || p[i] >= 0x1p-19f)) small = true;
+        if (__ballot(small) == 0ull) {
+            double t = 0.0;
+#pragma unroll
+            for (int i = 0; i < NPER; i++)
+                if (NPER * lane + i < E) t += (double)p[i];
+            for (int o = 32; o; o >>= 1) t += __shfl_xor(t, o);
+            return t;
+        }
         double sum = 0.0;
         for (int l = 0; l < 64 && NPER * l < E; l++) {
 #pragma unroll

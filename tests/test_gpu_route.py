@@ -92,3 +92,27 @@ def test_route_ties_and_nonfinite(be, orc):
     ok = (w.view(np.uint32) == w_w.view(np.uint32)) | (np.isnan(w) & np.isnan(w_w))
     assert ok.all()
     assert list(sel_w[1]) == list(range(cfg.K))
+
+
+SOFTMAX = [cf.C1, cf.C5_LAYER, cf.QWEN]
+
+
+@pytest.mark.parametrize("cfg", SOFTMAX, ids=[c.name for c in SOFTMAX])
+@pytest.mark.parametrize("xscale", [1.0, 8.0])
+def test_route_softmax_sum_paths(be, orc, cfg, xscale):
+    """The softmax's double sum takes a wave tree when every nonzero term is at least
+    2^-19 (then every partial sum is exact, so any order gives the expert-order sum) and
+    the expert-order scan otherwise.  x as drawn keeps every token on the tree; x * 8
+    spreads the logits so that every token has terms below 2^-19 and takes the scan.
+    Both must give the reference's bits."""
+    L = router_layer(orc, cfg, 77)
+    x = synth.make_x(orc, cfg, 78, 16) * np.float32(xscale)
+    lg_w, sel_w, w_w = orc.route(synth.desc_of(cfg), L, x)
+    lg64 = lg_w[:, :cfg.E].astype(np.float64)
+    p = np.exp(lg64 - lg64.max(1, keepdims=True)).astype(np.float32)
+    tiny = ((p > 0) & (p < 2.0 ** -19)).any(1)
+    assert (not tiny.any()) if xscale == 1.0 else tiny.all()      # the path each token takes
+    lg, sel, w = device_route(be, cfg, L, x)
+    assert np.array_equal(lg.view(np.uint32), lg_w.view(np.uint32))
+    assert np.array_equal(sel, sel_w)
+    assert np.array_equal(w.view(np.uint32), w_w.view(np.uint32))
