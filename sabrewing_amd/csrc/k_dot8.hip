@@ -318,6 +318,14 @@ struct GluL {
 // outputs per gate_up block of a batch: 128 or 64 when I allows (fewer blocks, so less
 // per-block start and epilogue per weight byte: B=32 gate_up 215 -> 190 us), else 32
 static int dg_ro(int I) { return I % 128 == 0 ? 128 : I % 64 == 0 ? 64 : 32; }
+// outputs per block of a grouped gate_up launch of nbx passes: 128 when that gives at
+// least 1024 blocks (two rounds of the 512 that are resident at once), else 64, so a
+// short grid ends in a smaller tail (C5 at B = 8: 768 blocks of 128 outputs took 95.7 us,
+// 1536 of 64 take 87.9; at B = 16, 1280 blocks of 128 run 130 us against 134 with 64)
+static int dg_ro_grid(int I, int nbx) {
+    const int ro = dg_ro(I);
+    return ro == 128 && (int64_t)nbx * (I / 128) < 1024 ? 64 : ro;
+}
 
 static int dot8_glu_check(SwQ4 W, int I, int &gsh) {
     if (!dot8_shape_ok(W.K) || I % 32 || W.O != 2 * I || !sw_q4_extent_ok(W)) return -1;
@@ -330,7 +338,7 @@ int sw_launch_q4_dot8_glu(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, const floa
     int gsh;
     if (dot8_glu_check(W, I, gsh) || g.ngroups_max <= 0) return -1;
     const Dot8GluArgs A = {W, gsh, xl, xs, g, I, hl, hs, nullptr, DotRoute{}};
-    const int RO = dg_ro(I);
+    const int RO = dg_ro_grid(I, g.ngroups_max);
     const dim3 grid((unsigned)g.ngroups_max, (unsigned)(I / RO));
     if (RO == 128) dispatch_pf_c16<GluL<0, DG_TT, 128>::L>(dg_pf_glu(W.K), dot8_c16(W.K), grid, dot8_glu_lds(W.K, DG_TT, 128), st, A);
     else if (RO == 64) dispatch_pf_c16<GluL<0, DG_TT, 64>::L>(dg_pf_glu(W.K), dot8_c16(W.K), grid, dot8_glu_lds(W.K, DG_TT, 64), st, A);
@@ -803,7 +811,7 @@ int sw_launch_stage_experts(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, const fl
     const int gnc = 1;
     const int skd = sd && S > 1 ? 1 : sg ? 2 : 0;
     const int nbx = picks ? K : g.ngroups_max;
-    const int RO = picks ? 32 : dg_ro(I);             // outputs per gate_up block
+    const int RO = picks ? 32 : dg_ro_grid(I, nbx);   // outputs per gate_up block
     const int nglu = nbx * (I / RO);
     const int nsh = skd == 1 ? sh_sk_rows(0, D) * sh_sk_cols(S, 2) : skd ? sh_sk_rows(1, Is) * sh_sk_cols(S, gnc)
                     : sd ? sh_down_blocks(D) : 0;
