@@ -750,7 +750,11 @@ static int forward(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const floa
         if (sw_launch_digits(g_st, x, S, D, f.xd, f.xds)) return fail_msg("digits launch");
     }
     if (sh && !sh_in && !sh_fused && shared_glu_batch(w, x, S, D, Is, f, !router_tiled(S, D, router_rows(d)))) return -1;
-    if (!in_experts && gate_dev(d, w, S, f)) return -1;
+    // a small batch on the dot8 kernels: its gate + top-k and the bucketing in one launch
+    // (up to 8 tokens, a wave each; beyond, a wave's several top-ks in a row cost more
+    // than the launch saves: 10.9 against 9.2 us at 16 tokens)
+    const bool gate_bucket = !in_experts && S > 1 && S <= 8 && !mf && E <= 1024;
+    if (!in_experts && !gate_bucket && gate_dev(d, w, S, f)) return -1;
     if (S == 1) {                        // one token: its K picks in rank order, fused down + combine
         { PROF("stage_experts");
           if (sw_launch_stage_experts(g_st, gu, f.xl, f.xs, SwGroups{}, I, f.hl, f.hs, f.sel, K,
@@ -782,9 +786,19 @@ static int forward(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const floa
               return fail_msg("combine launch"); }
         g_last_G_dev = 1; g_last_ng = 0;
     } else {
-        { PROF("bucket");
-          if (sw_launch_bucket(g_st, f.sel, S, K, E, f.gexp, f.gbeg, f.gcnt, f.G, f.grow, f.rowof, SW_DG_TT, f.items, f.P))
-              return fail_msg("bucket launch"); }
+        if (gate_bucket) {
+            PROF("gate_bucket");
+            const int ns = ink_ns(d);
+            const SwGateOpt o = {router_rows(d), ns, d->route_scale, d->topk, ns ? f.wsh : nullptr, ns};
+            if (sw_launch_gate_bucket(g_st, f.logits, f.scores, S, E, K, d->route_act, w->corr_bias, d->use_corr_bias,
+                                      d->norm_topk, f.sel, f.w, &o, f.gexp, f.gbeg, f.gcnt, f.G, f.grow, f.rowof, SW_DG_TT,
+                                      f.items, f.P))
+                return fail_msg("gate/top-k + bucket launch");
+        } else {
+            PROF("bucket");
+            if (sw_launch_bucket(g_st, f.sel, S, K, E, f.gexp, f.gbeg, f.gcnt, f.G, f.grow, f.rowof, SW_DG_TT, f.items, f.P))
+                return fail_msg("bucket launch");
+        }
         // one block per pass of up to SW_DG_TT tokens of a group (the passes of a group
         // with many tokens spread over blocks instead of queueing in one)
         SwGroups g = {f.gexp, f.gbeg, f.gcnt, f.grow, f.G, sw_npass_max(T, E, SW_DG_TT), 0, f.items, f.P};

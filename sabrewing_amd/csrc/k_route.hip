@@ -151,11 +151,16 @@ int sw_launch_gate_topk(hipStream_t st, const float *logits, const float *scores
 // 64 pairs of an expert, so each count is one byte: 16 KB for 1024 experts).
 #define BK_THREADS 1024
 #define BK_MAXE 1024
-__global__ __launch_bounds__(BK_THREADS) void k_bucket(const int *__restrict__ sel, int T, int K, int E,
-                                                       int *__restrict__ gexp, int *__restrict__ gbeg,
-                                                       int *__restrict__ gcnt, int *__restrict__ Gout,
-                                                       int *__restrict__ grow, int *__restrict__ rowof, int tt,
-                                                       int *__restrict__ items, int *__restrict__ Pout) {
+struct BucketArgs {
+    int *gexp, *gbeg, *gcnt, *Gout, *grow, *rowof;
+    int tt;
+    int *items, *Pout;
+};
+// by a block of BK_THREADS threads
+__device__ __forceinline__ void bucket_block(const int *__restrict__ sel, int T, int K, int E, const BucketArgs &B) {
+    int *__restrict__ gexp = B.gexp, *__restrict__ gbeg = B.gbeg, *__restrict__ gcnt = B.gcnt, *__restrict__ Gout = B.Gout;
+    int *__restrict__ grow = B.grow, *__restrict__ rowof = B.rowof, *__restrict__ items = B.items, *__restrict__ Pout = B.Pout;
+    const int tt = B.tt;
     __shared__ int cnt[BK_MAXE], run[BK_MAXE], sa[BK_MAXE], sb[BK_MAXE], sp[BK_MAXE];
     __shared__ uint8_t wcnt[BK_THREADS / 64][BK_MAXE];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -222,12 +227,60 @@ __global__ __launch_bounds__(BK_THREADS) void k_bucket(const int *__restrict__ s
     }
 }
 
+__global__ __launch_bounds__(BK_THREADS) void k_bucket(const int *__restrict__ sel, int T, int K, int E, BucketArgs B) {
+    bucket_block(sel, T, K, E, B);
+}
+
 int sw_launch_bucket(hipStream_t st, const int *sel, int S, int K, int E, int *gexp, int *gbeg,
                      int *gcnt, int *G, int *grow, int *rowof, int tt, int *items, int *P) {
     if (E <= 0 || E > BK_MAXE || S <= 0 || K <= 0 || tt <= 0 || (items && !P)) return -1;
     if ((int64_t)S * K >= (1 << 21)) return -1;      // pass offsets in 21 bits of an item
-    SW_LAUNCH(k_bucket, dim3(1), dim3(BK_THREADS), 0, st, sel, S * K, K, E, gexp, gbeg, gcnt, G, grow, rowof, tt,
-              items, P);
+    const BucketArgs B = {gexp, gbeg, gcnt, G, grow, rowof, tt, items, P};
+    SW_LAUNCH(k_bucket, dim3(1), dim3(BK_THREADS), 0, st, sel, S * K, K, E, B);
+    return launch_err();
+}
+
+// The gate + top-k of a batch of up to GB_MAXS tokens and the bucketing of its picks in
+// one block: wave w takes tokens w, w + 16, ... (each as k_gate_topk's wave), the block
+// barrier, then bucket_block over the picks -- one launch instead of two.
+#define GB_MAXS 32
+template <int NPER>
+__global__ __launch_bounds__(BK_THREADS) void k_gate_bucket(const float *__restrict__ logits, const float *__restrict__ scores,
+                                                            int S, int E, int K, int act, const float *__restrict__ bias,
+                                                            int use_bias, int norm, int *__restrict__ sel_all,
+                                                            float *__restrict__ w_all, SwGateOpt o, BucketArgs B) {
+    __shared__ uint64_t tab[32];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int s = wave; s < S; s += BK_THREADS / 64) {
+        int sk;
+        float wk;
+        gate_topk_wave<NPER>((sw_act_softmax(act) ? logits : scores) + (int64_t)s * o.ld, E, K, act, bias, use_bias, norm,
+                             tab, sk, wk, o.ns, o.rs, o.wsh ? o.wsh + (int64_t)s * o.wshld : nullptr);
+        if (lane < K) { sel_all[(int64_t)s * K + lane] = sk; w_all[(int64_t)s * o.wld + lane] = wk; }
+    }
+    __syncthreads();                                  // the block's picks are written
+    bucket_block(sel_all, S * K, K, E, B);
+}
+
+int sw_launch_gate_bucket(hipStream_t st, const float *logits, const float *scores, int S, int E, int K, int route_act,
+                          const float *corr_bias, int use_corr_bias, int norm_topk, int *sel, float *w,
+                          const SwGateOpt *opt, int *gexp, int *gbeg, int *gcnt, int *G, int *grow, int *rowof, int tt,
+                          int *items, int *P) {
+    if (E <= 0 || E > TK_MAXE || E > BK_MAXE || S <= 0 || S > GB_MAXS || K <= 0 || K > 64 || K > E || route_act < 0 ||
+        route_act > SW_ROUTE_ACT_MAX || tt <= 0 || (items && !P)) return -1;
+    if (!sw_act_softmax(route_act) && !scores) return -1;
+    const SwGateOpt o = opt ? *opt : SwGateOpt{E, 0, 1.f, K, nullptr, 0};
+    if (o.ld < E + o.ns || o.wld < K || o.ns < 0 || o.ns > 64 || (o.ns && route_act != SW_ROUTE_INKLING)) return -1;
+    const BucketArgs B = {gexp, gbeg, gcnt, G, grow, rowof, tt, items, P};
+    const int nper = (E + 63) / 64;
+#define SW_GB(NP) SW_LAUNCH(k_gate_bucket<NP>, dim3(1), dim3(BK_THREADS), 0, st, logits, scores, S, E, K, route_act, \
+                                     corr_bias, use_corr_bias, norm_topk, sel, w, o, B)
+    if (nper <= 1) SW_GB(1);
+    else if (nper <= 2) SW_GB(2);
+    else if (nper <= 4) SW_GB(4);
+    else if (nper <= 8) SW_GB(8);
+    else SW_GB(16);
+#undef SW_GB
     return launch_err();
 }
 

@@ -241,6 +241,12 @@ int sw_launch_gate_topk(hipStream_t st, const float *logits, const float *scores
                         const float *corr_bias, int use_corr_bias, int norm_topk, int *sel, float *w,
                         const SwGateOpt *opt = nullptr);
 // counting sort by expert; with items non-null also the pass list of tt tokens (SwGroups)
+// the gate + top-k and the bucketing of a batch of up to 32 tokens in one launch (the
+// arguments of sw_launch_gate_topk, then those of sw_launch_bucket)
+int sw_launch_gate_bucket(hipStream_t st, const float *logits, const float *scores, int S, int E, int K, int route_act,
+                          const float *corr_bias, int use_corr_bias, int norm_topk, int *sel, float *w,
+                          const SwGateOpt *opt, int *gexp, int *gbeg, int *gcnt, int *G, int *grow, int *rowof, int tt,
+                          int *items, int *P);
 int sw_launch_bucket(hipStream_t st, const int *sel, int S, int K, int E, int *gexp, int *gbeg,
                      int *gcnt, int *G, int *grow, int *rowof, int tt, int *items, int *P);
 // the reference CPU's 16-lane GEMV contracts (k_lanes.hip), bit for bit: wkind 0 bf16,
