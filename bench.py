@@ -67,9 +67,18 @@ def kernel_bytes(cfg, S, G):
              "stage_experts": gu_w + S * limb(D) + T * limb(I),
              "q4_down": dn_w + T * limb(I) + T * D * 4,
              "combine": T * D * 4 + 2 * S * D * 4 + (S * D * 4 if cfg.shared_mode else 0) + T * 8}
+        b["gate_bucket"] = b["gate_topk"] + b["bucket"]      # (one launch up to 8 tokens)
         if cfg.shared_mode:
-            b["shared_glu"] = sh_gu + S * D * 4 + S * Is * 4
-            b["shared_down"] = sh_dn + S * Is * 4 + S * D * 4
+            b["shared_glu"] = sh_gu + S * D * 4 + S * Is * 6
+            b["shared_down"] = sh_dn + S * Is * 6 + S * D * 4
+            # decode-sized batches: the shared expert's blocks ride in other launches (h as
+            # three bf16 parts, 6 bytes per value)
+            if S <= 32:
+                b["stage_experts"] += b["shared_glu"]
+                b["shared_down_combine"] = b["combine"] + sh_dn + S * Is * 6
+            elif S <= 128:
+                b["stage_route"] += sh_gu + S * Is * 6
+                b["stage_experts"] += b["shared_down"]
     return b
 
 
