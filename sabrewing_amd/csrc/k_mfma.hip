@@ -273,11 +273,18 @@ __global__ __launch_bounds__(MF_NT, 1) void k_mf(MfArgs A) {
         sw_i32x4 R0[2], R1[2];
         if (REAL) {
             const sw_i32x4 z = {0, 0, 0, 0};
+            // the MFMAs issue at raised wave priority: the SIMD's four waves, which leave
+            // each chunk's barrier together, then spread out instead of waiting on their
+            // products in step (C4: gate_up 2.33 -> 2.30 ms, down 1.32 -> 1.26 ms; the
+            // priority raised for the whole group, or for the LDS fetches, gained less)
+            __builtin_amdgcn_s_setprio(1);
 #pragma unroll
             for (int mi = 0; mi < 2; mi++) {
                 R0[mi] = __builtin_amdgcn_mfma_i32_16x16x64_i8(F.a[mi], F.b[0], z, 0, 0, 0);
                 R1[mi] = __builtin_amdgcn_mfma_i32_16x16x64_i8(F.a[mi], F.b[1], z, 0, 0, 0);
             }
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_setprio(0);
         }
 #pragma unroll
         for (int mi = 0; mi < 2; mi++)
