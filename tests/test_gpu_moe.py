@@ -56,14 +56,18 @@ def test_layer_small(be, orc, cfg, S_):
 
 
 @pytest.mark.parametrize("cfg", [SMALL[1], SMALL[4]], ids=lambda c: c.name)
-def test_grouped_equals_per_token(be, orc, cfg):
-    """every stream of a batch gets the same bits as its own single-token call"""
+@pytest.mark.parametrize("S_", [5, 32, 40])
+def test_grouped_equals_per_token(be, orc, cfg, S_):
+    """every stream of a batch gets the same bits as its own single-token call -- at 5
+    tokens (gate + top-k and bucketing in one launch), 32 (the shared expert's blocks in
+    the grouped gate_up and the combine launches) and 40 (in the routing and grouped
+    gate_up launches)"""
     L = synth.make_layer(orc, cfg, 41)
     dl = DeviceLayer.from_host(be, cfg, L)
-    x = synth.make_x(orc, cfg, 42, 32)
+    x = synth.make_x(orc, cfg, 42, S_)
     base = np.zeros_like(x)
     batched = be.moe_block(desc_of(cfg), dl.weights(), x, base)
-    single = np.stack([be.moe_block(desc_of(cfg), dl.weights(), x[s:s + 1], base[s:s + 1])[0] for s in range(32)])
+    single = np.stack([be.moe_block(desc_of(cfg), dl.weights(), x[s:s + 1], base[s:s + 1])[0] for s in range(S_)])
     dl.free()
     assert np.array_equal(batched.view(np.uint32), single.view(np.uint32))
 
