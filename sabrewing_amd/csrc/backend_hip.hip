@@ -564,10 +564,7 @@ static int carve_fwd(const LagHipMoeDesc *d, int S, FwdScratch &f, const Scratch
 // (each weight slice read once per tile, the same bits as the per-token blocks), then
 // the limbs of x as a kernel of their own; smaller batches keep the fused routing stage
 // (B = 32: 11 us against 22 + 4 us tiled, the tiles' x chunks waiting on one wave per CU)
-#ifndef SW_RT_MIN_S
-#define SW_RT_MIN_S 512
-#endif
-static bool router_tiled(int S, int D, int R) { return S >= 2 && D % 256 == 0 && (S >= SW_RT_MIN_S || R >= 4096); }
+static bool router_tiled(int S, int D, int R) { return S >= 2 && D % 256 == 0 && (S >= 512 || R >= 4096); }
 static int router_batch(const void *Wc, int w_bf16, const float *x, int S, int D, int R, const float *lbias,
                         float *logits, float *scores, int act, sw_u32x4 *xl, float *xs) {
     { PROF("router_tiles");

@@ -68,12 +68,8 @@ __global__ __launch_bounds__(64 * NW) void k_router_tiles(RouterArgs R, int S, i
 // token tile and waves per block (4 experts each, sharing the tile's x in LDS): 16 tokens
 // on 4 waves for prefill-sized batches (C4: 113 us against 122 on 8 waves), else 8 tokens
 // on 8 waves (a head-sized router: 32 rows per x tile; C5 head 75 us against 92 on one wave)
-#ifndef SW_RT_TT_S
-#define SW_RT_TT_S 8
-#define SW_RT_NW_S 8
-#endif
 static void router_tile_shape(int S, int &tt, int &nw) {
-    if (S >= 512) { tt = 16; nw = 4; } else { tt = SW_RT_TT_S; nw = SW_RT_NW_S; }
+    if (S >= 512) { tt = 16; nw = 4; } else { tt = 8; nw = 8; }
 }
 
 int sw_launch_router_tiles(hipStream_t st, const void *Wc, int w_bf16, const float *x, int S, int D, int E,
@@ -88,9 +84,9 @@ int sw_launch_router_tiles(hipStream_t st, const void *Wc, int w_bf16, const flo
     const dim3 grid((unsigned)((int64_t)nbx * ((S + tt - 1) / tt)));
 #define SW_RT(B, T, W) SW_LAUNCH((k_router_tiles<B, T, W>), grid, dim3(64 * W), 0, st, R, S, nbx)
     if (w_bf16) {
-        if (tt == 16) SW_RT(1, 16, 4); else SW_RT(1, SW_RT_TT_S, SW_RT_NW_S);
+        if (tt == 16) SW_RT(1, 16, 4); else SW_RT(1, 8, 8);
     } else {
-        if (tt == 16) SW_RT(0, 16, 4); else SW_RT(0, SW_RT_TT_S, SW_RT_NW_S);
+        if (tt == 16) SW_RT(0, 16, 4); else SW_RT(0, 8, 8);
     }
 #undef SW_RT
     return launch_err();
