@@ -182,6 +182,13 @@ int    lag_hip_last_groups(int *G, int *gexp, int *gbeg, int *gcnt, int cap);
 /* out[s] = x[s] / sqrt(mean(x[s]^2) + eps) * w, the squares summed in double
  * (rmsnorm_row, c/moe_math.h:58-62); out may be x.  0 = ok */
 int    lag_hip_rmsnorm(const float *x, const float *w, float *out, int S, int D, float eps);
+/* One stack layer in one call: xn = rmsnorm(h, norm_w, eps) as lag_hip_rmsnorm (the
+ * same bits), then h += MoE(xn) as lag_hip_moe_forward.  No counterpart in the
+ * reference (c/laguna.c:1156-1160 calls rmsnorm_row and the block separately); for
+ * stack callers: without a shared expert and below 512 tokens the routing launch
+ * applies the norm as it stages the rows, one launch fewer per layer.  0 = ok */
+int    lag_hip_moe_forward_rmsnorm(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const float *norm_w, float eps,
+                                   float *xn, float *h, int S);
 /* logits[S,V] = x[S,D] . head^T under the 16-lane contract of the head's
  * resmm -> matmul_bf16 (c/laguna.c:1156-1158; Wc from lag_hip_router_upload
  * of the [V,D] head), and with tok non-null tok[s] = the greedy pick of

@@ -28,7 +28,7 @@ EXPORTS = [
     "lag_hip_matmul_q4_g", "lag_hip_expert_q4_g", "lag_hip_moe_experts_g", "lag_hip_moe_group_g",
     "lag_hip_router_upload", "lag_hip_router_chain", "lag_hip_moe_forward", "lag_hip_moe_forward_noalloc",
     "lag_hip_moe_block", "lag_hip_route",
-    "lag_hip_last_groups", "lag_hip_rmsnorm", "lag_hip_head_argmax", "lag_hip_argmax", "lag_hip_set_grouped_kernel",
+    "lag_hip_last_groups", "lag_hip_rmsnorm", "lag_hip_moe_forward_rmsnorm", "lag_hip_head_argmax", "lag_hip_argmax", "lag_hip_set_grouped_kernel",
     "lag_hip_set_q4_mode",
     "lag_hip_alloc", "lag_hip_h2d", "lag_hip_d2h", "lag_hip_d2d", "lag_hip_memset",
     "lag_hip_graph_begin", "lag_hip_graph_end", "lag_hip_graph_launch", "lag_hip_graph_destroy", "lag_hip_sync",
@@ -109,6 +109,7 @@ def load_library(path=None):
     L.lag_hip_argmax.argtypes = [VP, C.c_int, C.c_int, VP]
     DP, WP = C.POINTER(LagHipMoeDesc), C.POINTER(LagHipMoeWeights)
     L.lag_hip_moe_forward.argtypes = [DP, WP, VP, VP, C.c_int]
+    L.lag_hip_moe_forward_rmsnorm.argtypes = [DP, WP, VP, C.c_float, VP, VP, C.c_int]
     L.lag_hip_moe_forward_noalloc.argtypes = [DP, WP, VP, VP, C.c_int]
     L.lag_hip_moe_block.argtypes = [DP, WP, F32P, F32P, C.c_int]
     L.lag_hip_route.argtypes = [DP, WP, VP, C.c_int, VP, VP, VP]
@@ -272,6 +273,12 @@ class Backend:
         for b in (lg, sel, w):
             b.free()
         return out
+
+    def moe_forward_rmsnorm(self, desc, weights, norm_w_dev, eps, xn_dev, h_dev, S):
+        """one stack layer: xn = rmsnorm(h), h += MoE(xn) (the norm inside the routing launch)"""
+        self.check(self.lib.lag_hip_moe_forward_rmsnorm(C.byref(desc), C.byref(weights), VP(int(norm_w_dev)),
+                                                        C.c_float(eps), VP(int(xn_dev)), VP(int(h_dev)), S),
+                   "lag_hip_moe_forward_rmsnorm")
 
     def rmsnorm(self, x_dev, w_dev, out_dev, S, D, eps):
         self.check(self.lib.lag_hip_rmsnorm(VP(int(x_dev)), VP(int(w_dev)), VP(int(out_dev)), S, D, C.c_float(eps)),

@@ -697,8 +697,10 @@ static int forward_idot(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const
 // counting sort, grouped gate_up, shared down, grouped down into slots, combine;
 // the grouped GEMMs on dot8 (passes of 2 tokens) or, for prefill-sized batches,
 // on the int8 MFMA (tiles of 64 tokens, the inputs as MFMA digits).
+// nw: x holds raw rows, normalised by the routing launch's router blocks (RMSNorm with
+// weights nw, eps) into xn, which every later launch reads in x's place
 static int forward(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const float *x, float *out, int S,
-                   const ScratchSrc &sc) {
+                   const ScratchSrc &sc, const float *nw = nullptr, float eps = 0.f, float *xn = nullptr) {
     if (!g_ok || fault_injected()) return -1;
     if (!desc_ok(d, w) || S <= 0) return fail_msg("moe_forward: unsupported descriptor/shape");
     if (g_q4_mode == 1 && d->gs == 0) return forward_idot(d, w, x, out, S, sc);
@@ -738,9 +740,10 @@ static int forward(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const floa
         if (sw_launch_stage_route(g_st, w->router, d->router_bf16, x, S, D, router_rows(d), w->logit_bias, f.logits, f.scores,
                                   d->route_act, mf ? nullptr : f.xl, f.xs, sh_in || (sh_fused && !sh_late) ? sg : nullptr, su,
                                   Is, f.shh, sh && !sh_in && !sh_fused ? f.shx : nullptr,
-                                  sh_fused && !sh_late ? f.shp : nullptr))
+                                  sh_fused && !sh_late ? f.shp : nullptr, nw, eps, xn))
             return fail_msg("routing stage launch");
     }
+    if (nw) x = xn;                      // the normalised rows from here on
     if (gated && gated_shared(d, w, x, S, f)) return -1;
     if (mf) {
         PROF("digits");
@@ -828,6 +831,22 @@ static int forward(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const floa
 
 extern "C" int lag_hip_moe_forward(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const float *x, float *out, int S) {
     return forward(d, w, x, out, S, kArena);
+}
+
+// a stack layer: xn = rmsnorm(h), h += MoE(xn) -- the norm inside the routing launch
+// when the routing stage runs (below 512 tokens), no shared expert reads x, and the
+// default contract is on; else the two launches of lag_hip_rmsnorm and the forward
+extern "C" int lag_hip_moe_forward_rmsnorm(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const float *norm_w,
+                                           float eps, float *xn, float *h, int S) {
+    if (!g_ok || !d || !w || !norm_w || !xn || !h || S <= 0) return -1;
+    if (!desc_ok(d, w)) return fail_msg("moe_forward_rmsnorm: unsupported descriptor/shape");
+    const bool fuse = d->shared_mode == LAG_HIP_SHARED_NONE && !router_tiled(S, d->hidden, router_rows(d)) &&
+                      !(g_q4_mode == 1 && d->gs == 0);
+    if (!fuse) {
+        if (lag_hip_rmsnorm(h, norm_w, xn, S, d->hidden, eps)) return -1;
+        return forward(d, w, xn, h, S, kArena);
+    }
+    return forward(d, w, h, h, S, kArena, norm_w, eps, xn);
 }
 
 // ------------------------------------------------- the allocation-free forward ----

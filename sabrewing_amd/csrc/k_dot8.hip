@@ -696,12 +696,13 @@ struct ShDownArgs { const uint16_t *Wd; const float *h; int Is, D; float *out; }
 
 // SK: the extra blocks are a batch's shared gate_up over column tiles of SK x 16 tokens
 // (sh_sk_block, inputs split from x), else the single token's (sh_glu_block)
-template <int BF16, int ONE, int SK>
+// NORM: the rows of x are raw, normalised by the router blocks (RMSNorm, R.nw)
+template <int BF16, int ONE, int SK, int NORM = 0>
 __global__ __launch_bounds__(SH_NT) void k_stage_route(RouterArgs R, int nbr, int S, ShGluArgs G, ShSkArgs Sk) {
     extern __shared__ __align__(16) float smem[];
     const int b = blockIdx.x;
     if (b < nbr * S) {
-        router_block<BF16, ONE>(R, b % nbr, b / nbr, nbr, smem);
+        router_block<BF16, ONE, NORM>(R, b % nbr, b / nbr, nbr, smem);
     } else if constexpr (SK > 0) {
         const int w = b - nbr * S, nrb = sh_sk_rows(1, Sk.O);
         sh_sk_block<1, SK, 1>(Sk, w % nrb, w / nrb, smem);
@@ -743,25 +744,29 @@ struct StageL {
     };
 };
 
-template <int ONE, int SK>
+template <int ONE, int SK, int NORM = 0>
 static void launch_stage_route(int bf16, dim3 grid, size_t lds, hipStream_t st, const RouterArgs &R, int nbr, int S,
                                const ShGluArgs &G, const ShSkArgs &Sk) {
-    if (bf16) SW_LAUNCH((k_stage_route<1, ONE, SK>), grid, dim3(SH_NT), lds, st, R, nbr, S, G, Sk);
-    else SW_LAUNCH((k_stage_route<0, ONE, SK>), grid, dim3(SH_NT), lds, st, R, nbr, S, G, Sk);
+    if (bf16) SW_LAUNCH((k_stage_route<1, ONE, SK, NORM>), grid, dim3(SH_NT), lds, st, R, nbr, S, G, Sk);
+    else SW_LAUNCH((k_stage_route<0, ONE, SK, NORM>), grid, dim3(SH_NT), lds, st, R, nbr, S, G, Sk);
 }
 
 // stage 1: router logits / scores and the limbs of x, and the shared
 // expert's gate_up when sg is non-null
 int sw_launch_stage_route(hipStream_t st, const void *Wc, int w_bf16, const float *x, int S, int D, int E,
                           const float *logit_bias, float *logits, float *scores, int route_act, sw_u32x4 *xl, float *xs,
-                          const uint16_t *sg, const uint16_t *su, int Is, float *sh_h, uint16_t *xp, uint16_t *sh_hp) {
+                          const uint16_t *sg, const uint16_t *su, int Is, float *sh_h, uint16_t *xp, uint16_t *sh_hp,
+                          const float *nw, float eps, float *xn) {
     if (D % 128 || E <= 0 || S <= 0 || route_act < 0 || route_act > SW_ROUTE_ACT_MAX || (!sw_act_softmax(route_act) && !scores)) return -1;
     if (xp && !sh_shape_ok(D)) return -1;
     const int one = router_one(S, E);
     const size_t rl = router_lds(D);
     if (rl > 65536 || D > 4 * RT_XB * (one ? SH_NT - 64 : SH_NT)) return -1;
     const int nbr = (E + router_epb(one, SH_NT) - 1) / router_epb(one, SH_NT);
-    const RouterArgs R = {Wc, x, D, E, logit_bias, logits, route_act, scores, xl, xs, xp};
+    // the RMSNorm of the rows (nw): not with the shared expert's blocks or parts, which
+    // read x as given
+    if (nw && (sg || xp || !xn)) return -1;
+    const RouterArgs R = {Wc, x, D, E, logit_bias, logits, route_act, scores, xl, xs, xp, nw, eps, xn};
     const ShGluArgs G = {sg, su, x, D, Is, sh_h};
     // the shared expert's gate_up: one token's blocks (h to sh_h), or with sh_hp a batch's
     // split-K blocks (h's parts to sh_hp)
@@ -774,7 +779,10 @@ int sw_launch_stage_route(hipStream_t st, const void *Wc, int w_bf16, const floa
     const size_t lds = lds_max(rl, !sg ? 0 : S == 1 ? sh_glu_lds(D) : sh_sk_lds(nc));
     if (lds > 65536) return -1;
     const int sk = sg && S > 1 ? nc : 0;
-    if (one) {
+    if (nw) {
+        if (one) launch_stage_route<1, 0, 1>(w_bf16, grid, lds, st, R, nbr, S, G, Sk);
+        else launch_stage_route<0, 0, 1>(w_bf16, grid, lds, st, R, nbr, S, G, Sk);
+    } else if (one) {
         if (sk) launch_stage_route<1, 1>(w_bf16, grid, lds, st, R, nbr, S, G, Sk);   // (ONE: S <= 4, so nc = 1)
         else launch_stage_route<1, 0>(w_bf16, grid, lds, st, R, nbr, S, G, Sk);
     } else if (sk == 1) {

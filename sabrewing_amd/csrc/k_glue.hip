@@ -8,39 +8,15 @@
 #include "sw_hip.h"
 #include "sw_gate.h"
 
-// out[r] = x[r] / rms(x[r]) * w (c/moe_math.h:58-62): the squares summed in
-// double (a product of two floats is exact in double), each thread over a
-// fixed stride in ascending order, then a fixed tree over the block; inv = 1 / sqrtf((float)(ss
-// / D) + eps); out = x * inv * w left to right.  The double sum differs from
-// the reference's sequential one only in its last bits, so the float it rounds
-// to is the same unless the two straddle a float rounding point.
-// A thread's values come in chunks of RN_CH loads issued together (a row of up to
-// RN_NT * RN_CH floats stays in registers for the output pass); past the row a
-// thread adds +0.0, which leaves its sum as it is.
-#define RN_NT 256
-#define RN_CH 16
+// out[r] = x[r] / rms(x[r]) * w (c/moe_math.h:58-62): the factor by rms_inv_block
+// (sw_gate.h), then out = x * inv * w left to right.
 __global__ __launch_bounds__(RN_NT) void k_rmsnorm(const float *__restrict__ x, const float *__restrict__ w,
                                                    float *__restrict__ out, int D, float eps) {
     __shared__ double part[RN_NT / 64];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x;
     const float *xr = x + (int64_t)blockIdx.x * D;
-    double ss = 0.0;
     float v[RN_CH];
-    for (int i0 = 0; i0 < D; i0 += RN_NT * RN_CH) {
-#pragma unroll
-        for (int k = 0; k < RN_CH; k++) {
-            const int i = i0 + tid + k * RN_NT;
-            v[k] = i < D ? xr[i] : 0.f;
-        }
-#pragma unroll
-        for (int k = 0; k < RN_CH; k++) ss += (double)v[k] * (double)v[k];
-    }
-    for (int o = 32; o; o >>= 1) ss += __shfl_xor(ss, o);
-    if (lane == 0) part[wave] = ss;
-    __syncthreads();
-    double tot = part[0];
-    for (int q = 1; q < RN_NT / 64; q++) tot += part[q];
-    const float inv = 1.f / sqrtf((float)(tot / D) + eps);
+    const float inv = rms_inv_block(xr, D, eps, part, v);
     float *orow = out + (int64_t)blockIdx.x * D;
     if (D <= RN_NT * RN_CH) {                          // the row is in registers
 #pragma unroll

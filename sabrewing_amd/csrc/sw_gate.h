@@ -323,4 +323,42 @@ __device__ __forceinline__ void limbs_group(float v, int i, sw_u32x4 *__restrict
     if (i == 0) *fdst = bad ? __builtin_nanf("") : ldexpf(1.0f, e - 3 * SW_NL);
 }
 
+
+// ---- RMSNorm (c/moe_math.h:58-62), the stack glue ----
+// The factor inv = 1 / sqrtf((float)(ss / D) + eps) of row xr, the squares summed in
+// double (a product of two floats is exact in double): threads 0..RN_NT-1 of the
+// block each over a fixed stride in ascending order (chunks of RN_CH loads issued
+// together; past the row a thread adds +0.0), then a fixed tree over the waves
+// (xor shuffles, then the RN_NT/64 wave sums left to right).  Threads beyond RN_NT
+// only meet the block barrier.  v keeps a thread's values of the last chunk (the
+// whole row when D <= RN_NT * RN_CH).  The double sum differs from the reference's
+// sequential one only in its last bits, so the float it rounds to is the same
+// unless the two straddle a float rounding point.  k_rmsnorm (k_glue.hip) and the
+// routing stage's normalising blocks (sw_router.h) both use this, so they give the
+// same bits.
+#define RN_NT 256
+#define RN_CH 16
+__device__ __forceinline__ float rms_inv_block(const float *__restrict__ xr, int D, float eps, double *part,
+                                               float (&v)[RN_CH]) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    double ss = 0.0;
+    if (tid < RN_NT) {
+        for (int i0 = 0; i0 < D; i0 += RN_NT * RN_CH) {
+#pragma unroll
+            for (int k = 0; k < RN_CH; k++) {
+                const int i = i0 + tid + k * RN_NT;
+                v[k] = i < D ? xr[i] : 0.f;
+            }
+#pragma unroll
+            for (int k = 0; k < RN_CH; k++) ss += (double)v[k] * (double)v[k];
+        }
+        for (int o = 32; o; o >>= 1) ss += __shfl_xor(ss, o);
+        if (lane == 0) part[wave] = ss;
+    }
+    __syncthreads();
+    double tot = part[0];
+    for (int q = 1; q < RN_NT / 64; q++) tot += part[q];
+    return 1.f / sqrtf((float)(tot / D) + eps);
+}
+
 #endif

@@ -301,7 +301,9 @@ int sw_launch_combine(hipStream_t st, const float *slots, const int *rowof, cons
 // fused decode stages (k_dot8.hip): stage 1 = router logits/scores/limbs
 // and the shared expert's gate_up (sg null: none; one token's h to sh_h, or a
 // batch's split-K blocks writing h's parts to sh_hp), with xp non-null also the
-// bf16 parts of x (sw_shared.h); stage 2 = routed gate_up (sel non-null: one
+// bf16 parts of x (sw_shared.h); with nw the rows of x are raw and the router
+// blocks apply the RMSNorm (weights nw, eps) as they stage them, writing the
+// normalised rows to xn (no shared expert then); stage 2 = routed gate_up (sel non-null: one
 // token's K picks, from sel or, with route_src, by a gate + top-k in every
 // block; else the groups g) + the shared expert's down (sd null: none; from
 // one token's h in sh_h, or a batch's from h's parts in sh_hp) or a batch's
@@ -309,7 +311,7 @@ int sw_launch_combine(hipStream_t st, const float *slots, const int *rowof, cons
 int sw_launch_stage_route(hipStream_t st, const void *Wc, int w_bf16, const float *x, int S, int D, int E,
                           const float *logit_bias, float *logits, float *scores, int route_act, sw_u32x4 *xl, float *xs,
                           const uint16_t *sg, const uint16_t *su, int Is, float *sh_h, uint16_t *xp = nullptr,
-                          uint16_t *sh_hp = nullptr);
+                          uint16_t *sh_hp = nullptr, const float *nw = nullptr, float eps = 0.f, float *xn = nullptr);
 int sw_launch_stage_experts(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, const float *xs, SwGroups g, int I, sw_u32x4 *hl,
                             float *hs, int *sel, int K, const float *route_src, int E, int act, const float *bias,
                             int use_bias, int norm, float *w, const uint16_t *sd, const float *sh_h, int S, int Is, int D,

@@ -35,6 +35,9 @@ struct RouterArgs {
     sw_u32x4 *xl;              // dot8 limbs of x, or null
     float *xs;
     uint16_t *xp;              // the bf16 parts of x for the shared expert's MFMA (sw_shared.h), or null
+    const float *nw;           // RMSNorm weight [D]: x is a raw row, normalised as it is staged
+    float eps;                 //   (rms_inv_block, then x * inv * w); null: x is used as given
+    float *xn;                 // with nw: the normalised rows [S, D], written by each token's first block
 };
 // experts per router block of nt threads: 4 (ONE: wave 0 runs the chains,
 // the other waves stage x -- the router spread over as many CUs as there are
@@ -45,7 +48,8 @@ __host__ inline int router_one(int S, int E) { return (int64_t)S * ((E + 3) / 4)
 
 // block bx (of nbx per token) of token s; smem: the dynamic LDS (router_lds
 // bytes)
-template <int BF16, int ONE>
+// NORM: x is a raw row, normalised as it is staged (R.nw, R.eps; R.xn written)
+template <int BF16, int ONE, int NORM = 0>
 __device__ __forceinline__ void router_block(const RouterArgs &R, int bx, int s, int nbx, float *smem) {
     constexpr int P = BF16 ? 8 : 4;
     __shared__ uint64_t tab[32];                     // expf table for the sigmoid / softplus scores
@@ -71,15 +75,28 @@ __device__ __forceinline__ void router_block(const RouterArgs &R, int bx, int s,
     // of unconditional loads (clamped; D <= 4 * RT_XB * xs), so no loop or branch join at
     // which the wait counts would drain slices in flight
     const int xs = ONE ? nt - 64 : nt, x0 = ONE ? 64 : 0, xt_id = tid - x0;
-    auto stage_x_load = [&](sw_f32x4 *xv) {
+    // (NORM: the norm weights come with x, the staged value is x * inv * w, and the first
+    // block of the token also writes it to R.xn)
+    const float *__restrict__ nwr = R.nw;
+    auto stage_x_load = [&](sw_f32x4 *xv, sw_f32x4 *wv) {
 #pragma unroll
         for (int u = 0; u < RT_XB; u++) xv[u] = *(const sw_f32x4 *)(xr + 4 * min(u * xs + xt_id, nx4 - 1));
+        if constexpr (NORM) {
+#pragma unroll
+            for (int u = 0; u < RT_XB; u++) wv[u] = *(const sw_f32x4 *)(nwr + 4 * min(u * xs + xt_id, nx4 - 1));
+        }
     };
-    auto stage_x_store = [&](const sw_f32x4 *xv) {
+    auto stage_x_store = [&](sw_f32x4 *xv, const sw_f32x4 *wv, float inv) {
+        float *xnr = NORM && R.xn && bx == 0 ? R.xn + (int64_t)s * D : nullptr;
 #pragma unroll
         for (int u = 0; u < RT_XB; u++) {
             const int i4 = u * xs + xt_id;
             if (i4 < nx4) {
+                if constexpr (NORM) {
+#pragma unroll
+                    for (int c = 0; c < 4; c++) xv[u][c] = xv[u][c] * inv * wv[u][c];
+                    if (xnr) *(sw_f32x4 *)(xnr + 4 * i4) = xv[u];
+                }
 #pragma unroll
                 for (int c = 0; c < 4; c++) {
                     const int k = 4 * i4 + c;
@@ -88,23 +105,44 @@ __device__ __forceinline__ void router_block(const RouterArgs &R, int bx, int s,
             }
         }
     };
+    __shared__ double rn_part[RN_NT / 64];
+    // the token's RMSNorm factor (every thread calls: the function holds a block barrier)
+    auto norm_inv = [&]() {
+        if constexpr (NORM) {
+            float v[RN_CH];
+            return rms_inv_block(xr, D, R.eps, rn_part, v);
+        } else {
+            return 1.f;
+        }
+    };
     const uint64_t tabv = sw_exp2f_tab[lane & 31];  // stored after the chain, where the scores need it
     sw_u32x4 ring[RT_PF];
-    if constexpr (ONE) {
+    if constexpr (ONE && NORM) {
+        sw_f32x4 xv[RT_XB], wv[RT_XB];
         if (wave == 0) {
 #pragma unroll
             for (int u = 0; u < RT_PF; u++) ring[u] = slice(u);
         } else {
-            sw_f32x4 xv[RT_XB];
-            stage_x_load(xv);
-            stage_x_store(xv);
+            stage_x_load(xv, wv);
+        }
+        const float inv = norm_inv();
+        if (wave != 0) stage_x_store(xv, wv, inv);
+    } else if constexpr (ONE) {
+        if (wave == 0) {
+#pragma unroll
+            for (int u = 0; u < RT_PF; u++) ring[u] = slice(u);
+        } else {
+            sw_f32x4 xv[RT_XB], wv[RT_XB];
+            stage_x_load(xv, wv);
+            stage_x_store(xv, wv, 1.f);
         }
     } else {
-        sw_f32x4 xv[RT_XB];
-        stage_x_load(xv);                             // x first, then every slice of the ring
+        sw_f32x4 xv[RT_XB], wv[RT_XB];
+        stage_x_load(xv, wv);                         // x first, then every slice of the ring
 #pragma unroll
         for (int u = 0; u < RT_PF; u++) ring[u] = slice(u);
-        stage_x_store(xv);
+        const float inv = norm_inv();
+        stage_x_store(xv, wv, inv);
     }
     __syncthreads();
     const float *xj = xt + j * ML;

@@ -60,13 +60,18 @@ class DeviceStack:
         self.bufs.append(b)
         return b
 
-    def step(self, h, xn, logits, tok, S):
-        """h [S, D] (device, updated in place), xn [S, D] scratch, logits [S, V], tok [S] int32"""
+    def step(self, h, xn, logits, tok, S, fused=True):
+        """h [S, D] (device, updated in place), xn [S, D] scratch, logits [S, V], tok [S] int32;
+        fused: each layer's RMSNorm inside its routing launch (lag_hip_moe_forward_rmsnorm,
+        the same bits as the separate rmsnorm + forward)"""
         be, D = self.be, self.cfg.D
         desc = desc_of(self.cfg)
         for l, dl in enumerate(self.layers):
-            be.rmsnorm(h, self.norms[l], xn, S, D, NORM_EPS)
-            be.moe_forward(desc, dl.weights(), xn, h, S)
+            if fused:
+                be.moe_forward_rmsnorm(desc, dl.weights(), self.norms[l], NORM_EPS, xn, h, S)
+            else:
+                be.rmsnorm(h, self.norms[l], xn, S, D, NORM_EPS)
+                be.moe_forward(desc, dl.weights(), xn, h, S)
         be.rmsnorm(h, self.final_norm, xn, S, D, NORM_EPS)
         be.head_argmax(self.head, True, xn, S, D, self.V, logits, tok)
 

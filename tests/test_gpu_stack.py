@@ -78,3 +78,33 @@ def test_small_stack(be, orc, S_):
     clear = margin > 20 * err
     assert clear.sum() >= max(1, S_ - 1), (margin, err)
     assert np.array_equal(tok[clear], wtok[clear])
+
+
+NORM_CASES = [(cf.scaled(cf.C5_LAYER, D=512, E=32, K=8, I=384), s) for s in (1, 4, 40)] + \
+             [(cf.scaled(cf.C2, D=512, E=32, K=6, I=256, Is=256, name="C2-small-shared"), 4)]
+
+
+@pytest.mark.parametrize("cfg,S_", NORM_CASES, ids=lambda v: getattr(v, "name", str(v)))
+def test_layer_norm_fused_bits(be, orc, cfg, S_):
+    """lag_hip_moe_forward_rmsnorm against lag_hip_rmsnorm then lag_hip_moe_forward: the
+    normalised rows and the updated residual bit for bit -- with the norm applied by the
+    router blocks as they stage x (one expert group per block at S <= 4, one token per
+    block at 40) and on the two-launch path a shared expert takes"""
+    from sabrewing_amd.backend import DeviceLayer, desc_of
+    L = synth.make_layer(orc, cfg, 91)
+    dl = DeviceLayer.from_host(be, cfg, L)
+    h0 = (synth.make_x(orc, cfg, 92, S_) * np.float32(3.0)).astype(np.float32)
+    w = norm_weights(orc, cfg, 93, 1)[0]
+    wd = be.upload(w)
+    h1, xn1 = be.upload(h0), be.alloc(S_ * cfg.D * 4)
+    be.rmsnorm(h1, wd, xn1, S_, cfg.D, NORM_EPS)
+    be.moe_forward(desc_of(cfg), dl.weights(), xn1, h1, S_)
+    h2, xn2 = be.upload(h0), be.alloc(S_ * cfg.D * 4)
+    be.moe_forward_rmsnorm(desc_of(cfg), dl.weights(), wd, NORM_EPS, xn2, h2, S_)
+    got = [be.d2h(b, h0.shape, np.float32) for b in (h1, xn1, h2, xn2)]
+    for b in (wd, h1, xn1, h2, xn2):
+        b.free()
+    dl.free()
+    assert np.array_equal(got[3].view(np.uint32), got[1].view(np.uint32))      # xn
+    assert np.array_equal(got[2].view(np.uint32), got[0].view(np.uint32))      # h
+    assert np.array_equal(got[1].view(np.uint32), orc.rmsnorm_rows(h0, w, NORM_EPS).view(np.uint32))
