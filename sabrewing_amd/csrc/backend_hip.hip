@@ -723,7 +723,8 @@ static int forward(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const floa
     const bool in_experts = E <= 256 && S == 1 && (d->route_act == 1 || sw_act_scores(d->route_act));
     // S == 1: the shared expert's gate_up and down run as extra blocks of stages 1 and 2
     // (they fill the chip while the routed chain waits on its router and top-k);
-    // S > 1: as kernels of their own over token tiles (the same arithmetic per token)
+    // S > 1: as extra blocks of other launches (below) or, for prefill-sized batches, as
+    // kernels of their own over token tiles (the same arithmetic per token either way)
     const bool sh_in = sh && S == 1;
     const bool mf = S > 1 && use_mfma(T, E, D, I);
     // a decode-sized batch on the dot8 kernels: the shared expert's split-K blocks ride in
