@@ -167,16 +167,22 @@ __device__ __forceinline__ void bucket_block(const int *__restrict__ sel, int T,
     __syncthreads();
     for (int p = tid; p < T; p += BK_THREADS) atomicAdd(&cnt[sel[p]], 1);
     __syncthreads();
-    // exclusive scans of cnt (packed offsets), of cnt > 0 (group index) and of
-    // the passes ceil(cnt / tt) (pass list offsets)
-    for (int i = tid; i < E; i += BK_THREADS) { sa[i] = cnt[i]; sb[i] = cnt[i] > 0; sp[i] = (cnt[i] + tt - 1) / tt; }
-    __syncthreads();
-    for (int off = 1; off < E; off <<= 1) {
-        int va = 0, vb = 0, vp = 0;
-        if (tid < E && tid >= off) { va = sa[tid - off]; vb = sb[tid - off]; vp = sp[tid - off]; }
+    // inclusive scans of cnt (packed offsets), of cnt > 0 (group index) and of the
+    // passes ceil(cnt / tt) (pass list offsets), expert tid by thread tid: a shuffle
+    // scan within each wave, then the totals of the earlier waves (integer sums, so the
+    // order of the additions does not matter)
+    {
+        __shared__ int wta[BK_THREADS / 64], wtb[BK_THREADS / 64], wtp[BK_THREADS / 64];
+        const int c0 = tid < E ? cnt[tid] : 0;
+        int va = c0, vb = c0 > 0, vp = (c0 + tt - 1) / tt;
+        for (int o = 1; o < 64; o <<= 1) {
+            const int ta = __shfl_up(va, o), tb = __shfl_up(vb, o), tp = __shfl_up(vp, o);
+            if (lane >= o) { va += ta; vb += tb; vp += tp; }
+        }
+        if (lane == 63) { wta[wave] = va; wtb[wave] = vb; wtp[wave] = vp; }
         __syncthreads();
-        if (tid < E && tid >= off) { sa[tid] += va; sb[tid] += vb; sp[tid] += vp; }
-        __syncthreads();
+        for (int w = 0; w < wave; w++) { va += wta[w]; vb += wtb[w]; vp += wtp[w]; }
+        if (tid < E) { sa[tid] = va; sb[tid] = vb; sp[tid] = vp; }
     }
     if (tid < E) {
         const int c = cnt[tid];
