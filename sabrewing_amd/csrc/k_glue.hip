@@ -33,19 +33,41 @@ __global__ __launch_bounds__(RN_NT) void k_rmsnorm(const float *__restrict__ x, 
 // from best = 0 ends on (c/laguna.c:1159): 0 when v[0] is NaN (nothing
 // compares greater than it), else the lowest index of the largest non-NaN
 // value (-0.0 and +0.0 equal).  Each thread takes the largest word (order
-// bits of v + 0.0, ~index) of its values; the block takes the largest word.
+// bits of v + 0.0, ~index) of its values; the block takes the largest word
+// (a maximum: the same word whatever order the values are taken in).  Rows
+// of a multiple of 4 values are read as float4, AM_U loads per thread in
+// flight before any is used.
 #define AM_NT 1024
+#define AM_U 8
 __global__ __launch_bounds__(AM_NT) void k_argmax(const float *__restrict__ logits, int V, int *__restrict__ tok) {
     __shared__ unsigned long long part[AM_NT / 64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float *v = logits + (int64_t)blockIdx.x * V;
     unsigned long long best = 0ull;
-    for (int i = tid; i < V; i += AM_NT) {
-        const float f = v[i];
+    auto take = [&](float f, int i) {
         if (f == f) {
             const unsigned long long k = ((unsigned long long)ord_f32(f + 0.0f) << 32) | (0xFFFFFFFFu - (uint32_t)i);
             best = k > best ? k : best;
         }
+    };
+    if ((V & 3) == 0) {
+        const sw_f32x4 *v4 = (const sw_f32x4 *)v;
+        const int n4 = V / 4;
+        for (int i0 = tid; i0 < n4; i0 += AM_NT * AM_U) {
+            sw_f32x4 r[AM_U];
+#pragma unroll
+            for (int u = 0; u < AM_U; u++) r[u] = v4[min(i0 + u * AM_NT, n4 - 1)];
+#pragma unroll
+            for (int u = 0; u < AM_U; u++) {
+                const int i = i0 + u * AM_NT;
+                if (i < n4) {
+#pragma unroll
+                    for (int c = 0; c < 4; c++) take(r[u][c], 4 * i + c);
+                }
+            }
+        }
+    } else {
+        for (int i = tid; i < V; i += AM_NT) take(v[i], i);
     }
     for (int o = 32; o; o >>= 1) {
         const unsigned long long t = __shfl_xor(best, o);

@@ -59,34 +59,38 @@ __global__ __launch_bounds__(512) void k_router_logits(RouterArgs R) {
 
 // a 1-D grid of (expert block, token tile) pairs, dealt so that an XCD runs whole
 // token tiles (all their expert blocks), whose x then comes from its L2
-template <int BF16, int TT, int NW>
+template <int BF16, int TT, int NW, int GPW>
 __global__ __launch_bounds__(64 * NW) void k_router_tiles(RouterArgs R, int S, int nbx) {
     const int w = sw_xcd_work((int)blockIdx.x, (int)gridDim.x);
-    router_tile_block<BF16, TT, NW>(R, S, w % nbx, w / nbx);
+    router_tile_block<BF16, TT, NW, GPW>(R, S, w % nbx, w / nbx);
 }
 
-// token tile and waves per block (4 experts each, sharing the tile's x in LDS): 16 tokens
-// on 4 waves for prefill-sized batches (C4: 113 us against 122 on 8 waves), else 8 tokens
-// on 8 waves (a head-sized router: 32 rows per x tile; C5 head 75 us against 92 on one wave)
-static void router_tile_shape(int S, int &tt, int &nw) {
-    if (S >= 512) { tt = 16; nw = 4; } else { tt = 8; nw = 8; }
+// token tile, waves per block and groups of 4 experts per wave.  bf16 weights: 8 waves of
+// two groups each (64 experts per block sharing the tile's x in LDS; LDS reads per weight
+// element halve against one group: C4 router 93 us against 111, C5 head 54 against 73), 16
+// tokens for prefill-sized batches, else 8.  f32 weights keep one group per wave (two
+// groups take 158-181 VGPRs): 16 tokens on 4 waves for prefill, else 8 tokens on 8 waves.
+static void router_tile_shape(int S, int bf16, int &tt, int &nw, int &gpw) {
+    tt = S >= 512 ? 16 : 8;
+    nw = bf16 || S < 512 ? 8 : 4;
+    gpw = bf16 ? 2 : 1;
 }
 
 int sw_launch_router_tiles(hipStream_t st, const void *Wc, int w_bf16, const float *x, int S, int D, int E,
                            const float *logit_bias, float *logits, float *scores, int route_act) {
     if (D % RT_CK || D > 65536 || E <= 0 || S <= 0 || route_act < 0 || route_act > SW_ROUTE_ACT_MAX) return -1;
     if ((int64_t)((E + 3) / 4) * 4 * D * (w_bf16 ? 2 : 4) > 0xFFFFFFFFll) return -1;
-    int tt, nw;
-    router_tile_shape(S, tt, nw);
+    int tt, nw, gpw;
+    router_tile_shape(S, w_bf16, tt, nw, gpw);
     const RouterArgs R = {Wc, x, D, E, logit_bias, logits, route_act, scores, nullptr, nullptr, nullptr};
     const int ng4 = (E + 3) / 4;
-    const int nbx = (ng4 + nw - 1) / nw;
+    const int nbx = (ng4 + nw * gpw - 1) / (nw * gpw);
     const dim3 grid((unsigned)((int64_t)nbx * ((S + tt - 1) / tt)));
-#define SW_RT(B, T, W) SW_LAUNCH((k_router_tiles<B, T, W>), grid, dim3(64 * W), 0, st, R, S, nbx)
+#define SW_RT(B, T, W, G) SW_LAUNCH((k_router_tiles<B, T, W, G>), grid, dim3(64 * W), 0, st, R, S, nbx)
     if (w_bf16) {
-        if (tt == 16) SW_RT(1, 16, 4); else SW_RT(1, 8, 8);
+        if (tt == 16) SW_RT(1, 16, 8, 2); else SW_RT(1, 8, 8, 2);
     } else {
-        if (tt == 16) SW_RT(0, 16, 4); else SW_RT(0, 8, 8);
+        if (tt == 16) SW_RT(0, 16, 4, 1); else SW_RT(0, 8, 8, 1);
     }
 #undef SW_RT
     return launch_err();

@@ -228,20 +228,23 @@ __device__ __forceinline__ void router_block(const RouterArgs &R, int bx, int s,
 __host__ inline size_t router_lds(int D) { return (size_t)16 * (D / 16 + 4) * 4; }
 
 // The same logits and scores for a tile of TT tokens per pass over the
-// weights: wave w of block (bx, by) runs the 16 chains of each of the four
-// experts of group bx * NW + w, for tokens TT by .. TT by + TT - 1 (lane
-// 16 q + j keeps chain j of expert 4 (bx NW + w) + q, one accumulator per
-// token), so a router slice is loaded once per TT tokens instead of once per
-// token.  x goes through LDS in chunks of 256 inputs (16 elements of every
-// chain), staged transposed, xt[t][j][m] = x[t][256 c + 16 m + j] (rows of
-// 20 floats: the 16 lanes of a row read 16 bytes each from distinct banks);
-// the next chunk's x is loaded into registers while this one is used, and
-// the slices of RT_TCH chunks of each lane's chain are in flight.  Every chain is the same
-// fma sequence as router_block's, so the results are the same bits.
+// weights: wave w of block (bx, by) runs the 16 chains of each of the 4 GPW
+// experts of groups GPW (bx NW + w) .. + GPW - 1, for tokens TT by .. TT by +
+// TT - 1 (lane 16 q + j keeps chain j of expert q of each of its groups, one
+// accumulator per group and token), so a router slice is loaded once per TT
+// tokens instead of once per token, and each x value read from LDS feeds
+// the chains of GPW experts (LDS reads are the limit: TT x values of 4 bytes
+// per weight element and group).  x goes through LDS in chunks of 256 inputs
+// (16 elements of every chain), staged transposed, xt[t][j][m] = x[t][256 c +
+// 16 m + j] (rows of 20 floats: the 16 lanes of a row read 16 bytes each from
+// distinct banks); the next chunk's x is loaded into registers while this one
+// is used, and the slices of RT_TCH chunks of each lane's chains are in
+// flight.  Every chain is the same fma sequence as router_block's, so the
+// results are the same bits.
 #define RT_CK 256
 #define RT_XS 20
 #define RT_TCH 3           // chunks of router slices in flight
-template <int BF16, int TT, int NW>
+template <int BF16, int TT, int NW, int GPW>
 __device__ __forceinline__ void router_tile_block(const RouterArgs &R, int S, int bx, int by) {
     constexpr int P = BF16 ? 8 : 4, SPC = 16 / P, NTH = 64 * NW;
     constexpr int XR4 = TT * RT_CK / 4 / NTH;          // float4 of x per thread per chunk
@@ -250,13 +253,15 @@ __device__ __forceinline__ void router_tile_block(const RouterArgs &R, int S, in
     __shared__ uint64_t tab[32];
     const int D = R.D, E = R.E, act = R.act;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, j = lane & 15;
-    const int eg = bx * NW + wave, e = eg * 4 + (lane >> 4);
-    const int ng4 = (E + 3) / 4, egc = eg < ng4 ? eg : ng4 - 1;
+    const int eg0 = (bx * NW + wave) * GPW;            // the wave's first group of 4 experts
+    const int ng4 = (E + 3) / 4;
     const int s0 = by * TT, nt = min(TT, S - s0);
     const int M = D / 16, NQ = M / P, NCH = D / RT_CK;
     const sw_rsrc rw = sw_make_rsrc(R.Wc, (uint32_t)ng4 * 4u * (uint32_t)D * (BF16 ? 2u : 4u));
-    const uint32_t voff = ((uint32_t)egc * NQ * 64 + lane) * 16;
-    auto slice = [&](int q) { return sw_ld16(rw, voff, (uint32_t)min(q, NQ - 1) * 1024u); };
+    uint32_t voff[GPW];                                // groups past the last clamp to it
+#pragma unroll
+    for (int g = 0; g < GPW; g++) voff[g] = ((uint32_t)min(eg0 + g, ng4 - 1) * NQ * 64 + lane) * 16;
+    auto slice = [&](int g, int q) { return sw_ld16(rw, voff[g], (uint32_t)min(q, NQ - 1) * 1024u); };
     // x float4 f of a chunk: token f / 64, inputs 4 (f % 64) .. +3 of the chunk
     auto xload = [&](int c, sw_f32x4 *xr) {
 #pragma unroll
@@ -277,33 +282,41 @@ __device__ __forceinline__ void router_tile_block(const RouterArgs &R, int S, in
             }
         }
     };
-    float acc[TT];
+    float acc[GPW][TT];
 #pragma unroll
-    for (int t = 0; t < TT; t++) acc[t] = 0.f;
-    // the slices of chunks c, c + 1 and c + 2 in flight (RT_TCH chunks ahead of their use)
-    sw_u32x4 wc[RT_TCH][SPC];
+    for (int g = 0; g < GPW; g++)
+#pragma unroll
+        for (int t = 0; t < TT; t++) acc[g][t] = 0.f;
+    // the slices of chunks c .. c + RT_TCH - 1 in flight (RT_TCH chunks ahead of their use)
+    sw_u32x4 wc[RT_TCH][GPW][SPC];
 #pragma unroll
     for (int u = 0; u < RT_TCH; u++)
 #pragma unroll
-        for (int sl = 0; sl < SPC; sl++) wc[u][sl] = slice(u * SPC + sl);
+        for (int g = 0; g < GPW; g++)
+#pragma unroll
+            for (int sl = 0; sl < SPC; sl++) wc[u][g][sl] = slice(g, u * SPC + sl);
     sw_f32x4 xr[XR4];
     xload(0, xr);
-    // element p of slice sl of the chunk against the tile's tokens: the slice widened once,
-    // then the tokens' x read from LDS four tokens at a time (so the reads in flight stay few)
-    auto use = [&](int sl, const sw_u32x4 &w) {
+    // element p of slice sl of the chunk against the tile's tokens: the slices widened once,
+    // then each token's x read from LDS once for the chains of every group (four tokens at a
+    // time, so the reads in flight stay few)
+    auto use = [&](int sl, const sw_u32x4 (&w)[GPW]) {
         const float *xj = xt + j * RT_XS + sl * P;
-        float wf[P];
-        if constexpr (BF16) {
+        float wf[GPW][P];
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-                wf[2 * q] = __builtin_bit_cast(float, w[q] << 16);
-                wf[2 * q + 1] = __builtin_bit_cast(float, w[q] & 0xFFFF0000u);
+        for (int g = 0; g < GPW; g++) {
+            if constexpr (BF16) {
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    wf[g][2 * q] = __builtin_bit_cast(float, w[g][q] << 16);
+                    wf[g][2 * q + 1] = __builtin_bit_cast(float, w[g][q] & 0xFFFF0000u);
+                }
+            } else {
+                // the whole vector is cast (a bit_cast of one element lvalue reads element 0)
+                const sw_f32x4 wv = __builtin_bit_cast(sw_f32x4, w[g]);
+#pragma unroll
+                for (int q = 0; q < 4; q++) wf[g][q] = wv[q];
             }
-        } else {
-            // the whole vector is cast (a bit_cast of one element lvalue reads element 0)
-            const sw_f32x4 wv = __builtin_bit_cast(sw_f32x4, w);
-#pragma unroll
-            for (int q = 0; q < 4; q++) wf[q] = wv[q];
         }
 #pragma unroll
         for (int t = 0; t < TT; t++) {
@@ -311,10 +324,13 @@ __device__ __forceinline__ void router_tile_block(const RouterArgs &R, int S, in
 #pragma unroll
             for (int h = 0; h < P / 4; h++) {
                 const sw_f32x4 xa = *(const sw_f32x4 *)(xp + 4 * h);
-                acc[t] = __builtin_fmaf(xa.x, wf[4 * h], acc[t]);
-                acc[t] = __builtin_fmaf(xa.y, wf[4 * h + 1], acc[t]);
-                acc[t] = __builtin_fmaf(xa.z, wf[4 * h + 2], acc[t]);
-                acc[t] = __builtin_fmaf(xa.w, wf[4 * h + 3], acc[t]);
+#pragma unroll
+                for (int g = 0; g < GPW; g++) {
+                    acc[g][t] = __builtin_fmaf(xa.x, wf[g][4 * h], acc[g][t]);
+                    acc[g][t] = __builtin_fmaf(xa.y, wf[g][4 * h + 1], acc[g][t]);
+                    acc[g][t] = __builtin_fmaf(xa.z, wf[g][4 * h + 2], acc[g][t]);
+                    acc[g][t] = __builtin_fmaf(xa.w, wf[g][4 * h + 3], acc[g][t]);
+                }
             }
             if ((t & 3) == 3) __builtin_amdgcn_sched_barrier(0);
         }
@@ -325,31 +341,44 @@ __device__ __forceinline__ void router_tile_block(const RouterArgs &R, int S, in
         xload(min(c + 1, NCH - 1), xr);
         __syncthreads();
 #pragma unroll
-        for (int sl = 0; sl < SPC; sl++) use(sl, wc[0][sl]);
+        for (int sl = 0; sl < SPC; sl++) {
+            sw_u32x4 w[GPW];
+#pragma unroll
+            for (int g = 0; g < GPW; g++) w[g] = wc[0][g][sl];
+            use(sl, w);
+        }
 #pragma unroll
         for (int u = 0; u + 1 < RT_TCH; u++)
 #pragma unroll
-            for (int sl = 0; sl < SPC; sl++) wc[u][sl] = wc[u + 1][sl];
+            for (int g = 0; g < GPW; g++)
 #pragma unroll
-        for (int sl = 0; sl < SPC; sl++) wc[RT_TCH - 1][sl] = slice((c + RT_TCH) * SPC + sl);
+                for (int sl = 0; sl < SPC; sl++) wc[u][g][sl] = wc[u + 1][g][sl];
+#pragma unroll
+        for (int g = 0; g < GPW; g++)
+#pragma unroll
+            for (int sl = 0; sl < SPC; sl++) wc[RT_TCH - 1][g][sl] = slice(g, (c + RT_TCH) * SPC + sl);
     }
     tab[lane & 31] = sw_exp2f_tab[lane & 31];         // every wave writes the whole table (equal values)
     __syncthreads();
 #pragma unroll
-    for (int t = 0; t < TT; t++) {
-        float v = acc[t];
-        v = v + __shfl_down(v, 8, 16);
-        v = v + __shfl_down(v, 4, 16);
-        v = v + __shfl_down(v, 2, 16);
-        v = v + __shfl_down(v, 1, 16);
-        if (j == 0 && e < E && t < nt) {
-            const int64_t s = s0 + t;
-            if (R.lbias) v = v + R.lbias[e];
-            R.logits[s * E + e] = v;
-            if (!sw_act_softmax(act) && R.scores)
-                R.scores[s * E + e] = act == 2   ? sw_softplus_ref_t(v, tab)
-                                      : act == 5 ? sw_sqrt_rn(sw_softplus_ref_t(v, tab))
-                                                 : sw_sigmoid_ref_t(v, tab);
+    for (int g = 0; g < GPW; g++) {
+        const int e = (eg0 + g) * 4 + (lane >> 4);
+#pragma unroll
+        for (int t = 0; t < TT; t++) {
+            float v = acc[g][t];
+            v = v + __shfl_down(v, 8, 16);
+            v = v + __shfl_down(v, 4, 16);
+            v = v + __shfl_down(v, 2, 16);
+            v = v + __shfl_down(v, 1, 16);
+            if (j == 0 && e < E && t < nt) {
+                const int64_t s = s0 + t;
+                if (R.lbias) v = v + R.lbias[e];
+                R.logits[s * E + e] = v;
+                if (!sw_act_softmax(act) && R.scores)
+                    R.scores[s * E + e] = act == 2   ? sw_softplus_ref_t(v, tab)
+                                          : act == 5 ? sw_sqrt_rn(sw_softplus_ref_t(v, tab))
+                                                     : sw_sigmoid_ref_t(v, tab);
+            }
         }
     }
 }

@@ -52,6 +52,50 @@ def test_head_logits_and_pick(be, orc):
         b.free()
 
 
+@pytest.mark.parametrize("bf16", [True, False])
+@pytest.mark.parametrize("S,V", [(2, 4099), (8, 4132), (13, 5000), (600, 1026)])
+def test_tiled_head_bits(be, orc, bf16, S, V):
+    """Heads of >= 4096 rows, and any head at >= 512 tokens, take the token-tiled router
+    (tiles of 8 or 16 tokens, two groups of 4 rows per wave for bf16 weights): logits
+    bit-exact for ragged token tiles and row counts whose last block holds fewer groups
+    than a block's waves take (the clamped loads), the pick of every row (V % 4 != 0: the
+    argmax's scalar path)."""
+    D = 512
+    rng = np.random.default_rng(S * 7 + V)
+    Wf = (rng.standard_normal((V, D)) * 0.02).astype(np.float32)
+    W = (Wf.view(np.uint32) >> 16).astype(np.uint16) if bf16 else Wf
+    x = rng.standard_normal((S, D)).astype(np.float32)
+    Wc = be.router_upload(W, bf16)
+    xd, ld, td = be.upload(x), be.alloc(S * V * 4), be.alloc(S * 4)
+    be.head_argmax(Wc, bf16, xd, S, D, V, ld, td)
+    logits = be.d2h(ld, (S, V), np.float32)
+    tok = be.d2h(td, (S,), np.int32)
+    want = orc.matmul_bf16(x, W) if bf16 else orc.matmul_f32(x, W)
+    assert np.array_equal(logits.view(np.uint32), want.view(np.uint32))
+    assert np.array_equal(tok, orc.argmax_rows(want))
+    for b in (Wc, xd, ld, td):
+        b.free()
+
+
+@pytest.mark.parametrize("V", [40004, 40001])
+def test_pick_long_rows(be, orc, V):
+    """Rows longer than one pass of the argmax block (32768 values as float4, 1024 as
+    scalars): ties between passes go to the lowest index, -0.0 == +0.0 across passes, a
+    maximum in the last partial float4 or scalar pass."""
+    rows = np.full((4, V), -3.0, np.float32)
+    rows[0, [33000, 100, 39999]] = 7.0                   # tie across passes
+    rows[1, V - 1] = 1.0                                 # the last value
+    rows[2, :] = -1.0; rows[2, 35000] = -0.0; rows[2, 20] = 0.0
+    rows[3, 0] = 2.0; rows[3, 32768] = np.nan; rows[3, 32769] = 2.5
+    want = [100, V - 1, 20, 32769]
+    assert np.array_equal(orc.argmax_rows(rows), want)
+    ld, td = be.upload(rows), be.alloc(4 * 4)
+    be.argmax(ld, 4, V, td)
+    assert np.array_equal(be.d2h(td, (4,), np.int32), want)
+    for b in (ld, td):
+        b.free()
+
+
 @pytest.mark.parametrize("S_", [1, 4])
 def test_small_stack(be, orc, S_):
     cfg = cf.scaled(cf.C5_LAYER, D=512, E=32, K=8, I=384)
