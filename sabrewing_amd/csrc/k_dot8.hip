@@ -142,8 +142,9 @@ static int dg_pf_glu(int K) { const int n = 32 / dg_rps(run_lanes(K / RG), 32, D
 static int dg_pf_rows(int K) { const int n = 64 / dg_rps(run_lanes(K / RG), 64, 256); return n < 8 ? n : 8; }
 
 // block (bx = group or rank, by = set of RO outputs: 32, or up to 128 for groups --
-// fewer, longer blocks per weight byte); runs: the dynamic LDS, [TT][2 RO][NC] floats
-template <int PF, int PICK, int NP, int TT, int C16, int RO, int PT = 0>
+// fewer, longer blocks per weight byte); runs: the dynamic LDS, [TT][2 RO][NC] floats;
+// NTL: a block whose pass is its group's only one loads its weights non-temporal
+template <int PF, int PICK, int NP, int TT, int C16, int RO, int PT = 0, int NTL = 1>
 __device__ __forceinline__ void dot8_glu_block(const Dot8GluArgs &A, int bx, int by, float *runs) {
     static_assert(PT == 0 || PICK == 0, "per-group tensors come with groups");
     static_assert(PICK == 0 || TT == 1, "picks are of one token");
@@ -164,7 +165,7 @@ __device__ __forceinline__ void dot8_glu_block(const Dot8GluArgs &A, int bx, int
     const int ng = W.gs > 0 ? K / W.gs : 1;
     const int sg = W.gs > 0 ? (g * RG) >> A.gsh : 0;
     const uint32_t rb = (uint32_t)K / 2, sb = (uint32_t)ng * 4;
-    int e, beg, tb, tend;
+    int e, beg, tb, tend, gcnt = 0;
     sw_u32x4 X[TT][SW_NL];
     float xf[TT];
     if constexpr (PICK) {                             // one token: rank bx of its picks
@@ -190,8 +191,9 @@ __device__ __forceinline__ void dot8_glu_block(const Dot8GluArgs &A, int bx, int
             e = A.sel[bx];
         }
     } else {
-        if (!grp_work(grp, bx, TT, e, beg, tb, tend)) return;
+        if (!grp_work(grp, bx, TT, e, beg, tb, tend, &gcnt)) return;
     }
+    const bool once = PICK || (tb == 0 && gcnt <= TT);
     // gate rows through (rq, rs), up rows through (rq2, rs2): one [E*2I] tensor, or the
     // group's own gate and up tensors (PT)
     sw_rsrc rq, rs, rq2, rs2;
@@ -216,72 +218,83 @@ __device__ __forceinline__ void dot8_glu_block(const Dot8GluArgs &A, int bx, int
     auto ws = [&](int s) -> const sw_rsrc & { return s < NSH ? rs : rs2; };
     const int NS = 2 * NSH;
     float *myruns = runs + (roc * NSH) * NC + c;      // this lane's run sum of step s: myruns[(t*64 + h*32 + j) * NC]
-    for (int t0 = tb; t0 < tend; t0 += TT) {
-        const int nt = min(TT, tend - t0);
-        if constexpr (PICK == 0) {
-#pragma unroll
-            for (int t = 0; t < TT; t++) {
-                const int pr = beg + t0 + (t < nt ? t : 0);
-                const int64_t tok = grp.grow ? grp.grow[pr] : pr;
-#pragma unroll
-                for (int l = 0; l < SW_NL; l++) X[t][l] = xl[(tok * G + g) * SW_NL + l];
-                xf[t] = xs[tok * G + g];
-            }
-        }
-        sw_u32x4 ra[PF];
-        float sa[PF];
-#pragma unroll
-        for (int u = 0; u < PF; u++) {
-            ra[u] = sw_ld16(wq(u), voq, srow(u) * rb);
-            sa[u] = sw_ld4f(ws(u), vos, srow(u) * sb);
-        }
-        auto step = [&](int s, int u, bool refill) {
-            const sw_u32x4 w = ra[u] ^ 0x88888888u;
-            const float sc = W.gs > 0 ? sa[u] : 1.0f;
-            if (refill) {
-                ra[u] = sw_ld16(wq(s + PF), voq, srow(s + PF) * rb);
-                sa[u] = sw_ld4f(ws(s + PF), vos, srow(s + PF) * sb);
-                __builtin_amdgcn_sched_barrier(0);
-            }
-            const int urow = s < NSH ? s : RO + s - NSH;                 // local row minus roc * NSH
-#pragma unroll
-            for (int t = 0; t < TT; t++) {
-                if (t < nt) {                          // uniform over the block
-                    const float p = row_term<C16>((float)dot8_group(w, X[t]) * (sc * xf[t]), gv, CH);
-                    if (lead) myruns[(t * 2 * RO + urow) * NC] = p;
+    // weight loads non-temporal (the nt policy) when this pass is the only one over the
+    // block's weights; cached when other passes re-read them
+    auto passes = [&](auto PC) {
+        constexpr int POL = decltype(PC)::v;
+        for (int t0 = tb; t0 < tend; t0 += TT) {
+            const int nt = min(TT, tend - t0);
+            if constexpr (PICK == 0) {
+    #pragma unroll
+                for (int t = 0; t < TT; t++) {
+                    const int pr = beg + t0 + (t < nt ? t : 0);
+                    const int64_t tok = grp.grow ? grp.grow[pr] : pr;
+    #pragma unroll
+                    for (int l = 0; l < SW_NL; l++) X[t][l] = xl[(tok * G + g) * SW_NL + l];
+                    xf[t] = xs[tok * G + g];
                 }
             }
-        };
-        int s0 = 0;
-        for (; s0 + PF < NS; s0 += PF) {
-#pragma unroll
-            for (int u = 0; u < PF; u++) step(s0 + u, u, true);
-        }
-#pragma unroll
-        for (int u = 0; u < PF; u++) step(s0 + u, u, false);
-        __syncthreads();
-        // token t of the tile by the threads RO t .. RO t + RO - 1 (a half-wave per limb group)
-        const int t = tid / RO, i = tid - t * RO;
-        if (t < nt) {
-            const float *rg = runs + (t * 2 * RO + i) * NC, *ru = runs + (t * 2 * RO + RO + i) * NC;
-            float yg = rg[0], yu = ru[0];
-            for (int cc = 1; cc < NC; cc++) { yg = yg + rg[cc]; yu = yu + ru[cc]; }
-            if (W.gs <= 0) {                            // per-row scales after the sum
-                if constexpr (PT) {
-                    yg = yg * A.tab[e].gs[i0 + i];
-                    yu = yu * A.tab[e].us[i0 + i];
-                } else {
-                    yg = yg * W.s[(int64_t)e * (2 * I) + i0 + i];
-                    yu = yu * W.s[(int64_t)e * (2 * I) + I + i0 + i];
-                }
+            sw_u32x4 ra[PF];
+            float sa[PF];
+    #pragma unroll
+            for (int u = 0; u < PF; u++) {
+                ra[u] = sw_ld16<POL>(wq(u), voq, srow(u) * rb);
+                sa[u] = sw_ld4f<POL>(ws(u), vos, srow(u) * sb);
             }
-            const float h = (yg / (1.0f + expf(-yg))) * yu;
-            // every 32 of the block's outputs are one limb group of the down projection's input
-            const int GI = I / RG, gi_out = (i0 + i) / RG;
-            const int64_t prow = beg + t0 + t;
-            limbs_group(h, i & 31, A.hl + (prow * GI + gi_out) * SW_NL, A.hs + prow * GI + gi_out);
+            auto step = [&](int s, int u, bool refill) {
+                const sw_u32x4 w = ra[u] ^ 0x88888888u;
+                const float sc = W.gs > 0 ? sa[u] : 1.0f;
+                if (refill) {
+                    ra[u] = sw_ld16<POL>(wq(s + PF), voq, srow(s + PF) * rb);
+                    sa[u] = sw_ld4f<POL>(ws(s + PF), vos, srow(s + PF) * sb);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                const int urow = s < NSH ? s : RO + s - NSH;                 // local row minus roc * NSH
+    #pragma unroll
+                for (int t = 0; t < TT; t++) {
+                    if (t < nt) {                          // uniform over the block
+                        const float p = row_term<C16>((float)dot8_group(w, X[t]) * (sc * xf[t]), gv, CH);
+                        if (lead) myruns[(t * 2 * RO + urow) * NC] = p;
+                    }
+                }
+            };
+            int s0 = 0;
+            for (; s0 + PF < NS; s0 += PF) {
+    #pragma unroll
+                for (int u = 0; u < PF; u++) step(s0 + u, u, true);
+            }
+    #pragma unroll
+            for (int u = 0; u < PF; u++) step(s0 + u, u, false);
+            __syncthreads();
+            // token t of the tile by the threads RO t .. RO t + RO - 1 (a half-wave per limb group)
+            const int t = tid / RO, i = tid - t * RO;
+            if (t < nt) {
+                const float *rg = runs + (t * 2 * RO + i) * NC, *ru = runs + (t * 2 * RO + RO + i) * NC;
+                float yg = rg[0], yu = ru[0];
+                for (int cc = 1; cc < NC; cc++) { yg = yg + rg[cc]; yu = yu + ru[cc]; }
+                if (W.gs <= 0) {                            // per-row scales after the sum
+                    if constexpr (PT) {
+                        yg = yg * A.tab[e].gs[i0 + i];
+                        yu = yu * A.tab[e].us[i0 + i];
+                    } else {
+                        yg = yg * W.s[(int64_t)e * (2 * I) + i0 + i];
+                        yu = yu * W.s[(int64_t)e * (2 * I) + I + i0 + i];
+                    }
+                }
+                const float h = (yg / (1.0f + expf(-yg))) * yu;
+                // every 32 of the block's outputs are one limb group of the down projection's input
+                const int GI = I / RG, gi_out = (i0 + i) / RG;
+                const int64_t prow = beg + t0 + t;
+                limbs_group(h, i & 31, A.hl + (prow * GI + gi_out) * SW_NL, A.hs + prow * GI + gi_out);
+            }
+            __syncthreads();
         }
-        __syncthreads();
+    };
+    if constexpr (NTL) {
+        if (once) passes(SwIc<2>{});
+        else passes(SwIc<0>{});
+    } else {
+        passes(SwIc<0>{});
     }
 }
 
@@ -371,7 +384,9 @@ struct Dot8RowsArgs {
     float *Y;
     const SwTab *tab;          // per-group tensors (the _tab launch) or null
 };
-template <int PF, int TT, int C16, int RB, int PT = 0>
+// (a block whose pass is its group's only one loads its weights non-temporal; not with
+// the 8-deep ring, which spills with both load paths)
+template <int PF, int TT, int C16, int RB, int PT = 0, int NTL = (PF < 8)>
 __device__ __forceinline__ void dot8_rows_block(const Dot8RowsArgs &A, int bx, int by, float *runs) {
     const SwQ4 W = A.W;
     const sw_u32x4 *__restrict__ xl = A.xl;
@@ -385,8 +400,8 @@ __device__ __forceinline__ void dot8_rows_block(const Dot8RowsArgs &A, int bx, i
     const bool worker = ro < RPS, lead = worker && (gq & (CH - 1)) == 0, gv = C16 || gq < G;
     const int g = gv ? gq : G - 1;
     const int roc = worker ? ro : 0;
-    int e, beg, tb, tend;
-    if (!grp_work(grp, bx, TT, e, beg, tb, tend)) return;
+    int e, beg, tb, tend, gcnt;
+    if (!grp_work(grp, bx, TT, e, beg, tb, tend, &gcnt)) return;
     const int r0 = by * RB;
     const int nrows = min(RB, O - r0);
     const int ng = W.gs > 0 ? K / W.gs : 1;
@@ -405,60 +420,71 @@ __device__ __forceinline__ void dot8_rows_block(const Dot8RowsArgs &A, int bx, i
     const uint32_t vos = (uint32_t)(roc * NS) * sb + (uint32_t)sg * 4;
     const uint32_t erow = (PT ? 0u : (uint32_t)e * (uint32_t)O) + (uint32_t)r0;
     float *myruns = runs + (roc * NS) * NC + c;
-    for (int t0 = tb; t0 < tend; t0 += TT) {
-        const int nt = min(TT, tend - t0);
-        sw_u32x4 X[TT][SW_NL];
-        float xf[TT];
-#pragma unroll
-        for (int t = 0; t < TT; t++) {
-            const int pr = beg + t0 + (t < nt ? t : 0);
-            const int64_t tok = grp.grow ? grp.grow[pr] : pr;
-#pragma unroll
-            for (int l = 0; l < SW_NL; l++) X[t][l] = xl[(tok * G + g) * SW_NL + l];
-            xf[t] = xs[tok * G + g];
-        }
-        sw_u32x4 ra[PF];
-        float sa[PF];
-#pragma unroll
-        for (int u = 0; u < PF; u++) {
-            ra[u] = sw_ld16(rq, voq, (erow + u) * rb);
-            sa[u] = sw_ld4f(rs, vos, (erow + u) * sb);
-        }
-        auto step = [&](int s, int u, bool refill) {
-            const sw_u32x4 w = ra[u] ^ 0x88888888u;
-            const float sc = W.gs > 0 ? sa[u] : 1.0f;
-            if (refill) {
-                ra[u] = sw_ld16(rq, voq, (erow + s + PF) * rb);
-                sa[u] = sw_ld4f(rs, vos, (erow + s + PF) * sb);
-                __builtin_amdgcn_sched_barrier(0);
-            }
-#pragma unroll
+    // weight loads non-temporal (the nt policy) when this pass is the only one over the
+    // block's weights; cached when other passes re-read them
+    auto passes = [&](auto PC) {
+        constexpr int POL = decltype(PC)::v;
+        for (int t0 = tb; t0 < tend; t0 += TT) {
+            const int nt = min(TT, tend - t0);
+            sw_u32x4 X[TT][SW_NL];
+            float xf[TT];
+    #pragma unroll
             for (int t = 0; t < TT; t++) {
-                if (t < nt) {                          // uniform over the block
-                    const float p = row_term<C16>((float)dot8_group(w, X[t]) * (sc * xf[t]), gv, CH);
-                    if (lead) myruns[(t * RB + s) * NC] = p;
+                const int pr = beg + t0 + (t < nt ? t : 0);
+                const int64_t tok = grp.grow ? grp.grow[pr] : pr;
+    #pragma unroll
+                for (int l = 0; l < SW_NL; l++) X[t][l] = xl[(tok * G + g) * SW_NL + l];
+                xf[t] = xs[tok * G + g];
+            }
+            sw_u32x4 ra[PF];
+            float sa[PF];
+    #pragma unroll
+            for (int u = 0; u < PF; u++) {
+                ra[u] = sw_ld16<POL>(rq, voq, (erow + u) * rb);
+                sa[u] = sw_ld4f<POL>(rs, vos, (erow + u) * sb);
+            }
+            auto step = [&](int s, int u, bool refill) {
+                const sw_u32x4 w = ra[u] ^ 0x88888888u;
+                const float sc = W.gs > 0 ? sa[u] : 1.0f;
+                if (refill) {
+                    ra[u] = sw_ld16<POL>(rq, voq, (erow + s + PF) * rb);
+                    sa[u] = sw_ld4f<POL>(rs, vos, (erow + s + PF) * sb);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+    #pragma unroll
+                for (int t = 0; t < TT; t++) {
+                    if (t < nt) {                          // uniform over the block
+                        const float p = row_term<C16>((float)dot8_group(w, X[t]) * (sc * xf[t]), gv, CH);
+                        if (lead) myruns[(t * RB + s) * NC] = p;
+                    }
+                }
+            };
+            int s0 = 0;
+            for (; s0 + PF < NS; s0 += PF) {
+    #pragma unroll
+                for (int u = 0; u < PF; u++) step(s0 + u, u, true);
+            }
+    #pragma unroll
+            for (int u = 0; u < PF; u++) step(s0 + u, u, false);
+            __syncthreads();
+            for (int it = tid; it < TT * RB; it += 256) {
+                const int t = it / RB, r = it - t * RB;
+                if (t < nt && r < nrows) {
+                    const float *rr = runs + it * NC;
+                    float y = rr[0];
+                    for (int cc = 1; cc < NC; cc++) y = y + rr[cc];
+                    if (W.gs <= 0) y = y * (PT ? A.tab[e].ds[r0 + r] : W.s[(int64_t)e * O + r0 + r]);
+                    Y[(int64_t)(beg + t0 + t) * O + r0 + r] = y;
                 }
             }
-        };
-        int s0 = 0;
-        for (; s0 + PF < NS; s0 += PF) {
-#pragma unroll
-            for (int u = 0; u < PF; u++) step(s0 + u, u, true);
+            __syncthreads();
         }
-#pragma unroll
-        for (int u = 0; u < PF; u++) step(s0 + u, u, false);
-        __syncthreads();
-        for (int it = tid; it < TT * RB; it += 256) {
-            const int t = it / RB, r = it - t * RB;
-            if (t < nt && r < nrows) {
-                const float *rr = runs + it * NC;
-                float y = rr[0];
-                for (int cc = 1; cc < NC; cc++) y = y + rr[cc];
-                if (W.gs <= 0) y = y * (PT ? A.tab[e].ds[r0 + r] : W.s[(int64_t)e * O + r0 + r]);
-                Y[(int64_t)(beg + t0 + t) * O + r0 + r] = y;
-            }
-        }
-        __syncthreads();
+    };
+    if constexpr (NTL) {
+        if (tb == 0 && gcnt <= TT) passes(SwIc<2>{});
+        else passes(SwIc<0>{});
+    } else {
+        passes(SwIc<0>{});
     }
 }
 
@@ -630,8 +656,8 @@ __device__ __forceinline__ void dot8_down_combine_block(const Dot8DownArgs &A, i
     float sa[DC_RB];
 #pragma unroll
     for (int r = 0; r < DC_RB; r++) {                // every row of the block in flight
-        ra[r] = sw_ld16(rq, voq, (uint32_t)r * rb);
-        sa[r] = sw_ld4f(rs, vos, (uint32_t)r * sb);
+        ra[r] = sw_ld16<2>(rq, voq, (uint32_t)r * rb);
+        sa[r] = sw_ld4f<2>(rs, vos, (uint32_t)r * sb);
     }
     float *myruns = runs + (ac * DC_RB) * NC + c;
 #pragma unroll
@@ -722,7 +748,9 @@ __global__ __launch_bounds__(DG_NT, PICK ? 1 : 4) void k_stage_experts(Dot8GluAr
     const int b = blockIdx.x;
     if (b < nglu) {
         const int w = PICK == 0 && A.grp.items ? sw_xcd_work(b, nglu) : b;
-        dot8_glu_block<PF, PICK, NP, TTG, C16, RO>(A, w % nbx, w / nbx, smem);
+        // (cached loads with the batch shared down or the 8-deep ring, which spill with
+        // both load paths)
+        dot8_glu_block<PF, PICK, NP, TTG, C16, RO, 0, SKD != 1 && PF < 8>(A, w % nbx, w / nbx, smem);
     } else if constexpr (SKD == 1) {
         const int w = b - nglu, nrb = sh_sk_rows(0, Skd.O);
         sh_sk_block<0, 2, 0>(Skd, w % nrb, w / nrb, smem);

@@ -57,12 +57,16 @@ typedef __amdgpu_buffer_rsrc_t sw_rsrc;
 __device__ __forceinline__ sw_rsrc sw_make_rsrc(const void *p, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, bytes, 0x00020000);
 }
+// POL: the load's cache policy; 2 = nt (non-temporal)
+template <int POL = 0>
 __device__ __forceinline__ sw_u32x4 sw_ld16(sw_rsrc r, uint32_t voff, uint32_t soff) {
-    return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+    return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, POL);
 }
+template <int POL = 0>
 __device__ __forceinline__ float sw_ld4f(sw_rsrc r, uint32_t voff, uint32_t soff) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, POL));
 }
+
 // The rank-order combine of token s at outputs d .. d+3:
 // out[s,d] (+)= (sum_a w[s,a] * slots[rowof[s,a], d]) * route_scale (+ shared[s,d])
 // The sum runs in rank order from 0 with one fused multiply-add per rank, the
@@ -166,7 +170,9 @@ __device__ __forceinline__ int sw_xcd_work(int b, int nb) {
 // the work of grouped block bx: expert e, the group's first packed row beg and
 // its tokens [t0, tend) -- one pass from the pass list, or the whole group
 // (false: nothing to do)
-__device__ __forceinline__ bool grp_work(const SwGroups &grp, int bx, int TT, int &e, int &beg, int &t0, int &tend) {
+// (cnt: the group's token count, when asked for)
+__device__ __forceinline__ bool grp_work(const SwGroups &grp, int bx, int TT, int &e, int &beg, int &t0, int &tend,
+                                         int *cnt = nullptr) {
     // (uniform over the block: read into scalar registers)
     auto u = [](int v) { return __builtin_amdgcn_readfirstlane(v); };
     if (grp.items) {
@@ -175,7 +181,9 @@ __device__ __forceinline__ bool grp_work(const SwGroups &grp, int bx, int TT, in
         t0 = v >> 10;
         e = u(grp.gexp[gi]);
         beg = u(grp.gbeg[gi]);
-        tend = min(t0 + TT, u(grp.gcnt[gi]));
+        const int n = u(grp.gcnt[gi]);
+        tend = min(t0 + TT, n);
+        if (cnt) *cnt = n;
         return true;
     }
     const int gvalid = grp.G ? u(*grp.G) : grp.ngroups_max;
@@ -184,8 +192,11 @@ __device__ __forceinline__ bool grp_work(const SwGroups &grp, int bx, int TT, in
     beg = grp.gbeg ? u(grp.gbeg[bx]) : 0;
     t0 = 0;
     tend = grp.gcnt ? u(grp.gcnt[bx]) : grp.cnt_const;
+    if (cnt) *cnt = tend;
     return true;
 }
+template <int N>
+struct SwIc { static constexpr int v = N; };
 
 // int4 weight tensor of E experts, O rows each, K inputs
 struct SwQ4 {
