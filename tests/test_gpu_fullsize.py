@@ -8,7 +8,8 @@ device-generated layers:
     gate and with the Zipf(1.1)-skewed router -- all 2048 rows' routing identical,
     all rows within the tolerance, and sampled streams (the hottest expert's
     included) bit-identical to their single-stream calls;
-  * C5: one full-shape layer (E=256, top-8 softmax, I=1536) at batch 8.
+  * C5: one full-shape layer (E=256, top-8 softmax, I=1536) at batch 8;
+  * 64 single-token calls queued back to back, bit-identical to one batched call.
 
 The oracle gets a host copy of each device layer with only the experts it routes
 to (tests/fullsize.py).  Tolerance: normwise max|a-b|/max|b| of the MoE update
@@ -105,6 +106,31 @@ def test_c4_prefill(be, orc, cfg):
 def test_c5_layer_b8(be, orc):
     """C5's layer shape (E=256, top-8 softmax, I=1536, no shared) at batch 8"""
     check_layer(be, orc, cf.C5_LAYER, 7500, cf.C5_BATCH)
+
+
+@pytest.mark.parametrize("cfg", [cf.C2, cf.C5_LAYER], ids=lambda c: c.name)
+def test_single_tokens_back_to_back(be, orc, cfg):
+    """64 single-token forwards queued back to back with no host synchronisation
+    between them (each token's gate + top-k runs in every block of its expert stage)
+    against one batched forward (a gate launch and the grouped kernels): every output
+    bit-identical to its batched row, with softplus scores (C2) and softmax logits (C5)."""
+    S_, seed = 64, 7600
+    x = synth.make_x(orc, cfg, seed, S_)
+    dl = DeviceLayer.generate(be, cfg, seed)
+    xd, ob, o1 = be.upload(x), be.upload(np.zeros_like(x)), be.upload(np.zeros_like(x))
+    try:
+        be.moe_forward(desc_of(cfg), dl.weights(), xd, ob, S_)
+        for s in range(S_):
+            off = s * cfg.D * 4
+            be.moe_forward(desc_of(cfg), dl.weights(), int(xd) + off, int(o1) + off, 1)
+        batch = be.d2h(ob, x.shape, np.float32)
+        single = be.d2h(o1, x.shape, np.float32)
+        bad = np.nonzero((single.view(np.uint32) != batch.view(np.uint32)).any(axis=1))[0]
+        assert bad.size == 0, f"tokens {bad.tolist()} differ"
+    finally:
+        for b in (xd, ob, o1):
+            b.free()
+        dl.free()
 
 
 def test_c5_stack_48_layers(be, orc):
