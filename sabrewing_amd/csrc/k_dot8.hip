@@ -386,7 +386,8 @@ struct Dot8RowsArgs {
 };
 // (a block whose pass is its group's only one loads its weights non-temporal; not with
 // the 8-deep ring, which spills with both load paths)
-template <int PF, int TT, int C16, int RB, int PT = 0, int NTL = (PF < 8)>
+// NT: threads per block (192 for rows of 48 lanes: four row slots, no idle lanes)
+template <int PF, int TT, int C16, int RB, int PT = 0, int NTL = (PF < 8), int NT = 256>
 __device__ __forceinline__ void dot8_rows_block(const Dot8RowsArgs &A, int bx, int by, float *runs) {
     const SwQ4 W = A.W;
     const sw_u32x4 *__restrict__ xl = A.xl;
@@ -395,7 +396,7 @@ __device__ __forceinline__ void dot8_rows_block(const Dot8RowsArgs &A, int bx, i
     float *__restrict__ Y = A.Y;
     const int K = W.K, G = K / RG, O = W.O, Gq = C16 ? G : run_lanes(G);
     const int CH = C16 ? CHG : (Gq < CHG ? Gq : CHG), NC = Gq / CH;
-    const int RPS = dg_rps(Gq, RB, 256), NS = RB / RPS;
+    const int RPS = dg_rps(Gq, RB, NT), NS = RB / RPS;
     const int tid = threadIdx.x, ro = tid / Gq, gq = tid - ro * Gq, c = gq / CH;
     const bool worker = ro < RPS, lead = worker && (gq & (CH - 1)) == 0, gv = C16 || gq < G;
     const int g = gv ? gq : G - 1;
@@ -467,7 +468,7 @@ __device__ __forceinline__ void dot8_rows_block(const Dot8RowsArgs &A, int bx, i
     #pragma unroll
             for (int u = 0; u < PF; u++) step(s0 + u, u, false);
             __syncthreads();
-            for (int it = tid; it < TT * RB; it += 256) {
+            for (int it = tid; it < TT * RB; it += NT) {
                 const int t = it / RB, r = it - t * RB;
                 if (t < nt && r < nrows) {
                     const float *rr = runs + it * NC;
@@ -488,21 +489,21 @@ __device__ __forceinline__ void dot8_rows_block(const Dot8RowsArgs &A, int bx, i
     }
 }
 
-template <int PF, int TT, int C16, int RB>
-__global__ __launch_bounds__(256, 4) void k_dot8_rows(Dot8RowsArgs A) {
+template <int PF, int TT, int C16, int RB, int NT>
+__global__ __launch_bounds__(NT, 4) void k_dot8_rows(Dot8RowsArgs A) {
     extern __shared__ __align__(16) float red[];
     const int nb = (int)(gridDim.x * gridDim.y);
     const int w = A.grp.items ? sw_xcd_work((int)(blockIdx.x + gridDim.x * blockIdx.y), nb)
                               : (int)(blockIdx.x + gridDim.x * blockIdx.y);
-    dot8_rows_block<PF, TT, C16, RB>(A, w % (int)gridDim.x, w / (int)gridDim.x, red);
+    dot8_rows_block<PF, TT, C16, RB, 0, (PF < 8), NT>(A, w % (int)gridDim.x, w / (int)gridDim.x, red);
 }
 #define RW_PF 4
-template <int RB>
+template <int RB, int NT>
 struct RowsL {
     template <int PF, int C16>
     struct L {
         static void go(dim3 grid, size_t lds, hipStream_t st, const Dot8RowsArgs &A) {
-            SW_LAUNCH((k_dot8_rows<PF, DG_TT, C16, RB>), grid, dim3(256), lds, st, A);
+            SW_LAUNCH((k_dot8_rows<PF, DG_TT, C16, RB, NT>), grid, dim3(NT), lds, st, A);
         }
     };
 };
@@ -518,8 +519,17 @@ int sw_launch_q4_dot8_rows(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, const flo
     // a ring of at most RW_PF steps: within 128 VGPRs, four blocks per CU
     const int pf = dg_pf_rows(W.K) < RW_PF ? dg_pf_rows(W.K) : RW_PF;
     const size_t lds = (size_t)DG_TT * RB * dot8_nc(W.K) * 4;
-    if (RB == 128) dispatch_pf_c16<RowsL<128>::L>(pf, dot8_c16(W.K), grid, lds, st, A);
-    else dispatch_pf_c16<RowsL<64>::L>(pf, dot8_c16(W.K), grid, lds, st, A);
+    // rows of 48 lanes (K = 1536, C5's down) in blocks of 192 threads: four row slots and
+    // no idle lanes, five blocks per CU (256 threads left 64 idle in each block)
+    const int G = W.K / RG, Gq = dot8_c16(W.K) ? G : run_lanes(G);
+    if (Gq == 48) {
+        if (RB == 128) dispatch_pf_c16<RowsL<128, 192>::L>(pf, dot8_c16(W.K), grid, lds, st, A);
+        else dispatch_pf_c16<RowsL<64, 192>::L>(pf, dot8_c16(W.K), grid, lds, st, A);
+    } else if (RB == 128) {
+        dispatch_pf_c16<RowsL<128, 256>::L>(pf, dot8_c16(W.K), grid, lds, st, A);
+    } else {
+        dispatch_pf_c16<RowsL<64, 256>::L>(pf, dot8_c16(W.K), grid, lds, st, A);
+    }
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
