@@ -4,19 +4,20 @@
 // in one VALU op.  A weight dword holds eight nibbles n (k = 8j + i at bits
 // 4i, the container layout of c/moe_quant.h), and n ^ 8 read as a signed
 // nibble is exactly n - 8, the weight's integer value: one XOR per eight
-// weights is the whole dequant.  The activation side is split into "limbs":
+// weights is the whole dequant.  The activation side is an integer per input:
 // for each group of 32 consecutive inputs, with 2^e the smallest power of two
 // above max|x| of the group, y = x * 2^-e in (-1, 1) is written as
-// sum_{l=1..NL} d_l 8^-l with signed digits d_l in [-8, 7] (round to nearest,
+// sum_{l=1..ND} d_l 8^-l with signed digits d_l in [-8, 7] (round to nearest,
 // clamp, carry the exact remainder), so
-//     x ~= 2^(e - 3 NL) * D,   D = sum_l d_l 8^(NL - l)   (|error| <= 2^e 8^-NL).
-// With NL = 7, |D| <= 8 (8^7 - 1) / 7 < 2^21.2 and the input error is at most
-// 2^e 8^-7 (~2.4e-7 of the group's largest input, a few f32 ulps).
-// For one weight row and one group, sum_k (n_k - 8) D_k is an exact int32
-// (Horner over the limbs: acc = (acc << 3) + four dot8; |acc| <= 32 * 8 *
-// 2^21.2 < 2^29.2), turned into f32 once (correctly rounded, the same in every
-// launch) and multiplied by s_row,group * 2^(e - 3 NL) (exact power-of-two
-// scaling of the weight scale).  A row's output is then the sum
+//     x ~= 2^(e - 3 ND) * D,   D = sum_l d_l 8^(ND - l)   (|error| <= 2^e 8^-ND).
+// With ND = 7, |D| <= 8 (8^7 - 1) / 7 < 2^21.2 and the input error is at most
+// 2^e 8^-7 (~2.4e-7 of the group's largest input, a few f32 ulps).  D is stored
+// as NL = 6 "limbs", its digits in balanced base 16 (each in [-8, 7], a signed
+// nibble like the weights).  For one weight row and one group, sum_k (n_k - 8) D_k
+// is an exact int32 (Horner over the limbs: acc = (acc << 4) + four dot8;
+// |acc| <= 32 * 8 * 2^21.2 < 2^29.2), turned into f32 once (correctly rounded, the
+// same in every launch) and multiplied by s_row,group * 2^(e - 3 ND) (exact
+// power-of-two scaling of the weight scale).  A row's output is then the sum
 // of its group terms in the fixed order of run_sum (sw_gate.h): runs of up to
 // 16 groups, each summed by a butterfly across the lanes holding them, the
 // run sums left to right.  Nothing of it depends on which tokens share a
@@ -51,11 +52,11 @@ int sw_launch_limbs(hipStream_t st, const float *x, int rows, int K, sw_u32x4 *x
 }
 
 // exact int32 sum_k (n_k - 8) D_k over one group: a = the group's 16 weight
-// bytes with every nibble XOR 8 (signed nibbles n - 8).  Horner over the
-// limbs folded into dot8 chains -- acc = (acc << 3), then limb l's four dot8
-// accumulate into it -- as two independent chains (limbs 0..3 and 4..6)
-// joined at the end: acc = (hi << 9) + lo.  Every partial sum is an exact
-// Horner prefix, below 2^29.2 in magnitude.
+// bytes with every nibble XOR 8 (signed nibbles n - 8).  Horner over the base-16
+// limbs folded into dot8 chains -- acc = (acc << 4), then limb l's four dot8
+// accumulate into it -- as two independent chains (limbs 0..2 and 3..5) joined
+// at the end: acc = (hi << 12) + lo.  Every partial sum is an exact Horner
+// prefix: |hi| <= 32 * 8 * 576, |hi << 12| < 2^29.2 + 32 * 8 * 2184 < 2^31.
 __device__ __forceinline__ int dot8_chain(sw_u32x4 a, const sw_u32x4 *X, int l0, int l1) {
     int acc = __builtin_amdgcn_sdot8((int)a.x, (int)X[l0].x, 0, false);
     acc = __builtin_amdgcn_sdot8((int)a.y, (int)X[l0].y, acc, false);
@@ -63,17 +64,17 @@ __device__ __forceinline__ int dot8_chain(sw_u32x4 a, const sw_u32x4 *X, int l0,
     acc = __builtin_amdgcn_sdot8((int)a.w, (int)X[l0].w, acc, false);
 #pragma unroll
     for (int l = l0 + 1; l < l1; l++) {
-        acc = __builtin_amdgcn_sdot8((int)a.x, (int)X[l].x, acc << 3, false);
+        acc = __builtin_amdgcn_sdot8((int)a.x, (int)X[l].x, acc << 4, false);
         acc = __builtin_amdgcn_sdot8((int)a.y, (int)X[l].y, acc, false);
         acc = __builtin_amdgcn_sdot8((int)a.z, (int)X[l].z, acc, false);
         acc = __builtin_amdgcn_sdot8((int)a.w, (int)X[l].w, acc, false);
     }
     return acc;
 }
-#define DOT8_SPLIT 4          // limbs of the high chain
+#define DOT8_SPLIT 3          // limbs of the high chain
 __device__ __forceinline__ int dot8_group(sw_u32x4 a, const sw_u32x4 *X) {
     const int hi = dot8_chain(a, X, 0, DOT8_SPLIT), lo = dot8_chain(a, X, DOT8_SPLIT, SW_NL);
-    return (hi << (3 * (SW_NL - DOT8_SPLIT))) + lo;
+    return (hi << (4 * (SW_NL - DOT8_SPLIT))) + lo;
 }
 
 // A row's terms: one per group of 32 inputs, the lanes of a row padded to

@@ -64,7 +64,7 @@ __device__ __forceinline__ void digits_group(float v, int i, uint32_t *__restric
     float y = ldexpf(v, -e);
     int D = 0;
 #pragma unroll
-    for (int l = 0; l < SW_NL; l++) D = D * 8 + (int)limb_digit(y);
+    for (int l = 0; l < SW_ND; l++) D = D * 8 + (int)limb_digit(y);
     if (bad) D = 0;
     const int E0 = ((D + 2048) & 4095) - 2048, E1 = (D - E0) >> 12;
     const int sh = 8 * ((i & 7) >> 1);
@@ -82,7 +82,7 @@ __device__ __forceinline__ void digits_group(float v, int i, uint32_t *__restric
         dst[16 + kq * 4 + par] = b[2];
         dst[16 + kq * 4 + 2 + par] = b[3];
     }
-    if (i == 0) *fdst = bad ? __builtin_nanf("") : ldexpf(1.0f, e - 3 * SW_NL);
+    if (i == 0) *fdst = bad ? __builtin_nanf("") : ldexpf(1.0f, e - 3 * SW_ND);
 }
 
 // rows x[r, K] f32 -> digits dg[r][K/32][32 dwords], factors xs[r][K/32]

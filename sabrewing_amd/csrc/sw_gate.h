@@ -269,12 +269,16 @@ __device__ void gate_topk_wave(const float *__restrict__ src, int E, int K, int 
 // ------------------------------------------------------------ limbs ----
 // The activation side of the int4 dot8 GEMV (k_dot8.hip).  For each group of
 // SW_RG consecutive inputs, with 2^e the smallest power of two above max|x|
-// of the group, y = x * 2^-e in (-1, 1) is written as sum_{l=1..NL} d_l 8^-l
+// of the group, y = x * 2^-e in (-1, 1) is written as sum_{l=1..ND} d_l 8^-l
 // with signed digits d_l in [-8, 7] (round to nearest, clamp, carry the exact
-// remainder), so x ~= 2^(e - 3 NL) * D with D = sum_l d_l 8^(NL - l) and
-// |error| <= 2^e 8^-NL.  Limb l of the group is 4 dwords of 32 nibbles (input
-// 8j + i at bits 4i of dword j, the weights' nibble order); the factor is
-// 2^(e - 3 NL), or NaN for a group holding a NaN or an infinity.
+// remainder), ND = SW_ND = 7, so x ~= 2^(e - 3 ND) * D with the integer
+// D = sum_l d_l 8^(ND - l), |D| < 2^21.2, and |error| <= 2^e 8^-ND.  D is stored
+// as SW_NL = 6 digits of balanced base 16 (every digit in [-8, 7], a complete
+// digit set for base 16; six cover |D| <= 8 (16^6 - 1) / 15), most significant
+// first, so the dot8 Horner runs 6 limbs with shifts of 4 instead of 7 with
+// shifts of 3 over the same integer.  Limb l of the group is 4 dwords of 32
+// nibbles (input 8j + i at bits 4i of dword j, the weights' nibble order); the
+// factor is 2^(e - 3 ND), or NaN for a group holding a NaN or an infinity.
 #define SW_RG 32
 // the group's exponent e (by the 32 lanes of a half-wave, v = this lane's
 // input): 2^e the smallest power of two above max|x|, 0 for an all-zero
@@ -305,11 +309,15 @@ __device__ __forceinline__ void limbs_group(float v, int i, sw_u32x4 *__restrict
     bool bad;
     const int e = limbs_exp(v, bad);
     float y = ldexpf(v, -e);                          // exact: |y| < 1
+    int D = 0;
+#pragma unroll
+    for (int l = 0; l < SW_ND; l++) D = D * 8 + (int)limb_digit(y);
     uint32_t dw[SW_NL];
 #pragma unroll
-    for (int l = 0; l < SW_NL; l++) {
-        const float d = limb_digit(y);
-        uint32_t nib = ((uint32_t)(int)d & 0xFu) << (4 * (i & 7));
+    for (int l = SW_NL - 1; l >= 0; l--) {            // the least significant digit first
+        const int d = ((D + 8) & 15) - 8;             // in [-8, 7], D - d a multiple of 16
+        D = (D - d) >> 4;                             // exact
+        uint32_t nib = ((uint32_t)d & 0xFu) << (4 * (i & 7));
         nib |= __shfl_xor(nib, 1, 32);
         nib |= __shfl_xor(nib, 2, 32);
         nib |= __shfl_xor(nib, 4, 32);
@@ -320,7 +328,7 @@ __device__ __forceinline__ void limbs_group(float v, int i, sw_u32x4 *__restrict
 #pragma unroll
         for (int l = 0; l < SW_NL; l++) ((uint32_t *)(dst + l))[j] = bad ? 0u : dw[l];
     }
-    if (i == 0) *fdst = bad ? __builtin_nanf("") : ldexpf(1.0f, e - 3 * SW_NL);
+    if (i == 0) *fdst = bad ? __builtin_nanf("") : ldexpf(1.0f, e - 3 * SW_ND);
 }
 
 

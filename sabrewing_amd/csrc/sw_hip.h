@@ -273,8 +273,11 @@ int sw_launch_lanes16_ld(hipStream_t st, const void *W, int wkind, int dp, const
 // h[i] = siluf(g[i]) * u[i] with the glibc-exact expf (c/moe_math.h:53)
 int sw_launch_silu_mul(hipStream_t st, const float *g, const float *u, int64_t n, float *h);
 // activation limbs for the dot8 GEMV (k_dot8.hip): rows x[rows, K] f32 ->
-// xl[rows][K/32][SW_NL] (32 signed nibbles each), xs[rows][K/32] f32
-#define SW_NL 7
+// xl[rows][K/32][SW_NL] (32 signed nibbles each), xs[rows][K/32] f32.  An input's
+// integer D is defined by SW_ND base-8 digits (limbs_group, sw_gate.h) and stored as
+// SW_NL balanced base-16 digits
+#define SW_ND 7
+#define SW_NL 6
 int sw_launch_limbs(hipStream_t st, const float *x, int rows, int K, sw_u32x4 *xl, float *xs);
 // SiLU-GLU(gate, up) for every packed row of every group, on the dot8 unit;
 // output h as limbs hl[packed row][I/32][SW_NL], hs[packed row][I/32]

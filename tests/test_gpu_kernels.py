@@ -144,8 +144,8 @@ def test_expert_and_moe_experts(be, orc, gs):
     got = be.expert_q4(x, off(dev.gu_q, e * 2 * I * D // 2), off(dev.gu_s, e * 2 * I * ngD * 4),
                        off(dev.dn_q, e * D * I // 2), off(dev.dn_s, e * D * ngI * 4), I, D, gs)
     want = cpu_expert(orc, L, e, x, gs)
-    # activations enter the int4 GEMV as 5 signed int4 limbs per 32-input group
-    # (2^-15 of the group's max); group scales add one f16 rounding on the MFMA side
+    # activations enter the int4 GEMV as one exact integer per input (2^-21 of its
+    # 32-input group's max); the rest is the f32 sum order
     assert normwise(got, want) < (2e-4 if gs == 0 else 2e-3)
     # K experts in one submission: out = sum_k w_k expert(sel_k)
     sel = np.array([4, 0, 5], np.int32); w = np.array([0.5, 0.3, 0.2], np.float32)
