@@ -27,10 +27,11 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 # what the kernels compute in: int4 weights and their f32 group scales against the
-# activations written per 32 inputs as 7 signed base-8 digits under a power-of-two
-# factor (exact integer dots, |input error| <= 2^-21 of the group's largest input);
+# activations written per 32 inputs as integers of 7 signed base-8 digits (held as 6
+# base-16 limbs) under a power-of-two factor (exact integer dots, |input error| <= 2^-21
+# of the group's largest input);
 # f32 accumulation; the router and the shared expert in f32 fma chains on bf16 weights
-DTYPE = ("int4 weights x 7-digit base-8 activation limbs per 32 inputs (2^-21 of the group max), "
+DTYPE = ("int4 weights x activation integers of 7 base-8 digits per 32 inputs (2^-21 of the group max, held as 6 base-16 limbs), "
          "exact int32 dots, f32 scales and accumulation; router f32 FMA chains on bf16 weights; "
          "shared expert bf16 weights x f32 inputs split exactly into three bf16 parts on the MFMA")
 # the reference CPU baseline's OpenMP placement (c/moe_util.h:78-86 sets one thread per
@@ -47,11 +48,11 @@ def log(*a):
 def kernel_bytes(cfg, S, G):
     """algorithmic HBM bytes per launch of each kernel of the forward pass:
     every weight byte the launch needs once, activations in and out once
-    (dot8 limbs: 7 x 16 bytes + one f32 factor per 32 inputs)"""
+    (dot8 limbs: 6 x 16 bytes + one f32 factor per 32 inputs)"""
     D, I, Is, E, K = cfg.D, cfg.I, cfg.Is, cfg.E, cfg.K
     ngD, ngI = (D // cfg.gs, I // cfg.gs) if cfg.gs else (1, 1)
     T = S * K
-    limb = lambda n: n // 32 * (7 * 16 + 4)
+    limb = lambda n: n // 32 * (6 * 16 + 4)
     gu_w = G * (2 * I * D // 2 + 2 * I * ngD * 4)
     dn_w = G * (D * I // 2 + D * ngI * 4)
     sh_gu = 2 * Is * D * 2 if cfg.shared_mode else 0
