@@ -785,9 +785,9 @@ struct StageL {
 
 template <int ONE, int SK, int NORM = 0>
 static void launch_stage_route(int bf16, dim3 grid, size_t lds, hipStream_t st, const RouterArgs &R, int nbr, int S,
-                               const ShGluArgs &G, const ShSkArgs &Sk) {
-    if (bf16) SW_LAUNCH((k_stage_route<1, ONE, SK, NORM>), grid, dim3(SH_NT), lds, st, R, nbr, S, G, Sk);
-    else SW_LAUNCH((k_stage_route<0, ONE, SK, NORM>), grid, dim3(SH_NT), lds, st, R, nbr, S, G, Sk);
+                               const ShGluArgs &G, const ShSkArgs &Sk, int nt = SH_NT) {
+    if (bf16) SW_LAUNCH((k_stage_route<1, ONE, SK, NORM>), grid, dim3(nt), lds, st, R, nbr, S, G, Sk);
+    else SW_LAUNCH((k_stage_route<0, ONE, SK, NORM>), grid, dim3(nt), lds, st, R, nbr, S, G, Sk);
 }
 
 // stage 1: router logits / scores and the limbs of x, and the shared
@@ -800,8 +800,17 @@ int sw_launch_stage_route(hipStream_t st, const void *Wc, int w_bf16, const floa
     if (xp && !sh_shape_ok(D)) return -1;
     const int one = router_one(S, E);
     const size_t rl = router_lds(D);
-    if (rl > 65536 || D > 4 * RT_XB * (one ? SH_NT - 64 : SH_NT)) return -1;
-    const int nbr = (E + router_epb(one, SH_NT) - 1) / router_epb(one, SH_NT);
+    // threads per router block of a batch without the shared expert's blocks or parts: 2
+    // waves (8 experts per block, twice the blocks of 4 waves over the CUs: B=8 9.8 -> 7.6
+    // us), 4 with the RMSNorm (rms_inv_block's fixed order is over 256 threads), more only
+    // when x needs them to stage (D <= 4 RT_XB threads)
+    int rnt = SH_NT;
+    if (!one && !sg && !xp) {
+        rnt = nw ? RN_NT : 128;
+        while (rnt < SH_NT && D > 4 * RT_XB * rnt) rnt *= 2;
+    }
+    if (rl > 65536 || D > 4 * RT_XB * (one ? SH_NT - 64 : rnt)) return -1;
+    const int nbr = (E + router_epb(one, rnt) - 1) / router_epb(one, rnt);
     // the RMSNorm of the rows (nw): not with the shared expert's blocks or parts, which
     // read x as given
     if (nw && (sg || xp || !xn)) return -1;
@@ -820,7 +829,7 @@ int sw_launch_stage_route(hipStream_t st, const void *Wc, int w_bf16, const floa
     const int sk = sg && S > 1 ? nc : 0;
     if (nw) {
         if (one) launch_stage_route<1, 0, 1>(w_bf16, grid, lds, st, R, nbr, S, G, Sk);
-        else launch_stage_route<0, 0, 1>(w_bf16, grid, lds, st, R, nbr, S, G, Sk);
+        else launch_stage_route<0, 0, 1>(w_bf16, grid, lds, st, R, nbr, S, G, Sk, rnt);
     } else if (one) {
         if (sk) launch_stage_route<1, 1>(w_bf16, grid, lds, st, R, nbr, S, G, Sk);   // (ONE: S <= 4, so nc = 1)
         else launch_stage_route<1, 0>(w_bf16, grid, lds, st, R, nbr, S, G, Sk);
@@ -829,7 +838,7 @@ int sw_launch_stage_route(hipStream_t st, const void *Wc, int w_bf16, const floa
     } else if (sk == 2) {
         launch_stage_route<0, 2>(w_bf16, grid, lds, st, R, nbr, S, G, Sk);
     } else {
-        launch_stage_route<0, 0>(w_bf16, grid, lds, st, R, nbr, S, G, Sk);
+        launch_stage_route<0, 0>(w_bf16, grid, lds, st, R, nbr, S, G, Sk, rnt);
     }
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
