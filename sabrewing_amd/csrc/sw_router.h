@@ -17,12 +17,17 @@
 // slices, slice q holding the next P elements (8 bf16 or 4 f32) of each of
 // its 64 chains, so one 16-byte load per lane reads one slice, contiguous,
 // and gives each lane the next P elements of its own chain; RT_PF slices are
-// in flight (all of a D = 4096 bf16 chain, issued before the block's other
-// traffic); a bf16 weight widens exactly to f32; x is
+// in flight in a single token's blocks (all of a D = 4096 bf16 chain, issued
+// before the block's other traffic), RT_PF_B in a batch's; a bf16 weight widens
+// exactly to f32; x is
 // staged transposed in LDS once per block, so chain j reads x[16m + j] as
 // xt[j][m]; the tree is four shuffles within each 16-lane row.  The chain is
 // M = D/16 dependent fmas per lane, the critical path of the routing.
 #define RT_PF 32
+// the slices in flight of a batch's router blocks (not ONE): 16 keeps their kernels within
+// 120-138 VGPRs, 3-4 waves per SIMD instead of 2 (B=64's routing launch with the shared
+// expert's blocks 41.5 -> 33.1 us, B=128 78.8 -> 58.2; B=2 unchanged)
+#define RT_PF_B 16
 #define RT_XB 8           // x float4 loads per thread: D <= 4 * RT_XB * threads
 struct RouterArgs {
     const void *Wc;            // router in the streaming order (k_chain_major)
@@ -116,12 +121,13 @@ __device__ __forceinline__ void router_block(const RouterArgs &R, int bx, int s,
         }
     };
     const uint64_t tabv = sw_exp2f_tab[lane & 31];  // stored after the chain, where the scores need it
-    sw_u32x4 ring[RT_PF];
+    constexpr int PFR = ONE ? RT_PF : RT_PF_B;       // slices in flight per lane
+    sw_u32x4 ring[PFR];
     if constexpr (ONE && NORM) {
         sw_f32x4 xv[RT_XB], wv[RT_XB];
         if (wave == 0) {
 #pragma unroll
-            for (int u = 0; u < RT_PF; u++) ring[u] = slice(u);
+            for (int u = 0; u < PFR; u++) ring[u] = slice(u);
         } else {
             stage_x_load(xv, wv);
         }
@@ -130,7 +136,7 @@ __device__ __forceinline__ void router_block(const RouterArgs &R, int bx, int s,
     } else if constexpr (ONE) {
         if (wave == 0) {
 #pragma unroll
-            for (int u = 0; u < RT_PF; u++) ring[u] = slice(u);
+            for (int u = 0; u < PFR; u++) ring[u] = slice(u);
         } else {
             sw_f32x4 xv[RT_XB], wv[RT_XB];
             stage_x_load(xv, wv);
@@ -140,7 +146,7 @@ __device__ __forceinline__ void router_block(const RouterArgs &R, int bx, int s,
         sw_f32x4 xv[RT_XB], wv[RT_XB];
         stage_x_load(xv, wv);                         // x first, then every slice of the ring
 #pragma unroll
-        for (int u = 0; u < RT_PF; u++) ring[u] = slice(u);
+        for (int u = 0; u < PFR; u++) ring[u] = slice(u);
         const float inv = norm_inv();
         stage_x_store(xv, wv, inv);
     }
@@ -179,16 +185,16 @@ __device__ __forceinline__ void router_block(const RouterArgs &R, int bx, int s,
         // full rounds with unconditional refills (a refill past the end re-reads the last
         // slice), then the last round without: no ring rotation, loads stay in flight
         int q0 = 0;
-        for (; q0 + RT_PF < NQ; q0 += RT_PF) {
+        for (; q0 + PFR < NQ; q0 += PFR) {
 #pragma unroll
-            for (int u = 0; u < RT_PF; u++) {         // the slot is consumed before its refill
+            for (int u = 0; u < PFR; u++) {         // the slot is consumed before its refill
                 chain4(q0 + u, ring[u]);
-                ring[u] = slice(q0 + u + RT_PF);
+                ring[u] = slice(q0 + u + PFR);
                 __builtin_amdgcn_sched_barrier(0);    // keep the refill here, not sunk to the round's end
             }
         }
 #pragma unroll
-        for (int u = 0; u < RT_PF; u++)
+        for (int u = 0; u < PFR; u++)
             if (q0 + u < NQ) chain4(q0 + u, ring[u]);
     }
     tab[lane & 31] = tabv;                            // every wave writes the whole table (equal values)
