@@ -35,8 +35,8 @@ __global__ __launch_bounds__(RN_NT) void k_rmsnorm(const float *__restrict__ x, 
 // value (-0.0 and +0.0 equal).  Each thread takes the largest word (order
 // bits of v + 0.0, ~index) of its values; the block takes the largest word
 // (a maximum: the same word whatever order the values are taken in).  Rows
-// of a multiple of 4 values are read as float4, AM_U loads per thread in
-// flight before any is used.
+// of a multiple of 4 values that start 16-byte aligned are read as float4,
+// AM_U loads per thread in flight before any is used.
 #define AM_NT 1024
 #define AM_U 8
 __global__ __launch_bounds__(AM_NT) void k_argmax(const float *__restrict__ logits, int V, int *__restrict__ tok) {
@@ -50,7 +50,7 @@ __global__ __launch_bounds__(AM_NT) void k_argmax(const float *__restrict__ logi
             best = k > best ? k : best;
         }
     };
-    if ((V & 3) == 0) {
+    if ((V & 3) == 0 && ((uintptr_t)v & 15) == 0) {
         const sw_f32x4 *v4 = (const sw_f32x4 *)v;
         const int n4 = V / 4;
         for (int i0 = tid; i0 < n4; i0 += AM_NT * AM_U) {

@@ -92,7 +92,11 @@ def test_pick_long_rows(be, orc, V):
     ld, td = be.upload(rows), be.alloc(4 * 4)
     be.argmax(ld, 4, V, td)
     assert np.array_equal(be.d2h(td, (4,), np.int32), want)
-    for b in (ld, td):
+    # rows starting 4 bytes past a 16-byte boundary (the scalar path)
+    lo = be.upload(np.concatenate([np.zeros(1, np.float32), rows.reshape(-1)]))
+    be.argmax(int(lo) + 4, 4, V, td)
+    assert np.array_equal(be.d2h(td, (4,), np.int32), want)
+    for b in (ld, td, lo):
         b.free()
 
 
