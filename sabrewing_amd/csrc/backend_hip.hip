@@ -505,7 +505,7 @@ static int carve_fwd(const LagHipMoeDesc *d, int S, FwdScratch &f, const Scratch
     const size_t o_sel = cv.take((size_t)T * 4), o_w = cv.take((size_t)T * 4);
     const size_t o_gexp = cv.take((size_t)E * 4), o_gbeg = cv.take((size_t)E * 4), o_gcnt = cv.take((size_t)E * 4);
     const size_t o_G = cv.take(4), o_grow = cv.take((size_t)T * 4), o_rowof = cv.take((size_t)T * 4);
-    const size_t o_items = cv.take((size_t)sw_npass_max(T, E, SW_DG_TT) * 4), o_P = cv.take(4);
+    const size_t o_items = cv.take((size_t)sw_npass_max(T, E, 1) * 4), o_P = cv.take(4);   // (one token per pass at most)
     const size_t o_hl = cv.take((size_t)T * (I / 32) * SW_NL * 16), o_hs = cv.take((size_t)T * (I / 32) * 4);
     const size_t o_slot = cv.take(S > 1 || idot ? (size_t)T * D * 4 : 4);
     size_t o_sh = 0, o_so = 0, o_su = 0;
@@ -787,22 +787,26 @@ static int forward(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const floa
               return fail_msg("combine launch"); }
         g_last_G_dev = 1; g_last_ng = 0;
     } else {
+        // tokens per pass of the grouped kernels: one when the pairs number at most 0.3 E
+        // (about one token per group: C5's 64 pairs of 256 experts, 7.19 -> 6.91 ms per
+        // step), else SW_DG_TT (B=32: 300 against 316 us with one)
+        const int tt = (int64_t)T * 10 <= (int64_t)E * 3 ? 1 : SW_DG_TT;
         if (gate_bucket) {
             PROF("gate_bucket");
             const int ns = ink_ns(d);
             const SwGateOpt o = {router_rows(d), ns, d->route_scale, d->topk, ns ? f.wsh : nullptr, ns};
             if (sw_launch_gate_bucket(g_st, f.logits, f.scores, S, E, K, d->route_act, w->corr_bias, d->use_corr_bias,
-                                      d->norm_topk, f.sel, f.w, &o, f.gexp, f.gbeg, f.gcnt, f.G, f.grow, f.rowof, SW_DG_TT,
+                                      d->norm_topk, f.sel, f.w, &o, f.gexp, f.gbeg, f.gcnt, f.G, f.grow, f.rowof, tt,
                                       f.items, f.P))
                 return fail_msg("gate/top-k + bucket launch");
         } else {
             PROF("bucket");
-            if (sw_launch_bucket(g_st, f.sel, S, K, E, f.gexp, f.gbeg, f.gcnt, f.G, f.grow, f.rowof, SW_DG_TT, f.items, f.P))
+            if (sw_launch_bucket(g_st, f.sel, S, K, E, f.gexp, f.gbeg, f.gcnt, f.G, f.grow, f.rowof, tt, f.items, f.P))
                 return fail_msg("bucket launch");
         }
-        // one block per pass of up to SW_DG_TT tokens of a group (the passes of a group
-        // with many tokens spread over blocks instead of queueing in one)
-        SwGroups g = {f.gexp, f.gbeg, f.gcnt, f.grow, f.G, sw_npass_max(T, E, SW_DG_TT), 0, f.items, f.P};
+        // one block per pass of up to tt tokens of a group (the passes of a group with many
+        // tokens spread over blocks instead of queueing in one)
+        SwGroups g = {f.gexp, f.gbeg, f.gcnt, f.grow, f.G, sw_npass_max(T, E, tt), 0, f.items, f.P, tt};
         { PROF("stage_experts");
           if (sw_launch_stage_experts(g_st, gu, f.xl, f.xs, g, I, f.hl, f.hs, nullptr, K, nullptr, E, d->route_act,
                                       w->corr_bias, d->use_corr_bias, d->norm_topk, f.w, sh_fused && !sh_late ? sd : nullptr,

@@ -350,7 +350,7 @@ static size_t dot8_glu_lds(int K, int TT, int RO = 32) { return (size_t)TT * 2 *
 int sw_launch_q4_dot8_glu(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, const float *xs, SwGroups g, int I,
                           sw_u32x4 *hl, float *hs) {
     int gsh;
-    if (dot8_glu_check(W, I, gsh) || g.ngroups_max <= 0) return -1;
+    if (dot8_glu_check(W, I, gsh) || g.ngroups_max <= 0 || (g.items && g.tt && g.tt != DG_TT)) return -1;
     const Dot8GluArgs A = {W, gsh, xl, xs, g, I, hl, hs, nullptr, DotRoute{}};
     const int RO = dg_ro_grid(I, g.ngroups_max);
     const dim3 grid((unsigned)g.ngroups_max, (unsigned)(I / RO));
@@ -499,12 +499,12 @@ __global__ __launch_bounds__(NT, 4) void k_dot8_rows(Dot8RowsArgs A) {
     dot8_rows_block<PF, TT, C16, RB, 0, (PF < 8), NT>(A, w % (int)gridDim.x, w / (int)gridDim.x, red);
 }
 #define RW_PF 4
-template <int RB, int NT>
+template <int RB, int NT, int TT>
 struct RowsL {
     template <int PF, int C16>
     struct L {
         static void go(dim3 grid, size_t lds, hipStream_t st, const Dot8RowsArgs &A) {
-            SW_LAUNCH((k_dot8_rows<PF, DG_TT, C16, RB, NT>), grid, dim3(NT), lds, st, A);
+            SW_LAUNCH((k_dot8_rows<PF, TT, C16, RB, NT>), grid, dim3(NT), lds, st, A);
         }
     };
 };
@@ -519,18 +519,22 @@ int sw_launch_q4_dot8_rows(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, const flo
     const Dot8RowsArgs A = {W, gsh, xl, xs, g, Y};
     // a ring of at most RW_PF steps: within 128 VGPRs, four blocks per CU
     const int pf = dg_pf_rows(W.K) < RW_PF ? dg_pf_rows(W.K) : RW_PF;
-    const size_t lds = (size_t)DG_TT * RB * dot8_nc(W.K) * 4;
+    const int tt = g.tt ? g.tt : DG_TT;                // tokens per pass of the items
+    if (tt != 1 && tt != DG_TT) return -1;
+    const size_t lds = (size_t)tt * RB * dot8_nc(W.K) * 4;
     // rows of 48 lanes (K = 1536, C5's down) in blocks of 192 threads: four row slots and
     // no idle lanes, five blocks per CU (256 threads left 64 idle in each block)
     const int G = W.K / RG, Gq = dot8_c16(W.K) ? G : run_lanes(G);
-    if (Gq == 48) {
-        if (RB == 128) dispatch_pf_c16<RowsL<128, 192>::L>(pf, dot8_c16(W.K), grid, lds, st, A);
-        else dispatch_pf_c16<RowsL<64, 192>::L>(pf, dot8_c16(W.K), grid, lds, st, A);
-    } else if (RB == 128) {
-        dispatch_pf_c16<RowsL<128, 256>::L>(pf, dot8_c16(W.K), grid, lds, st, A);
-    } else {
-        dispatch_pf_c16<RowsL<64, 256>::L>(pf, dot8_c16(W.K), grid, lds, st, A);
-    }
+#define SW_RW(T_) \
+    do { \
+        if (Gq == 48 && RB == 128) dispatch_pf_c16<RowsL<128, 192, T_>::L>(pf, dot8_c16(W.K), grid, lds, st, A); \
+        else if (Gq == 48) dispatch_pf_c16<RowsL<64, 192, T_>::L>(pf, dot8_c16(W.K), grid, lds, st, A); \
+        else if (RB == 128) dispatch_pf_c16<RowsL<128, 256, T_>::L>(pf, dot8_c16(W.K), grid, lds, st, A); \
+        else dispatch_pf_c16<RowsL<64, 256, T_>::L>(pf, dot8_c16(W.K), grid, lds, st, A); \
+    } while (0)
+    if (tt == 1) SW_RW(1);
+    else SW_RW(DG_TT);
+#undef SW_RW
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
@@ -884,17 +888,27 @@ int sw_launch_stage_experts(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, const fl
     // 8-step ring also fits but measured slower at B=32 (224 vs 215 us)
     const int pf = picks ? pf0 : (pf0 < 4 ? pf0 : 4);
     if (!picks) {
-        const size_t lds = lds_max(dot8_glu_lds(W.K, DG_TT, RO), shl);
+        // tokens per pass: one when the groups hold about one token each (the limbs of a
+        // second token then only cost registers), else DG_TT
+        const int tt = g.tt ? g.tt : DG_TT;
+        if (tt != 1 && tt != DG_TT) return -1;
+        const size_t lds = lds_max(dot8_glu_lds(W.K, tt, RO), shl);
+#define SW_STG_T(T_, K_) \
+    do { \
+        if (RO == 128) dispatch_pf_c16<StageL<0, 0, T_, 128, K_>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd, Skd); \
+        else if (RO == 64) dispatch_pf_c16<StageL<0, 0, T_, 64, K_>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd, Skd); \
+        else dispatch_pf_c16<StageL<0, 0, T_, 32, K_>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd, Skd); \
+    } while (0)
 #define SW_STG(K_) \
     do { \
-        if (RO == 128) dispatch_pf_c16<StageL<0, 0, DG_TT, 128, K_>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd, Skd); \
-        else if (RO == 64) dispatch_pf_c16<StageL<0, 0, DG_TT, 64, K_>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd, Skd); \
-        else dispatch_pf_c16<StageL<0, 0, DG_TT, 32, K_>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd, Skd); \
+        if (tt == 1) SW_STG_T(1, K_); \
+        else SW_STG_T(DG_TT, K_); \
     } while (0)
         if (skd == 1) SW_STG(1);
         else if (skd == 2) SW_STG(2);
         else SW_STG(0);
 #undef SW_STG
+#undef SW_STG_T
     } else {
         const size_t lds = lds_max(dot8_glu_lds(W.K, 1), shl);
         if (!route_src) dispatch_pf_c16<StageL<1, 0, 1>::L>(pf, c16, grid, lds, st, A, nbx, nglu, Sd, Skd);

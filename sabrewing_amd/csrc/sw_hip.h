@@ -138,6 +138,7 @@ struct SwGroups {
     // a block then takes one pass of up to DG_TT tokens from t0 instead of a whole group
     const int *items;
     const int *P;
+    int tt;                          // tokens per pass of the items (1 or 2; 0: SW_DG_TT)
 };
 #define SW_DG_TT 2             // tokens per weight pass of the grouped dot8 kernels
 // route activations whose gate is a softmax of the logits (computed with the
