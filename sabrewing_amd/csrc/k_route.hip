@@ -256,16 +256,21 @@ __global__ __launch_bounds__(BK_THREADS) void k_gate_bucket(const float *__restr
                                                             int use_bias, int norm, int *__restrict__ sel_all,
                                                             float *__restrict__ w_all, SwGateOpt o, BucketArgs B) {
     __shared__ uint64_t tab[32];
+    __shared__ int lsel[GB_MAXS * 64];                // the picks again, for the bucketing
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     for (int s = wave; s < S; s += BK_THREADS / 64) {
         int sk;
         float wk;
         gate_topk_wave<NPER>((sw_act_softmax(act) ? logits : scores) + (int64_t)s * o.ld, E, K, act, bias, use_bias, norm,
                              tab, sk, wk, o.ns, o.rs, o.wsh ? o.wsh + (int64_t)s * o.wshld : nullptr);
-        if (lane < K) { sel_all[(int64_t)s * K + lane] = sk; w_all[(int64_t)s * o.wld + lane] = wk; }
+        if (lane < K) {
+            sel_all[(int64_t)s * K + lane] = sk;
+            w_all[(int64_t)s * o.wld + lane] = wk;
+            lsel[s * K + lane] = sk;
+        }
     }
-    __syncthreads();                                  // the block's picks are written
-    bucket_block(sel_all, S * K, K, E, B);
+    __syncthreads();                                  // the block's picks are in LDS
+    bucket_block(lsel, S * K, K, E, B);
 }
 
 int sw_launch_gate_bucket(hipStream_t st, const float *logits, const float *scores, int S, int E, int K, int route_act,
