@@ -1,7 +1,7 @@
 """Parity at the benchmark's full configurations, on
 device-generated layers:
 
-  * C3: the C2 layer at batch 8, 32 and 64 -- routing identical to the oracle's,
+  * C3: the C2 layer at batch 4, 8, 32 and 64 -- routing identical to the oracle's,
     the layer within the tolerance, and every stream of the batch bit-identical
     to its own single-stream call;
   * C4: 2048-token prefill (the grouped GEMMs on the int8 MFMA), with the softplus
@@ -78,10 +78,11 @@ def check_layer(be, orc, cfg, seed, S_, sample=None):
         dl.free()
 
 
-@pytest.mark.parametrize("B", [8, 32, 64])
+@pytest.mark.parametrize("B", [4, 8, 32, 64])
 def test_c3_batches(be, orc, B):
     """C3: the C2 layer (softplus gate, K=10, shared expert) at B streams; every
-    stream checked against its single-stream output"""
+    stream checked against its single-stream output.  B = 4 takes the grouped kernels'
+    one-token passes (40 pairs of 256 experts) with the shared expert's batch blocks"""
     check_layer(be, orc, cf.C2, 7100 + B, B)
 
 
