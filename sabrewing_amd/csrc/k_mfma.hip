@@ -340,8 +340,8 @@ __global__ __launch_bounds__(MF_NT, 1) void k_mf(MfArgs A) {
 
     stage_load(0);
     stage_store(0);
-    __syncthreads();
     if (NC > 1) stage_load(1);
+    __syncthreads();
     for (int c = 0; c < NCV; c++) {
         if (wact) {
             if (FULL || c < NC) chunk_q(MfIc<1>{}, c);
