@@ -162,14 +162,23 @@ __device__ __forceinline__ void bucket_block(const int *__restrict__ sel, int T,
     int *__restrict__ grow = B.grow, *__restrict__ rowof = B.rowof, *__restrict__ items = B.items, *__restrict__ Pout = B.Pout;
     const int tt = B.tt;
     __shared__ int cnt[BK_MAXE], run[BK_MAXE], sa[BK_MAXE], sb[BK_MAXE], sp[BK_MAXE];
-    __shared__ uint8_t wcnt[BK_THREADS / 64][BK_MAXE];
+    __shared__ uint8_t wcnt[2][BK_THREADS / 64][BK_MAXE];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     for (int i = tid; i < E; i += BK_THREADS) {
         cnt[i] = 0;
-        for (int w = 0; w < BK_THREADS / 64; w++) wcnt[w][i] = 0;
+        for (int w = 0; w < BK_THREADS / 64; w++) wcnt[0][w][i] = wcnt[1][w][i] = 0;
     }
     __syncthreads();
-    for (int p = tid; p < T; p += BK_THREADS) atomicAdd(&cnt[sel[p]], 1);
+    // counts: eight picks' loads in flight per thread before their atomics (one load latency
+    // per 8 BK_THREADS picks instead of one per BK_THREADS)
+    for (int p0 = tid; p0 < T; p0 += 8 * BK_THREADS) {
+        int v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v[u] = p0 + u * BK_THREADS < T ? sel[p0 + u * BK_THREADS] : 0;
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            if (p0 + u * BK_THREADS < T) atomicAdd(&cnt[v[u]], 1);
+    }
     __syncthreads();
     // inclusive scans of cnt (packed offsets), of cnt > 0 (group index) and of the
     // passes ceil(cnt / tt) (pass list offsets), expert tid by thread tid: a shuffle
@@ -204,29 +213,56 @@ __device__ __forceinline__ void bucket_block(const int *__restrict__ sel, int T,
     int nbits = 0;
     while ((1 << nbits) < E) nbits++;
     const unsigned long long lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-    for (int base = 0; base < T; base += BK_THREADS) {
-        const int p = base + tid;
-        const bool act = p < T;
-        const int e = act ? sel[p] : 0;
-        unsigned long long peers = __ballot(act);
-        for (int b = 0; b < nbits; b++) {
-            const unsigned long long m = __ballot(act && ((e >> b) & 1));
-            peers &= ((e >> b) & 1) ? m : ~m;
+    // the picks in rounds of two halves of BK_THREADS (pair base + h BK_THREADS + tid), three
+    // barriers a round: a pair's slot is its expert's run, plus its expert's pairs in the
+    // round's first half (for h = 1), in the earlier waves of its half, and in its wave
+    // before its lane -- the pairs' own order (stable)
+    // (the next round's picks are loaded while a round runs)
+    auto pick = [&](int p) { return p < T ? sel[p] : 0; };
+    int en[2] = {pick(tid), pick(BK_THREADS + tid)};
+    for (int base = 0; base < T; base += 2 * BK_THREADS) {
+        const int nh = base + BK_THREADS < T ? 2 : 1;          // uniform over the block
+        int e[2], rank[2];
+        bool act[2];
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            act[h] = h < nh && base + h * BK_THREADS + tid < T;
+            e[h] = act[h] ? en[h] : 0;
         }
-        const int rank = __popcll(peers & lt);
-        if (act && rank == 0) wcnt[wave][e] = (uint8_t)__popcll(peers);
+        en[0] = pick(base + 2 * BK_THREADS + tid);
+        en[1] = pick(base + 3 * BK_THREADS + tid);
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            rank[h] = 0;
+            if (h < nh) {
+                unsigned long long peers = __ballot(act[h]);
+                for (int b = 0; b < nbits; b++) {
+                    const unsigned long long m = __ballot(act[h] && ((e[h] >> b) & 1));
+                    peers &= ((e[h] >> b) & 1) ? m : ~m;
+                }
+                rank[h] = __popcll(peers & lt);
+                if (act[h] && rank[h] == 0) wcnt[h][wave][e[h]] = (uint8_t)__popcll(peers);
+            }
+        }
         __syncthreads();
-        if (act) {
-            int pre = 0;
-            for (int w = 0; w < wave; w++) pre += wcnt[w][e];
-            const int slot = run[e] + pre + rank;
-            grow[slot] = p / K;
-            rowof[p] = slot;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            if (act[h]) {
+                const int p = base + h * BK_THREADS + tid;
+                int pre = 0;
+                if (h == 1)
+                    for (int w = 0; w < BK_THREADS / 64; w++) pre += wcnt[0][w][e[h]];
+                for (int w = 0; w < wave; w++) pre += wcnt[h][w][e[h]];
+                const int slot = run[e[h]] + pre + rank[h];
+                grow[slot] = p / K;
+                rowof[p] = slot;
+            }
         }
         __syncthreads();
         for (int i = tid; i < E; i += BK_THREADS) {
             int tot = 0;
-            for (int w = 0; w < BK_THREADS / 64; w++) { tot += wcnt[w][i]; wcnt[w][i] = 0; }
+            for (int h = 0; h < nh; h++)
+                for (int w = 0; w < BK_THREADS / 64; w++) { tot += wcnt[h][w][i]; wcnt[h][w][i] = 0; }
             run[i] += tot;
         }
         __syncthreads();
