@@ -194,7 +194,8 @@ __global__ __launch_bounds__(MF_NT, 1) void k_mf(MfArgs A) {
     // staging roles by whole waves; for gate_up rotated so that in a tile of 1-3 token tiles the
     // computing waves (token tiles tt < nact: waves 0 .. 4 nact - 1) take the roles with no work
     // (the digits of token tiles that do not compute are not staged) or the lightest (C4:
-    // gate_up 2.11 -> 2.04 ms; the down launch, 8 chunks, ran 2% slower with it)
+    // gate_up 2.11 -> 2.04 ms; the down launch, 8 chunks, ran 1-2% slower with it, also when
+    // rotated for one-column tiles only)
     const int nact = (nt + 15) >> 4;
     const int rot = GLU ? (nact == 1 ? 10 : nact < 4 ? 8 : 0) : 0;
     const int st = (tid + 64 * rot) & (MF_NT - 1);
