@@ -332,7 +332,8 @@ int sw_launch_gate_bucket(hipStream_t st, const float *logits, const float *scor
 }
 
 // ------------------------------------------------------------ combine ----
-// every (token, 4 outputs) by combine4 (sw_hip.h)
+// every (token, 4 outputs) by combine4 (sw_hip.h); the slots, read once, with nontemporal
+// loads (C4: 78.5 -> 70.4 us)
 __global__ void k_combine(const float *__restrict__ slots, const int *__restrict__ rowof, const float *__restrict__ w,
                           int S, int K, int D, float route_scale, const float *__restrict__ shared,
                           float *__restrict__ out, int accumulate, const float *__restrict__ wsh, int ns) {
@@ -340,7 +341,7 @@ __global__ void k_combine(const float *__restrict__ slots, const int *__restrict
     for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n4; i += (int64_t)gridDim.x * blockDim.x) {
         const int64_t s = i / (D / 4);
         const int d = (int)(i % (D / 4)) * 4;
-        combine4(slots, rowof, w, s, K, D, d, route_scale, shared, out, accumulate, wsh, ns);
+        combine4<1>(slots, rowof, w, s, K, D, d, route_scale, shared, out, accumulate, wsh, ns);
     }
 }
 

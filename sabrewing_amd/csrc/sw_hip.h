@@ -73,6 +73,8 @@ __device__ __forceinline__ float sw_ld4f(sw_rsrc r, uint32_t voff, uint32_t soff
 // operation sequence of moe_block's `acc[i] += w[a] * scr[i]` as the reference
 // build compiles it (c/moe_block.h:124-142; c/laguna.c:761-782); with wsh,
 // Inkling's ns gated shared outputs shared[s][ns][D] follow as fma(wsh[s,j], .).
+// NTL: the slots with nontemporal loads (slots that no later launch reads).
+template <int NTL = 0>
 __device__ __forceinline__ void combine4(const float *__restrict__ slots, const int *__restrict__ rowof,
                                          const float *__restrict__ w, int64_t s, int K, int D, int d, float route_scale,
                                          const float *__restrict__ shared, float *__restrict__ out, int accumulate,
@@ -85,7 +87,9 @@ __device__ __forceinline__ void combine4(const float *__restrict__ slots, const 
         for (int u = 0; u < 8; u++) {
             if (a0 + u < K) {
                 wa[u] = w[s * K + a0 + u];
-                v[u] = *(const sw_f32x4 *)(slots + (int64_t)rowof[s * K + a0 + u] * D + d);
+                const sw_f32x4 *sp = (const sw_f32x4 *)(slots + (int64_t)rowof[s * K + a0 + u] * D + d);
+                if constexpr (NTL) v[u] = __builtin_nontemporal_load(sp);
+                else v[u] = *sp;
             }
         }
 #pragma unroll
