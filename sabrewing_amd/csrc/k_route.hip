@@ -332,8 +332,11 @@ int sw_launch_gate_bucket(hipStream_t st, const float *logits, const float *scor
 }
 
 // ------------------------------------------------------------ combine ----
-// every (token, 4 outputs) by combine4 (sw_hip.h); the slots, read once, with nontemporal
-// loads (C4: 78.5 -> 70.4 us)
+// every (token, 4 outputs) by combine4 (sw_hip.h); NTL: the slots with nontemporal loads,
+// for slot arrays beyond the caches (C4, 335 MB: 78.5 -> 70.4 us; a decode batch's few MB,
+// still in L2 from the down launch, read slower so: 13.3 -> 15.5 us at B = 32)
+#define CB_NT_BYTES (64ll << 20)
+template <int NTL>
 __global__ void k_combine(const float *__restrict__ slots, const int *__restrict__ rowof, const float *__restrict__ w,
                           int S, int K, int D, float route_scale, const float *__restrict__ shared,
                           float *__restrict__ out, int accumulate, const float *__restrict__ wsh, int ns) {
@@ -341,7 +344,7 @@ __global__ void k_combine(const float *__restrict__ slots, const int *__restrict
     for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n4; i += (int64_t)gridDim.x * blockDim.x) {
         const int64_t s = i / (D / 4);
         const int d = (int)(i % (D / 4)) * 4;
-        combine4<1>(slots, rowof, w, s, K, D, d, route_scale, shared, out, accumulate, wsh, ns);
+        combine4<NTL>(slots, rowof, w, s, K, D, d, route_scale, shared, out, accumulate, wsh, ns);
     }
 }
 
@@ -349,8 +352,13 @@ int sw_launch_combine(hipStream_t st, const float *slots, const int *rowof, cons
                       float route_scale, const float *shared, float *out, int accumulate, const float *wsh, int ns) {
     if (D % 4 || S <= 0 || (wsh && (!shared || ns <= 0))) return -1;
     const int64_t n4 = (int64_t)S * (D / 4);
-    SW_LAUNCH(k_combine, dim3((unsigned)sw_imin64((n4 + 255) / 256, 4096)), dim3(256), 0, st, slots, rowof, w,
-                       S, K, D, route_scale, shared, out, accumulate, wsh, ns);
+    const dim3 grid((unsigned)sw_imin64((n4 + 255) / 256, 4096));
+    if ((int64_t)S * K * D * 4 >= CB_NT_BYTES)
+        SW_LAUNCH(k_combine<1>, grid, dim3(256), 0, st, slots, rowof, w, S, K, D, route_scale, shared, out, accumulate,
+                  wsh, ns);
+    else
+        SW_LAUNCH(k_combine<0>, grid, dim3(256), 0, st, slots, rowof, w, S, K, D, route_scale, shared, out, accumulate,
+                  wsh, ns);
     return launch_err();
 }
 
