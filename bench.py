@@ -26,6 +26,9 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+# MI355X dense bf16 MFMA (the peak BASELINE prices the prefill at; the kernels issue int8
+# MFMAs, 4 per int4 multiply-add of the layer, against a 5.0 P op/s int8 peak)
+MFMA_PEAK_TFS = 2500.0
 # what the kernels compute in: int4 weights and their f32 group scales against the
 # activations written per 32 inputs as integers of 7 signed base-8 digits (held as 6
 # base-16 limbs) under a power-of-two factor (exact integer dots, |input error| <= 2^-21
@@ -69,6 +72,12 @@ def kernel_bytes(cfg, S, G):
              "q4_down": dn_w + T * limb(I) + T * D * 4,
              "combine": T * D * 4 + 2 * S * D * 4 + (S * D * 4 if cfg.shared_mode else 0) + T * 8}
         b["gate_bucket"] = b["gate_topk"] + b["bucket"]      # (one launch up to 8 tokens)
+        # prefill-sized batches: the grouped GEMMs on the int8 MFMA over MFMA digits (128
+        # bytes + one f32 factor per 32 inputs)
+        dig = lambda n: n // 32 * (128 + 4)
+        b["digits"] = S * D * 4 + S * dig(D)
+        b["mf_glu"] = gu_w + S * dig(D) + T * dig(I)
+        b["mf_down"] = dn_w + T * dig(I) + T * D * 4
         if cfg.shared_mode:
             b["shared_glu"] = sh_gu + S * D * 4 + S * Is * 6
             b["shared_down"] = sh_dn + S * Is * 6 + S * D * 4
@@ -81,6 +90,18 @@ def kernel_bytes(cfg, S, G):
                 b["stage_route"] += sh_gu + S * Is * 6
                 b["stage_experts"] += b["shared_down"]
     return b
+
+
+def kernel_flops(cfg, S):
+    """algorithmic flops (2 per multiply-add of the layer's own arithmetic) per launch of
+    the kernels that run on the MFMA"""
+    D, I, Is, E, K = cfg.D, cfg.I, cfg.Is, cfg.E, cfg.K
+    T = S * K
+    f = {"mf_glu": 2 * T * 2 * I * D, "mf_down": 2 * T * D * I, "router_tiles": 2 * S * E * D}
+    if cfg.shared_mode:
+        f["shared_glu"] = 2 * S * 2 * Is * D
+        f["shared_down"] = 2 * S * D * Is
+    return f
 
 
 def cpu_baseline(be, cfg, dl, xs, seconds):
@@ -189,75 +210,96 @@ def per_row_modes(be, cfg, dl, xs, seconds, steps):
     return out
 
 
-def run_stack(args):
-    """--config C5-stack: the Config-5 decode step -- 48 resident MoE layers
-    (D=4096, E=256, top-8 softmax, I=1536, no shared expert), h += MoE(rmsnorm(h))
-    each, then rmsnorm, the bf16 4096x32000 head and the greedy pick, for a
-    batch of C5_BATCH streams."""
+def stack_result(be, args, steps, warmup):
+    """The Config-5 decode step -- 48 resident MoE layers (D=4096, E=256, top-8
+    softmax, I=1536, no shared expert), h += MoE(rmsnorm(h)) each, then rmsnorm,
+    the bf16 4096x32000 head and the greedy pick, for a batch of C5_BATCH streams:
+    W eager warmup steps, K timed steps (eager, then recorded as one graph and
+    replayed), per-kernel launch times; the stack is freed before returning."""
     from sabrewing_amd import configs as cf
-    from sabrewing_amd.backend import Backend, gen_x
+    from sabrewing_amd.backend import gen_x
     from sabrewing_amd.stack import DeviceStack
     cfg, L, V = cf.C5_LAYER, args.layers_stack, cf.C5_VOCAB
-    B = args.batch or cf.C5_BATCH
-    be = Backend(0)
-    be.set_grouped_kernel({"auto": 0, "dot8": 1, "mfma": 2}[args.grouped])
+    B = args.batch if args.config == "C5-stack" and args.batch else cf.C5_BATCH
     t0 = time.time()
     st = DeviceStack.generate(be, cfg, L, V, args.seed)
     log(f"generated the {L}-layer stack ({L * cfg.expert_bytes() * cfg.E / 1e9:.1f} GB of experts) in {time.time() - t0:.1f}s")
     D = cfg.D
-    nx = args.warmup + args.steps
+    nx = warmup + steps
     xs = gen_x(be, cfg, args.seed, B * nx)
     h, xn, lg, tok = be.alloc(B * D * 4), be.alloc(B * D * 4), be.alloc(B * V * 4), be.alloc(B * 4)
+    try:
+        def step(i):
+            be.check(be.lib.lag_hip_d2d(int(h), int(xs) + i * B * D * 4, B * D * 4), "d2d")
+            st.step(h, xn, lg, tok, B)
 
-    def step(i):
-        be.check(be.lib.lag_hip_d2d(int(h), int(xs) + i * B * D * 4, B * D * 4), "d2d")
-        st.step(h, xn, lg, tok, B)
-
-    for i in range(args.warmup):
-        step(i)
-    be.sync()
-    ev0, ev1 = be.event(), be.event()
-    be.record(ev0)
-    for i in range(args.steps):
-        step(args.warmup + i)
-    be.record(ev1)
-    be.sync()
-    ms_eager = be.elapsed_ms(ev0, ev1) / args.steps
-    ms = ms_eager
-    if not args.eager:
-        # the same K steps recorded once and replayed with one submission (as the B=1
-        # line): the device time of the steps without the host's per-launch cost
-        be.graph_begin()
-        for i in range(args.steps):
-            step(args.warmup + i)
-        g = be.graph_end()
-        be.graph_launch(g)
+        for i in range(warmup):
+            step(i)
         be.sync()
+        ev0, ev1 = be.event(), be.event()
         be.record(ev0)
-        be.graph_launch(g)
+        for i in range(steps):
+            step(warmup + i)
         be.record(ev1)
         be.sync()
-        be.graph_destroy(g)
-        ms = be.elapsed_ms(ev0, ev1) / args.steps
-    log(f"C5 stack B={B}: {ms * 1e3:.0f} us/step ({'eager' if args.eager else 'graph replay'}; eager {ms_eager * 1e3:.0f})")
-    be.profile_reset(); be.profile(True)
-    step(0); be.sync()
-    prof = be.profile_read(); be.profile(False)
-    kern = {k: {"avg_us": round(1e3 * v[0] / max(v[1], 1), 2), "launches": v[1]} for k, v in prof.items()}
+        ms_eager = be.elapsed_ms(ev0, ev1) / steps
+        ms = ms_eager
+        if not args.eager:
+            # the same K steps recorded once and replayed with one submission (as the B=1
+            # line): the device time of the steps without the host's per-launch cost
+            be.graph_begin()
+            for i in range(steps):
+                step(warmup + i)
+            g = be.graph_end()
+            be.graph_launch(g)
+            be.sync()
+            be.record(ev0)
+            be.graph_launch(g)
+            be.record(ev1)
+            be.sync()
+            be.graph_destroy(g)
+            ms = be.elapsed_ms(ev0, ev1) / steps
+        log(f"C5 stack B={B}: {ms * 1e3:.0f} us/step ({'eager' if args.eager else 'graph replay'}; eager {ms_eager * 1e3:.0f})")
+        be.profile_reset(); be.profile(True)
+        step(0); be.sync()
+        prof = be.profile_read(); be.profile(False)
+        kern = {k: {"avg_us": round(1e3 * v[0] / max(v[1], 1), 2), "launches": v[1]} for k, v in prof.items()}
+        # algorithmic bytes of a step: each layer's distinct experts (counted on the
+        # profiled step), its router, the head, the activations
+        head = V * D * 2
+        G_mean = cfg.E * (1.0 - (1.0 - 1.0 / cfg.E) ** (B * cfg.K))         # expected distinct experts per layer
+        step_bytes = L * (G_mean * cfg.expert_bytes() + cfg.router_bytes() + 4 * B * D * 4) + head
+        gbs = step_bytes / (ms * 1e-3) / 1e9
+        return {"workload": "C5-stack", "batch": B, "layers": L, "hidden": D, "experts": cfg.E, "topk": cfg.K,
+                "moe_inter": cfg.I, "vocab": V, "ms_per_step": round(ms, 4), "eager_ms_per_step": round(ms_eager, 4),
+                "tokens_per_s": round(B / (ms * 1e-3), 1), "steps": steps, "warmup": warmup,
+                "submission": "eager" if args.eager else "graph replay of the timed steps",
+                "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                             "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_step": int(step_bytes),
+                             "bytes_note": "48 x (expected distinct experts E(1-(1-1/E)^(B K)) x expert bytes + router) "
+                                           "+ the bf16 head + activations"},
+                "kernels": kern}
+    finally:
+        for b_ in (h, xn, lg, tok, xs):
+            b_.free()
+        st.free()
+
+
+def run_stack(args):
+    """--config C5-stack: the stack step alone, as its own JSON line."""
+    from sabrewing_amd.backend import Backend
+    be = Backend(0)
+    be.set_grouped_kernel({"auto": 0, "dot8": 1, "mfma": 2}[args.grouped])
+    r = stack_result(be, args, args.steps, args.warmup)
     res = {"metric": "Config-5 stack decode tokens/s (48 int4 MoE layers + RMSNorm + bf16 head + greedy pick)",
-           "value": round(B / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
-           "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
-           "vs_baseline": None, "dtype": DTYPE,
-           "submission": "eager" if args.eager else "graph replay of the timed steps",
-           "eager_ms_per_step": round(ms_eager, 4),
+           "value": r["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+           "warmup": args.warmup, "ms_per_step": r["ms_per_step"], "higher_is_better": True, "scaling": "weak",
+           "vs_baseline": None, "dtype": DTYPE, "submission": r["submission"],
+           "eager_ms_per_step": r["eager_ms_per_step"],
            "data": "synthetic: seeded N(0,0.02) weights generated on device, N(0,1) bf16-valued tokens",
-           "config": {"workload": "C5-stack", "batch": B, "layers": L, "hidden": D, "experts": cfg.E, "topk": cfg.K,
-                      "moe_inter": cfg.I, "vocab": V},
-           "kernels": kern}
+           "config": {k: r[k] for k in ("workload", "batch", "layers", "hidden", "experts", "topk", "moe_inter", "vocab")},
+           "roofline": r["roofline"], "kernels": r["kernels"]}
     print(json.dumps(res), flush=True)
-    for b in (h, xn, lg, tok, xs):
-        b.free()
-    st.free()
 
 
 def run_coli(args):
@@ -412,11 +454,15 @@ def measure(be, cfg, layers, B, args, seed, profile=True):
         prof = be.profile_read()
         be.profile(False)
         kb = kernel_bytes(cfg, B, G)
+        kf = kernel_flops(cfg, B) if B > 1 else {}
         kern = {k: {"avg_us": 1e3 * v[0] / max(v[1], 1), "launches": v[1]} for k, v in prof.items()}
         for k, v in kern.items():
             if k in kb:
                 v["bytes"] = kb[k]
                 v["GBs"] = kb[k] / (v["avg_us"] * 1e-6) / 1e9 if v["avg_us"] > 0 else 0.0
+            if k in kf:
+                v["flops"] = kf[k]
+                v["TFs"] = kf[k] / (v["avg_us"] * 1e-6) / 1e12 if v["avg_us"] > 0 else 0.0
         dom = max(kern, key=lambda k: kern[k]["avg_us"] * kern[k]["launches"])
         dk = kern[dom]
         # HBM bytes per launch of that kernel as rocprofv3 counted them (FETCH_SIZE x2 + WRITE_SIZE,
@@ -430,9 +476,19 @@ def measure(be, cfg, layers, B, args, seed, profile=True):
         r["G"] = G
         r["layer_bytes"] = cfg.step_bytes(B, G)
         r["layer_gbs"] = r["layer_bytes"] / (r["ms"] * 1e-3) / 1e9
-        r["roofline"] = {"bound": "hbm", "kernel": dom, "achieved": round(dk.get("GBs", 0.0), 1), "peak": HBM_PEAK_GBS,
-                         "unit": "GB/s", "frac": round(dk.get("GBs", 0.0) / HBM_PEAK_GBS, 4), "traffic": traffic,
-                         "bytes_per_launch": dk.get("bytes"), "avg_launch_us": round(dk["avg_us"], 2)}
+        if dom.startswith("mf_"):
+            # the prefill's grouped GEMMs on the MFMA: useful flops over the launch time
+            r["roofline"] = {"bound": "mfma", "kernel": dom, "achieved": round(dk["TFs"], 1), "peak": MFMA_PEAK_TFS,
+                             "unit": "TFLOP/s", "frac": round(dk["TFs"] / MFMA_PEAK_TFS, 4), "traffic": traffic,
+                             "flops_per_launch": dk["flops"], "bytes_per_launch": dk.get("bytes"),
+                             "hbm_GBs": round(dk.get("GBs", 0.0), 1), "avg_launch_us": round(dk["avg_us"], 2)}
+        else:
+            r["roofline"] = {"bound": "hbm", "kernel": dom, "achieved": round(dk.get("GBs", 0.0), 1),
+                             "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(dk.get("GBs", 0.0) / HBM_PEAK_GBS, 4),
+                             "traffic": traffic, "bytes_per_launch": dk.get("bytes"), "avg_launch_us": round(dk["avg_us"], 2)}
+        # the layer's own floor: its flops at the MFMA peak or its bytes at the HBM peak
+        r["layer_flops"] = cfg.flops(B)
+        r["floor_us"] = max(cfg.flops(B) / (MFMA_PEAK_TFS * 1e12), r["layer_bytes"] / (HBM_PEAK_GBS * 1e9)) * 1e6
         r["kernels"] = {k: {kk: (round(vv, 2) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                         for k, v in kern.items()}
         log(f"B={B} kernels:", json.dumps(r["kernels"]))
@@ -455,6 +511,56 @@ def measure(be, cfg, layers, B, args, seed, profile=True):
         for o in outs:
             o.free()
         xbuf.free()
+
+
+def extra_objects(be, args):
+    """C1 at batch 1, C4's 2048-token prefill (softplus and Zipf(1.1) routers) and the
+    C5 48-layer stack at batch 8, measured in the same run as the headline line (the
+    same timing: eager warmup, then the timed steps as one graph replay)."""
+    from argparse import Namespace
+    from sabrewing_amd import configs as cf
+    from sabrewing_amd.backend import DeviceLayer
+    out = {}
+
+    def layers_of(cfg, n, seed):
+        ls = []
+        for l in range(n):
+            dl = DeviceLayer.generate(be, cfg, seed, layer=l)
+            dl.seed, dl.layer = seed, l
+            ls.append(dl)
+        return ls
+
+    # C1: the OLMoE-shaped layer, one token per step, 12 layers rotated (each step reads
+    # 8 of a layer's 64 experts; 12 layers hold 3 GB)
+    ls = layers_of(cf.C1, args.layers, args.seed + 11)
+    try:
+        r = measure(be, cf.C1, ls, 1, args, args.seed + 13)
+        out["c1_b1"] = {"workload": cf.C1.name, "hidden": cf.C1.D, "experts": cf.C1.E, "topk": cf.C1.K,
+                        "moe_inter": cf.C1.I, "gs": cf.C1.gs, "router": "f32", **batch_summary(cf.C1, r),
+                        "kernels": r["kernels"]}
+    finally:
+        for dl in ls:
+            dl.free()
+    # C4: 2048 tokens in one chunk; every step reads all 256 experts (2 GB), two layers rotated
+    pa = Namespace(**{**vars(args), "steps": min(args.steps, 20), "warmup": min(args.warmup, 5)})
+    pre = {}
+    for cfg in (cf.C2, cf.C4_ZIPF):
+        ls = layers_of(cfg, 2, args.seed + 17)
+        try:
+            r = measure(be, cfg, ls, 2048, pa, args.seed + 19)
+            pre[cfg.name] = {"workload": cfg.name, "tokens": 2048, "zipf": cfg.zipf, **batch_summary(cfg, r),
+                             "layer_flops": r["layer_flops"], "floor_us": round(r["floor_us"], 1),
+                             "layer_roofline_frac": round(r["floor_us"] * 1e-3 / r["ms"], 4), "kernels": r["kernels"]}
+        finally:
+            for dl in ls:
+                dl.free()
+    out["prefill"] = {"steps": pa.steps, "warmup": pa.warmup,
+                      "note": "layer_roofline_frac = max(layer flops at the 2.5 PF/s bf16 MFMA peak, layer bytes at "
+                              "8 TB/s) / measured step time; roofline = the dominant kernel",
+                      **pre}
+    # C5: the 48-layer stack (145 GB of experts), batch 8
+    out["stack"] = stack_result(be, args, min(args.steps, 20), min(args.warmup, 5))
+    return out
 
 
 def batch_summary(cfg, r):
@@ -499,6 +605,15 @@ def run(args):
     if not args.no_sweep and B == 1:
         for b in (8, 32, 64):
             sweep[b] = measure(be, cfg, layers, b, args, args.seed + 101 * b)
+
+    # the other BASELINE configurations, each on device layers of its own (freed before
+    # the next; the first C2 layer stays for the CPU baseline below)
+    extra = {}
+    if not args.no_extra and B == 1 and cfg.name == "C2-laguna-softplus":
+        for dl in layers[1:]:
+            dl.free()
+        layers = layers[:1]
+        extra = extra_objects(be, args)
 
     # the CPU side last: the OpenMP team it starts pins the host thread (OMP_PROC_BIND)
     cpu = None
@@ -555,6 +670,7 @@ def run(args):
                           "target_ratio": 8.0}
     if sweep:
         res["batch_sweep"] = {str(b): batch_summary(cfg, v) for b, v in sweep.items()}
+    res.update(extra)
     print(json.dumps(res), flush=True)
     for dl in layers:
         dl.free()
@@ -579,6 +695,8 @@ def main():
     ap.add_argument("--eager", action="store_true",
                     help="time the per-call submission only (default: also record the steps as one graph and time its replay)")
     ap.add_argument("--no-sweep", action="store_true", help="B=1 only (no batch 8/32/64 objects)")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="no C1 / C4 prefill / C5 stack objects in the headline line")
     ap.add_argument("--timed-only", action="store_true",
                     help="stop after the timed steps (no per-kernel pass, no CPU baseline, no JSON line)")
     args = ap.parse_args()

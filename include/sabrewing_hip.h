@@ -19,7 +19,8 @@
  *                           residual), device activations, the descriptor of
  *                           c/moe_arch.h:33-41.
  *
- * Like the reference backend: one device and one stream per process, results
+ * Like the reference backend: one device and one stream per process (a second
+ * lag_hip_init naming another device fails), results
  * valid on return for the host-pointer entries, not thread-safe.
  * COLI_GPU_FAIL_AFTER=N makes every compute entry fail after N successful
  * calls (the reference's fault-injection hook, c/backend_cuda.cu:684-693). */
@@ -68,12 +69,12 @@ int    lag_hip_matmul_q8_s(float *y, const float *x, const void *q8, const void 
  * (c/moe_matmul.h:66-89, vdpbf16ps); I % 32 != 0 takes the f32-activation
  * contract, as the CPU does */
 int    lag_hip_matmul_bf16_rx(float *y, const float *x, const void *W, int S, int I, int O);
-/* Numerics of the host-activation matmuls: calls of up to 64 rows reproduce the
- * reference CPU's SIMD contracts bit for bit -- matmul_bf16 the 16 f32-activation
- * lanes of c/moe_matmul.h:92-110, matmul_q4 (per-row scales) matmul_q4_k's F32
- * lanes (c/moe_quant.h:85-109), matmul_q8 matmul_q8_k's F32 lanes
- * (c/moe_quant.h:378-391), matmul_bf16_rx the vdpbf16ps lanes; larger calls of
- * matmul_bf16 / matmul_q4 run on the MFMA GEMMs (within 1e-5 relative). */
+/* Numerics of the host-activation matmuls: every call, whatever its row count,
+ * reproduces the reference CPU's SIMD contracts bit for bit -- matmul_bf16 the
+ * 16 f32-activation lanes of c/moe_matmul.h:92-110, matmul_q4 (per-row scales)
+ * matmul_q4_k's F32 lanes (c/moe_quant.h:85-109), matmul_q8 matmul_q8_k's F32
+ * lanes (c/moe_quant.h:378-391), matmul_bf16_rx the vdpbf16ps lanes -- so a
+ * token's result does not depend on how many rows share its call. */
 
 /* ---------------- 2. group-scaled int4 forms (scale[o*ng + g], ng = I/gs) ---------------- */
 int    lag_hip_matmul_q4_g(float *y, const float *x, const void *packed, const void *scale,
@@ -159,11 +160,18 @@ int    lag_hip_moe_forward(const LagHipMoeDesc *d, const LagHipMoeWeights *w, co
  * the process ends) instead of the growing arena; the call makes no
  * hipMalloc/hipFree and no other allocation.  A shape whose scratch does not
  * fit returns -1 before any launch (lag_hip_last_error gives the bytes it
- * needed): the C2 layer (D=4096, E=256, K=10, I=Is=1024) fits up to S = 64.
+ * needed): the C2 layer (D=4096, E=256, K=10, I=Is=1024) fits up to S = 78
+ * (up to S = 66 with lag_hip_set_q4_mode(1) on per-row scales, which also
+ * keeps int8 activations and an f32 h).
  * Same results, bit for bit, as lag_hip_moe_forward.  Every call on a device
  * shares that device's array, so calls that overlap on one device race. */
 #define LAG_HIP_NOALLOC_SCRATCH_BYTES ((size_t)24 << 20)
 int    lag_hip_moe_forward_noalloc(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const float *x, float *out, int S);
+/* The device scratch bytes lag_hip_moe_forward(_noalloc) needs for S tokens of
+ * this layer in the current q4 mode (0 = unsupported descriptor or shape).
+ * Host arithmetic only: callable before lag_hip_init and without a device, so a
+ * caller can size its batches to the fixed region above. */
+size_t lag_hip_moe_forward_scratch_bytes(const LagHipMoeDesc *d, const LagHipMoeWeights *w, int S);
 /* the same with host x/out; synchronous */
 int    lag_hip_moe_block(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const float *x, float *out, int S);
 /* routing only (device pointers): logits [S,E] (may be NULL), sel [S,K], w [S,K];
@@ -219,6 +227,9 @@ void   lag_hip_event_destroy(void *ev);
  * finished recording owns the backend scratch it was recorded over until
  * lag_hip_graph_destroy (which waits for the stream, then frees it); later
  * calls of any size allocate their own, so they never disturb a live graph.
+ * A recording begun right after another one gets fresh scratch of the same
+ * capacity, so same-shaped graphs can be recorded back to back.  A destroy
+ * issued while a recording is open takes effect when that recording ends.
  * No counterpart in the reference (its decode loop launches per layer): this
  * is the launch-overhead-free way to drive a decode step. */
 int    lag_hip_graph_begin(void);

@@ -27,6 +27,7 @@ EXPORTS = [
     "lag_hip_matmul_q8", "lag_hip_matmul_q8_s", "lag_hip_matmul_bf16_rx",
     "lag_hip_matmul_q4_g", "lag_hip_expert_q4_g", "lag_hip_moe_experts_g", "lag_hip_moe_group_g",
     "lag_hip_router_upload", "lag_hip_router_chain", "lag_hip_moe_forward", "lag_hip_moe_forward_noalloc",
+    "lag_hip_moe_forward_scratch_bytes",
     "lag_hip_moe_block", "lag_hip_route",
     "lag_hip_last_groups", "lag_hip_rmsnorm", "lag_hip_moe_forward_rmsnorm", "lag_hip_head_argmax", "lag_hip_argmax", "lag_hip_set_grouped_kernel",
     "lag_hip_set_q4_mode",
@@ -111,6 +112,8 @@ def load_library(path=None):
     L.lag_hip_moe_forward.argtypes = [DP, WP, VP, VP, C.c_int]
     L.lag_hip_moe_forward_rmsnorm.argtypes = [DP, WP, VP, C.c_float, VP, VP, C.c_int]
     L.lag_hip_moe_forward_noalloc.argtypes = [DP, WP, VP, VP, C.c_int]
+    L.lag_hip_moe_forward_scratch_bytes.restype = C.c_size_t
+    L.lag_hip_moe_forward_scratch_bytes.argtypes = [DP, WP, C.c_int]
     L.lag_hip_moe_block.argtypes = [DP, WP, F32P, F32P, C.c_int]
     L.lag_hip_route.argtypes = [DP, WP, VP, C.c_int, VP, VP, VP]
     L.lag_hip_last_groups.argtypes = [C.POINTER(C.c_int), I32P, I32P, I32P, C.c_int]

@@ -111,9 +111,7 @@ static int grow_dev(Buf &b, size_t need) {
     b.cap = need * 2;
     return 0;
 }
-// per-token arrival counters of the routing stage: their own allocation (no
-// other scratch ever overlaps them), zero between launches (the last block of
-// each token resets its counter)
+// pinned host staging of the host-pointer entries, grown like the arena
 static int grow_pinned(Buf &b, size_t need) {
     if (need <= b.cap) return 0;
     if (b.p) (void)hipHostFree(b.p);
@@ -133,16 +131,26 @@ struct Carve {
 static int noalloc_setup(int dev);
 
 // ------------------------------------------------------------ lag family ----
+// One device per process, as the reference backend: the stream, the arena and the
+// uploaded weights all belong to the first device initialised, so a later call
+// naming another device is refused instead of silently keeping the first one's.
 extern "C" int lag_hip_init(int dev) {
-    if (g_ok && dev == g_dev) return 0;
+    if (g_ok) {
+        if (dev == g_dev) return 0;
+        snprintf(g_err, sizeof g_err, "lag_hip_init(%d): already initialised on device %d (one device per process)", dev,
+                 g_dev);
+        return -1;
+    }
     CK(hipSetDevice(dev), "hipSetDevice");
     if (!g_st) CK(hipStreamCreateWithFlags(&g_st, hipStreamNonBlocking), "stream creation");
     void *probe = nullptr;
     CK(hipMalloc(&probe, 1 << 20), "probe allocation");
     (void)hipFree(probe);
-    if (noalloc_setup(dev)) return -1;
     g_dev = dev;
     g_ok = 1;
+    // the allocation-free forward's scratch address: a failure here leaves that one
+    // entry unavailable (it reports not initialised) and every other entry working
+    (void)noalloc_setup(dev);
     return 0;
 }
 
@@ -496,7 +504,9 @@ static int desc_ok(const LagHipMoeDesc *d, const LagHipMoeWeights *w) {
 struct ScratchSrc { char *fixed; size_t cap; };
 static const ScratchSrc kArena = {nullptr, 0};
 
-static int carve_fwd(const LagHipMoeDesc *d, int S, FwdScratch &f, const ScratchSrc &src, bool idot = false) {
+// need: only report the bytes the layout takes (nothing allocated or assigned)
+static int carve_fwd(const LagHipMoeDesc *d, int S, FwdScratch &f, const ScratchSrc &src, bool idot = false,
+                     size_t *need = nullptr) {
     const int E = d->n_experts, K = d->topk, D = d->hidden, I = d->moe_inter, Is = d->shared_inter;
     const int T = S * K, R = router_rows(d), nsx = shared_count(d);
     Carve cv;
@@ -527,6 +537,7 @@ static int carve_fwd(const LagHipMoeDesc *d, int S, FwdScratch &f, const Scratch
         o_hq = cv.take((size_t)T * (I / 32) * 32); o_hqs = cv.take((size_t)T * (I / 32) * 4);
         o_hf = cv.take((size_t)T * I * 4);
     }
+    if (need) { *need = cv.off; return 0; }
     char *A;
     if (src.fixed) {
         if (cv.off > src.cap) {
@@ -877,10 +888,18 @@ static int noalloc_setup(int dev) {
     return 0;
 }
 
+extern "C" size_t lag_hip_moe_forward_scratch_bytes(const LagHipMoeDesc *d, const LagHipMoeWeights *w, int S) {
+    if (!desc_ok(d, w) || S <= 0) return 0;
+    FwdScratch f;
+    size_t n = 0;
+    return carve_fwd(d, S, f, kArena, g_q4_mode == 1 && d->gs == 0, &n) ? 0 : n;
+}
+
 extern "C" int lag_hip_moe_forward_noalloc(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const float *x, float *out,
                                            int S) {
-    if (!g_ok || g_dev < 0 || g_dev >= SW_NOALLOC_MAX_DEV || !g_scratch_ptr[g_dev])
-        return fail_msg("moe_forward_noalloc: backend not initialised");
+    if (!g_ok) return fail_msg("moe_forward_noalloc: backend not initialised");
+    if (g_dev < 0 || g_dev >= SW_NOALLOC_MAX_DEV || !g_scratch_ptr[g_dev])
+        return fail_msg("moe_forward_noalloc: the static scratch of this device is unavailable");
     const int prof = g_prof;
     g_prof = 0;                                  // the per-launch timing pool allocates events
     const int rc = forward(d, w, x, out, S, ScratchSrc{g_scratch_ptr[g_dev], SW_NOALLOC_SCRATCH_BYTES});
@@ -1022,13 +1041,29 @@ extern "C" const char *lag_hip_last_error(void) { return g_err; }
 // route, d2d) is recorded into one graph, replayed by lag_hip_graph_launch
 // with one submission.  The recorded kernels hold raw pointers into the
 // scratch arena, so a finished recording takes the arena with it (freed by
-// lag_hip_graph_destroy) and the next eager call allocates a fresh one: no
-// later call, whatever its size, can free or move memory that a live graph
-// replays over.
+// lag_hip_graph_destroy) and no later call, whatever its size, can free or
+// move memory that a live graph replays over.  A recording that starts with
+// no arena (the previous recording took it) first allocates one of the
+// capacity the last arena had, so graphs of the same shapes can be recorded
+// back to back; shapes beyond that capacity need an eager call first.
+// Destroying a graph while another recording is open is deferred to the end
+// of that recording (a stream synchronisation would break the capture).
 struct GraphRec { hipGraphExec_t exec; Buf arena; };
+static size_t g_arena_last_cap = 0;
+static std::vector<GraphRec *> g_graph_deferred;
+static void graph_free(GraphRec *r) {
+    (void)hipStreamSynchronize(g_st);   // no replay may still be reading the buffers
+    (void)hipGraphExecDestroy(r->exec);
+    if (r->arena.p) (void)hipFree(r->arena.p);
+    delete r;
+}
 extern "C" int lag_hip_graph_begin(void) {
     if (!g_ok || g_capturing) return -1;
     prof_flush();
+    if (!g_arena.p && g_arena_last_cap) {
+        CK(hipMalloc(&g_arena.p, g_arena_last_cap), "device scratch allocation");
+        g_arena.cap = g_arena_last_cap;
+    }
     CK(hipStreamBeginCapture(g_st, hipStreamCaptureModeRelaxed), "begin capture");
     g_capturing = 1;
     return 0;
@@ -1038,12 +1073,15 @@ extern "C" void *lag_hip_graph_end(void) {
     g_capturing = 0;
     hipGraph_t graph = nullptr;
     hipError_t e = hipStreamEndCapture(g_st, &graph);
+    for (GraphRec *r : g_graph_deferred) graph_free(r);
+    g_graph_deferred.clear();
     if (e != hipSuccess || !graph) { fail("end capture", e); return nullptr; }
     hipGraphExec_t exec = nullptr;
     e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
     (void)hipGraphDestroy(graph);
     if (e != hipSuccess) { fail("graph instantiate", e); return nullptr; }
     GraphRec *r = new GraphRec{exec, g_arena};
+    if (g_arena.cap) g_arena_last_cap = g_arena.cap;
     g_arena = Buf{};
     g_last_G_dev = 0;                   // the last groups now live in the graph's arena
     g_last_ng = 0;
@@ -1056,9 +1094,6 @@ extern "C" int lag_hip_graph_launch(void *g) {
 }
 extern "C" void lag_hip_graph_destroy(void *g) {
     if (!g) return;
-    GraphRec *r = (GraphRec *)g;
-    (void)hipStreamSynchronize(g_st);   // no replay may still be reading the buffers
-    (void)hipGraphExecDestroy(r->exec);
-    if (r->arena.p) (void)hipFree(r->arena.p);
-    delete r;
+    if (g_capturing) g_graph_deferred.push_back((GraphRec *)g);
+    else graph_free((GraphRec *)g);
 }

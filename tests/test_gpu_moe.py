@@ -1,12 +1,15 @@
 """The whole MoE block on the device (lag_hip_moe_block / moe_forward) against
 the CPU reference contract: routing identical, layer output within the
-benchmark tolerance (normwise max|a-b|/max|b| <= 2e-3), grouped batches
+benchmark tolerance (normwise max|a-b|/max|b| <= 2e-3 against the reference, and
+elementwise |a-b|/max(|b|, 1e-3 max|b|) <= 2e-3 against the reference at full size
+and against the exact float64 layer at reduced sizes), grouped batches
 bit-identical per token to single-token calls."""
 from dataclasses import replace
 
 import numpy as np
 import pytest
 
+from fullsize import errs, exact_layer
 from oracle import synth
 from sabrewing_amd import configs as cf
 from sabrewing_amd import synth as S
@@ -16,13 +19,6 @@ pytestmark = pytest.mark.gpu
 TOL = 2e-3
 
 
-def errs(got, want, base):
-    """normwise and floored-elementwise relative errors of the MoE update"""
-    dg, dw = got - base, want - base
-    m = float(np.max(np.abs(dw)))
-    nw = float(np.max(np.abs(dg - dw))) / m
-    el = float(np.max(np.abs(dg - dw) / np.maximum(np.abs(dw), 0.05 * m)))
-    return nw, el
 
 
 SMALL = [cf.scaled(cf.C1, D=512, E=16, K=4, I=256),
@@ -51,8 +47,24 @@ def test_layer_small(be, orc, cfg, S_):
     _, sel, _ = be.route(desc_of(cfg), dl.weights(), xd, S_)
     xd.free(); dl.free()
     assert np.array_equal(sel, sel_w)
-    nw, el = errs(got, want, base)
-    assert nw <= TOL, (nw, el)
+    check_small(orc, cfg, L, x, base, got, want, S_)
+
+
+def check_small(orc, cfg, L, x, base, got, want, S_):
+    """a reduced-size layer: normwise against the f32 reference (<= TOL), and elementwise
+    against the exact (float64) layer on the same picks, within TOL or within twice the
+    f32 reference's own elementwise error against that layer, whichever is larger.  At
+    these sizes f32 rounding alone can reach the bar where outputs cancel to near the
+    floor (C1-small, f32 activations: the reference is 2.3e-3 from exact arithmetic at
+    the 1e-3 floor), so the device is held to the reference's own accuracy there."""
+    _, sel_w, w_w = orc.route(synth.desc_of(cfg), L, x)
+    ex = exact_layer(cfg, L, x, base, sel_w, w_w)
+    nw, el_ref = errs(got, want, base)
+    _, el = errs(got, ex, base)
+    _, el_cpu = errs(want, ex, base)
+    print(f"[{cfg.name} S={S_}] normwise {nw:.2e}; elementwise vs exact {el:.2e} (the f32 reference's own "
+          f"{el_cpu:.2e}), vs the reference {el_ref:.2e}", flush=True)
+    assert nw <= TOL and el <= max(TOL, 2 * el_cpu), (nw, el, el_cpu)
 
 
 @pytest.mark.parametrize("cfg", [SMALL[1], SMALL[4]], ids=lambda c: c.name)
@@ -120,7 +132,8 @@ def test_layer_full_size(be, orc, cfg, S_):
     xd.free(); od.free(); dl.free()
     assert np.array_equal(sel, sel_w)
     nw, el = errs(got, want, base)
-    assert nw <= TOL, (nw, el)
+    print(f"[{cfg.name} S={S_}] normwise {nw:.2e}, elementwise {el:.2e}", flush=True)
+    assert nw <= TOL and el <= TOL, (nw, el)
 
 
 def test_device_x_generator(be, orc):
@@ -206,6 +219,53 @@ def test_graph_survives_larger_eager_calls(be, orc):
     dl.free()
 
 
+def test_graphs_recorded_back_to_back(be, orc):
+    """two recordings in a row with no eager call between them (one graph per layer,
+    the second gets fresh scratch of the first's capacity), and a third graph's
+    destroy issued while another recording is open: every replay bit-identical to
+    its eager result"""
+    cfg = SMALL[2]
+    Ls = [synth.make_layer(orc, cfg, 81 + i) for i in range(2)]
+    dls = [DeviceLayer.from_host(be, cfg, L) for L in Ls]
+    x = synth.make_x(orc, cfg, 83, 4)
+    zero = np.zeros_like(x)
+    xd = be.upload(x)
+    oe = [be.upload(zero) for _ in dls]
+    og = [be.upload(zero) for _ in dls]
+    want = []
+    for dl, o in zip(dls, oe):
+        be.moe_forward(desc_of(cfg), dl.weights(), xd, o, 4)
+        be.sync()
+        want.append(be.d2h(o, x.shape, np.float32))
+    gs = []
+    try:
+        for dl, o in zip(dls, og):
+            be.graph_begin()
+            be.moe_forward(desc_of(cfg), dl.weights(), xd, o, 4)
+            gs.append(be.graph_end())
+        be.graph_begin()                                   # destroy graph 0 while recording graph 2
+        be.graph_destroy(gs[0])
+        be.moe_forward(desc_of(cfg), dls[0].weights(), xd, og[0], 4)
+        gs[0] = be.graph_end()
+        for rep in range(3):
+            for i in (1, 0):
+                be.h2d(og[i], zero)
+                be.graph_launch(gs[i])
+                be.sync()
+                got = be.d2h(og[i], x.shape, np.float32)
+                assert np.array_equal(got.view(np.uint32), want[i].view(np.uint32)), (rep, i)
+            be.h2d(oe[0], zero)                            # eager work between replays
+            be.moe_forward(desc_of(cfg), dls[0].weights(), xd, oe[0], 4)
+            be.sync()
+    finally:
+        for g in gs:
+            be.graph_destroy(g)
+        for b in [xd] + oe + og:
+            b.free()
+        for dl in dls:
+            dl.free()
+
+
 @pytest.mark.parametrize("S_", [2, 33, 200])
 def test_device_bucket_matches_oracle(be, orc, S_):
     """the device counting sort (A11): groups in ascending expert id, begin
@@ -241,5 +301,4 @@ def test_layer_1024_experts(be, orc, S_):
     xd.free(); dl.free()
     _, sel_w, _ = orc.route(synth.desc_of(cfg), L, x)
     assert np.array_equal(sel, sel_w)
-    nw, el = errs(got, want, base)
-    assert nw <= TOL, (nw, el)
+    check_small(orc, cfg, L, x, base, got, want, S_)

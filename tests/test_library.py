@@ -117,3 +117,40 @@ def test_loader_relative_path_refused(tmp_path):
     # the loader falls back to the library next to itself
     out, _ = run_probe("libsabrewing_hip.so")
     assert out[5] == os.path.join(os.path.dirname(B.LOADER_PATH), "libsabrewing_hip.so")
+
+
+def test_noalloc_scratch_limit():
+    """lag_hip_moe_forward_scratch_bytes is host arithmetic (no device): the C2 layer's
+    scratch grows with S, and the largest S that fits the allocation-free forward's
+    static region is the one the header and the docs state"""
+    from sabrewing_amd import configs as cf
+    lib = B.load_library()
+    cfg = cf.C2
+    one = C.c_void_p(16)                                   # any non-null pointer: nothing is read
+    w = B.LagHipMoeWeights(one, one, None, one, one, one, one, one, one, one)
+    d = B.desc_of(cfg)
+    need = [lib.lag_hip_moe_forward_scratch_bytes(C.byref(d), C.byref(w), s) for s in range(1, 200)]
+    assert all(n > 0 for n in need) and all(a < b for a, b in zip(need, need[1:]))
+    cap = 24 << 20                                         # LAG_HIP_NOALLOC_SCRATCH_BYTES
+    fits = max(s for s, n in zip(range(1, 200), need) if n <= cap)
+    assert fits == NOALLOC_C2_MAX_S, fits
+    hdr = open(os.path.join(ROOT, "include", "sabrewing_hip.h")).read()
+    assert f"fits up to S = {NOALLOC_C2_MAX_S}" in hdr
+    # the IDOT contract on per-row scales carves its int8 activations and f32 h as well
+    d0 = B.LagHipMoeDesc(*[getattr(d, f[0]) for f in d._fields_])
+    d0.gs = 0
+    assert lib.lag_hip_set_q4_mode(1) == 0
+    try:
+        need1 = [lib.lag_hip_moe_forward_scratch_bytes(C.byref(d0), C.byref(w), s) for s in range(1, 200)]
+    finally:
+        lib.lag_hip_set_q4_mode(0)
+    assert max(s for s, n in zip(range(1, 200), need1) if n <= cap) == NOALLOC_C2_IDOT_MAX_S
+    assert f"up to S = {NOALLOC_C2_IDOT_MAX_S} with lag_hip_set_q4_mode(1)" in hdr
+    bad = B.LagHipMoeDesc(*[getattr(d, f[0]) for f in d._fields_])
+    bad.hidden = 100                                       # not a multiple of 128: unsupported
+    assert lib.lag_hip_moe_forward_scratch_bytes(C.byref(bad), C.byref(w), 1) == 0
+
+
+# the largest C2 batch that lag_hip_moe_forward_noalloc takes (default q4 mode)
+NOALLOC_C2_MAX_S = 78
+NOALLOC_C2_IDOT_MAX_S = 66
