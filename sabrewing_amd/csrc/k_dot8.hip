@@ -179,15 +179,19 @@ __device__ __forceinline__ void dot8_glu_block(const Dot8GluArgs &A, int bx, int
             __shared__ float tk_wk[64];
             __shared__ uint64_t tk_tab[32];
             const DotRoute rt = A.rt;
+            // a block needs its own pick only (passes 0 .. bx); the block of the last rank
+            // and the first outputs runs all K passes and writes the picks and weights
+            const bool writer = bx == rt.K - 1 && by == 0;
             if (tid < 64) {
                 int sk;
                 float wk;
-                gate_topk_wave<NP>(rt.src, rt.E, rt.K, rt.act, rt.bias, rt.use_bias, rt.norm, tk_tab, sk, wk);
+                gate_topk_wave<NP>(rt.src, rt.E, rt.K, rt.act, rt.bias, rt.use_bias, rt.norm, tk_tab, sk, wk, 0, 1.f,
+                                   nullptr, writer ? 0 : bx + 1);
                 if (tid < rt.K) { tk_sk[tid] = sk; tk_wk[tid] = wk; }
             }
             __syncthreads();
             e = __builtin_amdgcn_readfirstlane(tk_sk[bx]);
-            if (bx == 0 && by == 0 && tid < rt.K) { A.sel[tid] = tk_sk[tid]; rt.w[tid] = tk_wk[tid]; }
+            if (writer && tid < rt.K) { A.sel[tid] = tk_sk[tid]; rt.w[tid] = tk_wk[tid]; }
         } else {
             e = A.sel[bx];
         }
@@ -752,20 +756,38 @@ __global__ __launch_bounds__(SH_NT) void k_stage_route(RouterArgs R, int nbr, in
     }
 }
 
+// One token's gate_up units (rank a, 32 outputs c), unit u = a * nch + c (nch = I / 32),
+// dealt over the blocks.  Blocks b and b + ncu share a CU (the dispatcher places one
+// block on every CU before it places second ones), so when the units outnumber the
+// CUs the CUs that take two hold blocks [0, h) and [ncu, nglu), h = nglu - ncu: those
+// get the lowest ranks, whose routing (rank + 1 top-k passes) is the shortest.
+__device__ __forceinline__ int b1_unit(int b, int nglu, int ncu) {
+    const int h = nglu - ncu;
+    if (h <= 0 || h > ncu) return b;                // (no CU takes two, or some take more)
+    if (b < h) return b;
+    if (b >= ncu) return h + (b - ncu);
+    return 2 * h + (b - h);
+}
+
 // TTG: tokens per pass of the routed gate_up.  The extra blocks: the single token's
 // shared down (sh_down_block), or with SKD a batch's shared expert: 1 its down
 // (sh_sk_block over the parts of h), 2 its gate_up over column tiles of 16 tokens
-// (sh_sk_block, inputs split from x)
+// (sh_sk_block, inputs split from x).  ncu: the device's CUs (one token's unit order)
 template <int PF, int PICK, int NP, int TTG, int C16, int RO, int SKD>
 __global__ __launch_bounds__(DG_NT, PICK ? 1 : 4) void k_stage_experts(Dot8GluArgs A, int nbx, int nglu, ShDownArgs Sd,
-                                                                    ShSkArgs Skd) {
+                                                                    ShSkArgs Skd, int ncu) {
     extern __shared__ __align__(16) float smem[];
     const int b = blockIdx.x;
     if (b < nglu) {
-        const int w = PICK == 0 && A.grp.items ? sw_xcd_work(b, nglu) : b;
-        // (cached loads with the batch shared down or the 8-deep ring, which spill with
-        // both load paths)
-        dot8_glu_block<PF, PICK, NP, TTG, C16, RO, 0, SKD != 1 && PF < 8>(A, w % nbx, w / nbx, smem);
+        if constexpr (PICK) {
+            const int u = b1_unit(b, nglu, ncu), nch = nglu / nbx;
+            dot8_glu_block<PF, PICK, NP, TTG, C16, RO, 0, SKD != 1 && PF < 8>(A, u / nch, u % nch, smem);
+        } else {
+            const int w = A.grp.items ? sw_xcd_work(b, nglu) : b;
+            // (cached loads with the batch shared down or the 8-deep ring, which spill with
+            // both load paths)
+            dot8_glu_block<PF, PICK, NP, TTG, C16, RO, 0, SKD != 1 && PF < 8>(A, w % nbx, w / nbx, smem);
+        }
     } else if constexpr (SKD == 1) {
         const int w = b - nglu, nrb = sh_sk_rows(0, Skd.O);
         sh_sk_block<0, 2, 0>(Skd, w % nrb, w / nrb, smem);
@@ -782,7 +804,15 @@ struct StageL {
     struct L {
         static void go(dim3 grid, size_t lds, hipStream_t st, const Dot8GluArgs &A, int nbx, int nglu, const ShDownArgs &Sd,
                        const ShSkArgs &Skd) {
-            SW_LAUNCH((k_stage_experts<PF, PICK, NP, TTG, C16, RO, SKD>), grid, dim3(DG_NT), lds, st, A, nbx, nglu, Sd, Skd);
+            static int ncu = 0;
+            if (!ncu) {
+                int dev = 0;
+                if (hipGetDevice(&dev) != hipSuccess ||
+                    hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+                    ncu = 0;
+            }
+            SW_LAUNCH((k_stage_experts<PF, PICK, NP, TTG, C16, RO, SKD>), grid, dim3(DG_NT), lds, st, A, nbx, nglu, Sd, Skd,
+                      ncu);
         }
     };
 };

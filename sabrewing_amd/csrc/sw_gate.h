@@ -104,10 +104,12 @@ __device__ __forceinline__ float lanef(float v, int l) {
 // its own best slot and the state it leaves when that slot is taken ready
 // before the wave maximum is known, so a pass is the maximum, one ballot and
 // the winner's update.
+// kp (0 < kp < K): only picks 0 .. kp-1 are wanted -- the first kp passes run and the
+// weights are left unnormalised (a caller that needs one pick's expert, not the weights).
 template <int NPER>   // expert slots per lane: E <= 64 * NPER
 __device__ void gate_topk_wave(const float *__restrict__ src, int E, int K, int act, const float *__restrict__ bias,
                                int use_bias, int norm, uint64_t *tab, int &sk, float &wk, int ns = 0, float rs = 1.f,
-                               float *__restrict__ wsh = nullptr) {
+                               float *__restrict__ wsh = nullptr, int kp = 0) {
     const int lane = threadIdx.x & 63;
     float v[NPER], b[NPER];
     // every load of the token issued before any is used (clamped indices)
@@ -214,7 +216,8 @@ __device__ void gate_topk_wave(const float *__restrict__ src, int E, int K, int 
     int nv = 0;
 #pragma unroll
     for (int i = 0; i < NPER; i++) nv += __builtin_popcountll(__ballot(ko[i] != 0u));
-    const int kv = K < nv ? K : nv;
+    const int KP = kp > 0 && kp < K ? kp : K;
+    const int kv = KP < nv ? KP : nv;
     int a = 0;
     for (; a < kv; a++) {
         // this lane's best: the largest key, its first slot and that slot's weight
@@ -236,7 +239,7 @@ __device__ void gate_topk_wave(const float *__restrict__ src, int E, int K, int 
         for (int i = 0; i < NPER; i++) ko[i] = (win && ls == i) ? 0u : ko[i];
         if (lane == a) { sk = NPER * bl + slot; wk = wb; }
     }
-    for (; a < K; a++) {                              // nothing valid left: the lowest unselected id
+    for (; a < KP; a++) {                             // nothing valid left: the lowest unselected id
         const unsigned long long bal = __ballot(frm != 0u);
         const int ls = frm ? __builtin_ctz(frm) : 0;
         const int bl = bal ? __builtin_ctzll(bal) : 0;
@@ -248,7 +251,8 @@ __device__ void gate_topk_wave(const float *__restrict__ src, int E, int K, int 
         if (lane == bl) frm &= ~(1u << ls);
         if (lane == a) { sk = NPER * bl + slot; wk = wb; }
     }
-    if (act == 4) {                                   // qwen35: always, in double (c/qwen35.c:585-587)
+    if (KP < K) {                                     // picks only: no weights wanted
+    } else if (act == 4) {                            // qwen35: always, in double (c/qwen35.c:585-587)
         double tot = 0.0;
         for (int a = 0; a < K; a++) tot += (double)lanef(wk, a);
         wk = (float)((double)wk / tot);

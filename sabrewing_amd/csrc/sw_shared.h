@@ -82,17 +82,32 @@ __host__ __device__ inline size_t sh_down_lds(int Is) { return sh_job_lds(Is); }
 __host__ __device__ inline int sh_glu_blocks(int Is) { return Is / SH_GLU_O; }
 __host__ __device__ inline int sh_down_blocks(int D) { return D / SH_DN_O; }
 
-// the block's parts of one token's K inputs into LDS
+// The block's parts of one token's K inputs into LDS, in two halves, so a block can
+// issue the loads of its first chunk of x before its weight loads (a wave's loads
+// return in order: the x it waits on then does not queue behind the weights):
+// sh_parts_first loads this thread's first chunk (8 inputs), sh_stage_parts stores it
+// as parts and does the rest of x.
+struct ShX { sw_f32x4 v0, v1; };
+__device__ __forceinline__ ShX sh_parts_ld(const float *__restrict__ x, int c) {
+    return ShX{((const sw_f32x4 *)x)[2 * c], ((const sw_f32x4 *)x)[2 * c + 1]};
+}
+__device__ __forceinline__ void sh_parts_st(const ShX &v, int c, uint16_t *pl) {
+    sw_u32x4 p0, p1, p2;
+    sh_split8(v.v0, v.v1, p0, p1, p2);
+    uint16_t *dst = pl + (c >> 2) * 3 * SH_RG + (c & 3) * 8;
+    *(sw_u32x4 *)dst = p0;
+    *(sw_u32x4 *)(dst + SH_RG) = p1;
+    *(sw_u32x4 *)(dst + 2 * SH_RG) = p2;
+}
+__device__ __forceinline__ ShX sh_parts_first(const float *__restrict__ x, int K) {
+    return sh_parts_ld(x, min((int)threadIdx.x, K / 8 - 1));   // (clamped: no branch around the load)
+}
+__device__ __forceinline__ void sh_stage_parts(const float *__restrict__ x, int K, uint16_t *pl, const ShX &first) {
+    if ((int)threadIdx.x < K / 8) sh_parts_st(first, threadIdx.x, pl);
+    for (int c = threadIdx.x + blockDim.x; c < K / 8; c += blockDim.x) sh_parts_st(sh_parts_ld(x, c), c, pl);
+}
 __device__ __forceinline__ void sh_stage_parts(const float *__restrict__ x, int K, uint16_t *pl) {
-    for (int c = threadIdx.x; c < K / 8; c += blockDim.x) {
-        const sw_f32x4 v0 = ((const sw_f32x4 *)x)[2 * c], v1 = ((const sw_f32x4 *)x)[2 * c + 1];
-        sw_u32x4 p0, p1, p2;
-        sh_split8(v0, v1, p0, p1, p2);
-        uint16_t *dst = pl + (c >> 2) * 3 * SH_RG + (c & 3) * 8;
-        *(sw_u32x4 *)dst = p0;
-        *(sw_u32x4 *)(dst + SH_RG) = p1;
-        *(sw_u32x4 *)(dst + 2 * SH_RG) = p2;
-    }
+    sh_stage_parts(x, K, pl, sh_parts_first(x, K));
 }
 
 // wave `seg` of the block: NRT 16-row tiles (row m of tile t at rowp(t, m)) over segment
@@ -100,11 +115,11 @@ __device__ __forceinline__ void sh_stage_parts(const float *__restrict__ x, int 
 // column 0 holds the token; the other columns multiply zeros).  start() issues the
 // first SH_PF steps' weight loads (before the block stages the token's parts, so the
 // loads' latency overlaps that work); run() waits for the parts in LDS.
-template <int NRT>
+template <int NRT, int PFW = SH_PF>
 struct ShSegWave {
     const uint16_t *wr[NRT];
     int GS, g0;
-    sw_u32x4 ring[NRT][SH_PF];
+    sw_u32x4 ring[NRT][PFW];
     __device__ __forceinline__ sw_u32x4 ld(int t, int s) const {
         return *(const sw_u32x4 *)(wr[t] + (int64_t)(g0 + min(s, GS - 1)) * SH_RG);
     }
@@ -116,7 +131,7 @@ struct ShSegWave {
 #pragma unroll
         for (int t = 0; t < NRT; t++) wr[t] = rowp(t, m) + 8 * kq;
 #pragma unroll
-        for (int u = 0; u < SH_PF; u++)
+        for (int u = 0; u < PFW; u++)
 #pragma unroll
             for (int t = 0; t < NRT; t++)
                 if (u < GS) ring[t][u] = ld(t, u);          // uniform
@@ -137,16 +152,16 @@ struct ShSegWave {
         // full rounds with unconditional refills (clamped past the end), then the last
         // round without: no branch join inside a round, so the waits stay per step
         int s0 = 0;
-        for (; s0 + SH_PF < GS; s0 += SH_PF) {
+        for (; s0 + PFW < GS; s0 += PFW) {
 #pragma unroll
-            for (int u = 0; u < SH_PF; u++) {
+            for (int u = 0; u < PFW; u++) {
                 use(s0 + u, u);
 #pragma unroll
-                for (int t = 0; t < NRT; t++) ring[t][u] = ld(t, s0 + u + SH_PF);
+                for (int t = 0; t < NRT; t++) ring[t][u] = ld(t, s0 + u + PFW);
             }
         }
 #pragma unroll
-        for (int u = 0; u < SH_PF; u++)
+        for (int u = 0; u < PFW; u++)
             if (s0 + u < GS) use(s0 + u, u);               // uniform
     }
 };
@@ -178,11 +193,12 @@ __device__ __forceinline__ void sh_glu_block(const uint16_t *__restrict__ Wg, co
     uint16_t *pl = (uint16_t *)smem;
     float *red = smem + (size_t)D * 6 / 4;
     const int i0 = bid * SH_GLU_O, nseg = sh_nseg(D / SH_RG), wave = threadIdx.x >> 6;
+    const ShX x0 = sh_parts_first(x, D);              // x ahead of the weights in every wave's queue
     ShSegWave<1> sw;
     if (wave < nseg)
         sw.start([&](int, int m) { return (m < 8 ? Wg + (int64_t)(i0 + m) * D : Wu + (int64_t)(i0 + m - 8) * D); }, D,
                  wave, nseg);
-    sh_stage_parts(x, D, pl);
+    sh_stage_parts(x, D, pl, x0);
     __syncthreads();
     if (wave < nseg) {
         sw_f32x4 acc[1];
@@ -197,15 +213,18 @@ __device__ __forceinline__ void sh_glu_block(const uint16_t *__restrict__ Wg, co
     }
 }
 
-// down of one token for rows d0 = 32 bid .. +31 (f32 out)
+// down of one token for rows d0 = 32 bid .. +31 (f32 out; PFW: steps of weight loads in
+// flight per wave)
+template <int PFW = SH_PF>
 __device__ __forceinline__ void sh_down_block(const uint16_t *__restrict__ Wd, const float *__restrict__ h, int Is, int D,
                                               float *__restrict__ out, int bid, float *smem) {
     uint16_t *pl = (uint16_t *)smem;
     float *red = smem + (size_t)Is * 6 / 4;
     const int d0 = bid * SH_DN_O, nseg = sh_nseg(Is / SH_RG), wave = threadIdx.x >> 6;
-    ShSegWave<2> sw;
+    const ShX h0 = sh_parts_first(h, Is);             // h ahead of the weights in every wave's queue
+    ShSegWave<2, PFW> sw;
     if (wave < nseg) sw.start([&](int t, int m) { return Wd + (int64_t)(d0 + 16 * t + m) * Is; }, Is, wave, nseg);
-    sh_stage_parts(h, Is, pl);
+    sh_stage_parts(h, Is, pl, h0);
     __syncthreads();
     if (wave < nseg) {
         sw_f32x4 acc[2];
