@@ -737,6 +737,18 @@ int sw_launch_q4_dot8_down_combine(hipStream_t st, SwQ4 W, const sw_u32x4 *hl, c
 static size_t lds_max(size_t a, size_t b) { return a > b ? a : b; }
 
 struct ShGluArgs { const uint16_t *Wg, *Wu; const float *x; int D, Is; float *h; };
+
+// the device's CUs (one device per process; 0 if it cannot be read)
+static int sw_cu_count() {
+    static int ncu = -1;
+    if (ncu < 0) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            ncu = 0;
+    }
+    return ncu;
+}
+
 struct ShDownArgs { const uint16_t *Wd; const float *h; int Is, D; float *out; };
 
 // SK: the extra blocks are a batch's shared gate_up over column tiles of SK x 16 tokens
@@ -804,15 +816,8 @@ struct StageL {
     struct L {
         static void go(dim3 grid, size_t lds, hipStream_t st, const Dot8GluArgs &A, int nbx, int nglu, const ShDownArgs &Sd,
                        const ShSkArgs &Skd) {
-            static int ncu = 0;
-            if (!ncu) {
-                int dev = 0;
-                if (hipGetDevice(&dev) != hipSuccess ||
-                    hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-                    ncu = 0;
-            }
             SW_LAUNCH((k_stage_experts<PF, PICK, NP, TTG, C16, RO, SKD>), grid, dim3(DG_NT), lds, st, A, nbx, nglu, Sd, Skd,
-                      ncu);
+                      sw_cu_count());
         }
     };
 };

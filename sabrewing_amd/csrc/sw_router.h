@@ -153,9 +153,23 @@ __device__ __forceinline__ void router_block(const RouterArgs &R, int bx, int s,
     __syncthreads();
     const float *xj = xt + j * ML;
     float acc = 0.f;
+    // x of the slices two ahead is read from LDS while this slice's fmas run (the chain
+    // would otherwise wait out an LDS latency per slice): xn[0] holds slice q + 1's P
+    // values, xn[1] slice q + 2's
+    constexpr int XV = BF16 ? 2 : 1;                  // float4 of x per slice
+    sw_f32x4 xn[2][XV];
+    auto xload = [&](int q, sw_f32x4 *dst) {
+        const int qc = min(q, NQ - 1);
+#pragma unroll
+        for (int v = 0; v < XV; v++) dst[v] = *(const sw_f32x4 *)(xj + P * qc + 4 * v);
+    };
     auto chain4 = [&](int q, const sw_u32x4 &w) {
+        sw_f32x4 xc[XV];
+#pragma unroll
+        for (int v = 0; v < XV; v++) { xc[v] = xn[0][v]; xn[0][v] = xn[1][v]; }
+        xload(q + 2, xn[1]);
         if constexpr (BF16) {
-            const sw_f32x4 xa = *(const sw_f32x4 *)(xj + 8 * q), xb = *(const sw_f32x4 *)(xj + 8 * q + 4);
+            const sw_f32x4 xa = xc[0], xb = xc[XV - 1];
             acc = __builtin_fmaf(xa.x, __builtin_bit_cast(float, w.x << 16), acc);
             acc = __builtin_fmaf(xa.y, __builtin_bit_cast(float, w.x & 0xFFFF0000u), acc);
             acc = __builtin_fmaf(xa.z, __builtin_bit_cast(float, w.y << 16), acc);
@@ -167,7 +181,7 @@ __device__ __forceinline__ void router_block(const RouterArgs &R, int bx, int s,
         } else {
             // the whole vector is cast: clang lowers a bit_cast of a vector-element
             // lvalue to a read of element 0
-            const sw_f32x4 xa = *(const sw_f32x4 *)(xj + 4 * q), wf = __builtin_bit_cast(sw_f32x4, w);
+            const sw_f32x4 xa = xc[0], wf = __builtin_bit_cast(sw_f32x4, w);
             acc = __builtin_fmaf(xa.x, wf.x, acc);
             acc = __builtin_fmaf(xa.y, wf.y, acc);
             acc = __builtin_fmaf(xa.z, wf.z, acc);
@@ -182,6 +196,11 @@ __device__ __forceinline__ void router_block(const RouterArgs &R, int bx, int s,
         }
     }
     if (chain) {
+        sw_f32x4 x0[XV];
+        xload(0, x0);
+        xload(1, xn[1]);
+#pragma unroll
+        for (int v = 0; v < XV; v++) xn[0][v] = x0[v];
         // full rounds with unconditional refills (a refill past the end re-reads the last
         // slice), then the last round without: no ring rotation, loads stay in flight
         int q0 = 0;

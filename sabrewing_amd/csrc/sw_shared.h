@@ -79,7 +79,6 @@ __device__ __forceinline__ sw_f32x4 sh_mfma3(sw_u32x4 a, sw_u32x4 b0, sw_u32x4 b
 __host__ __device__ inline size_t sh_job_lds(int K) { return (size_t)K * 6 + 8 * 32 * 4; }
 __host__ __device__ inline size_t sh_glu_lds(int D) { return sh_job_lds(D); }
 __host__ __device__ inline size_t sh_down_lds(int Is) { return sh_job_lds(Is); }
-__host__ __device__ inline int sh_glu_blocks(int Is) { return Is / SH_GLU_O; }
 __host__ __device__ inline int sh_down_blocks(int D) { return D / SH_DN_O; }
 
 // The block's parts of one token's K inputs into LDS, in two halves, so a block can
@@ -130,11 +129,13 @@ struct ShSegWave {
         g0 = seg * GS;
 #pragma unroll
         for (int t = 0; t < NRT; t++) wr[t] = rowp(t, m) + 8 * kq;
+        // unconditional (ld clamps a step past the segment to its last): loads under a
+        // condition end at a join where the compiler waits for every load in flight,
+        // and the caller's first loads (x) must not wait for the ring
 #pragma unroll
         for (int u = 0; u < PFW; u++)
 #pragma unroll
-            for (int t = 0; t < NRT; t++)
-                if (u < GS) ring[t][u] = ld(t, u);          // uniform
+            for (int t = 0; t < NRT; t++) ring[t][u] = ld(t, u);
     }
     __device__ __forceinline__ void run(const uint16_t *pl, sw_f32x4 *acc) {
         const int lane = threadIdx.x & 63, m = lane & 15, kq = lane >> 4;
@@ -187,6 +188,7 @@ __device__ __forceinline__ float sh_fold(const float *red, int row, int nseg) {
 
 // gate_up of one token for outputs i0 = 8 bid .. +7: tile rows 0-7 the gate rows, 8-15 the
 // up rows; h[i] = silu(gate) * up (f32)
+__host__ __device__ inline int sh_glu_blocks(int Is) { return Is / SH_GLU_O; }
 __device__ __forceinline__ void sh_glu_block(const uint16_t *__restrict__ Wg, const uint16_t *__restrict__ Wu,
                                              const float *__restrict__ x, int D, int Is, float *__restrict__ h, int bid,
                                              float *smem) {
