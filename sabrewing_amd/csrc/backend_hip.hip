@@ -316,8 +316,8 @@ static int grouped_host(float *outh, const float *x, int S, const void *gu_q, co
         uint32_t *xd = (uint32_t *)(A + o_xd), *hd = (uint32_t *)(A + o_hd);
         float *xds = (float *)(A + o_xs), *hds = (float *)(A + o_hs);     // the factors: same sizes as the limbs'
         { PROF("digits"); if (sw_launch_digits(g_st, (const float *)(A + o_x), S, D, xd, xds)) return fail_msg("digits launch"); }
-        { PROF("mf_glu"); if (sw_launch_mf_glu(g_st, gu, xd, xds, gt, I, hd, hds)) return fail_msg("MFMA gate_up launch (shape unsupported?)"); }
-        { PROF("mf_down"); if (sw_launch_mf_rows(g_st, dn, hd, hds, gd, (float *)(A + o_slot))) return fail_msg("MFMA down launch (shape unsupported?)"); }
+        { PROF("mf_glu"); if (sw_launch_mf_glu(g_st, gu, xd, xds, S, gt, I, hd, hds)) return fail_msg("MFMA gate_up launch (shape unsupported?)"); }
+        { PROF("mf_down"); if (sw_launch_mf_rows(g_st, dn, hd, hds, T, gd, (float *)(A + o_slot))) return fail_msg("MFMA down launch (shape unsupported?)"); }
     } else if (run_experts(gu, dn, (const float *)(A + o_x), S, (sw_u32x4 *)(A + o_xl), (float *)(A + o_xs), 0, g, I,
                            (sw_u32x4 *)(A + o_hl), (float *)(A + o_hs), (float *)(A + o_slot), maxcnt)) return -1;
     const float *res = (const float *)(A + o_slot);
@@ -785,14 +785,14 @@ static int forward(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const floa
               return fail_msg("bucket launch"); }
         SwGroups g = {f.gexp, f.gbeg, f.gcnt, f.grow, f.G, sw_npass_max(T, E, SW_MF_TT), 0, f.items, f.P};
         { PROF("mf_glu");
-          if (sw_launch_mf_glu(g_st, gu, f.xd, f.xds, g, I, f.hd, f.hds)) return fail_msg("MFMA gate_up launch"); }
+          if (sw_launch_mf_glu(g_st, gu, f.xd, f.xds, S, g, I, f.hd, f.hds)) return fail_msg("MFMA gate_up launch"); }
         if (sh) {
             PROF("shared_down");
             if (sw_launch_sh_down(g_st, sd, f.shp, S, Is, D, f.sout)) return fail_msg("shared down launch");
         }
         SwGroups gd = g;
         gd.grow = nullptr;                 // the down reads the packed rows directly
-        { PROF("mf_down"); if (sw_launch_mf_rows(g_st, dn, f.hd, f.hds, gd, f.slots)) return fail_msg("MFMA down launch"); }
+        { PROF("mf_down"); if (sw_launch_mf_rows(g_st, dn, f.hd, f.hds, T, gd, f.slots)) return fail_msg("MFMA down launch"); }
         { PROF("combine");
           if (sw_launch_combine(g_st, f.slots, f.rowof, f.w, S, K, D, rs_c, sh || gated ? f.sout : nullptr, out, 1, wsh, nsg))
               return fail_msg("combine launch"); }

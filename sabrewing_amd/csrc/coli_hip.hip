@@ -220,8 +220,8 @@ int launch_group_mf(Ctx *c, const Groups &G, char *A, const GLay &L, int ntile) 
     uint32_t *xd = (uint32_t *)(A + L.xl), *hd = (uint32_t *)(A + L.hl);
     float *xds = (float *)(A + L.xs), *hds = (float *)(A + L.hs);
     if (sw_launch_digits(c->st, (const float *)(A + L.x), G.total, G.D, xd, xds)) return 0;
-    if (sw_launch_mf_glu_tab(c->st, gu, tab, xd, xds, gt, G.I, hd, hds)) return 0;
-    if (sw_launch_mf_rows_tab(c->st, dn, tab, hd, hds, gt, (float *)(A + L.y))) return 0;
+    if (sw_launch_mf_glu_tab(c->st, gu, tab, xd, xds, G.total, gt, G.I, hd, hds)) return 0;
+    if (sw_launch_mf_rows_tab(c->st, dn, tab, hd, hds, G.total, gt, (float *)(A + L.y))) return 0;
     return ok(hipGetLastError(), "expert group launch");
 }
 

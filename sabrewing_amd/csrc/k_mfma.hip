@@ -1,27 +1,26 @@
-// k_mfma.hip -- the grouped int4 expert GEMMs of prefill on the int8 matrix
-// cores, bit-identical to the dot8 kernels of k_dot8.hip.
+// k_mfma.hip -- the grouped int4 expert GEMMs of prefill on the matrix cores,
+// bit-identical to the dot8 kernels of k_dot8.hip.
 //
 // For a weight row and a group of 32 inputs, dot8 forms the exact integer
 // acc = sum_k w_k D_k (w_k = n_k - 8 in [-8, 7], D_k the 7-limb integer of
 // input k, |D_k| < 2^21.2) and the term (float)acc * (s * xf).  Here every D
 // is cut into two 12-bit digits, D = E1 2^12 + E0 with E0 the residue of D
-// mod 4096 in [-2048, 2048), and every E into a low nibble and a signed high
-// byte, E = lo + 16 hi (lo = E & 15, hi = E >> 4; both int8).  One
-// v_mfma_i32_16x16x64_i8 has 64 k-slots: the 32 weights as bytes w against
-// lo, and as bytes 16 w against hi, so it returns
-//     R = sum_k (w_k lo_k + 16 w_k hi_k) = sum_k w_k E_k
-// exactly (|R| < 2^19); the two of E0 and E1 give acc = (R1 << 12) + R0,
-// dot8's int32.  The terms and the canonical row sum (pairwise trees over
-// runs of 16 groups, padded with +0 terms, the runs added left to right)
-// follow dot8's operations one for one, so a token's output has the same
-// bits whichever kernel ran its group.
+// mod 4096 in [-2048, 2048) and |E1| <= 577.  The weights and both digits are
+// integers that f16 holds exactly, and every product (|w E| <= 2^14) and
+// every partial sum of 32 of them (< 2^19) is an integer that f32 holds
+// exactly, so two v_mfma_f32_16x16x32_f16 return R0 = sum_k w_k E0_k and
+// R1 = sum_k w_k E1_k exactly, whatever order the hardware adds in; then
+// fma(R1, 4096, R0) rounds the exact acc = 4096 R1 + R0 once, to nearest even,
+// which is (float)acc, dot8's conversion of its int32, bit for bit.  The
+// terms and the canonical row sum (pairwise trees over runs of 16 groups,
+// padded with +0 terms, the runs added left to right) follow dot8's
+// operations one for one, so a token's output has the same bits whichever
+// kernel ran its group.
 //
-// Digits in memory: per (input row, group) 128 bytes, the B operands of the
-// two MFMAs: byte op*64 + (k>>3)*16 + half*8 + (k&1)*4 + ((k&7)>>1) holds
-// input k's lo (half 0) or hi (half 1) digit of E0 (op 0) or E1 (op 1).
-// Lane l of the MFMA (column l % 16, k quarter q = l / 16) reads the 16
-// bytes of quarter q, and its A operand holds the same k-slots of a weight
-// row: [w of k = 8q+0,2,4,6 | w of 8q+1,3,5,7 | 16w of the same | 16w ...],
+// Digits in memory: per (input row, group) 128 bytes, E0 of the 32 inputs as
+// f16 in input order, then E1: the B operands of the two MFMAs.  Lane l of
+// an MFMA (column l % 16, k quarter q = l / 16) reads the 16 bytes of inputs
+// 8q .. 8q+7, and its A operand holds the same inputs of a weight row as f16,
 // expanded from packed dword q of the row's group (nibble k at bits 4(k&7)).
 //
 // Block: 128 weight rows (8 tiles of 16) x a tile of up to 64 tokens (4
@@ -45,23 +44,34 @@
 #define MF_DW 32           // digit dwords per (input row, group)
 #define MF_ROWS 128        // weight rows per block
 #define MF_TT SW_MF_TT     // tokens per block tile (64)
-#define MF_NT 1024         // threads per block: 16 waves
+#define MF_NT 1024         // threads per block: 16 waves, four per SIMD
 #define MF_CG 4            // input groups per staged chunk
-// one chunk buffer in LDS: expanded weights [g][tile 8][quarter 4][row 16] x 16 B,
-// digits [g][token tile 4][op 2][quarter 4][token 16] x 16 B, scales [g][row],
-// token factors [g][token]
+// the two chunk buffers in LDS, each operand's pair side by side (so that one base
+// register per operand and immediate offsets reach both): expanded weights
+// [buf][g][tile 8][quarter 4][row 16] x 16 B, digits [buf][g][token tile 4][op 2]
+// [quarter 4][token 16] x 16 B, scales [buf][g][row], token factors [buf][g][token]
+#define MF_A_SZ (MF_CG * MF_ROWS * 64)
+#define MF_B_SZ (MF_CG * MF_TT * 128)
+#define MF_S_SZ (MF_CG * MF_ROWS * 4)
+#define MF_X_SZ (MF_CG * MF_TT * 4)
 #define MF_A_OFF 0
-#define MF_B_OFF (MF_A_OFF + MF_CG * MF_ROWS * 64)
-#define MF_S_OFF (MF_B_OFF + MF_CG * MF_TT * 128)
-#define MF_X_OFF (MF_S_OFF + MF_CG * MF_ROWS * 4)
-#define MF_BUF (MF_X_OFF + MF_CG * MF_TT * 4)
+#define MF_B_OFF (MF_A_OFF + 2 * MF_A_SZ)
+#define MF_S_OFF (MF_B_OFF + 2 * MF_B_SZ)
+#define MF_X_OFF (MF_S_OFF + 2 * MF_S_SZ)
+#define MF_LDS_STAGE (MF_X_OFF + 2 * MF_X_SZ)
+#ifndef MF_PF
+#define MF_PF 1            // the next group's operands fetched during this group's products
+#endif
+#define MF_YLD 129         // floats per token row of the block's sums after the loop
 #define MF_HLD 65          // floats per token row of h in the gate_up epilogue
+#define MF_HL_OFF (MF_TT * MF_YLD * 4)
 
 // ------------------------------------------------------------ digits ----
 // one group by the 32 lanes of a half-wave (i = lane in the half): the same
-// exponent and 7 limbs as limbs_group, written as the MFMA digits above;
-// the factor 2^(e - 21) (NaN for a group holding a NaN or an infinity, whose
-// digits are 0) is limbs_group's
+// exponent and 7 limbs as limbs_group, written as the MFMA digits above (E0
+// then E1 of the 32 inputs as f16, each quarter of 8 inputs in the operand
+// order of mf_expand); the factor 2^(e - 21) (NaN for a group holding a NaN or
+// an infinity, whose digits are 0) is limbs_group's
 __device__ __forceinline__ void digits_group(float v, int i, uint32_t *__restrict__ dst, float *__restrict__ fdst) {
     bool bad;
     const int e = limbs_exp(v, bad);
@@ -71,20 +81,18 @@ __device__ __forceinline__ void digits_group(float v, int i, uint32_t *__restric
     for (int l = 0; l < SW_ND; l++) D = D * 8 + (int)limb_digit(y);
     if (bad) D = 0;
     const int E0 = ((D + 2048) & 4095) - 2048, E1 = (D - E0) >> 12;
-    const int sh = 8 * ((i & 7) >> 1);
-    uint32_t b[4] = {(uint32_t)(E0 & 15) << sh, (uint32_t)((E0 >> 4) & 255) << sh, (uint32_t)(E1 & 15) << sh,
-                     (uint32_t)((E1 >> 4) & 255) << sh};
-#pragma unroll
-    for (int q = 0; q < 4; q++) {
-        b[q] |= __shfl_xor(b[q], 2, 32);
-        b[q] |= __shfl_xor(b[q], 4, 32);
-    }
-    if ((i & 6) == 0) {                               // lane 8 kq + par holds the dwords of (kq, par)
-        const int kq = i >> 3, par = i & 1;
-        dst[kq * 4 + par] = b[0];
-        dst[kq * 4 + 2 + par] = b[1];
-        dst[16 + kq * 4 + par] = b[2];
-        dst[16 + kq * 4 + 2 + par] = b[3];
+    // the odd inputs of a quarter meet weights 16 w: their digits are E / 16 (exact:
+    // at most 11 significant bits, none below 2^-4)
+    const float sc = (i & 1) ? 0.0625f : 1.0f;
+    const uint32_t h0 = __builtin_bit_cast(uint16_t, (_Float16)((float)E0 * sc));
+    const uint32_t h1 = __builtin_bit_cast(uint16_t, (_Float16)((float)E1 * sc));
+    // input r = i & 7 of quarter q = i >> 3 sits at f16 slot (r & 1) * 4 + (r >> 1) of the
+    // quarter's 4 dwords: inputs r and r ^ 2 share a dword (r & 2 the high half)
+    const uint32_t o0 = (uint32_t)__shfl_xor((int)h0, 2, 32), o1 = (uint32_t)__shfl_xor((int)h1, 2, 32);
+    if ((i & 2) == 0) {
+        const int dw = (i >> 3) * 4 + (i & 1) * 2 + ((i >> 2) & 1);
+        dst[dw] = h0 | (o0 << 16);
+        dst[16 + dw] = h1 | (o1 << 16);
     }
     if (i == 0) *fdst = bad ? __builtin_nanf("") : ldexpf(1.0f, e - 3 * SW_ND);
 }
@@ -112,6 +120,7 @@ struct MfArgs {
     int gsh;
     const uint32_t *dg;     // input digits [rows][G][MF_DW]
     const float *xs;        // input factors [rows][G]
+    int dg_rows;            // rows of dg and xs (dg_rows * K * 4 < 2^32)
     SwGroups grp;           // tiles: items of up to MF_TT tokens, P live
     int I;                  // GLU: the intermediate size (W.O == 2 I)
     int nrb;                // row blocks
@@ -121,36 +130,23 @@ struct MfArgs {
     const SwTab *tab;       // per-group tensors (the _tab launches) or null
 };
 
-// the pairwise tree of a run of CH terms (CH a power of two <= 16), fed one
-// term at a time (gl = the term's index in the run, known at compile time
-// after unrolling): L holds the pending single, pair, quad and eight; the
-// run's sum lands in run after the last term
-template <int CH>
-__device__ __forceinline__ void tree_push(float p, int gl, float (&L)[4], float &run) {
-    if (CH == 1) { run = p; return; }
-    if ((gl & 1) == 0) { L[0] = p; return; }
-    float s = L[0] + p;
-    if (CH == 2) { run = s; return; }
-    if ((gl & 2) == 0) { L[1] = s; return; }
-    s = L[1] + s;
-    if (CH == 4) { run = s; return; }
-    if ((gl & 4) == 0) { L[2] = s; return; }
-    s = L[2] + s;
-    if (CH == 8) { run = s; return; }
-    if ((gl & 8) == 0) { L[3] = s; return; }
-    run = L[3] + s;
-}
-
-// the four int8 operand dwords of packed weight dword w (nibble n = w_k + 8
-// of k = 8q + c at bits 4c): bytes w of the even k, w of the odd k, 16 w of
-// the even k, 16 w of the odd k
+// the A operand of packed weight dword w (nibble n_r = w_r + 8 of input r of the
+// quarter at bits 4r) as f16 in the slot order of digits_group: (w0, w2), (w4, w6),
+// (16 w1, 16 w3), (16 w5, 16 w7).  An even input's nibble is the low nibble of a
+// byte, ORed under 0x64 into the f16 1024 + n; an odd input's is the high nibble,
+// giving 1024 + 16 n.  Adding -1032, resp. -1152, leaves w, resp. 16 w, exactly.
 __device__ __forceinline__ sw_i32x4 mf_expand(uint32_t w) {
-    const uint32_t wx = w ^ 0x88888888u;             // nibbles w_k as 4-bit two's complement
+    const uint32_t lo = w & 0x0F0F0F0Fu, hi = w & 0xF0F0F0F0u, magic = 0x64646464u;
+    const sw_half2 off_lo = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+    const sw_half2 off_hi = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+    // bytes (b0, 0x64, b1, 0x64) and (b2, 0x64, b3, 0x64) of lo and of hi
+    const uint32_t p0 = __builtin_amdgcn_perm(magic, lo, 0x04010400u), p1 = __builtin_amdgcn_perm(magic, lo, 0x04030402u);
+    const uint32_t p2 = __builtin_amdgcn_perm(magic, hi, 0x04010400u), p3 = __builtin_amdgcn_perm(magic, hi, 0x04030402u);
     sw_i32x4 a;
-    a[0] = (int)(((w & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u);          // n + 120 < 256, then bit 7 flipped: n - 8
-    a[1] = (int)((((w >> 4) & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u);
-    a[2] = (int)((wx << 4) & 0xF0F0F0F0u);
-    a[3] = (int)(wx & 0xF0F0F0F0u);
+    a[0] = __builtin_bit_cast(int, __builtin_bit_cast(sw_half2, p0) + off_lo);
+    a[1] = __builtin_bit_cast(int, __builtin_bit_cast(sw_half2, p1) + off_lo);
+    a[2] = __builtin_bit_cast(int, __builtin_bit_cast(sw_half2, p2) + off_hi);
+    a[3] = __builtin_bit_cast(int, __builtin_bit_cast(sw_half2, p3) + off_hi);
     return a;
 }
 
@@ -166,8 +162,9 @@ __global__ __launch_bounds__(MF_NT, 1) void k_mf(MfArgs A) {
     const int K = W.K, G = K / SW_RG, O = W.O;
     const int NC = G / MF_CG;                              // staged chunks (G % 4 == 0)
     const int NCV = (G + CH - 1) / CH * (CH / MF_CG);      // chunks of the padded runs
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, col = lane & 15, kq = lane >> 4;
-    const int mp = wave & 3, tt = wave >> 2;               // row tiles mp, mp + 4; token tile tt
+    // (the wave index in a scalar register: what derives from it is uniform to the compiler)
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, col = lane & 15,
+              kq = lane >> 4;
 
     // block -> (tile, row block), XCD-aware over the live blocks
     const int nlive = *grp.P * A.nrb;
@@ -176,7 +173,7 @@ __global__ __launch_bounds__(MF_NT, 1) void k_mf(MfArgs A) {
     const int tile = wk / A.nrb, rb = wk - tile * A.nrb;
     int e, beg, t0, tend;
     if (!grp_work(grp, tile, MF_TT, e, beg, t0, tend)) return;
-    const int nt = tend - t0;
+    const int nt = tend - t0, nact = (nt + 15) >> 4;       // tokens, token tiles with tokens
     const int i0 = rb * 64, r0 = rb * MF_ROWS;
     // weight row of local row r (GLU: gate rows i0..i0+63, then the up rows)
     // (PT: row r of the group's own gate, up or down tensor)
@@ -192,19 +189,17 @@ __global__ __launch_bounds__(MF_NT, 1) void k_mf(MfArgs A) {
     const int ng = W.gs > 0 ? K / W.gs : 1;
     const uint32_t rbytes = (uint32_t)K / 2;
     // staging roles by whole waves; for gate_up rotated so that in a tile of 1-3 token tiles the
-    // computing waves (token tiles tt < nact: waves 0 .. 4 nact - 1) take the roles with no work
-    // (the digits of token tiles that do not compute are not staged) or the lightest (C4:
-    // gate_up 2.11 -> 2.04 ms; the down launch, 8 chunks, ran 1-2% slower with it, also when
-    // rotated for one-column tiles only)
-    const int nact = (nt + 15) >> 4;
+    // computing waves take the roles with no work (the digits of token tiles that do not
+    // compute are not staged) or the lightest
     const int rot = GLU ? (nact == 1 ? 10 : nact < 4 ? 8 : 0) : 0;
     const int st = (tid + 64 * rot) & (MF_NT - 1);
+    const int sw_ = __builtin_amdgcn_readfirstlane(st >> 6);   // the staging role's wave index
     sw_rsrc rq, rs;
     if constexpr (PT) {
         // a staging thread's row ra = st & 127 is an up row iff (st >> 6) & 1: uniform per wave
         const SwTab tb_ = A.tab[e];
         if (GLU) {
-            const bool up = __builtin_amdgcn_readfirstlane((st >> 6) & 1);
+            const bool up = sw_ & 1;
             rq = sw_make_rsrc(up ? tb_.u : tb_.g, (uint32_t)A.I * rbytes);
             rs = sw_make_rsrc(up ? tb_.us : tb_.gs, (uint32_t)A.I * (uint32_t)ng * 4);
         } else {
@@ -216,163 +211,198 @@ __global__ __launch_bounds__(MF_NT, 1) void k_mf(MfArgs A) {
         rs = sw_q4_rs(W);
     }
 
-    // ---- staging: the units of a chunk of staging slot st (u = st & 511 within a group of 512 units)
+    // ---- staging: the units of a chunk of staging slot st
     //  weights (slots < 512): row ra = st & 127 of group st >> 7 (16 B packed, expanded on
     //           the store) + its scale
     //  digits:  16 B (op, quarter) of token tb of groups st >> 9 and (st >> 9) + 2: unit u of a
     //           group is token tile u >> 7, op (u >> 6) & 1, quarter (u >> 4) & 3, token u & 15;
     //           staged only for the token tiles that compute (dact)
     //  factors (slots < 256): token tx of group st >> 6
+    // Every load is a buffer load: the slot's part of its offset in a register set once,
+    // the chunk's in a scalar offset.
     constexpr int DG_PER = MF_CG * MF_TT * 8 / MF_NT;      // digit units per slot (2)
-    const bool wst = st < MF_CG * MF_ROWS;                 // uniform per wave
+    const bool wst = sw_ < 8;                              // uniform per wave
     const int ra = st & 127, ga = (st >> 7) & 3;
     const uint32_t rowa = srow(ra);
     const int tb = ((st >> 7) & 3) * 16 + (st & 15), opb = (st >> 6) & 1, kqb = (st >> 4) & 3, gb = st >> 9;
-    const uint32_t *__restrict__ dgb = A.dg + token(tb) * G * MF_DW + opb * 16 + kqb * 4;
     const int tx = st & 63, gx = (st >> 6) & 3;
-    const float *__restrict__ xsx = A.xs + token(tx) * G;
-    const bool dact = ((st >> 7) & 3) < nact;             // uniform per wave
+    const bool dact = ((sw_ >> 1) & 3) < nact;            // uniform per wave
+    const bool xst = sw_ < 4;
+    const sw_rsrc rd = sw_make_rsrc(A.dg, (uint32_t)A.dg_rows * (uint32_t)G * MF_DW * 4);
+    const sw_rsrc rx = sw_make_rsrc(A.xs, (uint32_t)A.dg_rows * (uint32_t)G * 4);
+    const uint32_t vq = rowa * rbytes + (uint32_t)ga * 16;
+    const uint32_t vs = (rowa * (uint32_t)ng + (uint32_t)((ga * SW_RG) >> A.gsh)) * 4;
+    const uint32_t vd = ((uint32_t)token(tb) * (uint32_t)G + (uint32_t)gb) * MF_DW * 4 + (uint32_t)(opb * 16 + kqb * 4) * 4;
+    const uint32_t vx = ((uint32_t)token(tx) * (uint32_t)G + (uint32_t)gx) * 4;
     sw_u32x4 pka, pkb[DG_PER];
     float psa = 1.0f, pxf = 0.f;
     auto stage_load = [&](int c) {
-        const int g0 = c * MF_CG;
+        const uint32_t g0 = (uint32_t)__builtin_amdgcn_readfirstlane(c * MF_CG);
         if (wst) {
-            pka = sw_ld16(rq, rowa * rbytes + (uint32_t)(g0 + ga) * 16, 0);
-            if (W.gs > 0) psa = sw_ld4f(rs, (rowa * (uint32_t)ng + (uint32_t)(((g0 + ga) * SW_RG) >> A.gsh)) * 4, 0);
+            pka = sw_ld16(rq, vq, g0 * 16);
+            // ((g0 + ga) * 32) >> gsh splits: g0 * 32 is a multiple of 128, ga * 32 < 128
+            if (W.gs > 0) psa = sw_ld4f(rs, vs, ((g0 * SW_RG) >> A.gsh) * 4);
         }
         if (dact)
 #pragma unroll
-            for (int v = 0; v < DG_PER; v++) pkb[v] = *(const sw_u32x4 *)(dgb + (g0 + gb + 2 * v) * MF_DW);
-        if (st < MF_CG * MF_TT) pxf = xsx[g0 + gx];
+            for (int v = 0; v < DG_PER; v++) pkb[v] = sw_ld16(rd, vd + (uint32_t)v * 2 * MF_DW * 4, g0 * MF_DW * 4);
+        if (xst) pxf = sw_ld4f(rx, vx, g0 * 4);
     };
     auto stage_store = [&](int buf) {
-        uint8_t *base = mf_lds + buf * MF_BUF;
-        sw_i32x4 *Al = (sw_i32x4 *)(base + MF_A_OFF);
-        sw_u32x4 *Bl = (sw_u32x4 *)(base + MF_B_OFF);
+        sw_i32x4 *Al = (sw_i32x4 *)(mf_lds + MF_A_OFF + buf * MF_A_SZ);
+        sw_u32x4 *Bl = (sw_u32x4 *)(mf_lds + MF_B_OFF + buf * MF_B_SZ);
         if (wst) {
             const int m = ra >> 4, i = ra & 15;
 #pragma unroll
             for (int q = 0; q < 4; q++) Al[((ga * 8 + m) * 4 + q) * 16 + i] = mf_expand(pka[q]);
-            ((float *)(base + MF_S_OFF))[ga * MF_ROWS + ra] = psa;
+            ((float *)(mf_lds + MF_S_OFF + buf * MF_S_SZ))[ga * MF_ROWS + ra] = psa;
         }
         if (dact)
 #pragma unroll
             for (int v = 0; v < DG_PER; v++) Bl[v * MF_NT + st] = pkb[v];
-        if (st < MF_CG * MF_TT) ((float *)(base + MF_X_OFF))[gx * MF_TT + tx] = pxf;
+        if (xst) ((float *)(mf_lds + MF_X_OFF + buf * MF_X_SZ))[gx * MF_TT + tx] = pxf;
     };
 
-    const bool wact = tt * 16 < nt;                        // uniform over the wave
-    float y[2][4], L[2][4][4], run[2][4];
-    // the LDS operands of one group for this wave
-    struct Frag {
-        sw_i32x4 a[2], b[2];
-        sw_f32x4 s4[2];
-        float xf;
-    };
-    auto fetch = [&](Frag &F, const uint8_t *base, int g) {
-        const sw_i32x4 *Al = (const sw_i32x4 *)(base + MF_A_OFF);
-        const sw_i32x4 *Bl = (const sw_i32x4 *)(base + MF_B_OFF);
-        const float *Sl = (const float *)(base + MF_S_OFF), *Xl = (const float *)(base + MF_X_OFF);
+    // ---- the compute waves' (row tile, token tile) pairs: two per wave (row tiles m, m + 4
+    // of token tile w >> 2) when 3-4 token tiles compute, else one (row tile w & 7 of token
+    // tile w >> 3), so that a tail tile's pairs still spread over all four SIMDs, two or
+    // four waves on each
+    constexpr int NQ = CH / MF_CG;                         // chunks per run
+    const int NR = NCV / NQ;                               // runs
+    sw_f32x4 y[2];
+    // the terms of one chunk's 4 groups summed as ((p0 + p1) + (p2 + p3)) per (row, token)
+    // into q (REAL = 0: the +0 terms of a run's padding, whose sum is +0)
+    auto quad = [&](auto NPC, auto RC, int buf, int tt, int m0, sw_f32x4 (&q)[2]) {
+        constexpr int NP = decltype(NPC)::v;
+        if constexpr (!decltype(RC)::v) {
 #pragma unroll
-        for (int mi = 0; mi < 2; mi++) {
-            const int m = mp + 4 * mi;
-            F.a[mi] = Al[((g * 8 + m) * 4 + kq) * 16 + col];
-            F.s4[mi] = *(const sw_f32x4 *)(Sl + g * MF_ROWS + 16 * m + 4 * kq);
-        }
-        F.b[0] = Bl[((g * 4 + tt) * 2 + 0) * 64 + lane];
-        F.b[1] = Bl[((g * 4 + tt) * 2 + 1) * 64 + lane];
-        F.xf = Xl[g * MF_TT + 16 * tt + col];
-    };
-    // the terms of one group (zero terms for the padding of a run: REAL = 0) into the trees
-    auto group = [&](const Frag &F, int gl, bool first, auto RC) {
-        constexpr bool REAL = decltype(RC)::v;
-        sw_i32x4 R0[2], R1[2];
-        if (REAL) {
-            const sw_i32x4 z = {0, 0, 0, 0};
-            // the MFMAs issue at raised wave priority: the SIMD's four waves, which leave
-            // each chunk's barrier together, then spread out instead of waiting on their
-            // products in step (C4: gate_up 2.33 -> 2.30 ms, down 1.32 -> 1.26 ms; the
-            // priority raised for the whole group, or for the LDS fetches, gained less)
-            __builtin_amdgcn_s_setprio(1);
+            for (int mi = 0; mi < NP; mi++) q[mi] = sw_f32x4{0.f, 0.f, 0.f, 0.f};
+            return;
+        } else {
+            // this lane's operands of group g: one base per operand plus immediate offsets
+            const uint8_t *pa = mf_lds + MF_A_OFF + buf * MF_A_SZ + ((m0 * 4 + kq) * 16 + col) * 16;
+            const uint8_t *pb = mf_lds + MF_B_OFF + buf * MF_B_SZ + (tt * 2 * 64 + lane) * 16;
+            const uint8_t *ps = mf_lds + MF_S_OFF + buf * MF_S_SZ + (16 * m0 + 4 * kq) * 4;
+            const uint8_t *px = mf_lds + MF_X_OFF + buf * MF_X_SZ + (16 * tt + col) * 4;
+            sw_f32x4 h[NP];                                // the pending pair (p0 + p1)
+            struct Frag {
+                sw_half8 a[NP], b0, b1;
+                sw_f32x4 s4[NP];
+                float xf;
+            };
+            auto fetch = [&](Frag &F, int g) {
 #pragma unroll
-            for (int mi = 0; mi < 2; mi++) {
-                R0[mi] = __builtin_amdgcn_mfma_i32_16x16x64_i8(F.a[mi], F.b[0], z, 0, 0, 0);
-                R1[mi] = __builtin_amdgcn_mfma_i32_16x16x64_i8(F.a[mi], F.b[1], z, 0, 0, 0);
-            }
-            __builtin_amdgcn_sched_barrier(0);
-            __builtin_amdgcn_s_setprio(0);
-        }
-#pragma unroll
-        for (int mi = 0; mi < 2; mi++)
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                float p = 0.f;                              // the +0 terms of a padded run
-                if (REAL) {
-                    const int acc = (R1[mi][j] << 12) + R0[mi][j];
-                    p = (float)acc * (F.s4[mi][j] * F.xf);
+                for (int mi = 0; mi < NP; mi++) {
+                    F.a[mi] = *(const sw_half8 *)(pa + (g * 8 + 4 * mi) * 4 * 16 * 16);
+                    F.s4[mi] = *(const sw_f32x4 *)(ps + (g * MF_ROWS + 64 * mi) * 4);
                 }
-                tree_push<CH>(p, gl, L[mi][j], run[mi][j]);
-                if (gl == CH - 1) y[mi][j] = first ? run[mi][j] : y[mi][j] + run[mi][j];
-            }
-    };
-    // one chunk: its 4 groups at positions Q*4 .. Q*4+3 of the run (Q known at compile time)
-    auto chunk = [&](auto QC, auto RC, int c) {
-        constexpr int Q = decltype(QC)::v;
-        const uint8_t *base = mf_lds + (c & 1) * MF_BUF;
-        const bool first = c < CH / MF_CG;                 // in the first run
-        // (one group's operands at a time: a second set for the next group measured slower,
-        // its registers spill at 128)
+                F.b0 = *(const sw_half8 *)(pb + (g * 4 * 2 + 0) * 64 * 16);
+                F.b1 = *(const sw_half8 *)(pb + (g * 4 * 2 + 1) * 64 * 16);
+                F.xf = *(const float *)(px + g * MF_TT * 4);
+            };
+            Frag Fr[2];
+            if (MF_PF) fetch(Fr[0], 0);
 #pragma unroll
-        for (int g = 0; g < MF_CG; g++) {
-            Frag F;
-            if (decltype(RC)::v) fetch(F, base, g);
-            group(F, Q * MF_CG + g, first, RC);
-            __builtin_amdgcn_sched_barrier(0);
+            for (int g = 0; g < MF_CG; g++) {
+                if (!MF_PF) fetch(Fr[g & 1], g);
+                const Frag &C = Fr[g & 1];
+                const sw_f32x4 z = {0.f, 0.f, 0.f, 0.f};
+                sw_f32x4 R0[NP], R1[NP];
+                // the MFMAs issue at raised wave priority: the SIMD's waves, which leave each
+                // chunk's barrier together, then spread out instead of waiting on their
+                // products in step
+                __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+                for (int mi = 0; mi < NP; mi++) {
+                    R0[mi] = __builtin_amdgcn_mfma_f32_16x16x32_f16(C.a[mi], C.b0, z, 0, 0, 0);
+                    R1[mi] = __builtin_amdgcn_mfma_f32_16x16x32_f16(C.a[mi], C.b1, z, 0, 0, 0);
+                }
+                __builtin_amdgcn_s_setprio(0);
+                // (MF_PF: the next group's operands load while these products finish)
+                if (MF_PF && g + 1 < MF_CG) fetch(Fr[(g + 1) & 1], g + 1);
+#pragma unroll
+                for (int mi = 0; mi < NP; mi++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        // (float)acc exactly, times (s * 2^(e - 21)), as dot8's term
+                        const float p = __builtin_fmaf(R1[mi][j], 4096.0f, R0[mi][j]) * (C.s4[mi][j] * C.xf);
+                        if (g == 0 || g == 2) h[mi][j] = p;
+                        else if (g == 1) q[mi][j] = h[mi][j] + p;
+                        else q[mi][j] = q[mi][j] + (h[mi][j] + p);
+                    }
+                __builtin_amdgcn_sched_barrier(0);         // one group's operands in flight at a time
+            }
         }
     };
-    auto chunk_q = [&](auto RC, int c) {
-        switch (c % (CH / MF_CG)) {
-            case 0: chunk(MfIc<0>{}, RC, c); break;
-            case 1: if constexpr (CH / MF_CG > 1) chunk(MfIc<1 % (CH / MF_CG)>{}, RC, c); break;
-            case 2: if constexpr (CH / MF_CG > 2) chunk(MfIc<2 % (CH / MF_CG)>{}, RC, c); break;
-            default: if constexpr (CH / MF_CG > 3) chunk(MfIc<3 % (CH / MF_CG)>{}, RC, c); break;
+    // the main loop for NP pairs per wave: runs of NQ chunks, each run's quads summed
+    // ((q0 + q1) + (q2 + q3)) (NQ = 4), the runs added left to right into y
+    auto main_loop = [&](auto NPC) {
+        constexpr int NP = decltype(NPC)::v;
+        const int tt = NP == 2 ? wave >> 2 : wave >> 3, m0 = NP == 2 ? wave & 3 : wave & 7;
+        const bool wact = tt < nact;                       // uniform over the wave
+        for (int r = 0; r < NR; r++) {
+            sw_f32x4 ra[NP], rb[NP], q[2];
+#pragma unroll
+            for (int Q = 0; Q < NQ; Q++) {
+                const int c = r * NQ + Q;
+                const int buf = NQ > 1 ? (Q & 1) : (c & 1);
+                if (wact) {
+                    // (a run-time test also for FULL: as a branch it keeps the compiler from
+                    // interleaving the unrolled chunks, which spills at 128 registers)
+                    if (c < NC) quad(NPC, MfIc<1>{}, buf, tt, m0, q);
+                    else quad(NPC, MfIc<0>{}, buf, tt, m0, q);
+#pragma unroll
+                    for (int mi = 0; mi < NP; mi++) {
+                        if (Q == 0) ra[mi] = q[mi];
+                        else if (Q == 1 && NQ == 4) ra[mi] = ra[mi] + q[mi];
+                        else if (Q == 2) rb[mi] = q[mi];
+                        else if (Q == 3) ra[mi] = ra[mi] + (rb[mi] + q[mi]);
+                        else ra[mi] = ra[mi] + q[mi];      // Q == 1 of NQ == 2
+                    }
+                }
+                if (c + 1 < NC) stage_store((c + 1) & 1);  // read by no wave since the last barrier
+                if (c + 2 < NC) stage_load(c + 2);         // registers only: issued before the barrier's wait
+                __syncthreads();
+            }
+            if (wact)
+#pragma unroll
+                for (int mi = 0; mi < NP; mi++) y[mi] = r == 0 ? ra[mi] : y[mi] + ra[mi];
         }
+        // the block's sums to LDS, [token][local row]; every wave is past its last read
+        float *yl = (float *)mf_lds;
+        if (wact)
+#pragma unroll
+            for (int mi = 0; mi < NP; mi++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) yl[(16 * tt + col) * MF_YLD + 16 * (m0 + 4 * mi) + 4 * kq + j] = y[mi][j];
     };
 
     stage_load(0);
     stage_store(0);
     if (NC > 1) stage_load(1);
     __syncthreads();
-    for (int c = 0; c < NCV; c++) {
-        if (wact) {
-            if (FULL || c < NC) chunk_q(MfIc<1>{}, c);
-            else if constexpr (!FULL) chunk_q(MfIc<0>{}, c);
-        }
-        if (c + 1 < NC) stage_store((c + 1) & 1);          // read by no wave since the last barrier
-        if (c + 2 < NC) stage_load(c + 2);                 // registers only: issued before the barrier's wait
-        __syncthreads();
-    }
+    if (nact > 2) main_loop(MfIc<2>{});
+    else main_loop(MfIc<1>{});
+    __syncthreads();
 
+    const float *yl = (const float *)mf_lds;
     if constexpr (GLU) {
-        // h = silu(gate) * up per (token, output), through LDS to the digit writers
-        float *hl = (float *)mf_lds;                       // [MF_TT][MF_HLD]; every wave is past its last read
+        // h = silu(gate) * up per (token, output), to the digit writers
+        float *hl = (float *)(mf_lds + MF_HL_OFF);         // [MF_TT][MF_HLD]
         const int I = A.I;
-        if (wact) {
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const int i = 16 * mp + 4 * kq + j, t = 16 * tt + col;
-                    float yg = y[0][j], yu = y[1][j];
-                    if (W.gs <= 0) {                        // per-row scales after the sum
-                        if constexpr (PT) {
-                            yg = yg * A.tab[e].gs[i0 + i];
-                            yu = yu * A.tab[e].us[i0 + i];
-                        } else {
-                            yg = yg * W.s[(int64_t)e * (2 * I) + i0 + i];
-                            yu = yu * W.s[(int64_t)e * (2 * I) + I + i0 + i];
-                        }
-                    }
-                    hl[t * MF_HLD + i] = (yg / (1.0f + expf(-yg))) * yu;
+        for (int v = tid; v < nt * 64; v += MF_NT) {
+            const int t = v >> 6, i = v & 63;
+            float yg = yl[t * MF_YLD + i], yu = yl[t * MF_YLD + 64 + i];
+            if (W.gs <= 0) {                                // per-row scales after the sum
+                if constexpr (PT) {
+                    yg = yg * A.tab[e].gs[i0 + i];
+                    yu = yu * A.tab[e].us[i0 + i];
+                } else {
+                    yg = yg * W.s[(int64_t)e * (2 * I) + i0 + i];
+                    yu = yu * W.s[(int64_t)e * (2 * I) + I + i0 + i];
                 }
+            }
+            hl[t * MF_HLD + i] = (yg / (1.0f + expf(-yg))) * yu;
         }
         __syncthreads();
         // the block's 64 outputs are two limb groups of the down projection's input
@@ -384,21 +414,13 @@ __global__ __launch_bounds__(MF_NT, 1) void k_mf(MfArgs A) {
             digits_group(hl[t * MF_HLD + 32 * q + i], i, A.hdg + (prow * GI + gi) * MF_DW, A.hxs + prow * GI + gi);
         }
     } else {
-        if (wact) {
-            const int t = 16 * tt + col;
-            if (t < nt) {
-                float *yrow = A.Y + (int64_t)(beg + t0 + t) * O;
-#pragma unroll
-                for (int mi = 0; mi < 2; mi++) {
-                    const int row = r0 + 16 * (mp + 4 * mi) + 4 * kq;
-                    if (row < O) {
-                        sw_f32x4 o;
-#pragma unroll
-                        for (int j = 0; j < 4; j++)
-                            o[j] = W.gs > 0 ? y[mi][j] : y[mi][j] * (PT ? A.tab[e].ds[row + j] : W.s[(int64_t)e * O + row + j]);
-                        *(sw_f32x4 *)(yrow + row) = o;
-                    }
-                }
+        // rows r0 .. r0 + 127 of each token (past O: not stored)
+        const int r = tid & (MF_ROWS - 1), row = r0 + r;
+        if (row < O) {
+            const float sc = W.gs > 0 ? 1.0f : (PT ? A.tab[e].ds[row] : W.s[(int64_t)e * O + row]);
+            for (int t = tid >> 7; t < nt; t += MF_NT / MF_ROWS) {
+                const float v = yl[t * MF_YLD + r];
+                A.Y[(int64_t)(beg + t0 + t) * O + row] = W.gs > 0 ? v : v * sc;
             }
         }
     }
@@ -406,8 +428,8 @@ __global__ __launch_bounds__(MF_NT, 1) void k_mf(MfArgs A) {
 
 // ------------------------------------------------------------ launch ----
 static size_t mf_lds_bytes() {
-    const size_t h = (size_t)MF_TT * MF_HLD * 4;
-    return 2 * MF_BUF > h ? 2 * MF_BUF : h;
+    const size_t h = MF_HL_OFF + (size_t)MF_TT * MF_HLD * 4;
+    return MF_LDS_STAGE > h ? MF_LDS_STAGE : h;
 }
 // dynamic LDS above 64 KB, raised once per kernel, outside any stream work
 template <int GLU, int CH, int FULL, int PT>
@@ -431,46 +453,48 @@ static int mf_dispatch(hipStream_t st, unsigned nblocks, const MfArgs &A) {
     if (CH == 4) return full ? mf_go<GLU, 4, 1, PT>(st, nblocks, A) : mf_go<GLU, 4, 0, PT>(st, nblocks, A);
     return -1;
 }
-// shapes: K a multiple of 128 (whole chunks of 4 input groups), tiles listed (items, P)
-static int mf_check(const SwQ4 &W, const SwGroups &g, int &gsh) {
+// shapes: K a multiple of 128 (whole chunks of 4 input groups), tiles listed (items, P),
+// the digits addressed by 32-bit offsets
+static int mf_check(const SwQ4 &W, const SwGroups &g, int &gsh, int dg_rows) {
     if (W.K % (SW_RG * MF_CG) || !g.items || !g.P || g.ngroups_max <= 0 || !sw_q4_extent_ok(W)) return -1;
+    if (dg_rows <= 0 || (uint64_t)dg_rows * (uint64_t)W.K * 4 > 0xFFFFFFFFull) return -1;
     return sw_q4_gsh(W, gsh);
 }
 
-int sw_launch_mf_glu(hipStream_t st, SwQ4 W, const uint32_t *dg, const float *xs, SwGroups g, int I, uint32_t *hdg,
-                     float *hxs) {
+int sw_launch_mf_glu(hipStream_t st, SwQ4 W, const uint32_t *dg, const float *xs, int dg_rows, SwGroups g, int I,
+                     uint32_t *hdg, float *hxs) {
     int gsh;
-    if (mf_check(W, g, gsh) || I % 64 || W.O != 2 * I) return -1;
+    if (mf_check(W, g, gsh, dg_rows) || I % 64 || W.O != 2 * I) return -1;
     const int nrb = I / 64;
-    const MfArgs A = {W, gsh, dg, xs, g, I, nrb, hdg, hxs, nullptr};
+    const MfArgs A = {W, gsh, dg, xs, dg_rows, g, I, nrb, hdg, hxs, nullptr};
     return mf_dispatch<1>(st, (unsigned)(g.ngroups_max * nrb), A);
 }
 
-int sw_launch_mf_rows(hipStream_t st, SwQ4 W, const uint32_t *dg, const float *xs, SwGroups g, float *Y) {
+int sw_launch_mf_rows(hipStream_t st, SwQ4 W, const uint32_t *dg, const float *xs, int dg_rows, SwGroups g, float *Y) {
     int gsh;
-    if (mf_check(W, g, gsh) || W.O % 4) return -1;
+    if (mf_check(W, g, gsh, dg_rows) || W.O % 4) return -1;
     const int nrb = (W.O + MF_ROWS - 1) / MF_ROWS;
-    const MfArgs A = {W, gsh, dg, xs, g, 0, nrb, nullptr, nullptr, Y};
+    const MfArgs A = {W, gsh, dg, xs, dg_rows, g, 0, nrb, nullptr, nullptr, Y};
     return mf_dispatch<0>(st, (unsigned)(g.ngroups_max * nrb), A);
 }
 
 // the same two GEMMs over per-group tensors: group c's gate/up/down are tab[gexp[c]]
 // (W gives O, K and gs; each tensor holds one expert)
-int sw_launch_mf_glu_tab(hipStream_t st, SwQ4 W, const SwTab *tab, const uint32_t *dg, const float *xs, SwGroups g,
-                         int I, uint32_t *hdg, float *hxs) {
+int sw_launch_mf_glu_tab(hipStream_t st, SwQ4 W, const SwTab *tab, const uint32_t *dg, const float *xs, int dg_rows,
+                         SwGroups g, int I, uint32_t *hdg, float *hxs) {
     int gsh;
     W.E = 1;
-    if (!tab || !hdg || !hxs || mf_check(W, g, gsh) || I % 64 || W.O != 2 * I) return -1;
+    if (!tab || !hdg || !hxs || mf_check(W, g, gsh, dg_rows) || I % 64 || W.O != 2 * I) return -1;
     const int nrb = I / 64;
-    const MfArgs A = {W, gsh, dg, xs, g, I, nrb, hdg, hxs, nullptr, tab};
+    const MfArgs A = {W, gsh, dg, xs, dg_rows, g, I, nrb, hdg, hxs, nullptr, tab};
     return mf_dispatch<1, 1>(st, (unsigned)(g.ngroups_max * nrb), A);
 }
-int sw_launch_mf_rows_tab(hipStream_t st, SwQ4 W, const SwTab *tab, const uint32_t *dg, const float *xs, SwGroups g,
-                          float *Y) {
+int sw_launch_mf_rows_tab(hipStream_t st, SwQ4 W, const SwTab *tab, const uint32_t *dg, const float *xs, int dg_rows,
+                          SwGroups g, float *Y) {
     int gsh;
     W.E = 1;
-    if (!tab || !Y || mf_check(W, g, gsh) || W.O % 4) return -1;
+    if (!tab || !Y || mf_check(W, g, gsh, dg_rows) || W.O % 4) return -1;
     const int nrb = (W.O + MF_ROWS - 1) / MF_ROWS;
-    const MfArgs A = {W, gsh, dg, xs, g, 0, nrb, nullptr, nullptr, Y, tab};
+    const MfArgs A = {W, gsh, dg, xs, dg_rows, g, 0, nrb, nullptr, nullptr, Y, tab};
     return mf_dispatch<0, 1>(st, (unsigned)(g.ngroups_max * nrb), A);
 }

@@ -346,13 +346,14 @@ int sw_launch_stage_experts(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, const fl
 #define SW_MF_TT 64
 #define SW_MF_DIGIT_BYTES 128     // MFMA digits of one (row, input group): 32 dwords
 int sw_launch_digits(hipStream_t st, const float *x, int rows, int K, uint32_t *dg, float *xs);
-int sw_launch_mf_glu(hipStream_t st, SwQ4 W, const uint32_t *dg, const float *xs, SwGroups g, int I, uint32_t *hdg,
-                     float *hxs);
-int sw_launch_mf_rows(hipStream_t st, SwQ4 W, const uint32_t *dg, const float *xs, SwGroups g, float *Y);
-int sw_launch_mf_glu_tab(hipStream_t st, SwQ4 W, const SwTab *tab, const uint32_t *dg, const float *xs, SwGroups g,
-                         int I, uint32_t *hdg, float *hxs);
-int sw_launch_mf_rows_tab(hipStream_t st, SwQ4 W, const SwTab *tab, const uint32_t *dg, const float *xs, SwGroups g,
-                          float *Y);
+// (dg_rows: the rows of dg and xs; dg_rows * K * 4 must stay below 2^32)
+int sw_launch_mf_glu(hipStream_t st, SwQ4 W, const uint32_t *dg, const float *xs, int dg_rows, SwGroups g, int I,
+                     uint32_t *hdg, float *hxs);
+int sw_launch_mf_rows(hipStream_t st, SwQ4 W, const uint32_t *dg, const float *xs, int dg_rows, SwGroups g, float *Y);
+int sw_launch_mf_glu_tab(hipStream_t st, SwQ4 W, const SwTab *tab, const uint32_t *dg, const float *xs, int dg_rows,
+                         SwGroups g, int I, uint32_t *hdg, float *hxs);
+int sw_launch_mf_rows_tab(hipStream_t st, SwQ4 W, const SwTab *tab, const uint32_t *dg, const float *xs, int dg_rows,
+                          SwGroups g, float *Y);
 // the reference's IDOT int4 contract (k_idot.hip, per-row scales): int8 activations
 // per 32-block xi[rows][K/32][8 dwords] + xs[rows][K/32], then grouped rows (whole groups)
 int sw_launch_idot_quant(hipStream_t st, const float *x, int rows, int K, uint32_t *xi, float *xs);
