@@ -153,6 +153,12 @@ __device__ __forceinline__ sw_i32x4 mf_expand(uint32_t w) {
 template <int N>
 struct MfIc { static constexpr int v = N; };
 
+// the value of lane J of each lane's quad (DPP quad_perm [J, J, J, J])
+template <int J>
+__device__ __forceinline__ float mf_quad_bcast(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x55 * J, 0xF, 0xF, true));
+}
+
 template <int GLU, int CH, int FULL, int PT>
 __global__ __launch_bounds__(MF_NT, 1) void k_mf(MfArgs A) {
     static_assert(MF_NT == 1024 && MF_CG * MF_ROWS == 512 && MF_CG * MF_TT * 8 == 2 * MF_NT, "staging map");
@@ -285,16 +291,19 @@ __global__ __launch_bounds__(MF_NT, 1) void k_mf(MfArgs A) {
             const uint8_t *ps = mf_lds + MF_S_OFF + buf * MF_S_SZ + (16 * m0 + 4 * kq) * 4;
             const uint8_t *px = mf_lds + MF_X_OFF + buf * MF_X_SZ + (16 * tt + col) * 4;
             sw_f32x4 h[NP];                                // the pending pair (p0 + p1)
+            // a lane's four rows 4 kq + j take their scales from the four lanes of its quad
+            // (lane col & 3 reads row 4 kq + (col & 3)), moved by DPP into the products: a
+            // quarter of the LDS reads of one 16-byte read per lane
             struct Frag {
                 sw_half8 a[NP], b0, b1;
-                sw_f32x4 s4[NP];
+                float s1[NP];
                 float xf;
             };
             auto fetch = [&](Frag &F, int g) {
 #pragma unroll
                 for (int mi = 0; mi < NP; mi++) {
                     F.a[mi] = *(const sw_half8 *)(pa + (g * 8 + 4 * mi) * 4 * 16 * 16);
-                    F.s4[mi] = *(const sw_f32x4 *)(ps + (g * MF_ROWS + 64 * mi) * 4);
+                    F.s1[mi] = *(const float *)(ps + (g * MF_ROWS + 64 * mi + (col & 3)) * 4);
                 }
                 F.b0 = *(const sw_half8 *)(pb + (g * 4 * 2 + 0) * 64 * 16);
                 F.b1 = *(const sw_half8 *)(pb + (g * 4 * 2 + 1) * 64 * 16);
@@ -321,15 +330,19 @@ __global__ __launch_bounds__(MF_NT, 1) void k_mf(MfArgs A) {
                 // (MF_PF: the next group's operands load while these products finish)
                 if (MF_PF && g + 1 < MF_CG) fetch(Fr[(g + 1) & 1], g + 1);
 #pragma unroll
-                for (int mi = 0; mi < NP; mi++)
+                for (int mi = 0; mi < NP; mi++) {
+                    // s * 2^(e - 21) of rows 4 kq + j (the DPP moves fold into the products)
+                    const float t4[4] = {mf_quad_bcast<0>(C.s1[mi]) * C.xf, mf_quad_bcast<1>(C.s1[mi]) * C.xf,
+                                         mf_quad_bcast<2>(C.s1[mi]) * C.xf, mf_quad_bcast<3>(C.s1[mi]) * C.xf};
 #pragma unroll
                     for (int j = 0; j < 4; j++) {
                         // (float)acc exactly, times (s * 2^(e - 21)), as dot8's term
-                        const float p = __builtin_fmaf(R1[mi][j], 4096.0f, R0[mi][j]) * (C.s4[mi][j] * C.xf);
+                        const float p = __builtin_fmaf(R1[mi][j], 4096.0f, R0[mi][j]) * t4[j];
                         if (g == 0 || g == 2) h[mi][j] = p;
                         else if (g == 1) q[mi][j] = h[mi][j] + p;
                         else q[mi][j] = q[mi][j] + (h[mi][j] + p);
                     }
+                }
                 __builtin_amdgcn_sched_barrier(0);         // one group's operands in flight at a time
             }
         }
