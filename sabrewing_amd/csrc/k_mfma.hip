@@ -62,9 +62,10 @@
 #ifndef MF_PF
 #define MF_PF 1            // the next group's operands fetched during this group's products
 #endif
-#define MF_YLD 129         // floats per token row of the block's sums after the loop
+#define MF_YLD 129         // floats per token row of a row block's gate and up sums (<= 32 tokens)
 #define MF_HLD 65          // floats per token row of h in the gate_up epilogue
-#define MF_HL_OFF (MF_TT * MF_YLD * 4)
+#define MF_EP_OFF MF_LDS_STAGE                            // the epilogue's own LDS
+#define MF_EP_SZ (MF_TT * MF_HLD * 4 > 32 * MF_YLD * 4 ? MF_TT * MF_HLD * 4 : 32 * MF_YLD * 4)
 
 // ------------------------------------------------------------ digits ----
 // one group by the 32 lanes of a half-wave (i = lane in the half): the same
@@ -124,6 +125,7 @@ struct MfArgs {
     SwGroups grp;           // tiles: items of up to MF_TT tokens, P live
     int I;                  // GLU: the intermediate size (W.O == 2 I)
     int nrb;                // row blocks
+    int rbper;              // row blocks per block (dividing nrb)
     uint32_t *hdg;          // GLU: h of every packed row as digits [T][I/32][MF_DW]
     float *hxs;             //      and factors [T][I/32]
     float *Y;               // rows: [T][O]
@@ -173,14 +175,19 @@ __global__ __launch_bounds__(MF_NT, 1) void k_mf(MfArgs A) {
               kq = lane >> 4;
 
     // block -> (tile, row block), XCD-aware over the live blocks
-    const int nlive = *grp.P * A.nrb;
+    // (a block takes rbper consecutive row blocks of one tile, its chunk pipeline running on
+    // from one row block to the next: one start and one drain per rbper row blocks)
+    const int rbper = GLU ? 1 : A.rbper;                   // (gate_up: one, known to the compiler)
+    const int nrg = A.nrb / rbper;                         // row-block runs per tile
+    const int nlive = *grp.P * nrg;
     if ((int)blockIdx.x >= nlive) return;
     const int wk = sw_xcd_work((int)blockIdx.x, nlive);
-    const int tile = wk / A.nrb, rb = wk - tile * A.nrb;
+    const int tile = wk / nrg, rbf = (wk - tile * nrg) * rbper;     // the block's first row block
     int e, beg, t0, tend;
     if (!grp_work(grp, tile, MF_TT, e, beg, t0, tend)) return;
     const int nt = tend - t0, nact = (nt + 15) >> 4;       // tokens, token tiles with tokens
-    const int i0 = rb * 64, r0 = rb * MF_ROWS;
+    const int i0 = rbf * 64, r0 = rbf * MF_ROWS;           // (of the first row block)
+    constexpr int RPB = GLU ? 64 : MF_ROWS;                // weight rows a row block moves on by
     // weight row of local row r (GLU: gate rows i0..i0+63, then the up rows)
     // (PT: row r of the group's own gate, up or down tensor)
     auto srow = [&](int r) -> uint32_t {
@@ -242,12 +249,16 @@ __global__ __launch_bounds__(MF_NT, 1) void k_mf(MfArgs A) {
     const uint32_t vx = ((uint32_t)token(tx) * (uint32_t)G + (uint32_t)gx) * 4;
     sw_u32x4 pka, pkb[DG_PER];
     float psa = 1.0f, pxf = 0.f;
-    auto stage_load = [&](int c) {
+    // chunk q of the block: chunk q % NCV of its row block q / NCV (the row block's rows in
+    // the vector offset, which the range check covers)
+    auto stage_load = [&](int q) {
+        const int rbi = GLU ? 0 : q / NCV, c = q - rbi * NCV;
         const uint32_t g0 = (uint32_t)__builtin_amdgcn_readfirstlane(c * MF_CG);
         if (wst) {
-            pka = sw_ld16(rq, vq, g0 * 16);
+            const uint32_t dr = (uint32_t)(rbi * RPB);
+            pka = sw_ld16(rq, vq + dr * rbytes, g0 * 16);
             // ((g0 + ga) * 32) >> gsh splits: g0 * 32 is a multiple of 128, ga * 32 < 128
-            if (W.gs > 0) psa = sw_ld4f(rs, vs, ((g0 * SW_RG) >> A.gsh) * 4);
+            if (W.gs > 0) psa = sw_ld4f(rs, vs + dr * (uint32_t)ng * 4, ((g0 * SW_RG) >> A.gsh) * 4);
         }
         if (dact)
 #pragma unroll
@@ -275,7 +286,6 @@ __global__ __launch_bounds__(MF_NT, 1) void k_mf(MfArgs A) {
     // four waves on each
     constexpr int NQ = CH / MF_CG;                         // chunks per run
     const int NR = NCV / NQ;                               // runs
-    sw_f32x4 y[2];
     // the terms of one chunk's 4 groups summed as ((p0 + p1) + (p2 + p3)) per (row, token)
     // into q (REAL = 0: the +0 terms of a run's padding, whose sum is +0)
     auto quad = [&](auto NPC, auto RC, int buf, int tt, int m0, sw_f32x4 (&q)[2]) {
@@ -347,103 +357,129 @@ __global__ __launch_bounds__(MF_NT, 1) void k_mf(MfArgs A) {
             }
         }
     };
-    // the main loop for NP pairs per wave: runs of NQ chunks, each run's quads summed
-    // ((q0 + q1) + (q2 + q3)) (NQ = 4), the runs added left to right into y
+    // a row block's sums out: gate_up, h = silu(gate) * up to its digits (two limb
+    // groups of the down's input per token); down, the rows of each token
+    auto epilogue = [&](auto NPC, int rb, const sw_f32x4 (&y)[2], int tt, int m0, bool wact) {
+        constexpr int NP = decltype(NPC)::v;
+        const int ib = rb * 64, rr0 = rb * MF_ROWS;
+        if constexpr (GLU) {
+            const int I = A.I;
+            float *el = (float *)(mf_lds + MF_EP_OFF);
+            auto gsc = [&](int i) -> float { return PT ? A.tab[e].gs[ib + i] : W.s[(int64_t)e * (2 * I) + ib + i]; };
+            auto usc = [&](int i) -> float { return PT ? A.tab[e].us[ib + i] : W.s[(int64_t)e * (2 * I) + I + ib + i]; };
+            if constexpr (NP == 2) {
+                // a lane holds the gate (row tile m0) and up (m0 + 4) sums of outputs 16 m0 + 4 kq + j
+                if (wact)
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const int i = 16 * m0 + 4 * kq + j, t = 16 * tt + col;
+                        float yg = y[0][j], yu = y[1][j];
+                        if (W.gs <= 0) {                        // per-row scales after the sum
+                            yg = yg * gsc(i);
+                            yu = yu * usc(i);
+                        }
+                        el[t * MF_HLD + i] = (yg / (1.0f + expf(-yg))) * yu;
+                    }
+            } else {
+                // (one row tile per wave: the gate and up sums of at most 32 tokens as they are)
+                if (wact)
+#pragma unroll
+                    for (int j = 0; j < 4; j++) el[(16 * tt + col) * MF_YLD + 16 * m0 + 4 * kq + j] = y[0][j];
+            }
+            __syncthreads();
+            // the row block's 64 outputs are two limb groups of the down projection's input
+            const int GI = I / SW_RG, hw = tid >> 5, i = tid & 31;
+            for (int job = hw; job < 2 * nt; job += MF_NT / 32) {
+                const int t = job >> 1, q = job & 1;
+                const int64_t prow = beg + t0 + t;
+                const int gi = 2 * rb + q;
+                float h;
+                if constexpr (NP == 2) {
+                    h = el[t * MF_HLD + 32 * q + i];
+                } else {
+                    const int o = 32 * q + i;
+                    float yg = el[t * MF_YLD + o], yu = el[t * MF_YLD + 64 + o];
+                    if (W.gs <= 0) {
+                        yg = yg * gsc(o);
+                        yu = yu * usc(o);
+                    }
+                    h = (yg / (1.0f + expf(-yg))) * yu;
+                }
+                digits_group(h, i, A.hdg + (prow * GI + gi) * MF_DW, A.hxs + prow * GI + gi);
+            }
+        } else {
+            // a lane holds rows 16 m + 4 kq .. + 3 of token 16 tt + col: one 16-byte store each
+            const int t = 16 * tt + col;
+            if (wact && t < nt) {
+                float *yrow = A.Y + (int64_t)(beg + t0 + t) * O;
+#pragma unroll
+                for (int mi = 0; mi < NP; mi++) {
+                    const int row = rr0 + 16 * (m0 + 4 * mi) + 4 * kq;
+                    if (row < O) {
+                        sw_f32x4 o;
+#pragma unroll
+                        for (int j = 0; j < 4; j++)
+                            o[j] = W.gs > 0 ? y[mi][j] : y[mi][j] * (PT ? A.tab[e].ds[row + j] : W.s[(int64_t)e * O + row + j]);
+                        *(sw_f32x4 *)(yrow + row) = o;
+                    }
+                }
+            }
+        }
+    };
+    // the main loop for NP pairs per wave: for each of the block's row blocks, runs of NQ
+    // chunks, each run's quads summed ((q0 + q1) + (q2 + q3)) (NQ = 4), the runs added
+    // left to right into y; then the row block's epilogue.  The staging runs over the
+    // block's chunks q = rbi NCV + c without a break between row blocks.
+    const int QT = rbper * NCV;
+    auto real = [&](int q) { return GLU ? q < NC : q - q / NCV * NCV < NC; };
     auto main_loop = [&](auto NPC) {
         constexpr int NP = decltype(NPC)::v;
         const int tt = NP == 2 ? wave >> 2 : wave >> 3, m0 = NP == 2 ? wave & 3 : wave & 7;
         const bool wact = tt < nact;                       // uniform over the wave
-        for (int r = 0; r < NR; r++) {
-            sw_f32x4 ra[NP], rb[NP], q[2];
+        for (int rbi = 0; rbi < rbper; rbi++) {
+            sw_f32x4 y[2];
+            for (int r = 0; r < NR; r++) {
+                sw_f32x4 ra[NP], rb[NP], q[2];
 #pragma unroll
-            for (int Q = 0; Q < NQ; Q++) {
-                const int c = r * NQ + Q;
-                const int buf = NQ > 1 ? (Q & 1) : (c & 1);
-                if (wact) {
-                    // (a run-time test also for FULL: as a branch it keeps the compiler from
-                    // interleaving the unrolled chunks, which spills at 128 registers)
-                    if (c < NC) quad(NPC, MfIc<1>{}, buf, tt, m0, q);
-                    else quad(NPC, MfIc<0>{}, buf, tt, m0, q);
+                for (int Q = 0; Q < NQ; Q++) {
+                    const int c = r * NQ + Q, qg = rbi * NCV + c;
+                    const int buf = NQ > 1 ? (Q & 1) : (qg & 1);   // (NCV is even when NQ > 1)
+                    if (wact) {
+                        // (a run-time test also for FULL: as a branch it keeps the compiler from
+                        // interleaving the unrolled chunks, which spills at 128 registers)
+                        if (c < NC) quad(NPC, MfIc<1>{}, buf, tt, m0, q);
+                        else quad(NPC, MfIc<0>{}, buf, tt, m0, q);
 #pragma unroll
-                    for (int mi = 0; mi < NP; mi++) {
-                        if (Q == 0) ra[mi] = q[mi];
-                        else if (Q == 1 && NQ == 4) ra[mi] = ra[mi] + q[mi];
-                        else if (Q == 2) rb[mi] = q[mi];
-                        else if (Q == 3) ra[mi] = ra[mi] + (rb[mi] + q[mi]);
-                        else ra[mi] = ra[mi] + q[mi];      // Q == 1 of NQ == 2
+                        for (int mi = 0; mi < NP; mi++) {
+                            if (Q == 0) ra[mi] = q[mi];
+                            else if (Q == 1 && NQ == 4) ra[mi] = ra[mi] + q[mi];
+                            else if (Q == 2) rb[mi] = q[mi];
+                            else if (Q == 3) ra[mi] = ra[mi] + (rb[mi] + q[mi]);
+                            else ra[mi] = ra[mi] + q[mi];  // Q == 1 of NQ == 2
+                        }
                     }
+                    if (qg + 1 < QT && real(qg + 1)) stage_store((qg + 1) & 1);  // read by no wave since the last barrier
+                    if (qg + 2 < QT && real(qg + 2)) stage_load(qg + 2);         // registers only: issued before the barrier's wait
+                    __syncthreads();
                 }
-                if (c + 1 < NC) stage_store((c + 1) & 1);  // read by no wave since the last barrier
-                if (c + 2 < NC) stage_load(c + 2);         // registers only: issued before the barrier's wait
-                __syncthreads();
+                if (wact)
+#pragma unroll
+                    for (int mi = 0; mi < NP; mi++) y[mi] = r == 0 ? ra[mi] : y[mi] + ra[mi];
             }
-            if (wact)
-#pragma unroll
-                for (int mi = 0; mi < NP; mi++) y[mi] = r == 0 ? ra[mi] : y[mi] + ra[mi];
+            epilogue(NPC, rbf + rbi, y, tt, m0, wact);
         }
-        // the block's sums to LDS, [token][local row]; every wave is past its last read
-        float *yl = (float *)mf_lds;
-        if (wact)
-#pragma unroll
-            for (int mi = 0; mi < NP; mi++)
-#pragma unroll
-                for (int j = 0; j < 4; j++) yl[(16 * tt + col) * MF_YLD + 16 * (m0 + 4 * mi) + 4 * kq + j] = y[mi][j];
     };
 
     stage_load(0);
     stage_store(0);
-    if (NC > 1) stage_load(1);
+    if (QT > 1 && real(1)) stage_load(1);
     __syncthreads();
     if (nact > 2) main_loop(MfIc<2>{});
     else main_loop(MfIc<1>{});
-    __syncthreads();
-
-    const float *yl = (const float *)mf_lds;
-    if constexpr (GLU) {
-        // h = silu(gate) * up per (token, output), to the digit writers
-        float *hl = (float *)(mf_lds + MF_HL_OFF);         // [MF_TT][MF_HLD]
-        const int I = A.I;
-        for (int v = tid; v < nt * 64; v += MF_NT) {
-            const int t = v >> 6, i = v & 63;
-            float yg = yl[t * MF_YLD + i], yu = yl[t * MF_YLD + 64 + i];
-            if (W.gs <= 0) {                                // per-row scales after the sum
-                if constexpr (PT) {
-                    yg = yg * A.tab[e].gs[i0 + i];
-                    yu = yu * A.tab[e].us[i0 + i];
-                } else {
-                    yg = yg * W.s[(int64_t)e * (2 * I) + i0 + i];
-                    yu = yu * W.s[(int64_t)e * (2 * I) + I + i0 + i];
-                }
-            }
-            hl[t * MF_HLD + i] = (yg / (1.0f + expf(-yg))) * yu;
-        }
-        __syncthreads();
-        // the block's 64 outputs are two limb groups of the down projection's input
-        const int GI = I / SW_RG, hw = tid >> 5, i = tid & 31;
-        for (int job = hw; job < 2 * nt; job += MF_NT / 32) {
-            const int t = job >> 1, q = job & 1;
-            const int64_t prow = beg + t0 + t;
-            const int gi = 2 * rb + q;
-            digits_group(hl[t * MF_HLD + 32 * q + i], i, A.hdg + (prow * GI + gi) * MF_DW, A.hxs + prow * GI + gi);
-        }
-    } else {
-        // rows r0 .. r0 + 127 of each token (past O: not stored)
-        const int r = tid & (MF_ROWS - 1), row = r0 + r;
-        if (row < O) {
-            const float sc = W.gs > 0 ? 1.0f : (PT ? A.tab[e].ds[row] : W.s[(int64_t)e * O + row]);
-            for (int t = tid >> 7; t < nt; t += MF_NT / MF_ROWS) {
-                const float v = yl[t * MF_YLD + r];
-                A.Y[(int64_t)(beg + t0 + t) * O + row] = W.gs > 0 ? v : v * sc;
-            }
-        }
-    }
 }
 
 // ------------------------------------------------------------ launch ----
-static size_t mf_lds_bytes() {
-    const size_t h = MF_HL_OFF + (size_t)MF_TT * MF_HLD * 4;
-    return MF_LDS_STAGE > h ? MF_LDS_STAGE : h;
-}
+static size_t mf_lds_bytes() { return (size_t)MF_EP_OFF + MF_EP_SZ; }
 // dynamic LDS above 64 KB, raised once per kernel, outside any stream work
 template <int GLU, int CH, int FULL, int PT>
 static int mf_go(hipStream_t st, unsigned nblocks, const MfArgs &A) {
@@ -466,6 +502,19 @@ static int mf_dispatch(hipStream_t st, unsigned nblocks, const MfArgs &A) {
     if (CH == 4) return full ? mf_go<GLU, 4, 1, PT>(st, nblocks, A) : mf_go<GLU, 4, 0, PT>(st, nblocks, A);
     return -1;
 }
+// row blocks per block: the down's 8-chunk row blocks four at a time (as nrb allows;
+// C4 down 1064 -> 968 us); the gate_up's 32-chunk ones one at a time (two measured
+// 1897 -> 1954 us: half the blocks balance worse over the CUs, and a start costs little
+// against 32 chunks)
+#ifndef MF_RBPER_ROWS
+#define MF_RBPER_ROWS 4
+#endif
+static int mf_rbper(int nrb, int glu) {
+    if (glu) return 1;
+    for (int r = MF_RBPER_ROWS; r > 1; r >>= 1)
+        if (nrb % r == 0) return r;
+    return 1;
+}
 // shapes: K a multiple of 128 (whole chunks of 4 input groups), tiles listed (items, P),
 // the digits addressed by 32-bit offsets
 static int mf_check(const SwQ4 &W, const SwGroups &g, int &gsh, int dg_rows) {
@@ -479,16 +528,18 @@ int sw_launch_mf_glu(hipStream_t st, SwQ4 W, const uint32_t *dg, const float *xs
     int gsh;
     if (mf_check(W, g, gsh, dg_rows) || I % 64 || W.O != 2 * I) return -1;
     const int nrb = I / 64;
-    const MfArgs A = {W, gsh, dg, xs, dg_rows, g, I, nrb, hdg, hxs, nullptr};
-    return mf_dispatch<1>(st, (unsigned)(g.ngroups_max * nrb), A);
+    const int rp = mf_rbper(nrb, 1);
+    const MfArgs A = {W, gsh, dg, xs, dg_rows, g, I, nrb, rp, hdg, hxs, nullptr};
+    return mf_dispatch<1>(st, (unsigned)(g.ngroups_max * (nrb / rp)), A);
 }
 
 int sw_launch_mf_rows(hipStream_t st, SwQ4 W, const uint32_t *dg, const float *xs, int dg_rows, SwGroups g, float *Y) {
     int gsh;
     if (mf_check(W, g, gsh, dg_rows) || W.O % 4) return -1;
     const int nrb = (W.O + MF_ROWS - 1) / MF_ROWS;
-    const MfArgs A = {W, gsh, dg, xs, dg_rows, g, 0, nrb, nullptr, nullptr, Y};
-    return mf_dispatch<0>(st, (unsigned)(g.ngroups_max * nrb), A);
+    const int rp = mf_rbper(nrb, 0);
+    const MfArgs A = {W, gsh, dg, xs, dg_rows, g, 0, nrb, rp, nullptr, nullptr, Y};
+    return mf_dispatch<0>(st, (unsigned)(g.ngroups_max * (nrb / rp)), A);
 }
 
 // the same two GEMMs over per-group tensors: group c's gate/up/down are tab[gexp[c]]
@@ -499,8 +550,9 @@ int sw_launch_mf_glu_tab(hipStream_t st, SwQ4 W, const SwTab *tab, const uint32_
     W.E = 1;
     if (!tab || !hdg || !hxs || mf_check(W, g, gsh, dg_rows) || I % 64 || W.O != 2 * I) return -1;
     const int nrb = I / 64;
-    const MfArgs A = {W, gsh, dg, xs, dg_rows, g, I, nrb, hdg, hxs, nullptr, tab};
-    return mf_dispatch<1, 1>(st, (unsigned)(g.ngroups_max * nrb), A);
+    const int rp = mf_rbper(nrb, 1);
+    const MfArgs A = {W, gsh, dg, xs, dg_rows, g, I, nrb, rp, hdg, hxs, nullptr, tab};
+    return mf_dispatch<1, 1>(st, (unsigned)(g.ngroups_max * (nrb / rp)), A);
 }
 int sw_launch_mf_rows_tab(hipStream_t st, SwQ4 W, const SwTab *tab, const uint32_t *dg, const float *xs, int dg_rows,
                           SwGroups g, float *Y) {
@@ -508,6 +560,7 @@ int sw_launch_mf_rows_tab(hipStream_t st, SwQ4 W, const SwTab *tab, const uint32
     W.E = 1;
     if (!tab || !Y || mf_check(W, g, gsh, dg_rows) || W.O % 4) return -1;
     const int nrb = (W.O + MF_ROWS - 1) / MF_ROWS;
-    const MfArgs A = {W, gsh, dg, xs, dg_rows, g, 0, nrb, nullptr, nullptr, Y, tab};
-    return mf_dispatch<0, 1>(st, (unsigned)(g.ngroups_max * nrb), A);
+    const int rp = mf_rbper(nrb, 0);
+    const MfArgs A = {W, gsh, dg, xs, dg_rows, g, 0, nrb, rp, nullptr, nullptr, Y, tab};
+    return mf_dispatch<0, 1>(st, (unsigned)(g.ngroups_max * (nrb / rp)), A);
 }
