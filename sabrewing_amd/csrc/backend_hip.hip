@@ -290,7 +290,7 @@ static int grouped_host(float *outh, const float *x, int S, const void *gu_q, co
     if (mf) {
         int *it = hi + 3 * G + 3 * T, n = 0;
         for (int i = 0; i < G; i++)
-            for (int t0 = 0; t0 < gcnt[i]; t0 += SW_MF_TT) it[n++] = (t0 << 10) | i;
+            for (int t0 = 0; t0 < gcnt[i]; t0 += sw_mf_tile(gcnt[i])) it[n++] = (t0 << 10) | i;
         it[n] = n;
     }
     CK(hipMemcpyAsync(A + o_x, H, xn, hipMemcpyHostToDevice, g_st), "x upload");

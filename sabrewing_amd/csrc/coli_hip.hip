@@ -236,7 +236,7 @@ int group_sync(const Groups &G, float *y, const float *x) {
     std::vector<int> items;
     if (mf) {
         for (int g = 0; g < G.count; g++)
-            for (int t0 = 0; t0 < G.cnt[g]; t0 += SW_MF_TT) items.push_back((t0 << 10) | g);
+            for (int t0 = 0; t0 < G.cnt[g]; t0 += sw_mf_tile(G.cnt[g])) items.push_back((t0 << 10) | g);
         items.push_back((int)items.size());
     }
     const int ni = (int)items.size();

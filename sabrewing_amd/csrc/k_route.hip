@@ -204,8 +204,8 @@ __device__ __forceinline__ void bucket_block(const int *__restrict__ sel, int T,
         if (c > 0) { gexp[gi] = tid; gbeg[gi] = offx; gcnt[gi] = c; }
         if (tid == E - 1) *Gout = sb[tid];
         if (items) {
-            const int np = (c + tt - 1) / tt, p0 = sp[tid] - np;
-            for (int k = 0; k < np; k++) items[p0 + k] = ((k * tt) << 10) | gi;
+            const int np = (c + tt - 1) / tt, p0 = sp[tid] - np, ts = sw_item_step(c, tt);
+            for (int k = 0; k < np; k++) items[p0 + k] = ((k * ts) << 10) | gi;
             if (tid == E - 1) *Pout = sp[tid];
         }
     }

@@ -163,6 +163,17 @@ __host__ __device__ inline bool sw_act_scores(int act) { return act == 0 || act 
 struct SwGateOpt { int ld, ns; float rs; int wld; float *wsh; int wshld; };
 // the upper bound of the passes of T packed rows in at most min(T, E) groups, tt tokens each
 __host__ __device__ inline int sw_npass_max(int T, int E, int tt) { return (T + (T < E ? T : E) * (tt - 1)) / tt; }
+#define SW_MF_TT 64               // the prefill MFMA kernels' largest token tile
+// the MFMA tiles of a group of n tokens: ceil(n / 64) of them (as 64-token tiles), each
+// of the same whole number of 16-token columns (80 tokens: 48 + 32, not 64 + 16 -- a
+// tail column costs most of what a full tile's staging does)
+__host__ __device__ inline int sw_mf_tile(int n) {
+    const int nt = (n + SW_MF_TT - 1) / SW_MF_TT, ts = ((n + nt - 1) / nt + 15) / 16 * 16;
+    return ts < SW_MF_TT ? ts : SW_MF_TT;
+}
+// the token step between the passes (items) of a group of n tokens listed with tt
+// tokens each: tt, or the balanced MFMA tile for tt = SW_MF_TT (the same count of passes)
+__host__ __device__ inline int sw_item_step(int n, int tt) { return tt == SW_MF_TT ? sw_mf_tile(n) : tt; }
 // XCD-aware block order: launches deal consecutive block ids to the 8 XCDs in
 // turn; work index w gives XCD k the contiguous range [k n/8, (k+1) n/8) of
 // the first n = 8 floor(nb/8) blocks, so neighbouring work (the passes of one
@@ -187,7 +198,7 @@ __device__ __forceinline__ bool grp_work(const SwGroups &grp, int bx, int TT, in
         e = u(grp.gexp[gi]);
         beg = u(grp.gbeg[gi]);
         const int n = u(grp.gcnt[gi]);
-        tend = min(t0 + TT, n);
+        tend = min(t0 + sw_item_step(n, TT), n);
         if (cnt) *cnt = n;
         return true;
     }
@@ -339,11 +350,10 @@ int sw_launch_stage_experts(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, const fl
 // the shared expert on the VALU (sw_shared.h): h[S, Is] = silu(Wg x) * (Wu x)
 // and out[S, D] = Wd h, bf16 weights, f32 activations
 // stack glue (k_glue.hip): RMSNorm rows, greedy argmax rows
-// prefill expert GEMMs on the int8 MFMA (k_mfma.hip), bit-identical to the
+// prefill expert GEMMs on the f16 MFMA (k_mfma.hip), bit-identical to the
 // dot8 ones: activations as MFMA digits dg[rows][K/32][32 dwords] + factors
 // xs[rows][K/32] (the limbs' exponent and integer, recut); tiles of up to 64
-// tokens of a group listed in g.items / g.P (sw_launch_bucket with tt = 64)
-#define SW_MF_TT 64
+// tokens of a group listed in g.items / g.P (sw_launch_bucket with tt = SW_MF_TT)
 #define SW_MF_DIGIT_BYTES 128     // MFMA digits of one (row, input group): 32 dwords
 int sw_launch_digits(hipStream_t st, const float *x, int rows, int K, uint32_t *dg, float *xs);
 // (dg_rows: the rows of dg and xs; dg_rows * K * 4 must stay below 2^32)
