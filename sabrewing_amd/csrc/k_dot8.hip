@@ -378,8 +378,8 @@ int sw_launch_q4_dot8_glu_picks(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, cons
 // projection of the grouped path): block = RB (128, or 64 when O is not a
 // multiple of 128) consecutive output rows of one group, a tile of up to
 // DG_TT tokens per weight pass; thread (row slot ro, input group g) takes
-// NS = RB/RPS consecutive rows, one per step; same fixed-order row sums, f32
-// rows out.
+// NS = RB/RPS rows, one per step (the RPS slots a step's RPS consecutive rows);
+// same fixed-order row sums, f32 rows out.  O a multiple of 64.
 struct Dot8RowsArgs {
     SwQ4 W;
     int gsh;
@@ -421,11 +421,15 @@ __device__ __forceinline__ void dot8_rows_block(const Dot8RowsArgs &A, int bx, i
         rq = sw_q4_rq(W);
         rs = sw_q4_rs(W);
     }
-    // rows past O read the next expert's rows (or zeros past the tensor) and are not stored
-    const uint32_t voq = (uint32_t)(roc * NS) * rb + (uint32_t)g * 16;
-    const uint32_t vos = (uint32_t)(roc * NS) * sb + (uint32_t)sg * 4;
+    // step s of row slot roc takes row s RPS + roc: the block's slots read RPS consecutive
+    // rows a step, one contiguous stretch of the tensor (B=32's down 89.8 -> 85.7 us, C5's
+    // 41.8 -> 40.0 us against NS consecutive rows per slot), the row slot's part in the vector
+    // offset and the step's in the scalar one.  RB divides O (the launches check), so every
+    // row a block reads is one of its group's: the range check leaves the scalar offset out
     const uint32_t erow = (PT ? 0u : (uint32_t)e * (uint32_t)O) + (uint32_t)r0;
-    float *myruns = runs + (roc * NS) * NC + c;
+    const uint32_t voq = ((uint32_t)roc) * rb + (uint32_t)g * 16;
+    const uint32_t vos = ((uint32_t)roc) * sb + (uint32_t)sg * 4;
+    float *myruns = runs + roc * NC + c;
     // weight loads non-temporal (the nt policy) when this pass is the only one over the
     // block's weights; cached when other passes re-read them
     auto passes = [&](auto PC) {
@@ -444,24 +448,27 @@ __device__ __forceinline__ void dot8_rows_block(const Dot8RowsArgs &A, int bx, i
             }
             sw_u32x4 ra[PF];
             float sa[PF];
+            // the next step's offsets, moved on by RPS rows a step
+            uint32_t vqn = voq, vsn = vos;
+            const uint32_t dq = (uint32_t)RPS * rb, ds = (uint32_t)RPS * sb;
     #pragma unroll
             for (int u = 0; u < PF; u++) {
-                ra[u] = sw_ld16<POL>(rq, voq, (erow + u) * rb);
-                sa[u] = sw_ld4f<POL>(rs, vos, (erow + u) * sb);
+                ra[u] = sw_ld16<POL>(rq, voq, (erow + u * RPS) * rb);
+                sa[u] = sw_ld4f<POL>(rs, vos, (erow + u * RPS) * sb);
             }
             auto step = [&](int s, int u, bool refill) {
                 const sw_u32x4 w = ra[u] ^ 0x88888888u;
                 const float sc = W.gs > 0 ? sa[u] : 1.0f;
                 if (refill) {
-                    ra[u] = sw_ld16<POL>(rq, voq, (erow + s + PF) * rb);
-                    sa[u] = sw_ld4f<POL>(rs, vos, (erow + s + PF) * sb);
+                    ra[u] = sw_ld16<POL>(rq, voq, (erow + (s + PF) * RPS) * rb);
+                    sa[u] = sw_ld4f<POL>(rs, vos, (erow + (s + PF) * RPS) * sb);
                     __builtin_amdgcn_sched_barrier(0);
                 }
     #pragma unroll
                 for (int t = 0; t < TT; t++) {
                     if (t < nt) {                          // uniform over the block
                         const float p = row_term<C16>((float)dot8_group(w, X[t]) * (sc * xf[t]), gv, CH);
-                        if (lead) myruns[(t * RB + s) * NC] = p;
+                        if (lead) myruns[(t * RB + s * RPS) * NC] = p;
                     }
                 }
             };
@@ -519,6 +526,7 @@ int sw_launch_q4_dot8_rows(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, const flo
     // 128 rows per block when O allows (half the blocks: half the per-block start and
     // epilogue per weight byte), else 64
     const int RB = W.O % 128 == 0 ? 128 : 64;          // (256 rows measured no faster at B=32)
+    if (W.O % RB) return -1;                           // (no block reads past its group's rows)
     const dim3 grid((unsigned)g.ngroups_max, (unsigned)((W.O + RB - 1) / RB));
     const Dot8RowsArgs A = {W, gsh, xl, xs, g, Y};
     // a ring of at most RW_PF steps: within 128 VGPRs, four blocks per CU
@@ -600,6 +608,7 @@ int sw_launch_q4_dot8_rows_tab(hipStream_t st, SwQ4 W, const SwTab *tab, const s
         sw_q4_gsh(W, gsh))
         return -1;
     const int RB = W.O % 128 == 0 && g.ngroups_max * (W.O / 128) >= 512 ? 128 : 64;
+    if (W.O % RB) return -1;                           // (no block reads past its group's rows)
     const dim3 grid((unsigned)g.ngroups_max, (unsigned)((W.O + RB - 1) / RB));
     const Dot8RowsArgs A = {W, gsh, xl, xs, g, Y, tab};
     const int pf = dg_pf_rows(W.K) < RW_PF ? dg_pf_rows(W.K) : RW_PF;

@@ -302,7 +302,8 @@ int sw_launch_q4_dot8_glu(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, const floa
 // the same for one token's K picks sel (block row a: expert sel[a], packed row a)
 int sw_launch_q4_dot8_glu_picks(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, const float *xs, int I, sw_u32x4 *hl, float *hs,
                                 const int *sel, int K);
-// Y[packed row, O] f32 for every group, input as limbs (the grouped down projection)
+// Y[packed row, O] f32 for every group, input as limbs (the grouped down projection);
+// O a multiple of 64
 int sw_launch_q4_dot8_rows(hipStream_t st, SwQ4 W, const sw_u32x4 *xl, const float *xs, SwGroups g, float *Y);
 // the same two grouped kernels over per-group tensors: W gives O, K and gs (its q, s
 // and E are unused); group c's tensors are tab[gexp[c]]
