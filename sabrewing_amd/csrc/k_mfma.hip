@@ -209,10 +209,10 @@ __global__ __launch_bounds__(MF_NT, 1) void k_mf(MfArgs A) {
     const int sw_ = __builtin_amdgcn_readfirstlane(st >> 6);   // the staging role's wave index
     sw_rsrc rq, rs;
     if constexpr (PT) {
-        // a staging thread's row ra = st & 127 is an up row iff (st >> 6) & 1: uniform per wave
+        // a staging thread's row ra (below) is an up row iff (st >> 8) & 1: uniform per wave
         const SwTab tb_ = A.tab[e];
         if (GLU) {
-            const bool up = sw_ & 1;
+            const bool up = (sw_ >> 2) & 1;
             rq = sw_make_rsrc(up ? tb_.u : tb_.g, (uint32_t)A.I * rbytes);
             rs = sw_make_rsrc(up ? tb_.us : tb_.gs, (uint32_t)A.I * (uint32_t)ng * 4);
         } else {
@@ -225,20 +225,23 @@ __global__ __launch_bounds__(MF_NT, 1) void k_mf(MfArgs A) {
     }
 
     // ---- staging: the units of a chunk of staging slot st
-    //  weights (slots < 512): row ra = st & 127 of group st >> 7 (16 B packed, expanded on
-    //           the store) + its scale
+    //  weights (slots < 512): row ra of group ga (below; 16 B packed, expanded on the store)
+    //           and its scale
     //  digits:  16 B (op, quarter) of token tb of groups st >> 9 and (st >> 9) + 2: unit u of a
     //           group is token tile u >> 7, op (u >> 6) & 1, quarter (u >> 4) & 3, token u & 15;
     //           staged only for the token tiles that compute (dact)
-    //  factors (slots < 256): token tx of group st >> 6
+    //  factors (slots < 256): token tx of group gx (as ra, ga)
     // Every load is a buffer load: the slot's part of its offset in a register set once,
     // the chunk's in a scalar offset.
     constexpr int DG_PER = MF_CG * MF_TT * 8 / MF_NT;      // digit units per slot (2)
     const bool wst = sw_ < 8;                              // uniform per wave
-    const int ra = st & 127, ga = (st >> 7) & 3;
+    // (a wave's 64 slots: 16 rows, each with the chunk's 4 groups, side by side in memory --
+    // a wave load touches 16 lines, not 64 -- the rows fastest within each 16-slot quarter, so
+    // that the LDS stores stay conflict-free)
+    const int ra = ((st >> 6) << 4) | (st & 15), ga = (st >> 4) & 3;
     const uint32_t rowa = srow(ra);
     const int tb = ((st >> 7) & 3) * 16 + (st & 15), opb = (st >> 6) & 1, kqb = (st >> 4) & 3, gb = st >> 9;
-    const int tx = st & 63, gx = (st >> 6) & 3;
+    const int tx = ((st >> 6) << 4) | (st & 15), gx = (st >> 4) & 3;   // (as ra, ga)
     const bool dact = ((sw_ >> 1) & 3) < nact;            // uniform per wave
     const bool xst = sw_ < 4;
     const sw_rsrc rd = sw_make_rsrc(A.dg, (uint32_t)A.dg_rows * (uint32_t)G * MF_DW * 4);
