@@ -26,8 +26,9 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
-# MI355X dense bf16 MFMA (the peak BASELINE prices the prefill at; the kernels issue int8
-# MFMAs, 4 per int4 multiply-add of the layer, against a 5.0 P op/s int8 peak)
+# MI355X dense bf16 MFMA (the peak BASELINE prices the prefill at; the kernels issue f16
+# MFMAs, 2 per int4 multiply-add of the layer (one per 12-bit digit), against the same
+# 2.5 P flop/s dense f16 peak)
 MFMA_PEAK_TFS = 2500.0
 # what the kernels compute in: int4 weights and their f32 group scales against the
 # activations written per 32 inputs as integers of 7 signed base-8 digits (held as 6
@@ -72,7 +73,7 @@ def kernel_bytes(cfg, S, G):
              "q4_down": dn_w + T * limb(I) + T * D * 4,
              "combine": T * D * 4 + 2 * S * D * 4 + (S * D * 4 if cfg.shared_mode else 0) + T * 8}
         b["gate_bucket"] = b["gate_topk"] + b["bucket"]      # (one launch up to 8 tokens)
-        # prefill-sized batches: the grouped GEMMs on the int8 MFMA over MFMA digits (128
+        # prefill-sized batches: the grouped GEMMs on the f16 MFMA over MFMA digits (128
         # bytes + one f32 factor per 32 inputs)
         dig = lambda n: n // 32 * (128 + 4)
         b["digits"] = S * D * 4 + S * dig(D)
@@ -350,7 +351,7 @@ def run_coli(args):
                      "weight_GBs_device": round(wbytes / (kern_us * 1e-6) / 1e9, 1),
                      "expert_rows_per_s_host": round(NE * rows / dt, 1),
                      "tera_ops_device": round(2 * 3 * I * D * NE * rows / (kern_us * 1e-6) / 1e12, 2),
-                     "kernel": "int8 MFMA" if rows >= 8 else "dot8 grouped"}
+                     "kernel": "f16 MFMA" if rows >= 8 else "dot8 grouped"}
         log(f"GLM-coli {name}: {dt * 1e6:.1f} us/call host, {kern_us:.1f} us device "
             f"({wbytes / (kern_us * 1e-6) / 1e9:.0f} GB/s of expert weights)")
     print(json.dumps({"metric": "coli_cuda_expert_group (GLM-4.5-shaped experts) side figure", "unit": "us/call",
@@ -687,7 +688,7 @@ def main():
     ap.add_argument("--layers", type=int, default=12)
     ap.add_argument("--seed", type=int, default=20261201)
     ap.add_argument("--grouped", choices=["auto", "dot8", "mfma"], default="auto",
-                    help="grouped expert GEMMs of batches: auto (int8 MFMA at >= 8 tokens per group), dot8, mfma")
+                    help="grouped expert GEMMs of batches: auto (f16 MFMA at >= 8 tokens per group), dot8, mfma")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--calib-copy-mb", type=int, default=0,

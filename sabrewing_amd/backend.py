@@ -344,7 +344,7 @@ class Backend:
     GROUPED_AUTO, GROUPED_DOT8, GROUPED_MFMA = 0, 1, 2
 
     def set_grouped_kernel(self, mode):
-        """the grouped expert GEMMs of batches: 0 auto, 1 dot8, 2 int8 MFMA
+        """the grouped expert GEMMs of batches: 0 auto, 1 dot8, 2 f16 MFMA
         (bit-identical); returns the previous mode"""
         prev = self.lib.lag_hip_set_grouped_kernel(int(mode))
         if prev < 0:

@@ -209,7 +209,7 @@ extern "C" int lag_hip_sync(void) {
     return 0;
 }
 
-// The grouped expert GEMMs of a batch: dot8 (k_dot8.hip) or the int8 MFMA
+// The grouped expert GEMMs of a batch: dot8 (k_dot8.hip) or the f16 MFMA
 // (k_mfma.hip), bit-identical; auto takes the MFMA when the groups average at
 // least SW_MF_MIN_AVG tokens (its 16-token tiles are then mostly full)
 static int g_grouped_kernel = 0;        // 0 auto, 1 dot8, 2 MFMA
@@ -707,7 +707,7 @@ static int forward_idot(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const
 // S > 1: routing stage, gate + top-k, shared gate_up over token tiles, the
 // counting sort, grouped gate_up, shared down, grouped down into slots, combine;
 // the grouped GEMMs on dot8 (passes of 2 tokens) or, for prefill-sized batches,
-// on the int8 MFMA (tiles of 64 tokens, the inputs as MFMA digits).
+// on the f16 MFMA (tiles of up to 64 tokens, the inputs as MFMA digits).
 // nw: x holds raw rows, normalised by the routing launch's router blocks (RMSNorm with
 // weights nw, eps) into xn, which every later launch reads in x's place
 static int forward(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const float *x, float *out, int S,
@@ -779,7 +779,7 @@ static int forward(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const floa
                                              wsh, nsg))
               return fail_msg("down/combine launch"); }
         g_last_G_dev = 0; g_last_ng = K;
-    } else if (mf) {                     // prefill: tiles of up to 64 tokens of a group on the int8 MFMA
+    } else if (mf) {                     // prefill: tiles of up to 64 tokens of a group on the f16 MFMA
         { PROF("bucket");
           if (sw_launch_bucket(g_st, f.sel, S, K, E, f.gexp, f.gbeg, f.gcnt, f.G, f.grow, f.rowof, SW_MF_TT, f.items, f.P))
               return fail_msg("bucket launch"); }

@@ -170,7 +170,7 @@ GLay glay(const Groups &G, int T, int xrows, int nextra = 0, bool mf = false) {
     L.end = cv.off;
     return L;
 }
-// the int8 MFMA GEMMs for prefill-sized groups (16-token tiles mostly full), as
+// the f16 MFMA GEMMs for prefill-sized groups (16-token tiles mostly full), as
 // the lag family's automatic choice: whole chunks of 4 input groups, >= 8 rows per group
 bool use_mf(const Groups &G) { return G.D % 128 == 0 && G.I % 128 == 0 && G.total >= 8 * G.count; }
 size_t meta_bytes(const Groups &G, int T) { return (size_t)(3 * G.count + T) * 4 + (size_t)G.count * sizeof(SwTab); }

@@ -5,7 +5,7 @@
 // acc = sum_k w_k D_k (w_k = n_k - 8 in [-8, 7], D_k the 7-limb integer of
 // input k, |D_k| < 2^21.2) and the term (float)acc * (s * xf).  Here every D
 // is cut into two 12-bit digits, D = E1 2^12 + E0 with E0 the residue of D
-// mod 4096 in [-2048, 2048) and |E1| <= 577.  The weights and both digits are
+// mod 4096 in [-2048, 2048) and |E1| <= 585.  The weights and both digits are
 // integers that f16 holds exactly, and every product (|w E| <= 2^14) and
 // every partial sum of 32 of them (< 2^19) is an integer that f32 holds
 // exactly, so two v_mfma_f32_16x16x32_f16 return R0 = sum_k w_k E0_k and
@@ -18,10 +18,10 @@
 // kernel ran its group.
 //
 // Digits in memory: per (input row, group) 128 bytes, E0 of the 32 inputs as
-// f16 in input order, then E1: the B operands of the two MFMAs.  Lane l of
-// an MFMA (column l % 16, k quarter q = l / 16) reads the 16 bytes of inputs
-// 8q .. 8q+7, and its A operand holds the same inputs of a weight row as f16,
-// expanded from packed dword q of the row's group (nibble k at bits 4(k&7)).
+// f16, then E1: the B operands of the two MFMAs.  Lane l of an MFMA (column
+// l % 16, k quarter q = l / 16) reads the 16 bytes of inputs 8q .. 8q+7 (in
+// the slot order of mf_expand), and its A operand holds the same inputs of a
+// weight row as f16, expanded from packed dword q of the row's group.
 //
 // Block: 128 weight rows (8 tiles of 16) x a tile of up to 64 tokens (4
 // tiles of 16) of one group, 16 waves; wave w takes row tiles w&3 and (w&3)+4
@@ -33,11 +33,14 @@
 // scales and the token factors -- are staged in LDS in two buffers: while the
 // waves compute one chunk from LDS, the next chunk's loads are in flight in
 // registers, issued before each chunk's barrier so that the waves waiting there
-// overlap them.  A tile's token tiles with no tokens compute nothing and have
-// no digits staged; a prefill's tiles are mostly one full tile per expert plus
-// a tail of 1-2 token tiles, whose fixed staging cost (the weights of all 128
-// rows) is most of their time.  The inner loop reads LDS only, every wave read
-// a contiguous 1 KB (conflict-free).
+// overlap them.  Each staging wave load covers 16 rows (or tokens) with the
+// chunk's 4 groups side by side in memory: 16 cache lines a load, not 64 (the
+// staging loads' cache lines, more than the VALU, set the chunk's time).  A
+// tile's token tiles with no tokens compute nothing and have no digits staged;
+// a group's tokens are split into equal tiles of whole 16-token columns
+// (sw_mf_tile).  The inner loop reads LDS only, every wave read a contiguous
+// 1 KB (conflict-free).  A down block takes up to 4 row blocks of its tile with
+// one staging pipeline running across them.
 #include "sw_hip.h"
 #include "sw_gate.h"
 

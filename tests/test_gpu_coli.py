@@ -2,7 +2,7 @@
 sabrewing_amd/csrc/coli_hip.hip) against the oracle and against the lag family.
 
   * expert groups: each row equals the same expert's lag_hip_expert_q4 output bit
-    for bit (the same dot8 kernels, or for prefill-sized groups the int8 MFMA
+    for bit (the same dot8 kernels, or for prefill-sized groups the f16 MFMA
     GEMMs, reading the group's three tensors through a per-group table) and the
     oracle's int4 expert (c/moe_quant.h / c/quant.h numerics) within the lag
     family's bounds;
@@ -137,7 +137,7 @@ def test_expert_group_one_row_each(coli, be, orc, gs):
 
 @pytest.mark.parametrize("gs", [0, 32])
 def test_prefill_group_on_the_mfma(coli, be, orc, gs):
-    """groups averaging >= 8 rows take the int8 MFMA GEMMs (64-token tiles, partial tiles,
+    """groups averaging >= 8 rows take the f16 MFMA GEMMs (64-token tiles, partial tiles,
     one group over two tiles): still each row's lag expert output bit for bit"""
     L = layer(orc, gs, seed=21)
     ex = Experts(coli, L, gs)

@@ -4,7 +4,7 @@ device-generated layers:
   * C3: the C2 layer at batch 4, 8, 32 and 64 -- routing identical to the oracle's,
     the layer within the tolerance, and every stream of the batch bit-identical
     to its own single-stream call;
-  * C4: 2048-token prefill (the grouped GEMMs on the int8 MFMA), with the softplus
+  * C4: 2048-token prefill (the grouped GEMMs on the f16 MFMA), with the softplus
     gate and with the Zipf(1.1)-skewed router -- all 2048 rows' routing identical,
     all rows within the tolerance, and sampled streams (the hottest expert's
     included) bit-identical to their single-stream calls;

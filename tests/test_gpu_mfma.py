@@ -1,4 +1,4 @@
-"""The int8 MFMA grouped GEMMs of prefill (k_mfma.hip) against the dot8 ones
+"""The f16 MFMA grouped GEMMs of prefill (k_mfma.hip) against the dot8 ones
 (k_dot8.hip): the same bits for every token, through the device-resident
 block (lag_hip_moe_forward) and through the host-grouped entry
 (lag_hip_moe_group), plus the oracle's bar (routing identical, normwise
