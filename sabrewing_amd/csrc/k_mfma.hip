@@ -212,10 +212,10 @@ __global__ __launch_bounds__(MF_NT, 1) void k_mf(MfArgs A) {
     const int sw_ = __builtin_amdgcn_readfirstlane(st >> 6);   // the staging role's wave index
     sw_rsrc rq, rs;
     if constexpr (PT) {
-        // a staging thread's row ra (below) is an up row iff (st >> 8) & 1: uniform per wave
+        // a staging thread's row ra (below) is an up row iff (st >> 9) & 1: uniform per wave
         const SwTab tb_ = A.tab[e];
         if (GLU) {
-            const bool up = (sw_ >> 2) & 1;
+            const bool up = (sw_ >> 3) & 1;
             rq = sw_make_rsrc(up ? tb_.u : tb_.g, (uint32_t)A.I * rbytes);
             rs = sw_make_rsrc(up ? tb_.us : tb_.gs, (uint32_t)A.I * (uint32_t)ng * 4);
         } else {
@@ -228,44 +228,46 @@ __global__ __launch_bounds__(MF_NT, 1) void k_mf(MfArgs A) {
     }
 
     // ---- staging: the units of a chunk of staging slot st
-    //  weights (slots < 512): row ra of group ga (below; 16 B packed, expanded on the store)
-    //           and its scale
+    //  weights (every slot): half hq of row ra's 16 B packed of group ga (below; expanded on
+    //           the store); slots of half 0 also the row's scale of the group
     //  digits:  16 B (op, quarter) of token tb of groups st >> 9 and (st >> 9) + 2: unit u of a
     //           group is token tile u >> 7, op (u >> 6) & 1, quarter (u >> 4) & 3, token u & 15;
     //           staged only for the token tiles that compute (dact)
-    //  factors (slots < 256): token tx of group gx (as ra, ga)
+    //  factors (the 4 waves with sw_ % 4 == 1): token tx of group gx (as ra, ga)
+    // (the staging work spread evenly over the 16 waves: the chunk's barrier waits for the
+    // slowest)
     // Every load is a buffer load: the slot's part of its offset in a register set once,
     // the chunk's in a scalar offset.
     constexpr int DG_PER = MF_CG * MF_TT * 8 / MF_NT;      // digit units per slot (2)
-    const bool wst = sw_ < 8;                              // uniform per wave
-    // (a wave's 64 slots: 16 rows, each with the chunk's 4 groups, side by side in memory --
-    // a wave load touches 16 lines, not 64 -- the rows fastest within each 16-slot quarter, so
-    // that the LDS stores stay conflict-free)
-    const int ra = ((st >> 6) << 4) | (st & 15), ga = (st >> 4) & 3;
+    // (a wave's 64 slots: one half of 16 rows, each with the chunk's 4 groups, side by side in
+    // memory -- a wave load touches 16 lines, not 64 -- the rows fastest within each 16-slot
+    // quarter, so that the LDS stores stay conflict-free)
+    const int ra = ((st >> 7) << 4) | (st & 15), ga = (st >> 4) & 3, hq = (st >> 6) & 1;
+    const bool sst = hq == 0;                              // uniform per wave
     const uint32_t rowa = srow(ra);
     const int tb = ((st >> 7) & 3) * 16 + (st & 15), opb = (st >> 6) & 1, kqb = (st >> 4) & 3, gb = st >> 9;
-    const int tx = ((st >> 6) << 4) | (st & 15), gx = (st >> 4) & 3;   // (as ra, ga)
+    const int xi = ((sw_ >> 2) << 6) | (st & 63);         // (factor slot)
+    const int tx = ((xi >> 6) << 4) | (xi & 15), gx = (xi >> 4) & 3;   // (as ra, ga)
     const bool dact = ((sw_ >> 1) & 3) < nact;            // uniform per wave
-    const bool xst = sw_ < 4;
+    const bool xst = (sw_ & 3) == 1;
     const sw_rsrc rd = sw_make_rsrc(A.dg, (uint32_t)A.dg_rows * (uint32_t)G * MF_DW * 4);
     const sw_rsrc rx = sw_make_rsrc(A.xs, (uint32_t)A.dg_rows * (uint32_t)G * 4);
-    const uint32_t vq = rowa * rbytes + (uint32_t)ga * 16;
+    const uint32_t vq = rowa * rbytes + (uint32_t)ga * 16 + (uint32_t)hq * 8;
     const uint32_t vs = (rowa * (uint32_t)ng + (uint32_t)((ga * SW_RG) >> A.gsh)) * 4;
     const uint32_t vd = ((uint32_t)token(tb) * (uint32_t)G + (uint32_t)gb) * MF_DW * 4 + (uint32_t)(opb * 16 + kqb * 4) * 4;
     const uint32_t vx = ((uint32_t)token(tx) * (uint32_t)G + (uint32_t)gx) * 4;
-    sw_u32x4 pka, pkb[DG_PER];
+    uint2 pka;
+    sw_u32x4 pkb[DG_PER];
     float psa = 1.0f, pxf = 0.f;
     // chunk q of the block: chunk q % NCV of its row block q / NCV (the row block's rows in
     // the vector offset, which the range check covers)
     auto stage_load = [&](int q) {
         const int rbi = GLU ? 0 : q / NCV, c = q - rbi * NCV;
         const uint32_t g0 = (uint32_t)__builtin_amdgcn_readfirstlane(c * MF_CG);
-        if (wst) {
-            const uint32_t dr = (uint32_t)(rbi * RPB);
-            pka = sw_ld16(rq, vq + dr * rbytes, g0 * 16);
-            // ((g0 + ga) * 32) >> gsh splits: g0 * 32 is a multiple of 128, ga * 32 < 128
-            if (W.gs > 0) psa = sw_ld4f(rs, vs + dr * (uint32_t)ng * 4, ((g0 * SW_RG) >> A.gsh) * 4);
-        }
+        const uint32_t dr = (uint32_t)(rbi * RPB);
+        pka = sw_ld8(rq, vq + dr * rbytes, g0 * 16);
+        // ((g0 + ga) * 32) >> gsh splits: g0 * 32 is a multiple of 128, ga * 32 < 128
+        if (sst && W.gs > 0) psa = sw_ld4f(rs, vs + dr * (uint32_t)ng * 4, ((g0 * SW_RG) >> A.gsh) * 4);
         if (dact)
 #pragma unroll
             for (int v = 0; v < DG_PER; v++) pkb[v] = sw_ld16(rd, vd + (uint32_t)v * 2 * MF_DW * 4, g0 * MF_DW * 4);
@@ -274,11 +276,11 @@ __global__ __launch_bounds__(MF_NT, 1) void k_mf(MfArgs A) {
     auto stage_store = [&](int buf) {
         sw_i32x4 *Al = (sw_i32x4 *)(mf_lds + MF_A_OFF + buf * MF_A_SZ);
         sw_u32x4 *Bl = (sw_u32x4 *)(mf_lds + MF_B_OFF + buf * MF_B_SZ);
-        if (wst) {
+        {
             const int m = ra >> 4, i = ra & 15;
-#pragma unroll
-            for (int q = 0; q < 4; q++) Al[((ga * 8 + m) * 4 + q) * 16 + i] = mf_expand(pka[q]);
-            ((float *)(mf_lds + MF_S_OFF + buf * MF_S_SZ))[ga * MF_ROWS + ra] = psa;
+            Al[((ga * 8 + m) * 4 + 2 * hq) * 16 + i] = mf_expand(pka.x);
+            Al[((ga * 8 + m) * 4 + 2 * hq + 1) * 16 + i] = mf_expand(pka.y);
+            if (sst) ((float *)(mf_lds + MF_S_OFF + buf * MF_S_SZ))[ga * MF_ROWS + ra] = psa;
         }
         if (dact)
 #pragma unroll

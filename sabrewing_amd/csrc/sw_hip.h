@@ -63,6 +63,11 @@ __device__ __forceinline__ sw_u32x4 sw_ld16(sw_rsrc r, uint32_t voff, uint32_t s
     return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, POL);
 }
 template <int POL = 0>
+__device__ __forceinline__ uint2 sw_ld8(sw_rsrc r, uint32_t voff, uint32_t soff) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, POL);
+    return make_uint2(v[0], v[1]);
+}
+template <int POL = 0>
 __device__ __forceinline__ float sw_ld4f(sw_rsrc r, uint32_t voff, uint32_t soff) {
     return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, POL));
 }
