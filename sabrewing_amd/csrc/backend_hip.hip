@@ -781,7 +781,9 @@ static int forward(const LagHipMoeDesc *d, const LagHipMoeWeights *w, const floa
         g_last_G_dev = 0; g_last_ng = K;
     } else if (mf) {                     // prefill: tiles of up to 64 tokens of a group on the f16 MFMA
         { PROF("bucket");
-          if (sw_launch_bucket(g_st, f.sel, S, K, E, f.gexp, f.gbeg, f.gcnt, f.G, f.grow, f.rowof, SW_MF_TT, f.items, f.P))
+          // (the split sort's counts in the slots, which the down launch writes later)
+          if (sw_launch_bucket(g_st, f.sel, S, K, E, f.gexp, f.gbeg, f.gcnt, f.G, f.grow, f.rowof, SW_MF_TT, f.items, f.P,
+                               (int *)f.slots))
               return fail_msg("bucket launch"); }
         SwGroups g = {f.gexp, f.gbeg, f.gcnt, f.grow, f.G, sw_npass_max(T, E, SW_MF_TT), 0, f.items, f.P};
         { PROF("mf_glu");

@@ -156,36 +156,31 @@ struct BucketArgs {
     int tt;
     int *items, *Pout;
 };
-// by a block of BK_THREADS threads
-__device__ __forceinline__ void bucket_block(const int *__restrict__ sel, int T, int K, int E, const BucketArgs &B) {
-    int *__restrict__ gexp = B.gexp, *__restrict__ gbeg = B.gbeg, *__restrict__ gcnt = B.gcnt, *__restrict__ Gout = B.Gout;
-    int *__restrict__ grow = B.grow, *__restrict__ rowof = B.rowof, *__restrict__ items = B.items, *__restrict__ Pout = B.Pout;
-    const int tt = B.tt;
-    __shared__ int cnt[BK_MAXE], run[BK_MAXE], sa[BK_MAXE], sb[BK_MAXE], sp[BK_MAXE];
-    __shared__ uint8_t wcnt[2][BK_THREADS / 64][BK_MAXE];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    for (int i = tid; i < E; i += BK_THREADS) {
-        cnt[i] = 0;
-        for (int w = 0; w < BK_THREADS / 64; w++) wcnt[0][w][i] = wcnt[1][w][i] = 0;
-    }
-    __syncthreads();
-    // counts: eight picks' loads in flight per thread before their atomics (one load latency
-    // per 8 BK_THREADS picks instead of one per BK_THREADS)
-    for (int p0 = tid; p0 < T; p0 += 8 * BK_THREADS) {
+// The parts of the sort, each by a block of BK_THREADS threads.
+// (1) cnt[e] += the picks of expert e among sel[p0 .. p1)
+__device__ __forceinline__ void bucket_count(const int *__restrict__ sel, int p0, int p1, int *cnt) {
+    const int tid = threadIdx.x;
+    // eight picks' loads in flight per thread before their atomics (one load latency per 8
+    // BK_THREADS picks instead of one per BK_THREADS)
+    for (int q0 = p0 + tid; q0 < p1; q0 += 8 * BK_THREADS) {
         int v[8];
 #pragma unroll
-        for (int u = 0; u < 8; u++) v[u] = p0 + u * BK_THREADS < T ? sel[p0 + u * BK_THREADS] : 0;
+        for (int u = 0; u < 8; u++) v[u] = q0 + u * BK_THREADS < p1 ? sel[q0 + u * BK_THREADS] : 0;
 #pragma unroll
         for (int u = 0; u < 8; u++)
-            if (p0 + u * BK_THREADS < T) atomicAdd(&cnt[v[u]], 1);
+            if (q0 + u * BK_THREADS < p1) atomicAdd(&cnt[v[u]], 1);
     }
-    __syncthreads();
-    // inclusive scans of cnt (packed offsets), of cnt > 0 (group index) and of the
-    // passes ceil(cnt / tt) (pass list offsets), expert tid by thread tid: a shuffle
-    // scan within each wave, then the totals of the earlier waves (integer sums, so the
-    // order of the additions does not matter)
+}
+// (2) from the experts' counts: run[e] = the first packed row of expert e; with write, the
+// group and pass tables.  Inclusive scans of cnt (packed offsets), of cnt > 0 (group index)
+// and of the passes (pass list offsets), expert tid by thread tid: a shuffle scan within each
+// wave, then the totals of the earlier waves (integer sums, so the order of the additions
+// does not matter).
+__device__ __forceinline__ void bucket_tables(const int *cnt, int E, const BucketArgs &B, bool write, int *run) {
+    __shared__ int sa[BK_MAXE], sb[BK_MAXE], sp[BK_MAXE];
+    __shared__ int wta[BK_THREADS / 64], wtb[BK_THREADS / 64], wtp[BK_THREADS / 64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, tt = B.tt;
     {
-        __shared__ int wta[BK_THREADS / 64], wtb[BK_THREADS / 64], wtp[BK_THREADS / 64];
         const int c0 = tid < E ? cnt[tid] : 0;
         int va = c0, vb = c0 > 0, vp = (c0 + tt - 1) / tt;
         for (int o = 1; o < 64; o <<= 1) {
@@ -201,32 +196,43 @@ __device__ __forceinline__ void bucket_block(const int *__restrict__ sel, int T,
         const int c = cnt[tid];
         const int offx = sa[tid] - c, gi = sb[tid] - (c > 0);
         run[tid] = offx;
-        if (c > 0) { gexp[gi] = tid; gbeg[gi] = offx; gcnt[gi] = c; }
-        if (tid == E - 1) *Gout = sb[tid];
-        if (items) {
-            const int np = (c + tt - 1) / tt, p0 = sp[tid] - np, ts = sw_item_step(c, tt);
-            for (int k = 0; k < np; k++) items[p0 + k] = ((k * ts) << 10) | gi;
-            if (tid == E - 1) *Pout = sp[tid];
+        if (write) {
+            if (c > 0) { B.gexp[gi] = tid; B.gbeg[gi] = offx; B.gcnt[gi] = c; }
+            if (tid == E - 1) *B.Gout = sb[tid];
+            if (B.items) {
+                const int np = (c + tt - 1) / tt, p0 = sp[tid] - np, ts = sw_item_step(c, tt);
+                for (int k = 0; k < np; k++) B.items[p0 + k] = ((k * ts) << 10) | gi;
+                if (tid == E - 1) *B.Pout = sp[tid];
+            }
         }
     }
+    __syncthreads();
+}
+// (3) the picks p0 .. p1 placed from run[] (advanced past them): rounds of two halves of
+// BK_THREADS (pair base + h BK_THREADS + tid), three barriers a round: a pair's slot is its
+// expert's run, plus its expert's pairs in the round's first half (for h = 1), in the earlier
+// waves of its half, and in its wave before its lane -- the pairs' own order (stable).  (The
+// next round's picks are loaded while a round runs.)
+__device__ __forceinline__ void bucket_rounds(const int *__restrict__ sel, int p0, int p1, int K, int E,
+                                              const BucketArgs &B, int *run) {
+    __shared__ uint8_t wcnt[2][BK_THREADS / 64][BK_MAXE];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    int *__restrict__ grow = B.grow, *__restrict__ rowof = B.rowof;
+    for (int i = tid; i < E; i += BK_THREADS)
+        for (int w = 0; w < BK_THREADS / 64; w++) wcnt[0][w][i] = wcnt[1][w][i] = 0;
     __syncthreads();
     int nbits = 0;
     while ((1 << nbits) < E) nbits++;
     const unsigned long long lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-    // the picks in rounds of two halves of BK_THREADS (pair base + h BK_THREADS + tid), three
-    // barriers a round: a pair's slot is its expert's run, plus its expert's pairs in the
-    // round's first half (for h = 1), in the earlier waves of its half, and in its wave
-    // before its lane -- the pairs' own order (stable)
-    // (the next round's picks are loaded while a round runs)
-    auto pick = [&](int p) { return p < T ? sel[p] : 0; };
-    int en[2] = {pick(tid), pick(BK_THREADS + tid)};
-    for (int base = 0; base < T; base += 2 * BK_THREADS) {
-        const int nh = base + BK_THREADS < T ? 2 : 1;          // uniform over the block
+    auto pick = [&](int p) { return p < p1 ? sel[p] : 0; };
+    int en[2] = {pick(p0 + tid), pick(p0 + BK_THREADS + tid)};
+    for (int base = p0; base < p1; base += 2 * BK_THREADS) {
+        const int nh = base + BK_THREADS < p1 ? 2 : 1;         // uniform over the block
         int e[2], rank[2];
         bool act[2];
 #pragma unroll
         for (int h = 0; h < 2; h++) {
-            act[h] = h < nh && base + h * BK_THREADS + tid < T;
+            act[h] = h < nh && base + h * BK_THREADS + tid < p1;
             e[h] = act[h] ? en[h] : 0;
         }
         en[0] = pick(base + 2 * BK_THREADS + tid);
@@ -267,6 +273,16 @@ __device__ __forceinline__ void bucket_block(const int *__restrict__ sel, int T,
         }
         __syncthreads();
     }
+}
+// the whole sort by one block
+__device__ __forceinline__ void bucket_block(const int *__restrict__ sel, int T, int K, int E, const BucketArgs &B) {
+    __shared__ int cnt[BK_MAXE], run[BK_MAXE];
+    for (int i = threadIdx.x; i < E; i += BK_THREADS) cnt[i] = 0;
+    __syncthreads();
+    bucket_count(sel, 0, T, cnt);
+    __syncthreads();
+    bucket_tables(cnt, E, B, true, run);
+    bucket_rounds(sel, 0, T, K, E, B, run);
 }
 
 // The same counting sort for at most 128 picks of at most 256 experts, by one wave and no
@@ -344,12 +360,55 @@ __global__ __launch_bounds__(BK_THREADS) void k_bucket(const int *__restrict__ s
     bucket_block(sel, T, K, E, B);
 }
 
+// The same sort of many picks over blocks of BK_CHUNK picks each (one round apiece): the
+// counts of every chunk, then every chunk placed from the experts' totals (the same scans,
+// block 0 writing the tables) plus the earlier chunks' counts of each expert -- the pairs'
+// own order over the chunks (C4's 20,480 picks: 40 -> 14 us)
+#define BK_CHUNK (2 * BK_THREADS)
+__global__ __launch_bounds__(BK_THREADS) void k_bucket_count(const int *__restrict__ sel, int T, int E,
+                                                             int *__restrict__ hist) {
+    __shared__ int cnt[BK_MAXE];
+    for (int i = threadIdx.x; i < E; i += BK_THREADS) cnt[i] = 0;
+    __syncthreads();
+    const int p0 = (int)blockIdx.x * BK_CHUNK;
+    bucket_count(sel, p0, min(T, p0 + BK_CHUNK), cnt);
+    __syncthreads();
+    for (int i = threadIdx.x; i < E; i += BK_THREADS) hist[(int64_t)blockIdx.x * E + i] = cnt[i];
+}
+__global__ __launch_bounds__(BK_THREADS) void k_bucket_scatter(const int *__restrict__ sel, int T, int K, int E,
+                                                               const int *__restrict__ hist, BucketArgs B) {
+    __shared__ int cnt[BK_MAXE], run[BK_MAXE], pre[BK_MAXE];
+    const int b = (int)blockIdx.x, nb = (int)gridDim.x;
+    for (int i = threadIdx.x; i < E; i += BK_THREADS) {
+        int tot = 0, before = 0;
+        for (int c = 0; c < nb; c++) {
+            const int h = hist[(int64_t)c * E + i];
+            tot += h;
+            if (c < b) before += h;
+        }
+        cnt[i] = tot;
+        pre[i] = before;
+    }
+    __syncthreads();
+    bucket_tables(cnt, E, B, b == 0, run);
+    for (int i = threadIdx.x; i < E; i += BK_THREADS) run[i] += pre[i];
+    __syncthreads();
+    const int p0 = b * BK_CHUNK;
+    bucket_rounds(sel, p0, min(T, p0 + BK_CHUNK), K, E, B, run);
+}
+
 int sw_launch_bucket(hipStream_t st, const int *sel, int S, int K, int E, int *gexp, int *gbeg,
-                     int *gcnt, int *G, int *grow, int *rowof, int tt, int *items, int *P) {
+                     int *gcnt, int *G, int *grow, int *rowof, int tt, int *items, int *P, int *hist) {
     if (E <= 0 || E > BK_MAXE || S <= 0 || K <= 0 || tt <= 0 || (items && !P)) return -1;
     if ((int64_t)S * K >= (1 << 21)) return -1;      // pass offsets in 21 bits of an item
     const BucketArgs B = {gexp, gbeg, gcnt, G, grow, rowof, tt, items, P};
-    SW_LAUNCH(k_bucket, dim3(1), dim3(BK_THREADS), 0, st, sel, S * K, K, E, B);
+    const int T = S * K, nb = (T + BK_CHUNK - 1) / BK_CHUNK;
+    if (hist && nb > 1) {
+        SW_LAUNCH(k_bucket_count, dim3((unsigned)nb), dim3(BK_THREADS), 0, st, sel, T, E, hist);
+        SW_LAUNCH(k_bucket_scatter, dim3((unsigned)nb), dim3(BK_THREADS), 0, st, sel, T, K, E, (const int *)hist, B);
+    } else {
+        SW_LAUNCH(k_bucket, dim3(1), dim3(BK_THREADS), 0, st, sel, T, K, E, B);
+    }
     return launch_err();
 }
 

@@ -279,8 +279,10 @@ int sw_launch_gate_bucket(hipStream_t st, const float *logits, const float *scor
                           const float *corr_bias, int use_corr_bias, int norm_topk, int *sel, float *w,
                           const SwGateOpt *opt, int *gexp, int *gbeg, int *gcnt, int *G, int *grow, int *rowof, int tt,
                           int *items, int *P);
+// (hist: scratch of ceil(S K / 2048) * E ints for a sort split over blocks, or null for one
+// block)
 int sw_launch_bucket(hipStream_t st, const int *sel, int S, int K, int E, int *gexp, int *gbeg,
-                     int *gcnt, int *G, int *grow, int *rowof, int tt, int *items, int *P);
+                     int *gcnt, int *G, int *grow, int *rowof, int tt, int *items, int *P, int *hist = nullptr);
 // the reference CPU's 16-lane GEMV contracts (k_lanes.hip), bit for bit: wkind 0 bf16,
 // 1 int8 (+ row scale), 2 per-row int4 (+ row scale), 3 group-scaled int4 (+ scales
 // [O][I/gs], matmul_i4_grouped's lanes; gs a multiple of 16 dividing 256, or of 256);
