@@ -177,17 +177,20 @@ __global__ __launch_bounds__(SH_SK_NT) void k_sh_sk(ShSkArgs A) {
 // The shared expert's down fused with the rank-order combine of a decode-sized batch:
 // block (bx, by) runs the down of rows 16 bx .. +15 for the 32 tokens of column tile
 // by (sh_sk_block, written to shared [S][D]), then combines those outputs of those
-// tokens (combine4, the combine launch's arithmetic) into out.
+// tokens (combine4, the combine launch's arithmetic) into out.  A block's 16 outputs
+// are half of each 128-byte line of the slot rows it reads: the row blocks go to the
+// XCDs in contiguous ranges, so both halves of a line are read through one L2.
 __global__ __launch_bounds__(SH_SK_NT) void k_sh_combine(ShSkArgs A, const float *__restrict__ slots,
                                                         const int *__restrict__ rowof, const float *__restrict__ w, int K,
                                                         float route_scale, float *__restrict__ out) {
     __shared__ float red[8 * 16 * 16 * 2];
-    sh_sk_block<0, 2, 0>(A, blockIdx.x, blockIdx.y, red);
+    const int rb = sw_xcd_work((int)blockIdx.x, (int)gridDim.x);
+    sh_sk_block<0, 2, 0>(A, rb, blockIdx.y, red);
     __syncthreads();                                    // the tile's shared outputs are written
     const int tid = threadIdx.x;
     if (tid < 32 * 4) {
         const int64_t s = (int64_t)blockIdx.y * 32 + (tid >> 2);
-        if (s < A.S) combine4(slots, rowof, w, s, K, A.O, blockIdx.x * 16 + 4 * (tid & 3), route_scale,
+        if (s < A.S) combine4(slots, rowof, w, s, K, A.O, rb * 16 + 4 * (tid & 3), route_scale,
                               (const float *)A.out, out, 1, nullptr, 0);
     }
 }
