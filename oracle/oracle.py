@@ -529,6 +529,42 @@ class RefLagunaHip:
         return h
 
 
+class RefQwen35Hip:
+    """The reference qwen35 engine's moe_forward_rows (c/qwen35.c:595-700) built
+    with -DCOLI_CUDA and linked against libsabrewing_loader.so
+    (oracle/_ref/libref_qwen35_hip.so): with device pointers, the engine's own
+    routing and counting sort hand the groups to lag_cuda_moe_group and its
+    shared expert to lag_cuda_matmul_bf16; with none, the engine's CPU path."""
+
+    def __init__(self):
+        self.lib = C.CDLL(os.path.join(HERE, "_ref", "libref_qwen35_hip.so"))
+        f = self.lib.ref_qwen35_moe_rows
+        f.restype = C.c_int
+        f.argtypes = [C.c_int] * 5 + [C.c_void_p] * 2 + [C.c_void_p] * 4 + [C.c_void_p] * 3 + [C.c_void_p] * 7 + \
+            [F32P, F32P, C.c_int]
+
+    @staticmethod
+    def available():
+        return os.path.exists(os.path.join(HERE, "_ref", "libref_qwen35_hip.so"))
+
+    def moe_rows(self, E, K, layer, sgate, x, dev=None):
+        """out [S, D] = the engine's MoE (routed + gated shared) of x; layer: per-row int4
+        experts, f32 router, bf16 shared expert; dev: device pointers (ints) gu_q, gu_s,
+        dn_q, dn_s, sg, su, sd, or None for the CPU path"""
+        assert layer.gs == 0 and not layer.router_bf16
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.zeros_like(x)
+        sgate = np.ascontiguousarray(sgate, np.float32)
+        rc = self.lib.ref_qwen35_moe_rows(
+            E, K, layer.D, layer.I, layer.Is, _ptr(layer.router), _ptr(sgate),
+            _ptr(layer.gu_q), _ptr(layer.gu_s), _ptr(layer.dn_q), _ptr(layer.dn_s),
+            _ptr(layer.sg), _ptr(layer.su), _ptr(layer.sd),
+            *[C.c_void_p(int(p) if dev else None) for p in (dev or [0] * 7)],
+            x, out, x.shape[0])
+        assert rc == 0
+        return out
+
+
 class RefCallers:
     """The OLMoE and qwen35 engines' routing from their own sources
     (oracle/_ref/libref_olmoe_*.so, libref_qwen35_*.so)."""

@@ -89,3 +89,37 @@ def test_reference_engine_moe_rows_on_device(be, orc, S_):
     nw = float(np.max(np.abs(dg - dw))) / float(np.max(np.abs(dw)))
     assert nw <= 2e-3, nw
     assert np.array_equal(got.view(np.uint32), got_pt.view(np.uint32))
+
+
+@pytest.mark.parametrize("S_", [1, 5, 150])
+def test_reference_qwen35_moe_rows_on_device(be, orc, S_):
+    """The qwen35 engine's moe_forward_rows (c/qwen35.c:595-700), the second caller of
+    lag_cuda_moe_group (c/qwen35.c:637-642), built with -DCOLI_CUDA against this
+    backend's loader (oracle/ref_qwen35.c): its host router, moe_route and counting
+    sort hand all S rows' groups to lag_cuda_moe_group in one call (no 128-row chunks,
+    unlike laguna), and its shared expert runs through lag_cuda_matmul_bf16 before the
+    engine's sigmoid gate.  Against the same engine on the CPU: within the benchmark
+    tolerance.  The host copies handed to the device run have zero scales and zero
+    shared weights, so a silent fallback to the engine's CPU path cannot pass."""
+    from dataclasses import replace
+    from oracle import synth
+    from oracle.oracle import RefQwen35Hip
+    from sabrewing_amd import configs as cf
+    if not RefQwen35Hip.available():
+        pytest.skip("qwen35 engine library not built (make -C oracle ref, with the reference sources present)")
+    cfg = replace(cf.scaled(cf.C2_SIGMOID, D=512, E=32, K=6, I=256, Is=256), gs=0, router_bf16=False)
+    L = synth.make_layer(orc, cfg, 81)
+    x = synth.make_x(orc, cfg, 82, S_)
+    sgate = (np.random.default_rng(83).standard_normal(cfg.D) * 0.05).astype(np.float32)
+    q = RefQwen35Hip()
+    want = q.moe_rows(cfg.E, cfg.K, L, sgate, x)
+    bufs = [be.upload(a) for a in (L.gu_q, L.gu_s, L.dn_q, L.dn_s, L.sg, L.su, L.sd)]
+    poisoned = replace(L, gu_s=np.zeros_like(L.gu_s), dn_s=np.zeros_like(L.dn_s), sg=np.zeros_like(L.sg),
+                       su=np.zeros_like(L.su), sd=np.zeros_like(L.sd))
+    got = q.moe_rows(cfg.E, cfg.K, poisoned, sgate, x, [int(b) for b in bufs])
+    for b in bufs:
+        b.free()
+    assert np.all(np.isfinite(got))
+    nw = float(np.max(np.abs(got - want))) / float(np.max(np.abs(want)))
+    print(f"S={S_}: normwise {nw:.2e}")
+    assert nw <= 2e-3, nw
