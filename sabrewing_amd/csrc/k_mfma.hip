@@ -92,7 +92,8 @@ __device__ __forceinline__ void digits_group(float v, int i, uint32_t *__restric
     const uint32_t h1 = __builtin_bit_cast(uint16_t, (_Float16)((float)E1 * sc));
     // input r = i & 7 of quarter q = i >> 3 sits at f16 slot (r & 1) * 4 + (r >> 1) of the
     // quarter's 4 dwords: inputs r and r ^ 2 share a dword (r & 2 the high half)
-    const uint32_t o0 = (uint32_t)__shfl_xor((int)h0, 2, 32), o1 = (uint32_t)__shfl_xor((int)h1, 2, 32);
+    const uint32_t o0 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)h0, 0x4E, 0xF, 0xF, true);   // lane i ^ 2
+    const uint32_t o1 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)h1, 0x4E, 0xF, 0xF, true);
     if ((i & 2) == 0) {
         const int dw = (i >> 3) * 4 + (i & 1) * 2 + ((i >> 2) & 1);
         dst[dw] = h0 | (o0 << 16);

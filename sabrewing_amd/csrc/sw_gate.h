@@ -286,18 +286,27 @@ __device__ void gate_topk_wave(const float *__restrict__ src, int E, int K, int 
 #define SW_RG 32
 // the group's exponent e (by the 32 lanes of a half-wave, v = this lane's
 // input): 2^e the smallest power of two above max|x|, 0 for an all-zero
-// group; bad = the group holds a NaN or an infinity
+// group; bad = the group holds a NaN or an infinity.  The maximum is taken over
+// the bits of |x| (non-negative floats order as their bits, and an infinity or a
+// NaN lies above every finite value): within each 16-lane row by DPP, then the
+// half-wave's two rows by one shuffle
 __device__ __forceinline__ int limbs_exp(float v, bool &bad) {
-    float m = fabsf(v);
-    bad = !(m <= 3.4028235e38f);                     // NaN or inf
-#pragma unroll
-    for (int o = 1; o < 32; o <<= 1) {
-        m = fmaxf(m, __shfl_xor(m, o, 32));
-        bad = bad | (__shfl_xor((int)bad, o, 32) != 0);
-    }
+    uint32_t mb = __builtin_bit_cast(uint32_t, v) & 0x7FFFFFFFu;
+    mb = dpp_umax<0xB1>(mb);                         // quad_perm [1,0,3,2]
+    mb = dpp_umax<0x4E>(mb);                         // quad_perm [2,3,0,1]
+    mb = dpp_umax<0x141>(mb);                        // row_half_mirror
+    mb = dpp_umax<0x140>(mb);                        // row_mirror
+    const uint32_t o = (uint32_t)__shfl_xor((int)mb, 16, 32);
+    mb = mb > o ? mb : o;
+    bad = mb > 0x7F7FFFFFu;                          // NaN or inf
     int e = 0;
-    if (m > 0.f && !bad) (void)frexpf(m, &e);        // m = f 2^e, f in [0.5, 1): 2^e > m
+    if (mb != 0u && !bad) (void)frexpf(__builtin_bit_cast(float, mb), &e);   // m = f 2^e, f in [0.5, 1): 2^e > m
     return e;
+}
+// OR over the 8 lanes of each aligned group of 8 (DPP within a row)
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_or(uint32_t v) {
+    return v | (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, true);
 }
 // the next digit of y (|y| <= 1): round to nearest, clamp to [-8, 7]; y keeps
 // the exact remainder (|y| <= 1)
@@ -322,9 +331,9 @@ __device__ __forceinline__ void limbs_group(float v, int i, sw_u32x4 *__restrict
         const int d = ((D + 8) & 15) - 8;             // in [-8, 7], D - d a multiple of 16
         D = (D - d) >> 4;                             // exact
         uint32_t nib = ((uint32_t)d & 0xFu) << (4 * (i & 7));
-        nib |= __shfl_xor(nib, 1, 32);
-        nib |= __shfl_xor(nib, 2, 32);
-        nib |= __shfl_xor(nib, 4, 32);
+        nib = dpp_or<0xB1>(nib);                      // quad_perm [1,0,3,2]
+        nib = dpp_or<0x4E>(nib);                      // quad_perm [2,3,0,1]
+        nib = dpp_or<0x141>(nib);                     // row_half_mirror: the other quad of the 8
         dw[l] = nib;                                  // lanes 8j.. hold dword j of limb l
     }
     if ((i & 7) == 0) {
