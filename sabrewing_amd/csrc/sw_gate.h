@@ -69,6 +69,48 @@ template <int CTRL>
 __device__ __forceinline__ float dpp_add(float v) {
     return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
 }
+// a lane's partner within its 16-lane row by rotation (row_ror:N): lane (i - N) mod 16.
+// The tails of the butterflies below pair lanes at distance 8, 4, 2, 1 after the
+// values already agree between lanes at every larger distance of the tree, so the
+// rotation hands each lane the value of lane i ^ N, whichever way it turns, and the
+// sums get the bits of the xor butterfly (a + b == b + a)
+template <int N>
+__device__ __forceinline__ float row_ror(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x120 + N, 0xF, 0xF, true));
+}
+template <int N>
+__device__ __forceinline__ double row_ror(double v) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, 0x120 + N, 0xF, 0xF, true);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), 0x120 + N, 0xF, 0xF, true);
+    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+// the reduce tree of a 16-lane row as __shfl_down by 8, 4, 2, 1: lane 0 ends with
+// ((v0 + v8) + (v4 + v12)) + ... (the router chains' _mm512_reduce_add_ps order)
+__device__ __forceinline__ float row_reduce16(float v) {
+    v = v + row_ror<8>(v);
+    v = v + row_ror<4>(v);
+    v = v + row_ror<2>(v);
+    return v + row_ror<1>(v);
+}
+// the xor butterfly over 64 lanes, pairs at distance 32, 16, 8, 4, 2, 1 in that order
+__device__ __forceinline__ double wave_xor_sum(double v) {
+    v += __shfl_xor(v, 32);
+    v += __shfl_xor(v, 16);
+    v += row_ror<8>(v);
+    v += row_ror<4>(v);
+    v += row_ror<2>(v);
+    return v + row_ror<1>(v);
+}
+// the maximum over 64 lanes (fmaxf: any order gives the same value)
+__device__ __forceinline__ float wave_fmax(float v) {
+    v = fmaxf(v, __shfl_xor(v, 32));
+    v = fmaxf(v, __shfl_xor(v, 16));
+    v = fmaxf(v, row_ror<8>(v));
+    v = fmaxf(v, row_ror<4>(v));
+    v = fmaxf(v, row_ror<2>(v));
+    return fmaxf(v, row_ror<1>(v));
+}
 __device__ __forceinline__ float run_sum16(float v) {
     v = dpp_add<0xB1>(v);                   // quad_perm [1,0,3,2]
     v = dpp_add<0x4E>(v);                   // quad_perm [2,3,0,1]
@@ -145,8 +187,7 @@ __device__ void gate_topk_wave(const float *__restrict__ src, int E, int K, int 
 #pragma unroll
             for (int i = 0; i < NPER; i++)
                 if (NPER * lane + i < E) t += (double)p[i];
-            for (int o = 32; o; o >>= 1) t += __shfl_xor(t, o);
-            return t;
+            return wave_xor_sum(t);
         }
         double sum = 0.0;
         for (int l = 0; l < 64 && NPER * l < E; l++) {
@@ -165,7 +206,7 @@ __device__ void gate_topk_wave(const float *__restrict__ src, int E, int K, int 
             const int e = NPER * lane + i;
             if (e < E && v[i] == v[i]) { mx = any ? fmaxf(mx, v[i]) : v[i]; any = true; }
         }
-        for (int o = 32; o; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+        mx = wave_fmax(mx);
         const float r0 = __shfl(v[0], 0);             // expert 0
         if (r0 != r0) mx = r0;                        // a NaN in slot 0 propagates, as in the scan
 #pragma unroll
@@ -187,7 +228,7 @@ __device__ void gate_topk_wave(const float *__restrict__ src, int E, int K, int 
             const int e = NPER * lane + i;
             if (e < E && v[i] > mx) mx = v[i];
         }
-        for (int o = 32; o; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+        mx = wave_fmax(mx);
 #pragma unroll
         for (int i = 0; i < NPER; i++) v[i] = sw_expf_t(v[i] - mx, tab);
         if (act == 3) {
@@ -373,7 +414,7 @@ __device__ __forceinline__ float rms_inv_block(const float *__restrict__ xr, int
 #pragma unroll
             for (int k = 0; k < RN_CH; k++) ss += (double)v[k] * (double)v[k];
         }
-        for (int o = 32; o; o >>= 1) ss += __shfl_xor(ss, o);
+        ss = wave_xor_sum(ss);
         if (lane == 0) part[wave] = ss;
     }
     __syncthreads();

@@ -218,11 +218,7 @@ __device__ __forceinline__ void router_block(const RouterArgs &R, int bx, int s,
     }
     tab[lane & 31] = tabv;                            // every wave writes the whole table (equal values)
     wave_sync();
-    float v = acc;
-    v = v + __shfl_down(v, 8, 16);
-    v = v + __shfl_down(v, 4, 16);
-    v = v + __shfl_down(v, 2, 16);
-    v = v + __shfl_down(v, 1, 16);
+    float v = row_reduce16(acc);
     if (j == 0 && valid) {
         if (R.lbias) v = v + R.lbias[e];
         R.logits[(int64_t)s * E + e] = v;
@@ -390,11 +386,7 @@ __device__ __forceinline__ void router_tile_block(const RouterArgs &R, int S, in
         const int e = (eg0 + g) * 4 + (lane >> 4);
 #pragma unroll
         for (int t = 0; t < TT; t++) {
-            float v = acc[g][t];
-            v = v + __shfl_down(v, 8, 16);
-            v = v + __shfl_down(v, 4, 16);
-            v = v + __shfl_down(v, 2, 16);
-            v = v + __shfl_down(v, 1, 16);
+            float v = row_reduce16(acc[g][t]);
             if (j == 0 && e < E && t < nt) {
                 const int64_t s = s0 + t;
                 if (R.lbias) v = v + R.lbias[e];
