@@ -629,6 +629,8 @@ int sw_launch_q4_dot8_rows_tab(hipStream_t st, SwQ4 W, const SwTab *tab, const s
 #ifndef DC_RB
 #define DC_RB 8            // 4 and 16 measured slower at B=1 (10.2 and 10.9 us against 9.8)
 #endif
+#define DC_KU 16           // ranks whose run sums are read ahead of the fma chain
+#define DC_NCM 4           // run sums per row read ahead (I <= 2048 at runs of 16 groups)
 struct Dot8DownArgs {
     SwQ4 W;
     int gsh;
@@ -697,12 +699,39 @@ __device__ __forceinline__ void dot8_down_combine_block(const Dot8DownArgs &A, i
     __syncthreads();
     if (tid < DC_RB) {
         float acc = 0.f;
-        for (int aa = 0; aa < K; aa++) {
-            const float *rr = runs + (aa * DC_RB + tid) * NC;
-            float y = rr[0];
-            for (int cc = 1; cc < NC; cc++) y = y + rr[cc];
-            if (W.gs <= 0) y = y * W.s[(int64_t)sel[aa] * D + d0 + tid];
-            acc = __builtin_fmaf(wk[aa], y, acc);
+        if (W.gs > 0 && NC <= DC_NCM) {
+            // every rank's run sums and weight read from LDS first, then the same additions
+            // and the rank-order fma chain (a loop over the ranks would wait out an LDS
+            // latency for each of its loads in turn)
+            for (int a0 = 0; a0 < K; a0 += DC_KU) {
+                float yr[DC_KU][DC_NCM], wr[DC_KU];
+#pragma unroll
+                for (int u = 0; u < DC_KU; u++) {
+                    const int aa = min(a0 + u, K - 1);
+                    const float *rr = runs + (aa * DC_RB + tid) * NC;
+#pragma unroll
+                    for (int cc = 0; cc < DC_NCM; cc++) yr[u][cc] = rr[min(cc, NC - 1)];
+                    wr[u] = wk[aa];
+                }
+#pragma unroll
+                for (int u = 0; u < DC_KU; u++) {
+                    if (a0 + u < K) {                 // (uniform)
+                        float y = yr[u][0];
+#pragma unroll
+                        for (int cc = 1; cc < DC_NCM; cc++)
+                            if (cc < NC) y = y + yr[u][cc];
+                        acc = __builtin_fmaf(wr[u], y, acc);
+                    }
+                }
+            }
+        } else {
+            for (int aa = 0; aa < K; aa++) {
+                const float *rr = runs + (aa * DC_RB + tid) * NC;
+                float y = rr[0];
+                for (int cc = 1; cc < NC; cc++) y = y + rr[cc];
+                if (W.gs <= 0) y = y * W.s[(int64_t)sel[aa] * D + d0 + tid];
+                acc = __builtin_fmaf(wk[aa], y, acc);
+            }
         }
         acc = acc * route_scale;
         if (A.wsh) {                                  // c/inkling.c:1176-1182: after the routed ranks
