@@ -238,7 +238,7 @@ int    lag_hip_graph_launch(void *g);
 void   lag_hip_graph_destroy(void *g);
 
 /* Kernel choice for the grouped expert GEMMs of lag_hip_moe_forward with
- * S > 1: 0 auto (the f16 MFMA when the batch's groups average >= 8 tokens,
+ * S > 1: 0 auto (the f16 MFMA when the batch's groups average >= 6.5 tokens,
  * else dot8), 1 dot8, 2 f16 MFMA.  Both give the same bits.  Returns the
  * previous mode, -1 for a bad one.  No counterpart in the reference (one
  * grouped kernel there, c/backend_cuda.cu:618-700): a tuning switch. */

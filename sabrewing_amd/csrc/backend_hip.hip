@@ -211,13 +211,15 @@ extern "C" int lag_hip_sync(void) {
 
 // The grouped expert GEMMs of a batch: dot8 (k_dot8.hip) or the f16 MFMA
 // (k_mfma.hip), bit-identical; auto takes the MFMA when the groups average at
-// least SW_MF_MIN_AVG tokens (its 16-token tiles are then mostly full)
+// least 6.5 tokens (SW_MF_MIN_AVG2 / 2).  Measured on the C2 layer (dot8 against MFMA
+// per step): B=160 1,009 against 1,055 us, B=176 1,088 against 1,065, B=192 1,167 against
+// 1,072, B=256 1,476 against 1,105.
 static int g_grouped_kernel = 0;        // 0 auto, 1 dot8, 2 MFMA
-#define SW_MF_MIN_AVG 8
+#define SW_MF_MIN_AVG2 13
 static bool use_mfma(int T, int E, int D, int I) {
     if (g_grouped_kernel == 1 || D % 128 || I % 128) return false;      // whole chunks of 4 input groups
     if (g_grouped_kernel == 2) return true;
-    return T >= SW_MF_MIN_AVG * (T < E ? T : E);
+    return 2 * (int64_t)T >= SW_MF_MIN_AVG2 * (int64_t)(T < E ? T : E);
 }
 extern "C" int lag_hip_set_grouped_kernel(int mode) {
     if (mode < 0 || mode > 2) return -1;
